@@ -1,0 +1,14 @@
+"""gpa_amd: the MI355X (gfx950) HIP backend of the DenseGPA attention core.
+
+Drop-in for the reference `gpa` package's DenseGPA/GPAConfig/GPAState API
+(src/gpa/__init__.py:1-9) with ``backend="hip"``.  The compute path is the
+hand-written HIP library `libgpa_hip.so` (C ABI declared in include/gpa_hip.h)
+driven from PyTorch-ROCm; there is no CPU or eager fallback.
+"""
+from .config import GPAConfig
+from .module import DenseGPA, QuadraticFeatures
+from .state import GPAState, LevelState, RelationState, ResidualSnapshot
+
+__all__ = ["DenseGPA", "GPAConfig", "GPAState", "LevelState", "RelationState",
+           "ResidualSnapshot", "QuadraticFeatures"]
+__version__ = "0.1.0"

@@ -1,0 +1,158 @@
+"""Loading and comparing the golden fixtures in tests/golden/*.npz.
+
+A fixture holds the reference's inputs, outputs, carried state and gradients
+for one seeded case (written by tests/golden/make_golden.py).  Tensors are
+stored whole ("full/<name>") or as a fingerprint ("fp/<name>": sum, sum|x|,
+sum x^2 and 64 evenly spaced samples of the flattened tensor).
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import torch
+
+from gpa_amd import DenseGPA, GPAConfig
+from gpa_amd.state import tensors
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+SAMPLES = 64
+DTYPES = {"float32": torch.float32, "float64": torch.float64, "bfloat16": torch.bfloat16}
+
+
+def names():
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+
+
+class Case:
+    def __init__(self, name: str):
+        self.name = name
+        with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+            self.z = {k: z[k] for k in z.files}
+        self.cfg = json.loads(str(self.z["config"]))
+        self.cfg["slots"] = tuple(self.cfg["slots"])
+        self.seed, self.batch, self.length, self.normalize_k, self.control_dim = (
+            int(x) for x in self.z["meta"])
+        self.dtype = DTYPES[str(self.z["dtype"])]
+        self.gate_noise = float(self.z["gate_noise"])
+        self.chunk_size = self.cfg["chunk_size"]
+
+    def has(self, name: str) -> bool:
+        return ("full/" + name) in self.z or ("fp/" + name) in self.z
+
+    def build(self):
+        """Seeded model and inputs, drawn in the fixture script's RNG order."""
+        cfg = dict(self.cfg)
+        cfg["chunk_size"] = max(2, cfg["chunk_size"])  # params do not depend on it
+        torch.manual_seed(self.seed)
+        model = DenseGPA(GPAConfig(**cfg))
+        if self.dtype == torch.float64:
+            model = model.double()
+        if self.gate_noise:
+            with torch.no_grad():
+                for w in model.gate_weight:
+                    w.normal_(0, self.gate_noise)
+        gen = torch.float64 if self.dtype == torch.float64 else torch.float32
+        h, dk, dv = cfg["heads"], cfg["key_dim"], cfg["value_dim"]
+        q = torch.randn(self.batch, self.length, h, dk, dtype=gen)
+        k = torch.randn_like(q)
+        v = torch.randn(self.batch, self.length, h, dv, dtype=gen)
+        if self.normalize_k:
+            k = torch.nn.functional.normalize(k, dim=-1)
+        ctrl = torch.randn(self.batch, self.length, self.control_dim, dtype=gen) if self.control_dim else None
+        q, k, v = (x.to(self.dtype) for x in (q, k, v))
+        if ctrl is not None and self.dtype == torch.bfloat16:
+            ctrl = ctrl.float()
+        return model, q, k, v, ctrl
+
+    def decode_inputs(self):
+        return tuple(torch.from_numpy(self.z["full/decode/" + n]).to(self.dtype) if ("full/decode/" + n) in self.z
+                     else None for n in ("q", "k", "v"))
+
+    def regen_decode_inputs(self):
+        torch.manual_seed(self.seed + 1)
+        gen = torch.float64 if self.dtype == torch.float64 else torch.float32
+        steps = self.steps()
+        h, dk, dv = self.cfg["heads"], self.cfg["key_dim"], self.cfg["value_dim"]
+        dq = torch.randn(self.batch, steps, h, dk, dtype=gen)
+        dk_ = torch.randn_like(dq)
+        dv_ = torch.randn(self.batch, steps, h, dv, dtype=gen)
+        if self.normalize_k:
+            dk_ = torch.nn.functional.normalize(dk_, dim=-1)
+        return tuple(x.to(self.dtype) for x in (dq, dk_, dv_))
+
+    def steps(self) -> int:
+        return int(self.z["full/decode/out"].shape[1]) if "full/decode/out" in self.z else 0
+
+
+def fingerprint(x: torch.Tensor) -> np.ndarray:
+    flat = x.detach().double().reshape(-1)
+    idx = torch.linspace(0, max(flat.numel() - 1, 0), SAMPLES).round().long()
+    head = torch.stack((flat.sum(), flat.abs().sum(), flat.square().sum()))
+    return torch.cat((head, flat[idx])).numpy()
+
+
+def grad_scale(case: Case) -> float:
+    """Largest |gradient| stored for the case (whole tensors and fingerprint samples)."""
+    top = 0.
+    for key, val in case.z.items():
+        if key.startswith("full/grad/"):
+            top = max(top, float(np.abs(val).max()) if val.size else 0.)
+        elif key.startswith("fp/grad/"):
+            top = max(top, float(np.abs(val[3:]).max()))
+    return top
+
+
+def compare(case: Case, name: str, x: torch.Tensor, rtol: float, atol: float = 0.) -> str | None:
+    """None if `x` matches the fixture entry, else a message.
+
+    Whole tensors: elementwise |d| <= atol + rtol*(|ref| + 0.1*max|ref|), and a
+    relative L2 error <= 10*rtol unless the tensor is itself at the `atol`
+    (roundoff) level.  Fingerprints: the sum within atol*n + rtol*sum|x|,
+    sum|x| and sum x^2 relatively, and the samples elementwise as above.
+    """
+    x = x.detach().double().cpu()
+    if "full/" + name in case.z:
+        ref = torch.from_numpy(case.z["full/" + name]).double()
+        if ref.shape != x.shape:
+            return f"{name}: shape {tuple(x.shape)} != {tuple(ref.shape)}"
+        if not ref.numel():
+            return None
+        scale = ref.abs().max().item()
+        rel = ((x - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+        worst = ((x - ref).abs() - atol - rtol * (ref.abs() + .1 * scale)).max().item()
+        tiny = ref.norm().item() <= 100 * atol * ref.numel() ** .5
+        if (rel > 10 * rtol and not tiny) or worst > 0:
+            return f"{name}: rel L2 {rel:.3e}, worst excess {worst:.3e} (rtol {rtol}, atol {atol:.1e})"
+        return None
+    ref = case.z["fp/" + name]
+    got = fingerprint(x)
+    n = x.numel()
+    bad = []
+    if abs(got[0] - ref[0]) > atol * n + rtol * max(abs(ref[1]), 1e-300):
+        bad.append(f"sum {got[0]:.6e} vs {ref[0]:.6e}")
+    for i, label, floor in ((1, "abs-sum", atol * n), (2, "sq-sum", 2 * atol * abs(ref[1]) + atol * atol * n)):
+        if abs(got[i] - ref[i]) > floor + rtol * abs(ref[i]):
+            bad.append(f"{label} {got[i]:.6e} vs {ref[i]:.6e}")
+    err = np.abs(got[3:] - ref[3:]) - atol - rtol * (np.abs(ref[3:]) + .1 * np.abs(ref[3:]).max())
+    if (err > 0).any():
+        bad.append(f"samples worst excess {err.max():.3e}")
+    return f"{name}: " + "; ".join(bad) if bad else None
+
+
+def compare_state(case: Case, prefix: str, state, rtol: float) -> list[str]:
+    errors = []
+    meta = case.z[prefix + "/meta"]
+    got_meta = [state.position, state.chunk_size, state.chunk_offset, 0 if state.frozen is None else 1]
+    if list(meta) != got_meta:
+        errors.append(f"{prefix} meta {got_meta} != {list(meta)}")
+    for n, x in enumerate(tensors(state)):
+        key = f"{prefix}/{n:03d}"
+        if not case.has(key):
+            errors.append(f"{key}: not in fixture")
+            continue
+        msg = compare(case, key, x, rtol)
+        if msg:
+            errors.append(msg)
+    return errors

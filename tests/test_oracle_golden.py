@@ -1,0 +1,75 @@
+"""Pin the oracle (and the product's parameter initialisation) to the reference.
+
+Every fixture in tests/golden/ was written by running the reference package on
+the CPU (tests/golden/make_golden.py).  Here the same seeded construction must
+give the same parameters and inputs, and the oracle must reproduce the
+reference's outputs, carried state, gradients of every parameter and input,
+cached-call partitions and single-token continuations.
+"""
+import pytest
+import torch
+
+import oracle
+from tests.golden_cases import Case, compare, compare_state, grad_scale, names
+
+# Same arithmetic in a different association order: fp64 agrees to ~1e-12,
+# fp32 to ~1e-6; bf16 activations agree except where an fp32 difference of
+# one ulp flips a bf16 rounding.
+RTOL = {torch.float64: 1e-9, torch.float32: 2e-5, torch.bfloat16: 2e-2}
+
+
+@pytest.mark.parametrize("name", names())
+def test_seeded_parameters_and_inputs_match_reference(name):
+    case = Case(name)
+    model, q, k, v, ctrl = case.build()
+    exact = 1e-12 if case.dtype == torch.float64 else 1e-6
+    errors = [compare(case, "param/" + n, p, exact) for n, p in model.named_parameters()]
+    errors += [compare(case, "in/" + n, x, exact) for n, x in (("q", q), ("k", k), ("v", v), ("control", ctrl))
+               if x is not None]
+    assert not [e for e in errors if e], errors
+
+
+@pytest.mark.parametrize("name", names())
+def test_oracle_forward_state_and_gradients_match_reference(name):
+    case = Case(name)
+    rtol = RTOL[case.dtype]
+    model, q, k, v, ctrl = case.build()
+    q, k, v = (x.requires_grad_() for x in (q, k, v))
+    if ctrl is not None:
+        ctrl.requires_grad_()
+    run = oracle.OracleRun(model, chunk_size=case.chunk_size)
+    out, state = run(q, k, v, control_input=ctrl)
+    errors = [compare(case, "out", out, rtol)] + compare_state(case, "state", state, rtol)
+    out.float().square().mean().backward()
+    # Gradients that vanish at initialisation (edge logits while every relation
+    # memory is still zero) are pure roundoff: floor them at 1e-3*rtol of the
+    # largest gradient of the case.
+    g_rtol = rtol if case.dtype != torch.bfloat16 else 5e-2
+    g_atol = 1e-3 * g_rtol * grad_scale(case)
+    for n, p in model.named_parameters():
+        if p.grad is not None:
+            assert case.has("grad/" + n), n
+            errors.append(compare(case, "grad/" + n, p.grad, g_rtol, g_atol))
+        else:
+            assert not case.has("grad/" + n), n
+    for n, x in (("q", q), ("k", k), ("v", v), ("control", ctrl)):
+        if x is not None:
+            errors.append(compare(case, "grad/in_" + n, x.grad, g_rtol, g_atol))
+    with torch.no_grad():
+        if "partitions" in case.z:
+            running, parts = None, []
+            for lo, hi in case.z["partitions"]:
+                y, running = run(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], running,
+                                 control_input=ctrl[:, lo:hi] if ctrl is not None else None)
+                parts.append(y)
+            errors.append(compare(case, "partition_out", torch.cat(parts, 1), rtol))
+        if case.steps():
+            dq, dk, dv = case.regen_decode_inputs()
+            running, ys = state, []
+            for t in range(case.steps()):
+                y, running = run(dq[:, t:t + 1], dk[:, t:t + 1], dv[:, t:t + 1], running)
+                ys.append(y)
+            errors.append(compare(case, "decode/out", torch.cat(ys, 1), rtol))
+            errors += compare_state(case, "decode/state", running, rtol)
+    errors = [e for e in errors if e]
+    assert not errors, errors
