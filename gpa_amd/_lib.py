@@ -1,0 +1,103 @@
+"""ctypes binding of libgpa_hip.so (C ABI in include/gpa_hip.h).
+
+The library is loaded from the package directory only.  If it is missing, or
+no gfx950 device is present, every entry point raises: there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
+ABI_VERSION = 1
+CHUNK_ROWS = 64
+MAX_KDIM = 256
+MAX_VDIM = 1024
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
+
+c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+c_fp = ctypes.POINTER(ctypes.c_float)
+
+
+class Operand(ctypes.Structure):
+    _fields_ = [("ptr", c_vp), ("sb", c_i64), ("st", c_i64), ("sh", c_i64)]
+
+
+class Problem(ctypes.Structure):
+    _fields_ = [("batch", c_i32), ("heads", c_i32), ("tokens", c_i32), ("offset", c_i32),
+                ("chunk", c_i32), ("kdim", c_i32), ("vdim", c_i32), ("dtype", c_i32),
+                ("q", Operand), ("k", Operand), ("v", Operand), ("g", Operand), ("beta", Operand),
+                ("s0", c_vp), ("s0_sb", c_i64), ("s0_sh", c_i64)]
+
+
+class Saved(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("kn", "qn", "w", "u", "delta", "tri", "gam", "beta", "states", "final")]
+
+
+class Grads(ctypes.Structure):
+    _fields_ = [("dout", Operand), ("dstates", c_vp), ("dfinal", c_vp),
+                ("dd0", c_vp), ("ddelta", c_vp), ("dhend", c_vp), ("dw", c_vp),
+                ("dq", Operand), ("dk", Operand), ("dv", Operand), ("dg", Operand), ("dbeta", Operand),
+                ("ds0", c_vp)]
+
+
+EXPORTS = {
+    "gpa_hip_abi_version": ([], ctypes.c_int),
+    "gpa_hip_last_error": ([], ctypes.c_char_p),
+    "gpa_gdn_nchunks": ([c_i32, c_i32, c_i32], c_i32),
+    "gpa_gdn_forward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, c_vp], ctypes.c_int),
+    "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads), c_vp],
+                         ctypes.c_int),
+}
+
+_lib = None
+
+
+class HipBackendError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the library (no device needed); raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipBackendError(f"{LIB_PATH} is not built: run `python -m gpa_amd.build`")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = args, res
+    if lib.gpa_hip_abi_version() != ABI_VERSION:
+        raise HipBackendError("libgpa_hip.so ABI version mismatch; rebuild it")
+    _lib = lib
+    return lib
+
+
+def require_device(t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise HipBackendError("backend='hip' needs tensors on a ROCm GPU (no CPU fallback)")
+    arch = getattr(torch.cuda.get_device_properties(t.device), "gcnArchName", "")
+    if not arch.startswith("gfx950"):
+        raise HipBackendError(f"backend='hip' is built for gfx950, found {arch!r}")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise HipBackendError(f"{what} failed ({rc}): {load().gpa_hip_last_error().decode()}")
+
+
+def operand(t: torch.Tensor | None, heads_dim: int = 2) -> Operand:
+    """Operand for a [B,T,H,...] tensor (or [B,T,H] scalars); last dim contiguous."""
+    if t is None:
+        return Operand(None, 0, 0, 0)
+    if t.ndim == 4 and t.stride(3) != 1:
+        raise ValueError("operand needs a contiguous last dimension")
+    return Operand(t.data_ptr(), t.stride(0), t.stride(1), t.stride(heads_dim))
+
+
+def stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

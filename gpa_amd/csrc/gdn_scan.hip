@@ -1,0 +1,1176 @@
+// Chunked gated-delta-rule (GDN) scan for gfx950: forward and backward.
+//
+// Per stream, S_t = e^{g_t} (I - b_t k_t k_t^T) S_{t-1} + b_t k_t v_t^T and
+// o_t = q_t^T S_t with k, q L2-normalised (reference src/gpa/ops.py:29-46,
+// 80-85).  Within a chunk of positions with in-chunk cumulative log decay G:
+//   A_ts = b_t e^{G_t-G_s} k_t.k_s (s<t),  T = (I+A)^-1,
+//   U = T diag(b) V,  W = T diag(b e^G) K,  D = U - W S_n,
+//   O = diag(e^G) Q S_n + (causal e^{G_t-G_s} Q K^T) D,
+//   S_{n+1} = e^{G_C} S_n + (diag(e^{G_C-G}) K)^T D.
+// Kernels:
+//   gdn_prep       chunk-parallel: normalise, G, T, W, U
+//   gdn_state_fwd  sequential over chunks, parallel over (stream, 32-column tile):
+//                  S_n (saved), D
+//   gdn_out_fwd    chunk-parallel: O
+//   gdn_dd0        chunk-parallel: P^T dO (the in-chunk part of dD)
+//   gdn_state_bwd  reverse sequential: dS at every chunk end, dD
+//   gdn_chunk_bwd  chunk-parallel: dq, dk, dv, dg, dbeta
+// All intermediates are float32; q/k/v/out may be bf16 (rounded exactly where
+// the reference rounds: the normalised keys/queries and the read).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gpa_hip.h"
+#include "gpa_common.h"
+
+namespace gpa {
+
+constexpr int R = GPA_CHUNK_ROWS;  // rows per chunk tile
+constexpr int NT = 256;            // threads per block
+constexpr int VT = 32;             // state columns per sequential block
+constexpr int KS = 64;             // staged K slice
+constexpr int LDR = R + 1;         // padded row stride of R x R tiles
+constexpr int LDS_ = KS + 1;       // padded row stride of R x KS tiles
+
+struct Geo {
+  int s, b, h, n;
+};
+
+__device__ __forceinline__ int token_at(const gpa_gdn_problem& p, int n, int r) {
+  if (r >= p.chunk) return -1;
+  const int t = n * p.chunk + r - p.offset;
+  return (t >= 0 && t < p.tokens) ? t : -1;
+}
+
+__device__ __forceinline__ int64_t op_base(const gpa_operand& o, int b, int h) {
+  return (int64_t)b * o.sb + (int64_t)h * o.sh;
+}
+
+template <typename E>
+__device__ __forceinline__ float op_load(const gpa_operand& o, int b, int h, int t, int d) {
+  return to_f32(reinterpret_cast<const E*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st + d]);
+}
+
+__device__ __forceinline__ float scalar_load(const gpa_operand& o, int b, int h, int t) {
+  return reinterpret_cast<const float*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st];
+}
+
+// Stream-major saved buffer offsets.
+__device__ __forceinline__ int64_t rows_off(int s, int n, int nch, int r, int width) {
+  return (((int64_t)s * nch + n) * R + r) * width;
+}
+__device__ __forceinline__ int64_t state_off(int s, int n, int nch, int K, int V) {
+  return ((int64_t)s * nch + n) * K * V;
+}
+
+// Sum over the 16 lanes that share (lane / 16) within a wave.
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 8, 16);
+  x += __shfl_xor(x, 4, 16);
+  x += __shfl_xor(x, 2, 16);
+  x += __shfl_xor(x, 1, 16);
+  return x;
+}
+__device__ __forceinline__ float sum64(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Load an R x KS slice (columns c0..c0+KS) of a saved [.., R, width] fp32 row
+// block into LDS with optional per-row scale; zero past `width`.
+__device__ __forceinline__ void stage_rows(float* dst, const float* src, int width, int c0,
+                                           const float* row_scale) {
+  for (int idx = threadIdx.x; idx < R * KS; idx += NT) {
+    const int r = idx / KS, c = idx % KS;
+    float x = (c0 + c < width) ? src[(int64_t)r * width + c0 + c] : 0.f;
+    if (row_scale) x *= row_scale[r];
+    dst[r * LDS_ + c] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_prep: one block per (chunk n = blockIdx.x, stream s = blockIdx.y).
+template <typename E, int KM>
+__global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
+  extern __shared__ float smem[];
+  float* kn_s = smem;                 // [R][KM+1]
+  float* a_s = kn_s + R * (KM + 1);   // [R][LDR]   A, then reused
+  float* t_s = a_s + R * LDR;         // [R][LDR]   T
+  float* v_s = t_s + R * LDR;         // [R][LDR]   b*V slice
+  float* gam_s = v_s + R * LDR;       // [R]
+  float* beta_s = gam_s + R;          // [R]
+  float* sc_s = beta_s + R;           // [R]  b e^G
+  const int n = blockIdx.x, s = blockIdx.y;
+  const int b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  if (tid < R) {
+    const int t = token_at(p, n, tid);
+    gam_s[tid] = t >= 0 ? scalar_load(p.g, b, h, t) : 0.f;
+    beta_s[tid] = t >= 0 ? scalar_load(p.beta, b, h, t) : 0.f;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int r = 0; r < R; ++r) { acc += gam_s[r]; gam_s[r] = acc; }
+  }
+  __syncthreads();
+  if (tid < R) {
+    sc_s[tid] = beta_s[tid] * __expf(gam_s[tid]);
+    sv.gam[rows_off(s, n, nch, 0, 1) + tid] = gam_s[tid];
+    sv.beta[rows_off(s, n, nch, 0, 1) + tid] = beta_s[tid];
+  }
+
+  // Normalise keys (and queries) row by row: wave w owns rows w, w+4, ...
+  for (int r = wave; r < R; r += NT / 64) {
+    const int t = token_at(p, n, r);
+    float x[KM / 64];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < KM / 64; ++i) {
+      const int d = lane + 64 * i;
+      x[i] = (t >= 0 && d < K) ? op_load<E>(p.k, b, h, t, d) : 0.f;
+      ss += x[i] * x[i];
+    }
+    const float den = fmaxf(sqrtf(sum64(ss)), 1e-6f);
+#pragma unroll
+    for (int i = 0; i < KM / 64; ++i) {
+      const int d = lane + 64 * i;
+      const float y = round_as<E>(x[i] / den);
+      kn_s[r * (KM + 1) + d] = y;
+      if (d < K) sv.kn[rows_off(s, n, nch, r, K) + d] = y;
+    }
+    if (p.q.ptr) {
+      float ssq = 0.f;
+#pragma unroll
+      for (int i = 0; i < KM / 64; ++i) {
+        const int d = lane + 64 * i;
+        x[i] = (t >= 0 && d < K) ? op_load<E>(p.q, b, h, t, d) : 0.f;
+        ssq += x[i] * x[i];
+      }
+      const float dq = fmaxf(sqrtf(sum64(ssq)), 1e-6f);
+#pragma unroll
+      for (int i = 0; i < KM / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < K) sv.qn[rows_off(s, n, nch, r, K) + d] = round_as<E>(x[i] / dq);
+      }
+    }
+  }
+  __syncthreads();
+
+  // Gram matrix -> A (strictly lower).  Thread tile: rows 4*ty+i, cols tx+16*j.
+  const int ty = tid / 16, tx = tid % 16;
+  {
+    float acc[4][4] = {};
+    for (int k = 0; k < KM; ++k) {
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = kn_s[(4 * ty + i) * (KM + 1) + k];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = kn_s[(tx + 16 * j) * (KM + 1) + k];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * ty + i, u = tx + 16 * j;
+        a_s[t * LDR + u] = (u < t) ? beta_s[t] * __expf(gam_s[t] - gam_s[u]) * acc[i][j] : 0.f;
+      }
+  }
+  __syncthreads();
+
+  // T = (I + A)^-1 by forward substitution; thread c owns column c.
+  if (tid < R) {
+    const int c = tid;
+    for (int t = 0; t < c; ++t) t_s[t * LDR + c] = 0.f;
+    t_s[c * LDR + c] = 1.f;
+    for (int t = c + 1; t < R; ++t) {
+      float acc = 0.f;
+      for (int u = c; u < t; ++u) acc += a_s[t * LDR + u] * t_s[u * LDR + c];
+      t_s[t * LDR + c] = -acc;
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < R * R; idx += NT)
+    sv.tri[rows_off(s, n, nch, 0, R) + idx] = t_s[(idx / R) * LDR + idx % R];
+
+  // W = T diag(b e^G) Kn.  Thread tile rows 4*ty+i, cols tx + 16*j.
+  {
+    float acc[4][KM / 16] = {};
+    for (int u = 0; u < R; ++u) {
+      float a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = t_s[(4 * ty + i) * LDR + u] * sc_s[u];
+#pragma unroll
+      for (int j = 0; j < KM / 16; ++j) {
+        const float c = kn_s[u * (KM + 1) + tx + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] += a[i] * c;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < KM / 16; ++j) {
+        const int k = tx + 16 * j;
+        if (k < K) sv.w[rows_off(s, n, nch, 4 * ty + i, K) + k] = acc[i][j];
+      }
+  }
+
+  // U = T diag(b) V, 64 value columns at a time.
+  for (int v0 = 0; v0 < V; v0 += R) {
+    __syncthreads();
+    for (int idx = tid; idx < R * R; idx += NT) {
+      const int r = idx / R, c = idx % R;
+      const int t = token_at(p, n, r);
+      v_s[r * LDR + c] = (t >= 0 && v0 + c < V) ? beta_s[r] * op_load<E>(p.v, b, h, t, v0 + c) : 0.f;
+    }
+    __syncthreads();
+    float acc[4][4] = {};
+    for (int u = 0; u < R; ++u) {
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = t_s[(4 * ty + i) * LDR + u];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = v_s[u * LDR + tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + tx + 16 * j;
+        if (v < V) sv.u[rows_off(s, n, nch, 4 * ty + i, V) + v] = acc[i][j];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_state_fwd: block (column tile blockIdx.x, stream blockIdx.y), loops chunks.
+template <int KM>
+__global__ __launch_bounds__(NT) void gdn_state_fwd(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
+  extern __shared__ float smem[];
+  float* st_s = smem;                   // [KM][VT+1]
+  float* w_s = st_s + KM * (VT + 1);    // [R][LDS_]
+  float* d_s = w_s + R * LDS_;          // [R][VT+1]
+  float* gam_s = d_s + R * (VT + 1);    // [R]
+  float* rs_s = gam_s + R;              // [R] row scales
+  const int s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x;
+  const int r = tid / VT, c = tid % VT;  // r in 0..7
+  const int v = blockIdx.x * VT + c;
+  const bool vok = v < V;
+
+  for (int i = 0; i < KM / 8; ++i) {
+    const int k = r + 8 * i;
+    st_s[k * (VT + 1) + c] = (p.s0 && k < K && vok)
+        ? p.s0[(int64_t)b * p.s0_sb + (int64_t)h * p.s0_sh + (int64_t)k * V + v] : 0.f;
+  }
+  __syncthreads();
+  for (int n = 0; n < nch; ++n) {
+    const int64_t so = state_off(s, n, nch, K, V);
+    if (vok)
+      for (int i = 0; i < KM / 8; ++i) {
+        const int k = r + 8 * i;
+        if (k < K) sv.states[so + (int64_t)k * V + v] = st_s[k * (VT + 1) + c];
+      }
+    // D = U - W S
+    float acc[R / 8];
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) acc[j] = vok ? sv.u[rows_off(s, n, nch, r + 8 * j, V) + v] : 0.f;
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(w_s, sv.w + rows_off(s, n, nch, 0, K), K, k0, nullptr);
+      __syncthreads();
+      for (int kk = 0; kk < KS; ++kk) {
+        const float sk = st_s[(k0 + kk) * (VT + 1) + c];
+#pragma unroll
+        for (int j = 0; j < R / 8; ++j) acc[j] -= w_s[(r + 8 * j) * LDS_ + kk] * sk;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) {
+      d_s[(r + 8 * j) * (VT + 1) + c] = acc[j];
+      if (vok) sv.delta[rows_off(s, n, nch, r + 8 * j, V) + v] = acc[j];
+    }
+    if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+    __syncthreads();
+    const float gc = gam_s[R - 1];
+    const float decay = __expf(gc);
+    if (tid < R) rs_s[tid] = __expf(gc - gam_s[tid]);
+    // S = e^{G_C} S + (diag(e^{G_C-G}) Kn)^T D
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(w_s, sv.kn + rows_off(s, n, nch, 0, K), K, k0, rs_s);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < KS / 8; ++i) {
+        const int kk = r + 8 * i;
+        float x = decay * st_s[(k0 + kk) * (VT + 1) + c];
+        for (int t = 0; t < R; ++t) x += w_s[t * LDS_ + kk] * d_s[t * (VT + 1) + c];
+        st_s[(k0 + kk) * (VT + 1) + c] = x;
+      }
+    }
+    __syncthreads();
+  }
+  if (vok)
+    for (int i = 0; i < KM / 8; ++i) {
+      const int k = r + 8 * i;
+      if (k < K) sv.final[(int64_t)s * K * V + (int64_t)k * V + v] = st_s[k * (VT + 1) + c];
+    }
+}
+
+// P = causal e^{G_t-G_s} Qn Kn^T into p_s ([R][LDR]); uses two R x KS slices.
+template <int KM>
+__device__ void build_p(float* p_s, float* a_s, float* b_s, const float* qn, const float* kn,
+                        const float* gam_s, int K) {
+  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < KM; k0 += KS) {
+    __syncthreads();
+    stage_rows(a_s, qn, K, k0, nullptr);
+    stage_rows(b_s, kn, K, k0, nullptr);
+    __syncthreads();
+    for (int kk = 0; kk < KS; ++kk) {
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = a_s[(4 * ty + i) * LDS_ + kk];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = b_s[(tx + 16 * j) * LDS_ + kk];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * ty + i, u = tx + 16 * j;
+      p_s[t * LDR + u] = (u <= t) ? __expf(gam_s[t] - gam_s[u]) * acc[i][j] : 0.f;
+    }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// gdn_out_fwd: O = diag(e^G) Qn S_n + P D, one block per (chunk, stream).
+template <typename E, int KM>
+__global__ __launch_bounds__(NT) void gdn_out_fwd(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_operand out,
+                                                   int nch) {
+  extern __shared__ float smem[];
+  float* p_s = smem;              // [R][LDR]
+  float* a_s = p_s + R * LDR;     // [R][LDS_]
+  float* b_s = a_s + R * LDS_;    // [R][LDS_]  (also KS x 64 state slice)
+  float* gam_s = b_s + R * LDS_;  // [R]
+  const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+  __syncthreads();
+  const float* qn = sv.qn + rows_off(s, n, nch, 0, K);
+  build_p<KM>(p_s, a_s, b_s, qn, sv.kn + rows_off(s, n, nch, 0, K), gam_s, K);
+  const float* st = sv.states + state_off(s, n, nch, K, V);
+  const float* dl = sv.delta + rows_off(s, n, nch, 0, V);
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(a_s, qn, K, k0, nullptr);
+      for (int idx = tid; idx < KS * 64; idx += NT) {
+        const int kk = idx / 64, c = idx % 64;
+        b_s[kk * LDS_ + c] = (k0 + kk < K && v0 + c < V) ? st[(int64_t)(k0 + kk) * V + v0 + c] : 0.f;
+      }
+      __syncthreads();
+      for (int kk = 0; kk < KS; ++kk) {
+        float a[4], c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = a_s[(4 * ty + i) * LDS_ + kk];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = b_s[kk * LDS_ + tx + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = __expf(gam_s[4 * ty + i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] *= e;
+    }
+    __syncthreads();
+    stage_rows(b_s, dl, V, v0, nullptr);
+    __syncthreads();
+    for (int u = 0; u < R; ++u) {
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = p_s[(4 * ty + i) * LDR + u];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = b_s[u * LDS_ + tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = token_at(p, n, 4 * ty + i);
+      if (t < 0) continue;
+      E* o = reinterpret_cast<E*>(out.ptr) + op_base(out, b, h) + (int64_t)t * out.st;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + tx + 16 * j;
+        if (v < V) o[v] = from_f32<E>(acc[i][j]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_dd0: dd0 = P^T dO (the part of dD not carried by the state).
+template <typename E, int KM>
+__global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
+                                               int nch) {
+  extern __shared__ float smem[];
+  float* p_s = smem;
+  float* a_s = p_s + R * LDR;
+  float* b_s = a_s + R * LDS_;
+  float* gam_s = b_s + R * LDS_;
+  const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+  __syncthreads();
+  build_p<KM>(p_s, a_s, b_s, sv.qn + rows_off(s, n, nch, 0, K), sv.kn + rows_off(s, n, nch, 0, K), gam_s, K);
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    __syncthreads();
+    for (int idx = tid; idx < R * 64; idx += NT) {
+      const int r = idx / 64, c = idx % 64;
+      const int t = token_at(p, n, r);
+      b_s[r * LDS_ + c] = (t >= 0 && v0 + c < V) ? op_load<E>(gr.dout, b, h, t, v0 + c) : 0.f;
+    }
+    __syncthreads();
+    float acc[4][4] = {};
+    for (int u = 0; u < R; ++u) {  // acc[t'][v] += P[u][t'] dO[u][v]
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = p_s[u * LDR + 4 * ty + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = b_s[u * LDS_ + tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + tx + 16 * j;
+        if (v < V) gr.dd0[rows_off(s, n, nch, 4 * ty + i, V) + v] = acc[i][j];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_state_bwd: reverse sequential dS; writes dS at every chunk end and dD.
+template <typename E, int KM>
+__global__ __launch_bounds__(NT) void gdn_state_bwd(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
+                                                     int nch) {
+  extern __shared__ float smem[];
+  float* ds_s = smem;                   // [KM][VT+1]
+  float* x_s = ds_s + KM * (VT + 1);    // [R][LDS_]
+  float* y_s = x_s + R * LDS_;          // [R][LDS_]
+  float* dd_s = y_s + R * LDS_;         // [R][VT+1]
+  float* o_s = dd_s + R * (VT + 1);     // [R][VT+1]
+  float* gam_s = o_s + R * (VT + 1);    // [R]
+  float* rs_s = gam_s + R;              // [R]
+  const int s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x;
+  const int r = tid / VT, c = tid % VT;
+  const int v = blockIdx.x * VT + c;
+  const bool vok = v < V;
+  const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr;
+
+  for (int i = 0; i < KM / 8; ++i) {
+    const int k = r + 8 * i;
+    ds_s[k * (VT + 1) + c] = (gr.dfinal && k < K && vok) ? gr.dfinal[(int64_t)s * K * V + (int64_t)k * V + v] : 0.f;
+  }
+  for (int n = nch - 1; n >= 0; --n) {
+    __syncthreads();
+    const int64_t so = state_off(s, n, nch, K, V);
+    if (vok)
+      for (int i = 0; i < KM / 8; ++i) {
+        const int k = r + 8 * i;
+        if (k < K) gr.dhend[so + (int64_t)k * V + v] = ds_s[k * (VT + 1) + c];
+      }
+    if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+    __syncthreads();
+    const float gc = gam_s[R - 1];
+    if (tid < R) rs_s[tid] = __expf(gc - gam_s[tid]);
+    // dD = dd0 + diag(e^{G_C-G}) Kn dS
+    float acc[R / 8];
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j)
+      acc[j] = (gr.dd0 && vok) ? gr.dd0[rows_off(s, n, nch, r + 8 * j, V) + v] : 0.f;
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(x_s, sv.kn + rows_off(s, n, nch, 0, K), K, k0, rs_s);
+      __syncthreads();
+      for (int kk = 0; kk < KS; ++kk) {
+        const float d = ds_s[(k0 + kk) * (VT + 1) + c];
+#pragma unroll
+        for (int j = 0; j < R / 8; ++j) acc[j] += x_s[(r + 8 * j) * LDS_ + kk] * d;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) {
+      const int t = r + 8 * j;
+      dd_s[t * (VT + 1) + c] = acc[j];
+      if (vok) gr.ddelta[rows_off(s, n, nch, t, V) + v] = acc[j];
+      float o = 0.f;
+      if (has_q && vok) {
+        const int tok = token_at(p, n, t);
+        if (tok >= 0) o = __expf(gam_s[t]) * op_load<E>(gr.dout, b, h, tok, v);
+      }
+      o_s[t * (VT + 1) + c] = o;
+    }
+    // dS_prev = e^{G_C} dS + Qn^T diag(e^G) dO - W^T dD + dstates[n]
+    const float decay = __expf(gc);
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      if (has_q) stage_rows(x_s, sv.qn + rows_off(s, n, nch, 0, K), K, k0, nullptr);
+      stage_rows(y_s, sv.w + rows_off(s, n, nch, 0, K), K, k0, nullptr);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < KS / 8; ++i) {
+        const int kk = r + 8 * i, k = k0 + kk;
+        float x = decay * ds_s[k * (VT + 1) + c];
+        if (has_q)
+          for (int t = 0; t < R; ++t) x += x_s[t * LDS_ + kk] * o_s[t * (VT + 1) + c];
+        for (int t = 0; t < R; ++t) x -= y_s[t * LDS_ + kk] * dd_s[t * (VT + 1) + c];
+        if (gr.dstates && vok && k < K) x += gr.dstates[so + (int64_t)k * V + v];
+        ds_s[k * (VT + 1) + c] = x;
+      }
+    }
+  }
+  __syncthreads();
+  if (vok)
+    for (int i = 0; i < KM / 8; ++i) {
+      const int k = r + 8 * i;
+      if (k < K) gr.ds0[(int64_t)s * K * V + (int64_t)k * V + v] = ds_s[k * (VT + 1) + c];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_chunk_bwd: all per-token gradients of one chunk.
+template <typename E, int KM>
+__global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
+                                                     int nch) {
+  constexpr int NJ = KM / 16;
+  extern __shared__ float smem[];
+  // Phase A layout: five value-column slices.
+  float* pa_do = smem;                      // [R][VT+1]
+  float* pa_d = pa_do + R * (VT + 1);       // [R][VT+1]
+  float* pa_dd = pa_d + R * (VT + 1);       // [R][VT+1]
+  float* pa_h = pa_dd + R * (VT + 1);       // [KM][VT+1]
+  float* pa_dh = pa_h + KM * (VT + 1);      // [KM][VT+1]
+  // Phase B/C layout (aliases phase A).
+  float* pm = smem;                         // [R][LDR]  P then dQK
+  float* km = pm + R * LDR;                 // [R][LDR]  A (strictly lower)
+  float* tm = km + R * LDR;                 // [R][LDR]  T
+  float* dt = tm + R * LDR;                 // [R][LDR]  dT, then dKK sym
+  float* xm = dt + R * LDR;                 // [R][LDR]  scratch R x R
+  float* a_s = xm + R * LDR;                // [R][LDS_]
+  float* b_s = a_s + R * LDS_;              // [R][LDS_]
+  constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
+  constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
+  constexpr int BASE = PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC;
+  float* gam_s = smem + BASE;               // [R]
+  float* bet_s = gam_s + R;                 // [R]
+  float* dgam_s = bet_s + R;                // [R]
+  float* dbet_s = dgam_s + R;               // [R]
+  float* red_s = dbet_s + R;                // [4]
+
+  const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr;
+  const float* kn = sv.kn + rows_off(s, n, nch, 0, K);
+  const float* qn = sv.qn + rows_off(s, n, nch, 0, K);
+  const float* st = sv.states + state_off(s, n, nch, K, V);
+  const float* dh = gr.dhend + state_off(s, n, nch, K, V);
+  const float* dl = sv.delta + rows_off(s, n, nch, 0, V);
+  const float* ddl = gr.ddelta + rows_off(s, n, nch, 0, V);
+  float* dw = gr.dw + rows_off(s, n, nch, 0, K);
+
+  if (tid < R) {
+    gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+    bet_s[tid] = sv.beta[rows_off(s, n, nch, 0, 1) + tid];
+    dgam_s[tid] = 0.f;
+    dbet_s[tid] = 0.f;
+  }
+  if (tid < 4) red_s[tid] = 0.f;
+  __syncthreads();
+  const float gc = gam_s[R - 1];
+
+  // ---- Phase A: value-axis contractions against S_n and dS_{n+1}.
+  float dq[4][NJ] = {}, dk[4][NJ] = {}, dwr[4][NJ] = {};
+  float decay_dot = 0.f;
+  for (int v0 = 0; v0 < V; v0 += VT) {
+    __syncthreads();
+    for (int idx = tid; idx < R * VT; idx += NT) {
+      const int r = idx / VT, c = idx % VT, v = v0 + c;
+      float o = 0.f;
+      if (has_q && v < V) {
+        const int t = token_at(p, n, r);
+        if (t >= 0) o = op_load<E>(gr.dout, b, h, t, v);
+      }
+      pa_do[r * (VT + 1) + c] = o;
+      pa_d[r * (VT + 1) + c] = v < V ? dl[(int64_t)r * V + v] : 0.f;
+      pa_dd[r * (VT + 1) + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+    }
+    for (int idx = tid; idx < KM * VT; idx += NT) {
+      const int k = idx / VT, c = idx % VT, v = v0 + c;
+      const bool ok = k < K && v < V;
+      const float hv = ok ? st[(int64_t)k * V + v] : 0.f;
+      const float dv = ok ? dh[(int64_t)k * V + v] : 0.f;
+      pa_h[k * (VT + 1) + c] = hv;
+      pa_dh[k * (VT + 1) + c] = dv;
+      decay_dot += hv * dv;
+    }
+    __syncthreads();
+    for (int c = 0; c < VT; ++c) {
+      float o[4], d[4], dd[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * ty + i;
+        o[i] = pa_do[t * (VT + 1) + c];
+        d[i] = pa_d[t * (VT + 1) + c];
+        dd[i] = pa_dd[t * (VT + 1) + c];
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int k = tx + 16 * j;
+        const float hv = pa_h[k * (VT + 1) + c], dv = pa_dh[k * (VT + 1) + c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dq[i][j] += o[i] * hv;
+          dwr[i][j] -= dd[i] * hv;
+          dk[i][j] += d[i] * dv;
+        }
+      }
+    }
+  }
+  decay_dot = sum64(decay_dot);
+  if ((tid & 63) == 0) atomicAdd(&red_s[0], decay_dot);
+  // dW to scratch; dQn = e^G dO S^T; dKn = e^{G_C-G} (D dS^T); decay gradients.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 4 * ty + i;
+    const float eg = __expf(gam_s[t]), ek = __expf(gc - gam_s[t]);
+    float rq = 0.f, rk = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int k = tx + 16 * j;
+      if (k < K) dw[(int64_t)t * K + k] = dwr[i][j];
+      dq[i][j] *= eg;
+      dk[i][j] *= ek;
+      if (k < K) {
+        if (has_q) rq += dq[i][j] * qn[(int64_t)t * K + k];  // qn is NULL without a query
+        rk += dk[i][j] * kn[(int64_t)t * K + k];
+      }
+    }
+    rq = sum16(rq);
+    rk = sum16(rk);
+    if (tx == 0) {
+      atomicAdd(&dgam_s[t], (has_q ? rq : 0.f) - rk);
+      atomicAdd(&dgam_s[R - 1], rk);
+    }
+  }
+  if (!has_q) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dq[i][j] = 0.f;
+  }
+  __syncthreads();  // phase A LDS free; dW visible below via global (same block)
+  if (tid == 0) atomicAdd(&dgam_s[R - 1], __expf(gc) * red_s[0]);
+
+  // ---- Phase B: P path (only when there is a read gradient).
+  if (has_q) {
+    build_p<KM>(pm, a_s, b_s, qn, kn, gam_s, K);  // pm = P
+    // xm = causal dO D^T
+    {
+      float acc[4][4] = {};
+      for (int v0 = 0; v0 < V; v0 += KS) {
+        __syncthreads();
+        for (int idx = tid; idx < R * KS; idx += NT) {
+          const int r = idx / KS, c = idx % KS, v = v0 + c;
+          float o = 0.f;
+          const int t = token_at(p, n, r);
+          if (t >= 0 && v < V) o = op_load<E>(gr.dout, b, h, t, v);
+          a_s[r * LDS_ + c] = o;
+          b_s[r * LDS_ + c] = v < V ? dl[(int64_t)r * V + v] : 0.f;
+        }
+        __syncthreads();
+        for (int cc = 0; cc < KS; ++cc) {
+          float a[4], c2[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a[i] = a_s[(4 * ty + i) * LDS_ + cc];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) c2[j] = b_s[(tx + 16 * j) * LDS_ + cc];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c2[j];
+        }
+      }
+      // dP -> decay gradients; dQK = dP e^{G_t-G_s} into pm.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * ty + i;
+        float rowsum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int u = tx + 16 * j;
+          const float dp = (u <= t) ? acc[i][j] : 0.f;
+          const float pv = pm[t * LDR + u];
+          const float g = dp * pv;
+          rowsum += g;
+          atomicAdd(&dgam_s[u], -g);
+          xm[t * LDR + u] = (u <= t) ? dp * __expf(gam_s[t] - gam_s[u]) : 0.f;
+        }
+        rowsum = sum16(rowsum);
+        if (tx == 0) atomicAdd(&dgam_s[t], rowsum);
+      }
+    }
+    __syncthreads();
+    // dQn += dQK Kn ; dKn += dQK^T Qn
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(a_s, kn, K, k0, nullptr);
+      stage_rows(b_s, qn, K, k0, nullptr);
+      __syncthreads();
+      for (int u = 0; u < R; ++u) {
+        float x[4], xt[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = xm[(4 * ty + i) * LDR + u];   // dQK[t][u]
+          xt[i] = xm[u * LDR + 4 * ty + i];    // dQK[u][t]
+        }
+#pragma unroll
+        for (int jj = 0; jj < KS / 16; ++jj) {
+          const int j = k0 / 16 + jj;
+          const float kv = a_s[u * LDS_ + tx + 16 * jj];
+          const float qv = b_s[u * LDS_ + tx + 16 * jj];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dq[i][j] += x[i] * kv;
+            dk[i][j] += xt[i] * qv;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- Phase C: the T = (I+A)^-1 path.
+  __syncthreads();
+  for (int idx = tid; idx < R * R; idx += NT) tm[(idx / R) * LDR + idx % R] = sv.tri[rows_off(s, n, nch, 0, R) + idx];
+  // km = Kn Kn^T;  dt = dD (diag(b) V)^T + dW (diag(b e^G) Kn)^T.
+  {
+    float kk_acc[4][4] = {}, wk_acc[4][4] = {}, dv_acc[4][4] = {};
+    for (int k0 = 0; k0 < KM; k0 += KS) {
+      __syncthreads();
+      stage_rows(a_s, kn, K, k0, nullptr);
+      stage_rows(b_s, dw, K, k0, nullptr);
+      __syncthreads();
+      for (int kk = 0; kk < KS; ++kk) {
+        float a[4], w2[4], c2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = a_s[(4 * ty + i) * LDS_ + kk];
+          w2[i] = b_s[(4 * ty + i) * LDS_ + kk];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c2[j] = a_s[(tx + 16 * j) * LDS_ + kk];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            kk_acc[i][j] += a[i] * c2[j];
+            wk_acc[i][j] += w2[i] * c2[j];
+          }
+      }
+    }
+    for (int v0 = 0; v0 < V; v0 += KS) {
+      __syncthreads();
+      for (int idx = tid; idx < R * KS; idx += NT) {
+        const int r = idx / KS, c = idx % KS, v = v0 + c;
+        a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+        const int t = token_at(p, n, r);
+        b_s[r * LDS_ + c] = (t >= 0 && v < V) ? bet_s[r] * op_load<E>(p.v, b, h, t, v) : 0.f;
+      }
+      __syncthreads();
+      for (int cc = 0; cc < KS; ++cc) {
+        float a[4], c2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = a_s[(4 * ty + i) * LDS_ + cc];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c2[j] = b_s[(tx + 16 * j) * LDS_ + cc];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dv_acc[i][j] += a[i] * c2[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * ty + i, u = tx + 16 * j;
+        km[t * LDR + u] = kk_acc[i][j];
+        dt[t * LDR + u] = dv_acc[i][j] + bet_s[u] * __expf(gam_s[u]) * wk_acc[i][j];
+      }
+  }
+  __syncthreads();
+  // xm = dT T^T ; then dA = -(T^T xm), strictly lower, into dt.
+  {
+    float acc[4][4] = {};
+    for (int u = 0; u < R; ++u) {
+      float a[4], c2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = dt[(4 * ty + i) * LDR + u];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c2[j] = tm[(tx + 16 * j) * LDR + u];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c2[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xm[(4 * ty + i) * LDR + tx + 16 * j] = acc[i][j];
+  }
+  __syncthreads();
+  {
+    float acc[4][4] = {};
+    for (int u = 0; u < R; ++u) {
+      float a[4], c2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = tm[u * LDR + 4 * ty + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c2[j] = xm[u * LDR + tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c2[j];
+    }
+    // dA_ts (s<t) = -acc; A_ts = b_t E_ts KK_ts.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * ty + i;
+      float rb = 0.f, rg = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int u = tx + 16 * j;
+        // Only s < t is live: e^{G_t-G_s} may overflow above the diagonal.
+        const bool live = u < t;
+        const float da = live ? -acc[i][j] : 0.f;
+        const float e = live ? __expf(gam_s[t] - gam_s[u]) : 0.f;
+        const float ekk = e * km[t * LDR + u];
+        rb += da * ekk;
+        const float ga = da * bet_s[t] * ekk;  // dA * A
+        rg += ga;
+        if (live) atomicAdd(&dgam_s[u], -ga);
+        xm[t * LDR + u] = da * bet_s[t] * e;  // dKK (strictly lower)
+      }
+      rb = sum16(rb);
+      rg = sum16(rg);
+      if (tx == 0) {
+        atomicAdd(&dbet_s[t], rb);
+        atomicAdd(&dgam_s[t], rg);
+      }
+    }
+  }
+  __syncthreads();
+  // dt = dKK + dKK^T (symmetric)
+  for (int idx = tid; idx < R * R; idx += NT) {
+    const int t = idx / R, u = idx % R;
+    dt[t * LDR + u] = xm[t * LDR + u] + xm[u * LDR + t];
+  }
+  __syncthreads();
+  // dKn += dKKsym Kn ;  dKn += diag(b e^G) T^T dW, with beta/decay gradients.
+  for (int k0 = 0; k0 < KM; k0 += KS) {
+    __syncthreads();
+    stage_rows(a_s, kn, K, k0, nullptr);
+    stage_rows(b_s, dw, K, k0, nullptr);
+    __syncthreads();
+    float tdw[4][KS / 16] = {};
+    for (int u = 0; u < R; ++u) {
+      float x[4], tt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = dt[(4 * ty + i) * LDR + u];
+        tt[i] = tm[u * LDR + 4 * ty + i];  // T[u][s]
+      }
+#pragma unroll
+      for (int jj = 0; jj < KS / 16; ++jj) {
+        const float kv = a_s[u * LDS_ + tx + 16 * jj];
+        const float wv = b_s[u * LDS_ + tx + 16 * jj];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dk[i][k0 / 16 + jj] += x[i] * kv;
+          tdw[i][jj] += tt[i] * wv;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sr = 4 * ty + i;
+      const float eg = __expf(gam_s[sr]);
+      float rdot = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < KS / 16; ++jj) {
+        const float kv = a_s[sr * LDS_ + tx + 16 * jj];
+        dk[i][k0 / 16 + jj] += bet_s[sr] * eg * tdw[i][jj];
+        rdot += kv * tdw[i][jj];
+      }
+      rdot = sum16(rdot);
+      if (tx == 0) {
+        atomicAdd(&dbet_s[sr], eg * rdot);
+        atomicAdd(&dgam_s[sr], bet_s[sr] * eg * rdot);
+      }
+    }
+  }
+  // dV = diag(b) T^T dD ; dbeta += rows of V . (T^T dD)
+  for (int v0 = 0; v0 < V; v0 += KS) {
+    __syncthreads();
+    for (int idx = tid; idx < R * KS; idx += NT) {
+      const int r = idx / KS, c = idx % KS, v = v0 + c;
+      a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+      const int t = token_at(p, n, r);
+      b_s[r * LDS_ + c] = (t >= 0 && v < V) ? op_load<E>(p.v, b, h, t, v) : 0.f;
+    }
+    __syncthreads();
+    float acc[4][4] = {};
+    for (int u = 0; u < R; ++u) {
+      float tt[4], c2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tt[i] = tm[u * LDR + 4 * ty + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c2[j] = a_s[u * LDS_ + tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += tt[i] * c2[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sr = 4 * ty + i;
+      const int t = token_at(p, n, sr);
+      float rdot = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + tx + 16 * j;
+        rdot += b_s[sr * LDS_ + tx + 16 * j] * acc[i][j];
+        if (t >= 0 && v < V)
+          reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)t * gr.dv.st + v] =
+              bet_s[sr] * acc[i][j];
+      }
+      rdot = sum16(rdot);
+      if (tx == 0) atomicAdd(&dbet_s[sr], rdot);
+    }
+  }
+  __syncthreads();
+
+  // ---- Phase D: g and beta per token; L2-normalisation backward for q, k.
+  if (tid < R) {
+    const int t = token_at(p, n, tid);
+    if (t >= 0) {
+      float acc = 0.f;
+      for (int u = tid; u < R; ++u) acc += dgam_s[u];
+      float* dg = reinterpret_cast<float*>(gr.dg.ptr);
+      float* db = reinterpret_cast<float*>(gr.dbeta.ptr);
+      dg[op_base(gr.dg, b, h) + (int64_t)t * gr.dg.st] = acc;
+      db[op_base(gr.dbeta, b, h) + (int64_t)t * gr.dbeta.st] = dbet_s[tid];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * ty + i;
+    const int t = token_at(p, n, r);
+    for (int which = 0; which < 2; ++which) {
+      if (which == 0 && !has_q) {
+        if (p.q.ptr && gr.dq.ptr && t >= 0)
+          for (int j = 0; j < NJ; ++j) {
+            const int k = tx + 16 * j;
+            if (k < K) reinterpret_cast<float*>(gr.dq.ptr)[op_base(gr.dq, b, h) + (int64_t)t * gr.dq.st + k] = 0.f;
+          }
+        continue;
+      }
+      const gpa_operand& src = which == 0 ? p.q : p.k;
+      const gpa_operand& dst = which == 0 ? gr.dq : gr.dk;
+      float ss = 0.f, dot = 0.f, xs[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int k = tx + 16 * j;
+        xs[j] = (t >= 0 && k < K) ? op_load<E>(src, b, h, t, k) : 0.f;
+        ss += xs[j] * xs[j];
+      }
+      ss = sum16(ss);
+      const float nrm = sqrtf(ss);
+      const float den = fmaxf(nrm, 1e-6f);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dot += (xs[j] / den) * (which == 0 ? dq[i][j] : dk[i][j]);
+      dot = sum16(dot);
+      if (t < 0) continue;
+      float* out = reinterpret_cast<float*>(dst.ptr) + op_base(dst, b, h) + (int64_t)t * dst.st;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int k = tx + 16 * j;
+        if (k >= K) continue;
+        const float g = which == 0 ? dq[i][j] : dk[i][j];
+        out[k] = nrm > 1e-6f ? (g - (xs[j] / den) * dot) / den : g / 1e-6f;
+      }
+    }
+  }
+}
+
+}  // namespace gpa
+
+// ===========================================================================
+// Host launchers.
+namespace {
+
+using namespace gpa;
+
+int check_problem(const gpa_gdn_problem* p) {
+  if (!p) return fail(GPA_HIP_EINVAL, "null problem");
+  if (p->batch < 1 || p->heads < 1 || p->tokens < 1)
+    return fail(GPA_HIP_EINVAL, "gdn: batch, heads and tokens must be >= 1");
+  if (p->chunk < 1 || p->chunk > GPA_CHUNK_ROWS)
+    return fail(GPA_HIP_EINVAL, "gdn: chunk must be in [1, 64]");
+  if (p->offset < 0 || p->offset >= p->chunk)
+    return fail(GPA_HIP_EINVAL, "gdn: offset must be in [0, chunk)");
+  if (p->kdim < 1 || p->kdim > GPA_MAX_KDIM) return fail(GPA_HIP_EUNSUPPORTED, "gdn: key width must be in [1, 256]");
+  if (p->vdim < 1 || p->vdim > GPA_MAX_VDIM) return fail(GPA_HIP_EUNSUPPORTED, "gdn: value width must be in [1, 1024]");
+  if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "gdn: dtype");
+  if (!p->k.ptr || !p->v.ptr || !p->g.ptr || !p->beta.ptr) return fail(GPA_HIP_EINVAL, "gdn: null k/v/g/beta");
+  if ((int64_t)p->batch * p->heads > 65535) return fail(GPA_HIP_EUNSUPPORTED, "gdn: more than 65535 streams");
+  return GPA_HIP_OK;
+}
+
+int kmax_for(int k) { return k <= 64 ? 64 : (k <= 128 ? 128 : 256); }
+
+// Kernels above 64 KiB of dynamic LDS must say so once per instantiation.
+template <typename F>
+int allow_lds(F kernel, size_t bytes) {
+  if (bytes <= 65536) return GPA_HIP_OK;
+  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  return err == hipSuccess ? GPA_HIP_OK : fail(GPA_HIP_EHIP, "hipFuncSetAttribute(max dynamic LDS) failed");
+}
+
+template <typename E, int KM>
+int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, hipStream_t st, int nch) {
+  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
+  const size_t lds_prep = sizeof(float) * (R * (KM + 1) + 3 * R * LDR + 3 * R);
+  if (int rc = allow_lds(gdn_prep<E, KM>, lds_prep)) return rc;
+  hipLaunchKernelGGL((gdn_prep<E, KM>), grid_c, block, lds_prep, st, p, sv, nch);
+  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
+  if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
+  hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
+  if (p.q.ptr && out.ptr) {
+    const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+    hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
+  }
+  return check_launch("gdn_forward");
+}
+
+template <typename E, int KM>
+int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_grads gr, hipStream_t st,
+                    int nch) {
+  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
+  const bool has_q = p.q.ptr && gr.dout.ptr;
+  if (has_q) {
+    const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+    hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
+  } else {
+    gr.dd0 = nullptr;
+  }
+  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
+  if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
+  constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
+  constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
+  const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
+  if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
+  hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  return check_launch("gdn_backward");
+}
+
+template <typename E>
+int dispatch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, hipStream_t st, int nch) {
+  switch (kmax_for(p.kdim)) {
+    case 64: return launch_forward<E, 64>(p, sv, out, st, nch);
+    case 128: return launch_forward<E, 128>(p, sv, out, st, nch);
+    default: return launch_forward<E, 256>(p, sv, out, st, nch);
+  }
+}
+
+template <typename E>
+int dispatch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr,
+                      hipStream_t st, int nch) {
+  switch (kmax_for(p.kdim)) {
+    case 64: return launch_backward<E, 64>(p, sv, gr, st, nch);
+    case 128: return launch_backward<E, 128>(p, sv, gr, st, nch);
+    default: return launch_backward<E, 256>(p, sv, gr, st, nch);
+  }
+}
+
+}  // namespace
+
+extern "C" int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk) {
+  if (tokens < 1 || chunk < 1 || chunk > GPA_CHUNK_ROWS || offset < 0 || offset >= chunk) return 0;
+  return (offset + tokens + chunk - 1) / chunk;
+}
+
+extern "C" int gpa_gdn_forward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved, gpa_operand out,
+                               hipStream_t stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (!saved || !saved->kn || !saved->w || !saved->u || !saved->delta || !saved->tri || !saved->gam ||
+      !saved->beta || !saved->states || !saved->final)
+    return fail(GPA_HIP_EINVAL, "gdn_forward: a saved buffer is null");
+  if (problem->q.ptr && (!saved->qn || !out.ptr)) return fail(GPA_HIP_EINVAL, "gdn_forward: q given without qn/out");
+  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
+  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, *saved, out, stream, nch)
+                                          : dispatch_forward<float>(*problem, *saved, out, stream, nch);
+}
+
+extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved,
+                                const gpa_gdn_grads* grads, hipStream_t stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (!saved || !grads) return fail(GPA_HIP_EINVAL, "gdn_backward: null saved/grads");
+  if (!grads->ddelta || !grads->dhend || !grads->dw || !grads->dk.ptr || !grads->dv.ptr || !grads->dg.ptr ||
+      !grads->dbeta.ptr || !grads->ds0)
+    return fail(GPA_HIP_EINVAL, "gdn_backward: a gradient buffer is null");
+  if (problem->q.ptr && grads->dout.ptr && (!grads->dd0 || !grads->dq.ptr || !saved->qn))
+    return fail(GPA_HIP_EINVAL, "gdn_backward: read gradient needs dd0, dq and qn");
+  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
+  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, stream, nch)
+                                          : dispatch_backward<float>(*problem, *saved, *grads, stream, nch);
+}

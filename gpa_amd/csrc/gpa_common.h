@@ -1,0 +1,36 @@
+// Shared device helpers and host error reporting for libgpa_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gpa {
+
+// bfloat16 is carried as its bit pattern.
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float((uint32_t)x.bits << 16); }
+
+// Round-to-nearest-even float -> bfloat16 (NaN kept quiet).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return bf16_t{(uint16_t)((u >> 16) | 0x40u)};
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16_t{(uint16_t)(u >> 16)};
+}
+
+template <typename E> __device__ __forceinline__ E from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return f32_to_bf16(x); }
+
+// Value after a round trip through E: the reference rounds normalised keys and
+// queries to the activation dtype before the fp32 state arithmetic.
+template <typename E> __device__ __forceinline__ float round_as(float x) { return to_f32(from_f32<E>(x)); }
+
+}  // namespace gpa
+
+// Host side: thread-local last error and launch checking (defined in abi.hip).
+int fail(int code, const char* message);
+int check_launch(const char* what);

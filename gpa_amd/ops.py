@@ -1,0 +1,137 @@
+"""Autograd operators over libgpa_hip.
+
+`gdn_scan_hip` is the HIP replacement of the reference `gdn_scan`
+(src/gpa/ops.py:49-85) for a group of streams laid out as [B,T,H,D], extended
+with what the block-lagged model needs from a chunked scan: the state at the
+start of every chunk (the block boundaries of attention.py:397) and a token
+offset that aligns chunks with blocks that began in an earlier call.
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def _contig_last(x: Tensor) -> Tensor:
+    return x if x.stride(-1) == 1 else x.contiguous()
+
+
+def _f32_state(s: Tensor) -> Tensor:
+    s = s.float() if s.dtype != torch.float32 else s
+    return s if (s.stride(3) == 1 and s.stride(2) == s.shape[3]) else s.contiguous()
+
+
+class _GDNScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int):
+        lib = _lib.load()
+        bsz, tokens, heads, kd = k.shape
+        vd = v.shape[-1]
+        dev = k.device
+        nch = lib.gpa_gdn_nchunks(tokens, offset, chunk)
+        if nch <= 0:
+            raise ValueError("gdn_scan_hip: invalid chunk geometry")
+        streams = bsz * heads
+        rows = streams * nch * _lib.CHUNK_ROWS
+        f32 = dict(device=dev, dtype=torch.float32)
+        kn = torch.empty(rows * kd, **f32)
+        qn = torch.empty(rows * kd, **f32) if q is not None else None
+        w = torch.empty(rows * kd, **f32)
+        u = torch.empty(rows * vd, **f32)
+        delta = torch.empty(rows * vd, **f32)
+        tri = torch.empty(rows * _lib.CHUNK_ROWS, **f32)
+        gam = torch.empty(rows, **f32)
+        bet = torch.empty(rows, **f32)
+        states = torch.empty(bsz, heads, nch, kd, vd, **f32)
+        final = torch.empty(bsz, heads, kd, vd, **f32)
+        out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype) if q is not None else None
+        s0f = _f32_state(s0) if s0 is not None else None
+        prob = _lib.Problem(bsz, heads, tokens, offset, chunk, kd, vd, _lib.DTYPE_CODES[k.dtype],
+                            _lib.operand(q), _lib.operand(k), _lib.operand(v),
+                            _lib.operand(g), _lib.operand(beta),
+                            s0f.data_ptr() if s0f is not None else None,
+                            s0f.stride(0) if s0f is not None else 0, s0f.stride(1) if s0f is not None else 0)
+        saved = _lib.Saved(kn.data_ptr(), qn.data_ptr() if qn is not None else None, w.data_ptr(), u.data_ptr(),
+                           delta.data_ptr(), tri.data_ptr(), gam.data_ptr(), bet.data_ptr(),
+                           states.data_ptr(), final.data_ptr())
+        _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), _lib.stream_handle(dev)), "gpa_gdn_forward")
+        ctx.geom = (chunk, offset, nch, q is not None, s0 is not None)
+        ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final)
+        return out, states, final
+
+    @staticmethod
+    def backward(ctx, dout, dstates, dfinal):
+        lib = _lib.load()
+        chunk, offset, nch, has_q, has_s0 = ctx.geom
+        (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final) = ctx.saved_tensors
+        bsz, tokens, heads, kd = k.shape
+        vd = v.shape[-1]
+        dev = k.device
+        streams = bsz * heads
+        rows = streams * nch * _lib.CHUNK_ROWS
+        f32 = dict(device=dev, dtype=torch.float32)
+        want_read = has_q and dout is not None
+        if want_read:
+            dout = _contig_last(dout.to(k.dtype))
+        dd0 = torch.empty(rows * vd, **f32) if want_read else None
+        ddelta = torch.empty(rows * vd, **f32)
+        dhend = torch.empty(streams * nch * kd * vd, **f32)
+        dw = torch.empty(rows * kd, **f32)
+        dq = torch.zeros(bsz, tokens, heads, kd, **f32) if has_q else None
+        dk = torch.empty(bsz, tokens, heads, kd, **f32)
+        dv = torch.empty(bsz, tokens, heads, vd, **f32)
+        dg = torch.empty(bsz, tokens, heads, **f32)
+        db = torch.empty(bsz, tokens, heads, **f32)
+        ds0 = torch.empty(bsz, heads, kd, vd, **f32)
+        dstates = dstates.float().contiguous() if dstates is not None else None
+        dfinal = dfinal.float().contiguous() if dfinal is not None else None
+        prob = _lib.Problem(bsz, heads, tokens, offset, chunk, kd, vd, _lib.DTYPE_CODES[k.dtype],
+                            _lib.operand(q), _lib.operand(k), _lib.operand(v),
+                            _lib.operand(g), _lib.operand(beta),
+                            s0f.data_ptr() if s0f is not None else None,
+                            s0f.stride(0) if s0f is not None else 0, s0f.stride(1) if s0f is not None else 0)
+        saved = _lib.Saved(kn.data_ptr(), qn.data_ptr() if qn is not None else None, w.data_ptr(), u.data_ptr(),
+                           delta.data_ptr(), tri.data_ptr(), gam.data_ptr(), bet.data_ptr(),
+                           states.data_ptr(), final.data_ptr())
+        grads = _lib.Grads(_lib.operand(dout if want_read else None),
+                           dstates.data_ptr() if dstates is not None else None,
+                           dfinal.data_ptr() if dfinal is not None else None,
+                           dd0.data_ptr() if dd0 is not None else None, ddelta.data_ptr(), dhend.data_ptr(),
+                           dw.data_ptr(), _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
+                           _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
+        _lib.check(lib.gpa_gdn_backward(prob, saved, grads, _lib.stream_handle(dev)), "gpa_gdn_backward")
+        dq_out = dq.to(q.dtype) if (has_q and ctx.needs_input_grad[0]) else None
+        return (dq_out, dk.to(k.dtype), dv.to(v.dtype), dg, db,
+                ds0 if has_s0 else None, None, None)
+
+
+def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor | None,
+                 *, chunk: int, offset: int = 0):
+    """Chunked GDN scan of B*H streams on the GPU.
+
+    q, k [B,T,H,K] (q may be None), v [B,T,H,V] in float32 or bfloat16 with a
+    contiguous last axis; g, beta [B,T,H] float32 (any strides, e.g. expanded
+    constants); s0 [B,H,K,V] (None = zeros).  Returns
+    (out [B,T,H,V] or None, states [B,H,N,K,V], final [B,H,K,V]) where
+    states[:, :, n] is the state at the start of chunk n and chunk 0 begins
+    `offset` positions before token 0.
+    """
+    _lib.require_device(k)
+    if k.dtype not in _lib.DTYPE_CODES or v.dtype != k.dtype or (q is not None and q.dtype != k.dtype):
+        raise ValueError("gdn_scan_hip: q/k/v must share float32 or bfloat16")
+    if k.ndim != 4 or v.ndim != 4 or v.shape[:3] != k.shape[:3] or (q is not None and q.shape != k.shape):
+        raise ValueError("gdn_scan_hip: expected q,k [B,T,H,K] and v [B,T,H,V]")
+    if g.shape != k.shape[:3] or beta.shape != k.shape[:3]:
+        raise ValueError("gdn_scan_hip: g and beta must be [B,T,H]")
+    if k.shape[-1] > _lib.MAX_KDIM or v.shape[-1] > _lib.MAX_VDIM:
+        raise ValueError(f"gdn_scan_hip: widths above K={_lib.MAX_KDIM}, V={_lib.MAX_VDIM} are not built")
+    if s0 is not None and s0.shape != (k.shape[0], k.shape[2], k.shape[3], v.shape[3]):
+        raise ValueError("gdn_scan_hip: s0 must be [B,H,K,V]")
+    if not 1 <= chunk <= _lib.CHUNK_ROWS or not 0 <= offset < chunk:
+        raise ValueError("gdn_scan_hip: need 1 <= chunk <= 64 and 0 <= offset < chunk")
+    q = _contig_last(q) if q is not None else None
+    k, v = _contig_last(k), _contig_last(v)
+    g, beta = g.float(), beta.float()
+    return _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)

@@ -1,0 +1,116 @@
+/*
+ * gpa_hip.h -- C ABI of libgpa_hip.so, the gfx950 HIP backend of the DenseGPA
+ * attention core.
+ *
+ * Every entry point takes plain device pointers, sizes and element strides,
+ * enqueues its kernels on the given HIP stream and returns 0 on success or a
+ * negative GPA_HIP_E* code; gpa_hip_last_error() then describes the failure
+ * (per calling thread).  The library never allocates device memory, never
+ * synchronises and keeps no mutable global state: every buffer (inputs,
+ * outputs, the intermediates a backward pass needs) is owned by the caller,
+ * so calls are reentrant and may be captured into a HIP graph.
+ *
+ * Operand convention.  A scan runs `batch*heads` independent streams.  Element
+ * (stream s = b*heads + h, token t, feature d) of a gpa_operand lives at
+ * ptr[b*sb + t*st + h*sh + d]: this addresses the reference's time-first
+ * [B,T,H,D] tensors (and any packed or expanded view of them) without copies.
+ * Per-token scalars (g, beta, their gradients) use the same rule with d = 0.
+ *
+ * Chunk geometry.  Position p of a stream holds token t = p - offset; the
+ * positions before token 0 and after token T-1 are "void" (no state change, no
+ * output).  Chunk n covers positions [n*chunk, (n+1)*chunk) and is stored as
+ * GPA_CHUNK_ROWS rows, the rows past `chunk` also void.  nchunks =
+ * ceil((offset + tokens) / chunk).  Chunk boundaries are the block boundaries
+ * of the block-lagged model (reference src/gpa/attention.py:397).
+ */
+#ifndef GPA_HIP_H
+#define GPA_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPA_HIP_ABI_VERSION 1
+#define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
+#define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
+#define GPA_MAX_VDIM 1024   /* value width of a scan */
+
+#define GPA_HIP_OK 0
+#define GPA_HIP_EINVAL (-1)      /* bad argument: shape, pointer, stride */
+#define GPA_HIP_EUNSUPPORTED (-2) /* valid but not built: dtype, width */
+#define GPA_HIP_EHIP (-3)        /* a HIP runtime call failed */
+
+#define GPA_DTYPE_F32 0
+#define GPA_DTYPE_BF16 1
+
+typedef struct gpa_operand {
+    void *ptr;
+    int64_t sb, st, sh;
+} gpa_operand;
+
+/* One group of GDN scans with common widths (reference ops.py:49-85 and the
+ * packed level/edge launches of packed.py:77,121,155). */
+typedef struct gpa_gdn_problem {
+    int32_t batch, heads;   /* streams = batch*heads */
+    int32_t tokens;         /* T >= 1 real tokens */
+    int32_t offset;         /* void positions before token 0, 0 <= offset < chunk */
+    int32_t chunk;          /* 1..GPA_CHUNK_ROWS */
+    int32_t kdim, vdim;     /* 1..GPA_MAX_KDIM, 1..GPA_MAX_VDIM */
+    int32_t dtype;          /* GPA_DTYPE_*: q, k, v, out, dout element type */
+    gpa_operand q, k, v;    /* q.ptr may be NULL: no output read */
+    gpa_operand g, beta;    /* float32 log-decay (<= 0) and write strength */
+    const float *s0;        /* [batch,heads,K,V] at s0[b*s0_sb + h*s0_sh + k*V + v]; NULL = zeros */
+    int64_t s0_sb, s0_sh;
+} gpa_gdn_problem;
+
+/* Caller-owned float32 intermediates, all stream-major and contiguous:
+ *   kn, qn, w      [streams, nchunks, 64, K]  normalised keys/queries, W = T diag(b e^G) Kn
+ *   u, delta       [streams, nchunks, 64, V]  U = T diag(b) V, delta = U - W S_n
+ *   tri            [streams, nchunks, 64, 64] T = (I + A)^-1
+ *   gam, beta      [streams, nchunks, 64]     in-chunk cumulative log decay, beta (void rows 0)
+ *   states         [streams, nchunks, K, V]   state at the start of every chunk
+ *   final          [streams, K, V]            state after the last token
+ * qn is written only when problem.q.ptr != NULL. */
+typedef struct gpa_gdn_saved {
+    float *kn, *qn, *w, *u, *delta, *tri, *gam, *beta, *states, *final;
+} gpa_gdn_saved;
+
+/* Backward inputs and outputs.  dout (problem dtype, strided like out) may be
+ * NULL (no read gradient); dstates [streams,nchunks,K,V] injects gradients of
+ * the chunk-start states (NULL = none); dfinal [streams,K,V] (NULL = none).
+ * Scratch (caller-owned float32): dd [streams,nchunks,64,V] x2, dhend
+ * [streams,nchunks,K,V], dw [streams,nchunks,64,K].  Gradient outputs are
+ * float32 operands: dq (skipped when q was NULL), dk [.. K], dv [.. V],
+ * dg, dbeta per token; ds0 [streams,K,V] contiguous. */
+typedef struct gpa_gdn_grads {
+    gpa_operand dout;
+    const float *dstates, *dfinal;
+    float *dd0, *ddelta, *dhend, *dw;
+    gpa_operand dq, dk, dv, dg, dbeta;
+    float *ds0;
+} gpa_gdn_grads;
+
+int gpa_hip_abi_version(void);
+const char *gpa_hip_last_error(void);
+/* Number of chunks a problem spans (0 on invalid geometry). */
+int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk);
+
+/* Forward chunked gated-delta-rule scan; `out` (problem dtype) receives
+ * u(q_t)^T S_t when q.ptr != NULL.
+ * Replaces reference src/gpa/ops.py:49-85 (gdn_scan, backend dispatch at
+ * ops.py:58-79) for a whole group of streams. */
+int gpa_gdn_forward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
+                    gpa_operand out, hipStream_t stream);
+
+/* Backward of gpa_gdn_forward from its saved intermediates (the autograd of
+ * ops.py:49-85 in the reference, plus chunk-start state injections). */
+int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
+                     const gpa_gdn_grads *grads, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GPA_HIP_H */

@@ -1,0 +1,57 @@
+"""The C ABI library builds, loads on a CPU-only host and exports every symbol
+that include/gpa_hip.h declares (no compute call is made here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gpa_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(gpa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks",
+                     "gpa_gdn_forward", "gpa_gdn_backward"):
+        assert expected in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from gpa_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libgpa_hip.so not built (python -m gpa_amd.build)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    typed = _lib.load()
+    assert typed.gpa_hip_abi_version() == _lib.ABI_VERSION
+    assert set(_lib.EXPORTS) <= set(_declared())
+    # Pure host helpers.
+    assert typed.gpa_gdn_nchunks(130, 0, 64) == 3
+    assert typed.gpa_gdn_nchunks(1, 63, 64) == 1
+    assert typed.gpa_gdn_nchunks(2, 63, 64) == 2
+    assert typed.gpa_gdn_nchunks(5, 4, 4) == 0  # offset must be < chunk
+
+
+def test_ctypes_structs_match_c_layout():
+    from gpa_amd import _lib
+    assert ctypes.sizeof(_lib.Operand) == 32
+    # 8 int32, 5 operands, pointer + 2 int64
+    assert ctypes.sizeof(_lib.Problem) == 32 + 5 * 32 + 24
+    assert ctypes.sizeof(_lib.Saved) == 10 * 8
+    assert ctypes.sizeof(_lib.Grads) == 32 + 6 * 8 + 5 * 32 + 8
+
+
+def test_backend_refuses_cpu_tensors():
+    import torch
+    from gpa_amd import _lib
+    from gpa_amd.ops import gdn_scan_hip
+    x = torch.zeros(1, 2, 1, 4)
+    with pytest.raises(_lib.HipBackendError):
+        gdn_scan_hip(x, x, x, torch.zeros(1, 2, 1), torch.zeros(1, 2, 1), None, chunk=2)

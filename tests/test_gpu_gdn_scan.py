@@ -1,0 +1,159 @@
+"""HIP chunked GDN scan vs the oracle's per-token recurrence (reference ops.py:29-85).
+
+The HIP operator returns the read, the state at the start of every chunk and
+the final state; its backward takes gradients for all three.  The oracle runs
+the literal recurrence in float64 on the CPU from the same inputs (bf16 inputs
+are compared after their exact widening), segment by segment so that the
+chunk-start states are observable.
+"""
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _inputs(b, t, h, kd, vd, dtype, seed, q=True, s0=True, const_gates=False):
+    g = torch.Generator().manual_seed(seed)
+    qq = torch.randn(b, t, h, kd, generator=g) if q else None
+    kk = torch.randn(b, t, h, kd, generator=g)
+    vv = torch.randn(b, t, h, vd, generator=g)
+    if const_gates:
+        gate = -torch.rand(1, 1, h, generator=g).expand(b, t, h) * .5
+        beta = torch.rand(1, 1, h, generator=g).expand(b, t, h)
+    else:
+        gate = -torch.rand(b, t, h, generator=g) * .5
+        beta = torch.rand(b, t, h, generator=g)
+    state = torch.randn(b, h, kd, vd, generator=g) * .3 if s0 else None
+    cast = lambda x: None if x is None else x.to(dtype)  # noqa: E731
+    return cast(qq), cast(kk), cast(vv), gate, beta, state
+
+
+def _oracle_segments(q, k, v, g, beta, s0, chunk, offset):
+    """Per-token oracle in float64; returns out, chunk-start states, final."""
+    b, t, h, kd = k.shape
+    vd = v.shape[-1]
+    d = lambda x: None if x is None else x.detach().double()  # noqa: E731
+    q, k, v, g, beta = d(q), d(k), d(v), d(g), d(beta)
+    state = d(s0) if s0 is not None else torch.zeros(b, h, kd, vd, dtype=torch.float64)
+    nch = (offset + t + chunk - 1) // chunk
+    outs, starts = [], []
+    for n in range(nch):
+        lo, hi = max(0, n * chunk - offset), min(t, (n + 1) * chunk - offset)
+        starts.append(state)
+        qq = q[:, lo:hi] if q is not None else k[:, lo:hi]
+        y, state = oracle.gdn_scan(qq, k[:, lo:hi], v[:, lo:hi], g[:, lo:hi], beta[:, lo:hi], state)
+        outs.append(y)
+    return torch.cat(outs, 1), torch.stack(starts, 2), state
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+CASES = [
+    # (B, T, H, K, V, chunk, offset, dtype)
+    (2, 9, 2, 4, 3, 3, 0, torch.float32),
+    (2, 9, 2, 4, 3, 4, 2, torch.float32),
+    (1, 1, 3, 32, 48, 64, 5, torch.float32),
+    (1, 130, 2, 32, 48, 64, 0, torch.float32),
+    (1, 70, 2, 64, 128, 64, 17, torch.float32),
+    (1, 130, 1, 128, 128, 64, 0, torch.float32),
+    (1, 96, 1, 128, 256, 64, 0, torch.float32),
+    (1, 96, 1, 256, 128, 64, 30, torch.float32),
+    (1, 130, 2, 128, 128, 64, 0, torch.bfloat16),
+    (1, 64, 1, 256, 256, 64, 0, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}K{c[3]}V{c[4]}C{c[5]}o{c[6]}{str(c[7])[6:]}")
+def test_gdn_forward_matches_recurrence(case):
+    from gpa_amd.ops import gdn_scan_hip
+    b, t, h, kd, vd, chunk, offset, dtype = case
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=hash(case) % 1000)
+    out, states, final = gdn_scan_hip(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), s0.to(DEV),
+                                      chunk=chunk, offset=offset)
+    ref_out, ref_states, ref_final = _oracle_segments(q, k, v, g, beta, s0, chunk, offset)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    print(case, "out", _rel(out, ref_out), "states", _rel(states, ref_states), "final", _rel(final, ref_final))
+    assert out.dtype == dtype
+    assert _rel(out, ref_out) < tol
+    assert _rel(states, ref_states) < tol
+    assert _rel(final, ref_final) < tol
+
+
+@pytest.mark.parametrize("case", CASES[:8] + CASES[8:], ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}K{c[3]}V{c[4]}C{c[5]}o{c[6]}{str(c[7])[6:]}")
+@pytest.mark.parametrize("with_q", [True, False])
+def test_gdn_backward_matches_autograd_of_recurrence(case, with_q):
+    from gpa_amd.ops import gdn_scan_hip
+    b, t, h, kd, vd, chunk, offset, dtype = case
+    if t > 96 and kd * vd > 128 * 128:
+        pytest.skip("oracle autograd too slow at this size")
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=7 + hash(case) % 1000, q=with_q,
+                                   const_gates=(kd == 32))
+    gen = torch.Generator().manual_seed(3)
+    nch = (offset + t + chunk - 1) // chunk
+    w_out = torch.randn(b, t, h, vd, generator=gen, dtype=torch.float64)
+    w_states = torch.randn(b, h, nch, kd, vd, generator=gen, dtype=torch.float64) * .1
+    w_final = torch.randn(b, h, kd, vd, generator=gen, dtype=torch.float64)
+
+    def loss(out, states, final):
+        total = (states.double() * w_states.to(states.device)).sum() + (final.double() * w_final.to(final.device)).sum()
+        if out is not None:
+            total = total + (out.double() * w_out.to(out.device)).sum()
+        return total
+
+    # HIP
+    leaves = [x.to(DEV).requires_grad_() if x is not None else None for x in (q, k, v)]
+    g_d = g.to(DEV).requires_grad_()
+    b_d = beta.to(DEV).requires_grad_()
+    s_d = s0.to(DEV).requires_grad_()
+    out, states, final = gdn_scan_hip(leaves[0], leaves[1], leaves[2], g_d, b_d, s_d, chunk=chunk, offset=offset)
+    loss(out, states, final).backward()
+    # Oracle in float64 from the same (possibly bf16-valued) inputs.
+    ref_leaves = [x.detach().double().requires_grad_() if x is not None else None for x in (q, k, v)]
+    g_r = g.double().requires_grad_()
+    b_r = beta.double().requires_grad_()
+    s_r = s0.double().requires_grad_()
+    ro, rs, rf = _oracle_segments_autograd(ref_leaves, g_r, b_r, s_r, chunk, offset)
+    loss(ro if with_q else None, rs, rf).backward()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    pairs = [("dk", leaves[1].grad, ref_leaves[1].grad), ("dv", leaves[2].grad, ref_leaves[2].grad),
+             ("dg", g_d.grad, g_r.grad), ("dbeta", b_d.grad, b_r.grad), ("ds0", s_d.grad, s_r.grad)]
+    if with_q:
+        pairs.append(("dq", leaves[0].grad, ref_leaves[0].grad))
+    errs = {name: _rel(a, r) for name, a, r in pairs}
+    print(case, with_q, errs)
+    assert all(e < tol for e in errs.values()), errs
+
+
+def _oracle_segments_autograd(leaves, g, beta, s0, chunk, offset):
+    q, k, v = leaves
+    b, t, h, kd = k.shape
+    vd = v.shape[-1]
+    state = s0
+    nch = (offset + t + chunk - 1) // chunk
+    outs, starts = [], []
+    for n in range(nch):
+        lo, hi = max(0, n * chunk - offset), min(t, (n + 1) * chunk - offset)
+        starts.append(state)
+        qq = q[:, lo:hi] if q is not None else k[:, lo:hi]
+        y, state = oracle.gdn_scan(qq, k[:, lo:hi], v[:, lo:hi], g[:, lo:hi], beta[:, lo:hi], state)
+        outs.append(y)
+    return torch.cat(outs, 1), torch.stack(starts, 2), state
+
+
+def test_gdn_rejects_bad_geometry_before_launch():
+    from gpa_amd.ops import gdn_scan_hip
+    q, k, v, g, beta, s0 = _inputs(1, 4, 1, 8, 8, torch.float32, seed=1)
+    with pytest.raises(ValueError):
+        gdn_scan_hip(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), s0.to(DEV), chunk=65)
+    with pytest.raises(ValueError):
+        gdn_scan_hip(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), s0.to(DEV), chunk=4, offset=4)
+    big = torch.zeros(1, 4, 1, 300, device=DEV)
+    with pytest.raises(ValueError):
+        gdn_scan_hip(big, big, v.to(DEV), g.to(DEV), beta.to(DEV), None, chunk=4)
