@@ -12,7 +12,8 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
+MAX_TIMED = 4
 CHUNK_ROWS = 64
 MAX_KDIM = 256
 MAX_VDIM = 1024
@@ -44,13 +45,18 @@ class Grads(ctypes.Structure):
                 ("ds0", c_vp)]
 
 
+class Timing(ctypes.Structure):
+    _fields_ = [("events", c_vp * (MAX_TIMED + 1)), ("launched", c_i32)]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
     "gpa_gdn_nchunks": ([c_i32, c_i32, c_i32], c_i32),
-    "gpa_gdn_forward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, c_vp], ctypes.c_int),
-    "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads), c_vp],
-                         ctypes.c_int),
+    "gpa_gdn_forward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, ctypes.POINTER(Timing), c_vp],
+                        ctypes.c_int),
+    "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads),
+                          ctypes.POINTER(Timing), c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -28,3 +28,9 @@ int check_launch(const char* what) {
 extern "C" int gpa_hip_abi_version(void) { return GPA_HIP_ABI_VERSION; }
 
 extern "C" const char* gpa_hip_last_error(void) { return g_last_error.c_str(); }
+
+void mark(gpa_timing* timing, hipStream_t stream) {
+  if (!timing || timing->launched > GPA_MAX_TIMED) return;
+  (void)hipEventRecord(timing->events[timing->launched], stream);
+  timing->launched += 1;
+}

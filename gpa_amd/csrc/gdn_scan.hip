@@ -1082,29 +1082,35 @@ int allow_lds(F kernel, size_t bytes) {
 }
 
 template <typename E, int KM>
-int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, hipStream_t st, int nch) {
+int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, gpa_timing* tm,
+                   hipStream_t st, int nch) {
   const dim3 grid_c(nch, p.batch * p.heads), block(NT);
   const size_t lds_prep = sizeof(float) * (R * (KM + 1) + 3 * R * LDR + 3 * R);
   if (int rc = allow_lds(gdn_prep<E, KM>, lds_prep)) return rc;
+  mark(tm, st);
   hipLaunchKernelGGL((gdn_prep<E, KM>), grid_c, block, lds_prep, st, p, sv, nch);
   const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
   const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
   if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
+  mark(tm, st);
   hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
   if (p.q.ptr && out.ptr) {
     const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+    mark(tm, st);
     hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
   }
+  mark(tm, st);
   return check_launch("gdn_forward");
 }
 
 template <typename E, int KM>
-int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_grads gr, hipStream_t st,
-                    int nch) {
+int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_grads gr, gpa_timing* tm,
+                    hipStream_t st, int nch) {
   const dim3 grid_c(nch, p.batch * p.heads), block(NT);
   const bool has_q = p.q.ptr && gr.dout.ptr;
   if (has_q) {
     const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+    mark(tm, st);
     hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
   } else {
     gr.dd0 = nullptr;
@@ -1112,31 +1118,35 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
   const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
   const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
   if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
+  mark(tm, st);
   hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
   constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
   constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
   const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
   if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
+  mark(tm, st);
   hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  mark(tm, st);
   return check_launch("gdn_backward");
 }
 
 template <typename E>
-int dispatch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, hipStream_t st, int nch) {
+int dispatch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, gpa_timing* tm,
+                     hipStream_t st, int nch) {
   switch (kmax_for(p.kdim)) {
-    case 64: return launch_forward<E, 64>(p, sv, out, st, nch);
-    case 128: return launch_forward<E, 128>(p, sv, out, st, nch);
-    default: return launch_forward<E, 256>(p, sv, out, st, nch);
+    case 64: return launch_forward<E, 64>(p, sv, out, tm, st, nch);
+    case 128: return launch_forward<E, 128>(p, sv, out, tm, st, nch);
+    default: return launch_forward<E, 256>(p, sv, out, tm, st, nch);
   }
 }
 
 template <typename E>
 int dispatch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr,
-                      hipStream_t st, int nch) {
+                      gpa_timing* tm, hipStream_t st, int nch) {
   switch (kmax_for(p.kdim)) {
-    case 64: return launch_backward<E, 64>(p, sv, gr, st, nch);
-    case 128: return launch_backward<E, 128>(p, sv, gr, st, nch);
-    default: return launch_backward<E, 256>(p, sv, gr, st, nch);
+    case 64: return launch_backward<E, 64>(p, sv, gr, tm, st, nch);
+    case 128: return launch_backward<E, 128>(p, sv, gr, tm, st, nch);
+    default: return launch_backward<E, 256>(p, sv, gr, tm, st, nch);
   }
 }
 
@@ -1148,7 +1158,7 @@ extern "C" int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk
 }
 
 extern "C" int gpa_gdn_forward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved, gpa_operand out,
-                               hipStream_t stream) {
+                               gpa_timing* timing, hipStream_t stream) {
   int rc = check_problem(problem);
   if (rc) return rc;
   if (!saved || !saved->kn || !saved->w || !saved->u || !saved->delta || !saved->tri || !saved->gam ||
@@ -1156,12 +1166,13 @@ extern "C" int gpa_gdn_forward(const gpa_gdn_problem* problem, const gpa_gdn_sav
     return fail(GPA_HIP_EINVAL, "gdn_forward: a saved buffer is null");
   if (problem->q.ptr && (!saved->qn || !out.ptr)) return fail(GPA_HIP_EINVAL, "gdn_forward: q given without qn/out");
   const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
-  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, *saved, out, stream, nch)
-                                          : dispatch_forward<float>(*problem, *saved, out, stream, nch);
+  if (timing) timing->launched = 0;
+  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, *saved, out, timing, stream, nch)
+                                          : dispatch_forward<float>(*problem, *saved, out, timing, stream, nch);
 }
 
 extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved,
-                                const gpa_gdn_grads* grads, hipStream_t stream) {
+                                const gpa_gdn_grads* grads, gpa_timing* timing, hipStream_t stream) {
   int rc = check_problem(problem);
   if (rc) return rc;
   if (!saved || !grads) return fail(GPA_HIP_EINVAL, "gdn_backward: null saved/grads");
@@ -1171,6 +1182,7 @@ extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_sa
   if (problem->q.ptr && grads->dout.ptr && (!grads->dd0 || !grads->dq.ptr || !saved->qn))
     return fail(GPA_HIP_EINVAL, "gdn_backward: read gradient needs dd0, dq and qn");
   const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
-  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, stream, nch)
-                                          : dispatch_backward<float>(*problem, *saved, *grads, stream, nch);
+  if (timing) timing->launched = 0;
+  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, timing, stream, nch)
+                                          : dispatch_backward<float>(*problem, *saved, *grads, timing, stream, nch);
 }

@@ -34,3 +34,7 @@ template <typename E> __device__ __forceinline__ float round_as(float x) { retur
 // Host side: thread-local last error and launch checking (defined in abi.hip).
 int fail(int code, const char* message);
 int check_launch(const char* what);
+
+// Records timing->events[timing->launched++] on `stream` (no-op without timing).
+struct gpa_timing;
+void mark(gpa_timing* timing, hipStream_t stream);

@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, profiling
 
 
 def _contig_last(x: Tensor) -> Tensor:
@@ -56,7 +56,9 @@ class _GDNScan(torch.autograd.Function):
         saved = _lib.Saved(kn.data_ptr(), qn.data_ptr() if qn is not None else None, w.data_ptr(), u.data_ptr(),
                            delta.data_ptr(), tri.data_ptr(), gam.data_ptr(), bet.data_ptr(),
                            states.data_ptr(), final.data_ptr())
-        _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), _lib.stream_handle(dev)), "gpa_gdn_forward")
+        timing = profiling.forward_timing(kd, vd, chunk, tokens * streams, k.dtype, q is not None)
+        _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), timing, _lib.stream_handle(dev)),
+                   "gpa_gdn_forward")
         ctx.geom = (chunk, offset, nch, q is not None, s0 is not None)
         ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final)
         return out, states, final
@@ -101,7 +103,8 @@ class _GDNScan(torch.autograd.Function):
                            dd0.data_ptr() if dd0 is not None else None, ddelta.data_ptr(), dhend.data_ptr(),
                            dw.data_ptr(), _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
                            _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
-        _lib.check(lib.gpa_gdn_backward(prob, saved, grads, _lib.stream_handle(dev)), "gpa_gdn_backward")
+        timing = profiling.backward_timing(kd, vd, chunk, tokens * streams, k.dtype, want_read)
+        _lib.check(lib.gpa_gdn_backward(prob, saved, grads, timing, _lib.stream_handle(dev)), "gpa_gdn_backward")
         dq_out = dq.to(q.dtype) if (has_q and ctx.needs_input_grad[0]) else None
         return (dq_out, dk.to(k.dtype), dv.to(v.dtype), dg, db,
                 ds0 if has_s0 else None, None, None)

@@ -1,0 +1,270 @@
+"""Level-major block-lagged schedule of the DenseGPA core on the HIP backend.
+
+The reference walks the sequence block by block (attention.py:376-405) and,
+inside each block, level by level (attention.py:309-329).  Block n of level
+j+1 only needs level j's *block-start* states, and the level-j recurrences
+never depend on the query (docs/EQUATIONS.md:57-60).  So this schedule runs
+each level once over the whole call:
+
+  for level j:   A_j scan (reads raw_j = u(q)^T A_t, keeps A at every block start)
+                 B_j scan (state only, keeps B at every block start)
+                 writes a_j = softmax(u(key) A_hat), counts, logits and the
+                 residual key/value of level j+1 from those block-start states
+  all edges:     R_ij scans (messages u(p_i)^T R_t)
+  route reader:  edge softmax -> aggregate -> normalise/tanh -> route MLP -> q_out
+  outer reads:   o_j = u(q_out_j)^T B_t, mixed over levels
+
+Every GDN recurrence is the HIP chunked scan (`ops.gdn_scan_hip`, chunks
+aligned with the model's blocks, including a block begun in an earlier call).
+The per-token glue between scans runs as float32 device tensor ops, rounding
+to the activation dtype where the reference rounds.  There is no CPU path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib
+from .ops import gdn_scan_hip
+from .state import GPAState, LevelState, RelationState, ResidualSnapshot
+
+_F32 = torch.float32
+
+
+def _unit(x: Tensor) -> Tensor:
+    """u(x) computed in float32, rounded back to x's dtype (ops.py:14-17)."""
+    return F.normalize(x.float(), p=2, dim=-1, eps=1e-6).to(x.dtype)
+
+
+def _mm(x: Tensor, w: Tensor, eq: str, dtype: torch.dtype) -> Tensor:
+    """A dtype-typed einsum: operands rounded to `dtype`, float32 accumulate,
+    result rounded to `dtype` (what a bf16 einsum with fp32 accumulation does)."""
+    return torch.einsum(eq, x.to(dtype).float(), w.to(dtype).float()).to(dtype)
+
+
+class _Blocks:
+    """Token <-> (block, row) views for a call that starts `offset` rows into a block."""
+
+    def __init__(self, tokens: int, offset: int, chunk: int):
+        self.t, self.o, self.c = tokens, offset, chunk
+        self.n = (offset + tokens + chunk - 1) // chunk
+        self.tail = self.n * chunk - offset - tokens
+
+    def split(self, x: Tensor) -> Tensor:
+        """[B,T,H,D] -> [B,N,C,H,D] with void rows zero."""
+        y = F.pad(x, (0, 0, 0, 0, self.o, self.tail))
+        return y.view(x.shape[0], self.n, self.c, *x.shape[2:])
+
+    def merge(self, y: Tensor) -> Tensor:
+        return y.reshape(y.shape[0], self.n * self.c, *y.shape[3:])[:, self.o:self.o + self.t]
+
+
+def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
+    """Frozen state of every block: the cached snapshot for block 0, the scan's
+    block-start states after it (attention.py:304, 342-344)."""
+    if starts.shape[2] == 1:
+        return first.unsqueeze(2)
+    return torch.cat((first.unsqueeze(2).to(starts.dtype), starts[:, :, 1:]), dim=2)
+
+
+class _Level:
+    __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "logits", "a_final", "b_final",
+                 "a_starts", "b_starts")
+
+
+def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, position_ids: Tensor,
+                control: Tensor | None, *, want_routes: bool = False):
+    cfg = model.config
+    _lib.require_device(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("backend='hip' computes in float32 or bfloat16 activations")
+    if cfg.positional_mode == "moments":
+        raise ValueError("positional_mode='moments' is not built for backend='hip'")
+    bsz, tokens, heads, dk = q.shape
+    dtype = q.dtype
+    chunk, offset = cfg.chunk_size, state.chunk_offset
+    blocks = _Blocks(tokens, offset, chunk)
+    frozen0 = state.frozen or tuple(ResidualSnapshot(lv.inner, lv.outer) for lv in state.levels)
+    scan = dict(chunk=chunk, offset=offset)
+
+    # ---- level pass (storage + inner reads), attention.py:309-329
+    key, value = k, v
+    levels: list[_Level] = []
+    for j, (old, snap) in enumerate(zip(state.levels, frozen0)):
+        lv = _Level()
+        slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
+        g_in, b_in, g_out, b_out = _gates(model, key, j, control)
+        raw, a_starts, a_final = gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan)
+        _, b_starts, b_final = gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **scan)
+        a_hat = _snapshots(a_starts, snap.inner)       # [B,H,N,Dk,M]
+        b_hat = _snapshots(b_starts, snap.outer)       # [B,H,N,M,Dv]
+        write = _assignment(cfg, slot)
+        if write is None:
+            kb = blocks.split(_unit(key).float())       # [B,N,C,H,Dk]
+            write = blocks.merge(torch.einsum("bnchd,bhndm->bnchm", kb, a_hat)).softmax(-1)
+        write = write.to(dtype)
+        counts = old.count[:, None] + write.float().cumsum(1)
+        wb = blocks.split(write.float())
+        rk = blocks.merge(torch.einsum("bhndm,bnchm->bnchd", a_hat, wb))
+        rv = blocks.merge(torch.einsum("bnchm,bhnmv->bnchv", wb, b_hat))
+        lv.slot, lv.value, lv.g_out, lv.b_out = slot, value, g_out, b_out
+        lv.write, lv.counts = write, counts
+        lv.logits = _base_logits(model, raw, counts, j)
+        lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, a_starts, b_starts
+        levels.append(lv)
+        key, value = _residual(model, key, value, rk, rv, j)
+
+    # ---- relations, attention.py:206-223
+    local = [lv.logits.softmax(-1).to(dtype) for lv in levels]
+    incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan)
+
+    # ---- route reader, attention.py:225-262
+    routes, queries = _bridge(model, q, [lv.logits for lv in levels], incoming, [lv.counts for lv in levels])
+
+    # ---- outer reads and level mix, attention.py:333-341
+    weights = model.output_logits.softmax(0)
+    out = 0
+    for j, (lv, qo) in enumerate(zip(levels, queries)):
+        read, _, _ = gdn_scan_hip(qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer, **scan)
+        out = out + weights[j][..., None] * read
+    out = out.to(v.dtype)
+
+    # ---- new cache, attention.py:342-344
+    new_offset = (offset + tokens) % chunk
+    frozen = None
+    if new_offset:
+        last = blocks.n - 1
+        frozen = frozen0 if last == 0 else tuple(
+            ResidualSnapshot(lv.a_starts[:, :, last], lv.b_starts[:, :, last]) for lv in levels)
+    new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.counts[:, -1], None) for lv in levels)
+    new_state = GPAState(new_levels, relations, state.position + tokens, chunk, new_offset, frozen)
+    return out, new_state, (tuple(routes) if want_routes else None)
+
+
+# --------------------------------------------------------------------------- glue
+def _slot_feature(cfg, x: Tensor) -> Tensor:
+    """attention.py:179-184."""
+    if cfg.slot_feature == "softmax":
+        return (cfg.slot_scale * x.float()).softmax(-1).to(x.dtype)
+    if cfg.slot_feature == "tanh":
+        return (cfg.slot_scale * x.float()).tanh().to(x.dtype)
+    return x
+
+
+def _assignment(cfg, slot: Tensor):
+    """attention.py:186-188."""
+    if cfg.slot_feature == "softmax":
+        return slot
+    return (slot / .25).softmax(-1) if cfg.rsa_update else None
+
+
+def _gates(model, key: Tensor, j: int, control: Tensor | None):
+    """Scalar decay/strength gates per token and head (attention.py:161-174)."""
+    cfg = model.config
+    w = model.gate_weight[j]
+    if cfg.control_dim:
+        raw = _mm(control, w, "btd,hdc->bthc", control.dtype)
+    else:
+        src = key if cfg.rsa_update else _unit(key)
+        raw = _mm(src, w, "bthd,hdc->bthc", key.dtype)
+    raw = raw.float() + model.gate_bias[j]
+    g_in, b_in, g_out, b_out = raw.unbind(-1)
+    g_in = -F.softplus(g_in).clamp(max=10.)
+    g_out = -F.softplus(g_out).clamp(max=10.)
+    if cfg.rsa_update:
+        tier = (1., .1, .01, .001)[j] if cfg.levels == 4 else .1 ** j
+        g_in, g_out = g_in * tier, g_out * tier
+    if cfg.positional_mode == "none":
+        g_in, g_out = g_in * 0, g_out * 0
+    return g_in, cfg.beta_max * b_in.sigmoid(), g_out, cfg.beta_max * b_out.sigmoid()
+
+
+def _base_logits(model, raw: Tensor, counts: Tensor, j: int) -> Tensor:
+    """read_scale*raw + softplus(c_j) log1p(n) (attention.py:196-204)."""
+    cfg = model.config
+    gain = F.softplus(model.count_gain_raw[j])[..., None]
+    if cfg.learn_read_scale:
+        scale = model.read_log_scale[j].clamp(math.log(.25), math.log(64.)).exp()[..., None]
+    else:
+        scale = cfg.read_scale
+    return scale * raw.float() + gain * counts.log1p()
+
+
+def _residual(model, key, value, rk, rv, j):
+    """attention.py:190-194."""
+    eta = 1 + .25 * model.residual_raw[j].tanh()
+    new_key = (key - eta[:, 0, None] * rk.to(key.dtype)).to(key.dtype)
+    new_value = (value - eta[:, 1, None] * rv.to(value.dtype)).to(value.dtype)
+    return new_key, new_value
+
+
+def _relations(model, local, writes, rel_states, scan):
+    """Every ordered edge's R_ij scan (attention.py:206-223)."""
+    cfg = model.config
+    incoming = [[] for _ in local]
+    finals = []
+    for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
+        lead = writes[i].shape[:-1]
+        g = (-F.softplus(model.relation_decay_raw[e])).expand(lead)
+        if cfg.positional_mode == "none":
+            g = g * 0
+        beta = model.relation_beta_raw[e].sigmoid().expand(lead)
+        target = writes[j]
+        if cfg.rsa_update:
+            norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
+            target = (target / norm[..., None]).to(target.dtype)
+            beta = (beta * norm.square()).clamp_max(.9)
+        msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
+        incoming[j].append((e, msg))
+        finals.append(RelationState(i, j, memory))
+    return incoming, tuple(finals)
+
+
+def _bridge(model, q: Tensor, logits, incoming, counts):
+    """Route reader and query projection per target level (attention.py:225-262)."""
+    cfg = model.config
+    dtype = q.dtype
+    routes, queries = [], []
+    for j, base in enumerate(logits):
+        if incoming[j]:
+            ids = [e for e, _ in incoming[j]]
+            w = model.edge_logits[ids].softmax(0)
+            total = 0
+            if cfg.paper_product_read:
+                for wt, (e, msg) in zip(w, incoming[j]):
+                    src_norm = logits[model.edges[e][0]].softmax(-1).norm(dim=-1, keepdim=True)
+                    total = total + wt[..., None] * msg.float() * src_norm
+                gain = model.relation_gain[j].clamp(-4, 4).exp()[..., None]
+                base = base + base.shape[-1] * gain * total
+                if cfg.relation_marginal:
+                    base = base - gain * counts[j].log1p()
+            else:
+                for wt, (_, msg) in zip(w, incoming[j]):
+                    total = total + wt[..., None] * msg.float()
+                centred = total - total.mean(-1, keepdim=True)
+                z = centred / (centred.square().mean(-1, keepdim=True) + 1e-5).sqrt()
+                base = base + model.relation_gain[j][..., None] * z.tanh()
+        route = base.softmax(-1).to(dtype)
+        hidden = F.gelu(_mm(route, model.route_up[j], "bthm,hmr->bthr", dtype).float()).to(dtype)
+        route = (route.float() + model.route_mlp_gain[j][..., None]
+                 * _mm(hidden, model.route_down[j], "bthr,hrm->bthm", dtype).float()).to(dtype)
+        if cfg.rsa_update:
+            wide = route.float()
+            route = (wide / wide.abs().sum(-1, keepdim=True).clamp(.25, 4.)).to(dtype)
+        qo = _mm(route, model.route_weight[j], "bthm,hmn->bthn", dtype)
+        qw = model.query_weight[j]
+        if cfg.shared_query_center:
+            qw = qw + model.center[j].transpose(-1, -2) / cfg.query_scale
+        direct = (cfg.query_scale * _mm(q, qw, "bthd,hdm->bthm", dtype).float()).to(dtype)
+        direct = _slot_feature(cfg, direct)
+        if cfg.balanced_bridge:
+            mix = .1 + .8 * model.bridge_mix_raw[j].sigmoid()[..., None]
+            qo = (mix * _unit(qo).float() + (1 - mix) * _unit(direct).float()).to(dtype)
+        else:
+            qo = (qo.float() + direct.float()).to(dtype)
+        routes.append(route)
+        queries.append(qo)
+    return routes, queries

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 1
+#define GPA_HIP_ABI_VERSION 2
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -93,6 +93,16 @@ typedef struct gpa_gdn_grads {
     float *ds0;
 } gpa_gdn_grads;
 
+/* Optional kernel timing: when non-NULL, events[i] is recorded on the stream
+ * before the i-th kernel an entry point launches and events[n] after the
+ * last one (n = *launched on return, at most GPA_MAX_TIMED).  The events are
+ * created and read by the caller (hipEventCreate / hipEventElapsedTime). */
+#define GPA_MAX_TIMED 4
+typedef struct gpa_timing {
+    hipEvent_t events[GPA_MAX_TIMED + 1];
+    int32_t launched;
+} gpa_timing;
+
 int gpa_hip_abi_version(void);
 const char *gpa_hip_last_error(void);
 /* Number of chunks a problem spans (0 on invalid geometry). */
@@ -103,12 +113,12 @@ int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk);
  * Replaces reference src/gpa/ops.py:49-85 (gdn_scan, backend dispatch at
  * ops.py:58-79) for a whole group of streams. */
 int gpa_gdn_forward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
-                    gpa_operand out, hipStream_t stream);
+                    gpa_operand out, gpa_timing *timing, hipStream_t stream);
 
 /* Backward of gpa_gdn_forward from its saved intermediates (the autograd of
  * ops.py:49-85 in the reference, plus chunk-start state injections). */
 int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
-                     const gpa_gdn_grads *grads, hipStream_t stream);
+                     const gpa_gdn_grads *grads, gpa_timing *timing, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,69 @@
+"""Host-side behaviour of the gpa_amd module that needs no GPU: configuration
+validation (reference attention.py:45-75 plus the HIP backend's own rules),
+state_dict compatibility, cache topology checks and the no-fallback rule."""
+from dataclasses import replace
+
+import pytest
+import torch
+
+from gpa_amd import DenseGPA, GPAConfig, _lib
+
+
+@pytest.mark.parametrize("bad", [
+    dict(heads=0), dict(chunk_size=1), dict(backend="torch"), dict(backend="fla"), dict(slots=()),
+    dict(slots=(4, 0)), dict(positional_mode="x"), dict(beta_init=.95), dict(relation_beta_init=1.),
+    dict(decay_init=0.), dict(execution="fast"), dict(read_scale=0.), dict(relation_marginal=True),
+    dict(slot_feature="relu"), dict(control_dim=-1), dict(positional_mode="moments", key_dim=5),
+])
+def test_config_rejects(bad):
+    with pytest.raises(ValueError):
+        GPAConfig(**bad)
+
+
+def test_config_defaults_and_edges():
+    cfg = GPAConfig()
+    assert cfg.backend == "hip" and cfg.chunk_size == 64
+    assert cfg.edges == tuple((i, j) for i in range(4) for j in range(4) if i != j)
+    replace(cfg, execution="staged")  # accepted and ignored
+
+
+def test_state_dict_round_trip_and_names():
+    a = DenseGPA(GPAConfig(heads=2, key_dim=4, value_dim=3, slots=(3, 5), chunk_size=4, balanced_bridge=True,
+                           learn_read_scale=True, quadratic_features=True))
+    b = DenseGPA(a.config)
+    b.load_state_dict(a.state_dict(), strict=True)
+    # The reference's named_parameters() order (optimizer state is positional):
+    # direct parameters first, then the per-level lists, then the feature map.
+    names = [n for n, _ in a.named_parameters()]
+    assert names == ['residual_raw', 'count_gain_raw', 'moment_gain', 'route_mlp_gain', 'output_logits',
+                     'edge_logits', 'relation_gain', 'relation_decay_raw', 'relation_beta_raw', 'bridge_mix_raw',
+                     'read_log_scale', 'center.0', 'center.1', 'inner_prefix.0', 'inner_prefix.1',
+                     'outer_prefix.0', 'outer_prefix.1', 'route_weight.0', 'route_weight.1', 'query_weight.0',
+                     'query_weight.1', 'route_up.0', 'route_up.1', 'route_down.0', 'route_down.1',
+                     'gate_weight.0', 'gate_weight.1', 'gate_bias.0', 'gate_bias.1', 'relation_prefix.0',
+                     'relation_prefix.1', 'feature_map.left', 'feature_map.right', 'feature_map.gain_raw']
+    assert "_edge_source" not in a.state_dict()
+
+
+def test_initial_state_layout():
+    m = DenseGPA(GPAConfig(heads=2, key_dim=4, value_dim=3, slots=(3, 5), chunk_size=4))
+    s = m.initial_state(3)
+    assert s.levels[0].inner.shape == (3, 2, 4, 3) and s.levels[1].outer.shape == (3, 2, 5, 3)
+    assert s.relations[0].memory.shape == (3, 2, 3, 5) and s.relations[1].memory.shape == (3, 2, 5, 3)
+    assert s.numel() == 3 * 2 * (4 * 3 + 3 * 3 + 3 + 4 * 5 + 5 * 3 + 5 + 2 * 15)
+    assert s.chunk_size == 4 and s.chunk_offset == 0 and s.frozen is None
+
+
+def test_forward_validation_and_no_cpu_fallback():
+    m = DenseGPA(GPAConfig(heads=2, key_dim=4, value_dim=3, slots=(3,), chunk_size=4))
+    q = torch.randn(1, 5, 2, 4)
+    v = torch.randn(1, 5, 2, 3)
+    with pytest.raises(ValueError):
+        m(q, q, torch.randn(1, 5, 2, 4))
+    with pytest.raises(ValueError):
+        m(q, q, v, position_ids=torch.arange(4))
+    other = DenseGPA(GPAConfig(heads=2, key_dim=4, value_dim=3, slots=(3, 3), chunk_size=4)).initial_state(1)
+    with pytest.raises(ValueError):
+        m(q, q, v, other)
+    with pytest.raises(_lib.HipBackendError):
+        m(q, q, v)
