@@ -1,0 +1,87 @@
+// Device helpers shared by the GDN scan kernels (gdn_scan.hip, gdn_state_mfma.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gpa_common.h"
+#include "gpa_hip.h"
+
+namespace gpa {
+
+constexpr int R = GPA_CHUNK_ROWS;  // rows per chunk tile
+constexpr int NT = 256;            // threads per block
+constexpr int VT = 32;             // state columns per sequential block
+constexpr int KS = 64;             // staged K slice
+constexpr int LDR = R + 1;         // padded row stride of R x R tiles
+constexpr int LDS_ = KS + 1;       // padded row stride of R x KS tiles
+
+// Barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load and store of the wave (a workgroup-scope fence); a
+// kernel whose waves exchange data through LDS alone, and which never reads
+// back global memory it writes, keeps its global traffic in flight across
+// this barrier.  The "memory" clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ int token_at(const gpa_gdn_problem& p, int n, int r) {
+  if (r >= p.chunk) return -1;
+  const int t = n * p.chunk + r - p.offset;
+  return (t >= 0 && t < p.tokens) ? t : -1;
+}
+
+__device__ __forceinline__ int64_t op_base(const gpa_operand& o, int b, int h) {
+  return (int64_t)b * o.sb + (int64_t)h * o.sh;
+}
+
+template <typename E>
+__device__ __forceinline__ float op_load(const gpa_operand& o, int b, int h, int t, int d) {
+  return to_f32(reinterpret_cast<const E*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st + d]);
+}
+
+__device__ __forceinline__ float scalar_load(const gpa_operand& o, int b, int h, int t) {
+  return reinterpret_cast<const float*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st];
+}
+
+// Stream-major saved buffer offsets.
+__device__ __forceinline__ int64_t rows_off(int s, int n, int nch, int r, int width) {
+  return (((int64_t)s * nch + n) * R + r) * width;
+}
+__device__ __forceinline__ int64_t state_off(int s, int n, int nch, int K, int V) {
+  return ((int64_t)s * nch + n) * K * V;
+}
+
+// Sum over the 16 lanes that share (lane / 16) within a wave.
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 8, 16);
+  x += __shfl_xor(x, 4, 16);
+  x += __shfl_xor(x, 2, 16);
+  x += __shfl_xor(x, 1, 16);
+  return x;
+}
+__device__ __forceinline__ float sum64(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Load an R x KS slice (columns c0..c0+KS) of a saved [.., R, width] fp32 row
+// block into LDS with optional per-row scale; zero past `width`.
+__device__ __forceinline__ void stage_rows(float* dst, const float* src, int width, int c0,
+                                           const float* row_scale) {
+  for (int idx = threadIdx.x; idx < R * KS; idx += NT) {
+    const int r = idx / KS, c = idx % KS;
+    float x = (c0 + c < width) ? src[(int64_t)r * width + c0 + c] : 0.f;
+    if (row_scale) x *= row_scale[r];
+    dst[r * LDS_ + c] = x;
+  }
+}
+
+
+// MFMA launchers for the bf16 state recurrences (gdn_state_mfma.hip); they
+// return nonzero if the width is not built.
+template <int KM>
+int launch_state_fwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStream_t st);
+template <int KM>
+int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
+                          hipStream_t st);
+
+}  // namespace gpa

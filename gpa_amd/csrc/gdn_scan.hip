@@ -20,73 +20,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "gpa_hip.h"
 #include "gpa_common.h"
+#include "gdn_common.h"
 
 namespace gpa {
-
-constexpr int R = GPA_CHUNK_ROWS;  // rows per chunk tile
-constexpr int NT = 256;            // threads per block
-constexpr int VT = 32;             // state columns per sequential block
-constexpr int KS = 64;             // staged K slice
-constexpr int LDR = R + 1;         // padded row stride of R x R tiles
-constexpr int LDS_ = KS + 1;       // padded row stride of R x KS tiles
-
-struct Geo {
-  int s, b, h, n;
-};
-
-__device__ __forceinline__ int token_at(const gpa_gdn_problem& p, int n, int r) {
-  if (r >= p.chunk) return -1;
-  const int t = n * p.chunk + r - p.offset;
-  return (t >= 0 && t < p.tokens) ? t : -1;
-}
-
-__device__ __forceinline__ int64_t op_base(const gpa_operand& o, int b, int h) {
-  return (int64_t)b * o.sb + (int64_t)h * o.sh;
-}
-
-template <typename E>
-__device__ __forceinline__ float op_load(const gpa_operand& o, int b, int h, int t, int d) {
-  return to_f32(reinterpret_cast<const E*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st + d]);
-}
-
-__device__ __forceinline__ float scalar_load(const gpa_operand& o, int b, int h, int t) {
-  return reinterpret_cast<const float*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st];
-}
-
-// Stream-major saved buffer offsets.
-__device__ __forceinline__ int64_t rows_off(int s, int n, int nch, int r, int width) {
-  return (((int64_t)s * nch + n) * R + r) * width;
-}
-__device__ __forceinline__ int64_t state_off(int s, int n, int nch, int K, int V) {
-  return ((int64_t)s * nch + n) * K * V;
-}
-
-// Sum over the 16 lanes that share (lane / 16) within a wave.
-__device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 8, 16);
-  x += __shfl_xor(x, 4, 16);
-  x += __shfl_xor(x, 2, 16);
-  x += __shfl_xor(x, 1, 16);
-  return x;
-}
-__device__ __forceinline__ float sum64(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-  return x;
-}
-
-// Load an R x KS slice (columns c0..c0+KS) of a saved [.., R, width] fp32 row
-// block into LDS with optional per-row scale; zero past `width`.
-__device__ __forceinline__ void stage_rows(float* dst, const float* src, int width, int c0,
-                                           const float* row_scale) {
-  for (int idx = threadIdx.x; idx < R * KS; idx += NT) {
-    const int r = idx / KS, c = idx % KS;
-    float x = (c0 + c < width) ? src[(int64_t)r * width + c0 + c] : 0.f;
-    if (row_scale) x *= row_scale[r];
-    dst[r * LDS_ + c] = x;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // gdn_prep: one block per (chunk n = blockIdx.x, stream s = blockIdx.y).
@@ -1072,6 +1012,12 @@ int check_problem(const gpa_gdn_problem* p) {
 
 int kmax_for(int k) { return k <= 64 ? 64 : (k <= 128 ? 128 : 256); }
 
+// The bf16 state recurrences run on MFMA when every 16-wide k step is whole.
+template <typename E>
+bool use_mfma(const gpa_gdn_problem& p) {
+  return std::is_same<E, bf16_t>::value && p.kdim % 16 == 0;
+}
+
 // Kernels above 64 KiB of dynamic LDS must say so once per instantiation.
 template <typename F>
 int allow_lds(F kernel, size_t bytes) {
@@ -1089,11 +1035,15 @@ int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operan
   if (int rc = allow_lds(gdn_prep<E, KM>, lds_prep)) return rc;
   mark(tm, st);
   hipLaunchKernelGGL((gdn_prep<E, KM>), grid_c, block, lds_prep, st, p, sv, nch);
-  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
-  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
-  if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
   mark(tm, st);
-  hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
+  if (use_mfma<E>(p)) {
+    if (int rc = launch_state_fwd_mfma<KM>(p, sv, nch, st)) return rc;
+  } else {
+    const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+    const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
+    if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
+    hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
+  }
   if (p.q.ptr && out.ptr) {
     const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
     mark(tm, st);
@@ -1115,11 +1065,15 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
   } else {
     gr.dd0 = nullptr;
   }
-  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
-  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
-  if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
   mark(tm, st);
-  hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
+  if (use_mfma<E>(p)) {
+    if (int rc = launch_state_bwd_mfma<KM>(p, sv, gr, nch, st)) return rc;
+  } else {
+    const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+    const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
+    if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
+    hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
+  }
   constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
   constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
   const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);

@@ -43,6 +43,11 @@ def _kmax(k: int) -> int:
     return 64 if k <= 64 else (128 if k <= 128 else 256)
 
 
+def _mfma(k: int, dtype) -> bool:
+    """Mirror of the library's choice of the MFMA state recurrences."""
+    return _tag(dtype) == "bf16" and k % 16 == 0
+
+
 def _tag(dtype) -> str:
     return "bf16" if str(dtype).endswith("bfloat16") else "f32"
 
@@ -110,8 +115,9 @@ def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     if _active is None:
         return None
     e, km = _tag(dtype), _kmax(k)
+    state = f"gdn_state_fwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_fwd<{km}>"
     kernels = [(f"gdn_prep<{e},{km}>", (4 * c * k + 2 * c * v + c * c / 3) * tokens),
-               (f"gdn_state_fwd<{km}>", 4 * k * v * tokens)]
+               (state, 4 * k * v * tokens)]
     if read:
         kernels.append((f"gdn_out_fwd<{e},{km}>", (2 * k * v + 2 * c * k + 2 * c * v) * tokens))
     return _active.timing(kernels)
@@ -124,7 +130,8 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     kernels = []
     if read:
         kernels.append((f"gdn_dd0<{e},{km}>", (2 * c * k + 2 * c * v) * tokens))
-    kernels.append((f"gdn_state_bwd<{e},{km}>", (6 if read else 4) * k * v * tokens))
+    state = f"gdn_state_bwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_bwd<{e},{km}>"
+    kernels.append((state, (6 if read else 4) * k * v * tokens))
     chunk = 4 * k * v + 8 * c * k + 4 * c * v + 4 * c * c
     if read:
         chunk += 2 * k * v + 6 * c * k + 2 * c * v

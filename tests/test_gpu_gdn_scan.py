@@ -67,6 +67,13 @@ CASES = [
     (1, 96, 1, 256, 128, 64, 30, torch.float32),
     (1, 130, 2, 128, 128, 64, 0, torch.bfloat16),
     (1, 64, 1, 256, 256, 64, 0, torch.bfloat16),
+    # bf16 MFMA state path: K below its tile, partial 64-column tiles, offsets.
+    (2, 70, 2, 32, 48, 64, 17, torch.bfloat16),
+    (1, 100, 3, 64, 200, 64, 63, torch.bfloat16),
+    (1, 129, 1, 256, 96, 64, 1, torch.bfloat16),
+    (1, 20, 2, 48, 16, 8, 3, torch.bfloat16),
+    # bf16 FMA path (K not a multiple of 16)
+    (1, 40, 2, 40, 24, 16, 5, torch.bfloat16),
 ]
 
 
