@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_TIMED = 4
 CHUNK_ROWS = 64
 MAX_KDIM = 256
@@ -35,12 +35,13 @@ class Problem(ctypes.Structure):
 
 
 class Saved(ctypes.Structure):
-    _fields_ = [(n, c_vp) for n in ("kn", "qn", "w", "u", "delta", "tri", "gam", "beta", "states", "final")]
+    _fields_ = [(n, c_vp) for n in ("kn", "qn", "w", "u", "delta", "tri", "gam", "beta", "states", "final",
+                                    "wrow", "wcol", "krow", "kcol", "qcol")]
 
 
 class Grads(ctypes.Structure):
     _fields_ = [("dout", Operand), ("dstates", c_vp), ("dfinal", c_vp),
-                ("dd0", c_vp), ("ddelta", c_vp), ("dhend", c_vp), ("dw", c_vp),
+                ("dd0", c_vp), ("o", c_vp), ("ddelta", c_vp), ("dhend", c_vp), ("dw", c_vp),
                 ("dq", Operand), ("dk", Operand), ("dv", Operand), ("dg", Operand), ("dbeta", Operand),
                 ("ds0", c_vp)]
 
@@ -53,6 +54,7 @@ EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
     "gpa_gdn_nchunks": ([c_i32, c_i32, c_i32], c_i32),
+    "gpa_gdn_path": ([ctypes.POINTER(Problem)], c_i32),
     "gpa_gdn_forward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, ctypes.POINTER(Timing), c_vp],
                         ctypes.c_int),
     "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads),

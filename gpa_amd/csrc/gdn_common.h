@@ -43,12 +43,21 @@ __device__ __forceinline__ float scalar_load(const gpa_operand& o, int b, int h,
 }
 
 // Stream-major saved buffer offsets.
+// [S][N][R][width] (position rows): kn, qn, w, dw, tri (width R), gam, beta (width 1)
 __device__ __forceinline__ int64_t rows_off(int s, int n, int nch, int r, int width) {
   return (((int64_t)s * nch + n) * R + r) * width;
 }
+// [S][N][V][K] value-major chunk-start states: element (k,v) at +v*K+k
 __device__ __forceinline__ int64_t state_off(int s, int n, int nch, int K, int V) {
   return ((int64_t)s * nch + n) * K * V;
 }
+// [S][N][V][R] value-major position data (u, delta, dd0, o, ddelta): (r,v) at +v*R+r
+__device__ __forceinline__ int64_t vc_off(int s, int n, int nch, int V) {
+  return ((int64_t)s * nch + n) * V * R;
+}
+// Per-chunk sizes (bf16 elements) of the MFMA fragment buffers.
+__host__ __device__ __forceinline__ int frag_row_elems(int K, int per_lane) { return 2 * (K / 16) * 64 * per_lane; }
+__host__ __device__ __forceinline__ int frag_col_elems(int K, int per_lane) { return ((K + 31) / 32) * 4 * 64 * per_lane; }
 
 // Sum over the 16 lanes that share (lane / 16) within a wave.
 __device__ __forceinline__ float sum16(float x) {

@@ -30,11 +30,14 @@ namespace gpa {
 
 // ---------------------------------------------------------------------------
 // gdn_prep: one block per (chunk n = blockIdx.x, stream s = blockIdx.y).
-template <typename E, int KM>
+// MF: also write the bf16 MFMA fragments of W, Kn and Qn (see gpa_hip.h);
+// W in fp32 is then not needed and not written.
+template <typename E, int KM, bool MF>
 __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
-  extern __shared__ float smem[];
-  float* kn_s = smem;                 // [R][KM+1]
-  float* a_s = kn_s + R * (KM + 1);   // [R][LDR]   A, then reused
+  constexpr int KP = KM + 4;          // padded row stride (keeps 16-byte alignment)
+  extern __shared__ __align__(16) float smem[];
+  float* kn_s = smem;                 // [R][KP]
+  float* a_s = kn_s + R * KP;         // [R][LDR]   A
   float* t_s = a_s + R * LDR;         // [R][LDR]   T
   float* v_s = t_s + R * LDR;         // [R][LDR]   b*V slice
   float* gam_s = v_s + R * LDR;       // [R]
@@ -44,6 +47,8 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
   const int b = s / p.heads, h = s % p.heads;
   const int K = p.kdim, V = p.vdim, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const int K16 = K / 16;
+  const int64_t chunk_id = (int64_t)s * nch + n;
 
   if (tid < R) {
     const int t = token_at(p, n, tid);
@@ -63,6 +68,7 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
   }
 
   // Normalise keys (and queries) row by row: wave w owns rows w, w+4, ...
+  __bf16* qcol = MF && p.q.ptr ? reinterpret_cast<__bf16*>(sv.qcol) + chunk_id * frag_col_elems(K, 8) : nullptr;
   for (int r = wave; r < R; r += NT / 64) {
     const int t = token_at(p, n, r);
     float x[KM / 64];
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
     for (int i = 0; i < KM / 64; ++i) {
       const int d = lane + 64 * i;
       const float y = round_as<E>(x[i] / den);
-      kn_s[r * (KM + 1) + d] = y;
+      kn_s[r * KP + d] = y;
       if (d < K) sv.kn[rows_off(s, n, nch, r, K) + d] = y;
     }
     if (p.q.ptr) {
@@ -93,11 +99,42 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
 #pragma unroll
       for (int i = 0; i < KM / 64; ++i) {
         const int d = lane + 64 * i;
-        if (d < K) sv.qn[rows_off(s, n, nch, r, K) + d] = round_as<E>(x[i] / dq);
+        if (d < K) {
+          const float y = round_as<E>(x[i] / dq);
+          sv.qn[rows_off(s, n, nch, r, K) + d] = y;
+          if (MF) {  // Qn^T fragment (rb, cs), lane (d%32) + 32*((r/8)%2), element r%8
+            const int rb = d >> 5, cs = r >> 4, ln = (d & 31) + 32 * ((r >> 3) & 1);
+            qcol[((rb * 4 + cs) * 64 + ln) * 8 + (r & 7)] = (__bf16)y;
+          }
+        }
       }
     }
   }
   __syncthreads();
+
+  if (MF) {
+    // Kn row and column fragments (exact in bf16), one 16-byte piece per step.
+    __bf16* krow = reinterpret_cast<__bf16*>(sv.krow) + chunk_id * frag_row_elems(K, 8);
+    __bf16* kcol = reinterpret_cast<__bf16*>(sv.kcol) + chunk_id * frag_col_elems(K, 8);
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    for (int piece = tid; piece < 2 * K16 * 64; piece += NT) {
+      const int ln = piece & 63, ks = (piece >> 6) % K16, rt = (piece >> 6) / K16;
+      const float* src = kn_s + (32 * rt + (ln & 31)) * KP + 16 * ks + 8 * (ln >> 5);
+      bf16x8 f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (__bf16)src[e];
+      *reinterpret_cast<bf16x8*>(krow + (int64_t)piece * 8) = f;
+    }
+    const int RB = (K + 31) / 32;
+    for (int piece = tid; piece < RB * 4 * 64; piece += NT) {
+      const int ln = piece & 63, cs = (piece >> 6) & 3, rb = piece >> 8;
+      const int k = 32 * rb + (ln & 31), c0 = 16 * cs + 8 * (ln >> 5);
+      bf16x8 f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (__bf16)(k < K ? kn_s[(c0 + e) * KP + k] : 0.f);
+      *reinterpret_cast<bf16x8*>(kcol + (int64_t)piece * 8) = f;
+    }
+  }
 
   // Gram matrix -> A (strictly lower).  Thread tile: rows 4*ty+i, cols tx+16*j.
   const int ty = tid / 16, tx = tid % 16;
@@ -106,9 +143,9 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
     for (int k = 0; k < KM; ++k) {
       float a[4], c[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = kn_s[(4 * ty + i) * (KM + 1) + k];
+      for (int i = 0; i < 4; ++i) a[i] = kn_s[(4 * ty + i) * KP + k];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = kn_s[(tx + 16 * j) * (KM + 1) + k];
+      for (int j = 0; j < 4; ++j) c[j] = kn_s[(tx + 16 * j) * KP + k];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -139,30 +176,71 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
   for (int idx = tid; idx < R * R; idx += NT)
     sv.tri[rows_off(s, n, nch, 0, R) + idx] = t_s[(idx / R) * LDR + idx % R];
 
-  // W = T diag(b e^G) Kn.  Thread tile rows 4*ty+i, cols tx + 16*j.
-  {
-    float acc[4][KM / 16] = {};
+  // W = T diag(b e^G) Kn.  Thread tile: rows 4*ty+i, 8 consecutive columns 8*tx + 128*pass.
+  for (int c0 = 8 * tx; c0 < KM; c0 += 128) {
+    float acc[4][8] = {};
     for (int u = 0; u < R; ++u) {
       float a[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = t_s[(4 * ty + i) * LDR + u] * sc_s[u];
+      const float4 k0 = *reinterpret_cast<const float4*>(&kn_s[u * KP + c0]);
+      const float4 k1 = *reinterpret_cast<const float4*>(&kn_s[u * KP + c0 + 4]);
+      const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
 #pragma unroll
-      for (int j = 0; j < KM / 16; ++j) {
-        const float c = kn_s[u * (KM + 1) + tx + 16 * j];
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i][j] += a[i] * c;
+        for (int e = 0; e < 8; ++e) acc[i][e] += a[i] * kv[e];
+    }
+    if (c0 >= K) continue;
+    if (!MF) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float* dst = sv.w + rows_off(s, n, nch, 4 * ty + i, K) + c0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (c0 + e < K) dst[e] = acc[i][e];
+      }
+    } else {
+      typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+      __bf16* wrow = reinterpret_cast<__bf16*>(sv.wrow) + chunk_id * frag_row_elems(K, 16);
+      __bf16* wcol = reinterpret_cast<__bf16*>(sv.wcol) + chunk_id * frag_col_elems(K, 16);
+      // Row fragment: row t, columns c0..c0+7 = fragment (t/32, c0/16), lane t%32 + 32*((c0/8)%2).
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * ty + i;
+        const int ln = (t & 31) + 32 * ((c0 >> 3) & 1);
+        __bf16* dst = wrow + (((t >> 5) * K16 + (c0 >> 4)) * 64 + ln) * 16;
+        bf16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          hi[e] = (__bf16)acc[i][e];
+          lo[e] = (__bf16)(acc[i][e] - (float)hi[e]);
+        }
+        *reinterpret_cast<bf16x8*>(dst) = hi;
+        *reinterpret_cast<bf16x8*>(dst + 8) = lo;
+      }
+      // Column fragment: column k, rows 4*ty..4*ty+3 = fragment (k/32, t/16),
+      // lane k%32 + 32*((t/8)%2), elements t%8 .. t%8+3.
+      const int t0 = 4 * ty;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = c0 + e;
+        const int ln = (k & 31) + 32 * ((t0 >> 3) & 1);
+        __bf16* dst = wcol + (((k >> 5) * 4 + (t0 >> 4)) * 64 + ln) * 16 + (t0 & 7);
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hi[i] = (__bf16)acc[i][e];
+          lo[i] = (__bf16)(acc[i][e] - (float)hi[i]);
+        }
+        *reinterpret_cast<bf16x4*>(dst) = hi;
+        *reinterpret_cast<bf16x4*>(dst + 8) = lo;
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < KM / 16; ++j) {
-        const int k = tx + 16 * j;
-        if (k < K) sv.w[rows_off(s, n, nch, 4 * ty + i, K) + k] = acc[i][j];
-      }
   }
 
-  // U = T diag(b) V, 64 value columns at a time.
+  // U = T diag(b) V, 64 value columns at a time, stored value-major.
   for (int v0 = 0; v0 < V; v0 += R) {
     __syncthreads();
     for (int idx = tid; idx < R * R; idx += NT) {
@@ -183,13 +261,13 @@ __global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
     }
+    float* um = sv.u + vc_off(s, n, nch, V);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = v0 + tx + 16 * j;
-        if (v < V) sv.u[rows_off(s, n, nch, 4 * ty + i, V) + v] = acc[i][j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int v = v0 + tx + 16 * j;
+      if (v < V)
+        *reinterpret_cast<float4*>(&um[(int64_t)v * R + 4 * ty]) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+    }
   }
 }
 
@@ -220,12 +298,13 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd(gpa_gdn_problem p, gpa_gdn_s
     if (vok)
       for (int i = 0; i < KM / 8; ++i) {
         const int k = r + 8 * i;
-        if (k < K) sv.states[so + (int64_t)k * V + v] = st_s[k * (VT + 1) + c];
+        if (k < K) sv.states[so + (int64_t)v * K + k] = st_s[k * (VT + 1) + c];
       }
     // D = U - W S
+    const float* um = sv.u + vc_off(s, n, nch, V);
     float acc[R / 8];
 #pragma unroll
-    for (int j = 0; j < R / 8; ++j) acc[j] = vok ? sv.u[rows_off(s, n, nch, r + 8 * j, V) + v] : 0.f;
+    for (int j = 0; j < R / 8; ++j) acc[j] = vok ? um[(int64_t)v * R + r + 8 * j] : 0.f;
     for (int k0 = 0; k0 < KM; k0 += KS) {
       __syncthreads();
       stage_rows(w_s, sv.w + rows_off(s, n, nch, 0, K), K, k0, nullptr);
@@ -236,10 +315,11 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd(gpa_gdn_problem p, gpa_gdn_s
         for (int j = 0; j < R / 8; ++j) acc[j] -= w_s[(r + 8 * j) * LDS_ + kk] * sk;
       }
     }
+    float* dm = sv.delta + vc_off(s, n, nch, V);
 #pragma unroll
     for (int j = 0; j < R / 8; ++j) {
       d_s[(r + 8 * j) * (VT + 1) + c] = acc[j];
-      if (vok) sv.delta[rows_off(s, n, nch, r + 8 * j, V) + v] = acc[j];
+      if (vok) dm[(int64_t)v * R + r + 8 * j] = acc[j];
     }
     if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
     __syncthreads();
@@ -318,15 +398,15 @@ __global__ __launch_bounds__(NT) void gdn_out_fwd(gpa_gdn_problem p, gpa_gdn_sav
   const float* qn = sv.qn + rows_off(s, n, nch, 0, K);
   build_p<KM>(p_s, a_s, b_s, qn, sv.kn + rows_off(s, n, nch, 0, K), gam_s, K);
   const float* st = sv.states + state_off(s, n, nch, K, V);
-  const float* dl = sv.delta + rows_off(s, n, nch, 0, V);
+  const float* dl = sv.delta + vc_off(s, n, nch, V);
   for (int v0 = 0; v0 < V; v0 += 64) {
     float acc[4][4] = {};
     for (int k0 = 0; k0 < KM; k0 += KS) {
       __syncthreads();
       stage_rows(a_s, qn, K, k0, nullptr);
       for (int idx = tid; idx < KS * 64; idx += NT) {
-        const int kk = idx / 64, c = idx % 64;
-        b_s[kk * LDS_ + c] = (k0 + kk < K && v0 + c < V) ? st[(int64_t)(k0 + kk) * V + v0 + c] : 0.f;
+        const int kk = idx % KS, c = idx / KS;
+        b_s[kk * LDS_ + c] = (k0 + kk < K && v0 + c < V) ? st[(int64_t)(v0 + c) * K + k0 + kk] : 0.f;
       }
       __syncthreads();
       for (int kk = 0; kk < KS; ++kk) {
@@ -348,7 +428,10 @@ __global__ __launch_bounds__(NT) void gdn_out_fwd(gpa_gdn_problem p, gpa_gdn_sav
       for (int j = 0; j < 4; ++j) acc[i][j] *= e;
     }
     __syncthreads();
-    stage_rows(b_s, dl, V, v0, nullptr);
+    for (int idx = tid; idx < R * 64; idx += NT) {
+      const int u = idx % R, c = idx / R;
+      b_s[u * LDS_ + c] = v0 + c < V ? dl[(int64_t)(v0 + c) * R + u] : 0.f;
+    }
     __syncthreads();
     for (int u = 0; u < R; ++u) {
       float a[4], c[4];
@@ -376,7 +459,8 @@ __global__ __launch_bounds__(NT) void gdn_out_fwd(gpa_gdn_problem p, gpa_gdn_sav
 }
 
 // ---------------------------------------------------------------------------
-// gdn_dd0: dd0 = P^T dO (the part of dD not carried by the state).
+// gdn_dd0: dd0 = P^T dO (the part of dD not carried by the state), and
+// o = diag(e^G) dO, both value-major [V][R] per chunk.
 template <typename E, int KM>
 __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
                                                int nch) {
@@ -390,6 +474,8 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
   if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
   __syncthreads();
   build_p<KM>(p_s, a_s, b_s, sv.qn + rows_off(s, n, nch, 0, K), sv.kn + rows_off(s, n, nch, 0, K), gam_s, K);
+  float* d0 = gr.dd0 + vc_off(s, n, nch, V);
+  float* om = gr.o + vc_off(s, n, nch, V);
   for (int v0 = 0; v0 < V; v0 += 64) {
     __syncthreads();
     for (int idx = tid; idx < R * 64; idx += NT) {
@@ -398,6 +484,10 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
       b_s[r * LDS_ + c] = (t >= 0 && v0 + c < V) ? op_load<E>(gr.dout, b, h, t, v0 + c) : 0.f;
     }
     __syncthreads();
+    for (int idx = tid; idx < R * 64; idx += NT) {
+      const int r = idx % R, c = idx / R;
+      if (v0 + c < V) om[(int64_t)(v0 + c) * R + r] = __expf(gam_s[r]) * b_s[r * LDS_ + c];
+    }
     float acc[4][4] = {};
     for (int u = 0; u < R; ++u) {  // acc[t'][v] += P[u][t'] dO[u][v]
       float a[4], c[4];
@@ -411,12 +501,11 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
         for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = v0 + tx + 16 * j;
-        if (v < V) gr.dd0[rows_off(s, n, nch, 4 * ty + i, V) + v] = acc[i][j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int v = v0 + tx + 16 * j;
+      if (v < V)
+        *reinterpret_cast<float4*>(&d0[(int64_t)v * R + 4 * ty]) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+    }
   }
 }
 
@@ -450,17 +539,19 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd(gpa_gdn_problem p, gpa_gdn_s
     if (vok)
       for (int i = 0; i < KM / 8; ++i) {
         const int k = r + 8 * i;
-        if (k < K) gr.dhend[so + (int64_t)k * V + v] = ds_s[k * (VT + 1) + c];
+        if (k < K) gr.dhend[so + (int64_t)v * K + k] = ds_s[k * (VT + 1) + c];
       }
     if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
     __syncthreads();
     const float gc = gam_s[R - 1];
     if (tid < R) rs_s[tid] = __expf(gc - gam_s[tid]);
     // dD = dd0 + diag(e^{G_C-G}) Kn dS
+    const float* d0 = gr.dd0 ? gr.dd0 + vc_off(s, n, nch, V) : nullptr;
+    const float* om = has_q ? gr.o + vc_off(s, n, nch, V) : nullptr;
+    float* ddm = gr.ddelta + vc_off(s, n, nch, V);
     float acc[R / 8];
 #pragma unroll
-    for (int j = 0; j < R / 8; ++j)
-      acc[j] = (gr.dd0 && vok) ? gr.dd0[rows_off(s, n, nch, r + 8 * j, V) + v] : 0.f;
+    for (int j = 0; j < R / 8; ++j) acc[j] = (d0 && vok) ? d0[(int64_t)v * R + r + 8 * j] : 0.f;
     for (int k0 = 0; k0 < KM; k0 += KS) {
       __syncthreads();
       stage_rows(x_s, sv.kn + rows_off(s, n, nch, 0, K), K, k0, rs_s);
@@ -475,13 +566,8 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd(gpa_gdn_problem p, gpa_gdn_s
     for (int j = 0; j < R / 8; ++j) {
       const int t = r + 8 * j;
       dd_s[t * (VT + 1) + c] = acc[j];
-      if (vok) gr.ddelta[rows_off(s, n, nch, t, V) + v] = acc[j];
-      float o = 0.f;
-      if (has_q && vok) {
-        const int tok = token_at(p, n, t);
-        if (tok >= 0) o = __expf(gam_s[t]) * op_load<E>(gr.dout, b, h, tok, v);
-      }
-      o_s[t * (VT + 1) + c] = o;
+      if (vok) ddm[(int64_t)v * R + t] = acc[j];
+      o_s[t * (VT + 1) + c] = (om && vok) ? om[(int64_t)v * R + t] : 0.f;
     }
     // dS_prev = e^{G_C} dS + Qn^T diag(e^G) dO - W^T dD + dstates[n]
     const float decay = __expf(gc);
@@ -497,7 +583,7 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd(gpa_gdn_problem p, gpa_gdn_s
         if (has_q)
           for (int t = 0; t < R; ++t) x += x_s[t * LDS_ + kk] * o_s[t * (VT + 1) + c];
         for (int t = 0; t < R; ++t) x -= y_s[t * LDS_ + kk] * dd_s[t * (VT + 1) + c];
-        if (gr.dstates && vok && k < K) x += gr.dstates[so + (int64_t)k * V + v];
+        if (gr.dstates && vok && k < K) x += gr.dstates[so + (int64_t)v * K + k];
         ds_s[k * (VT + 1) + c] = x;
       }
     }
@@ -547,8 +633,8 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
   const float* qn = sv.qn + rows_off(s, n, nch, 0, K);
   const float* st = sv.states + state_off(s, n, nch, K, V);
   const float* dh = gr.dhend + state_off(s, n, nch, K, V);
-  const float* dl = sv.delta + rows_off(s, n, nch, 0, V);
-  const float* ddl = gr.ddelta + rows_off(s, n, nch, 0, V);
+  const float* dl = sv.delta + vc_off(s, n, nch, V);    // value-major [V][R]
+  const float* ddl = gr.ddelta + vc_off(s, n, nch, V);
   float* dw = gr.dw + rows_off(s, n, nch, 0, K);
 
   if (tid < R) {
@@ -574,14 +660,17 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
         if (t >= 0) o = op_load<E>(gr.dout, b, h, t, v);
       }
       pa_do[r * (VT + 1) + c] = o;
-      pa_d[r * (VT + 1) + c] = v < V ? dl[(int64_t)r * V + v] : 0.f;
-      pa_dd[r * (VT + 1) + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+    }
+    for (int idx = tid; idx < R * VT; idx += NT) {
+      const int r = idx % R, c = idx / R, v = v0 + c;
+      pa_d[r * (VT + 1) + c] = v < V ? dl[(int64_t)v * R + r] : 0.f;
+      pa_dd[r * (VT + 1) + c] = v < V ? ddl[(int64_t)v * R + r] : 0.f;
     }
     for (int idx = tid; idx < KM * VT; idx += NT) {
-      const int k = idx / VT, c = idx % VT, v = v0 + c;
+      const int k = idx % KM, c = idx / KM, v = v0 + c;
       const bool ok = k < K && v < V;
-      const float hv = ok ? st[(int64_t)k * V + v] : 0.f;
-      const float dv = ok ? dh[(int64_t)k * V + v] : 0.f;
+      const float hv = ok ? st[(int64_t)v * K + k] : 0.f;
+      const float dv = ok ? dh[(int64_t)v * K + k] : 0.f;
       pa_h[k * (VT + 1) + c] = hv;
       pa_dh[k * (VT + 1) + c] = dv;
       decay_dot += hv * dv;
@@ -658,7 +747,7 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
           const int t = token_at(p, n, r);
           if (t >= 0 && v < V) o = op_load<E>(gr.dout, b, h, t, v);
           a_s[r * LDS_ + c] = o;
-          b_s[r * LDS_ + c] = v < V ? dl[(int64_t)r * V + v] : 0.f;
+          b_s[r * LDS_ + c] = v < V ? dl[(int64_t)v * R + r] : 0.f;
         }
         __syncthreads();
         for (int cc = 0; cc < KS; ++cc) {
@@ -754,7 +843,7 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
       __syncthreads();
       for (int idx = tid; idx < R * KS; idx += NT) {
         const int r = idx / KS, c = idx % KS, v = v0 + c;
-        a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+        a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)v * R + r] : 0.f;
         const int t = token_at(p, n, r);
         b_s[r * LDS_ + c] = (t >= 0 && v < V) ? bet_s[r] * op_load<E>(p.v, b, h, t, v) : 0.f;
       }
@@ -897,7 +986,7 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
     __syncthreads();
     for (int idx = tid; idx < R * KS; idx += NT) {
       const int r = idx / KS, c = idx % KS, v = v0 + c;
-      a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)r * V + v] : 0.f;
+      a_s[r * LDS_ + c] = v < V ? ddl[(int64_t)v * R + r] : 0.f;
       const int t = token_at(p, n, r);
       b_s[r * LDS_ + c] = (t >= 0 && v < V) ? op_load<E>(p.v, b, h, t, v) : 0.f;
     }
@@ -1031,12 +1120,18 @@ template <typename E, int KM>
 int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, gpa_timing* tm,
                    hipStream_t st, int nch) {
   const dim3 grid_c(nch, p.batch * p.heads), block(NT);
-  const size_t lds_prep = sizeof(float) * (R * (KM + 1) + 3 * R * LDR + 3 * R);
-  if (int rc = allow_lds(gdn_prep<E, KM>, lds_prep)) return rc;
+  const bool mf = use_mfma<E>(p);
+  const size_t lds_prep = sizeof(float) * (R * (KM + 4) + 3 * R * LDR + 3 * R);
   mark(tm, st);
-  hipLaunchKernelGGL((gdn_prep<E, KM>), grid_c, block, lds_prep, st, p, sv, nch);
+  if (mf) {
+    if (int rc = allow_lds(gdn_prep<E, KM, true>, lds_prep)) return rc;
+    hipLaunchKernelGGL((gdn_prep<E, KM, true>), grid_c, block, lds_prep, st, p, sv, nch);
+  } else {
+    if (int rc = allow_lds(gdn_prep<E, KM, false>, lds_prep)) return rc;
+    hipLaunchKernelGGL((gdn_prep<E, KM, false>), grid_c, block, lds_prep, st, p, sv, nch);
+  }
   mark(tm, st);
-  if (use_mfma<E>(p)) {
+  if (mf) {
     if (int rc = launch_state_fwd_mfma<KM>(p, sv, nch, st)) return rc;
   } else {
     const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -1064,6 +1159,7 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
     hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
   } else {
     gr.dd0 = nullptr;
+    gr.o = nullptr;
   }
   mark(tm, st);
   if (use_mfma<E>(p)) {
@@ -1106,6 +1202,23 @@ int dispatch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const g
 
 }  // namespace
 
+static int path_of(const gpa_gdn_problem* p) { return p->dtype == GPA_DTYPE_BF16 && p->kdim % 16 == 0 ? 1 : 0; }
+
+static int check_saved(const gpa_gdn_problem* p, const gpa_gdn_saved* sv) {
+  if (!sv || !sv->kn || !sv->u || !sv->delta || !sv->tri || !sv->gam || !sv->beta || !sv->states || !sv->final)
+    return fail(GPA_HIP_EINVAL, "gdn: a saved buffer is null");
+  if (p->q.ptr && !sv->qn) return fail(GPA_HIP_EINVAL, "gdn: q given without qn");
+  if (path_of(p)) {
+    if (!sv->wrow || !sv->wcol || !sv->krow || !sv->kcol || (p->q.ptr && !sv->qcol))
+      return fail(GPA_HIP_EINVAL, "gdn: the MFMA path needs the fragment buffers");
+  } else if (!sv->w) {
+    return fail(GPA_HIP_EINVAL, "gdn: the FMA path needs w");
+  }
+  return GPA_HIP_OK;
+}
+
+extern "C" int32_t gpa_gdn_path(const gpa_gdn_problem* problem) { return problem ? path_of(problem) : 0; }
+
 extern "C" int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk) {
   if (tokens < 1 || chunk < 1 || chunk > GPA_CHUNK_ROWS || offset < 0 || offset >= chunk) return 0;
   return (offset + tokens + chunk - 1) / chunk;
@@ -1115,10 +1228,8 @@ extern "C" int gpa_gdn_forward(const gpa_gdn_problem* problem, const gpa_gdn_sav
                                gpa_timing* timing, hipStream_t stream) {
   int rc = check_problem(problem);
   if (rc) return rc;
-  if (!saved || !saved->kn || !saved->w || !saved->u || !saved->delta || !saved->tri || !saved->gam ||
-      !saved->beta || !saved->states || !saved->final)
-    return fail(GPA_HIP_EINVAL, "gdn_forward: a saved buffer is null");
-  if (problem->q.ptr && (!saved->qn || !out.ptr)) return fail(GPA_HIP_EINVAL, "gdn_forward: q given without qn/out");
+  if (int rc2 = check_saved(problem, saved)) return rc2;
+  if (problem->q.ptr && !out.ptr) return fail(GPA_HIP_EINVAL, "gdn_forward: q given without out");
   const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
   if (timing) timing->launched = 0;
   return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, *saved, out, timing, stream, nch)
@@ -1129,12 +1240,13 @@ extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_sa
                                 const gpa_gdn_grads* grads, gpa_timing* timing, hipStream_t stream) {
   int rc = check_problem(problem);
   if (rc) return rc;
-  if (!saved || !grads) return fail(GPA_HIP_EINVAL, "gdn_backward: null saved/grads");
+  if (!grads) return fail(GPA_HIP_EINVAL, "gdn_backward: null grads");
+  if (int rc2 = check_saved(problem, saved)) return rc2;
   if (!grads->ddelta || !grads->dhend || !grads->dw || !grads->dk.ptr || !grads->dv.ptr || !grads->dg.ptr ||
       !grads->dbeta.ptr || !grads->ds0)
     return fail(GPA_HIP_EINVAL, "gdn_backward: a gradient buffer is null");
-  if (problem->q.ptr && grads->dout.ptr && (!grads->dd0 || !grads->dq.ptr || !saved->qn))
-    return fail(GPA_HIP_EINVAL, "gdn_backward: read gradient needs dd0, dq and qn");
+  if (problem->q.ptr && grads->dout.ptr && (!grads->dd0 || !grads->o || !grads->dq.ptr))
+    return fail(GPA_HIP_EINVAL, "gdn_backward: read gradient needs dd0, o and dq");
   const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
   if (timing) timing->launched = 0;
   return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, timing, stream, nch)

@@ -23,7 +23,21 @@ def _f32_state(s: Tensor) -> Tensor:
     return s if (s.stride(3) == 1 and s.stride(2) == s.shape[3]) else s.contiguous()
 
 
+def _problem(q, k, v, g, beta, s0f, chunk, offset):
+    bsz, tokens, heads, kd = k.shape
+    return _lib.Problem(bsz, heads, tokens, offset, chunk, kd, v.shape[-1], _lib.DTYPE_CODES[k.dtype],
+                        _lib.operand(q), _lib.operand(k), _lib.operand(v), _lib.operand(g), _lib.operand(beta),
+                        s0f.data_ptr() if s0f is not None else None,
+                        s0f.stride(0) if s0f is not None else 0, s0f.stride(1) if s0f is not None else 0)
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
 class _GDNScan(torch.autograd.Function):
+    """One group of GDN scans; saved intermediates per include/gpa_hip.h."""
+
     @staticmethod
     def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int):
         lib = _lib.load()
@@ -33,53 +47,57 @@ class _GDNScan(torch.autograd.Function):
         nch = lib.gpa_gdn_nchunks(tokens, offset, chunk)
         if nch <= 0:
             raise ValueError("gdn_scan_hip: invalid chunk geometry")
-        streams = bsz * heads
-        rows = streams * nch * _lib.CHUNK_ROWS
+        s0f = _f32_state(s0) if s0 is not None else None
+        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        mfma = lib.gpa_gdn_path(prob) == 1
+        chunks = bsz * heads * nch
+        rows = chunks * _lib.CHUNK_ROWS
         f32 = dict(device=dev, dtype=torch.float32)
+        b16 = dict(device=dev, dtype=torch.bfloat16)
         kn = torch.empty(rows * kd, **f32)
         qn = torch.empty(rows * kd, **f32) if q is not None else None
-        w = torch.empty(rows * kd, **f32)
+        w = torch.empty(rows * kd, **f32) if not mfma else None
         u = torch.empty(rows * vd, **f32)
         delta = torch.empty(rows * vd, **f32)
         tri = torch.empty(rows * _lib.CHUNK_ROWS, **f32)
         gam = torch.empty(rows, **f32)
         bet = torch.empty(rows, **f32)
-        states = torch.empty(bsz, heads, nch, kd, vd, **f32)
+        states = torch.empty(bsz, heads, nch, vd, kd, **f32)   # value-major chunk-start states
         final = torch.empty(bsz, heads, kd, vd, **f32)
+        frags = [None] * 5
+        if mfma:
+            k16, rb = kd // 16, (kd + 31) // 32
+            frags = [torch.empty(chunks * 2 * k16 * 64 * 16, **b16),   # wrow
+                     torch.empty(chunks * rb * 4 * 64 * 16, **b16),    # wcol
+                     torch.empty(chunks * 2 * k16 * 64 * 8, **b16),    # krow
+                     torch.empty(chunks * rb * 4 * 64 * 8, **b16),     # kcol
+                     torch.empty(chunks * rb * 4 * 64 * 8, **b16) if q is not None else None]  # qcol
         out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype) if q is not None else None
-        s0f = _f32_state(s0) if s0 is not None else None
-        prob = _lib.Problem(bsz, heads, tokens, offset, chunk, kd, vd, _lib.DTYPE_CODES[k.dtype],
-                            _lib.operand(q), _lib.operand(k), _lib.operand(v),
-                            _lib.operand(g), _lib.operand(beta),
-                            s0f.data_ptr() if s0f is not None else None,
-                            s0f.stride(0) if s0f is not None else 0, s0f.stride(1) if s0f is not None else 0)
-        saved = _lib.Saved(kn.data_ptr(), qn.data_ptr() if qn is not None else None, w.data_ptr(), u.data_ptr(),
-                           delta.data_ptr(), tri.data_ptr(), gam.data_ptr(), bet.data_ptr(),
-                           states.data_ptr(), final.data_ptr())
-        timing = profiling.forward_timing(kd, vd, chunk, tokens * streams, k.dtype, q is not None)
+        saved = _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
+        timing = profiling.forward_timing(kd, vd, chunk, tokens * bsz * heads, k.dtype, q is not None)
         _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), timing, _lib.stream_handle(dev)),
                    "gpa_gdn_forward")
-        ctx.geom = (chunk, offset, nch, q is not None, s0 is not None)
-        ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final)
+        ctx.geom = (chunk, offset, nch, q is not None, s0 is not None, mfma)
+        ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)
         return out, states, final
 
     @staticmethod
     def backward(ctx, dout, dstates, dfinal):
         lib = _lib.load()
-        chunk, offset, nch, has_q, has_s0 = ctx.geom
-        (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final) = ctx.saved_tensors
+        chunk, offset, nch, has_q, has_s0, mfma = ctx.geom
+        (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags) = ctx.saved_tensors
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
         dev = k.device
-        streams = bsz * heads
-        rows = streams * nch * _lib.CHUNK_ROWS
+        rows = bsz * heads * nch * _lib.CHUNK_ROWS
         f32 = dict(device=dev, dtype=torch.float32)
         want_read = has_q and dout is not None
         if want_read:
             dout = _contig_last(dout.to(k.dtype))
         dd0 = torch.empty(rows * vd, **f32) if want_read else None
+        obuf = torch.empty(rows * vd, **f32) if want_read else None
         ddelta = torch.empty(rows * vd, **f32)
-        dhend = torch.empty(streams * nch * kd * vd, **f32)
+        dhend = torch.empty(bsz * heads * nch * kd * vd, **f32)
         dw = torch.empty(rows * kd, **f32)
         dq = torch.zeros(bsz, tokens, heads, kd, **f32) if has_q else None
         dk = torch.empty(bsz, tokens, heads, kd, **f32)
@@ -89,21 +107,13 @@ class _GDNScan(torch.autograd.Function):
         ds0 = torch.empty(bsz, heads, kd, vd, **f32)
         dstates = dstates.float().contiguous() if dstates is not None else None
         dfinal = dfinal.float().contiguous() if dfinal is not None else None
-        prob = _lib.Problem(bsz, heads, tokens, offset, chunk, kd, vd, _lib.DTYPE_CODES[k.dtype],
-                            _lib.operand(q), _lib.operand(k), _lib.operand(v),
-                            _lib.operand(g), _lib.operand(beta),
-                            s0f.data_ptr() if s0f is not None else None,
-                            s0f.stride(0) if s0f is not None else 0, s0f.stride(1) if s0f is not None else 0)
-        saved = _lib.Saved(kn.data_ptr(), qn.data_ptr() if qn is not None else None, w.data_ptr(), u.data_ptr(),
-                           delta.data_ptr(), tri.data_ptr(), gam.data_ptr(), bet.data_ptr(),
-                           states.data_ptr(), final.data_ptr())
-        grads = _lib.Grads(_lib.operand(dout if want_read else None),
-                           dstates.data_ptr() if dstates is not None else None,
-                           dfinal.data_ptr() if dfinal is not None else None,
-                           dd0.data_ptr() if dd0 is not None else None, ddelta.data_ptr(), dhend.data_ptr(),
-                           dw.data_ptr(), _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
+        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        saved = _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
+        grads = _lib.Grads(_lib.operand(dout if want_read else None), _ptr(dstates), _ptr(dfinal),
+                           _ptr(dd0), _ptr(obuf), ddelta.data_ptr(), dhend.data_ptr(), dw.data_ptr(),
+                           _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
                            _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
-        timing = profiling.backward_timing(kd, vd, chunk, tokens * streams, k.dtype, want_read)
+        timing = profiling.backward_timing(kd, vd, chunk, tokens * bsz * heads, k.dtype, want_read)
         _lib.check(lib.gpa_gdn_backward(prob, saved, grads, timing, _lib.stream_handle(dev)), "gpa_gdn_backward")
         dq_out = dq.to(q.dtype) if (has_q and ctx.needs_input_grad[0]) else None
         return (dq_out, dk.to(k.dtype), dv.to(v.dtype), dg, db,
@@ -137,4 +147,5 @@ def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor
     q = _contig_last(q) if q is not None else None
     k, v = _contig_last(k), _contig_last(v)
     g, beta = g.float(), beta.float()
-    return _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)
+    out, states_vk, final = _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)
+    return out, states_vk.transpose(-1, -2), final

@@ -116,7 +116,8 @@ def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
         return None
     e, km = _tag(dtype), _kmax(k)
     state = f"gdn_state_fwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_fwd<{km}>"
-    kernels = [(f"gdn_prep<{e},{km}>", (4 * c * k + 2 * c * v + c * c / 3) * tokens),
+    kernels = [(f"gdn_prep<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
+                (4 * c * k + 2 * c * v + c * c / 3) * tokens),
                (state, 4 * k * v * tokens)]
     if read:
         kernels.append((f"gdn_out_fwd<{e},{km}>", (2 * k * v + 2 * c * k + 2 * c * v) * tokens))

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 2
+#define GPA_HIP_ABI_VERSION 3
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -66,29 +66,43 @@ typedef struct gpa_gdn_problem {
     int64_t s0_sb, s0_sh;
 } gpa_gdn_problem;
 
-/* Caller-owned float32 intermediates, all stream-major and contiguous:
- *   kn, qn, w      [streams, nchunks, 64, K]  normalised keys/queries, W = T diag(b e^G) Kn
- *   u, delta       [streams, nchunks, 64, V]  U = T diag(b) V, delta = U - W S_n
- *   tri            [streams, nchunks, 64, 64] T = (I + A)^-1
- *   gam, beta      [streams, nchunks, 64]     in-chunk cumulative log decay, beta (void rows 0)
- *   states         [streams, nchunks, K, V]   state at the start of every chunk
- *   final          [streams, K, V]            state after the last token
+/* Caller-owned intermediates, stream-major and contiguous (S = streams,
+ * N = nchunks, per chunk):
+ *   kn, qn         f32 [S,N,64,K]   normalised keys / queries (rows = positions)
+ *   w              f32 [S,N,64,K]   W = T diag(b e^G) Kn  (FMA path only)
+ *   u, delta       f32 [S,N,V,64]   U = T diag(b) V, D = U - W S_n  (value-major)
+ *   tri            f32 [S,N,64,64]  T = (I + A)^-1
+ *   gam, beta      f32 [S,N,64]     in-chunk cumulative log decay, beta (void rows 0)
+ *   states         f32 [S,N,V,K]    state at the start of every chunk, value-major
+ *                                   (element (k,v) of chunk n at [v*K + k])
+ *   final          f32 [S,K,V]      state after the last token (key-major)
+ * On the MFMA path (gpa_gdn_path() == 1) the sequential kernels read their
+ * matrix operands as bf16 MFMA fragments written by the chunk kernel; with
+ * K16 = K/16 and RB = ceil(K/32), per chunk:
+ *   wrow  [2][K16][64][16]  W rows:     lane l of fragment (rt,ks) holds
+ *                           W[32rt + l%32][16ks + 8(l/32) + e], e<8, as hi then lo
+ *   wcol  [RB][4][64][16]   W^T rows:   fragment (rb,cs), lane l, element e is
+ *                           W[16cs + 8(l/32) + e][32rb + l%32], hi then lo
+ *   krow  [2][K16][64][8]   Kn rows (exact in bf16), same placement as wrow
+ *   kcol  [RB][4][64][8]    Kn^T rows, same placement as wcol
+ *   qcol  [RB][4][64][8]    Qn^T rows (only with a query)
  * qn is written only when problem.q.ptr != NULL. */
 typedef struct gpa_gdn_saved {
     float *kn, *qn, *w, *u, *delta, *tri, *gam, *beta, *states, *final;
+    void *wrow, *wcol, *krow, *kcol, *qcol;
 } gpa_gdn_saved;
 
 /* Backward inputs and outputs.  dout (problem dtype, strided like out) may be
- * NULL (no read gradient); dstates [streams,nchunks,K,V] injects gradients of
- * the chunk-start states (NULL = none); dfinal [streams,K,V] (NULL = none).
- * Scratch (caller-owned float32): dd [streams,nchunks,64,V] x2, dhend
- * [streams,nchunks,K,V], dw [streams,nchunks,64,K].  Gradient outputs are
- * float32 operands: dq (skipped when q was NULL), dk [.. K], dv [.. V],
- * dg, dbeta per token; ds0 [streams,K,V] contiguous. */
+ * NULL (no read gradient); dstates f32 [S,N,V,K] (value-major, like states)
+ * injects gradients of the chunk-start states (NULL = none); dfinal f32
+ * [S,K,V] (NULL = none).  Caller-owned f32 scratch: dd0, o, ddelta
+ * [S,N,V,64], dhend [S,N,V,K], dw [S,N,64,K].  Gradient outputs are f32
+ * operands: dq (skipped when q was NULL), dk [.. K], dv [.. V], dg, dbeta per
+ * token; ds0 [S,K,V] contiguous. */
 typedef struct gpa_gdn_grads {
     gpa_operand dout;
     const float *dstates, *dfinal;
-    float *dd0, *ddelta, *dhend, *dw;
+    float *dd0, *o, *ddelta, *dhend, *dw;
     gpa_operand dq, dk, dv, dg, dbeta;
     float *ds0;
 } gpa_gdn_grads;
@@ -107,6 +121,9 @@ int gpa_hip_abi_version(void);
 const char *gpa_hip_last_error(void);
 /* Number of chunks a problem spans (0 on invalid geometry). */
 int32_t gpa_gdn_nchunks(int32_t tokens, int32_t offset, int32_t chunk);
+/* 1 when the problem runs its state recurrences on bf16 MFMA (bf16 data,
+ * K a multiple of 16) and needs the fragment buffers; 0 on the fp32 FMA path. */
+int32_t gpa_gdn_path(const gpa_gdn_problem *problem);
 
 /* Forward chunked gated-delta-rule scan; `out` (problem dtype) receives
  * u(q_t)^T S_t when q.ptr != NULL.

@@ -17,7 +17,7 @@ def _declared():
 
 def test_header_declares_the_entry_points():
     names = _declared()
-    for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks",
+    for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
                      "gpa_gdn_forward", "gpa_gdn_backward"):
         assert expected in names
 
@@ -37,6 +37,13 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert typed.gpa_gdn_nchunks(1, 63, 64) == 1
     assert typed.gpa_gdn_nchunks(2, 63, 64) == 2
     assert typed.gpa_gdn_nchunks(5, 4, 4) == 0  # offset must be < chunk
+    prob = _lib.Problem()
+    prob.dtype, prob.kdim = 1, 128
+    assert typed.gpa_gdn_path(prob) == 1      # bf16, K % 16 == 0: MFMA recurrences
+    prob.kdim = 40
+    assert typed.gpa_gdn_path(prob) == 0
+    prob.dtype, prob.kdim = 0, 128
+    assert typed.gpa_gdn_path(prob) == 0      # fp32: FMA recurrences
 
 
 def test_ctypes_structs_match_c_layout():
@@ -44,8 +51,9 @@ def test_ctypes_structs_match_c_layout():
     assert ctypes.sizeof(_lib.Operand) == 32
     # 8 int32, 5 operands, pointer + 2 int64
     assert ctypes.sizeof(_lib.Problem) == 32 + 5 * 32 + 24
-    assert ctypes.sizeof(_lib.Saved) == 10 * 8
-    assert ctypes.sizeof(_lib.Grads) == 32 + 6 * 8 + 5 * 32 + 8
+    assert ctypes.sizeof(_lib.Saved) == 15 * 8
+    assert ctypes.sizeof(_lib.Grads) == 32 + 7 * 8 + 5 * 32 + 8
+    assert ctypes.sizeof(_lib.Timing) == 5 * 8 + 8
 
 
 def test_backend_refuses_cpu_tensors():
