@@ -53,7 +53,7 @@ def f_forward_per_token_head(dk: int, dv: int, slots, c: int) -> float:
     return total
 
 
-def cpu_baseline(sample_tokens: int = 64) -> dict:
+def cpu_baseline(sample_tokens: int = 512) -> dict:
     """The oracle (per-token reference algorithm, fp32) timed on this host."""
     import torch
 

@@ -106,7 +106,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             kb = blocks.split(_unit(key).float())       # [B,N,C,H,Dk]
             write = blocks.merge(torch.einsum("bnchd,bhndm->bnchm", kb, a_hat)).softmax(-1)
         write = write.to(dtype)
-        counts = old.count[:, None] + write.float().cumsum(1)
+        counts = old.count[:, None] + _cumsum_tokens(write.float())
         wb = blocks.split(write.float())
         rk = blocks.merge(torch.einsum("bhndm,bnchm->bnchd", a_hat, wb))
         rv = blocks.merge(torch.einsum("bnchm,bhnmv->bnchv", wb, b_hat))
@@ -145,6 +145,12 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
 
 
 # --------------------------------------------------------------------------- glue
+def _cumsum_tokens(x: Tensor) -> Tensor:
+    """Cumulative sum over tokens of a [B,T,H,M] tensor, scanned along the
+    innermost axis (a scan over an outer axis is far slower on the GPU)."""
+    return x.permute(0, 2, 3, 1).contiguous().cumsum(-1).permute(0, 3, 1, 2).contiguous()
+
+
 def _slot_feature(cfg, x: Tensor) -> Tensor:
     """attention.py:179-184."""
     if cfg.slot_feature == "softmax":
