@@ -1170,12 +1170,16 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
     if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
     hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
   }
-  constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
-  constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
-  const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
-  if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
   mark(tm, st);
-  hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  if (p.kdim % 4 == 0) {
+    if (int rc = launch_chunk_bwd_mfma<E, KM>(p, sv, gr, nch, st)) return rc;
+  } else {
+    constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
+    constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
+    const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
+    if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
+    hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  }
   mark(tm, st);
   return check_launch("gdn_backward");
 }

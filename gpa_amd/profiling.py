@@ -11,9 +11,8 @@ together with each launch's algorithmic FLOP count:
   gdn_out_fwd    2KV + 2CK + 2CV          Q S, Q K^T, P D
   gdn_dd0        2CK + 2CV                Q K^T, P^T dO
   gdn_state_bwd  4KV (+2KV with a read)   K dS, W^T dD (+ Q^T dO)
-  gdn_chunk_bwd  4KV + 8CK + 4CV + 4C^2   dD S^T, D dS^T, K K^T, dW K^T, dD (bV)^T,
-                 (+2KV + 6CK + 2CV)       dT T^T, T^T X, dKK K, T^T dW, T^T dD
-                                          (+ dO S^T, Q K^T, dO D^T, dQK K, dQK^T Q)
+  gdn_chunk_bwd  4KV + 4CV + 4CK + 2C^2   D dS^T, Y S^T, dD D^T, T^T dD, K K^T, T^T X,
+                 (+2KV + 2CV + 6CK)       dKK K (+ dO S^T, dO D^T, Q K^T, dQK K, dQK^T Q)
 with C the chunk length, K/V the scan widths, per real token of every stream.
 Outside the context manager nothing is recorded and no event exists.
 """
@@ -133,8 +132,9 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
         kernels.append((f"gdn_dd0<{e},{km}>", (2 * c * k + 2 * c * v) * tokens))
     state = f"gdn_state_bwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_bwd<{e},{km}>"
     kernels.append((state, (6 if read else 4) * k * v * tokens))
-    chunk = 4 * k * v + 8 * c * k + 4 * c * v + 4 * c * c
+    chunk = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c
     if read:
-        chunk += 2 * k * v + 6 * c * k + 2 * c * v
-    kernels.append((f"gdn_chunk_bwd<{e},{km}>", chunk * tokens))
+        chunk += 2 * k * v + 2 * c * v + 6 * c * k
+    name = "gdn_chunk_bwd_mfma" if k % 4 == 0 else "gdn_chunk_bwd"
+    kernels.append((f"{name}<{e},{km}>", chunk * tokens))
     return _active.timing(kernels)
