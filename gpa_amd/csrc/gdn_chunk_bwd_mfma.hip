@@ -13,7 +13,11 @@
 // plus the gate gradients of every e^G factor and b, then the L2
 // normalisation backward of q and k.  The contraction over the value axis is
 // streamed through LDS in 16-value slices; each wave owns fixed 32x32 output
-// tiles and keeps them in accumulators for the whole kernel.
+// tiles and keeps them in accumulators for the whole kernel.  The block
+// recomputes the row norms of its raw keys and queries (the same sums as the
+// forward's normalisation) and keeps x/|x| for one key panel in LDS: the
+// rounded copy is the matrix operand Kn/Qn, the unrounded one the input of the
+// normalisation backward.
 //
 // Operand feeding.  A 32x32x2 MFMA step takes one A and one B value per lane:
 // A(row l%32, c), B(c, col l%32) with c = 2 s + l/32.  This file instead
@@ -25,6 +29,8 @@
 // accumulator of a 32x32 tile holds, in lane l register r, row
 // 8 (r/4) + 4 (l/32) + r%4 and column l%32.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "gdn_common.h"
 
@@ -57,15 +63,6 @@ __device__ __forceinline__ f32x4 ld_c(const float* m, int ld, int x, int c0) {
 // ... or with x contiguous.
 __device__ __forceinline__ f32x4 ld_x(const float* m, int ld, int x, int c0) {
   return f32x4{m[c0 * ld + x], m[(c0 + 1) * ld + x], m[(c0 + 2) * ld + x], m[(c0 + 3) * ld + x]};
-}
-
-// A copy of a uniform value the compiler cannot see through: values derived
-// from it inside a loop are not hoisted out of the loop (where they would
-// occupy registers for its whole length).
-template <typename T>
-__device__ __forceinline__ T opaque(T x) {
-  asm volatile("" : "+s"(x));
-  return x;
 }
 
 __device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
@@ -103,54 +100,82 @@ __device__ __forceinline__ int sum_index(int lane) {
   return 8 * ((lane >> 4) & 1) + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 1) & 1);
 }
 
+// Four consecutive activation-type elements as floats (8 bytes for bf16).
+__device__ __forceinline__ f32x4 ld_c(const bf16_t* m, int ld, int x, int c0) {
+  const uint2 w = *reinterpret_cast<const uint2*>(m + x * ld + c0);
+  return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+               __uint_as_float(w.y & 0xffff0000u)};
+}
+
+template <typename E>
+__device__ __forceinline__ E op_raw(const gpa_operand& o, int b, int h, int t, int d) {
+  return reinterpret_cast<const E*>(o.ptr)[op_base(o, b, h) + (int64_t)t * o.st + d];
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Eight consecutive floats rounded to bf16 (round to nearest even).
+__device__ __forceinline__ bf16x8 pack8(const float* x) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(x), c = *reinterpret_cast<const f32x4*>(x + 4);
+  bf16x8 r;
+  r[0] = (__bf16)a.x; r[1] = (__bf16)a.y; r[2] = (__bf16)a.z; r[3] = (__bf16)a.w;
+  r[4] = (__bf16)c.x; r[5] = (__bf16)c.y; r[6] = (__bf16)c.z; r[7] = (__bf16)c.w;
+  return r;
+}
+
+template <typename E>
+__device__ __forceinline__ f32x4 round4(f32x4 x) {
+  return f32x4{round_as<E>(x.x), round_as<E>(x.y), round_as<E>(x.z), round_as<E>(x.w)};
+}
+
 }  // namespace
 
 // LDS plan (floats).  One key panel (KM <= 128): the R x R matrices reuse the
 // staging area once the value loop is done; two panels keep dQK and dKK apart.
-template <int KM>
+template <typename E, int KM>
 struct ChunkBwdLayout {
   static constexpr int KP = KM < 128 ? KM : 128;  // key panel
   static constexpr int NP = KM / KP;
   static constexpr int VS = 16;                   // value slice
-  static constexpr int LDO = VS + 4, LT = R + 4, LS = KP + 4, KSL = 32, LKN = KSL + 4;
+  static constexpr int LDO = VS + 4, LT = R + 4, LS = KP + 4, LX = KP + 4;
+  static constexpr int EQ = R * LDO * (int)sizeof(E) / 4;  // floats of one [R][LDO] activation tile
   // value-loop staging
-  static constexpr int DO = 0, VV = DO + R * LDO, D = VV + R * LDO, DD = D + VS * LT, Y = DD + VS * LT,
-                       S = Y + VS * LT, DS = S + VS * LS, V_END = DS + VS * LS;
-  // key-loop staging (P, KK)
-  static constexpr int QK = 0, KK = QK + R * LKN, K_END = KK + R * LKN;
+  static constexpr int DO = 0, VV = DO + EQ, D = VV + EQ, DD = D + VS * LT, Y = DD + VS * LT, S = Y + VS * LT,
+                       DS = S + VS * LS, V_END = DS + VS * LS;
   static constexpr int RR1 = 2 * R * LT;  // xm + dQK inside the staging area (one panel)
-  static constexpr int STAGE = V_END > RR1 ? (V_END > K_END ? V_END : K_END) : (RR1 > K_END ? RR1 : K_END);
-  static constexpr int T_OFF = 0;
+  static constexpr int STAGE = (NP == 1 && RR1 > V_END) ? RR1 : V_END;
   static constexpr int OWN = NP == 1 ? 0 : 2 * R * LT;  // separate dQK, dKK
-  static constexpr int STAGE_OFF = R * LT + OWN;
+  static constexpr int T_OFF = 0, XK_OFF = R * LT + OWN, XQ_OFF = XK_OFF + R * LX, STAGE_OFF = XQ_OFF + R * LX;
   static constexpr int XM_OFF = STAGE_OFF;
   static constexpr int DQK_OFF = NP == 1 ? STAGE_OFF + R * LT : R * LT;
   static constexpr int DKK_OFF = NP == 1 ? STAGE_OFF : 2 * R * LT;
   static constexpr int SC_OFF = STAGE_OFF + STAGE;
-  static constexpr int TOTAL = SC_OFF + 9 * R + 4;
+  static constexpr int TOTAL = SC_OFF + 13 * R + 4;
+  static constexpr size_t BYTES = sizeof(float) * TOTAL;
 };
 
 template <typename E, int KM>
 __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv,
-                                                                          gpa_gdn_grads gr, int nch) {
-  using L = ChunkBwdLayout<KM>;
-  constexpr int KP = L::KP, NP = L::NP, VS = L::VS, LDO = L::LDO, LT = L::LT, LS = L::LS, KSL = L::KSL,
-                LKN = L::LKN;
-  constexpr int NTW = KP / 64;        // R x KP output tiles per wave
-  constexpr int SQ = VS * KP / 4 / NT;  // float4 of S per thread per slice
-  static_assert(SQ >= 1 && VS * R / 4 == NT && R * VS == 4 * NT, "staging shape");
+                                                           gpa_gdn_grads gr, int nch) {
+  using L = ChunkBwdLayout<E, KM>;
+  constexpr int KP = L::KP, NP = L::NP, VS = L::VS, LDO = L::LDO, LT = L::LT, LS = L::LS, LX = L::LX;
+  constexpr int NTW = KP / 64;          // R x KP output tiles per wave
+  constexpr int SQ = VS * KP / 4 / NT;  // float4 of S (and of dS) per thread per slice
+  constexpr int DQ = VS * R / 4 / NT;   // float4 of D (and of dD) per thread per slice
+  constexpr int OQ = R * VS / NT;       // elements of dO (and of V) per thread per slice
+  static_assert(SQ >= 1 && DQ >= 1 && VS % 16 == 0, "staging shape");
   extern __shared__ __align__(16) float smem[];
   float* tm = smem + L::T_OFF;
+  float* xk_s = smem + L::XK_OFF;
+  float* xq_s = smem + L::XQ_OFF;
   float* stage = smem + L::STAGE_OFF;
-  float* do_s = stage + L::DO;
-  float* vv_s = stage + L::VV;
+  E* do_s = reinterpret_cast<E*>(stage + L::DO);
+  E* vv_s = reinterpret_cast<E*>(stage + L::VV);
   float* d_s = stage + L::D;
   float* dd_s = stage + L::DD;
   float* y_s = stage + L::Y;
   float* s_s = stage + L::S;
   float* ds_s = stage + L::DS;
-  float* qk_s = stage + L::QK;
-  float* kk_s = stage + L::KK;
   float* xm = smem + L::XM_OFF;
   float* dqk = smem + L::DQK_OFF;
   float* dkk = smem + L::DKK_OFF;
@@ -158,19 +183,23 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
   float* bet_s = gam_s + R;
   float* dgam_s = bet_s + R;
   float* dbet_s = dgam_s + R;
-  float* qss_s = dbet_s + R;
-  float* qxg_s = qss_s + R;
-  float* kss_s = qxg_s + R;
-  float* kxg_s = kss_s + R;
-  int* tok_s = reinterpret_cast<int*>(kxg_s + R);  // token of each row (-1: void)
-  float* red_s = kxg_s + 2 * R;
+  float* qnrm_s = dbet_s + R;  // |q_t|, |k_t| of the raw rows
+  float* knrm_s = qnrm_s + R;
+  float* qdot_s = knrm_s + R;  // sum_k x/|x| . dX of the rows
+  float* kdot_s = qdot_s + R;
+  float* eg_s = kdot_s + R;   // e^{G_t}
+  float* ek_s = eg_s + R;     // e^{G_C - G_t}
+  float* qrd_s = ek_s + R;    // 1 / max(|q_t|, 1e-6), 1 / max(|k_t|, 1e-6)
+  float* krd_s = qrd_s + R;
+  int* tok_s = reinterpret_cast<int*>(krd_s + R);  // token of each row (-1: void)
+  float* red_s = krd_s + 2 * R;
 
   const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
   const int K = p.kdim, V = p.vdim, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hh = lane >> 5;
   const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr;
-  const float* kn0 = sv.kn + rows_off(s, n, nch, 0, K);
-  const float* qn0 = has_q ? sv.qn + rows_off(s, n, nch, 0, K) : nullptr;
+  const float* kn = sv.kn + rows_off(s, n, nch, 0, K);
+  const float* qn = has_q ? sv.qn + rows_off(s, n, nch, 0, K) : nullptr;
   const float* st = sv.states + state_off(s, n, nch, K, V);
   const float* dh = gr.dhend + state_off(s, n, nch, K, V);
   const float* dl = sv.delta + vc_off(s, n, nch, V);
@@ -181,7 +210,7 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
     bet_s[tid] = sv.beta[rows_off(s, n, nch, 0, 1) + tid];
     dgam_s[tid] = dbet_s[tid] = 0.f;
-    qss_s[tid] = qxg_s[tid] = kss_s[tid] = kxg_s[tid] = 0.f;
+    qdot_s[tid] = kdot_s[tid] = 0.f;
     tok_s[tid] = token_at(p, n, tid);
   }
   if (tid < 4) red_s[tid] = 0.f;
@@ -189,8 +218,59 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     const int t = i / (R / 4), c = 4 * (i % (R / 4));
     *reinterpret_cast<f32x4*>(tm + t * LT + c) = *reinterpret_cast<const f32x4*>(tri + t * R + c);
   }
+  // Row norms of the raw keys and queries, summed in the forward's order; with
+  // one panel also x/|x| for every key column.  Every load of the wave is
+  // issued (at a clamped address, from a stand-in operand when there is no
+  // query) before the first use.
+  {
+    constexpr int NI = KM / 64, NR = R / 4;
+    const gpa_operand& qsrc = has_q ? p.q : p.k;
+    float xk[NR][NI], xq[NR][NI];
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const int tok = token_at(p, n, wave + 4 * j), tt = tok >= 0 ? tok : 0;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int d = lane + 64 * i, dd = d < K ? d : 0;
+        xk[j][i] = op_load<E>(p.k, b, h, tt, dd);
+        xq[j][i] = op_load<E>(qsrc, b, h, tt, dd);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const int r = wave + 4 * j, tok = token_at(p, n, r);
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const bool ok = tok >= 0 && lane + 64 * i < K;
+        xk[j][i] = ok ? xk[j][i] : 0.f;
+        xq[j][i] = (ok && has_q) ? xq[j][i] : 0.f;
+        sk += xk[j][i] * xk[j][i];
+        sq += xq[j][i] * xq[j][i];
+      }
+      const float nk = sqrtf(sum64(sk)), nq = sqrtf(sum64(sq));
+      if (lane == 0) {
+        knrm_s[r] = nk;
+        qnrm_s[r] = nq;
+        krd_s[r] = 1.f / fmaxf(nk, 1e-6f);
+        qrd_s[r] = 1.f / fmaxf(nq, 1e-6f);
+      }
+      if (NP == 1) {
+        const float dk = fmaxf(nk, 1e-6f), dq = fmaxf(nq, 1e-6f);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          xk_s[r * LX + lane + 64 * i] = xk[j][i] / dk;
+          xq_s[r * LX + lane + 64 * i] = xq[j][i] / dq;
+        }
+      }
+    }
+  }
   __syncthreads();
   const float gc = gam_s[R - 1];
+  if (tid < R) {
+    eg_s[tid] = __expf(gam_s[tid]);
+    ek_s[tid] = __expf(gc - gam_s[tid]);
+  }
 
   // Output tiles: R x KP tiles m < NTW at rows 32 rt(m), panel columns 32 kt;
   // the R x R tile at (32 rr, 32 ru).
@@ -202,62 +282,91 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
   // dQn, dKn of the current panel (the last one after the loop); earlier
   // panels are parked unnormalised in dq/dk and re-read by the same lanes.
   f32x16 dq[NTW], dka[NTW], dkw[NTW];
-  float ddot = 0.f;                 // this thread's share of <S_n, dS>
+  float ddot = 0.f;  // this thread's share of <S_n, dS>
   const int nsl = (V + VS - 1) / VS;
 
 #pragma unroll 1
   for (int panel = 0; panel < NP; ++panel) {
     const int kb = panel * KP;
-    const int K = opaque(p.kdim);
-    const float* kn = opaque(kn0);
-    const float* qn = opaque(qn0);
+    if (NP > 1) {
+      if (panel > 0) __syncthreads();  // the previous panel's x/|x| is no longer read
+#pragma unroll
+      for (int j = 0; j < R / 4; ++j) {
+        const int r = wave + 4 * j, tok = tok_s[r], tt = tok >= 0 ? tok : 0;
+        const float dk = fmaxf(knrm_s[r], 1e-6f), dq = fmaxf(qnrm_s[r], 1e-6f);
+#pragma unroll
+        for (int i = 0; i < KP / 64; ++i) {
+          const int d = kb + lane + 64 * i;
+          const bool ok = tok >= 0 && d < K;
+          const float xk = op_load<E>(p.k, b, h, tt, ok ? d : 0);
+          const float xq = op_load<E>(has_q ? p.q : p.k, b, h, tt, ok ? d : 0);
+          xk_s[r * LX + lane + 64 * i] = ok ? xk / dk : 0.f;
+          xq_s[r * LX + lane + 64 * i] = (ok && has_q) ? xq / dq : 0.f;
+        }
+      }
+    }
 #pragma unroll
     for (int m = 0; m < NTW; ++m) dq[m] = dka[m] = dkw[m] = f32x16{};
 
     // ---- value loop: register prefetch of slice sl+1 while slice sl is in LDS.
-    f32x4 rs[SQ], rds[SQ], rd, rdd;
-    float rdo[4], rv[4];
+    f32x4 rs[SQ], rds[SQ], rd[DQ], rdd[DQ];
+    E rdo[OQ], rv[OQ];
+    // fetch() only issues loads (at a clamped, always valid address); the
+    // masks of void or out-of-range entries are applied in stash(), after the
+    // MFMA work of the current slice, so the loads stay in flight meanwhile.
+    const gpa_operand& dosrc = has_q ? gr.dout : p.v;  // stand-in of the same shape when there is no read
+    int vnext = 0;
     auto fetch = [&](int v0) {
+      vnext = v0;
 #pragma unroll
       for (int i = 0; i < SQ; ++i) {
         const int idx = tid + NT * i, vr = idx / (KP / 4), c = 4 * (idx % (KP / 4));
         const int v = v0 + vr, k = kb + c;
-        const bool ok = v < V && k < K;
-        rs[i] = ok ? *reinterpret_cast<const f32x4*>(st + (int64_t)v * K + k) : f32x4{};
-        rds[i] = ok ? *reinterpret_cast<const f32x4*>(dh + (int64_t)v * K + k) : f32x4{};
-      }
-      {
-        const int vr = tid / (R / 4), c = 4 * (tid % (R / 4)), v = v0 + vr;
-        rd = v < V ? *reinterpret_cast<const f32x4*>(dl + (int64_t)v * R + c) : f32x4{};
-        rdd = v < V ? *reinterpret_cast<const f32x4*>(ddl + (int64_t)v * R + c) : f32x4{};
+        const int64_t o = (v < V && k < K) ? (int64_t)v * K + k : 0;
+        rs[i] = *reinterpret_cast<const f32x4*>(st + o);
+        rds[i] = *reinterpret_cast<const f32x4*>(dh + o);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < DQ; ++i) {
+        const int idx = tid + NT * i, vr = idx / (R / 4), c = 4 * (idx % (R / 4)), v = v0 + vr;
+        const int64_t o = v < V ? (int64_t)v * R + c : 0;
+        rd[i] = *reinterpret_cast<const f32x4*>(dl + o);
+        rdd[i] = *reinterpret_cast<const f32x4*>(ddl + o);
+      }
+#pragma unroll
+      for (int i = 0; i < OQ; ++i) {
         const int idx = tid + NT * i, t = idx / VS, v = v0 + idx % VS;
-        const int tok = token_at(p, n, t);
+        const int tok = tok_s[t];
         const bool ok = tok >= 0 && v < V;
-        rdo[i] = (has_q && ok) ? op_load<E>(gr.dout, b, h, tok, v) : 0.f;
-        rv[i] = (panel == 0 && ok) ? op_load<E>(p.v, b, h, tok, v) : 0.f;
+        const int tt = ok ? tok : 0, vv = ok ? v : 0;
+        rdo[i] = op_raw<E>(dosrc, b, h, tt, vv);
+        rv[i] = op_raw<E>(p.v, b, h, tt, vv);
       }
     };
     auto stash = [&]() {
+      const int v0 = vnext;
 #pragma unroll
       for (int i = 0; i < SQ; ++i) {
         const int idx = tid + NT * i, vr = idx / (KP / 4), c = 4 * (idx % (KP / 4));
-        *reinterpret_cast<f32x4*>(s_s + vr * LS + c) = rs[i];
-        *reinterpret_cast<f32x4*>(ds_s + vr * LS + c) = rds[i];
-        ddot += rs[i].x * rds[i].x + rs[i].y * rds[i].y + rs[i].z * rds[i].z + rs[i].w * rds[i].w;
-      }
-      {
-        const int vr = tid / (R / 4), c = 4 * (tid % (R / 4));
-        *reinterpret_cast<f32x4*>(d_s + vr * LT + c) = rd;
-        *reinterpret_cast<f32x4*>(dd_s + vr * LT + c) = rdd;
+        const bool ok = v0 + vr < V && kb + c < K;
+        const f32x4 a = ok ? rs[i] : f32x4{}, d = ok ? rds[i] : f32x4{};
+        *reinterpret_cast<f32x4*>(s_s + vr * LS + c) = a;
+        *reinterpret_cast<f32x4*>(ds_s + vr * LS + c) = d;
+        ddot += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < DQ; ++i) {
+        const int idx = tid + NT * i, vr = idx / (R / 4), c = 4 * (idx % (R / 4));
+        const bool ok = v0 + vr < V;
+        *reinterpret_cast<f32x4*>(d_s + vr * LT + c) = ok ? rd[i] : f32x4{};
+        *reinterpret_cast<f32x4*>(dd_s + vr * LT + c) = ok ? rdd[i] : f32x4{};
+      }
+#pragma unroll
+      for (int i = 0; i < OQ; ++i) {
         const int idx = tid + NT * i, t = idx / VS, c = idx % VS;
-        do_s[t * LDO + c] = rdo[i];
-        vv_s[t * LDO + c] = rv[i];
+        const bool ok = tok_s[t] >= 0 && v0 + c < V;
+        do_s[t * LDO + c] = (ok && has_q) ? rdo[i] : from_f32<E>(0.f);
+        vv_s[t * LDO + c] = (ok && panel == 0) ? rv[i] : from_f32<E>(0.f);
       }
     };
 
@@ -267,26 +376,26 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     for (int sl = 0; sl < nsl; ++sl) {
       const int v0 = sl * VS;
       if (sl + 1 < nsl) fetch(v0 + VS);
-      // Y slice: rows 16 wave .. +15, the 16 values of the slice (16x16x4).
-      {
+#pragma unroll
+      for (int j = 0; j < VS / 16; ++j) {  // Y tile: rows 16 wave .. +15, slice values 16 j .. +15
         const int tq = lane & 15, q = lane >> 4;
         f32x4 y = {};
 #pragma unroll
         for (int g = 0; g < R / 16; ++g) {
           const int c0 = 16 * g + 4 * q;
-          mma16(y, ld_x(tm, LT, 16 * wave + tq, c0), ld_c(dd_s, LT, tq, c0));
+          mma16(y, ld_x(tm, LT, 16 * wave + tq, c0), ld_c(dd_s, LT, 16 * j + tq, c0));
         }
-        *reinterpret_cast<f32x4*>(y_s + tq * LT + 16 * wave + 4 * q) = y;
+        *reinterpret_cast<f32x4*>(y_s + (16 * j + tq) * LT + 16 * wave + 4 * q) = y;
         if (panel == 0) {
           float part[4];
-          const int v = v0 + tq;
+          const int v = v0 + 16 * j + tq;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * wave + 4 * q + r;
-            const int tok = token_at(p, n, t);
+            const int tok = tok_s[t];
             if (tok >= 0 && v < V)
               reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)tok * gr.dv.st + v] = bet_s[t] * y[r];
-            part[r] = vv_s[t * LDO + tq] * y[r];
+            part[r] = to_f32(vv_s[t * LDO + 16 * j + tq]) * y[r];
           }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -327,8 +436,7 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
 
     // ---- value-axis terms: scale rows, gate gradients, merge the Y term into dKn.
     {
-      const int k = kb + 32 * kt + li;
-      const bool kin = k < K;
+      const int kc = 32 * kt + li;  // panel column
       float rk_total = 0.f;
 #pragma unroll
       for (int m = 0; m < NTW; ++m) {
@@ -337,11 +445,11 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int t = 32 * rt + acc_row(r, hh);
-          const float eg = __expf(gam_s[t]), ek = __expf(gc - gam_s[t]);
-          const float kv = kin ? kn[(int64_t)t * K + k] : 0.f;
+          const float eg = eg_s[t], ek = ek_s[t];
+          const float kv = round_as<E>(xk_s[t * LX + kc]);
           if (has_q) {
             dq[m][r] *= eg;
-            pq[r] = (kin ? qn[(int64_t)t * K + k] : 0.f) * dq[m][r];
+            pq[r] = round_as<E>(xq_s[t * LX + kc]) * dq[m][r];
           } else {
             pq[r] = 0.f;
           }
@@ -354,7 +462,7 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
         const float sq = tile_row_sum(pq, lane), sk = tile_row_sum(pk, lane), sw = tile_row_sum(pw, lane);
         if ((lane & 1) == 0) {
           const int t = 32 * rt + acc_row(sum_index(lane), hh);
-          const float eg = __expf(gam_s[t]);
+          const float eg = eg_s[t];
           atomicAdd(&dgam_s[t], sq - sk + bet_s[t] * eg * sw);
           atomicAdd(&dbet_s[t], eg * sw);
           rk_total += sk;
@@ -367,23 +475,37 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     if (panel == 0) {
       // ---- P and KK on this wave's R x R tile: contraction over all keys.
       f32x16 pt = {}, kkt = {};
-      for (int k0 = 0; k0 < KM; k0 += KSL) {
-        __syncthreads();
-        for (int i = tid; i < R * KSL; i += NT) {
-          const int r = i / KSL, c = i % KSL, k = k0 + c;
-          qk_s[r * LKN + c] = (has_q && k < K) ? qn[(int64_t)r * K + k] : 0.f;
-          kk_s[r * LKN + c] = k < K ? kn[(int64_t)r * K + k] : 0.f;
+      if (NP == 1 && std::is_same<E, bf16_t>::value) {
+        // bf16 MFMA: the rounded rows are exact in bf16 (32x32x16, lane l holds
+        // row l%32, columns 16 g + 8 (l/32) .. +7).
+#pragma unroll 4
+        for (int g = 0; g < KM / 16; ++g) {
+          const int c0 = 16 * g + 8 * hh;
+          const bf16x8 bk = pack8(xk_s + (32 * ru + li) * LX + c0);
+          if (has_q) pt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack8(xq_s + (32 * rr + li) * LX + c0), bk, pt, 0, 0, 0);
+          kkt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack8(xk_s + (32 * rr + li) * LX + c0), bk, kkt, 0, 0, 0);
         }
-        __syncthreads();
-#pragma unroll
-        for (int g = 0; g < KSL / 8; ++g) {
+      } else if (NP == 1) {
+#pragma unroll 4
+        for (int g = 0; g < KM / 8; ++g) {
           const int c0 = 8 * g + 4 * hh;
-          const f32x4 bk = ld_c(kk_s, LKN, 32 * ru + li, c0);
-          if (has_q) mma8(pt, ld_c(qk_s, LKN, 32 * rr + li, c0), bk);
-          mma8(kkt, ld_c(kk_s, LKN, 32 * rr + li, c0), bk);
+          const f32x4 bk = ld_c(xk_s, LX, 32 * ru + li, c0);
+          if (has_q) mma8(pt, ld_c(xq_s, LX, 32 * rr + li, c0), bk);
+          mma8(kkt, ld_c(xk_s, LX, 32 * rr + li, c0), bk);
+        }
+      } else {  // both panels: the rounded rows straight from the forward's buffers
+#pragma unroll 4
+        for (int g = 0; g < KM / 8; ++g) {
+          const int c0 = 8 * g + 4 * hh;
+          const bool in = c0 < K;  // K % 4 == 0: a 4-column group is wholly in or out
+          const int cc = in ? c0 : 0;
+          f32x4 bk = ld_c(kn, K, 32 * ru + li, cc), ak = ld_c(kn, K, 32 * rr + li, cc);
+          f32x4 aq = has_q ? ld_c(qn, K, 32 * rr + li, cc) : f32x4{};
+          if (!in) bk = ak = aq = f32x4{};
+          if (has_q) mma8(pt, aq, bk);
+          mma8(kkt, ak, bk);
         }
       }
-      __syncthreads();
       // ---- dP: gate gradients and dQK; X to LDS.
       {
         const int u = 32 * ru + li;
@@ -444,74 +566,50 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
 
     // ---- position-axis terms: dQn += dQK Kn; dKn += dQK^T Qn + (dKK + dKK^T) Kn.
     {
-      const int k = kb + 32 * kt + li;
-      const bool kin = k < K;
-      f32x4 bk[R / 8], bq[R / 8];
-#pragma unroll
+      const int kc = 32 * kt + li;
+#pragma unroll 2
       for (int g = 0; g < R / 8; ++g) {
         const int c0 = 8 * g + 4 * hh;
+        const f32x4 bk = round4<E>(ld_x(xk_s, LX, kc, c0));
+        const f32x4 bq = round4<E>(ld_x(xq_s, LX, kc, c0));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bk[g][e] = kin ? kn[(int64_t)(c0 + e) * K + k] : 0.f;
-          bq[g][e] = (has_q && kin) ? qn[(int64_t)(c0 + e) * K + k] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < NTW; ++m) {
-        const int row = 32 * tile_rt(m) + li;
-#pragma unroll
-        for (int g = 0; g < R / 8; ++g) {
-          const int c0 = 8 * g + 4 * hh;
+        for (int m = 0; m < NTW; ++m) {
+          const int row = 32 * tile_rt(m) + li;
           if (has_q) {
-            mma8(dq[m], ld_c(dqk, LT, row, c0), bk[g]);
-            mma8(dka[m], ld_x(dqk, LT, row, c0), bq[g]);
+            mma8(dq[m], ld_c(dqk, LT, row, c0), bk);
+            mma8(dka[m], ld_x(dqk, LT, row, c0), bq);
           }
-          mma8(dka[m], ld_c(dkk, LT, row, c0) + ld_x(dkk, LT, row, c0), bk[g]);
+          mma8(dka[m], ld_c(dkk, LT, row, c0) + ld_x(dkk, LT, row, c0), bk);
         }
       }
     }
 
-    // ---- normalisation backward, part 1: row sums of x^2 and x . g.
+    // ---- normalisation backward, part 1: x/|x| . dX per row.
     {
-      const int k = kb + 32 * kt + li;
-      const bool kin = k < K;
+      const int kc = 32 * kt + li, k = kb + kc;
 #pragma unroll
       for (int m = 0; m < NTW; ++m) {
         const int rt = tile_rt(m);
-        float a[16], c[16], aq[16], cq[16];
+        float ck[16], cq[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int t = 32 * rt + acc_row(r, hh);
-          const int tok = tok_s[t];  // read from LDS inside the panel loop: keeps row offsets out of registers
-          const bool ok = tok >= 0 && kin;
-          const float xk = ok ? op_load<E>(p.k, b, h, tok, k) : 0.f;
-          a[r] = xk * xk;
-          c[r] = xk * dka[m][r];
-          const float xq = (ok && has_q) ? op_load<E>(p.q, b, h, tok, k) : 0.f;
-          aq[r] = xq * xq;
-          cq[r] = xq * dq[m][r];
+          ck[r] = xk_s[t * LX + kc] * dka[m][r];
+          cq[r] = xq_s[t * LX + kc] * dq[m][r];
         }
-        const float sa = tile_row_sum(a, lane), sc = tile_row_sum(c, lane);
-        float saq = 0.f, scq = 0.f;
-        if (has_q) {
-          saq = tile_row_sum(aq, lane);
-          scq = tile_row_sum(cq, lane);
-        }
+        const float sk = tile_row_sum(ck, lane);
+        const float sq = has_q ? tile_row_sum(cq, lane) : 0.f;
         if ((lane & 1) == 0) {
           const int t = 32 * rt + acc_row(sum_index(lane), hh);
-          atomicAdd(&kss_s[t], sa);
-          atomicAdd(&kxg_s[t], sc);
-          if (has_q) {
-            atomicAdd(&qss_s[t], saq);
-            atomicAdd(&qxg_s[t], scq);
-          }
+          atomicAdd(&kdot_s[t], sk);
+          if (has_q) atomicAdd(&qdot_s[t], sq);
         }
-        if (panel + 1 < NP) {
+        if (panel + 1 < NP && k < K) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int tok = tok_s[32 * rt + acc_row(r, hh)];
-            if (tok < 0 || !kin) continue;
-            if (has_q && gr.dq.ptr)
+            if (tok < 0) continue;
+            if (has_q)
               reinterpret_cast<float*>(gr.dq.ptr)[op_base(gr.dq, b, h) + (int64_t)tok * gr.dq.st + k] = dq[m][r];
             reinterpret_cast<float*>(gr.dk.ptr)[op_base(gr.dk, b, h) + (int64_t)tok * gr.dk.st + k] = dka[m][r];
           }
@@ -525,40 +623,59 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
   __syncthreads();
   if (tid == 0) dgam_s[R - 1] += __expf(gc) * red_s[0];
 
-  // ---- normalisation backward, part 2: write dq, dk (every panel).
+  // ---- normalisation backward, part 2: dX = (g - x^ (x^ . g)) / |x| for every
+  // panel; an earlier panel's g and x are re-read from global memory (all of a
+  // tile's loads are issued before its stores).
+  float* dqo = gr.dq.ptr && p.q.ptr ? reinterpret_cast<float*>(gr.dq.ptr) + op_base(gr.dq, b, h) : nullptr;
+  float* dko = reinterpret_cast<float*>(gr.dk.ptr) + op_base(gr.dk, b, h);
 #pragma unroll 1
   for (int panel = 0; panel < NP; ++panel) {
-    const int k = panel * KP + 32 * kt + li;
-    if (k >= K) continue;
+    const int kc = 32 * kt + li, k = panel * KP + kc;
+    const bool kin = k < K, parked = panel + 1 < NP;
 #pragma unroll
     for (int m = 0; m < NTW; ++m) {
       const int rt = tile_rt(m);
+      float xk[16], xq[16], gk[16], gq[16];
+      int tk[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = 32 * rt + acc_row(r, hh);
-        const int tok = token_at(p, n, t);
-        if (tok < 0) continue;
-        for (int which = 0; which < 2; ++which) {
-          const gpa_operand& src = which == 0 ? p.q : p.k;
-          const gpa_operand& dst = which == 0 ? gr.dq : gr.dk;
-          if (!src.ptr || !dst.ptr) continue;
-          float* out = reinterpret_cast<float*>(dst.ptr) + op_base(dst, b, h) + (int64_t)tok * dst.st;
-          if (which == 0 && !has_q) {
-            out[k] = 0.f;
-            continue;
+        const int tok = tok_s[t];
+        const bool ok = tok >= 0 && kin;
+        const int tt = ok ? tok : 0, kk = ok ? k : 0;
+        tk[r] = ok ? tok : -1;
+        if (parked) {
+          xk[r] = op_load<E>(p.k, b, h, tt, kk) / fmaxf(knrm_s[t], 1e-6f);  // the forward's x/|x|
+          gk[r] = dko[(int64_t)tt * gr.dk.st + kk];
+          if (has_q) {
+            xq[r] = op_load<E>(p.q, b, h, tt, kk) / fmaxf(qnrm_s[t], 1e-6f);
+            gq[r] = dqo[(int64_t)tt * gr.dq.st + kk];
           }
-          const float g = panel + 1 < NP ? out[k] : (which == 0 ? dq[m][r] : dka[m][r]);
-          const float ss = which == 0 ? qss_s[t] : kss_s[t], xg = which == 0 ? qxg_s[t] : kxg_s[t];
-          const float nrm = sqrtf(ss), den = fmaxf(nrm, 1e-6f);
-          const float xh = op_load<E>(src, b, h, tok, k) / den;
-          out[k] = nrm > 1e-6f ? (g - xh * (xg / den)) / den : g / 1e-6f;
+        } else {
+          xk[r] = xk_s[t * LX + kc];
+          gk[r] = dka[m][r];
+          xq[r] = xq_s[t * LX + kc];
+          gq[r] = dq[m][r];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * rt + acc_row(r, hh);
+        if (tk[r] < 0) continue;
+        {
+          dko[(int64_t)tk[r] * gr.dk.st + k] = (knrm_s[t] > 1e-6f ? gk[r] - xk[r] * kdot_s[t] : gk[r]) * krd_s[t];
+        }
+        if (has_q) {
+          dqo[(int64_t)tk[r] * gr.dq.st + k] = (qnrm_s[t] > 1e-6f ? gq[r] - xq[r] * qdot_s[t] : gq[r]) * qrd_s[t];
+        } else if (dqo) {
+          dqo[(int64_t)tk[r] * gr.dq.st + k] = 0.f;
         }
       }
     }
   }
   __syncthreads();
   if (tid < R) {
-    const int tok = token_at(p, n, tid);
+    const int tok = tok_s[tid];
     if (tok >= 0) {
       float acc = 0.f;
       for (int u = tid; u < R; ++u) acc += dgam_s[u];
@@ -569,9 +686,14 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
 }
 
 template <typename E, int KM>
+size_t chunk_bwd_mfma_lds() {
+  return ChunkBwdLayout<E, KM>::BYTES;
+}
+
+template <typename E, int KM>
 int launch_chunk_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
                           hipStream_t st) {
-  const size_t lds = sizeof(float) * ChunkBwdLayout<KM>::TOTAL;
+  const size_t lds = ChunkBwdLayout<E, KM>::BYTES;
   if (lds > 65536) {
     const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_chunk_bwd_mfma<E, KM>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -581,17 +703,15 @@ int launch_chunk_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
   return GPA_HIP_OK;
 }
 
-template int launch_chunk_bwd_mfma<float, 64>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                              int, hipStream_t);
-template int launch_chunk_bwd_mfma<float, 128>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                               int, hipStream_t);
-template int launch_chunk_bwd_mfma<float, 256>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                               int, hipStream_t);
-template int launch_chunk_bwd_mfma<bf16_t, 64>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                               int, hipStream_t);
-template int launch_chunk_bwd_mfma<bf16_t, 128>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                                int, hipStream_t);
-template int launch_chunk_bwd_mfma<bf16_t, 256>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&,
-                                                int, hipStream_t);
+#define GPA_CHUNK_BWD_MFMA(E, KM)                                                                              \
+  template size_t chunk_bwd_mfma_lds<E, KM>();                                                                  \
+  template int launch_chunk_bwd_mfma<E, KM>(const gpa_gdn_problem&, const gpa_gdn_saved&, const gpa_gdn_grads&, \
+                                            int, hipStream_t);
+GPA_CHUNK_BWD_MFMA(float, 64)
+GPA_CHUNK_BWD_MFMA(float, 128)
+GPA_CHUNK_BWD_MFMA(bf16_t, 64)
+GPA_CHUNK_BWD_MFMA(bf16_t, 128)
+GPA_CHUNK_BWD_MFMA(bf16_t, 256)
+#undef GPA_CHUNK_BWD_MFMA
 
 }  // namespace gpa

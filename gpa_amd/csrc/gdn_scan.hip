@@ -1171,8 +1171,11 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
     hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
   }
   mark(tm, st);
-  if (p.kdim % 4 == 0) {
-    if (int rc = launch_chunk_bwd_mfma<E, KM>(p, sv, gr, nch, st)) return rc;
+  // The MFMA chunk kernel keeps 64 x 256 fp32 rows in LDS only for bf16.
+  constexpr bool mfma_chunk = !(std::is_same<E, float>::value && KM == 256);
+  if (mfma_chunk && p.kdim % 4 == 0) {
+    if constexpr (mfma_chunk)
+      if (int rc = launch_chunk_bwd_mfma<E, KM>(p, sv, gr, nch, st)) return rc;
   } else {
     constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
     constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;

@@ -135,6 +135,7 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     chunk = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c
     if read:
         chunk += 2 * k * v + 2 * c * v + 6 * c * k
-    name = "gdn_chunk_bwd_mfma" if k % 4 == 0 else "gdn_chunk_bwd"
+    mfma_chunk = k % 4 == 0 and not (km == 256 and e == "f32")
+    name = "gdn_chunk_bwd_mfma" if mfma_chunk else "gdn_chunk_bwd"
     kernels.append((f"{name}<{e},{km}>", chunk * tokens))
     return _active.timing(kernels)
