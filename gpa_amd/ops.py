@@ -35,12 +35,22 @@ def _ptr(t):
     return t.data_ptr() if t is not None else None
 
 
+def _in_use_here(*tensors):
+    """Mark tensors made on another stream as read by the current one, so the
+    caching allocator keeps their memory until this stream's work is done."""
+    stream = torch.cuda.current_stream()
+    for t in tensors:
+        if t is not None:
+            t.record_stream(stream)
+
+
 class _GDNScan(torch.autograd.Function):
     """One group of GDN scans; saved intermediates per include/gpa_hip.h."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int):
         lib = _lib.load()
+        _in_use_here(q, k, v, g, beta, s0)
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
         dev = k.device
@@ -84,6 +94,7 @@ class _GDNScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, dstates, dfinal):
         lib = _lib.load()
+        _in_use_here(dout, dstates, dfinal)
         chunk, offset, nch, has_q, has_s0, mfma = ctx.geom
         (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags) = ctx.saved_tensors
         bsz, tokens, heads, kd = k.shape

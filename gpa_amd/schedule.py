@@ -32,6 +32,52 @@ from .ops import gdn_scan_hip
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 
 _F32 = torch.float32
+_LANES = 4          # side streams for independent scans (the device has 4 hardware queues per process)
+_STREAMS: dict = {}
+
+
+def _side_streams(device) -> list:
+    """The device's side streams (default priority), created once."""
+    pool = _STREAMS.get(device)
+    if pool is None:
+        pool = _STREAMS[device] = [torch.cuda.Stream(device=device) for _ in range(_LANES)]
+    return pool
+
+
+def _tensors(x):
+    if isinstance(x, Tensor):
+        yield x
+    elif isinstance(x, (tuple, list)):
+        for y in x:
+            yield from _tensors(y)
+    elif hasattr(x, "tensors"):
+        yield from x.tensors()
+
+
+def _concurrent(jobs):
+    """Run independent jobs (fn, input tensors) on the side streams, job i on
+    stream i % 4, and return their results in order.  Every side stream first
+    waits for the current stream; the current stream then waits for all of
+    them.  Inputs are recorded as used on their side stream and results as
+    used on the current stream, so the caching allocator does not hand their
+    memory to another stream early.  Autograd runs each job's backward on the
+    job's stream, so the backward scans overlap the same way."""
+    main = torch.cuda.current_stream()
+    streams = _side_streams(main.device)[:len(jobs)]
+    for stream in streams:
+        stream.wait_stream(main)
+    results = []
+    for i, (fn, inputs) in enumerate(jobs):
+        stream = streams[i % len(streams)]
+        for t in _tensors(inputs):
+            t.record_stream(stream)
+        with torch.cuda.stream(stream):
+            results.append(fn())
+    for stream in streams:
+        main.wait_stream(stream)
+    for t in _tensors(results):
+        t.record_stream(main)
+    return results
 
 
 def _unit(x: Tensor) -> Tensor:
@@ -97,8 +143,11 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         lv = _Level()
         slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
         g_in, b_in, g_out, b_out = _gates(model, key, j, control)
-        raw, a_starts, a_final = gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan)
-        _, b_starts, b_final = gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **scan)
+        (raw, a_starts, a_final), (_, b_starts, b_final) = _concurrent([
+            (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan),
+             (q, key, slot, g_in, b_in, old.inner)),
+            (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **scan),
+             (slot, value, g_out, b_out, old.outer))])
         a_hat = _snapshots(a_starts, snap.inner)       # [B,H,N,Dk,M]
         b_hat = _snapshots(b_starts, snap.outer)       # [B,H,N,M,Dv]
         write = _assignment(cfg, slot)
@@ -126,9 +175,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
 
     # ---- outer reads and level mix, attention.py:333-341
     weights = model.output_logits.softmax(0)
+
+    def outer_read(lv, qo, s0):
+        return lambda: gdn_scan_hip(qo, lv.slot, lv.value, lv.g_out, lv.b_out, s0, **scan)[0]
+
+    reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
+                          (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
+                         for j, (lv, qo) in enumerate(zip(levels, queries))])
     out = 0
-    for j, (lv, qo) in enumerate(zip(levels, queries)):
-        read, _, _ = gdn_scan_hip(qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer, **scan)
+    for j, read in enumerate(reads):
         out = out + weights[j][..., None] * read
     out = out.to(v.dtype)
 
@@ -210,20 +265,27 @@ def _residual(model, key, value, rk, rv, j):
 def _relations(model, local, writes, rel_states, scan):
     """Every ordered edge's R_ij scan (attention.py:206-223)."""
     cfg = model.config
+
+    def edge(e, i, j, old):
+        def run():
+            lead = writes[i].shape[:-1]
+            g = (-F.softplus(model.relation_decay_raw[e])).expand(lead)
+            if cfg.positional_mode == "none":
+                g = g * 0
+            beta = model.relation_beta_raw[e].sigmoid().expand(lead)
+            target = writes[j]
+            if cfg.rsa_update:
+                norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
+                target = (target / norm[..., None]).to(target.dtype)
+                beta = (beta * norm.square()).clamp_max(.9)
+            msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
+            return msg, memory
+        return run, (local[i], writes[i], writes[j], old.memory)
+
+    done = _concurrent([edge(e, i, j, old) for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))])
     incoming = [[] for _ in local]
     finals = []
-    for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
-        lead = writes[i].shape[:-1]
-        g = (-F.softplus(model.relation_decay_raw[e])).expand(lead)
-        if cfg.positional_mode == "none":
-            g = g * 0
-        beta = model.relation_beta_raw[e].sigmoid().expand(lead)
-        target = writes[j]
-        if cfg.rsa_update:
-            norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
-            target = (target / norm[..., None]).to(target.dtype)
-            beta = (beta * norm.square()).clamp_max(.9)
-        msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
+    for e, ((i, j), (msg, memory)) in enumerate(zip(model.edges, done)):
         incoming[j].append((e, msg))
         finals.append(RelationState(i, j, memory))
     return incoming, tuple(finals)
