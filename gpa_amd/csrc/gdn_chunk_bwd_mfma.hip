@@ -130,44 +130,53 @@ __device__ __forceinline__ f32x4 round4(f32x4 x) {
 
 }  // namespace
 
-// LDS plan (floats).  One key panel (KM <= 128): the R x R matrices reuse the
-// staging area once the value loop is done; two panels keep dQK and dKK apart.
+// LDS plan (floats).  The R x R matrices reuse the staging area once the value
+// loop is done.  Up to 128 keys, x/|x| is kept unrounded (fp32); with 256 keys
+// (bf16 only) it is kept rounded, as bf16, and the normalisation backward
+// re-reads the raw rows.
 template <typename E, int KM>
 struct ChunkBwdLayout {
-  static constexpr int KP = KM < 128 ? KM : 128;  // key panel
-  static constexpr int NP = KM / KP;
+  static constexpr bool XR = KM > 128;
   static constexpr int VS = 16;                   // value slice
-  static constexpr int LDO = VS + 4, LT = R + 4, LS = KP + 4, LX = KP + 4;
+  static constexpr int LDO = VS + 4, LT = R + 4, LS = KM + 4;
+  static constexpr int LX = XR ? KM + 8 : KM + 4;  // row stride of x/|x| (bf16 elements when XR)
+  static constexpr int XF = XR ? R * LX / 2 : R * LX;
   static constexpr int EQ = R * LDO * (int)sizeof(E) / 4;  // floats of one [R][LDO] activation tile
   // value-loop staging
   static constexpr int DO = 0, VV = DO + EQ, D = VV + EQ, DD = D + VS * LT, Y = DD + VS * LT, S = Y + VS * LT,
                        DS = S + VS * LS, V_END = DS + VS * LS;
-  static constexpr int RR1 = 2 * R * LT;  // xm + dQK inside the staging area (one panel)
-  static constexpr int STAGE = (NP == 1 && RR1 > V_END) ? RR1 : V_END;
-  static constexpr int OWN = NP == 1 ? 0 : 2 * R * LT;  // separate dQK, dKK
-  static constexpr int T_OFF = 0, XK_OFF = R * LT + OWN, XQ_OFF = XK_OFF + R * LX, STAGE_OFF = XQ_OFF + R * LX;
-  static constexpr int XM_OFF = STAGE_OFF;
-  static constexpr int DQK_OFF = NP == 1 ? STAGE_OFF + R * LT : R * LT;
-  static constexpr int DKK_OFF = NP == 1 ? STAGE_OFF : 2 * R * LT;
+  static constexpr int RR1 = 2 * R * LT;  // xm (dKK) + dQK
+  static constexpr int STAGE = RR1 > V_END ? RR1 : V_END;
+  static constexpr int T_OFF = 0, XK_OFF = R * LT, XQ_OFF = XK_OFF + XF, STAGE_OFF = XQ_OFF + XF;
+  static constexpr int XM_OFF = STAGE_OFF, DQK_OFF = STAGE_OFF + R * LT, DKK_OFF = STAGE_OFF;
   static constexpr int SC_OFF = STAGE_OFF + STAGE;
   static constexpr int TOTAL = SC_OFF + 13 * R + 4;
   static constexpr size_t BYTES = sizeof(float) * TOTAL;
 };
 
+constexpr int CB_WAVES = 8, CB_NT = 64 * CB_WAVES;  // threads of a chunk-backward block
+
 template <typename E, int KM>
-__global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv,
-                                                           gpa_gdn_grads gr, int nch) {
+__global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv,
+                                                              gpa_gdn_grads gr, int nch) {
   using L = ChunkBwdLayout<E, KM>;
-  constexpr int KP = L::KP, NP = L::NP, VS = L::VS, LDO = L::LDO, LT = L::LT, LS = L::LS, LX = L::LX;
-  constexpr int NTW = KP / 64;          // R x KP output tiles per wave
-  constexpr int SQ = VS * KP / 4 / NT;  // float4 of S (and of dS) per thread per slice
-  constexpr int DQ = VS * R / 4 / NT;   // float4 of D (and of dD) per thread per slice
-  constexpr int OQ = R * VS / NT;       // elements of dO (and of V) per thread per slice
-  static_assert(SQ >= 1 && DQ >= 1 && VS % 16 == 0, "staging shape");
+  constexpr bool XR = L::XR;
+  static_assert(!XR || std::is_same<E, bf16_t>::value, "rounded x/|x| needs bf16 activations");
+  constexpr int VS = L::VS, LDO = L::LDO, LT = L::LT, LS = L::LS, LX = L::LX;
+  constexpr int NW = CB_WAVES, NTH = CB_NT, KT = KM / 32;
+  constexpr int NTW = KT >= 4 ? KT / 4 : 1;  // R x K output tiles per owning wave
+  // Per-slice staging counts (float4 of S/dS, of D/dD; elements of dO/V) and
+  // their per-thread shares; entries past a count are loaded from index 0
+  // (always valid) and not stored.
+  constexpr int SC = VS * KM / 4, DC = VS * R / 4, OC = R * VS;
+  constexpr int SQ = (SC + NTH - 1) / NTH, DQ = (DC + NTH - 1) / NTH, OQ = (OC + NTH - 1) / NTH;
+  static_assert(VS % 16 == 0, "value slice");
   extern __shared__ __align__(16) float smem[];
   float* tm = smem + L::T_OFF;
-  float* xk_s = smem + L::XK_OFF;
+  float* xk_s = smem + L::XK_OFF;  // x/|x| (fp32), or its bf16 rounding when XR
   float* xq_s = smem + L::XQ_OFF;
+  bf16_t* xkb = reinterpret_cast<bf16_t*>(xk_s);
+  bf16_t* xqb = reinterpret_cast<bf16_t*>(xq_s);
   float* stage = smem + L::STAGE_OFF;
   E* do_s = reinterpret_cast<E*>(stage + L::DO);
   E* vv_s = reinterpret_cast<E*>(stage + L::VV);
@@ -198,13 +207,14 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
   const int K = p.kdim, V = p.vdim, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hh = lane >> 5;
   const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr;
-  const float* kn = sv.kn + rows_off(s, n, nch, 0, K);
-  const float* qn = has_q ? sv.qn + rows_off(s, n, nch, 0, K) : nullptr;
   const float* st = sv.states + state_off(s, n, nch, K, V);
   const float* dh = gr.dhend + state_off(s, n, nch, K, V);
   const float* dl = sv.delta + vc_off(s, n, nch, V);
   const float* ddl = gr.ddelta + vc_off(s, n, nch, V);
   const float* tri = sv.tri + rows_off(s, n, nch, 0, R);
+  // x/|x| rounded to the activation type (the matrix operand Kn, Qn) ...
+  auto kr = [&](int t, int k) { return XR ? to_f32(xkb[t * LX + k]) : round_as<E>(xk_s[t * LX + k]); };
+  auto qr = [&](int t, int k) { return XR ? to_f32(xqb[t * LX + k]) : round_as<E>(xq_s[t * LX + k]); };
 
   if (tid < R) {
     gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
@@ -214,21 +224,21 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     tok_s[tid] = token_at(p, n, tid);
   }
   if (tid < 4) red_s[tid] = 0.f;
-  for (int i = tid; i < R * R / 4; i += NT) {
+  for (int i = tid; i < R * R / 4; i += NTH) {
     const int t = i / (R / 4), c = 4 * (i % (R / 4));
     *reinterpret_cast<f32x4*>(tm + t * LT + c) = *reinterpret_cast<const f32x4*>(tri + t * R + c);
   }
-  // Row norms of the raw keys and queries, summed in the forward's order; with
-  // one panel also x/|x| for every key column.  Every load of the wave is
-  // issued (at a clamped address, from a stand-in operand when there is no
-  // query) before the first use.
+  // Row norms of the raw keys and queries, summed in the forward's order, and
+  // x/|x| for every key column.  Every load of the wave is issued (at a clamped
+  // address, from a stand-in operand when there is no query) before the first
+  // use.
+  const gpa_operand& qsrc = has_q ? p.q : p.k;
   {
-    constexpr int NI = KM / 64, NR = R / 4;
-    const gpa_operand& qsrc = has_q ? p.q : p.k;
+    constexpr int NI = KM / 64, NR = R / NW;
     float xk[NR][NI], xq[NR][NI];
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
-      const int tok = token_at(p, n, wave + 4 * j), tt = tok >= 0 ? tok : 0;
+      const int tok = token_at(p, n, wave + NW * j), tt = tok >= 0 ? tok : 0;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int d = lane + 64 * i, dd = d < K ? d : 0;
@@ -238,7 +248,7 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     }
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
-      const int r = wave + 4 * j, tok = token_at(p, n, r);
+      const int r = wave + NW * j, tok = token_at(p, n, r);
       float sk = 0.f, sq = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -255,12 +265,16 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
         krd_s[r] = 1.f / fmaxf(nk, 1e-6f);
         qrd_s[r] = 1.f / fmaxf(nq, 1e-6f);
       }
-      if (NP == 1) {
-        const float dk = fmaxf(nk, 1e-6f), dq = fmaxf(nq, 1e-6f);
+      const float dk = fmaxf(nk, 1e-6f), dq = fmaxf(nq, 1e-6f);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          xk_s[r * LX + lane + 64 * i] = xk[j][i] / dk;
-          xq_s[r * LX + lane + 64 * i] = xq[j][i] / dq;
+      for (int i = 0; i < NI; ++i) {
+        const int c = r * LX + lane + 64 * i;
+        if (XR) {
+          xkb[c] = from_f32<bf16_t>(xk[j][i] / dk);
+          xqb[c] = from_f32<bf16_t>(xq[j][i] / dq);
+        } else {
+          xk_s[c] = xk[j][i] / dk;
+          xq_s[c] = xq[j][i] / dq;
         }
       }
     }
@@ -272,70 +286,55 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     ek_s[tid] = __expf(gc - gam_s[tid]);
   }
 
-  // Output tiles: R x KP tiles m < NTW at rows 32 rt(m), panel columns 32 kt;
-  // the R x R tile at (32 rr, 32 ru).
-  const int kt = NTW == 2 ? wave : (wave & 1);
-  const int rr = wave >> 1, ru = wave & 1;
-  auto tile_rt = [&](int m) { return NTW == 2 ? m : (wave >> 1); };
+  // Tiles.  Waves below 2 KT own NTW R x K output tiles of dQn, dKn and the
+  // Y S^T term, tile m at rows 32 rt(m), columns 32 kt; the R x R tile
+  // (32 rr, 32 ru) is shared by wave w (dP, P: waves 0-3) and wave w + 4
+  // (X, KK, dA: waves 4-7).
+  const bool own = wave < 2 * KT;
+  const int kt = own ? (NTW == 2 ? wave : wave % KT) : 0;
+  auto tile_rt = [&](int m) { return NTW == 2 ? m : (own ? wave / KT : 0); };
+  const int rr = (wave & 3) >> 1, ru = wave & 1;
+  const bool grp_p = wave < 4;
 
-  f32x16 dp = {}, xt = {};
-  // dQn, dKn of the current panel (the last one after the loop); earlier
-  // panels are parked unnormalised in dq/dk and re-read by the same lanes.
+  f32x16 dp = {};  // dP on waves 0-3, X on waves 4-7
   f32x16 dq[NTW], dka[NTW], dkw[NTW];
+#pragma unroll
+  for (int m = 0; m < NTW; ++m) dq[m] = dka[m] = dkw[m] = f32x16{};
   float ddot = 0.f;  // this thread's share of <S_n, dS>
   const int nsl = (V + VS - 1) / VS;
 
-#pragma unroll 1
-  for (int panel = 0; panel < NP; ++panel) {
-    const int kb = panel * KP;
-    if (NP > 1) {
-      if (panel > 0) __syncthreads();  // the previous panel's x/|x| is no longer read
-#pragma unroll
-      for (int j = 0; j < R / 4; ++j) {
-        const int r = wave + 4 * j, tok = tok_s[r], tt = tok >= 0 ? tok : 0;
-        const float dk = fmaxf(knrm_s[r], 1e-6f), dq = fmaxf(qnrm_s[r], 1e-6f);
-#pragma unroll
-        for (int i = 0; i < KP / 64; ++i) {
-          const int d = kb + lane + 64 * i;
-          const bool ok = tok >= 0 && d < K;
-          const float xk = op_load<E>(p.k, b, h, tt, ok ? d : 0);
-          const float xq = op_load<E>(has_q ? p.q : p.k, b, h, tt, ok ? d : 0);
-          xk_s[r * LX + lane + 64 * i] = ok ? xk / dk : 0.f;
-          xq_s[r * LX + lane + 64 * i] = (ok && has_q) ? xq / dq : 0.f;
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < NTW; ++m) dq[m] = dka[m] = dkw[m] = f32x16{};
-
-    // ---- value loop: register prefetch of slice sl+1 while slice sl is in LDS.
+  // ---- value loop: register prefetch of slice sl+1 while slice sl is in LDS.
+  // fetch() only issues loads (at a clamped, always valid address); the masks
+  // of void or out-of-range entries are applied in stash(), after the MFMA
+  // work of the current slice, so the loads stay in flight meanwhile.
+  {
+    const gpa_operand& dosrc = has_q ? gr.dout : p.v;  // stand-in of the same shape when there is no read
     f32x4 rs[SQ], rds[SQ], rd[DQ], rdd[DQ];
     E rdo[OQ], rv[OQ];
-    // fetch() only issues loads (at a clamped, always valid address); the
-    // masks of void or out-of-range entries are applied in stash(), after the
-    // MFMA work of the current slice, so the loads stay in flight meanwhile.
-    const gpa_operand& dosrc = has_q ? gr.dout : p.v;  // stand-in of the same shape when there is no read
     int vnext = 0;
     auto fetch = [&](int v0) {
       vnext = v0;
 #pragma unroll
       for (int i = 0; i < SQ; ++i) {
-        const int idx = tid + NT * i, vr = idx / (KP / 4), c = 4 * (idx % (KP / 4));
-        const int v = v0 + vr, k = kb + c;
-        const int64_t o = (v < V && k < K) ? (int64_t)v * K + k : 0;
+        const int idx0 = tid + NTH * i, idx = idx0 < SC ? idx0 : 0;
+        const int vr = idx / (KM / 4), c = 4 * (idx % (KM / 4));
+        const int v = v0 + vr;
+        const int64_t o = (v < V && c < K) ? (int64_t)v * K + c : 0;
         rs[i] = *reinterpret_cast<const f32x4*>(st + o);
         rds[i] = *reinterpret_cast<const f32x4*>(dh + o);
       }
 #pragma unroll
       for (int i = 0; i < DQ; ++i) {
-        const int idx = tid + NT * i, vr = idx / (R / 4), c = 4 * (idx % (R / 4)), v = v0 + vr;
+        const int idx0 = tid + NTH * i, idx = idx0 < DC ? idx0 : 0;
+        const int vr = idx / (R / 4), c = 4 * (idx % (R / 4)), v = v0 + vr;
         const int64_t o = v < V ? (int64_t)v * R + c : 0;
         rd[i] = *reinterpret_cast<const f32x4*>(dl + o);
         rdd[i] = *reinterpret_cast<const f32x4*>(ddl + o);
       }
 #pragma unroll
       for (int i = 0; i < OQ; ++i) {
-        const int idx = tid + NT * i, t = idx / VS, v = v0 + idx % VS;
+        const int idx0 = tid + NTH * i, idx = idx0 < OC ? idx0 : 0;
+        const int t = idx / VS, v = v0 + idx % VS;
         const int tok = tok_s[t];
         const bool ok = tok >= 0 && v < V;
         const int tt = ok ? tok : 0, vv = ok ? v : 0;
@@ -347,8 +346,10 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
       const int v0 = vnext;
 #pragma unroll
       for (int i = 0; i < SQ; ++i) {
-        const int idx = tid + NT * i, vr = idx / (KP / 4), c = 4 * (idx % (KP / 4));
-        const bool ok = v0 + vr < V && kb + c < K;
+        const int idx = tid + NTH * i;
+        if (SC % NTH != 0 && idx >= SC) continue;
+        const int vr = idx / (KM / 4), c = 4 * (idx % (KM / 4));
+        const bool ok = v0 + vr < V && c < K;
         const f32x4 a = ok ? rs[i] : f32x4{}, d = ok ? rds[i] : f32x4{};
         *reinterpret_cast<f32x4*>(s_s + vr * LS + c) = a;
         *reinterpret_cast<f32x4*>(ds_s + vr * LS + c) = d;
@@ -356,17 +357,21 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
       }
 #pragma unroll
       for (int i = 0; i < DQ; ++i) {
-        const int idx = tid + NT * i, vr = idx / (R / 4), c = 4 * (idx % (R / 4));
+        const int idx = tid + NTH * i;
+        if (DC % NTH != 0 && idx >= DC) continue;
+        const int vr = idx / (R / 4), c = 4 * (idx % (R / 4));
         const bool ok = v0 + vr < V;
         *reinterpret_cast<f32x4*>(d_s + vr * LT + c) = ok ? rd[i] : f32x4{};
         *reinterpret_cast<f32x4*>(dd_s + vr * LT + c) = ok ? rdd[i] : f32x4{};
       }
 #pragma unroll
       for (int i = 0; i < OQ; ++i) {
-        const int idx = tid + NT * i, t = idx / VS, c = idx % VS;
+        const int idx = tid + NTH * i;
+        if (OC % NTH != 0 && idx >= OC) continue;
+        const int t = idx / VS, c = idx % VS;
         const bool ok = tok_s[t] >= 0 && v0 + c < V;
         do_s[t * LDO + c] = (ok && has_q) ? rdo[i] : from_f32<E>(0.f);
-        vv_s[t * LDO + c] = (ok && panel == 0) ? rv[i] : from_f32<E>(0.f);
+        vv_s[t * LDO + c] = ok ? rv[i] : from_f32<E>(0.f);
       }
     };
 
@@ -376,55 +381,55 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
     for (int sl = 0; sl < nsl; ++sl) {
       const int v0 = sl * VS;
       if (sl + 1 < nsl) fetch(v0 + VS);
-#pragma unroll
-      for (int j = 0; j < VS / 16; ++j) {  // Y tile: rows 16 wave .. +15, slice values 16 j .. +15
-        const int tq = lane & 15, q = lane >> 4;
+      // Y tile (16x16x4): rows 16 (w % 4) .. +15, slice values 16 (w / 4) .. +15.
+      if (wave < 4 * (VS / 16)) {
+        const int tq = lane & 15, q = lane >> 4, t0 = 16 * (wave & 3), j = wave >> 2;
         f32x4 y = {};
 #pragma unroll
         for (int g = 0; g < R / 16; ++g) {
           const int c0 = 16 * g + 4 * q;
-          mma16(y, ld_x(tm, LT, 16 * wave + tq, c0), ld_c(dd_s, LT, 16 * j + tq, c0));
+          mma16(y, ld_x(tm, LT, t0 + tq, c0), ld_c(dd_s, LT, 16 * j + tq, c0));
         }
-        *reinterpret_cast<f32x4*>(y_s + (16 * j + tq) * LT + 16 * wave + 4 * q) = y;
-        if (panel == 0) {
-          float part[4];
-          const int v = v0 + 16 * j + tq;
+        *reinterpret_cast<f32x4*>(y_s + (16 * j + tq) * LT + t0 + 4 * q) = y;
+        float part[4];
+        const int v = v0 + 16 * j + tq;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = 16 * wave + 4 * q + r;
-            const int tok = tok_s[t];
-            if (tok >= 0 && v < V)
-              reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)tok * gr.dv.st + v] = bet_s[t] * y[r];
-            part[r] = to_f32(vv_s[t * LDO + 16 * j + tq]) * y[r];
-          }
+        for (int r = 0; r < 4; ++r) {
+          const int t = t0 + 4 * q + r;
+          const int tok = tok_s[t];
+          if (tok >= 0 && v < V)
+            reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)tok * gr.dv.st + v] = bet_s[t] * y[r];
+          part[r] = to_f32(vv_s[t * LDO + 16 * j + tq]) * y[r];
+        }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = part[r];
-            x += __shfl_xor(x, 8);
-            x += __shfl_xor(x, 4);
-            x += __shfl_xor(x, 2);
-            x += __shfl_xor(x, 1);
-            if (tq == 0) atomicAdd(&dbet_s[16 * wave + 4 * q + r], x);
-          }
+        for (int r = 0; r < 4; ++r) {
+          float x = part[r];
+          x += __shfl_xor(x, 8);
+          x += __shfl_xor(x, 4);
+          x += __shfl_xor(x, 2);
+          x += __shfl_xor(x, 1);
+          if (tq == 0) atomicAdd(&dbet_s[t0 + 4 * q + r], x);
         }
       }
       __syncthreads();
 #pragma unroll
       for (int g = 0; g < VS / 8; ++g) {
         const int c0 = 8 * g + 4 * hh;
-        const f32x4 bs = ld_x(s_s, LS, 32 * kt + li, c0);
-        const f32x4 bds = ld_x(ds_s, LS, 32 * kt + li, c0);
+        if (own) {
+          const f32x4 bs = ld_x(s_s, LS, 32 * kt + li, c0), bds = ld_x(ds_s, LS, 32 * kt + li, c0);
 #pragma unroll
-        for (int m = 0; m < NTW; ++m) {
-          const int row = 32 * tile_rt(m) + li;
-          if (has_q) mma8(dq[m], ld_c(do_s, LDO, row, c0), bs);
-          mma8(dka[m], ld_x(d_s, LT, row, c0), bds);
-          mma8(dkw[m], ld_x(y_s, LT, row, c0), bs);
+          for (int m = 0; m < NTW; ++m) {
+            const int row = 32 * tile_rt(m) + li;
+            if (has_q) mma8(dq[m], ld_c(do_s, LDO, row, c0), bs);
+            mma8(dka[m], ld_x(d_s, LT, row, c0), bds);
+            mma8(dkw[m], ld_x(y_s, LT, row, c0), bs);
+          }
         }
-        if (panel == 0) {
-          const f32x4 bu = ld_x(d_s, LT, 32 * ru + li, c0);
+        const f32x4 bu = ld_x(d_s, LT, 32 * ru + li, c0);
+        if (grp_p) {
           if (has_q) mma8(dp, ld_c(do_s, LDO, 32 * rr + li, c0), bu);
-          mma8(xt, ld_x(dd_s, LT, 32 * rr + li, c0), bu);
+        } else {
+          mma8(dp, ld_x(dd_s, LT, 32 * rr + li, c0), bu);
         }
       }
       __syncthreads();
@@ -433,187 +438,201 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
         __syncthreads();
       }
     }
+  }
 
-    // ---- value-axis terms: scale rows, gate gradients, merge the Y term into dKn.
-    {
-      const int kc = 32 * kt + li;  // panel column
-      float rk_total = 0.f;
+  // ---- value-axis terms: scale rows, gate gradients, merge the Y term into dKn.
+  if (own) {
+    const int k = 32 * kt + li;
+    float rk_total = 0.f;
 #pragma unroll
-      for (int m = 0; m < NTW; ++m) {
-        const int rt = tile_rt(m);
-        float pq[16], pk[16], pw[16];
+    for (int m = 0; m < NTW; ++m) {
+      const int rt = tile_rt(m);
+      float pq[16], pk[16], pw[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * rt + acc_row(r, hh);
-          const float eg = eg_s[t], ek = ek_s[t];
-          const float kv = round_as<E>(xk_s[t * LX + kc]);
-          if (has_q) {
-            dq[m][r] *= eg;
-            pq[r] = round_as<E>(xq_s[t * LX + kc]) * dq[m][r];
-          } else {
-            pq[r] = 0.f;
-          }
-          dka[m][r] *= ek;
-          pk[r] = kv * dka[m][r];
-          const float w = -dkw[m][r];
-          pw[r] = kv * w;
-          dka[m][r] += bet_s[t] * eg * w;
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * rt + acc_row(r, hh);
+        const float eg = eg_s[t], ek = ek_s[t];
+        const float kv = kr(t, k);
+        if (has_q) {
+          dq[m][r] *= eg;
+          pq[r] = qr(t, k) * dq[m][r];
+        } else {
+          pq[r] = 0.f;
         }
-        const float sq = tile_row_sum(pq, lane), sk = tile_row_sum(pk, lane), sw = tile_row_sum(pw, lane);
-        if ((lane & 1) == 0) {
-          const int t = 32 * rt + acc_row(sum_index(lane), hh);
-          const float eg = eg_s[t];
-          atomicAdd(&dgam_s[t], sq - sk + bet_s[t] * eg * sw);
-          atomicAdd(&dbet_s[t], eg * sw);
-          rk_total += sk;
-        }
+        dka[m][r] *= ek;
+        pk[r] = kv * dka[m][r];
+        const float w = -dkw[m][r];
+        pw[r] = kv * w;
+        dka[m][r] += bet_s[t] * eg * w;
       }
-      rk_total = sum64(rk_total);
-      if (lane == 0) atomicAdd(&dgam_s[R - 1], rk_total);
+      const float sq = tile_row_sum(pq, lane), sk = tile_row_sum(pk, lane), sw = tile_row_sum(pw, lane);
+      if ((lane & 1) == 0) {
+        const int t = 32 * rt + acc_row(sum_index(lane), hh);
+        const float eg = eg_s[t];
+        atomicAdd(&dgam_s[t], sq - sk + bet_s[t] * eg * sw);
+        atomicAdd(&dbet_s[t], eg * sw);
+        rk_total += sk;
+      }
     }
+    rk_total = sum64(rk_total);
+    if (lane == 0) atomicAdd(&dgam_s[R - 1], rk_total);
+  }
 
-    if (panel == 0) {
-      // ---- P and KK on this wave's R x R tile: contraction over all keys.
-      f32x16 pt = {}, kkt = {};
-      if (NP == 1 && std::is_same<E, bf16_t>::value) {
-        // bf16 MFMA: the rounded rows are exact in bf16 (32x32x16, lane l holds
-        // row l%32, columns 16 g + 8 (l/32) .. +7).
+  // ---- P (waves 0-3) and KK (waves 4-7) on the R x R tile: contraction over all keys.
+  f32x16 pk2 = {};
+  if (!grp_p || has_q) {
+    if (std::is_same<E, bf16_t>::value) {
+      // bf16 MFMA: the rounded rows are exact in bf16 (32x32x16, lane l holds
+      // row l%32, columns 16 g + 8 (l/32) .. +7).
 #pragma unroll 4
-        for (int g = 0; g < KM / 16; ++g) {
-          const int c0 = 16 * g + 8 * hh;
-          const bf16x8 bk = pack8(xk_s + (32 * ru + li) * LX + c0);
-          if (has_q) pt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack8(xq_s + (32 * rr + li) * LX + c0), bk, pt, 0, 0, 0);
-          kkt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack8(xk_s + (32 * rr + li) * LX + c0), bk, kkt, 0, 0, 0);
+      for (int g = 0; g < KM / 16; ++g) {
+        const int c0 = 16 * g + 8 * hh;
+        bf16x8 a, bk;
+        if (XR) {
+          a = *reinterpret_cast<const bf16x8*>((grp_p ? xqb : xkb) + (32 * rr + li) * LX + c0);
+          bk = *reinterpret_cast<const bf16x8*>(xkb + (32 * ru + li) * LX + c0);
+        } else {
+          a = pack8((grp_p ? xq_s : xk_s) + (32 * rr + li) * LX + c0);
+          bk = pack8(xk_s + (32 * ru + li) * LX + c0);
         }
-      } else if (NP == 1) {
+        pk2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bk, pk2, 0, 0, 0);
+      }
+    } else {
 #pragma unroll 4
-        for (int g = 0; g < KM / 8; ++g) {
-          const int c0 = 8 * g + 4 * hh;
-          const f32x4 bk = ld_c(xk_s, LX, 32 * ru + li, c0);
-          if (has_q) mma8(pt, ld_c(xq_s, LX, 32 * rr + li, c0), bk);
-          mma8(kkt, ld_c(xk_s, LX, 32 * rr + li, c0), bk);
-        }
-      } else {  // both panels: the rounded rows straight from the forward's buffers
-#pragma unroll 4
-        for (int g = 0; g < KM / 8; ++g) {
-          const int c0 = 8 * g + 4 * hh;
-          const bool in = c0 < K;  // K % 4 == 0: a 4-column group is wholly in or out
-          const int cc = in ? c0 : 0;
-          f32x4 bk = ld_c(kn, K, 32 * ru + li, cc), ak = ld_c(kn, K, 32 * rr + li, cc);
-          f32x4 aq = has_q ? ld_c(qn, K, 32 * rr + li, cc) : f32x4{};
-          if (!in) bk = ak = aq = f32x4{};
-          if (has_q) mma8(pt, aq, bk);
-          mma8(kkt, ak, bk);
-        }
+      for (int g = 0; g < KM / 8; ++g) {
+        const int c0 = 8 * g + 4 * hh;
+        mma8(pk2, ld_c(grp_p ? xq_s : xk_s, LX, 32 * rr + li, c0), ld_c(xk_s, LX, 32 * ru + li, c0));
       }
-      // ---- dP: gate gradients and dQK; X to LDS.
-      {
-        const int u = 32 * ru + li;
-        float prow[16], pcol = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * rr + acc_row(r, hh);
-          const bool live = u <= t;
-          const float e = live ? __expf(gam_s[t] - gam_s[u]) : 0.f;
-          const float dpv = (has_q && live) ? dp[r] : 0.f;
-          const float g = dpv * e * pt[r];
-          prow[r] = g;
-          pcol += g;
-          dqk[t * LT + u] = dpv * e;
-          xm[t * LT + u] = xt[r];
-        }
-        const float srow = tile_row_sum(prow, lane);
-        if ((lane & 1) == 0) atomicAdd(&dgam_s[32 * rr + acc_row(sum_index(lane), hh)], srow);
-        pcol += __shfl_xor(pcol, 32);
-        if (hh == 0) atomicAdd(&dgam_s[u], -pcol);
-      }
-      __syncthreads();
-      // ---- dA = -(T^T X), strictly lower: b, gate and dKK.
-      {
-        f32x16 da = {};
-#pragma unroll
-        for (int g = 0; g < R / 8; ++g) {
-          const int c0 = 8 * g + 4 * hh;
-          mma8(da, ld_x(tm, LT, 32 * rr + li, c0), ld_x(xm, LT, 32 * ru + li, c0));
-        }
-        __syncthreads();  // xm is read by every wave before dKK overwrites it
-        const int u = 32 * ru + li;
-        float rb[16], rg[16], gcol = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * rr + acc_row(r, hh);
-          const bool live = u < t;  // e^{G_t-G_u} may overflow above the diagonal
-          const float dav = live ? -da[r] : 0.f;
-          const float e = live ? __expf(gam_s[t] - gam_s[u]) : 0.f;
-          const float ekk = e * kkt[r];
-          rb[r] = dav * ekk;
-          const float ga = dav * bet_s[t] * ekk;
-          rg[r] = ga;
-          gcol += ga;
-          dkk[t * LT + u] = dav * bet_s[t] * e;
-        }
-        const float sb = tile_row_sum(rb, lane), sg = tile_row_sum(rg, lane);
-        if ((lane & 1) == 0) {
-          const int t = 32 * rr + acc_row(sum_index(lane), hh);
-          atomicAdd(&dbet_s[t], sb);
-          atomicAdd(&dgam_s[t], sg);
-        }
-        gcol += __shfl_xor(gcol, 32);
-        if (hh == 0) atomicAdd(&dgam_s[u], -gcol);
-      }
-      __syncthreads();
     }
-
-    // ---- position-axis terms: dQn += dQK Kn; dKn += dQK^T Qn + (dKK + dKK^T) Kn.
-    {
-      const int kc = 32 * kt + li;
-#pragma unroll 2
+  }
+  {
+    const int u = 32 * ru + li;
+    if (grp_p) {
+      // ---- dP: gate gradients and dQK.
+      float prow[16], pcol = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * rr + acc_row(r, hh);
+        const bool live = u <= t;
+        const float e = live ? __expf(gam_s[t] - gam_s[u]) : 0.f;
+        const float dpv = (has_q && live) ? dp[r] : 0.f;
+        const float g = dpv * e * pk2[r];
+        prow[r] = g;
+        pcol += g;
+        dqk[t * LT + u] = dpv * e;
+      }
+      const float srow = tile_row_sum(prow, lane);
+      if ((lane & 1) == 0) atomicAdd(&dgam_s[32 * rr + acc_row(sum_index(lane), hh)], srow);
+      pcol += __shfl_xor(pcol, 32);
+      if (hh == 0) atomicAdd(&dgam_s[u], -pcol);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xm[(32 * rr + acc_row(r, hh)) * LT + u] = dp[r];
+    }
+    __syncthreads();
+    // ---- dA = -(T^T X), strictly lower (waves 4-7): b, gate and dKK.
+    f32x16 da = {};
+    if (!grp_p) {
+#pragma unroll
       for (int g = 0; g < R / 8; ++g) {
         const int c0 = 8 * g + 4 * hh;
-        const f32x4 bk = round4<E>(ld_x(xk_s, LX, kc, c0));
-        const f32x4 bq = round4<E>(ld_x(xq_s, LX, kc, c0));
-#pragma unroll
-        for (int m = 0; m < NTW; ++m) {
-          const int row = 32 * tile_rt(m) + li;
-          if (has_q) {
-            mma8(dq[m], ld_c(dqk, LT, row, c0), bk);
-            mma8(dka[m], ld_x(dqk, LT, row, c0), bq);
-          }
-          mma8(dka[m], ld_c(dkk, LT, row, c0) + ld_x(dkk, LT, row, c0), bk);
-        }
+        mma8(da, ld_x(tm, LT, 32 * rr + li, c0), ld_x(xm, LT, 32 * ru + li, c0));
       }
     }
+    __syncthreads();  // xm is read by every wave before dKK overwrites it
+    if (!grp_p) {
+      float rb[16], rg[16], gcol = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * rr + acc_row(r, hh);
+        const bool live = u < t;  // e^{G_t-G_u} may overflow above the diagonal
+        const float dav = live ? -da[r] : 0.f;
+        const float e = live ? __expf(gam_s[t] - gam_s[u]) : 0.f;
+        const float ekk = e * pk2[r];
+        rb[r] = dav * ekk;
+        const float ga = dav * bet_s[t] * ekk;
+        rg[r] = ga;
+        gcol += ga;
+        dkk[t * LT + u] = dav * bet_s[t] * e;
+      }
+      const float sb = tile_row_sum(rb, lane), sg = tile_row_sum(rg, lane);
+      if ((lane & 1) == 0) {
+        const int t = 32 * rr + acc_row(sum_index(lane), hh);
+        atomicAdd(&dbet_s[t], sb);
+        atomicAdd(&dgam_s[t], sg);
+      }
+      gcol += __shfl_xor(gcol, 32);
+      if (hh == 0) atomicAdd(&dgam_s[u], -gcol);
+    }
+    __syncthreads();
+  }
 
-    // ---- normalisation backward, part 1: x/|x| . dX per row.
-    {
-      const int kc = 32 * kt + li, k = kb + kc;
+  // ---- position-axis terms, then the normalisation backward.
+  // Exact x/|x| at this lane's tile elements (the raw rows when XR).
+  float xe[NTW][16], qe[NTW][16];
+  if (own) {
+    const int k = 32 * kt + li;
+#pragma unroll 2
+    for (int g = 0; g < R / 8; ++g) {
+      const int c0 = 8 * g + 4 * hh;
+      const f32x4 bk = f32x4{kr(c0, k), kr(c0 + 1, k), kr(c0 + 2, k), kr(c0 + 3, k)};
+      const f32x4 bq = f32x4{qr(c0, k), qr(c0 + 1, k), qr(c0 + 2, k), qr(c0 + 3, k)};
 #pragma unroll
       for (int m = 0; m < NTW; ++m) {
-        const int rt = tile_rt(m);
-        float ck[16], cq[16];
+        const int row = 32 * tile_rt(m) + li;
+        if (has_q) {
+          mma8(dq[m], ld_c(dqk, LT, row, c0), bk);
+          mma8(dka[m], ld_x(dqk, LT, row, c0), bq);
+        }
+        mma8(dka[m], ld_c(dkk, LT, row, c0) + ld_x(dkk, LT, row, c0), bk);
+      }
+    }
+    if (XR) {
+      const bool kin = k < K;
+#pragma unroll
+      for (int m = 0; m < NTW; ++m)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int t = 32 * rt + acc_row(r, hh);
-          ck[r] = xk_s[t * LX + kc] * dka[m][r];
-          cq[r] = xq_s[t * LX + kc] * dq[m][r];
+          const int tok = tok_s[32 * tile_rt(m) + acc_row(r, hh)];
+          const bool ok = tok >= 0 && kin;
+          const int tt = ok ? tok : 0, kk = ok ? k : 0;
+          xe[m][r] = op_load<E>(p.k, b, h, tt, kk);
+          qe[m][r] = op_load<E>(qsrc, b, h, tt, kk);
         }
-        const float sk = tile_row_sum(ck, lane);
-        const float sq = has_q ? tile_row_sum(cq, lane) : 0.f;
-        if ((lane & 1) == 0) {
-          const int t = 32 * rt + acc_row(sum_index(lane), hh);
-          atomicAdd(&kdot_s[t], sk);
-          if (has_q) atomicAdd(&qdot_s[t], sq);
-        }
-        if (panel + 1 < NP && k < K) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int tok = tok_s[32 * rt + acc_row(r, hh)];
-            if (tok < 0) continue;
-            if (has_q)
-              reinterpret_cast<float*>(gr.dq.ptr)[op_base(gr.dq, b, h) + (int64_t)tok * gr.dq.st + k] = dq[m][r];
-            reinterpret_cast<float*>(gr.dk.ptr)[op_base(gr.dk, b, h) + (int64_t)tok * gr.dk.st + k] = dka[m][r];
-          }
+      for (int m = 0; m < NTW; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = 32 * tile_rt(m) + acc_row(r, hh);
+          const bool ok = tok_s[t] >= 0 && kin;
+          xe[m][r] = ok ? xe[m][r] * krd_s[t] : 0.f;
+          qe[m][r] = (ok && has_q) ? qe[m][r] * qrd_s[t] : 0.f;
         }
+    } else {
+#pragma unroll
+      for (int m = 0; m < NTW; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = 32 * tile_rt(m) + acc_row(r, hh);
+          xe[m][r] = xk_s[t * LX + k];
+          qe[m][r] = xq_s[t * LX + k];
+        }
+    }
+    // part 1: x/|x| . dX per row
+#pragma unroll
+    for (int m = 0; m < NTW; ++m) {
+      float ck[16], cq[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        ck[r] = xe[m][r] * dka[m][r];
+        cq[r] = qe[m][r] * dq[m][r];
+      }
+      const float sk = tile_row_sum(ck, lane);
+      const float sq = has_q ? tile_row_sum(cq, lane) : 0.f;
+      if ((lane & 1) == 0) {
+        const int t = 32 * tile_rt(m) + acc_row(sum_index(lane), hh);
+        atomicAdd(&kdot_s[t], sk);
+        if (has_q) atomicAdd(&qdot_s[t], sq);
       }
     }
   }
@@ -623,54 +642,28 @@ __global__ __launch_bounds__(NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p, g
   __syncthreads();
   if (tid == 0) dgam_s[R - 1] += __expf(gc) * red_s[0];
 
-  // ---- normalisation backward, part 2: dX = (g - x^ (x^ . g)) / |x| for every
-  // panel; an earlier panel's g and x are re-read from global memory (all of a
-  // tile's loads are issued before its stores).
-  float* dqo = gr.dq.ptr && p.q.ptr ? reinterpret_cast<float*>(gr.dq.ptr) + op_base(gr.dq, b, h) : nullptr;
-  float* dko = reinterpret_cast<float*>(gr.dk.ptr) + op_base(gr.dk, b, h);
-#pragma unroll 1
-  for (int panel = 0; panel < NP; ++panel) {
-    const int kc = 32 * kt + li, k = panel * KP + kc;
-    const bool kin = k < K, parked = panel + 1 < NP;
+  // ---- part 2: dX = (g - x^ (x^ . g)) / |x|.
+  if (own) {
+    const int k = 32 * kt + li;
+    float* dqo = gr.dq.ptr && p.q.ptr ? reinterpret_cast<float*>(gr.dq.ptr) + op_base(gr.dq, b, h) : nullptr;
+    float* dko = reinterpret_cast<float*>(gr.dk.ptr) + op_base(gr.dk, b, h);
+    if (k < K) {
 #pragma unroll
-    for (int m = 0; m < NTW; ++m) {
-      const int rt = tile_rt(m);
-      float xk[16], xq[16], gk[16], gq[16];
-      int tk[16];
+      for (int m = 0; m < NTW; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 32 * rt + acc_row(r, hh);
-        const int tok = tok_s[t];
-        const bool ok = tok >= 0 && kin;
-        const int tt = ok ? tok : 0, kk = ok ? k : 0;
-        tk[r] = ok ? tok : -1;
-        if (parked) {
-          xk[r] = op_load<E>(p.k, b, h, tt, kk) / fmaxf(knrm_s[t], 1e-6f);  // the forward's x/|x|
-          gk[r] = dko[(int64_t)tt * gr.dk.st + kk];
+        for (int r = 0; r < 16; ++r) {
+          const int t = 32 * tile_rt(m) + acc_row(r, hh);
+          const int tok = tok_s[t];
+          if (tok < 0) continue;
+          dko[(int64_t)tok * gr.dk.st + k] =
+              (knrm_s[t] > 1e-6f ? dka[m][r] - xe[m][r] * kdot_s[t] : dka[m][r]) * krd_s[t];
           if (has_q) {
-            xq[r] = op_load<E>(p.q, b, h, tt, kk) / fmaxf(qnrm_s[t], 1e-6f);
-            gq[r] = dqo[(int64_t)tt * gr.dq.st + kk];
+            dqo[(int64_t)tok * gr.dq.st + k] =
+                (qnrm_s[t] > 1e-6f ? dq[m][r] - qe[m][r] * qdot_s[t] : dq[m][r]) * qrd_s[t];
+          } else if (dqo) {
+            dqo[(int64_t)tok * gr.dq.st + k] = 0.f;
           }
-        } else {
-          xk[r] = xk_s[t * LX + kc];
-          gk[r] = dka[m][r];
-          xq[r] = xq_s[t * LX + kc];
-          gq[r] = dq[m][r];
         }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 32 * rt + acc_row(r, hh);
-        if (tk[r] < 0) continue;
-        {
-          dko[(int64_t)tk[r] * gr.dk.st + k] = (knrm_s[t] > 1e-6f ? gk[r] - xk[r] * kdot_s[t] : gk[r]) * krd_s[t];
-        }
-        if (has_q) {
-          dqo[(int64_t)tk[r] * gr.dq.st + k] = (qnrm_s[t] > 1e-6f ? gq[r] - xq[r] * qdot_s[t] : gq[r]) * qrd_s[t];
-        } else if (dqo) {
-          dqo[(int64_t)tk[r] * gr.dq.st + k] = 0.f;
-        }
-      }
     }
   }
   __syncthreads();
@@ -699,7 +692,7 @@ int launch_chunk_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) return fail(GPA_HIP_EHIP, "hipFuncSetAttribute(max dynamic LDS) failed");
   }
-  hipLaunchKernelGGL((gdn_chunk_bwd_mfma<E, KM>), dim3(nch, p.batch * p.heads), dim3(NT), lds, st, p, sv, gr, nch);
+  hipLaunchKernelGGL((gdn_chunk_bwd_mfma<E, KM>), dim3(nch, p.batch * p.heads), dim3(CB_NT), lds, st, p, sv, gr, nch);
   return GPA_HIP_OK;
 }
 
