@@ -92,6 +92,9 @@ int launch_state_fwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int
 template <int KM>
 int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
                           hipStream_t st);
+// MFMA chunk preparation (gdn_prep_mfma.hip); mf: write the bf16 fragments.
+template <typename E, int KM>
+int launch_prep_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, bool mf, int nch, hipStream_t st);
 // fp32-MFMA chunk backward (gdn_chunk_bwd_mfma.hip); needs kdim % 4 == 0.
 template <typename E, int KM>
 int launch_chunk_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,

@@ -8,7 +8,7 @@
 //   O = diag(e^G) Q S_n + (causal e^{G_t-G_s} Q K^T) D,
 //   S_{n+1} = e^{G_C} S_n + (diag(e^{G_C-G}) K)^T D.
 // Kernels:
-//   gdn_prep       chunk-parallel: normalise, G, T, W, U
+//   gdn_prep_mfma  chunk-parallel: normalise, G, T, W, U (gdn_prep_mfma.hip)
 //   gdn_state_fwd  sequential over chunks, parallel over (stream, 32-column tile):
 //                  S_n (saved), D
 //   gdn_out_fwd    chunk-parallel: O
@@ -27,249 +27,6 @@
 #include "gdn_common.h"
 
 namespace gpa {
-
-// ---------------------------------------------------------------------------
-// gdn_prep: one block per (chunk n = blockIdx.x, stream s = blockIdx.y).
-// MF: also write the bf16 MFMA fragments of W, Kn and Qn (see gpa_hip.h);
-// W in fp32 is then not needed and not written.
-template <typename E, int KM, bool MF>
-__global__ __launch_bounds__(NT) void gdn_prep(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
-  constexpr int KP = KM + 4;          // padded row stride (keeps 16-byte alignment)
-  extern __shared__ __align__(16) float smem[];
-  float* kn_s = smem;                 // [R][KP]
-  float* a_s = kn_s + R * KP;         // [R][LDR]   A
-  float* t_s = a_s + R * LDR;         // [R][LDR]   T
-  float* v_s = t_s + R * LDR;         // [R][LDR]   b*V slice
-  float* gam_s = v_s + R * LDR;       // [R]
-  float* beta_s = gam_s + R;          // [R]
-  float* sc_s = beta_s + R;           // [R]  b e^G
-  const int n = blockIdx.x, s = blockIdx.y;
-  const int b = s / p.heads, h = s % p.heads;
-  const int K = p.kdim, V = p.vdim, tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int K16 = K / 16;
-  const int64_t chunk_id = (int64_t)s * nch + n;
-
-  if (tid < R) {
-    const int t = token_at(p, n, tid);
-    gam_s[tid] = t >= 0 ? scalar_load(p.g, b, h, t) : 0.f;
-    beta_s[tid] = t >= 0 ? scalar_load(p.beta, b, h, t) : 0.f;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int r = 0; r < R; ++r) { acc += gam_s[r]; gam_s[r] = acc; }
-  }
-  __syncthreads();
-  if (tid < R) {
-    sc_s[tid] = beta_s[tid] * __expf(gam_s[tid]);
-    sv.gam[rows_off(s, n, nch, 0, 1) + tid] = gam_s[tid];
-    sv.beta[rows_off(s, n, nch, 0, 1) + tid] = beta_s[tid];
-  }
-
-  // Normalise keys (and queries) row by row: wave w owns rows w, w+4, ...
-  __bf16* qcol = MF && p.q.ptr ? reinterpret_cast<__bf16*>(sv.qcol) + chunk_id * frag_col_elems(K, 8) : nullptr;
-  for (int r = wave; r < R; r += NT / 64) {
-    const int t = token_at(p, n, r);
-    float x[KM / 64];
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < KM / 64; ++i) {
-      const int d = lane + 64 * i;
-      x[i] = (t >= 0 && d < K) ? op_load<E>(p.k, b, h, t, d) : 0.f;
-      ss += x[i] * x[i];
-    }
-    const float den = fmaxf(sqrtf(sum64(ss)), 1e-6f);
-#pragma unroll
-    for (int i = 0; i < KM / 64; ++i) {
-      const int d = lane + 64 * i;
-      const float y = round_as<E>(x[i] / den);
-      kn_s[r * KP + d] = y;
-      if (d < K) sv.kn[rows_off(s, n, nch, r, K) + d] = y;
-    }
-    if (p.q.ptr) {
-      float ssq = 0.f;
-#pragma unroll
-      for (int i = 0; i < KM / 64; ++i) {
-        const int d = lane + 64 * i;
-        x[i] = (t >= 0 && d < K) ? op_load<E>(p.q, b, h, t, d) : 0.f;
-        ssq += x[i] * x[i];
-      }
-      const float dq = fmaxf(sqrtf(sum64(ssq)), 1e-6f);
-#pragma unroll
-      for (int i = 0; i < KM / 64; ++i) {
-        const int d = lane + 64 * i;
-        if (d < K) {
-          const float y = round_as<E>(x[i] / dq);
-          sv.qn[rows_off(s, n, nch, r, K) + d] = y;
-          if (MF) {  // Qn^T fragment (rb, cs), lane (d%32) + 32*((r/8)%2), element r%8
-            const int rb = d >> 5, cs = r >> 4, ln = (d & 31) + 32 * ((r >> 3) & 1);
-            qcol[((rb * 4 + cs) * 64 + ln) * 8 + (r & 7)] = (__bf16)y;
-          }
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  if (MF) {
-    // Kn row and column fragments (exact in bf16), one 16-byte piece per step.
-    __bf16* krow = reinterpret_cast<__bf16*>(sv.krow) + chunk_id * frag_row_elems(K, 8);
-    __bf16* kcol = reinterpret_cast<__bf16*>(sv.kcol) + chunk_id * frag_col_elems(K, 8);
-    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-    for (int piece = tid; piece < 2 * K16 * 64; piece += NT) {
-      const int ln = piece & 63, ks = (piece >> 6) % K16, rt = (piece >> 6) / K16;
-      const float* src = kn_s + (32 * rt + (ln & 31)) * KP + 16 * ks + 8 * (ln >> 5);
-      bf16x8 f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = (__bf16)src[e];
-      *reinterpret_cast<bf16x8*>(krow + (int64_t)piece * 8) = f;
-    }
-    const int RB = (K + 31) / 32;
-    for (int piece = tid; piece < RB * 4 * 64; piece += NT) {
-      const int ln = piece & 63, cs = (piece >> 6) & 3, rb = piece >> 8;
-      const int k = 32 * rb + (ln & 31), c0 = 16 * cs + 8 * (ln >> 5);
-      bf16x8 f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = (__bf16)(k < K ? kn_s[(c0 + e) * KP + k] : 0.f);
-      *reinterpret_cast<bf16x8*>(kcol + (int64_t)piece * 8) = f;
-    }
-  }
-
-  // Gram matrix -> A (strictly lower).  Thread tile: rows 4*ty+i, cols tx+16*j.
-  const int ty = tid / 16, tx = tid % 16;
-  {
-    float acc[4][4] = {};
-    for (int k = 0; k < KM; ++k) {
-      float a[4], c[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = kn_s[(4 * ty + i) * KP + k];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = kn_s[(tx + 16 * j) * KP + k];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = 4 * ty + i, u = tx + 16 * j;
-        a_s[t * LDR + u] = (u < t) ? beta_s[t] * __expf(gam_s[t] - gam_s[u]) * acc[i][j] : 0.f;
-      }
-  }
-  __syncthreads();
-
-  // T = (I + A)^-1 by forward substitution; thread c owns column c.
-  if (tid < R) {
-    const int c = tid;
-    for (int t = 0; t < c; ++t) t_s[t * LDR + c] = 0.f;
-    t_s[c * LDR + c] = 1.f;
-    for (int t = c + 1; t < R; ++t) {
-      float acc = 0.f;
-      for (int u = c; u < t; ++u) acc += a_s[t * LDR + u] * t_s[u * LDR + c];
-      t_s[t * LDR + c] = -acc;
-    }
-  }
-  __syncthreads();
-  for (int idx = tid; idx < R * R; idx += NT)
-    sv.tri[rows_off(s, n, nch, 0, R) + idx] = t_s[(idx / R) * LDR + idx % R];
-
-  // W = T diag(b e^G) Kn.  Thread tile: rows 4*ty+i, 8 consecutive columns 8*tx + 128*pass.
-  for (int c0 = 8 * tx; c0 < KM; c0 += 128) {
-    float acc[4][8] = {};
-    for (int u = 0; u < R; ++u) {
-      float a[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = t_s[(4 * ty + i) * LDR + u] * sc_s[u];
-      const float4 k0 = *reinterpret_cast<const float4*>(&kn_s[u * KP + c0]);
-      const float4 k1 = *reinterpret_cast<const float4*>(&kn_s[u * KP + c0 + 4]);
-      const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] += a[i] * kv[e];
-    }
-    if (c0 >= K) continue;
-    if (!MF) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float* dst = sv.w + rows_off(s, n, nch, 4 * ty + i, K) + c0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (c0 + e < K) dst[e] = acc[i][e];
-      }
-    } else {
-      typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-      __bf16* wrow = reinterpret_cast<__bf16*>(sv.wrow) + chunk_id * frag_row_elems(K, 16);
-      __bf16* wcol = reinterpret_cast<__bf16*>(sv.wcol) + chunk_id * frag_col_elems(K, 16);
-      // Row fragment: row t, columns c0..c0+7 = fragment (t/32, c0/16), lane t%32 + 32*((c0/8)%2).
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 4 * ty + i;
-        const int ln = (t & 31) + 32 * ((c0 >> 3) & 1);
-        __bf16* dst = wrow + (((t >> 5) * K16 + (c0 >> 4)) * 64 + ln) * 16;
-        bf16x8 hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          hi[e] = (__bf16)acc[i][e];
-          lo[e] = (__bf16)(acc[i][e] - (float)hi[e]);
-        }
-        *reinterpret_cast<bf16x8*>(dst) = hi;
-        *reinterpret_cast<bf16x8*>(dst + 8) = lo;
-      }
-      // Column fragment: column k, rows 4*ty..4*ty+3 = fragment (k/32, t/16),
-      // lane k%32 + 32*((t/8)%2), elements t%8 .. t%8+3.
-      const int t0 = 4 * ty;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int k = c0 + e;
-        const int ln = (k & 31) + 32 * ((t0 >> 3) & 1);
-        __bf16* dst = wcol + (((k >> 5) * 4 + (t0 >> 4)) * 64 + ln) * 16 + (t0 & 7);
-        bf16x4 hi, lo;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          hi[i] = (__bf16)acc[i][e];
-          lo[i] = (__bf16)(acc[i][e] - (float)hi[i]);
-        }
-        *reinterpret_cast<bf16x4*>(dst) = hi;
-        *reinterpret_cast<bf16x4*>(dst + 8) = lo;
-      }
-    }
-  }
-
-  // U = T diag(b) V, 64 value columns at a time, stored value-major.
-  for (int v0 = 0; v0 < V; v0 += R) {
-    __syncthreads();
-    for (int idx = tid; idx < R * R; idx += NT) {
-      const int r = idx / R, c = idx % R;
-      const int t = token_at(p, n, r);
-      v_s[r * LDR + c] = (t >= 0 && v0 + c < V) ? beta_s[r] * op_load<E>(p.v, b, h, t, v0 + c) : 0.f;
-    }
-    __syncthreads();
-    float acc[4][4] = {};
-    for (int u = 0; u < R; ++u) {
-      float a[4], c[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = t_s[(4 * ty + i) * LDR + u];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = v_s[u * LDR + tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c[j];
-    }
-    float* um = sv.u + vc_off(s, n, nch, V);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int v = v0 + tx + 16 * j;
-      if (v < V)
-        *reinterpret_cast<float4*>(&um[(int64_t)v * R + 4 * ty]) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // gdn_state_fwd: block (column tile blockIdx.x, stream blockIdx.y), loops chunks.
@@ -1121,15 +878,8 @@ int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operan
                    hipStream_t st, int nch) {
   const dim3 grid_c(nch, p.batch * p.heads), block(NT);
   const bool mf = use_mfma<E>(p);
-  const size_t lds_prep = sizeof(float) * (R * (KM + 4) + 3 * R * LDR + 3 * R);
   mark(tm, st);
-  if (mf) {
-    if (int rc = allow_lds(gdn_prep<E, KM, true>, lds_prep)) return rc;
-    hipLaunchKernelGGL((gdn_prep<E, KM, true>), grid_c, block, lds_prep, st, p, sv, nch);
-  } else {
-    if (int rc = allow_lds(gdn_prep<E, KM, false>, lds_prep)) return rc;
-    hipLaunchKernelGGL((gdn_prep<E, KM, false>), grid_c, block, lds_prep, st, p, sv, nch);
-  }
+  if (int rc = launch_prep_mfma<E, KM>(p, sv, mf, nch, st)) return rc;
   mark(tm, st);
   if (mf) {
     if (int rc = launch_state_fwd_mfma<KM>(p, sv, nch, st)) return rc;

@@ -115,7 +115,7 @@ def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
         return None
     e, km = _tag(dtype), _kmax(k)
     state = f"gdn_state_fwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_fwd<{km}>"
-    kernels = [(f"gdn_prep<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
+    kernels = [(f"gdn_prep_mfma<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
                 (4 * c * k + 2 * c * v + c * c / 3) * tokens),
                (state, 4 * k * v * tokens)]
     if read:
