@@ -38,6 +38,8 @@ def _ptr(t):
 def _in_use_here(*tensors):
     """Mark tensors made on another stream as read by the current one, so the
     caching allocator keeps their memory until this stream's work is done."""
+    if torch.cuda.is_current_stream_capturing():
+        return  # a capture runs on one stream
     stream = torch.cuda.current_stream()
     for t in tensors:
         if t is not None:
@@ -160,3 +162,68 @@ def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor
     g, beta = g.float(), beta.float()
     out, states_vk, final = _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)
     return out, states_vk.transpose(-1, -2), final
+
+
+# --------------------------------------------------------------------------- reference-signature operators
+def _check_scan_args(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor) -> None:
+    """The reference's argument checks and messages (src/gpa/ops.py:52-55)."""
+    if q.shape != k.shape or q.shape[:3] != v.shape[:3]:
+        raise ValueError("q/k must share [B,T,H,K], v must share [B,T,H]")
+    if g.shape != q.shape[:3] or beta.shape != q.shape[:3]:
+        raise ValueError("g and beta must be scalar per token/head: [B,T,H]")
+
+
+def gdn_scan(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, initial_state: Tensor, *,
+             backend: str = "hip", chunk_size: int = 64) -> tuple[Tensor, Tensor]:
+    """Drop-in for the reference `gdn_scan` (src/gpa/ops.py:49-85): q,k [B,T,H,K],
+    v [B,T,H,V], scalar g/beta [B,T,H], initial_state [B,H,K,V] key-major.
+    Returns (out [B,T,H,V] in q's dtype, final state [B,H,K,V] float32).  Empty
+    T returns (empty, initial_state) unchanged, as the reference does."""
+    _check_scan_args(q, k, v, g, beta)
+    if q.shape[1] == 0:
+        return v.new_empty(*v.shape), initial_state
+    if backend != "hip":
+        raise ValueError(f"unknown backend: {backend}")
+    out, _, final = gdn_scan_hip(q, k, v, g, beta, initial_state, chunk=chunk_size)
+    return out, final
+
+
+def gdn_update(state: Tensor, key: Tensor, value: Tensor, log_gate: Tensor, beta: Tensor) -> Tensor:
+    """One GDN step of every stream (src/gpa/ops.py:29-42): S [B,H,K,V], k [B,H,K],
+    v [B,H,V], scalar g/beta [B,H]; the HIP scan over a single token."""
+    if log_gate.shape != key.shape[:-1] or beta.shape != key.shape[:-1]:
+        raise ValueError("GDN scalar gates/beta must be [B,H], not vector gates")
+    _, _, final = gdn_scan_hip(None, key[:, None], value[:, None], log_gate[:, None], beta[:, None], state,
+                               chunk=1)
+    return final.to(state.dtype)
+
+
+def memory_read(query: Tensor, state: Tensor) -> Tensor:
+    """u(q)^T S per stream (src/gpa/ops.py:45-46): q [B,H,K], S [B,H,K,V] -> [B,H,V]."""
+    _lib.require_device(query)
+    qn = torch.nn.functional.normalize(query.float(), p=2, dim=-1, eps=1e-6).to(query.dtype)
+    return torch.matmul(qn.to(state.dtype)[..., None, :], state)[..., 0, :].to(query.dtype)
+
+
+class TwoStageState:
+    """Carried state of `two_stage_gdn` (src/gpa/ops.py:140-143): inner [B,H,Dk,M],
+    outer [B,H,M,Dv], key-major."""
+    __slots__ = ("inner", "outer")
+
+    def __init__(self, inner: Tensor, outer: Tensor):
+        self.inner, self.outer = inner, outer
+
+
+def two_stage_gdn(q: Tensor, k: Tensor, slots: Tensor, v: Tensor, gi: Tensor, bi: Tensor, go: Tensor,
+                  bo: Tensor, state: TwoStageState, *, route_weight: Tensor | None = None,
+                  query_weight: Tensor | None = None, query_scale: float = 1 / 16,
+                  backend: str = "hip") -> tuple[Tensor, TwoStageState]:
+    """GDN(softmax(GDN(q,k,slots)) W_rs + q W_qs/16, slots, v) (src/gpa/ops.py:146-163)."""
+    inner, a = gdn_scan(q, k, slots, gi, bi, state.inner, backend=backend)
+    route = inner.float().softmax(-1).to(q.dtype)
+    if route_weight is not None:
+        route = torch.nn.functional.linear(route, route_weight.to(route.dtype))
+    if query_weight is not None:
+        route = route + query_scale * torch.nn.functional.linear(q, query_weight.to(q.dtype))
+    out, b = gdn_scan(route, slots, v, go, bo, state.outer, backend=backend)
+    return out, TwoStageState(a, b)

@@ -61,7 +61,12 @@ def _concurrent(jobs):
     them.  Inputs are recorded as used on their side stream and results as
     used on the current stream, so the caching allocator does not hand their
     memory to another stream early.  Autograd runs each job's backward on the
-    job's stream, so the backward scans overlap the same way."""
+    job's stream, so the backward scans overlap the same way.  During a graph
+    capture the jobs run in order on the capturing stream."""
+    if torch.cuda.is_current_stream_capturing():
+        # Inside a HIP graph capture everything stays on the capturing stream
+        # (no cross-stream fork/join, no allocator stream records).
+        return [fn() for fn, _ in jobs]
     main = torch.cuda.current_stream()
     streams = _side_streams(main.device)[:len(jobs)]
     for stream in streams:
@@ -291,6 +296,13 @@ def _relations(model, local, writes, rel_states, scan):
     return incoming, tuple(finals)
 
 
+def _incoming_index(model, j: int) -> Tensor:
+    """Device index of the edges into level j (i-major order), built from the
+    module's edge-target buffer so that no host copy happens inside a graph
+    capture."""
+    return (model._edge_target == j).nonzero_static(size=model.config.levels - 1)[:, 0]
+
+
 def _bridge(model, q: Tensor, logits, incoming, counts):
     """Route reader and query projection per target level (attention.py:225-262)."""
     cfg = model.config
@@ -298,8 +310,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
     routes, queries = [], []
     for j, base in enumerate(logits):
         if incoming[j]:
-            ids = [e for e, _ in incoming[j]]
-            w = model.edge_logits[ids].softmax(0)
+            w = model.edge_logits.index_select(0, _incoming_index(model, j)).softmax(0)
             total = 0
             if cfg.paper_product_read:
                 for wt, (e, msg) in zip(w, incoming[j]):

@@ -19,5 +19,5 @@ Pinning (how the restatement itself is checked):
     and gradcheck (tests/test_oracle_math.py).
 """
 from .reference import (  # noqa: F401
-    OracleRun, additive_scan, forward, gdn_read, gdn_scan, gdn_step, initial_state, rope, unit,
+    OracleRun, additive_scan, forward, gdn_read, gdn_scan, gdn_step, initial_state, rope, two_stage, unit,
 )

@@ -1,0 +1,78 @@
+"""The reference-signature operators on the GPU vs the oracle (reference
+src/gpa/ops.py:29-85, 140-163): gdn_scan, gdn_update, memory_read and
+two_stage_gdn, in float32 (1e-4 relative) and bfloat16 (2e-2 relative)."""
+import pytest
+import torch
+
+import oracle
+from gpa_amd import TwoStageState, two_stage_gdn
+from gpa_amd.ops import gdn_scan, gdn_update, memory_read
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _scan_inputs(b, t, h, kd, vd, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, t, h, kd, generator=g).to(dtype)
+    k = torch.randn(b, t, h, kd, generator=g).to(dtype)
+    v = torch.randn(b, t, h, vd, generator=g).to(dtype)
+    gate = -torch.rand(b, t, h, generator=g) * .3
+    beta = torch.rand(b, t, h, generator=g)
+    s0 = torch.randn(b, h, kd, vd, generator=g) * .2
+    return q, k, v, gate, beta, s0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_gdn_scan_reference_signature(dtype):
+    q, k, v, g, beta, s0 = _scan_inputs(2, 150, 3, 32, 24, dtype, 0)
+    out, final = gdn_scan(*(x.to(DEV) for x in (q, k, v, g, beta, s0)))
+    ref_out, ref_final = oracle.gdn_scan(q.double(), k.double(), v.double(), g.double(), beta.double(),
+                                         s0.double())
+    assert out.dtype == dtype and final.dtype == torch.float32
+    assert _rel(out, ref_out) < TOL[dtype] and _rel(final, ref_final) < TOL[dtype]
+
+
+def test_gdn_scan_empty_returns_initial_state():
+    q, k, v, g, beta, s0 = _scan_inputs(1, 0, 2, 8, 4, torch.float32, 1)
+    s0 = s0.to(DEV)
+    out, final = gdn_scan(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), s0)
+    assert out.shape == (1, 0, 2, 4) and final is s0
+
+
+def test_gdn_update_and_memory_read_match_one_step():
+    q, k, v, g, beta, s0 = _scan_inputs(2, 1, 3, 16, 8, torch.float32, 2)
+    s1 = gdn_update(s0.to(DEV), k[:, 0].to(DEV), v[:, 0].to(DEV), g[:, 0].to(DEV), beta[:, 0].to(DEV))
+    ref = oracle.gdn_step(s0.double(), k[:, 0].double(), v[:, 0].double(), g[:, 0].double(), beta[:, 0].double())
+    assert _rel(s1, ref) < 1e-5
+    y = memory_read(q[:, 0].to(DEV), s1)
+    assert _rel(y, oracle.gdn_read(q[:, 0].double(), ref)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_two_stage_gdn_matches_oracle(dtype):
+    b, t, h, dk, m, dv = 1, 70, 2, 16, 12, 10
+    gen = torch.Generator().manual_seed(3)
+    q = torch.randn(b, t, h, dk, generator=gen).to(dtype)
+    k = torch.randn(b, t, h, dk, generator=gen).to(dtype)
+    slots = torch.randn(b, t, h, m, generator=gen).to(dtype)
+    v = torch.randn(b, t, h, dv, generator=gen).to(dtype)
+    gates = [-torch.rand(b, t, h, generator=gen) * .2, torch.rand(b, t, h, generator=gen),
+             -torch.rand(b, t, h, generator=gen) * .2, torch.rand(b, t, h, generator=gen)]
+    inner = torch.randn(b, h, dk, m, generator=gen) * .1
+    outer = torch.randn(b, h, m, dv, generator=gen) * .1
+    rw = torch.randn(m, m, generator=gen) / m ** .5
+    qw = torch.randn(m, dk, generator=gen) / dk ** .5
+    out, st = two_stage_gdn(q.to(DEV), k.to(DEV), slots.to(DEV), v.to(DEV), *(x.to(DEV) for x in gates),
+                            TwoStageState(inner.to(DEV), outer.to(DEV)), route_weight=rw.to(DEV),
+                            query_weight=qw.to(DEV))
+    ref_out, ref_a, ref_b = oracle.two_stage(q, k, slots, v, *gates, inner, outer, route_weight=rw,
+                                             query_weight=qw)
+    tol = TOL[dtype]
+    assert _rel(out, ref_out) < tol and _rel(st.inner, ref_a) < tol and _rel(st.outer, ref_b) < tol

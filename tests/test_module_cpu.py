@@ -67,3 +67,17 @@ def test_forward_validation_and_no_cpu_fallback():
         m(q, q, v, other)
     with pytest.raises(_lib.HipBackendError):
         m(q, q, v)
+
+
+def test_reference_signature_ops_validate_like_the_reference():
+    from gpa_amd.ops import gdn_scan
+    x = torch.zeros(1, 3, 2, 4)
+    with pytest.raises(ValueError, match="q/k must share"):
+        gdn_scan(x, torch.zeros(1, 3, 2, 5), x, torch.zeros(1, 3, 2), torch.zeros(1, 3, 2), None)
+    with pytest.raises(ValueError, match="scalar per token"):
+        gdn_scan(x, x, x, torch.zeros(1, 3, 2, 1), torch.zeros(1, 3, 2), None)
+    s0 = torch.zeros(1, 2, 4, 4)
+    out, final = gdn_scan(x[:, :0], x[:, :0], x[:, :0], torch.zeros(1, 0, 2), torch.zeros(1, 0, 2), s0)
+    assert out.shape == (1, 0, 2, 4) and final is s0
+    with pytest.raises(ValueError, match="unknown backend"):
+        gdn_scan(x, x, x, torch.zeros(1, 3, 2), torch.zeros(1, 3, 2), s0, backend="torch")
