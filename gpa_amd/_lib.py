@@ -12,7 +12,10 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
+DECODE_MAX_LEVELS = 4
+DECODE_MAX_EDGES = 12
+DECODE_MAX_WIDTH = 256
 MAX_TIMED = 4
 CHUNK_ROWS = 64
 MAX_KDIM = 256
@@ -50,6 +53,28 @@ class Timing(ctypes.Structure):
     _fields_ = [("events", c_vp * (MAX_TIMED + 1)), ("launched", c_i32)]
 
 
+class DecodeState(ctypes.Structure):
+    _fields_ = [("ptr", c_vp), ("sb", c_i64)]
+
+
+class DecodeLevel(ctypes.Structure):
+    _fields_ = [("slots", c_i32)] + [(n, c_vp) for n in ("center", "gate_weight", "gate_bias", "route_weight",
+                                                           "query_weight", "route_up", "route_down")] + \
+               [(n, DecodeState) for n in ("inner", "outer", "count", "snap_inner", "snap_outer")] + \
+               [(n, c_vp) for n in ("inner_out", "outer_out", "count_out")]
+
+
+class DecodeProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "heads", "key_dim", "value_dim", "levels", "dtype",
+                                     "positional_none")] + \
+               [(n, ctypes.c_float) for n in ("read_scale", "query_scale", "beta_max")] + \
+               [(n, Operand) for n in ("q", "k", "v", "out")] + \
+               [(n, c_vp) for n in ("residual_raw", "count_gain_raw", "route_mlp_gain", "output_logits",
+                                    "relation_gain", "edge_logits", "relation_decay_raw", "relation_beta_raw")] + \
+               [("level", DecodeLevel * DECODE_MAX_LEVELS), ("relation", DecodeState * DECODE_MAX_EDGES),
+                ("relation_out", c_vp * DECODE_MAX_EDGES)]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -59,6 +84,7 @@ EXPORTS = {
                         ctypes.c_int),
     "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads),
                           ctypes.POINTER(Timing), c_vp], ctypes.c_int),
+    "gpa_decode_step": ([ctypes.POINTER(DecodeProblem), c_vp], ctypes.c_int),
 }
 
 _lib = None

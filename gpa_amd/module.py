@@ -160,9 +160,12 @@ class DenseGPA(nn.Module):
             position_ids = torch.arange(state.position, state.position + q.shape[1], device=q.device)
         if position_ids.shape not in ((q.shape[1],), (q.shape[0], q.shape[1])):
             raise ValueError("position_ids must be [T] or [B,T]")
+        from .decode import decode_step, decode_supported
         from .schedule import run_segment
         if q.shape[1] == 0:
             out, new_state, routes = v.new_empty(v.shape), state, None
+        elif not return_diagnostics and decode_supported(self, q, k, v, state, control_input):
+            (out, new_state), routes = decode_step(self, q, k, v, state), None
         else:
             out, new_state, routes = run_segment(self, q, k, v, state, position_ids, control_input,
                                                  want_routes=return_diagnostics)

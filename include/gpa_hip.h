@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 3
+#define GPA_HIP_ABI_VERSION 4
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -136,6 +136,58 @@ int gpa_gdn_forward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
  * ops.py:49-85 in the reference, plus chunk-start state injections). */
 int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
                      const gpa_gdn_grads *grads, gpa_timing *timing, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Batched single-token decode step of the whole DenseGPA core (the reference's
+ * chunk-mode decode: _block_segment at T = 1, src/gpa/attention.py:299-345 and
+ * 396-405), default flags: positional_mode gated or none, linear slot
+ * features, no control input, legacy route reader, no rsa/product/shared
+ * centre/balanced bridge/learned read scale.  One workgroup per (b, h) stream
+ * walks levels, edges, route reader and outer reads for the token; every state
+ * matrix is read and written once.
+ *
+ * States are fp32, [B, H, rows, cols] with each head's matrix contiguous and a
+ * batch stride `sb` in elements (0 for a prefix broadcast over the batch).
+ * Outputs are new, contiguous [B, H, rows, cols] buffers (inputs are never
+ * written).  snap_inner/snap_outer are the block-start snapshots the write and
+ * the residuals read (the current states when the token starts a block).
+ * Parameters are the module's fp32 tensors, contiguous, in the shapes of
+ * src/gpa/attention.py:95-142. */
+#define GPA_DECODE_MAX_LEVELS 4
+#define GPA_DECODE_MAX_EDGES 12
+#define GPA_DECODE_MAX_WIDTH 256  /* key_dim, value_dim and every slot count */
+
+typedef struct gpa_decode_state {
+    const float *ptr;
+    int64_t sb;
+} gpa_decode_state;
+
+typedef struct gpa_decode_level {
+    int32_t slots;
+    const float *center, *gate_weight, *gate_bias;            /* [H,M,Dk], [H,Dk,4], [H,4] */
+    const float *route_weight, *query_weight;                 /* [H,M,M], [H,Dk,M] */
+    const float *route_up, *route_down;                       /* [H,M,2M], [H,2M,M] */
+    gpa_decode_state inner, outer, count;                     /* [B,H,Dk,M], [B,H,M,Dv], [B,H,M] */
+    gpa_decode_state snap_inner, snap_outer;                  /* frozen [B,H,Dk,M], [B,H,M,Dv] */
+    float *inner_out, *outer_out, *count_out;
+} gpa_decode_level;
+
+typedef struct gpa_decode_problem {
+    int32_t batch, heads, key_dim, value_dim, levels, dtype;
+    int32_t positional_none;        /* 1: decay gates are zero (positional_mode "none") */
+    float read_scale, query_scale, beta_max;
+    gpa_operand q, k, v, out;       /* [B,1,H,D] activations (t stride unused) */
+    const float *residual_raw;      /* [L,H,2] */
+    const float *count_gain_raw, *route_mlp_gain, *output_logits, *relation_gain;  /* [L,H] */
+    const float *edge_logits, *relation_decay_raw, *relation_beta_raw;            /* [E,H] */
+    gpa_decode_level level[GPA_DECODE_MAX_LEVELS];
+    gpa_decode_state relation[GPA_DECODE_MAX_EDGES];   /* edge e = (i -> j), i-major: [B,H,Mi,Mj] */
+    float *relation_out[GPA_DECODE_MAX_EDGES];
+} gpa_decode_problem;
+
+/* One decode token of every stream (no autograd).  Replaces the T = 1 call of
+ * DenseGPA.forward in chunk mode (reference attention.py:347-413). */
+int gpa_decode_step(const gpa_decode_problem *problem, hipStream_t stream);
 
 #ifdef __cplusplus
 }

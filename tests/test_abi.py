@@ -18,7 +18,7 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
-                     "gpa_gdn_forward", "gpa_gdn_backward"):
+                     "gpa_gdn_forward", "gpa_gdn_backward", "gpa_decode_step"):
         assert expected in names
 
 
@@ -54,6 +54,12 @@ def test_ctypes_structs_match_c_layout():
     assert ctypes.sizeof(_lib.Saved) == 15 * 8
     assert ctypes.sizeof(_lib.Grads) == 32 + 7 * 8 + 5 * 32 + 8
     assert ctypes.sizeof(_lib.Timing) == 5 * 8 + 8
+    assert ctypes.sizeof(_lib.DecodeState) == 16
+    # slots (+pad), 7 parameter pointers, 5 states, 3 output pointers
+    assert ctypes.sizeof(_lib.DecodeLevel) == 8 + 7 * 8 + 5 * 16 + 3 * 8
+    # 7 int32 + 3 float, 4 operands, 8 pointers, 4 levels, 12 states, 12 pointers
+    assert _lib.DecodeProblem.level.offset == 40 + 4 * 32 + 8 * 8
+    assert ctypes.sizeof(_lib.DecodeProblem) == 232 + 4 * 168 + 12 * 16 + 12 * 8
 
 
 def test_backend_refuses_cpu_tensors():
