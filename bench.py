@@ -8,11 +8,15 @@ before the timed region.
 
     python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu]
 
-Prints ONE JSON line.  `value` is tokens/s of the whole job; `roofline` is the
-dominant kernel's achieved rate against the bf16 MFMA peak (algorithmic FLOP
-per launch / average launch time, timed with HIP events on the launch stream);
-`step_roofline` is the same for the whole step; `cpu_baseline` times the CPU
-oracle (the reference's per-token torch algorithm) on a bounded sample.
+Prints ONE JSON line.  `value` is tokens/s of the whole job over the timed
+steps (independent scans overlap on side streams).  `roofline` is the dominant
+kernel's achieved rate against the bf16 MFMA peak: algorithmic FLOP per launch
+/ average launch time, timed with HIP events on the launch stream during one
+extra step in which the schedule runs on one stream (no kernel overlaps
+another, so the interval is the kernel's own run time and agrees with a rocprof
+kernel trace of that step).  `step_roofline` is the whole step's algorithmic
+FLOP over the timed step time; `cpu_baseline` times the CPU oracle (the
+reference's per-token torch algorithm) on a bounded sample.
 """
 from __future__ import annotations
 
@@ -30,6 +34,12 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 METRIC = "GPA attn fwd+bwd tokens/s @T=8192 bf16; decode tok/s; % of roofline"
 SHAPE = dict(heads=16, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64)
+# HBM bytes per launch of a kernel in this workload, from rocprofv3 FETCH_SIZE
+# (x2.0) and WRITE_SIZE (x1.0) passes calibrated on a 1 GiB copy
+# (profiles/dense_gpa_layer_T8192_pmc_traffic.md).  Used for `roofline.traffic`
+# when that kernel is the dominant one.
+MEASURED_TRAFFIC = {"gdn_state_bwd_mfma<128>": (303177.3 * 2.0 + 239238.7) * 1024,
+                    "gdn_chunk_bwd_mfma<bf16,128>": (368116.2 * 2.0 + 212254.3) * 1024}
 BATCH, TOKENS = 1, 8192
 
 
@@ -100,7 +110,7 @@ def main() -> int:
 
     import torch
 
-    from gpa_amd import DenseGPA, GPAConfig, profiling
+    from gpa_amd import DenseGPA, GPAConfig, profiling, schedule
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
@@ -121,14 +131,25 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    with profiling.kernel_timer() as timer:
-        start = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - start
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
     ms = elapsed / args.steps * 1e3
     tokens_per_s = BATCH * TOKENS * args.steps / elapsed
+
+    # Kernel roofline: one more step with the schedule on one stream, so that
+    # each kernel's HIP-event interval is its own run time (with side streams a
+    # big-grid kernel also waits for CUs held by its neighbours).  The idle gap
+    # before it marks the step in a rocprof kernel trace
+    # (`python -m gpa_amd.profiling trace <kernel_trace.csv>` summarises it).
+    time.sleep(0.3)
+    with schedule.one_stream(), profiling.kernel_timer() as timer:
+        serial_start = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        serial_ms = (time.perf_counter() - serial_start) * 1e3
 
     flop_step = 3 * f_forward_per_token_head(dk, dv, SHAPE["slots"], SHAPE["chunk_size"]) * BATCH * TOKENS * h
     step_tflops = flop_step / (ms * 1e-3) / 1e12
@@ -137,8 +158,10 @@ def main() -> int:
     if dominant is not None:
         roofline = {"bound": "mfma", "kernel": dominant["name"], "achieved": dominant["tflops"],
                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": dominant["tflops"] / PEAK_BF16_TFLOPS,
-                    "traffic": None, "avg_launch_us": dominant["avg_us"], "launches": dominant["launches"],
-                    "share_of_step": dominant["total_ms"] / (ms * args.steps)}
+                    "traffic": MEASURED_TRAFFIC.get(dominant["name"]),
+                    "avg_launch_us": dominant["avg_us"], "launches": dominant["launches"],
+                    "share_of_step": dominant["total_ms"] / serial_ms,
+                    "timed_in": f"one extra step on one stream ({serial_ms:.1f} ms)"}
     result = {
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",

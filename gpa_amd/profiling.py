@@ -139,3 +139,98 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     name = "gdn_chunk_bwd_mfma" if mfma_chunk else "gdn_chunk_bwd"
     kernels.append((f"{name}<{e},{km}>", chunk * tokens))
     return _active.timing(kernels)
+
+
+def summarize_trace(path: str, gap_ms: float = 100.0, top: int = 25) -> str:
+    """Markdown summary of a rocprofv3 `--kernel-trace --output-format csv`
+    kernel trace: per-kernel calls, total and average duration over the whole
+    run, and over the dispatches after the last idle gap of at least `gap_ms`
+    (bench.py leaves such a gap before its single-stream timing step)."""
+    import csv
+
+    with open(path, newline="") as f:
+        rows = list(csv.DictReader(f))
+    recs = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in rows)
+    if not recs:
+        return "(empty trace)\n"
+    cut, last_end = 0, recs[0][1]
+    for i, (b, e, _) in enumerate(recs[1:], 1):
+        if b - last_end >= gap_ms * 1e6:
+            cut = i
+        last_end = max(last_end, e)
+
+    def short(name: str) -> str:
+        name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+        depth = 0
+        for i, ch in enumerate(name):
+            depth += ch == "<"
+            depth -= ch == ">"
+            if ch == "(" and depth == 0:
+                name = name[:i]
+                break
+        return name if len(name) <= 90 else name[:87] + "..."
+
+    def table(part, title):
+        stats: dict = {}
+        for b, e, n in part:
+            c, t = stats.get(short(n), (0, 0))
+            stats[short(n)] = (c + 1, t + (e - b))
+        span = (max(e for _, e, _ in part) - min(b for b, _, _ in part)) / 1e6
+        total = sum(t for _, t in stats.values())
+        lines = [f"### {title}", "",
+                 f"{len(part)} dispatches, {len(stats)} kernels, {total / 1e6:.2f} ms kernel time "
+                 f"in a {span:.2f} ms span.", "",
+                 "| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
+        for n, (c, t) in sorted(stats.items(), key=lambda kv: -kv[1][1])[:top]:
+            lines.append(f"| `{n}` | {c} | {t / 1e6:.2f} | {t / c / 1e3:.1f} | {100 * t / total:.2f} |")
+        return "\n".join(lines) + "\n"
+
+    out = table(recs, "Whole run")
+    if cut:
+        out += "\n" + table(recs[cut:], f"After the last idle gap of at least {gap_ms:g} ms")
+    return out
+
+
+def summarize_counters(path: str) -> str:
+    """Markdown table of a rocprofv3 `--pmc` counter_collection.csv: per kernel
+    and counter, the dispatch count and the mean value per dispatch."""
+    import csv
+
+    stats: dict = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            key = (r["Kernel_Name"].split("(")[0].replace("void ", "").replace("(anonymous namespace)::", ""),
+                   r["Counter_Name"])
+            c, t = stats.get(key, (0, 0.0))
+            stats[key] = (c + 1, t + float(r["Counter_Value"]))
+    lines = ["| kernel | counter | dispatches | mean per dispatch |", "|---|---|---:|---:|"]
+    for (n, ctr), (c, t) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"| `{n[:90]}` | {ctr} | {c} | {t / c:.1f} |")
+    return "\n".join(lines) + "\n"
+
+
+def copy_kernel(nbytes: int, reps: int = 3) -> None:
+    """A plain device copy of `nbytes` (reads and writes that many bytes per
+    launch): the calibration kernel for FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    x = torch.ones(nbytes // 4, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(f"copied {nbytes} bytes x {reps}", flush=True)
+
+
+if __name__ == "__main__":
+    import sys
+
+    cmd, arg = sys.argv[1], sys.argv[2]
+    if cmd == "trace":
+        print(summarize_trace(arg))
+    elif cmd == "counters":
+        print(summarize_counters(arg))
+    elif cmd == "copy":
+        copy_kernel(int(arg))
+    else:
+        raise SystemExit("usage: python -m gpa_amd.profiling trace|counters <csv> | copy <bytes>")

@@ -21,6 +21,7 @@ to the activation dtype where the reference rounds.  There is no CPU path.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -34,6 +35,19 @@ from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 _F32 = torch.float32
 _LANES = 4          # side streams for independent scans (the device has 4 hardware queues per process)
 _STREAMS: dict = {}
+_SERIAL = [False]   # set by `one_stream()`
+
+
+@contextlib.contextmanager
+def one_stream():
+    """Run every job of the schedule in order on the current stream, so that no
+    two kernels overlap (used to time kernels one at a time)."""
+    before = _SERIAL[0]
+    _SERIAL[0] = True
+    try:
+        yield
+    finally:
+        _SERIAL[0] = before
 
 
 def _side_streams(device) -> list:
@@ -63,7 +77,7 @@ def _concurrent(jobs):
     memory to another stream early.  Autograd runs each job's backward on the
     job's stream, so the backward scans overlap the same way.  During a graph
     capture the jobs run in order on the capturing stream."""
-    if torch.cuda.is_current_stream_capturing():
+    if _SERIAL[0] or torch.cuda.is_current_stream_capturing():
         # Inside a HIP graph capture everything stays on the capturing stream
         # (no cross-stream fork/join, no allocator stream records).
         return [fn() for fn, _ in jobs]
