@@ -2,14 +2,12 @@
 
 Field names, defaults and the `ValueError` contract mirror the reference
 `GPAConfig` (src/gpa/attention.py:17-75) so that configurations and
-checkpoints move between the two packages unchanged.  Two differences are
-deliberate:
-
-* `backend` defaults to and only accepts ``"hip"``.  The ``torch``/``fla``
-  backends belong to the reference package; this package is the gfx950
-  backend that drops in beside them.
-* The HIP backend is a chunk backend (like the reference's ``fla`` rule at
-  attention.py:74-75): ``chunk_size`` must be > 1.
+checkpoints move between the two packages unchanged.  One difference is
+deliberate: `backend` defaults to and only accepts ``"hip"``.  The
+``torch``/``fla`` backends belong to the reference package; this package is the
+gfx950 backend that drops in beside them.  As in the reference,
+``chunk_size == 1`` selects the tokenwise model (attention.py:264-297) and
+``chunk_size > 1`` the block-lagged chunk model.
 
 `execution` is accepted for API compatibility and ignored: every reference
 schedule (reference/packed/triton/staged) computes the same function
@@ -81,8 +79,6 @@ class GPAConfig:
             (self.read_scale > 0, "read_scale must be positive"),
             (not self.shared_query_center or self.query_scale > 0,
              "shared query-center parameterization needs query_scale > 0"),
-            (self.chunk_size > 1,
-             "the HIP backend is a chunk backend: select chunk_size > 1"),
         )
         for ok, message in checks:
             if not ok:

@@ -161,9 +161,12 @@ class DenseGPA(nn.Module):
         if position_ids.shape not in ((q.shape[1],), (q.shape[0], q.shape[1])):
             raise ValueError("position_ids must be [T] or [B,T]")
         from .decode import decode_step, decode_supported
-        from .schedule import run_segment
+        from .schedule import run_segment, run_tokens
         if q.shape[1] == 0:
             out, new_state, routes = v.new_empty(v.shape), state, None
+        elif cfg.chunk_size == 1:
+            out, new_state, routes = run_tokens(self, q, k, v, state, control_input,
+                                                want_routes=return_diagnostics)
         elif not return_diagnostics and decode_supported(self, q, k, v, state, control_input):
             (out, new_state), routes = decode_step(self, q, k, v, state), None
         else:

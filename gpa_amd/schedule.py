@@ -218,6 +218,73 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     return out, new_state, (tuple(routes) if want_routes else None)
 
 
+def run_tokens(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, control: Tensor | None, *,
+               want_routes: bool = False):
+    """The tokenwise model (`chunk_size == 1`, attention.py:264-297, the loop at
+    :385-393).  Each token passes through every level with the updated states:
+    the write reads the updated inner state, the residuals use the updated
+    inner and outer states, the relation scans and the route reader follow,
+    and each level's output reads its updated outer state.  Every GDN step is
+    the HIP scan at chunk length 1; the glue is the device code of the chunk
+    schedule on one-token views."""
+    cfg = model.config
+    _lib.require_device(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("backend='hip' computes in float32 or bfloat16 activations")
+    if cfg.positional_mode == "moments":
+        raise ValueError("positional_mode='moments' is not built for backend='hip'")
+    outs, routes = [], []
+    for t in range(q.shape[1]):
+        ctl = control[:, t:t + 1] if control is not None else None
+        out, state, r = _token(model, q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], state, ctl)
+        outs.append(out)
+        routes.append(r)
+    routes = tuple(torch.cat(r, 1) for r in zip(*routes)) if want_routes else None
+    return torch.cat(outs, 1), state, routes
+
+
+def _read(x: Tensor, s: Tensor) -> Tensor:
+    """u(x)^T S for one token: x [B,1,H,K], S [B,H,K,V] -> [B,1,H,V] in x's
+    dtype (ops.py:44-46)."""
+    return torch.einsum("bthk,bhkv->bthv", _unit(x).float(), s.float()).to(x.dtype)
+
+
+def _token(model, q, k, v, state: GPAState, control):
+    """One token of the tokenwise model (attention.py:264-297), on [B,1,H,.] views."""
+    cfg = model.config
+    dtype = q.dtype
+    step = dict(chunk=1, offset=0)
+    key, value = k, v
+    new_levels, writes, logits = [], [], []
+    for j, old in enumerate(state.levels):
+        slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
+        g_in, b_in, g_out, b_out = _gates(model, key, j, control)
+        (raw, _, a), (_, _, b) = _concurrent([
+            (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **step),
+             (q, key, slot, g_in, b_in, old.inner)),
+            (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **step),
+             (slot, value, g_out, b_out, old.outer))])
+        write = _assignment(cfg, slot)
+        if write is None:
+            write = _read(key, a).softmax(-1)
+        count = old.count + write[:, 0].to(old.count.dtype)
+        logits.append(_base_logits(model, raw, count[:, None], j))
+        writes.append(write)
+        new_levels.append(LevelState(a, b, count, None))
+        rk = torch.einsum("bhdm,bthm->bthd", a, write.float())
+        rv = torch.einsum("bthm,bhmv->bthv", write.float(), b)
+        key, value = _residual(model, key, value, rk, rv, j)
+    local = [lg.softmax(-1).to(dtype) for lg in logits]
+    incoming, relations = _relations(model, local, writes, state.relations, step)
+    routes, queries = _bridge(model, q, logits, incoming, [lv.count[:, None] for lv in new_levels])
+    weights = model.output_logits.softmax(0)
+    out = 0
+    for j, qo in enumerate(queries):
+        out = out + weights[j][..., None] * _read(qo, new_levels[j].outer)
+    new = GPAState(tuple(new_levels), relations, state.position + 1, cfg.chunk_size)
+    return out.to(v.dtype), new, routes
+
+
 # --------------------------------------------------------------------------- glue
 def _cumsum_tokens(x: Tensor) -> Tensor:
     """Cumulative sum over tokens of a [B,T,H,M] tensor, scanned along the

@@ -44,7 +44,6 @@ class Case:
     def build(self):
         """Seeded model and inputs, drawn in the fixture script's RNG order."""
         cfg = dict(self.cfg)
-        cfg["chunk_size"] = max(2, cfg["chunk_size"])  # params do not depend on it
         torch.manual_seed(self.seed)
         model = DenseGPA(GPAConfig(**cfg))
         if self.dtype == torch.float64:

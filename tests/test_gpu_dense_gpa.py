@@ -62,6 +62,12 @@ CONFIGS = {
                     b=1, t=130),
     "c3_dims": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64),
                     b=1, t=130, normalize_k=True),
+    # the tokenwise model (chunk_size 1)
+    "tokenwise": dict(cfg=dict(heads=2, key_dim=16, value_dim=8, slots=(6, 4, 5), chunk_size=1), b=2, t=8),
+    "tokenwise_lm": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1, control_dim=5,
+                                  rsa_update=True, paper_product_read=True, shared_query_center=True,
+                                  balanced_bridge=True, relation_marginal=True, read_scale=8., beta_init=.6,
+                                  decay_init=1e-4), b=1, t=4, gate_noise=.1, control_dim=5),
 }
 
 
@@ -86,7 +92,7 @@ def _run_both(name, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
-    if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "tiny_unequal_c3", "lm_flags"):
+    if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "tiny_unequal_c3", "lm_flags", "tokenwise"):
         pytest.skip("bf16 covered on the configuration-shaped cases")
     tol = TOL[dtype]
     (hm, xs, c_hip, out, state), (rm, rs, c_ref, ref_out, ref_state) = _run_both(name, dtype)
@@ -111,7 +117,7 @@ def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("name", ["tiny_unequal_c3", "c2_dims"])
+@pytest.mark.parametrize("name", ["tiny_unequal_c3", "c2_dims", "tokenwise"])
 def test_cached_partitions_and_decode_match_oracle(name):
     spec = CONFIGS[name]
     model, q, k, v, ctrl = _setup(spec["cfg"], spec["b"], spec["t"], torch.float32, seed=9)

@@ -10,7 +10,7 @@ from gpa_amd import DenseGPA, GPAConfig, _lib
 
 
 @pytest.mark.parametrize("bad", [
-    dict(heads=0), dict(chunk_size=1), dict(backend="torch"), dict(backend="fla"), dict(slots=()),
+    dict(heads=0), dict(chunk_size=0), dict(backend="torch"), dict(backend="fla"), dict(slots=()),
     dict(slots=(4, 0)), dict(positional_mode="x"), dict(beta_init=.95), dict(relation_beta_init=1.),
     dict(decay_init=0.), dict(execution="fast"), dict(read_scale=0.), dict(relation_marginal=True),
     dict(slot_feature="relu"), dict(control_dim=-1), dict(positional_mode="moments", key_dim=5),
