@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -75,6 +75,26 @@ class DecodeProblem(ctypes.Structure):
                 ("relation_out", c_vp * DECODE_MAX_EDGES)]
 
 
+ROUTE_MAX_WIDTH = 256
+ROUTE_MAX_INCOMING = 3
+ROUTE_ROWS = 32
+
+
+class RouteProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "slots", "key_dim", "incoming", "dtype")] + \
+               [("query_scale", ctypes.c_float), ("base", Operand), ("msg", Operand * ROUTE_MAX_INCOMING),
+                ("q", Operand)] + \
+               [(n, c_vp) for n in ("edge_weight", "gain", "mlp_gain", "up_t", "down_t", "rs_t", "qs_t",
+                                    "up", "down", "rs", "qs")] + \
+               [("qo", Operand), ("route", Operand)] + [(n, c_vp) for n in ("r0", "h1", "hd")]
+
+
+class RouteGrads(ctypes.Structure):
+    _fields_ = [(n, Operand) for n in ("dqo", "droute", "dbase")] + \
+               [("dmsg", Operand * ROUTE_MAX_INCOMING), ("dq", Operand)] + \
+               [(n, c_vp) for n in ("dh1", "dhd", "dqs", "partials")]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -85,6 +105,10 @@ EXPORTS = {
     "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads),
                           ctypes.POINTER(Timing), c_vp], ctypes.c_int),
     "gpa_decode_step": ([ctypes.POINTER(DecodeProblem), c_vp], ctypes.c_int),
+    "gpa_route_forward": ([ctypes.POINTER(RouteProblem), c_vp], ctypes.c_int),
+    "gpa_route_backward": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp], ctypes.c_int),
+    "gpa_route_weight_grads": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp, c_vp, c_vp,
+                                c_vp, c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -1,0 +1,659 @@
+// Route reader of one target level: forward, backward and weight gradients of
+// the default read of the reference's _bridge (src/gpa/attention.py:225-262,
+// legacy branch :236-240; the closed form of packed.py:16-35).
+//
+// A workgroup owns 32 token rows of one head.  Row phases (8 threads per
+// row) do the per-row softmax and normalisation work; the four products per
+// row tile (r0 U, gelu(h1) D, r1 W_rs, q W_qs in the forward; their
+// transposes in the backward) run as 32x32 output tiles on MFMA, A rows from
+// LDS and B rows from the padded weight matrices (L2-resident, shared by all
+// row tiles of a head).  Every product rounds its operands and result to the
+// activation type and accumulates in float32, as the reference's typed
+// einsums do; the gradients round where the reference's bf16 tensors do.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "mfma_tiles.h"
+
+namespace gpa {
+namespace {
+
+constexpr int RR = GPA_ROUTE_ROWS;  // token rows per workgroup
+constexpr int RW = 4;               // waves per workgroup
+constexpr int RNT = 64 * RW;
+constexpr int RMAX = GPA_ROUTE_MAX_WIDTH;
+constexpr int RPER = RMAX / 8;      // columns per thread in a row phase (8 threads per row)
+constexpr int RTMAX = RMAX / 32 / RW;  // M-column tiles per wave (at most)
+
+__host__ __device__ constexpr int pad16(int x) { return (x + 15) & ~15; }
+__host__ __device__ constexpr int pad32(int x) { return (x + 31) & ~31; }
+
+template <typename E> struct Wt;
+template <> struct Wt<float> { using type = float; };
+template <> struct Wt<bf16_t> { using type = bf16_t; };
+
+// acc += A[32][K] B, A rows in LDS (already in the activation type's values,
+// zero beyond K up to k16), B given as rows bt[n0 + c][0..k16) (zero padded).
+__device__ __forceinline__ void tile_gemm(f32x16& acc, const float* a, int lda, const bf16_t* bt, int ldb,
+                                          int k16, int n0, int lane) {
+  const float* ar = a + (lane & 31) * lda + 8 * (lane >> 5);
+  const bf16_t* br = bt + (int64_t)(n0 + (lane & 31)) * ldb + 8 * (lane >> 5);
+  for (int k0 = 0; k0 < k16; k0 += 16) {
+    const bf16x8 av = pack8(ar + k0);
+    const bf16x8 bv = *reinterpret_cast<const bf16x8*>(br + k0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+  }
+}
+__device__ __forceinline__ void tile_gemm(f32x16& acc, const float* a, int lda, const float* bt, int ldb, int k16,
+                                          int n0, int lane) {
+  const float* ar = a + (lane & 31) * lda + 4 * (lane >> 5);
+  const float* br = bt + (int64_t)(n0 + (lane & 31)) * ldb + 4 * (lane >> 5);
+  for (int k0 = 0; k0 < k16; k0 += 8)
+    mma8(acc, *reinterpret_cast<const f32x4*>(ar + k0), *reinterpret_cast<const f32x4*>(br + k0));
+}
+
+__device__ __forceinline__ float sum8(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  return x + __shfl_xor(x, 4);
+}
+__device__ __forceinline__ float max8(float x) {
+  x = fmaxf(x, __shfl_xor(x, 1));
+  x = fmaxf(x, __shfl_xor(x, 2));
+  return fmaxf(x, __shfl_xor(x, 4));
+}
+
+__device__ __forceinline__ float gelu(float x) { return .5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_grad(float x) {
+  return .5f * (1.f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-.5f * x * x);
+}
+
+struct Rows {
+  int tokens, heads;
+  __device__ __forceinline__ int64_t at(const gpa_operand& o, int r, int h) const {
+    return (int64_t)(r / tokens) * o.sb + (int64_t)(r % tokens) * o.st + (int64_t)h * o.sh;
+  }
+};
+
+// Relation read and softmax of one row (8 threads, columns part + 8 i):
+// returns base' = base + gain tanh z in v[], and fills z[] / inc[] when asked.
+template <typename E>
+__device__ __forceinline__ void row_base(const gpa_route_problem& p, const Rows& rows, int r, int h, int part,
+                                         float (&v)[RPER], float (&z)[RPER], float& inv_sig) {
+  const int M = p.slots;
+  const float* base = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, r, h);
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = part + 8 * i;
+    v[i] = m < M ? base[m] : 0.f;
+    z[i] = 0.f;
+  }
+  inv_sig = 0.f;
+  if (p.incoming == 0) return;
+  for (int e = 0; e < p.incoming; ++e) {
+    const float w = p.edge_weight[e * p.heads + h];
+    const E* msg = reinterpret_cast<const E*>(p.msg[e].ptr) + rows.at(p.msg[e], r, h);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = part + 8 * i;
+      if (m < M) z[i] += w * to_f32(msg[m]);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) s += z[i];
+  const float mean = sum8(s) / M;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = part + 8 * i;
+    z[i] = m < M ? z[i] - mean : 0.f;
+    q += z[i] * z[i];
+  }
+  const float sig = sqrtf(sum8(q) / M + 1e-5f);
+  inv_sig = 1.f / sig;
+  const float gain = p.gain[h];
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    z[i] = z[i] / sig;
+    v[i] += gain * tanhf(z[i]);
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void row_softmax(int M, int part, const float (&v)[RPER], float (&pr)[RPER]) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i)
+    if (part + 8 * i < M) mx = fmaxf(mx, v[i]);
+  mx = max8(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    pr[i] = part + 8 * i < M ? __expf(v[i] - mx) : 0.f;
+    s += pr[i];
+  }
+  s = sum8(s);
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) pr[i] /= s;
+}
+
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
+  using W = typename Wt<E>::type;
+  HIP_DYNAMIC_SHARED(float, lds)
+  const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens;
+  const int h = blockIdx.y, row0 = blockIdx.x * RR;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kM = pad16(M), k2M = pad16(2 * M), kD = pad16(Dk);
+  const int lda = kM + 4, ldh = (k2M > kD ? k2M : kD) + 4;
+  float* A = lds;             // r0, then r1        [RR][lda]
+  float* Hs = lds + RR * lda; // gelu(h1), then q   [RR][ldh]
+  const Rows rows{p.tokens, p.heads};
+  E* sr0 = reinterpret_cast<E*>(p.r0) + (int64_t)h * R * M;
+  E* sh1 = reinterpret_cast<E*>(p.h1) + (int64_t)h * R * 2 * M;
+  E* shd = reinterpret_cast<E*>(p.hd) + (int64_t)h * R * M;
+
+  // ---- r0 = softmax(base + gain tanh z)
+  {
+    const int row = tid >> 3, part = tid & 7, r = row0 + row;
+    const bool valid = r < R;
+    float v[RPER], z[RPER], pr[RPER], inv;
+    row_base<E>(p, rows, valid ? r : R - 1, h, part, v, z, inv);
+    row_softmax<E>(M, part, v, pr);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = part + 8 * i;
+      if (m < kM) {
+        const float x = (valid && m < M) ? round_as<E>(pr[i]) : 0.f;
+        A[row * lda + m] = x;
+        if (valid && m < M) sr0[(int64_t)r * M + m] = from_f32<E>(x);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- h1 = r0 U, gelu(h1) -> Hs
+  {
+    const W* ut = reinterpret_cast<const W*>(p.up_t) + (int64_t)h * pad32(2 * M) * kM;
+    for (int t = wave; t < pad32(2 * M) / 32; t += RW) {
+      f32x16 acc = {};
+      tile_gemm(acc, A, lda, ut, kM, kM, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < 2 * M) {
+          const float h1 = round_as<E>(acc[i]);
+          if (r < R) sh1[(int64_t)r * 2 * M + col] = from_f32<E>(h1);
+          Hs[row * ldh + col] = round_as<E>(gelu(h1));
+        } else if (col < k2M) {
+          Hs[row * ldh + col] = 0.f;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- hd = gelu(h1) D, r1 = r0 + mlp_gain hd -> A and the route output
+  {
+    const W* dt = reinterpret_cast<const W*>(p.down_t) + (int64_t)h * pad32(M) * k2M;
+    const float g = p.mlp_gain[h];
+    E* route = reinterpret_cast<E*>(p.route.ptr);
+    for (int t = wave; t < pad32(M) / 32; t += RW) {
+      f32x16 acc = {};
+      tile_gemm(acc, Hs, ldh, dt, k2M, k2M, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < M) {
+          const float hd = round_as<E>(acc[i]);
+          const float r1 = round_as<E>(A[row * lda + col] + g * hd);
+          A[row * lda + col] = r1;
+          if (r < R) {
+            shd[(int64_t)r * M + col] = from_f32<E>(hd);
+            route[rows.at(p.route, r, h) + col] = from_f32<E>(r1);
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- q -> Hs
+  {
+    const int row = tid >> 3, part = tid & 7, r = row0 + row;
+    const bool valid = r < R;
+    const E* q = reinterpret_cast<const E*>(p.q.ptr) + rows.at(p.q, valid ? r : R - 1, h);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int d = part + 8 * i;
+      if (d < kD) Hs[row * ldh + d] = (valid && d < Dk) ? to_f32(q[d]) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- qo = r1 W_rs + query_scale (q W_qs)
+  {
+    const W* rt = reinterpret_cast<const W*>(p.rs_t) + (int64_t)h * pad32(M) * kM;
+    const W* qt = reinterpret_cast<const W*>(p.qs_t) + (int64_t)h * pad32(M) * kD;
+    E* qo = reinterpret_cast<E*>(p.qo.ptr);
+    for (int t = wave; t < pad32(M) / 32; t += RW) {
+      f32x16 a3 = {}, a4 = {};
+      tile_gemm(a3, A, lda, rt, kM, kM, 32 * t, lane);
+      tile_gemm(a4, Hs, ldh, qt, kD, kD, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < M && r < R) {
+          const float dir = round_as<E>(p.query_scale * round_as<E>(a4[i]));
+          qo[rows.at(p.qo, r, h) + col] = from_f32<E>(round_as<E>(round_as<E>(a3[i]) + dir));
+        }
+      }
+    }
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_grads g) {
+  using W = typename Wt<E>::type;
+  HIP_DYNAMIC_SHARED(float, lds)
+  __shared__ float red[RW][2 + GPA_ROUTE_MAX_INCOMING];
+  const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens, H = p.heads, NI = p.incoming;
+  const int h = blockIdx.y, row0 = blockIdx.x * RR;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kM = pad16(M), k2M = pad16(2 * M);
+  const int lda = kM + 4, ldh = k2M + 4;
+  float* G = lds;                // dqo, then round(qs dqo)   [RR][lda]
+  float* A2 = lds + RR * lda;    // d hd, then d r0           [RR][lda]
+  float* H2 = A2 + RR * lda;     // d h1                      [RR][ldh]
+  const Rows rows{p.tokens, p.heads};
+  const E* sh1 = reinterpret_cast<const E*>(p.h1) + (int64_t)h * R * 2 * M;
+  const E* shd = reinterpret_cast<const E*>(p.hd) + (int64_t)h * R * M;
+  E* gdh1 = reinterpret_cast<E*>(g.dh1) + (int64_t)h * R * 2 * M;
+  E* gdhd = reinterpret_cast<E*>(g.dhd) + (int64_t)h * R * M;
+  E* gdqs = reinterpret_cast<E*>(g.dqs) + (int64_t)h * R * M;
+  float part_mg = 0.f, part_gain = 0.f, part_w[GPA_ROUTE_MAX_INCOMING] = {0.f, 0.f, 0.f};
+
+  // ---- dqo -> G
+  {
+    const int row = tid >> 3, part = tid & 7, r = row0 + row;
+    const bool valid = r < R;
+    const E* dqo = reinterpret_cast<const E*>(g.dqo.ptr) + rows.at(g.dqo, valid ? r : R - 1, h);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = part + 8 * i;
+      if (m < kM) G[row * lda + m] = (valid && m < M) ? to_f32(dqo[m]) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- d r1 = dqo W_rs^T (+ d route); d hd = mlp_gain d r1 -> A2
+  f32x16 dr1[RTMAX];
+  {
+    const W* rs = reinterpret_cast<const W*>(p.rs) + (int64_t)h * pad32(M) * kM;
+    const float gm = p.mlp_gain[h];
+    const E* droute = reinterpret_cast<const E*>(g.droute.ptr);
+#pragma unroll
+    for (int s = 0; s < RTMAX; ++s) {
+      const int t = wave + RW * s;
+      dr1[s] = f32x16{};
+      if (t >= pad32(M) / 32) continue;
+      f32x16 acc = {};
+      tile_gemm(acc, G, lda, rs, kM, kM, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < M) {
+          float d = round_as<E>(acc[i]);
+          if (droute && r < R) d = round_as<E>(d + to_f32(droute[rows.at(g.droute, r, h) + col]));
+          if (r >= R) d = 0.f;
+          dr1[s][i] = d;
+          const float dhd = round_as<E>(gm * d);
+          A2[row * lda + col] = dhd;
+          if (r < R) {
+            part_mg += d * to_f32(shd[(int64_t)r * M + col]);
+            gdhd[(int64_t)r * M + col] = from_f32<E>(dhd);
+          }
+        } else if (col < kM) {
+          A2[row * lda + col] = 0.f;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- G <- round(query_scale dqo) (the gradient of q W_qs)
+  {
+    const int row = tid >> 3, part = tid & 7, r = row0 + row;
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = part + 8 * i;
+      if (m < M) {
+        const float x = round_as<E>(p.query_scale * G[row * lda + m]);
+        G[row * lda + m] = x;
+        if (r < R) gdqs[(int64_t)r * M + m] = from_f32<E>(x);
+      }
+    }
+  }
+
+  // ---- d h1 = (d hd D^T) gelu'(h1) -> H2
+  {
+    const W* down = reinterpret_cast<const W*>(p.down) + (int64_t)h * pad32(2 * M) * kM;
+    for (int t = wave; t < pad32(2 * M) / 32; t += RW) {
+      f32x16 acc = {};
+      tile_gemm(acc, A2, lda, down, kM, kM, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < 2 * M) {
+          float d = 0.f;
+          if (r < R) {
+            const float x = to_f32(sh1[(int64_t)r * 2 * M + col]);
+            d = round_as<E>(round_as<E>(acc[i]) * gelu_grad(x));
+            gdh1[(int64_t)r * 2 * M + col] = from_f32<E>(d);
+          }
+          H2[row * ldh + col] = d;
+        } else if (col < k2M) {
+          H2[row * ldh + col] = 0.f;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- d r0 = d r1 + d h1 U^T -> A2;  d q = round(qs dqo) W_qs^T
+  {
+    const W* up = reinterpret_cast<const W*>(p.up) + (int64_t)h * pad32(M) * k2M;
+#pragma unroll
+    for (int s = 0; s < RTMAX; ++s) {
+      const int t = wave + RW * s;
+      if (t >= pad32(M) / 32) continue;
+      f32x16 acc = {};
+      tile_gemm(acc, H2, ldh, up, k2M, k2M, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31);
+        if (col < M) A2[row * lda + col] = round_as<E>(dr1[s][i] + round_as<E>(acc[i]));
+      }
+    }
+    const W* qs = reinterpret_cast<const W*>(p.qs) + (int64_t)h * pad32(Dk) * kM;
+    E* dq = reinterpret_cast<E*>(g.dq.ptr);
+    for (int t = wave; t < pad32(Dk) / 32; t += RW) {
+      f32x16 acc = {};
+      tile_gemm(acc, G, lda, qs, kM, kM, 32 * t, lane);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < Dk && r < R) dq[rows.at(g.dq, r, h) + col] = from_f32<E>(round_as<E>(acc[i]));
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax and relation-read backward of each row
+  {
+    const int row = tid >> 3, part = tid & 7, r = row0 + row;
+    const bool valid = r < R;
+    const int rc = valid ? r : R - 1;
+    float v[RPER], z[RPER], pr[RPER], inv;
+    row_base<E>(p, rows, rc, h, part, v, z, inv);
+    row_softmax<E>(M, part, v, pr);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPER; ++i)
+      if (part + 8 * i < M) s += pr[i] * A2[row * lda + part + 8 * i];
+    s = sum8(s);
+    float* dbase = reinterpret_cast<float*>(g.dbase.ptr) + rows.at(g.dbase, rc, h);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = part + 8 * i;
+      // d base' (the softmax input) overwrites v
+      v[i] = m < M ? pr[i] * (A2[row * lda + m] - s) : 0.f;
+      if (valid && m < M) dbase[m] = v[i];
+    }
+    if (NI > 0) {
+      const float gain = p.gain[h];
+      float dz[RPER], szz = 0.f;
+#pragma unroll
+      for (int i = 0; i < RPER; ++i) {
+        const int m = part + 8 * i;
+        const float th = tanhf(z[i]);
+        if (valid && m < M) part_gain += v[i] * th;
+        dz[i] = m < M ? gain * v[i] * (1.f - th * th) : 0.f;
+        szz += dz[i] * z[i];
+      }
+      const float mzz = sum8(szz) / M;
+      float sc = 0.f;
+#pragma unroll
+      for (int i = 0; i < RPER; ++i) {
+        dz[i] = part + 8 * i < M ? (dz[i] - z[i] * mzz) * inv : 0.f;  // d centred
+        sc += dz[i];
+      }
+      const float mc = sum8(sc) / M;
+#pragma unroll
+      for (int i = 0; i < RPER; ++i) dz[i] -= mc;  // d incoming
+      for (int e = 0; e < NI; ++e) {
+        const float w = p.edge_weight[e * H + h];
+        const E* msg = reinterpret_cast<const E*>(p.msg[e].ptr) + rows.at(p.msg[e], rc, h);
+        E* dmsg = reinterpret_cast<E*>(g.dmsg[e].ptr) + rows.at(g.dmsg[e], rc, h);
+        float sw = 0.f;
+#pragma unroll
+        for (int i = 0; i < RPER; ++i) {
+          const int m = part + 8 * i;
+          if (m < M) {
+            sw += dz[i] * to_f32(msg[m]);
+            if (valid) dmsg[m] = from_f32<E>(round_as<E>(w * dz[i]));
+          }
+        }
+        if (valid) part_w[e] += sw;
+      }
+    }
+  }
+
+  // ---- per-block sums of the scalar gradients
+  {
+    float vals[2 + GPA_ROUTE_MAX_INCOMING] = {part_mg, part_gain, part_w[0], part_w[1], part_w[2]};
+#pragma unroll
+    for (int k = 0; k < 2 + GPA_ROUTE_MAX_INCOMING; ++k) {
+      float x = vals[k];
+      for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+      if (lane == 0) red[wave][k] = x;
+    }
+    __syncthreads();
+    if (tid < 2 + NI) {
+      float x = 0.f;
+      for (int w = 0; w < RW; ++w) x += red[w][tid];
+      g.partials[((int64_t)blockIdx.x * H + h) * (2 + NI) + tid] = x;
+    }
+  }
+}
+
+// C[h][i][j] = sum_r A[h][r][i] B[h][r][j] over the R rows: one 32x32 tile of
+// C per workgroup, the rows split over its waves and the partial tiles summed
+// in LDS.  A may be mapped through round(gelu(.)) on load (d D from h1).
+struct TnOperand {
+  const void* ptr;
+  int64_t rs, hs;  // row and head strides (elements)
+  int width;
+  int gelu;
+};
+
+template <typename E>
+__device__ __forceinline__ float tn_load(const TnOperand& o, int h, int r, int c, int R) {
+  if (r >= R || c >= o.width) return 0.f;
+  const float x = to_f32(reinterpret_cast<const E*>(o.ptr)[(int64_t)h * o.hs + (int64_t)r * o.rs + c]);
+  return o.gelu ? round_as<E>(gelu(x)) : x;
+}
+
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_gemm_tn(TnOperand a, TnOperand b, float* c, int R) {
+  __shared__ float part[RW][32][33];
+  const int h = blockIdx.y, tn = (b.width + 31) / 32;
+  const int i0 = 32 * (blockIdx.x / tn), j0 = 32 * (blockIdx.x % tn);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int step = std::is_same<E, float>::value ? 8 : 16;
+  const int span = ((R + RW - 1) / RW + step - 1) / step * step;
+  const int rbeg = wave * span, rend = rbeg + span;
+  f32x16 acc = {};
+  for (int k0 = rbeg; k0 < rend; k0 += step) {
+    if constexpr (std::is_same<E, float>::value) {
+      const int k = k0 + 4 * (lane >> 5);
+      const f32x4 av{tn_load<E>(a, h, k, i0 + (lane & 31), R), tn_load<E>(a, h, k + 1, i0 + (lane & 31), R),
+                     tn_load<E>(a, h, k + 2, i0 + (lane & 31), R), tn_load<E>(a, h, k + 3, i0 + (lane & 31), R)};
+      const f32x4 bv{tn_load<E>(b, h, k, j0 + (lane & 31), R), tn_load<E>(b, h, k + 1, j0 + (lane & 31), R),
+                     tn_load<E>(b, h, k + 2, j0 + (lane & 31), R), tn_load<E>(b, h, k + 3, j0 + (lane & 31), R)};
+      mma8(acc, av, bv);
+    } else {
+      const int k = k0 + 8 * (lane >> 5);
+      float xa[8], xb[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        xa[s] = tn_load<E>(a, h, k + s, i0 + (lane & 31), R);
+        xb[s] = tn_load<E>(b, h, k + s, j0 + (lane & 31), R);
+      }
+      bf16x8 av, bv;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        av[s] = (__bf16)xa[s];
+        bv[s] = (__bf16)xb[s];
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part[wave][acc_row(i, lane >> 5)][lane & 31] = acc[i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 32 * 32; idx += RNT) {
+    const int i = idx / 32, j = idx % 32;
+    if (i0 + i < a.width && j0 + j < b.width) {
+      float x = 0.f;
+      for (int w = 0; w < RW; ++w) x += part[w][i][j];
+      c[((int64_t)h * a.width + i0 + i) * b.width + j0 + j] = round_as<E>(x);
+    }
+  }
+}
+
+int check_route(const gpa_route_problem* p) {
+  if (!p) return fail(GPA_HIP_EINVAL, "route: null problem");
+  if (p->batch < 1 || p->tokens < 1 || p->heads < 1) return fail(GPA_HIP_EINVAL, "route: empty shape");
+  if (p->slots < 1 || p->slots > RMAX || p->key_dim < 1 || p->key_dim > RMAX)
+    return fail(GPA_HIP_EUNSUPPORTED, "route: slots and key width must be in [1, 256]");
+  if (p->incoming < 0 || p->incoming > GPA_ROUTE_MAX_INCOMING)
+    return fail(GPA_HIP_EUNSUPPORTED, "route: at most 3 incoming edges");
+  if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "route: dtype");
+  if ((int64_t)p->batch * p->tokens > 0x7fffffff / 2 / GPA_ROUTE_MAX_WIDTH)
+    return fail(GPA_HIP_EUNSUPPORTED, "route: too many rows");
+  if (!p->base.ptr || !p->q.ptr || !p->gain || !p->mlp_gain || (p->incoming && !p->edge_weight))
+    return fail(GPA_HIP_EINVAL, "route: null input");
+  for (int e = 0; e < p->incoming; ++e)
+    if (!p->msg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message");
+  if (!p->r0 || !p->h1 || !p->hd) return fail(GPA_HIP_EINVAL, "route: null saved rows");
+  return GPA_HIP_OK;
+}
+
+// The stride between consecutive rows r = b*T + t of a [B,T,H,X] operand, if
+// rows are uniformly strided.
+bool row_stride(const gpa_operand& o, int batch, int tokens, int64_t& rs) {
+  if (tokens == 1) rs = o.sb;
+  else if (batch == 1 || o.sb == (int64_t)tokens * o.st) rs = o.st;
+  else return false;
+  return true;
+}
+
+size_t fwd_lds(const gpa_route_problem& p) {
+  const int kM = pad16(p.slots), k2M = pad16(2 * p.slots), kD = pad16(p.key_dim);
+  return sizeof(float) * RR * ((kM + 4) + (k2M > kD ? k2M : kD) + 4);
+}
+size_t bwd_lds(const gpa_route_problem& p) {
+  const int kM = pad16(p.slots), k2M = pad16(2 * p.slots);
+  return sizeof(float) * RR * (2 * (kM + 4) + k2M + 4);
+}
+
+template <typename K>
+int set_lds(K kernel, size_t bytes) {
+  if (bytes > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) != hipSuccess)
+    return fail(GPA_HIP_EHIP, "route: cannot raise the LDS limit");
+  return GPA_HIP_OK;
+}
+
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_route(problem)) return rc;
+  if (!problem->up_t || !problem->down_t || !problem->rs_t || !problem->qs_t || !problem->qo.ptr ||
+      !problem->route.ptr)
+    return fail(GPA_HIP_EINVAL, "route: null forward weight or output");
+  const int R = problem->batch * problem->tokens;
+  const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
+  const size_t lds = fwd_lds(*problem);
+  if (problem->dtype == GPA_DTYPE_BF16) {
+    if (int rc = set_lds(route_fwd<bf16_t>, lds)) return rc;
+    hipLaunchKernelGGL(route_fwd<bf16_t>, grid, block, lds, stream, *problem);
+  } else {
+    if (int rc = set_lds(route_fwd<float>, lds)) return rc;
+    hipLaunchKernelGGL(route_fwd<float>, grid, block, lds, stream, *problem);
+  }
+  return check_launch("gpa_route_forward");
+}
+
+extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_route_grads* grads,
+                                  hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_route(problem)) return rc;
+  if (!grads || !grads->dqo.ptr || !grads->dbase.ptr || !grads->dq.ptr || !grads->dh1 || !grads->dhd ||
+      !grads->dqs || !grads->partials || !problem->up || !problem->down || !problem->rs || !problem->qs)
+    return fail(GPA_HIP_EINVAL, "route: null gradient buffer or backward weight");
+  for (int e = 0; e < problem->incoming; ++e)
+    if (!grads->dmsg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message gradient");
+  const int R = problem->batch * problem->tokens;
+  const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
+  const size_t lds = bwd_lds(*problem);
+  if (problem->dtype == GPA_DTYPE_BF16) {
+    if (int rc = set_lds(route_bwd<bf16_t>, lds)) return rc;
+    hipLaunchKernelGGL(route_bwd<bf16_t>, grid, block, lds, stream, *problem, *grads);
+  } else {
+    if (int rc = set_lds(route_bwd<float>, lds)) return rc;
+    hipLaunchKernelGGL(route_bwd<float>, grid, block, lds, stream, *problem, *grads);
+  }
+  return check_launch("gpa_route_backward");
+}
+
+extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gpa_route_grads* grads, float* d_up,
+                                      float* d_down, float* d_rs, float* d_qs, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_route(problem)) return rc;
+  if (!grads || !grads->dqo.ptr || !grads->dh1 || !grads->dhd || !grads->dqs || !problem->route.ptr || !d_up ||
+      !d_down || !d_rs || !d_qs)
+    return fail(GPA_HIP_EINVAL, "route: null weight-gradient buffer");
+  const int M = problem->slots, Dk = problem->key_dim, R = problem->batch * problem->tokens, H = problem->heads;
+  // Rows r = b*T + t of a [B,T,H,X] operand must sit at r * (row stride).
+  int64_t rs_route, rs_dqo, rs_q;
+  if (!row_stride(problem->route, problem->batch, problem->tokens, rs_route) ||
+      !row_stride(grads->dqo, problem->batch, problem->tokens, rs_dqo) ||
+      !row_stride(problem->q, problem->batch, problem->tokens, rs_q))
+    return fail(GPA_HIP_EINVAL, "route: route, dqo and q rows must be uniformly strided");
+  const int64_t R64 = R;
+  const TnOperand r0{problem->r0, M, R64 * M, M, 0};
+  const TnOperand hid{problem->h1, 2 * M, R64 * 2 * M, 2 * M, 1};
+  const TnOperand dh1{grads->dh1, 2 * M, R64 * 2 * M, 2 * M, 0};
+  const TnOperand dhd{grads->dhd, M, R64 * M, M, 0};
+  const TnOperand dqs{grads->dqs, M, R64 * M, M, 0};
+  const TnOperand r1{problem->route.ptr, rs_route, problem->route.sh, M, 0};
+  const TnOperand dqo{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M, 0};
+  const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk, 0};
+  struct Job { TnOperand a, b; float* c; } jobs[4] = {{r0, dh1, d_up}, {hid, dhd, d_down}, {r1, dqo, d_rs},
+                                                        {q, dqs, d_qs}};
+  for (const Job& j : jobs) {
+    const dim3 grid(((j.a.width + 31) / 32) * ((j.b.width + 31) / 32), H), block(RNT);
+    if (problem->dtype == GPA_DTYPE_BF16)
+      hipLaunchKernelGGL(route_gemm_tn<bf16_t>, grid, block, 0, stream, j.a, j.b, j.c, R);
+    else
+      hipLaunchKernelGGL(route_gemm_tn<float>, grid, block, 0, stream, j.a, j.b, j.c, R);
+  }
+  return check_launch("gpa_route_weight_grads");
+}

@@ -1,0 +1,154 @@
+"""Fused route reader of one target level (`gpa_route_forward/backward`).
+
+The default read of the reference's `_bridge` (src/gpa/attention.py:225-262,
+legacy branch :236-240), for every token of every head of one target level j:
+
+    inc = sum_e w_e m_e;  z = centre(inc) / rms;  r0 = softmax(base + gain tanh z)
+    r1  = r0 + mlp_gain gelu(r0 U) D;   qo = r1 W_rs + query_scale q W_qs
+
+`route_reader` returns (qo, r1) in the activation dtype and is differentiable
+in every input: the base logits, the messages, q, the edge weights, both gains
+and the four weight matrices.  It is used by the schedule for the default
+flags (`supported`); the other read variants keep the device glue.
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def supported(cfg, dtype: torch.dtype, slots: int) -> bool:
+    return (dtype in _lib.DTYPE_CODES and not cfg.paper_product_read and not cfg.rsa_update
+            and not cfg.shared_query_center and not cfg.balanced_bridge and cfg.slot_feature == "linear"
+            and slots <= _lib.ROUTE_MAX_WIDTH and cfg.key_dim <= _lib.ROUTE_MAX_WIDTH
+            and cfg.levels - 1 <= _lib.ROUTE_MAX_INCOMING)
+
+
+def _pad(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def _pack(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
+    """[H,K,N] weight -> [H,N32,K16] rows of the contraction for each output
+    column (transpose=True), or [H,K,N] -> [H,K32,N16] (transpose=False:
+    output column = K, contraction = N); rounded to `dtype`, zero padded."""
+    w = w.detach().to(dtype)
+    if transpose:
+        w = w.transpose(1, 2)
+    h, n, k = w.shape
+    out = torch.zeros(h, _pad(n, 32), _pad(k, 16), device=w.device, dtype=dtype)
+    out[:, :n, :k] = w
+    return out
+
+
+def _operand(t: Tensor | None) -> _lib.Operand:
+    return _lib.operand(t)
+
+
+def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, saved):
+    bsz, tokens, heads, dk = q.shape
+    p = _lib.RouteProblem()
+    p.batch, p.tokens, p.heads, p.slots, p.key_dim = bsz, tokens, heads, base.shape[-1], dk
+    p.incoming, p.dtype, p.query_scale = len(msgs), _lib.DTYPE_CODES[q.dtype], float(query_scale)
+    p.base, p.q = _operand(base), _operand(q)
+    for e, m in enumerate(msgs):
+        p.msg[e] = _operand(m)
+    p.edge_weight = edge_w.data_ptr() if msgs else None
+    p.gain, p.mlp_gain = gain.data_ptr(), mlp_gain.data_ptr()
+    for name, w in weights.items():
+        setattr(p, name, w.data_ptr())
+    p.qo, p.route = _operand(outs[0]), _operand(outs[1])
+    p.r0, p.h1, p.hd = (t.data_ptr() for t in saved)
+    return p
+
+
+class _RouteReader(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs):
+        _lib.require_device(q)
+        ctx.set_materialize_grads(False)
+        lib = _lib.load()
+        dtype = q.dtype
+        bsz, tokens, heads, _ = q.shape
+        m = base.shape[-1]
+        rows = bsz * tokens
+        base = base.float().contiguous()
+        q = q.contiguous()
+        msgs = tuple(x.to(dtype).contiguous() for x in msgs)
+        edge_w = edge_w.detach().float().contiguous() if msgs else None
+        g, mg = gain.detach().float().contiguous(), mlp_gain.detach().float().contiguous()
+        weights = {"up_t": _pack(up, dtype, True), "down_t": _pack(down, dtype, True),
+                   "rs_t": _pack(rs, dtype, True), "qs_t": _pack(qs, dtype, True)}
+        qo = torch.empty(bsz, tokens, heads, m, device=q.device, dtype=dtype)
+        route = torch.empty_like(qo)
+        saved = (torch.empty(heads, rows, m, device=q.device, dtype=dtype),
+                 torch.empty(heads, rows, 2 * m, device=q.device, dtype=dtype),
+                 torch.empty(heads, rows, m, device=q.device, dtype=dtype))
+        prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved)
+        _lib.check(lib.gpa_route_forward(prob, _lib.stream_handle(q.device)), "gpa_route_forward")
+        ctx.query_scale = query_scale
+        ctx.n_in = len(msgs)
+        ctx.param_dtypes = (edge_w.dtype if msgs else None, gain.dtype, mlp_gain.dtype,
+                            up.dtype, down.dtype, rs.dtype, qs.dtype)
+        ctx.save_for_backward(base, q, edge_w if msgs else None, g, mg, up, down, rs, qs, route, *saved, *msgs)
+        return qo, route
+
+    @staticmethod
+    def backward(ctx, dqo, droute):
+        lib = _lib.load()
+        base, q, edge_w, g, mg, up, down, rs, qs, route, r0, h1, hd, *msgs = ctx.saved_tensors
+        dtype = q.dtype
+        bsz, tokens, heads, dk = q.shape
+        m = base.shape[-1]
+        rows = bsz * tokens
+        dev = q.device
+        if dqo is None:
+            dqo = torch.zeros_like(route)
+        dqo = dqo.to(dtype).contiguous()
+        droute = droute.to(dtype).contiguous() if droute is not None else None
+        weights = {"up_t": None, "down_t": None, "rs_t": None, "qs_t": None,
+                   "up": _pack(up, dtype, False), "down": _pack(down, dtype, False),
+                   "rs": _pack(rs, dtype, False), "qs": _pack(qs, dtype, False)}
+        prob = _problem(base, q, edge_w, g, mg, msgs, ctx.query_scale,
+                        {k: v for k, v in weights.items() if v is not None},
+                        (route, route), (r0, h1, hd))
+        dbase = torch.empty_like(base)
+        dmsgs = [torch.empty_like(x) for x in msgs]
+        dq = torch.empty_like(q)
+        dh1 = torch.empty(heads, rows, 2 * m, device=dev, dtype=dtype)
+        dhd = torch.empty(heads, rows, m, device=dev, dtype=dtype)
+        dqs = torch.empty(heads, rows, m, device=dev, dtype=dtype)
+        blocks = (rows + _lib.ROUTE_ROWS - 1) // _lib.ROUTE_ROWS
+        partials = torch.empty(blocks, heads, 2 + len(msgs), device=dev, dtype=torch.float32)
+        gr = _lib.RouteGrads()
+        gr.dqo, gr.droute, gr.dbase, gr.dq = (_operand(dqo), _operand(droute), _operand(dbase), _operand(dq))
+        for e, x in enumerate(dmsgs):
+            gr.dmsg[e] = _operand(x)
+        gr.dh1, gr.dhd, gr.dqs, gr.partials = dh1.data_ptr(), dhd.data_ptr(), dqs.data_ptr(), partials.data_ptr()
+        stream = _lib.stream_handle(dev)
+        _lib.check(lib.gpa_route_backward(prob, gr, stream), "gpa_route_backward")
+        d_up = torch.empty(heads, m, 2 * m, device=dev, dtype=torch.float32)
+        d_down = torch.empty(heads, 2 * m, m, device=dev, dtype=torch.float32)
+        d_rs = torch.empty(heads, m, m, device=dev, dtype=torch.float32)
+        d_qs = torch.empty(heads, dk, m, device=dev, dtype=torch.float32)
+        _lib.check(lib.gpa_route_weight_grads(prob, gr, d_up.data_ptr(), d_down.data_ptr(), d_rs.data_ptr(),
+                                              d_qs.data_ptr(), stream), "gpa_route_weight_grads")
+        sums = partials.sum(0)
+        dt = ctx.param_dtypes
+        d_edge = sums[:, 2:].t().contiguous().to(dt[0]) if msgs else None
+        return (dbase, dq, d_edge, sums[:, 1].to(dt[1]), sums[:, 0].to(dt[2]), d_up.to(dt[3]), d_down.to(dt[4]),
+                d_rs.to(dt[5]), d_qs.to(dt[6]), None, *dmsgs)
+
+
+def route_reader(base: Tensor, q: Tensor, edge_w: Tensor | None, gain: Tensor, mlp_gain: Tensor, up: Tensor,
+                 down: Tensor, rs: Tensor, qs: Tensor, query_scale: float, msgs) -> tuple[Tensor, Tensor]:
+    """(qo, route) of one target level; base [B,T,H,M] float32 logits, q
+    [B,T,H,Dk], msgs the incoming messages [B,T,H,M] in edge order with their
+    softmax weights edge_w [n_in,H]; gain, mlp_gain [H]; U [H,M,2M],
+    D [H,2M,M], W_rs [H,M,M], W_qs [H,Dk,M]."""
+    if not msgs:
+        # no incoming edges: the relation gain and edge weights are unused (no gradient)
+        gain, edge_w = gain.detach(), gain.new_zeros(0, gain.shape[0])
+    return _RouteReader.apply(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs)

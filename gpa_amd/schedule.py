@@ -30,6 +30,8 @@ from torch import Tensor
 
 from . import _lib
 from .ops import gdn_scan_hip
+from .route import route_reader
+from .route import supported as fused_route_supported
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 
 _F32 = torch.float32
@@ -384,12 +386,24 @@ def _incoming_index(model, j: int) -> Tensor:
     return (model._edge_target == j).nonzero_static(size=model.config.levels - 1)[:, 0]
 
 
+_FUSED_ROUTE = [True]  # the fused route reader for the default read (route.py)
+
+
 def _bridge(model, q: Tensor, logits, incoming, counts):
     """Route reader and query projection per target level (attention.py:225-262)."""
     cfg = model.config
     dtype = q.dtype
     routes, queries = [], []
     for j, base in enumerate(logits):
+        if _FUSED_ROUTE[0] and fused_route_supported(cfg, dtype, base.shape[-1]):
+            w = (model.edge_logits.index_select(0, _incoming_index(model, j)).softmax(0)
+                 if incoming[j] else None)
+            qo, route = route_reader(base, q, w, model.relation_gain[j], model.route_mlp_gain[j],
+                                     model.route_up[j], model.route_down[j], model.route_weight[j],
+                                     model.query_weight[j], cfg.query_scale, [msg for _, msg in incoming[j]])
+            routes.append(route)
+            queries.append(qo)
+            continue
         if incoming[j]:
             w = model.edge_logits.index_select(0, _incoming_index(model, j)).softmax(0)
             total = 0

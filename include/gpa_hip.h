@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 4
+#define GPA_HIP_ABI_VERSION 5
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -188,6 +188,67 @@ typedef struct gpa_decode_problem {
 /* One decode token of every stream (no autograd).  Replaces the T = 1 call of
  * DenseGPA.forward in chunk mode (reference attention.py:347-413). */
 int gpa_decode_step(const gpa_decode_problem *problem, hipStream_t stream);
+
+/* ---------------------------------------------------------------- route reader
+ * The route reader of one target level j with the default read (reference
+ * _bridge, attention.py:225-262, legacy branch :236-240; closed form
+ * packed.py:16-35), for every token of every head:
+ *   inc   = sum_e w_e m_e                      (w = softmax of the incoming edge logits)
+ *   z     = (inc - mean inc) / sqrt(mean (inc - mean inc)^2 + 1e-5)
+ *   r0    = softmax(base + gain tanh z)        (rounded to the activation type)
+ *   h1    = r0 U,  hd = gelu(h1) D,  r1 = r0 + mlp_gain hd      (= the returned route)
+ *   qo    = r1 W_rs + query_scale (q W_qs)
+ * with each product's operands and result rounded to the activation type and
+ * float32 accumulation, as the reference's typed einsums do.  Rows are the
+ * R = batch*tokens token positions; activation tensors are [B,T,H,X] operands
+ * whose rows are uniformly strided (sb = tokens*st).
+ *
+ * Weights are passed pre-padded in the activation type, one [H][N32][K16]
+ * matrix per product (N32 = N rounded up to 32, K16 = K rounded up to 16, zero
+ * padding), row n holding the contraction over k for output column n:
+ *   forward  up_t = U^T [2M][M], down_t = D^T [M][2M], rs_t = W_rs^T [M][M], qs_t = W_qs^T [M][Dk]
+ *   backward up = U [M][2M], down = D [2M][M], rs = W_rs [M][M], qs = W_qs [Dk][M]
+ * Saved rows (activation type, head-major [H][R][width]): r0 (M), h1 (2M), hd (M). */
+#define GPA_ROUTE_MAX_WIDTH 256   /* slots M and key width Dk */
+#define GPA_ROUTE_MAX_INCOMING 3
+#define GPA_ROUTE_ROWS 32         /* token rows per workgroup; partials have ceil(R/32) rows */
+
+typedef struct gpa_route_problem {
+    int32_t batch, tokens, heads, slots, key_dim, incoming, dtype;
+    float query_scale;
+    gpa_operand base;                             /* float32 [B,T,H,M] base logits */
+    gpa_operand msg[GPA_ROUTE_MAX_INCOMING];      /* [B,T,H,M] incoming messages */
+    gpa_operand q;                                /* [B,T,H,Dk] */
+    const float *edge_weight;                     /* [incoming][H] */
+    const float *gain, *mlp_gain;                 /* [H] */
+    const void *up_t, *down_t, *rs_t, *qs_t;      /* forward weights (see above) */
+    const void *up, *down, *rs, *qs;              /* backward weights */
+    gpa_operand qo, route;                        /* outputs [B,T,H,M] */
+    void *r0, *h1, *hd;                           /* saved rows */
+} gpa_route_problem;
+
+typedef struct gpa_route_grads {
+    gpa_operand dqo, droute;                      /* incoming gradients; droute.ptr may be NULL */
+    gpa_operand dbase;                            /* float32 out */
+    gpa_operand dmsg[GPA_ROUTE_MAX_INCOMING];     /* out */
+    gpa_operand dq;                               /* out [B,T,H,Dk] */
+    void *dh1, *dhd, *dqs;                        /* out rows [H][R][2M | M | M]: grads of h1, hd and of q W_qs */
+    float *partials;                              /* out [ceil(R/32)][H][2 + incoming]:
+                                                     d mlp_gain, d gain, d w_e summed over the block's rows */
+} gpa_route_grads;
+
+/* Forward of the route reader.  Replaces the legacy-read body of _bridge
+ * (reference attention.py:225-262) and the fused Triton route
+ * (triton_route.py:11-151, packed.py:130-136). */
+int gpa_route_forward(const gpa_route_problem *problem, hipStream_t stream);
+/* Backward: input and row gradients, plus per-block partial sums of the scalar
+ * parameter gradients.  Needs the forward's saved rows and outputs. */
+int gpa_route_backward(const gpa_route_problem *problem, const gpa_route_grads *grads, hipStream_t stream);
+/* Weight gradients summed over rows, float32 [H][K][N] in the parameters'
+ * own layouts: d U [M][2M], d D [2M][M], d W_rs [M][M], d W_qs [Dk][M]
+ * (each rounded to the activation type, as the reference's typed products are). */
+int gpa_route_weight_grads(const gpa_route_problem *problem, const gpa_route_grads *grads, float *d_up,
+                           float *d_down, float *d_rs, float *d_qs, hipStream_t stream);
 
 #ifdef __cplusplus
 }

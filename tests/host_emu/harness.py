@@ -1,0 +1,142 @@
+"""Host build of libgpa_hip's kernels for CPU tests (test infrastructure).
+
+`build(dir)` compiles the named kernel sources with host clang and
+AddressSanitizer against the HIP emulation in this directory (workgroups as
+threads, barriers, wave shuffles, MFMA lane layouts, dynamic LDS sized per
+launch).  `HostLib` stands in for the loaded library: each entry point dumps
+its struct arguments and every buffer they point into (the whole storage of
+each live tensor, found through the garbage collector) to a runner process,
+which allocates each buffer with its exact size, runs the kernels and writes
+the buffers back.  Any out-of-bounds access aborts the runner.
+"""
+from __future__ import annotations
+
+import ctypes
+import gc
+import os
+import shutil
+import struct
+import subprocess
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+CLANG = "/opt/rocm/llvm/bin/clang++"
+ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3}
+
+
+def compiler() -> str | None:
+    return CLANG if os.path.exists(CLANG) else shutil.which("clang++")
+
+
+def build(out_dir: str, sources) -> str:
+    exe = os.path.join(out_dir, "host_runner")
+    cmd = [compiler(), "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
+           "-Wno-unused-command-line-argument", "-I", HERE, "-I", os.path.join(ROOT, "include"),
+           "-I", os.path.join(ROOT, "gpa_amd", "csrc"), "-x", "c++"]
+    cmd += [os.path.join(ROOT, "gpa_amd", "csrc", s) for s in sources]
+    cmd += ["-x", "none", os.path.join(HERE, "runner.cpp"), "-o", exe, "-lpthread"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode:
+        raise RuntimeError(res.stderr[-4000:])
+    return exe
+
+
+def _pointer_fields(ctype, base=0):
+    out = []
+    for name, t in ctype._fields_:
+        off = base + getattr(ctype, name).offset
+        if t is ctypes.c_void_p:
+            out.append(off)
+        elif issubclass(t, ctypes.Structure):
+            out += _pointer_fields(t, off)
+        elif issubclass(t, ctypes.Array):
+            for i in range(t._length_):
+                o = off + i * ctypes.sizeof(t._type_)
+                if t._type_ is ctypes.c_void_p:
+                    out.append(o)
+                elif issubclass(t._type_, ctypes.Structure):
+                    out += _pointer_fields(t._type_, o)
+    return out
+
+
+def _storages():
+    spans = {}
+    for o in gc.get_objects():
+        if isinstance(o, torch.Tensor) and o.device.type == "cpu":
+            s = o.untyped_storage()
+            if s.nbytes():
+                spans[s.data_ptr()] = s.nbytes()
+    return sorted(spans.items())
+
+
+class HostLib:
+    """Stands in for `gpa_amd._lib.load()` with the host build."""
+
+    def __init__(self, exe: str, workdir: str):
+        self.exe, self.workdir = exe, workdir
+
+    def _locate(self, spans, p):
+        hit = [(i, p - b) for i, (b, n) in enumerate(spans) if b <= p < b + n]
+        if len(hit) != 1:
+            raise AssertionError(f"pointer {p:#x} is not inside exactly one live tensor storage")
+        return hit[0]
+
+    def _call(self, entry: str, blobs, raw=()):
+        spans = _storages()
+        fin, fout = os.path.join(self.workdir, "in.bin"), os.path.join(self.workdir, "out.bin")
+        with open(fin, "wb") as f:
+            f.write(struct.pack("<qq", ENTRIES[entry], len(blobs)))
+            for blob in blobs:
+                data = ctypes.string_at(ctypes.addressof(blob), ctypes.sizeof(blob))
+                f.write(struct.pack("<q", len(data)) + data)
+            f.write(struct.pack("<q", len(spans)))
+            for b, n in spans:
+                f.write(struct.pack("<q", n) + ctypes.string_at(b, n))
+            for blob in blobs:
+                data = ctypes.string_at(ctypes.addressof(blob), ctypes.sizeof(blob))
+                recs = []
+                for off in _pointer_fields(type(blob)):
+                    p = struct.unpack_from("<Q", data, off)[0]
+                    if p:
+                        recs.append((off, *self._locate(spans, p)))
+                f.write(struct.pack("<q", len(recs)))
+                for rec in recs:
+                    f.write(struct.pack("<qqq", *rec))
+            f.write(struct.pack("<q", len(raw)))
+            for p in raw:
+                f.write(struct.pack("<qq", *(self._locate(spans, p) if p else (-1, 0))))
+        res = subprocess.run([self.exe, fin, fout], capture_output=True, text=True, timeout=900)
+        if res.returncode:
+            raise AssertionError(f"host run of {entry} failed ({res.returncode}):\n{res.stderr[-6000:]}")
+        data = open(fout, "rb").read()
+        pos = 0
+        for b, n in spans:
+            ctypes.memmove(b, data[pos:pos + n], n)
+            pos += n
+        return 0
+
+    def gpa_decode_step(self, prob, stream):
+        return self._call("gpa_decode_step", [prob])
+
+    def gpa_route_forward(self, prob, stream):
+        return self._call("gpa_route_forward", [prob])
+
+    def gpa_route_backward(self, prob, grads, stream):
+        return self._call("gpa_route_backward", [prob, grads])
+
+    def gpa_route_weight_grads(self, prob, grads, d_up, d_down, d_rs, d_qs, stream):
+        return self._call("gpa_route_weight_grads", [prob, grads], [d_up, d_down, d_rs, d_qs])
+
+    def gpa_hip_last_error(self):
+        return b""
+
+
+def use_host(monkeypatch, host: HostLib) -> None:
+    """Route `gpa_amd._lib` to the host build for the duration of a test."""
+    from gpa_amd import _lib
+
+    monkeypatch.setattr(_lib, "load", lambda: host)
+    monkeypatch.setattr(_lib, "require_device", lambda t: None)
+    monkeypatch.setattr(_lib, "stream_handle", lambda d: 0)

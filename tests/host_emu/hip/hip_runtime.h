@@ -29,6 +29,9 @@ struct dim3 {
   unsigned x = 1, y = 1, z = 1;
   dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
 };
+struct uint2 {
+  unsigned x, y;
+};
 struct EmuIdx {
   unsigned x, y, z;
 };
@@ -48,6 +51,73 @@ inline float __shfl_xor(float v, int m, int width = 64) {
   return r;
 }
 inline float atomicAdd(float* p, float v) { return std::atomic_ref<float>(*p).fetch_add(v); }
+
+// MFMA: every lane posts its operands, then computes its own accumulator
+// registers from the whole wave's operands (lane layouts of the gfx950
+// instructions: A(row l%32, k), B(k, col l%32), accumulator lane l register r
+// at row 8(r/4) + 4(l/32) + r%4, column l%32; 16x16x4: A(row l%16, k = l/16),
+// accumulator row 4(l/16) + r).
+typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
+typedef float emu_f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
+extern float emu_ma[16][64][8], emu_mb[16][64][8];
+inline void emu_post(const float* a, const float* b, int n) {
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  for (int i = 0; i < n; ++i) {
+    emu_ma[w][l][i] = a[i];
+    emu_mb[w][l][i] = b[i];
+  }
+  emu_wave_barrier[w]->arrive_and_wait();
+}
+inline emu_f32x16 emu_mfma_32x32x16_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x16 c) {
+  float fa[8], fb[8];
+  for (int i = 0; i < 8; ++i) {
+    fa[i] = (float)a[i];
+    fb[i] = (float)b[i];
+  }
+  emu_post(fa, fb, 8);
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r / 4) + 4 * (l / 32) + r % 4, col = l % 32;
+    float s = 0.f;
+    for (int k = 0; k < 16; ++k) s += emu_ma[w][row + 32 * (k / 8)][k % 8] * emu_mb[w][col + 32 * (k / 8)][k % 8];
+    c[r] += s;
+  }
+  emu_wave_barrier[w]->arrive_and_wait();
+  return c;
+}
+inline emu_f32x16 emu_mfma_32x32x2_f32(float a, float b, emu_f32x16 c) {
+  emu_post(&a, &b, 1);
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r / 4) + 4 * (l / 32) + r % 4, col = l % 32;
+    c[r] += emu_ma[w][row][0] * emu_mb[w][col][0] + emu_ma[w][row + 32][0] * emu_mb[w][col + 32][0];
+  }
+  emu_wave_barrier[w]->arrive_and_wait();
+  return c;
+}
+inline emu_f32x4 emu_mfma_16x16x4_f32(float a, float b, emu_f32x4 c) {
+  emu_post(&a, &b, 1);
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * (l / 16) + r, col = l % 16;
+    float s = 0.f;
+    for (int k = 0; k < 4; ++k) s += emu_ma[w][row + 16 * k][0] * emu_mb[w][col + 16 * k][0];
+    c[r] += s;
+  }
+  emu_wave_barrier[w]->arrive_and_wait();
+  return c;
+}
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, x, y, z) emu_mfma_32x32x16_bf16(a, b, c)
+#define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu_mfma_32x32x2_f32(a, b, c)
+#define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) emu_mfma_16x16x4_f32(a, b, c)
+
+// Dynamic LDS: an allocation of exactly the launch's size per workgroup.
+extern char* emu_dynamic_lds;
+#define HIP_DYNAMIC_SHARED(type, var) type* var = reinterpret_cast<type*>(emu_dynamic_lds);
+#define hipSuccess 0
+#define hipFuncAttributeMaxDynamicSharedMemorySize 8
+inline int hipFuncSetAttribute(const void*, int, int) { return 0; }
 inline float __expf(float x) { return expf(x); }
 inline float __uint_as_float(uint32_t u) {
   float f;
@@ -61,21 +131,24 @@ inline uint32_t __float_as_uint(float f) {
 }
 
 template <typename K, typename... A>
-void emu_launch(K kernel, dim3 grid, dim3 block, A... args) {
+void emu_launch(K kernel, dim3 grid, dim3 block, size_t lds_bytes, A... args) {
   const unsigned nt = block.x;
-  for (unsigned bx = 0; bx < grid.x; ++bx) {
-    std::barrier<> bar(nt);
-    emu_block_barrier = &bar;
-    emu_wave_barrier.clear();
-    for (unsigned w = 0; w < (nt + 63) / 64; ++w) emu_wave_barrier.emplace_back(new std::barrier<>(64));
-    std::vector<std::thread> threads;
-    for (unsigned t = 0; t < nt; ++t)
-      threads.emplace_back([=] {
-        threadIdx = {t, 0, 0};
-        blockIdx = {bx, 0, 0};
-        kernel(args...);
-      });
-    for (auto& th : threads) th.join();
-  }
+  for (unsigned by = 0; by < grid.y; ++by)
+    for (unsigned bx = 0; bx < grid.x; ++bx) {
+      std::barrier<> bar(nt);
+      emu_block_barrier = &bar;
+      emu_wave_barrier.clear();
+      for (unsigned w = 0; w < (nt + 63) / 64; ++w) emu_wave_barrier.emplace_back(new std::barrier<>(64));
+      std::vector<char> lds(lds_bytes ? lds_bytes : 1);
+      emu_dynamic_lds = lds.data();
+      std::vector<std::thread> threads;
+      for (unsigned t = 0; t < nt; ++t)
+        threads.emplace_back([=] {
+          threadIdx = {t, 0, 0};
+          blockIdx = {bx, by, 0};
+          kernel(args...);
+        });
+      for (auto& th : threads) th.join();
+    }
 }
-#define hipLaunchKernelGGL(k, g, b, s, st, ...) emu_launch(k, g, b, __VA_ARGS__)
+#define hipLaunchKernelGGL(k, g, b, s, st, ...) emu_launch(k, g, b, s, __VA_ARGS__)

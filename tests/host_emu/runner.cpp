@@ -1,7 +1,8 @@
-// Runs one gpa_decode_step of the host build on a problem dump (test
-// infrastructure).  Dump: struct bytes; the buffers (each allocated here with
-// its exact size, so AddressSanitizer bounds every access); the pointer fields
-// as (struct offset, buffer, byte offset).  Writes every buffer back.
+// Runs one entry point of the host build of the library on a dump (test
+// infrastructure).  Dump: the entry point's index; its struct arguments as
+// blobs; the buffers (each allocated here with its exact size, so
+// AddressSanitizer bounds every access); the pointer fields of the blobs and
+// the raw pointer arguments as (buffer, byte offset).  Writes every buffer back.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -15,6 +16,8 @@ thread_local EmuIdx threadIdx, blockIdx;
 std::barrier<>* emu_block_barrier;
 std::vector<std::unique_ptr<std::barrier<>>> emu_wave_barrier;
 float emu_xchg[16][64];
+float emu_ma[16][64][8], emu_mb[16][64][8];
+char* emu_dynamic_lds;
 static std::string last_error;
 int fail(int code, const char* message) {
   last_error = message;
@@ -32,8 +35,12 @@ int main(int argc, char** argv) {
   if (argc != 3) return 2;
   FILE* f = fopen(argv[1], "rb");
   if (!f) return 2;
-  std::vector<char> st(get(f));
-  if (fread(st.data(), 1, st.size(), f) != st.size()) return 4;
+  const int64_t entry = get(f);
+  std::vector<std::vector<char>> blobs(get(f));
+  for (auto& b : blobs) {
+    b.resize(get(f));
+    if (fread(b.data(), 1, b.size(), f) != b.size()) return 4;
+  }
   const int64_t nbuf = get(f);
   std::vector<char*> buf(nbuf);
   std::vector<int64_t> bytes(nbuf);
@@ -42,16 +49,41 @@ int main(int argc, char** argv) {
     buf[i] = static_cast<char*>(malloc(bytes[i]));
     if (fread(buf[i], 1, bytes[i], f) != (size_t)bytes[i]) return 4;
   }
-  const int64_t nptr = get(f);
-  for (int64_t i = 0; i < nptr; ++i) {
-    const int64_t off = get(f), id = get(f), boff = get(f);
-    char* p = buf[id] + boff;
-    memcpy(st.data() + off, &p, 8);
+  for (auto& b : blobs) {
+    const int64_t nptr = get(f);
+    for (int64_t i = 0; i < nptr; ++i) {
+      const int64_t off = get(f), id = get(f), boff = get(f);
+      char* p = buf[id] + boff;
+      memcpy(b.data() + off, &p, 8);
+    }
+  }
+  std::vector<void*> raw(get(f));
+  for (auto& r : raw) {
+    const int64_t id = get(f), boff = get(f);
+    r = id < 0 ? nullptr : buf[id] + boff;
   }
   fclose(f);
-  const int rc = gpa_decode_step(reinterpret_cast<gpa_decode_problem*>(st.data()), nullptr);
+  int rc = -1;
+  switch (entry) {
+    case 0:
+      rc = gpa_decode_step(reinterpret_cast<gpa_decode_problem*>(blobs.at(0).data()), nullptr);
+      break;
+    case 1:
+      rc = gpa_route_forward(reinterpret_cast<gpa_route_problem*>(blobs.at(0).data()), nullptr);
+      break;
+    case 2:
+      rc = gpa_route_backward(reinterpret_cast<gpa_route_problem*>(blobs.at(0).data()),
+                              reinterpret_cast<gpa_route_grads*>(blobs.at(1).data()), nullptr);
+      break;
+    case 3:
+      rc = gpa_route_weight_grads(reinterpret_cast<gpa_route_problem*>(blobs.at(0).data()),
+                                  reinterpret_cast<gpa_route_grads*>(blobs.at(1).data()),
+                                  static_cast<float*>(raw.at(0)), static_cast<float*>(raw.at(1)),
+                                  static_cast<float*>(raw.at(2)), static_cast<float*>(raw.at(3)), nullptr);
+      break;
+  }
   if (rc) {
-    fprintf(stderr, "gpa_decode_step rc=%d: %s\n", rc, last_error.c_str());
+    fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());
     return 3;
   }
   f = fopen(argv[2], "wb");

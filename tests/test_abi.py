@@ -18,7 +18,8 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
-                     "gpa_gdn_forward", "gpa_gdn_backward", "gpa_decode_step"):
+                     "gpa_gdn_forward", "gpa_gdn_backward", "gpa_decode_step", "gpa_route_forward",
+                     "gpa_route_backward", "gpa_route_weight_grads"):
         assert expected in names
 
 
@@ -60,6 +61,10 @@ def test_ctypes_structs_match_c_layout():
     # 7 int32 + 3 float, 4 operands, 8 pointers, 4 levels, 12 states, 12 pointers
     assert _lib.DecodeProblem.level.offset == 40 + 4 * 32 + 8 * 8
     assert ctypes.sizeof(_lib.DecodeProblem) == 232 + 4 * 168 + 12 * 16 + 12 * 8
+    # 7 int32 + float, 5 operands, 11 pointers, 2 operands, 3 pointers
+    assert ctypes.sizeof(_lib.RouteProblem) == 32 + 5 * 32 + 11 * 8 + 2 * 32 + 3 * 8
+    # 7 operands, 4 pointers
+    assert ctypes.sizeof(_lib.RouteGrads) == 7 * 32 + 4 * 8
 
 
 def test_backend_refuses_cpu_tensors():
