@@ -35,22 +35,36 @@ template <> struct Wt<bf16_t> { using type = bf16_t; };
 
 // acc += A[32][K] B, A rows in LDS (already in the activation type's values,
 // zero beyond K up to k16), B given as rows bt[n0 + c][0..k16) (zero padded).
+// The B fragments of up to 8 contraction steps are loaded before their MFMAs,
+// so that their latency overlaps.
 __device__ __forceinline__ void tile_gemm(f32x16& acc, const float* a, int lda, const bf16_t* bt, int ldb,
                                           int k16, int n0, int lane) {
   const float* ar = a + (lane & 31) * lda + 8 * (lane >> 5);
   const bf16_t* br = bt + (int64_t)(n0 + (lane & 31)) * ldb + 8 * (lane >> 5);
-  for (int k0 = 0; k0 < k16; k0 += 16) {
-    const bf16x8 av = pack8(ar + k0);
-    const bf16x8 bv = *reinterpret_cast<const bf16x8*>(br + k0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+  for (int k0 = 0; k0 < k16; k0 += 8 * 16) {
+    bf16x8 bv[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (k0 + 16 * s < k16) bv[s] = *reinterpret_cast<const bf16x8*>(br + k0 + 16 * s);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (k0 + 16 * s < k16)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack8(ar + k0 + 16 * s), bv[s], acc, 0, 0, 0);
   }
 }
 __device__ __forceinline__ void tile_gemm(f32x16& acc, const float* a, int lda, const float* bt, int ldb, int k16,
                                           int n0, int lane) {
   const float* ar = a + (lane & 31) * lda + 4 * (lane >> 5);
   const float* br = bt + (int64_t)(n0 + (lane & 31)) * ldb + 4 * (lane >> 5);
-  for (int k0 = 0; k0 < k16; k0 += 8)
-    mma8(acc, *reinterpret_cast<const f32x4*>(ar + k0), *reinterpret_cast<const f32x4*>(br + k0));
+  for (int k0 = 0; k0 < k16; k0 += 8 * 8) {
+    f32x4 bv[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (k0 + 8 * s < k16) bv[s] = *reinterpret_cast<const f32x4*>(br + k0 + 8 * s);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (k0 + 8 * s < k16) mma8(acc, *reinterpret_cast<const f32x4*>(ar + k0 + 8 * s), bv[s]);
+  }
 }
 
 __device__ __forceinline__ float sum8(float x) {
@@ -469,69 +483,110 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   }
 }
 
-// C[h][i][j] = sum_r A[h][r][i] B[h][r][j] over the R rows: one 32x32 tile of
-// C per workgroup, the rows split over its waves and the partial tiles summed
-// in LDS.  A may be mapped through round(gelu(.)) on load (d D from h1).
+// Weight gradients C[h][i][j] = sum_r A[h][r][i] B[h][r][j] over the R rows.
+// A workgroup owns a 64x64 tile of C (a 32x32 quadrant per wave) and a span
+// of WKC rows; slabs of 32 rows of A and B are read with 16-byte loads,
+// stored transposed in LDS, and fed to MFMA; the spans' partial tiles are
+// added into C (cleared first) with float atomics and rounded at the end.
 struct TnOperand {
   const void* ptr;
   int64_t rs, hs;  // row and head strides (elements)
   int width;
-  int gelu;
+  int gelu;        // A mapped through round(gelu(.)) on load (d D from h1)
 };
 
+constexpr int WT = 64;     // output tile
+constexpr int WK = 32;     // rows per slab
+constexpr int WP = WK + 1; // LDS pitch (floats)
+constexpr int WKC = 256;   // rows per workgroup
+
 template <typename E>
-__device__ __forceinline__ float tn_load(const TnOperand& o, int h, int r, int c, int R) {
-  if (r >= R || c >= o.width) return 0.f;
-  const float x = to_f32(reinterpret_cast<const E*>(o.ptr)[(int64_t)h * o.hs + (int64_t)r * o.rs + c]);
-  return o.gelu ? round_as<E>(gelu(x)) : x;
+__device__ __forceinline__ void load8(const TnOperand& o, int h, int r, int c, int rend, float (&x)[8]) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) x[s] = 0.f;
+  if (r >= rend) return;
+  const E* p = reinterpret_cast<const E*>(o.ptr) + (int64_t)h * o.hs + (int64_t)r * o.rs + c;
+  if (c + 8 <= o.width && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    if constexpr (std::is_same<E, float>::value) {
+      const f32x4 u = reinterpret_cast<const f32x4*>(p)[0], v = reinterpret_cast<const f32x4*>(p)[1];
+      x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w; x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+    } else {
+      const uint4 w = *reinterpret_cast<const uint4*>(p);
+      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        x[2 * s] = __uint_as_float(ws[s] << 16);
+        x[2 * s + 1] = __uint_as_float(ws[s] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (c + s < o.width) x[s] = to_f32(p[s]);
+  }
+  if (o.gelu) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x[s] = round_as<E>(gelu(x[s]));
+  }
 }
 
 template <typename E>
-__global__ __launch_bounds__(RNT) void route_gemm_tn(TnOperand a, TnOperand b, float* c, int R) {
-  __shared__ float part[RW][32][33];
-  const int h = blockIdx.y, tn = (b.width + 31) / 32;
-  const int i0 = 32 * (blockIdx.x / tn), j0 = 32 * (blockIdx.x % tn);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int step = std::is_same<E, float>::value ? 8 : 16;
-  const int span = ((R + RW - 1) / RW + step - 1) / step * step;
-  const int rbeg = wave * span, rend = rbeg + span;
+__global__ __launch_bounds__(RNT) void route_wgrad(TnOperand a, TnOperand b, float* c, int R) {
+  __shared__ float As[WT][WP], Bs[WT][WP];
+  const int h = blockIdx.y, tj = (b.width + WT - 1) / WT;
+  const int i0 = WT * (blockIdx.x / tj), j0 = WT * (blockIdx.x % tj);
+  const int rbeg = blockIdx.z * WKC, rend = rbeg + WKC < R ? rbeg + WKC : R;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wi = (wave & 1) * 32 + (lane & 31), wj = (wave >> 1) * 32 + (lane & 31);
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
   f32x16 acc = {};
-  for (int k0 = rbeg; k0 < rend; k0 += step) {
+  for (int k0 = rbeg; k0 < rend; k0 += WK) {
+    float xa[8], xb[8];
+    load8<E>(a, h, k0 + lr, i0 + lc, rend, xa);
+    load8<E>(b, h, k0 + lr, j0 + lc, rend, xb);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      As[lc + s][lr] = xa[s];
+      Bs[lc + s][lr] = xb[s];
+    }
+    __syncthreads();
     if constexpr (std::is_same<E, float>::value) {
-      const int k = k0 + 4 * (lane >> 5);
-      const f32x4 av{tn_load<E>(a, h, k, i0 + (lane & 31), R), tn_load<E>(a, h, k + 1, i0 + (lane & 31), R),
-                     tn_load<E>(a, h, k + 2, i0 + (lane & 31), R), tn_load<E>(a, h, k + 3, i0 + (lane & 31), R)};
-      const f32x4 bv{tn_load<E>(b, h, k, j0 + (lane & 31), R), tn_load<E>(b, h, k + 1, j0 + (lane & 31), R),
-                     tn_load<E>(b, h, k + 2, j0 + (lane & 31), R), tn_load<E>(b, h, k + 3, j0 + (lane & 31), R)};
-      mma8(acc, av, bv);
+#pragma unroll
+      for (int kk = 0; kk < WK; kk += 8) {
+        const int k = kk + 4 * (lane >> 5);
+        mma8(acc, f32x4{As[wi][k], As[wi][k + 1], As[wi][k + 2], As[wi][k + 3]},
+             f32x4{Bs[wj][k], Bs[wj][k + 1], Bs[wj][k + 2], Bs[wj][k + 3]});
+      }
     } else {
-      const int k = k0 + 8 * (lane >> 5);
-      float xa[8], xb[8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        xa[s] = tn_load<E>(a, h, k + s, i0 + (lane & 31), R);
-        xb[s] = tn_load<E>(b, h, k + s, j0 + (lane & 31), R);
-      }
-      bf16x8 av, bv;
+      for (int kk = 0; kk < WK; kk += 16) {
+        const int k = kk + 8 * (lane >> 5);
+        bf16x8 av, bv;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        av[s] = (__bf16)xa[s];
-        bv[s] = (__bf16)xb[s];
+        for (int s = 0; s < 8; ++s) {
+          av[s] = (__bf16)As[wi][k + s];
+          bv[s] = (__bf16)Bs[wj][k + s];
+        }
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
       }
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) part[wave][acc_row(i, lane >> 5)][lane & 31] = acc[i];
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * 32; idx += RNT) {
-    const int i = idx / 32, j = idx % 32;
-    if (i0 + i < a.width && j0 + j < b.width) {
-      float x = 0.f;
-      for (int w = 0; w < RW; ++w) x += part[w][i][j];
-      c[((int64_t)h * a.width + i0 + i) * b.width + j0 + j] = round_as<E>(x);
-    }
+  for (int r = 0; r < 16; ++r) {
+    const int i = i0 + (wave & 1) * 32 + acc_row(r, lane >> 5), j = j0 + wj;
+    if (i < a.width && j < b.width) atomicAdd(&c[((int64_t)h * a.width + i) * b.width + j], acc[r]);
   }
+}
+
+__global__ void fill_zero(float* c, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    c[i] = 0.f;
+}
+template <typename E>
+__global__ void round_in_place(float* c, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    c[i] = round_as<E>(c[i]);
 }
 
 int check_route(const gpa_route_problem* p) {
@@ -648,12 +703,17 @@ extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gp
   const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk, 0};
   struct Job { TnOperand a, b; float* c; } jobs[4] = {{r0, dh1, d_up}, {hid, dhd, d_down}, {r1, dqo, d_rs},
                                                         {q, dqs, d_qs}};
+  const bool bf = problem->dtype == GPA_DTYPE_BF16;
   for (const Job& j : jobs) {
-    const dim3 grid(((j.a.width + 31) / 32) * ((j.b.width + 31) / 32), H), block(RNT);
-    if (problem->dtype == GPA_DTYPE_BF16)
-      hipLaunchKernelGGL(route_gemm_tn<bf16_t>, grid, block, 0, stream, j.a, j.b, j.c, R);
+    const int64_t n = (int64_t)H * j.a.width * j.b.width;
+    const dim3 fill_grid((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64));
+    hipLaunchKernelGGL(fill_zero, fill_grid, dim3(256), 0, stream, j.c, n);
+    const dim3 grid(((j.a.width + WT - 1) / WT) * ((j.b.width + WT - 1) / WT), H, (R + WKC - 1) / WKC);
+    if (bf)
+      hipLaunchKernelGGL(route_wgrad<bf16_t>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
     else
-      hipLaunchKernelGGL(route_gemm_tn<float>, grid, block, 0, stream, j.a, j.b, j.c, R);
+      hipLaunchKernelGGL(route_wgrad<float>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
+    if (bf) hipLaunchKernelGGL(round_in_place<bf16_t>, fill_grid, dim3(256), 0, stream, j.c, n);
   }
   return check_launch("gpa_route_weight_grads");
 }

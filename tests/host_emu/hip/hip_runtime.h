@@ -32,10 +32,13 @@ struct dim3 {
 struct uint2 {
   unsigned x, y;
 };
+struct uint4 {
+  unsigned x, y, z, w;
+};
 struct EmuIdx {
   unsigned x, y, z;
 };
-extern thread_local EmuIdx threadIdx, blockIdx;
+extern thread_local EmuIdx threadIdx, blockIdx, blockDim, gridDim;
 extern std::barrier<>* emu_block_barrier;
 extern std::vector<std::unique_ptr<std::barrier<>>> emu_wave_barrier;
 extern float emu_xchg[16][64];
@@ -132,23 +135,29 @@ inline uint32_t __float_as_uint(float f) {
 
 template <typename K, typename... A>
 void emu_launch(K kernel, dim3 grid, dim3 block, size_t lds_bytes, A... args) {
+  // One team of blockDim.x threads runs the workgroups one after another; a
+  // barrier separates workgroups (their __shared__ objects are shared statics).
   const unsigned nt = block.x;
-  for (unsigned by = 0; by < grid.y; ++by)
-    for (unsigned bx = 0; bx < grid.x; ++bx) {
-      std::barrier<> bar(nt);
-      emu_block_barrier = &bar;
-      emu_wave_barrier.clear();
-      for (unsigned w = 0; w < (nt + 63) / 64; ++w) emu_wave_barrier.emplace_back(new std::barrier<>(64));
-      std::vector<char> lds(lds_bytes ? lds_bytes : 1);
-      emu_dynamic_lds = lds.data();
-      std::vector<std::thread> threads;
-      for (unsigned t = 0; t < nt; ++t)
-        threads.emplace_back([=] {
-          threadIdx = {t, 0, 0};
-          blockIdx = {bx, by, 0};
-          kernel(args...);
-        });
-      for (auto& th : threads) th.join();
-    }
+  std::barrier<> bar(nt), between(nt);
+  emu_block_barrier = &bar;
+  emu_wave_barrier.clear();
+  for (unsigned w = 0; w < (nt + 63) / 64; ++w) emu_wave_barrier.emplace_back(new std::barrier<>(64));
+  std::vector<char> lds(lds_bytes ? lds_bytes : 1);
+  emu_dynamic_lds = lds.data();
+  std::vector<std::thread> threads;
+  for (unsigned t = 0; t < nt; ++t)
+    threads.emplace_back([&, t] {
+      threadIdx = {t, 0, 0};
+      blockDim = {block.x, block.y, block.z};
+      gridDim = {grid.x, grid.y, grid.z};
+      for (unsigned bz = 0; bz < grid.z; ++bz)
+        for (unsigned by = 0; by < grid.y; ++by)
+          for (unsigned bx = 0; bx < grid.x; ++bx) {
+            blockIdx = {bx, by, bz};
+            kernel(args...);
+            between.arrive_and_wait();
+          }
+    });
+  for (auto& th : threads) th.join();
 }
 #define hipLaunchKernelGGL(k, g, b, s, st, ...) emu_launch(k, g, b, s, __VA_ARGS__)

@@ -12,7 +12,7 @@
 
 #include "gpa_hip.h"
 
-thread_local EmuIdx threadIdx, blockIdx;
+thread_local EmuIdx threadIdx, blockIdx, blockDim, gridDim;
 std::barrier<>* emu_block_barrier;
 std::vector<std::unique_ptr<std::barrier<>>> emu_wave_barrier;
 float emu_xchg[16][64];
