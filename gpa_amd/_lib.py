@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -95,6 +95,24 @@ class RouteGrads(ctypes.Structure):
                [(n, c_vp) for n in ("dh1", "dhd", "dqs", "partials")]
 
 
+LEVEL_MAX_WIDTH = 256
+
+
+class LevelProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "key_dim", "value_dim", "slots", "chunk",
+                                     "offset", "dtype")] + \
+               [("key", Operand), ("value", Operand)] + \
+               [(n, c_vp) for n in ("a_states", "b_states", "a_first", "b_first")] + \
+               [("a_first_sb", c_i64), ("b_first_sb", c_i64), ("eta", c_vp)] + \
+               [(n, Operand) for n in ("write", "key_out", "value_out")] + [("rk", c_vp), ("rv", c_vp),
+                                                                             ("stats", c_vp)]
+
+
+class LevelGrads(ctypes.Structure):
+    _fields_ = [(n, Operand) for n in ("dwrite", "dkey_out", "dvalue_out", "dkey")] + \
+               [(n, c_vp) for n in ("da_states", "db_states", "da_first", "db_first", "deta")]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -109,6 +127,8 @@ EXPORTS = {
     "gpa_route_backward": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp], ctypes.c_int),
     "gpa_route_weight_grads": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp, c_vp, c_vp,
                                 c_vp, c_vp], ctypes.c_int),
+    "gpa_level_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
+    "gpa_level_backward": ([ctypes.POINTER(LevelProblem), ctypes.POINTER(LevelGrads), c_vp], ctypes.c_int),
 }
 
 _lib = None

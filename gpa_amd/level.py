@@ -1,0 +1,128 @@
+"""Fused level write and residual of the chunk model (`gpa_level_forward/backward`).
+
+For every token of block n (reference _block_segment, src/gpa/attention.py:
+314-329, _residual :190-194), from the block's snapshots A^_n [Dk,M] and
+B^_n [M,Dv]:
+
+    w = softmax(u(key) A^_n);   key' = key - eta0 A^_n w;   value' = value - eta1 w^T B^_n
+
+The snapshots are the scans' chunk-start states, read in place (value-major,
+as `gdn_scan_hip` saves them), except block 0 when the call starts inside a
+block: then it is the cached snapshot.  `level_mix` is differentiable in the
+keys, values, both state tensors, the cached snapshots and eta; the state
+gradients come back in the states' own layout.
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def supported(cfg, dtype: torch.dtype, key_dim: int, value_dim: int, slots: int) -> bool:
+    return (dtype in _lib.DTYPE_CODES and cfg.slot_feature == "linear" and not cfg.rsa_update
+            and max(key_dim, value_dim, slots) <= _lib.LEVEL_MAX_WIDTH and cfg.chunk_size <= 64)
+
+
+def _snapshot(t: Tensor | None) -> tuple[Tensor | None, int]:
+    """A [B,H,R,C] float32 snapshot with contiguous heads; keeps a broadcast
+    batch (stride 0) as it is."""
+    if t is None:
+        return None, 0
+    t = t.detach().float()
+    h, r, c = t.shape[1:]
+    if t.stride()[1:] != (r * c, c, 1):
+        t = t.contiguous()
+    return t, t.stride(0)
+
+
+def _problem(key, value, a_vm, b_vm, a_first, b_first, eta, chunk, offset, outs, saved):
+    bsz, tokens, heads, dk = key.shape
+    p = _lib.LevelProblem()
+    p.batch, p.tokens, p.heads, p.key_dim, p.value_dim = bsz, tokens, heads, dk, value.shape[-1]
+    p.slots, p.chunk, p.offset, p.dtype = a_vm.shape[-2], chunk, offset, _lib.DTYPE_CODES[key.dtype]
+    p.key, p.value = _lib.operand(key), _lib.operand(value)
+    p.a_states, p.b_states = a_vm.data_ptr(), b_vm.data_ptr()
+    (af, asb), (bf, bsb) = a_first, b_first
+    p.a_first, p.a_first_sb = (af.data_ptr() if af is not None else None), asb
+    p.b_first, p.b_first_sb = (bf.data_ptr() if bf is not None else None), bsb
+    p.eta = eta.data_ptr()
+    p.write, p.key_out, p.value_out = (_lib.operand(t) for t in outs)
+    p.rk, p.rv, p.stats = (t.data_ptr() for t in saved)
+    return p
+
+
+class _LevelMix(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, key, value, a_vm, b_vm, a_first, b_first, eta, chunk, offset):
+        _lib.require_device(key)
+        ctx.set_materialize_grads(False)
+        lib = _lib.load()
+        dtype = key.dtype
+        bsz, tokens, heads, dk = key.shape
+        dv, m = value.shape[-1], a_vm.shape[-2]
+        key, value = key.contiguous(), value.contiguous()
+        a_vm, b_vm = a_vm.detach().float().contiguous(), b_vm.detach().float().contiguous()
+        firsts = (_snapshot(a_first), _snapshot(b_first))
+        eta = eta.detach().float().contiguous()
+        write = torch.empty(bsz, tokens, heads, m, device=key.device, dtype=dtype)
+        key_out, value_out = torch.empty_like(key), torch.empty_like(value)
+        rk = torch.empty(bsz, tokens, heads, dk, device=key.device, dtype=dtype)
+        rv = torch.empty(bsz, tokens, heads, dv, device=key.device, dtype=dtype)
+        stats = torch.empty(bsz, tokens, heads, 2, device=key.device, dtype=torch.float32)
+        prob = _problem(key, value, a_vm, b_vm, *firsts, eta, chunk, offset, (write, key_out, value_out),
+                        (rk, rv, stats))
+        _lib.check(lib.gpa_level_forward(prob, _lib.stream_handle(key.device)), "gpa_level_forward")
+        ctx.chunk, ctx.offset = chunk, offset
+        ctx.has_first = (a_first is not None, b_first is not None)
+        ctx.first_sb = (firsts[0][1], firsts[1][1])
+        ctx.save_for_backward(key, value, a_vm, b_vm, firsts[0][0], firsts[1][0], eta, write, rk, rv, stats)
+        return write, key_out, value_out
+
+    @staticmethod
+    def backward(ctx, dwrite, dkey_out, dvalue_out):
+        lib = _lib.load()
+        key, value, a_vm, b_vm, af, bf, eta, write, rk, rv, stats = ctx.saved_tensors
+        dtype = key.dtype
+        bsz, tokens, heads, dk = key.shape
+        dv = value.shape[-1]
+        value_used = dvalue_out is not None
+        zeros = lambda t, like: torch.zeros_like(like) if t is None else t.to(dtype).contiguous()  # noqa: E731
+        dwrite, dkey_out, dvalue_out = zeros(dwrite, write), zeros(dkey_out, key), zeros(dvalue_out, value)
+        prob = _problem(key, value, a_vm, b_vm, (af, ctx.first_sb[0]), (bf, ctx.first_sb[1]), eta, ctx.chunk,
+                        ctx.offset, (write, write, write), (rk, rv, stats))
+        prob.key_out, prob.value_out = _lib.operand(key), _lib.operand(value)
+        da = torch.empty_like(a_vm)
+        db = torch.empty_like(b_vm)
+        if af is not None:
+            da[:, :, 0].zero_()
+        if bf is not None:
+            db[:, :, 0].zero_()
+        da_first = torch.empty(bsz, heads, dk, a_vm.shape[-2], device=key.device) if af is not None else None
+        db_first = torch.empty(bsz, heads, b_vm.shape[-1], dv, device=key.device) if bf is not None else None
+        nblocks = a_vm.shape[2]
+        deta = torch.empty(bsz * heads * nblocks, 2, device=key.device)
+        dkey = torch.empty_like(key)
+        gr = _lib.LevelGrads()
+        gr.dwrite, gr.dkey_out, gr.dvalue_out, gr.dkey = (_lib.operand(t) for t in (dwrite, dkey_out, dvalue_out,
+                                                                                    dkey))
+        gr.da_states, gr.db_states, gr.deta = da.data_ptr(), db.data_ptr(), deta.data_ptr()
+        gr.da_first = da_first.data_ptr() if da_first is not None else None
+        gr.db_first = db_first.data_ptr() if db_first is not None else None
+        _lib.check(lib.gpa_level_backward(prob, gr, _lib.stream_handle(key.device)), "gpa_level_backward")
+        deta = deta.view(bsz, heads, nblocks, 2).sum((0, 2))
+        if not value_used:
+            # value' unused (the last level): B^ and value get no gradient, so
+            # the outer scan's state backward is not woken for nothing
+            db, db_first, dvalue_out = None, None, None
+        return dkey, dvalue_out, da, db, da_first, db_first, deta, None, None
+
+
+def level_mix(key: Tensor, value: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: Tensor | None,
+              b_first: Tensor | None, eta: Tensor, chunk: int, offset: int):
+    """(write, key', value') of one level.  key [B,T,H,Dk], value [B,T,H,Dv];
+    a_vm [B,H,N,M,Dk] and b_vm [B,H,N,Dv,M]: the scans' value-major chunk-start
+    states; a_first [B,H,Dk,M] / b_first [B,H,M,Dv]: cached block-0 snapshots
+    (None: block 0 is the scans' initial state); eta [H,2]."""
+    return _LevelMix.apply(key, value, a_vm, b_vm, a_first, b_first, eta, chunk, offset)

@@ -143,9 +143,10 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
 
 def summarize_trace(path: str, gap_ms: float = 100.0, top: int = 25) -> str:
     """Markdown summary of a rocprofv3 `--kernel-trace --output-format csv`
-    kernel trace: per-kernel calls, total and average duration over the whole
-    run, and over the dispatches after the last idle gap of at least `gap_ms`
-    (bench.py leaves such a gap before its single-stream timing step)."""
+    kernel trace: per-kernel calls, total and average duration, busy time and
+    concurrency, over the whole run and over each segment that follows an idle
+    gap of at least `gap_ms` (bench.py leaves one before its timed steps and
+    one before its single-stream timing step)."""
     import csv
 
     with open(path, newline="") as f:
@@ -153,10 +154,10 @@ def summarize_trace(path: str, gap_ms: float = 100.0, top: int = 25) -> str:
     recs = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in rows)
     if not recs:
         return "(empty trace)\n"
-    cut, last_end = 0, recs[0][1]
+    cuts, last_end = [], recs[0][1]
     for i, (b, e, _) in enumerate(recs[1:], 1):
         if b - last_end >= gap_ms * 1e6:
-            cut = i
+            cuts.append(i)
         last_end = max(last_end, e)
 
     def short(name: str) -> str:
@@ -177,17 +178,27 @@ def summarize_trace(path: str, gap_ms: float = 100.0, top: int = 25) -> str:
             stats[short(n)] = (c + 1, t + (e - b))
         span = (max(e for _, e, _ in part) - min(b for b, _, _ in part)) / 1e6
         total = sum(t for _, t in stats.values())
+        busy, cur_b, cur_e = 0, None, None  # union of the kernel intervals
+        for b, e, _ in sorted(part):
+            if cur_e is None or b > cur_e:
+                busy += (cur_e - cur_b) if cur_e is not None else 0
+                cur_b, cur_e = b, e
+            else:
+                cur_e = max(cur_e, e)
+        busy = (busy + cur_e - cur_b) / 1e6
         lines = [f"### {title}", "",
                  f"{len(part)} dispatches, {len(stats)} kernels, {total / 1e6:.2f} ms kernel time "
-                 f"in a {span:.2f} ms span.", "",
+                 f"in a {span:.2f} ms span; some kernel running for {busy:.2f} ms "
+                 f"(mean concurrency {total / 1e6 / max(busy, 1e-9):.2f} while busy).", "",
                  "| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
         for n, (c, t) in sorted(stats.items(), key=lambda kv: -kv[1][1])[:top]:
             lines.append(f"| `{n}` | {c} | {t / 1e6:.2f} | {t / c / 1e3:.1f} | {100 * t / total:.2f} |")
         return "\n".join(lines) + "\n"
 
     out = table(recs, "Whole run")
-    if cut:
-        out += "\n" + table(recs[cut:], f"After the last idle gap of at least {gap_ms:g} ms")
+    bounds = cuts + [len(recs)]
+    for n, (lo, hi) in enumerate(zip(bounds[:-1], bounds[1:]), 1):
+        out += "\n" + table(recs[lo:hi], f"Segment {n} after an idle gap of at least {gap_ms:g} ms")
     return out
 
 

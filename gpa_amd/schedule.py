@@ -30,6 +30,8 @@ from torch import Tensor
 
 from . import _lib
 from .ops import gdn_scan_hip
+from .level import level_mix
+from .level import supported as fused_level_supported
 from .route import route_reader
 from .route import supported as fused_route_supported
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
@@ -169,23 +171,26 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
              (q, key, slot, g_in, b_in, old.inner)),
             (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **scan),
              (slot, value, g_out, b_out, old.outer))])
-        a_hat = _snapshots(a_starts, snap.inner)       # [B,H,N,Dk,M]
-        b_hat = _snapshots(b_starts, snap.outer)       # [B,H,N,M,Dv]
+        # Snapshots: block 0 uses the cached ones, which are the scans' own
+        # initial states unless the call starts inside a block.
+        first_a = None if snap.inner is old.inner else snap.inner
+        first_b = None if snap.outer is old.outer else snap.outer
+        eta = 1 + .25 * model.residual_raw[j].tanh()
         write = _assignment(cfg, slot)
-        if write is None:
-            kb = blocks.split(_unit(key).float())       # [B,N,C,H,Dk]
-            write = blocks.merge(torch.einsum("bnchd,bhndm->bnchm", kb, a_hat)).softmax(-1)
-        write = write.to(dtype)
+        if write is None and _FUSED_LEVEL[0] and fused_level_supported(cfg, dtype, key.shape[-1], value.shape[-1],
+                                                                       slot.shape[-1]):
+            write, key_next, value_next = level_mix(key, value, a_starts.transpose(-1, -2),
+                                                    b_starts.transpose(-1, -2), first_a, first_b, eta, chunk, offset)
+        else:
+            write, key_next, value_next = _level_mix_torch(key, value, a_starts, b_starts, snap.inner, snap.outer,
+                                                           eta, blocks, write)
         counts = old.count[:, None] + _cumsum_tokens(write.float())
-        wb = blocks.split(write.float())
-        rk = blocks.merge(torch.einsum("bhndm,bnchm->bnchd", a_hat, wb))
-        rv = blocks.merge(torch.einsum("bnchm,bhnmv->bnchv", wb, b_hat))
         lv.slot, lv.value, lv.g_out, lv.b_out = slot, value, g_out, b_out
         lv.write, lv.counts = write, counts
         lv.logits = _base_logits(model, raw, counts, j)
         lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, a_starts, b_starts
         levels.append(lv)
-        key, value = _residual(model, key, value, rk, rv, j)
+        key, value = key_next, value_next
 
     # ---- relations, attention.py:206-223
     local = [lv.logits.softmax(-1).to(dtype) for lv in levels]
@@ -345,9 +350,34 @@ def _base_logits(model, raw: Tensor, counts: Tensor, j: int) -> Tensor:
 def _residual(model, key, value, rk, rv, j):
     """attention.py:190-194."""
     eta = 1 + .25 * model.residual_raw[j].tanh()
+    return _residual_eta(key, value, rk, rv, eta)
+
+
+def _residual_eta(key, value, rk, rv, eta):
     new_key = (key - eta[:, 0, None] * rk.to(key.dtype)).to(key.dtype)
     new_value = (value - eta[:, 1, None] * rv.to(value.dtype)).to(value.dtype)
     return new_key, new_value
+
+
+_FUSED_LEVEL = [True]  # the fused level write and residual (level.py)
+
+
+def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):
+    """The level write and residual as device ops (attention.py:314-329): the
+    write (unless given by the slot feature), A^ w, w^T B^ and the residual
+    step, from the block snapshots ([B,H,N,Dk,M] / [B,H,N,M,Dv] views of the
+    scans' states, block 0 from the cached snapshots)."""
+    dtype = key.dtype
+    a_hat = _snapshots(a_starts, snap_inner)       # [B,H,N,Dk,M]
+    b_hat = _snapshots(b_starts, snap_outer)       # [B,H,N,M,Dv]
+    if write is None:
+        kb = blocks.split(_unit(key).float())       # [B,N,C,H,Dk]
+        write = blocks.merge(torch.einsum("bnchd,bhndm->bnchm", kb, a_hat)).softmax(-1)
+    write = write.to(dtype)
+    wb = blocks.split(write.float())
+    rk = blocks.merge(torch.einsum("bhndm,bnchm->bnchd", a_hat, wb))
+    rv = blocks.merge(torch.einsum("bnchm,bhnmv->bnchv", wb, b_hat))
+    return (write, *_residual_eta(key, value, rk, rv, eta))
 
 
 def _relations(model, local, writes, rel_states, scan):

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 5
+#define GPA_HIP_ABI_VERSION 6
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -249,6 +249,44 @@ int gpa_route_backward(const gpa_route_problem *problem, const gpa_route_grads *
  * (each rounded to the activation type, as the reference's typed products are). */
 int gpa_route_weight_grads(const gpa_route_problem *problem, const gpa_route_grads *grads, float *d_up,
                            float *d_down, float *d_rs, float *d_qs, hipStream_t stream);
+
+/* ---------------------------------------------------------------- level mix
+ * The block-lagged write and residual of one level (reference _block_segment,
+ * attention.py:314-329; _residual :190-194), for every token t of block n of
+ * every stream, from the block-start snapshots A^_n [Dk][M] and B^_n [M][Dv]:
+ *   w   = softmax(u(key) A^_n)                    (rounded to the activation type)
+ *   rk  = A^_n w,  rv = w^T B^_n                  (each rounded)
+ *   key' = key - eta0 rk,  value' = value - eta1 rv   (rounded)
+ * A^_n, B^_n are the scans' chunk-start states (value-major, as gdn_scan
+ * saves them) except block 0, which may come from a cached snapshot.  Blocks
+ * follow the scan geometry: block n holds tokens n*chunk - offset .. +chunk-1. */
+#define GPA_LEVEL_MAX_WIDTH 256     /* key_dim, value_dim and slots */
+
+typedef struct gpa_level_problem {
+    int32_t batch, tokens, heads, key_dim, value_dim, slots, chunk, offset, dtype;
+    gpa_operand key, value;              /* [B,T,H,Dk], [B,T,H,Dv] */
+    const float *a_states, *b_states;    /* [B,H,N][M][Dk] and [B,H,N][Dv][M] float32, contiguous */
+    const float *a_first, *b_first;      /* block-0 snapshots [B,H][Dk][M], [B,H][M][Dv], or NULL */
+    int64_t a_first_sb, b_first_sb;      /* their batch strides (0: broadcast over the batch) */
+    const float *eta;                    /* [H][2]: 1 + .25 tanh(residual_raw[j]) */
+    gpa_operand write, key_out, value_out;   /* outputs */
+    void *rk, *rv;                       /* saved rounded reconstructions, contiguous [B,T,H,Dk], [B,T,H,Dv] */
+    float *stats;                        /* saved softmax row max and sum, contiguous [B,T,H,2] */
+} gpa_level_problem;
+
+typedef struct gpa_level_grads {
+    gpa_operand dwrite, dkey_out, dvalue_out;  /* incoming; dwrite excludes the rk/rv paths */
+    gpa_operand dkey;                          /* out: the gradient of key through this step */
+    float *da_states, *db_states;              /* out, layouts of a_states / b_states (block 0 included
+                                                  unless a_first is given) */
+    float *da_first, *db_first;                /* out when a_first / b_first are given: [B,H][Dk][M], [B,H][M][Dv] */
+    float *deta;                               /* out [B*H*N][2]: per-block sums of d eta0, d eta1 */
+} gpa_level_grads;
+
+/* Forward / backward of the level write and residual (the reference's level
+ * glue at attention.py:314-329, autograd through it for the backward). */
+int gpa_level_forward(const gpa_level_problem *problem, hipStream_t stream);
+int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *grads, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -23,19 +23,21 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 CLANG = "/opt/rocm/llvm/bin/clang++"
-ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3}
+ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3,
+           "gpa_level_forward": 4, "gpa_level_backward": 5}
+SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip"]
 
 
 def compiler() -> str | None:
     return CLANG if os.path.exists(CLANG) else shutil.which("clang++")
 
 
-def build(out_dir: str, sources) -> str:
+def build(out_dir: str, sources=None) -> str:
     exe = os.path.join(out_dir, "host_runner")
     cmd = [compiler(), "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
            "-Wno-unused-command-line-argument", "-I", HERE, "-I", os.path.join(ROOT, "include"),
            "-I", os.path.join(ROOT, "gpa_amd", "csrc"), "-x", "c++"]
-    cmd += [os.path.join(ROOT, "gpa_amd", "csrc", s) for s in sources]
+    cmd += [os.path.join(ROOT, "gpa_amd", "csrc", s) for s in (sources or SOURCES)]
     cmd += ["-x", "none", os.path.join(HERE, "runner.cpp"), "-o", exe, "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode:
@@ -128,6 +130,12 @@ class HostLib:
 
     def gpa_route_weight_grads(self, prob, grads, d_up, d_down, d_rs, d_qs, stream):
         return self._call("gpa_route_weight_grads", [prob, grads], [d_up, d_down, d_rs, d_qs])
+
+    def gpa_level_forward(self, prob, stream):
+        return self._call("gpa_level_forward", [prob])
+
+    def gpa_level_backward(self, prob, grads, stream):
+        return self._call("gpa_level_backward", [prob, grads])
 
     def gpa_hip_last_error(self):
         return b""

@@ -81,6 +81,13 @@ int main(int argc, char** argv) {
                                   static_cast<float*>(raw.at(0)), static_cast<float*>(raw.at(1)),
                                   static_cast<float*>(raw.at(2)), static_cast<float*>(raw.at(3)), nullptr);
       break;
+    case 4:
+      rc = gpa_level_forward(reinterpret_cast<gpa_level_problem*>(blobs.at(0).data()), nullptr);
+      break;
+    case 5:
+      rc = gpa_level_backward(reinterpret_cast<gpa_level_problem*>(blobs.at(0).data()),
+                              reinterpret_cast<gpa_level_grads*>(blobs.at(1).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

@@ -28,7 +28,7 @@ CASES = {
 def runner(tmp_path_factory):
     if harness.compiler() is None:
         pytest.skip("no host clang")
-    return harness.build(str(tmp_path_factory.mktemp("host_emu")), ["gpa_decode.hip", "route_reader.hip"])
+    return harness.build(str(tmp_path_factory.mktemp("host_emu")))
 
 
 def _rel(a, b):
