@@ -59,23 +59,6 @@ __device__ __forceinline__ Split8 load_split(const __bf16* p) {
   return s;
 }
 
-__device__ __forceinline__ Split8 negate(const Split8& a) {
-  Split8 s;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s.hi[e] = (__bf16)(-(float)a.hi[e]);
-    s.lo[e] = (__bf16)(-(float)a.lo[e]);
-  }
-  return s;
-}
-
-// hi*hi + hi*lo + lo*hi
-__device__ __forceinline__ f32x16 mfma3(const Split8& a, bf16x8 bh, bf16x8 bl, f32x16 c) {
-  c = mfma(a.hi, bh, c);
-  c = mfma(a.hi, bl, c);
-  return mfma(a.lo, bh, c);
-}
-
 // Write a 32x32 fp32 tile, transposed and split into bf16 hi/lo, to
 // hi[(col0 + col) * ld + row0 + row] and lo[...].
 __device__ __forceinline__ void put_split_t(__bf16* hi, __bf16* lo, int ld, int row0, int col0, const f32x16& acc,
@@ -100,18 +83,21 @@ __device__ __forceinline__ bf16x8 lds_frag(const __bf16* lds, int ld, int col0, 
 }
 
 // A value-major [V][R] tile column v, rows row0 + 8g + 4(l/32) + 0..3 for g < 4,
-// as the 16 accumulator elements of lane l (zero when v >= V).
+// as the 16 accumulator elements of lane l (zero when v >= V).  GUARD = false
+// when the caller knows v < V.
+template <bool GUARD = true>
 __device__ __forceinline__ void load_acc_vc(float (&x)[16], const float* m, int v, int V, int row0, int l) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (v < V) q = *reinterpret_cast<const float4*>(m + (int64_t)v * R + row0 + 8 * g + 4 * (l >> 5));
+    if (!GUARD || v < V) q = *reinterpret_cast<const float4*>(m + (int64_t)v * R + row0 + 8 * g + 4 * (l >> 5));
     x[4 * g] = q.x; x[4 * g + 1] = q.y; x[4 * g + 2] = q.z; x[4 * g + 3] = q.w;
   }
 }
 
+template <bool GUARD = true>
 __device__ __forceinline__ void store_acc_vc(float* m, int v, int V, int row0, const f32x16& x, int l) {
-  if (v >= V) return;
+  if (GUARD && v >= V) return;
 #pragma unroll
   for (int g = 0; g < 4; ++g)
     *reinterpret_cast<float4*>(m + (int64_t)v * R + row0 + 8 * g + 4 * (l >> 5)) =
@@ -119,22 +105,24 @@ __device__ __forceinline__ void store_acc_vc(float* m, int v, int V, int row0, c
 }
 
 // Value-major [V][K] state tile: rows k0 + 8g + 4(l/32) + 0..3, column v.
+template <bool GUARD = true>
 __device__ __forceinline__ void store_state(float* m, int v, int V, int K, int k0, const f32x16& x, int l) {
-  if (v >= V) return;
+  if (GUARD && v >= V) return;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int k = k0 + 8 * g + 4 * (l >> 5);
-    if (k < K)
+    if (!GUARD || k < K)
       *reinterpret_cast<float4*>(m + (int64_t)v * K + k) = make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]);
   }
 }
 
+template <bool GUARD = true>
 __device__ __forceinline__ void add_state(f32x16& x, const float* m, int v, int V, int K, int k0, int l) {
-  if (v >= V) return;
+  if (GUARD && v >= V) return;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int k = k0 + 8 * g + 4 * (l >> 5);
-    if (k < K) {
+    if (!GUARD || k < K) {
       const float4 q = *reinterpret_cast<const float4*>(m + (int64_t)v * K + k);
       x[4 * g] += q.x; x[4 * g + 1] += q.y; x[4 * g + 2] += q.z; x[4 * g + 3] += q.w;
     }
@@ -170,7 +158,24 @@ __device__ __forceinline__ void store_km(float* m, int64_t base, int v, int V, i
 
 }  // namespace
 
-template <int KM>
+// Chunk operand addresses.  `Fast` kernels assume K == KM and V % 64 == 0, so
+// every fragment and column they touch exists and the chunk loop is straight
+// line code; the general instantiation guards k steps, row blocks and
+// columns.
+template <int KM, bool FAST>
+struct Shape {
+  int K, V, K16;
+  __device__ __forceinline__ Shape(const gpa_gdn_problem& p)
+      : K(FAST ? KM : p.kdim), V(p.vdim), K16((FAST ? KM : p.kdim) / 16) {}
+  __device__ __forceinline__ bool kstep(int ks) const { return FAST || ks < K16; }
+  __device__ __forceinline__ bool rows(int rb) const { return FAST || 32 * rb < K; }
+  __device__ __forceinline__ bool col(int v) const { return FAST || v < V; }
+};
+
+// Loads whose next-chunk copy is issued right after the last use of the
+// current one: with every operand reloaded as soon as it is dead, each load
+// has a whole chunk step to arrive, and no extra registers are needed.
+template <int KM, bool FAST>
 __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
   constexpr int KLD = KM + TPAD;
   constexpr int NRB = KM / 32 >= 4 ? KM / 128 : 1;  // 32-row blocks of the state per wave
@@ -179,9 +184,9 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
   __bf16* sl = sh + MV * KLD;                        // [MV][KLD]  S^T lo
   __bf16* dh = sl + MV * KLD;                        // [MV][CT]   (e^{G_C-G} D)^T hi
   __bf16* dl = dh + MV * CT;                         // [MV][CT]   lo
+  const Shape<KM, FAST> sp(p);
   const int s = blockIdx.y, b = s / p.heads, h = s % p.heads;
-  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int K16 = K / 16;
+  const int K = sp.K, V = sp.V, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int v0 = blockIdx.x * MV;
   const bool owns = (KM / 32 >= 4) || w < KM / 32;  // row blocks rb = w + 4*i
   const int rt = w >> 1, ct = w & 1;               // this wave's D tile
@@ -195,33 +200,26 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
       load_km(acc[i][cb], p.s0, (int64_t)b * p.s0_sb + (int64_t)h * p.s0_sh, v0 + 32 * cb + (l & 31), V, K,
               owns ? 32 * (w + 4 * i) : K, l);
 
-  // Loop-carried chunk-start operands.
+  const __bf16* wrow = reinterpret_cast<const __bf16*>(sv.wrow) + (int64_t)s * nch * frag_row;
+  const __bf16* kcol = reinterpret_cast<const __bf16*>(sv.kcol) + (int64_t)s * nch * frag_col;
+  auto w_at = [&](int n, int ks) { return wrow + (int64_t)n * frag_row + ((rt * sp.K16 + ks) * 64 + l) * 16; };
+  auto k_at = [&](int n, int rb, int cs) { return kcol + (int64_t)n * frag_col + ((rb * 4 + cs) * 64 + l) * 8; };
   Split8 wr[KM / 16];
+  bf16x8 kf[NRB][R / 16];
   float ur[16], gr_[16], gcr;
-  auto load_start = [&](int n) {
-    const __bf16* wf = reinterpret_cast<const __bf16*>(sv.wrow) + ((int64_t)s * nch + n) * frag_row;
 #pragma unroll
-    for (int ks = 0; ks < KM / 16; ++ks)
-      if (ks < K16) wr[ks] = load_split(wf + ((rt * K16 + ks) * 64 + l) * 16);
-    load_acc_vc(ur, sv.u + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
-    load_gates(gr_, gcr, sv.gam + rows_off(s, n, nch, 0, 1), 32 * rt, l);
-  };
-  load_start(0);
+  for (int ks = 0; ks < KM / 16; ++ks)
+    if (sp.kstep(ks)) wr[ks] = load_split(w_at(0, ks));
+#pragma unroll
+  for (int i = 0; i < NRB; ++i)
+#pragma unroll
+    for (int cs = 0; cs < R / 16; ++cs)
+      kf[i][cs] = owns && sp.rows(w + 4 * i) ? *reinterpret_cast<const bf16x8*>(k_at(0, w + 4 * i, cs)) : bf16x8{};
+  load_acc_vc<!FAST>(ur, sv.u + vc_off(s, 0, nch, V), vd, V, 32 * rt, l);
+  load_gates(gr_, gcr, sv.gam + rows_off(s, 0, nch, 0, 1), 32 * rt, l);
+
   for (int n = 0; n < nch; ++n) {
-    const int64_t cid = (int64_t)s * nch + n;
-    // This chunk's GEMM2 operands (Kn^T fragments).
-    bf16x8 kf[NRB][R / 16];
-    {
-      const __bf16* kc = reinterpret_cast<const __bf16*>(sv.kcol) + cid * frag_col;
-#pragma unroll
-      for (int i = 0; i < NRB; ++i)
-#pragma unroll
-        for (int cs = 0; cs < R / 16; ++cs) {
-          const int rb = w + 4 * i;
-          if (owns && 32 * rb < K) kf[i][cs] = *reinterpret_cast<const bf16x8*>(kc + ((rb * 4 + cs) * 64 + l) * 8);
-          else kf[i][cs] = bf16x8{};
-        }
-    }
+    const int nn = n + 1 < nch ? n + 1 : n;  // operands of the next chunk (reloaded once at the end)
     // (a) S_n -> saved states (value-major) and LDS (transposed, split).
     if (owns) {
       float* sm = sv.states + state_off(s, n, nch, K, V);
@@ -230,41 +228,83 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           const int k0 = 32 * (w + 4 * i);
-          store_state(sm, v0 + 32 * cb + (l & 31), V, K, k0, acc[i][cb], l);
-          put_split_t(sh, sl, KLD, k0, 32 * cb, acc[i][cb], l);
+          if (sp.rows(w + 4 * i)) {
+            store_state<!FAST>(sm, v0 + 32 * cb + (l & 31), V, K, k0, acc[i][cb], l);
+            put_split_t(sh, sl, KLD, k0, 32 * cb, acc[i][cb], l);
+          }
         }
     }
     lds_barrier();
-    // (c) D = U - W S for the (rt, ct) tile.
-    f32x16 d = {};
+    // (c) D = U - W S for the (rt, ct) tile; each W fragment is reloaded once used.
+    // Two accumulation chains (hi*hi + lo*hi, hi*lo), and the LDS fragments of
+    // the next k step are read while the current one multiplies.
+    f32x16 d;
+    {
+      f32x16 d1 = {}, d2 = {};
+      bf16x8 fb[2][2];
+      fb[0][0] = lds_frag(sh, KLD, 32 * ct, 0, l);
+      fb[0][1] = lds_frag(sl, KLD, 32 * ct, 0, l);
 #pragma unroll
-    for (int ks = 0; ks < KM / 16; ++ks)
-      if (ks < K16) d = mfma3(wr[ks], lds_frag(sh, KLD, 32 * ct, 16 * ks, l), lds_frag(sl, KLD, 32 * ct, 16 * ks, l), d);
+      for (int ks = 0; ks < KM / 16; ++ks)
+        if (sp.kstep(ks)) {
+          if (ks + 1 < KM / 16 && sp.kstep(ks + 1)) {
+            fb[(ks + 1) & 1][0] = lds_frag(sh, KLD, 32 * ct, 16 * (ks + 1), l);
+            fb[(ks + 1) & 1][1] = lds_frag(sl, KLD, 32 * ct, 16 * (ks + 1), l);
+          }
+          const bf16x8 bh = fb[ks & 1][0], bl = fb[ks & 1][1];
+          d1 = mfma(wr[ks].hi, bh, d1);
+          d2 = mfma(wr[ks].hi, bl, d2);
+          d1 = mfma(wr[ks].lo, bh, d1);
+          wr[ks] = load_split(w_at(nn, ks));
+        }
+      d = d1 + d2;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) d[r] = ur[r] - d[r];
-    store_acc_vc(sv.delta + vc_off(s, n, nch, V), vd, V, 32 * rt, d, l);
+    load_acc_vc<!FAST>(ur, sv.u + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
+    store_acc_vc<!FAST>(sv.delta + vc_off(s, n, nch, V), vd, V, 32 * rt, d, l);
 #pragma unroll
     for (int r = 0; r < 16; ++r) d[r] *= __expf(gcr - gr_[r]);
-    put_split_t(dh, dl, CT, 32 * rt, 32 * ct, d, l);
     const float decay = __expf(gcr);
-    if (n + 1 < nch) load_start(n + 1);
+    load_gates(gr_, gcr, sv.gam + rows_off(s, nn, nch, 0, 1), 32 * rt, l);
+    put_split_t(dh, dl, CT, 32 * rt, 32 * ct, d, l);
     lds_barrier();
-    // (e) S = e^{G_C} S + Kn^T (e^{G_C-G} D).
+    // (e) S = e^{G_C} S + Kn^T (e^{G_C-G} D); each Kn^T fragment is reloaded once used.
+    // The next (a) writes only sh/sl, which no wave reads after the barrier above,
+    // and the next (c) epilogue writes dh/dl only after the next barrier, so the
+    // step needs no closing barrier.
     if (owns) {
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
         acc[i][0] *= decay;
         acc[i][1] *= decay;
+      }
+      bf16x8 fb[2][2][2];  // [buffer][cb][hi, lo]
 #pragma unroll
-        for (int cs = 0; cs < R / 16; ++cs)
+      for (int cb = 0; cb < 2; ++cb) {
+        fb[0][cb][0] = lds_frag(dh, CT, 32 * cb, 0, l);
+        fb[0][cb][1] = lds_frag(dl, CT, 32 * cb, 0, l);
+      }
+#pragma unroll
+      for (int cs = 0; cs < R / 16; ++cs) {
+        if (cs + 1 < R / 16) {
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb) {
-            acc[i][cb] = mfma(kf[i][cs], lds_frag(dh, CT, 32 * cb, 16 * cs, l), acc[i][cb]);
-            acc[i][cb] = mfma(kf[i][cs], lds_frag(dl, CT, 32 * cb, 16 * cs, l), acc[i][cb]);
+            fb[(cs + 1) & 1][cb][0] = lds_frag(dh, CT, 32 * cb, 16 * (cs + 1), l);
+            fb[(cs + 1) & 1][cb][1] = lds_frag(dl, CT, 32 * cb, 16 * (cs + 1), l);
           }
+        }
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int i = 0; i < NRB; ++i)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma(kf[i][cs], fb[cs & 1][cb][h2], acc[i][cb]);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+          if (sp.rows(w + 4 * i)) kf[i][cs] = *reinterpret_cast<const bf16x8*>(k_at(nn, w + 4 * i, cs));
       }
     }
-    lds_barrier();
   }
   if (owns) {
 #pragma unroll
@@ -275,7 +315,7 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
   }
 }
 
-template <int KM>
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
 __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
                                                           int nch) {
   constexpr int KLD = KM + TPAD;
@@ -283,15 +323,14 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __bf16* sh = reinterpret_cast<__bf16*>(smem_raw);  // [MV][KLD]  dS^T hi
   __bf16* sl = sh + MV * KLD;                        // [MV][KLD]  lo
-  __bf16* dh = sl + MV * KLD;                        // [MV][CT]   dD^T hi
+  __bf16* dh = sl + MV * KLD;                        // [MV][CT]   -dD^T hi
   __bf16* dl = dh + MV * CT;                         // [MV][CT]   lo
   __bf16* oh = dl + MV * CT;                         // [MV][CT]   o^T hi
   __bf16* ol = oh + MV * CT;                         // [MV][CT]   lo
+  const Shape<KM, FAST> sp(p);
   const int s = blockIdx.y;
-  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int K16 = K / 16;
+  const int K = sp.K, V = sp.V, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int v0 = blockIdx.x * MV;
-  const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr;
   const bool owns = (KM / 32 >= 4) || w < KM / 32;
   const int rt = w >> 1, ct = w & 1;
   const int vd = v0 + 32 * ct + (l & 31);
@@ -304,57 +343,53 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
       load_km(acc[i][cb], gr.dfinal, (int64_t)s * K * V, v0 + 32 * cb + (l & 31), V, K, owns ? 32 * (w + 4 * i) : K,
               l);
 
-  // Loop-carried chunk-start operands.
+  const __bf16* krow = reinterpret_cast<const __bf16*>(sv.krow) + (int64_t)s * nch * frag_row;
+  const __bf16* wcol = reinterpret_cast<const __bf16*>(sv.wcol) + (int64_t)s * nch * frag_wcol;
+  const __bf16* qcol = HAS_Q ? reinterpret_cast<const __bf16*>(sv.qcol) + (int64_t)s * nch * frag_col : nullptr;
+  auto k_at = [&](int n, int ks) { return krow + (int64_t)n * frag_row + ((rt * sp.K16 + ks) * 64 + l) * 8; };
+  auto w_at = [&](int n, int rb, int cs) { return wcol + (int64_t)n * frag_wcol + ((rb * 4 + cs) * 64 + l) * 16; };
+  auto q_at = [&](int n, int rb, int cs) { return qcol + (int64_t)n * frag_col + ((rb * 4 + cs) * 64 + l) * 8; };
   bf16x8 kr[KM / 16];
+  Split8 wf[NRB][R / 16];
+  bf16x8 qf[HAS_Q ? NRB : 1][R / 16];
+  f32x16 inj[HAS_INJ ? NRB : 1][2];
   float d0r[16], orr[16], gr_[16], gcr;
-  auto load_start = [&](int n) {
-    const __bf16* kf = reinterpret_cast<const __bf16*>(sv.krow) + ((int64_t)s * nch + n) * frag_row;
+  auto load_inj = [&](int n) {
+    if constexpr (HAS_INJ) {
 #pragma unroll
-    for (int ks = 0; ks < KM / 16; ++ks)
-      if (ks < K16) kr[ks] = *reinterpret_cast<const bf16x8*>(kf + ((rt * K16 + ks) * 64 + l) * 8);
-    if (gr.dd0) {
-      load_acc_vc(d0r, gr.dd0 + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) d0r[r] = 0.f;
-    }
-    if (has_q) {
-      load_acc_vc(orr, gr.o + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) orr[r] = 0.f;
-    }
-    load_gates(gr_, gcr, sv.gam + rows_off(s, n, nch, 0, 1), 32 * rt, l);
-  };
-  load_start(nch - 1);
-  for (int n = nch - 1; n >= 0; --n) {
-    const int64_t cid = (int64_t)s * nch + n;
-    // This chunk's GEMM2 operands (W^T, Qn^T fragments) and state injections.
-    Split8 wf[NRB][R / 16];
-    bf16x8 qf[NRB][R / 16];
-    f32x16 inj[NRB][2];
-    {
-      const __bf16* wc = reinterpret_cast<const __bf16*>(sv.wcol) + cid * frag_wcol;
-      const __bf16* qc = has_q ? reinterpret_cast<const __bf16*>(sv.qcol) + cid * frag_col : nullptr;
-#pragma unroll
-      for (int i = 0; i < NRB; ++i) {
-        const int rb = w + 4 * i;
-        const bool ok = owns && 32 * rb < K;
-#pragma unroll
-        for (int cs = 0; cs < R / 16; ++cs) {
-          if (ok) wf[i][cs] = load_split(wc + ((rb * 4 + cs) * 64 + l) * 16);
-          else wf[i][cs] = Split8{bf16x8{}, bf16x8{}};
-          if (ok && has_q) qf[i][cs] = *reinterpret_cast<const bf16x8*>(qc + ((rb * 4 + cs) * 64 + l) * 8);
-          else qf[i][cs] = bf16x8{};
-        }
+      for (int i = 0; i < NRB; ++i)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           inj[i][cb] = f32x16{};
-          if (gr.dstates && ok)
-            add_state(inj[i][cb], gr.dstates + state_off(s, n, nch, K, V), v0 + 32 * cb + (l & 31), V, K, 32 * rb, l);
+          if (owns && sp.rows(w + 4 * i))
+            add_state<!FAST>(inj[i][cb], gr.dstates + state_off(s, n, nch, K, V), v0 + 32 * cb + (l & 31), V, K,
+                      32 * (w + 4 * i), l);
         }
+    }
+  };
+  {
+    const int n = nch - 1;
+#pragma unroll
+    for (int ks = 0; ks < KM / 16; ++ks)
+      if (sp.kstep(ks)) kr[ks] = *reinterpret_cast<const bf16x8*>(k_at(n, ks));
+#pragma unroll
+    for (int i = 0; i < NRB; ++i) {
+      const bool ok = owns && sp.rows(w + 4 * i);
+#pragma unroll
+      for (int cs = 0; cs < R / 16; ++cs) {
+        wf[i][cs] = ok ? load_split(w_at(n, w + 4 * i, cs)) : Split8{bf16x8{}, bf16x8{}};
+        if constexpr (HAS_Q) qf[i][cs] = ok ? *reinterpret_cast<const bf16x8*>(q_at(n, w + 4 * i, cs)) : bf16x8{};
       }
     }
+    if constexpr (HAS_Q) {
+      load_acc_vc<!FAST>(d0r, gr.dd0 + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
+      load_acc_vc<!FAST>(orr, gr.o + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
+    }
+    load_gates(gr_, gcr, sv.gam + rows_off(s, n, nch, 0, 1), 32 * rt, l);
+    load_inj(n);
+  }
+  for (int n = nch - 1; n >= 0; --n) {
+    const int nn = n > 0 ? n - 1 : 0;  // operands of the next (earlier) chunk
     // (a) dS -> dhend (value-major) and LDS (transposed, split).
     if (owns) {
       float* dm = gr.dhend + state_off(s, n, nch, K, V);
@@ -363,55 +398,110 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           const int k0 = 32 * (w + 4 * i);
-          store_state(dm, v0 + 32 * cb + (l & 31), V, K, k0, acc[i][cb], l);
-          put_split_t(sh, sl, KLD, k0, 32 * cb, acc[i][cb], l);
-        }
-    }
-    lds_barrier();
-    // (c) dD = dd0 + e^{G_C-G} (Kn dS); stage o^T.
-    f32x16 d = {};
-#pragma unroll
-    for (int ks = 0; ks < KM / 16; ++ks)
-      if (ks < K16) {
-        d = mfma(kr[ks], lds_frag(sh, KLD, 32 * ct, 16 * ks, l), d);
-        d = mfma(kr[ks], lds_frag(sl, KLD, 32 * ct, 16 * ks, l), d);
-      }
-    f32x16 o;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      d[r] = d0r[r] + __expf(gcr - gr_[r]) * d[r];
-      o[r] = orr[r];
-    }
-    store_acc_vc(gr.ddelta + vc_off(s, n, nch, V), vd, V, 32 * rt, d, l);
-    put_split_t(dh, dl, CT, 32 * rt, 32 * ct, d, l);
-    put_split_t(oh, ol, CT, 32 * rt, 32 * ct, o, l);
-    const float decay = __expf(gcr);
-    if (n > 0) load_start(n - 1);
-    lds_barrier();
-    // (e) dS = e^{G_C} dS + Qn^T o - W^T dD + dstates[n].
-    if (owns) {
-#pragma unroll
-      for (int i = 0; i < NRB; ++i) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) acc[i][cb] = acc[i][cb] * decay + inj[i][cb];
-#pragma unroll
-        for (int cs = 0; cs < R / 16; ++cs) {
-          const Split8 aw = negate(wf[i][cs]);
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-            acc[i][cb] = mfma3(aw, lds_frag(dh, CT, 32 * cb, 16 * cs, l), lds_frag(dl, CT, 32 * cb, 16 * cs, l),
-                               acc[i][cb]);
-          if (has_q) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-              acc[i][cb] = mfma(qf[i][cs], lds_frag(oh, CT, 32 * cb, 16 * cs, l), acc[i][cb]);
-              acc[i][cb] = mfma(qf[i][cs], lds_frag(ol, CT, 32 * cb, 16 * cs, l), acc[i][cb]);
-            }
+          if (sp.rows(w + 4 * i)) {
+            store_state<!FAST>(dm, v0 + 32 * cb + (l & 31), V, K, k0, acc[i][cb], l);
+            put_split_t(sh, sl, KLD, k0, 32 * cb, acc[i][cb], l);
           }
         }
-      }
     }
     lds_barrier();
+    // (c) dD = dd0 + e^{G_C-G} (Kn dS); stage o^T.  Kn fragments are reloaded once
+    // used; hi and lo parts accumulate in separate chains and the next k step's
+    // LDS fragments are read while the current one multiplies.
+    f32x16 d;
+    {
+      f32x16 d1 = {}, d2 = {};
+      bf16x8 fb[2][2];
+      fb[0][0] = lds_frag(sh, KLD, 32 * ct, 0, l);
+      fb[0][1] = lds_frag(sl, KLD, 32 * ct, 0, l);
+#pragma unroll
+      for (int ks = 0; ks < KM / 16; ++ks)
+        if (sp.kstep(ks)) {
+          if (ks + 1 < KM / 16 && sp.kstep(ks + 1)) {
+            fb[(ks + 1) & 1][0] = lds_frag(sh, KLD, 32 * ct, 16 * (ks + 1), l);
+            fb[(ks + 1) & 1][1] = lds_frag(sl, KLD, 32 * ct, 16 * (ks + 1), l);
+          }
+          d1 = mfma(kr[ks], fb[ks & 1][0], d1);
+          d2 = mfma(kr[ks], fb[ks & 1][1], d2);
+          kr[ks] = *reinterpret_cast<const bf16x8*>(k_at(nn, ks));
+        }
+      d = d1 + d2;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) d[r] = (HAS_Q ? d0r[r] : 0.f) + __expf(gcr - gr_[r]) * d[r];
+    const float decay = __expf(gcr);
+    load_gates(gr_, gcr, sv.gam + rows_off(s, nn, nch, 0, 1), 32 * rt, l);
+    store_acc_vc<!FAST>(gr.ddelta + vc_off(s, n, nch, V), vd, V, 32 * rt, d, l);
+    put_split_t(dh, dl, CT, 32 * rt, 32 * ct, -d, l);  // -dD: (e) adds W^T (-dD)
+    if constexpr (HAS_Q) {
+      f32x16 o;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[r] = orr[r];
+      put_split_t(oh, ol, CT, 32 * rt, 32 * ct, o, l);
+      load_acc_vc<!FAST>(d0r, gr.dd0 + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
+      load_acc_vc<!FAST>(orr, gr.o + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
+    }
+    lds_barrier();
+    // (e) dS = e^{G_C} dS + Qn^T o - W^T dD + dstates[n]; fragments are reloaded once
+    // used.  As in the forward kernel, no closing barrier is needed: the next (a)
+    // writes sh/sl only, and the next (c) epilogue writes dh..ol after a barrier.
+    if (owns) {
+#pragma unroll
+      for (int i = 0; i < NRB; ++i)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          acc[i][cb] *= decay;
+          if constexpr (HAS_INJ) acc[i][cb] += inj[i][cb];
+        }
+      constexpr int NF = HAS_Q ? 4 : 2;  // -dD hi, lo, o hi, lo
+      bf16x8 fb[2][2][NF];                // [buffer][cb][part]
+      auto read_b = [&](bf16x8 (&f)[2][NF], int cs) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          f[cb][0] = lds_frag(dh, CT, 32 * cb, 16 * cs, l);
+          f[cb][1] = lds_frag(dl, CT, 32 * cb, 16 * cs, l);
+          if constexpr (HAS_Q) {
+            f[cb][2] = lds_frag(oh, CT, 32 * cb, 16 * cs, l);
+            f[cb][3] = lds_frag(ol, CT, 32 * cb, 16 * cs, l);
+          }
+        }
+      };
+      read_b(fb[0], 0);
+#pragma unroll
+      for (int cs = 0; cs < R / 16; ++cs) {
+        if (cs + 1 < R / 16) read_b(fb[(cs + 1) & 1], cs + 1);
+        const auto& f = fb[cs & 1];
+        // W^T (-dD): hi*hi, hi*lo, lo*hi; then Qn^T o: q*hi, q*lo.  The chains of
+        // the (row block, column block) tiles are interleaved.
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma(wf[i][cs].hi, f[cb][0], acc[i][cb]);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma(wf[i][cs].hi, f[cb][1], acc[i][cb]);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma(wf[i][cs].lo, f[cb][0], acc[i][cb]);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+          if (sp.rows(w + 4 * i)) wf[i][cs] = load_split(w_at(nn, w + 4 * i, cs));
+        if constexpr (HAS_Q) {
+#pragma unroll
+          for (int h2 = 2; h2 < 4; ++h2)
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+#pragma unroll
+              for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma(qf[i][cs], f[cb][h2], acc[i][cb]);
+#pragma unroll
+          for (int i = 0; i < NRB; ++i)
+            if (sp.rows(w + 4 * i)) qf[i][cs] = *reinterpret_cast<const bf16x8*>(q_at(nn, w + 4 * i, cs));
+        }
+      }
+    }
+    load_inj(nn);
   }
   if (owns) {
 #pragma unroll
@@ -437,20 +527,42 @@ int allow_lds_mfma(F kernel, size_t bytes) {
 template <int KM>
 int launch_state_fwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStream_t st) {
   const size_t lds = sizeof(__bf16) * (2 * MV * (KM + TPAD) + 2 * MV * CT);
-  if (int rc = allow_lds_mfma(gdn_state_fwd_mfma<KM>, lds)) return rc;
-  hipLaunchKernelGGL((gdn_state_fwd_mfma<KM>), dim3((p.vdim + MV - 1) / MV, p.batch * p.heads), dim3(NT), lds, st,
-                     p, sv, nch);
+  const dim3 grid((p.vdim + MV - 1) / MV, p.batch * p.heads);
+  if (p.kdim == KM && p.vdim % MV == 0) {
+    if (int rc = allow_lds_mfma(gdn_state_fwd_mfma<KM, true>, lds)) return rc;
+    hipLaunchKernelGGL((gdn_state_fwd_mfma<KM, true>), grid, dim3(NT), lds, st, p, sv, nch);
+  } else {
+    if (int rc = allow_lds_mfma(gdn_state_fwd_mfma<KM, false>, lds)) return rc;
+    hipLaunchKernelGGL((gdn_state_fwd_mfma<KM, false>), grid, dim3(NT), lds, st, p, sv, nch);
+  }
   return GPA_HIP_OK;
+}
+
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+int launch_bwd(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch, hipStream_t st) {
+  const size_t lds = sizeof(__bf16) * (2 * MV * (KM + TPAD) + 4 * MV * CT);
+  if (int rc = allow_lds_mfma(gdn_state_bwd_mfma<KM, FAST, HAS_Q, HAS_INJ>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd_mfma<KM, FAST, HAS_Q, HAS_INJ>), dim3((p.vdim + MV - 1) / MV, p.batch * p.heads),
+                     dim3(NT), lds, st, p, sv, gr, nch);
+  return GPA_HIP_OK;
+}
+
+template <int KM, bool FAST>
+int launch_bwd_flags(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
+                     hipStream_t st) {
+  const bool has_q = p.q.ptr != nullptr && gr.dout.ptr != nullptr, has_inj = gr.dstates != nullptr;
+  if (has_q)
+    return has_inj ? launch_bwd<KM, FAST, true, true>(p, sv, gr, nch, st)
+                   : launch_bwd<KM, FAST, true, false>(p, sv, gr, nch, st);
+  return has_inj ? launch_bwd<KM, FAST, false, true>(p, sv, gr, nch, st)
+                 : launch_bwd<KM, FAST, false, false>(p, sv, gr, nch, st);
 }
 
 template <int KM>
 int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
                           hipStream_t st) {
-  const size_t lds = sizeof(__bf16) * (2 * MV * (KM + TPAD) + 4 * MV * CT);
-  if (int rc = allow_lds_mfma(gdn_state_bwd_mfma<KM>, lds)) return rc;
-  hipLaunchKernelGGL((gdn_state_bwd_mfma<KM>), dim3((p.vdim + MV - 1) / MV, p.batch * p.heads), dim3(NT), lds, st,
-                     p, sv, gr, nch);
-  return GPA_HIP_OK;
+  return p.kdim == KM && p.vdim % MV == 0 ? launch_bwd_flags<KM, true>(p, sv, gr, nch, st)
+                                          : launch_bwd_flags<KM, false>(p, sv, gr, nch, st);
 }
 
 template int launch_state_fwd_mfma<64>(const gpa_gdn_problem&, const gpa_gdn_saved&, int, hipStream_t);

@@ -53,6 +53,9 @@ class _GDNScan(torch.autograd.Function):
     def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int):
         lib = _lib.load()
         _in_use_here(q, k, v, g, beta, s0)
+        # Outputs nobody differentiates (often the chunk-start states) reach the
+        # backward as None, so it neither fills nor streams zero gradients.
+        ctx.set_materialize_grads(False)
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
         dev = k.device

@@ -72,6 +72,7 @@ CASES = [
     (1, 100, 3, 64, 200, 64, 63, torch.bfloat16),
     (1, 129, 1, 256, 96, 64, 1, torch.bfloat16),
     (1, 20, 2, 48, 16, 8, 3, torch.bfloat16),
+    (1, 100, 2, 64, 128, 64, 5, torch.bfloat16),
     # bf16 FMA path (K not a multiple of 16)
     (1, 40, 2, 40, 24, 16, 5, torch.bfloat16),
 ]
@@ -95,11 +96,14 @@ def test_gdn_forward_matches_recurrence(case):
 
 @pytest.mark.parametrize("case", CASES[:8] + CASES[8:], ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}K{c[3]}V{c[4]}C{c[5]}o{c[6]}{str(c[7])[6:]}")
 @pytest.mark.parametrize("with_q", [True, False])
-def test_gdn_backward_matches_autograd_of_recurrence(case, with_q):
+@pytest.mark.parametrize("inject", [True, False], ids=["states", "nostates"])
+def test_gdn_backward_matches_autograd_of_recurrence(case, with_q, inject):
     from gpa_amd.ops import gdn_scan_hip
     b, t, h, kd, vd, chunk, offset, dtype = case
     if t > 96 and kd * vd > 128 * 128:
         pytest.skip("oracle autograd too slow at this size")
+    if not inject and not (dtype == torch.bfloat16 and kd % 16 == 0):
+        pytest.skip("only the MFMA state kernels have a separate no-injection build")
     q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=7 + hash(case) % 1000, q=with_q,
                                    const_gates=(kd == 32))
     gen = torch.Generator().manual_seed(3)
@@ -109,7 +113,9 @@ def test_gdn_backward_matches_autograd_of_recurrence(case, with_q):
     w_final = torch.randn(b, h, kd, vd, generator=gen, dtype=torch.float64)
 
     def loss(out, states, final):
-        total = (states.double() * w_states.to(states.device)).sum() + (final.double() * w_final.to(final.device)).sum()
+        total = (final.double() * w_final.to(final.device)).sum()
+        if inject:
+            total = total + (states.double() * w_states.to(states.device)).sum()
         if out is not None:
             total = total + (out.double() * w_out.to(out.device)).sum()
         return total
