@@ -95,6 +95,14 @@ int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
 // MFMA chunk preparation (gdn_prep_mfma.hip); mf: write the bf16 fragments.
 template <typename E, int KM>
 int launch_prep_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, bool mf, int nch, hipStream_t st);
+// bf16-MFMA output read and its chunk-local gradient (gdn_out_mfma.hip); bf16,
+// kdim % 16 == 0 and vdim <= GPA_OUT_MFMA_MAX_V.
+constexpr int GPA_OUT_MFMA_MAX_V = 256;
+template <int KM>
+int launch_out_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, int nch, hipStream_t st);
+template <int KM>
+int launch_dd0_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
+                    hipStream_t st);
 // fp32-MFMA chunk backward (gdn_chunk_bwd_mfma.hip); needs kdim % 4 == 0.
 template <typename E, int KM>
 int launch_chunk_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,

@@ -890,9 +890,13 @@ int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operan
     hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
   }
   if (p.q.ptr && out.ptr) {
-    const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
     mark(tm, st);
-    hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
+    if (mf && p.vdim <= GPA_OUT_MFMA_MAX_V) {
+      if (int rc = launch_out_mfma<KM>(p, sv, out, nch, st)) return rc;
+    } else {
+      const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+      hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
+    }
   }
   mark(tm, st);
   return check_launch("gdn_forward");
@@ -904,9 +908,13 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
   const dim3 grid_c(nch, p.batch * p.heads), block(NT);
   const bool has_q = p.q.ptr && gr.dout.ptr;
   if (has_q) {
-    const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
     mark(tm, st);
-    hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
+    if (use_mfma<E>(p) && p.vdim <= GPA_OUT_MFMA_MAX_V) {
+      if (int rc = launch_dd0_mfma<KM>(p, sv, gr, nch, st)) return rc;
+    } else {
+      const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+      hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
+    }
   } else {
     gr.dd0 = nullptr;
     gr.o = nullptr;
