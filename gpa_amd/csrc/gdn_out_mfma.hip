@@ -231,3 +231,303 @@ template int launch_dd0_mfma<256>(const gpa_gdn_problem&, const gpa_gdn_saved&, 
                                   hipStream_t);
 
 }  // namespace gpa
+
+// ===========================================================================
+// The read of a scan that ran without a query (a late read), and its query
+// gradient.  gdn_prep_q normalises the query rows of one (chunk, stream) like
+// the scan's own preparation does (x / max(|x|, 1e-6), rounded to the
+// activation type) and writes Qn and its fragments; the read itself is
+// gdn_out_mfma.  gdn_read_dq_mfma computes the query gradient alone:
+//   dQn = diag(e^G) dO S_n^T + (causal e^{G_t-G_u} dO D^T) Kn
+//   dq  = (dQn - q^ (q^ . dQn)) / |q|              (q^ = q / |q| unrounded)
+// The other gradients of the read (keys, values, gates, states) are those of
+// the scan backward with this query and dO, which the caller runs later.
+namespace gpa {
+
+template <typename E, int KM, bool MF>
+__global__ __launch_bounds__(ONT) void gdn_prep_q(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
+  const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NI = KM / 64, NR = R / OWAVES;
+  const int64_t chunk_id = (int64_t)s * nch + n;
+  __bf16* qcol = MF ? reinterpret_cast<__bf16*>(sv.qcol) + chunk_id * frag_col_elems(K, 8) : nullptr;
+  float xq[NR][NI];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int tok = token_at(p, n, wave + OWAVES * j), tt = tok >= 0 ? tok : 0;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int d = lane + 64 * i, dd = d < K ? d : 0;
+      xq[j][i] = op_load<E>(p.q, b, h, tt, dd);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int r = wave + OWAVES * j, tok = token_at(p, n, r);
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      xq[j][i] = (tok >= 0 && lane + 64 * i < K) ? xq[j][i] : 0.f;
+      sq += xq[j][i] * xq[j][i];
+    }
+    const float dq = fmaxf(sqrtf(sum64(sq)), 1e-6f);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int d = lane + 64 * i;
+      if (d < K) {
+        const float yq = round_as<E>(xq[j][i] / dq);
+        sv.qn[rows_off(s, n, nch, r, K) + d] = yq;
+        if (MF) {  // Qn^T fragment (d/32, r/16), lane d%32 + 32 ((r/8) % 2), element r % 8
+          const int rb = d >> 5, cs = r >> 4, ln = (d & 31) + 32 * ((r >> 3) & 1);
+          qcol[((rb * 4 + cs) * 64 + ln) * 8 + (r & 7)] = (__bf16)yq;
+        }
+      }
+    }
+  }
+}
+
+// LDS of gdn_read_dq_mfma (bf16 elements): S_n^T and D^T of one 64-value
+// slice, split (hi, lo), then the masked dO D^T (split) for the Kn product.
+template <int KM>
+struct ReadDqLayout {
+  static constexpr int VSL = 64;
+  static constexpr int ST = KM * PLD, DT = R * PLD;
+  static constexpr int ST_HI = 0, ST_LO = ST, DT_HI = 2 * ST, DT_LO = DT_HI + DT, END = DT_LO + DT;
+  static constexpr size_t BYTES = sizeof(__bf16) * END + sizeof(float) * 4 * R;
+};
+
+template <int KM>
+__global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_operand dout,
+                                                         gpa_operand dqo, int nch) {
+  using L = ReadDqLayout<KM>;
+  constexpr int VSL = L::VSL, NTW = KM >= 64 ? KM / 64 : 1;  // 32x32 dQn tiles per wave
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __bf16* sth = reinterpret_cast<__bf16*>(smem_raw) + L::ST_HI;  // [k][v - v0]
+  __bf16* stl = reinterpret_cast<__bf16*>(smem_raw) + L::ST_LO;
+  __bf16* dth = reinterpret_cast<__bf16*>(smem_raw) + L::DT_HI;  // [u][v - v0], then dQK [t][u]
+  __bf16* dtl = reinterpret_cast<__bf16*>(smem_raw) + L::DT_LO;
+  float* gam_s = reinterpret_cast<float*>(reinterpret_cast<__bf16*>(smem_raw) + L::END);
+  float* qrd_s = gam_s + R;   // 1 / max(|q_t|, 1e-6)
+  float* qnm_s = qrd_s + R;   // |q_t|
+  float* qdot_s = qnm_s + R;  // q^ . dQn per row
+  const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int K = p.kdim, V = p.vdim, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int li = l & 31, hh = l >> 5, rt = w & 1;
+  const int KT = K / 32 > 0 ? (K + 31) / 32 : 1;
+  if (tid < R) {
+    gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
+    qdot_s[tid] = 0.f;
+  }
+  {  // query row norms, 4 threads per row
+    const int row = tid >> 2, part = tid & 3, tok = token_at(p, n, row);
+    float ss = 0.f;
+    if (tok >= 0)
+      for (int c = part; c < K; c += 4) {
+        const float x = op_load<bf16_t>(p.q, b, h, tok, c);
+        ss += x * x;
+      }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    if (part == 0) {
+      const float nq = sqrtf(ss);
+      qnm_s[row] = nq;
+      qrd_s[row] = 1.f / fmaxf(nq, 1e-6f);
+    }
+  }
+  const float* st = sv.states + state_off(s, n, nch, K, V);
+  const float* dl = sv.delta + vc_off(s, n, nch, V);
+  // dO rows of this wave's row tile: row t = 32 rt + l%32 (zero for void rows).
+  const int tq = 32 * rt + li, tokq = token_at(p, n, tq);
+  const bf16_t* dorow = reinterpret_cast<const bf16_t*>(dout.ptr) + op_base(dout, b, h) +
+                        (int64_t)(tokq >= 0 ? tokq : 0) * dout.st;
+  f32x16 aq[NTW], ap = {};
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) aq[j] = f32x16{};
+  const int pc = w >> 1;  // dO D^T tile (rt, pc)
+  for (int v0 = 0; v0 < V; v0 += VSL) {
+    __syncthreads();
+    // S_n^T slice: thread -> (value v, 4 keys), split into hi / lo.
+    for (int idx = tid; idx < VSL * (KM / 4); idx += ONT) {
+      const int vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (v < V && k < K) x = *reinterpret_cast<const float4*>(st + (int64_t)v * K + k);
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const __bf16 hi = (__bf16)xs[e];
+        sth[(k + e) * PLD + vl] = hi;
+        stl[(k + e) * PLD + vl] = (__bf16)(xs[e] - (float)hi);
+      }
+    }
+    // D^T slice: thread -> (value v, 4 positions).
+    for (int idx = tid; idx < VSL * (R / 4); idx += ONT) {
+      const int vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (v < V) x = *reinterpret_cast<const float4*>(dl + (int64_t)v * R + u);
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const __bf16 hi = (__bf16)xs[e];
+        dth[(u + e) * PLD + vl] = hi;
+        dtl[(u + e) * PLD + vl] = (__bf16)(xs[e] - (float)hi);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int vs = 0; vs < VSL / 16; ++vs) {
+      const int vv = v0 + 16 * vs + 8 * hh;
+      bf16x8 a = bf16x8{};
+      if (tokq >= 0 && vv < V) a = *reinterpret_cast<const bf16x8*>(dorow + vv);  // V % 8 == 0
+      const int c = 16 * vs + 8 * hh;
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const int kt = pc + 2 * j;
+        if (kt < KT) {
+          const int o = (32 * kt + li) * PLD + c;
+          aq[j] = mfma_bf16(a, *reinterpret_cast<const bf16x8*>(&sth[o]), aq[j]);
+          aq[j] = mfma_bf16(a, *reinterpret_cast<const bf16x8*>(&stl[o]), aq[j]);
+        }
+      }
+      const int o = (32 * pc + li) * PLD + c;
+      ap = mfma_bf16(a, *reinterpret_cast<const bf16x8*>(&dth[o]), ap);
+      ap = mfma_bf16(a, *reinterpret_cast<const bf16x8*>(&dtl[o]), ap);
+    }
+  }
+  __syncthreads();
+  // dQK = causal e^{G_t-G_u} dO D^T -> LDS [t][u], split.
+  {
+    const int u = 32 * pc + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * rt + acc_row(r, hh);
+      const float x = u <= t ? __expf(gam_s[t] - gam_s[u]) * ap[r] : 0.f;
+      const __bf16 hi = (__bf16)x;
+      dth[t * PLD + u] = hi;
+      dtl[t * PLD + u] = (__bf16)(x - (float)hi);
+    }
+  }
+  __syncthreads();
+  // dQn = e^G (dO S_n^T) + dQK Kn; Kn^T fragments (kcol) are the B operands.
+  const __bf16* kcol = reinterpret_cast<const __bf16*>(sv.kcol) + ((int64_t)s * nch + n) * frag_col_elems(K, 8);
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int kt = pc + 2 * j;
+    if (kt >= KT) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) aq[j][r] *= __expf(gam_s[32 * rt + acc_row(r, hh)]);
+#pragma unroll
+    for (int us = 0; us < R / 16; ++us) {
+      const int o = (32 * rt + li) * PLD + 16 * us + 8 * hh;
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(kcol + ((kt * 4 + us) * 64 + l) * 8);
+      aq[j] = mfma_bf16(*reinterpret_cast<const bf16x8*>(&dth[o]), kb, aq[j]);
+      aq[j] = mfma_bf16(*reinterpret_cast<const bf16x8*>(&dtl[o]), kb, aq[j]);
+    }
+  }
+  // Normalisation backward: q^ . dQn per row, then dq.
+  float qe[NTW][16];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int kt = pc + 2 * j, k = 32 * kt + li;
+    float c[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * rt + acc_row(r, hh), tok = token_at(p, n, t);
+      const bool ok = kt < KT && k < K && tok >= 0;
+      qe[j][r] = ok ? op_load<bf16_t>(p.q, b, h, tok, k) * qrd_s[t] : 0.f;
+      c[r] = qe[j][r] * aq[j][r];
+    }
+    const float sq = tile_row_sum(c, l);
+    if ((l & 1) == 0 && kt < KT) atomicAdd(&qdot_s[32 * rt + acc_row(sum_index(l), hh)], sq);
+  }
+  __syncthreads();
+  float* dq = reinterpret_cast<float*>(dqo.ptr) + op_base(dqo, b, h);
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int kt = pc + 2 * j, k = 32 * kt + li;
+    if (kt >= KT || k >= K) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * rt + acc_row(r, hh), tok = token_at(p, n, t);
+      if (tok >= 0)
+        dq[(int64_t)tok * dqo.st + k] = (qnm_s[t] > 1e-6f ? aq[j][r] - qe[j][r] * qdot_s[t] : aq[j][r]) * qrd_s[t];
+    }
+  }
+}
+
+}  // namespace gpa
+
+namespace {
+
+using namespace gpa;
+
+template <typename F>
+int allow_lds_read(F kernel, size_t bytes) {
+  if (bytes <= 65536) return GPA_HIP_OK;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes) == hipSuccess
+             ? GPA_HIP_OK
+             : fail(GPA_HIP_EHIP, "gdn_read: cannot raise the LDS limit");
+}
+
+int read_kmax(int k) { return k <= 64 ? 64 : (k <= 128 ? 128 : 256); }
+
+int check_read(const gpa_gdn_problem* p, const gpa_gdn_saved* sv) {
+  if (!p || !sv) return fail(GPA_HIP_EINVAL, "gdn_read: null problem or saved");
+  if (p->batch < 1 || p->heads < 1 || p->tokens < 1 || p->chunk < 1 || p->chunk > GPA_CHUNK_ROWS ||
+      p->offset < 0 || p->offset >= p->chunk)
+    return fail(GPA_HIP_EINVAL, "gdn_read: bad shape");
+  if (p->dtype != GPA_DTYPE_BF16 || p->kdim % 16 != 0 || p->kdim > 256 || p->vdim % 8 != 0 ||
+      p->vdim > GPA_OUT_MFMA_MAX_V)
+    return fail(GPA_HIP_EUNSUPPORTED, "gdn_read: needs bf16, key width a multiple of 16 up to 256 and value width "
+                                      "a multiple of 8 up to 256");
+  if (!p->q.ptr) return fail(GPA_HIP_EINVAL, "gdn_read: null query");
+  if (!sv->kn || !sv->qn || !sv->delta || !sv->states || !sv->gam || !sv->kcol || !sv->qcol)
+    return fail(GPA_HIP_EINVAL, "gdn_read: a saved buffer is null");
+  return GPA_HIP_OK;
+}
+
+template <int KM>
+int read_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, int nch, hipStream_t st) {
+  hipLaunchKernelGGL((gdn_prep_q<bf16_t, KM, true>), dim3(nch, p.batch * p.heads), dim3(ONT), 0, st, p, sv, nch);
+  return launch_out_mfma<KM>(p, sv, out, nch, st);
+}
+
+template <int KM>
+int read_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand dout, gpa_operand dq, int nch,
+                  hipStream_t st) {
+  const size_t lds = ReadDqLayout<KM>::BYTES;
+  if (int rc = allow_lds_read(gdn_read_dq_mfma<KM>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_read_dq_mfma<KM>), dim3(nch, p.batch * p.heads), dim3(ONT), lds, st, p, sv, dout, dq,
+                     nch);
+  return GPA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int gpa_gdn_read(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved, gpa_operand out,
+                            hipStream_t stream) {
+  if (int rc = check_read(problem, saved)) return rc;
+  if (!out.ptr) return fail(GPA_HIP_EINVAL, "gdn_read: null output");
+  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
+  int rc;
+  switch (read_kmax(problem->kdim)) {
+    case 64: rc = read_forward<64>(*problem, *saved, out, nch, stream); break;
+    case 128: rc = read_forward<128>(*problem, *saved, out, nch, stream); break;
+    default: rc = read_forward<256>(*problem, *saved, out, nch, stream); break;
+  }
+  return rc ? rc : check_launch("gpa_gdn_read");
+}
+
+extern "C" int gpa_gdn_read_backward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved, gpa_operand dout,
+                                     gpa_operand dq, hipStream_t stream) {
+  if (int rc = check_read(problem, saved)) return rc;
+  if (!dout.ptr || !dq.ptr) return fail(GPA_HIP_EINVAL, "gdn_read_backward: null dout or dq");
+  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
+  int rc;
+  switch (read_kmax(problem->kdim)) {
+    case 64: rc = read_backward<64>(*problem, *saved, dout, dq, nch, stream); break;
+    case 128: rc = read_backward<128>(*problem, *saved, dout, dq, nch, stream); break;
+    default: rc = read_backward<256>(*problem, *saved, dout, dq, nch, stream); break;
+  }
+  return rc ? rc : check_launch("gpa_gdn_read_backward");
+}

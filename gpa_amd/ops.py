@@ -50,7 +50,7 @@ class _GDNScan(torch.autograd.Function):
     """One group of GDN scans; saved intermediates per include/gpa_hip.h."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int):
+    def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int, box=None):
         lib = _lib.load()
         _in_use_here(q, k, v, g, beta, s0)
         # Outputs nobody differentiates (often the chunk-start states) reach the
@@ -93,15 +93,28 @@ class _GDNScan(torch.autograd.Function):
         _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), timing, _lib.stream_handle(dev)),
                    "gpa_gdn_forward")
         ctx.geom = (chunk, offset, nch, q is not None, s0 is not None, mfma)
+        ctx.box = box
         ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)
-        return out, states, final
+        token = None
+        if box is not None:  # a late read will use these intermediates
+            box.args = (k, v, g, beta, s0f, chunk, offset, nch)
+            box.saved = (kn, w, u, delta, tri, gam, bet, states, final, *frags)
+            token = torch.zeros(1, device=dev)
+        return out, states, final, token
 
     @staticmethod
-    def backward(ctx, dout, dstates, dfinal):
+    def backward(ctx, dout, dstates, dfinal, dtoken=None):
         lib = _lib.load()
         _in_use_here(dout, dstates, dfinal)
         chunk, offset, nch, has_q, has_s0, mfma = ctx.geom
         (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags) = ctx.saved_tensors
+        box = ctx.box
+        late = box is not None and box.dout is not None
+        if late:  # the late read's gradient joins this backward as its read
+            q, qn, dout = box.q, box.qn, box.dout
+            frags[4] = box.qcol
+            has_q = True
+            _in_use_here(q, qn, dout, box.qcol)
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
         dev = k.device
@@ -131,9 +144,74 @@ class _GDNScan(torch.autograd.Function):
                            _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
         timing = profiling.backward_timing(kd, vd, chunk, tokens * bsz * heads, k.dtype, want_read)
         _lib.check(lib.gpa_gdn_backward(prob, saved, grads, timing, _lib.stream_handle(dev)), "gpa_gdn_backward")
-        dq_out = dq.to(q.dtype) if (has_q and ctx.needs_input_grad[0]) else None
+        if late:  # dq of the late read was returned by the read itself
+            box.release()
+        dq_out = dq.to(q.dtype) if (has_q and not late and ctx.needs_input_grad[0]) else None
         return (dq_out, dk.to(k.dtype), dv.to(v.dtype), dg, db,
-                ds0 if has_s0 else None, None, None)
+                ds0 if has_s0 else None, None, None, None)
+
+
+class _ReadBox:
+    """What a scan forward without a query hands to its late read, and what
+    the read's backward hands back to the scan's backward."""
+
+    def __init__(self):
+        self.args = self.saved = None
+        self.q = self.qn = self.qcol = self.dout = None
+
+    def release(self):
+        self.q = self.qn = self.qcol = self.dout = None
+
+
+class _GDNRead(torch.autograd.Function):
+    """u(q)^T S of a scan that ran without a query (gpa_gdn_read).  Its
+    backward computes dq alone (gpa_gdn_read_backward) and leaves dO for the
+    scan's backward, which autograd runs after it: the read consumes the
+    scan's `token` output."""
+
+    @staticmethod
+    def forward(ctx, q, token, box):
+        lib = _lib.load()
+        if box.q is not None:
+            raise ValueError("gdn_scan_deferred: the read of a scan can be taken once")
+        k, v, g, beta, s0f, chunk, offset, nch = box.args
+        kn, w, u, delta, tri, gam, bet, states, final, *frags = box.saved
+        _in_use_here(q, k, v, g, beta, s0f, kn, delta, gam, states, frags[3])
+        bsz, tokens, heads, kd = k.shape
+        vd = v.shape[-1]
+        dev = k.device
+        chunks = bsz * heads * nch
+        qn = torch.empty(chunks * _lib.CHUNK_ROWS * kd, device=dev, dtype=torch.float32)
+        qcol = torch.empty(chunks * ((kd + 31) // 32) * 4 * 64 * 8, device=dev, dtype=torch.bfloat16)
+        out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype)
+        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        saved = _read_saved(box, qn, qcol)
+        _lib.check(lib.gpa_gdn_read(prob, saved, _lib.operand(out), _lib.stream_handle(dev)), "gpa_gdn_read")
+        box.q, box.qn, box.qcol = q, qn, qcol
+        ctx.box = box
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        box = ctx.box
+        k, v, g, beta, s0f, chunk, offset, nch = box.args
+        q = box.q
+        dout = dout.to(k.dtype).contiguous()
+        dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        saved = _read_saved(box, box.qn, box.qcol)
+        _lib.check(lib.gpa_gdn_read_backward(prob, saved, _lib.operand(dout), _lib.operand(dq),
+                                             _lib.stream_handle(q.device)), "gpa_gdn_read_backward")
+        box.dout = dout
+        return dq.to(q.dtype), torch.zeros(1, device=q.device), None
+
+
+def _read_saved(box, qn, qcol):
+    kn, w, u, delta, tri, gam, bet, states, final, *frags = box.saved
+    frags = list(frags)
+    frags[4] = qcol
+    return _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
 
 
 def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor | None,
@@ -163,8 +241,36 @@ def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor
     q = _contig_last(q) if q is not None else None
     k, v = _contig_last(k), _contig_last(v)
     g, beta = g.float(), beta.float()
-    out, states_vk, final = _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)
+    out, states_vk, final, _ = _GDNScan.apply(q, k, v, g, beta, s0, chunk, offset)
     return out, states_vk.transpose(-1, -2), final
+
+
+def read_supported(k: Tensor, v: Tensor) -> bool:
+    """Whether gdn_scan_deferred can take a late read of these keys/values
+    (bf16, K a multiple of 16 up to 256, V a multiple of 8 up to 256)."""
+    kd, vd = k.shape[-1], v.shape[-1]
+    return k.dtype == torch.bfloat16 and kd % 16 == 0 and kd <= 256 and vd % 8 == 0 and vd <= 256
+
+
+def gdn_scan_deferred(k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor | None, *, chunk: int,
+                      offset: int = 0):
+    """`gdn_scan_hip(None, ...)` whose read comes later: returns (states,
+    final, read), where read(q) [B,T,H,K] gives the out that
+    `gdn_scan_hip(q, k, v, g, beta, s0, ...)` would, without running the state
+    recurrence again.  The gradients of the read and of the scan's own outputs
+    are taken by one scan backward.  Keys/values must pass `read_supported`."""
+    if not read_supported(k, v):
+        raise ValueError("gdn_scan_deferred: needs bf16, K % 16 == 0 <= 256 and V % 8 == 0 <= 256")
+    box = _ReadBox()
+    _, states_vk, final, token = _GDNScan.apply(None, _contig_last(k), _contig_last(v), g.float(), beta.float(),
+                                                s0, chunk, offset, box)
+
+    def read(q: Tensor) -> Tensor:
+        if q.shape != k.shape or q.dtype != k.dtype:
+            raise ValueError("gdn_scan_deferred: the query must match the keys' shape and dtype")
+        return _GDNRead.apply(_contig_last(q), token, box)
+
+    return states_vk.transpose(-1, -2), final, read
 
 
 # --------------------------------------------------------------------------- reference-signature operators

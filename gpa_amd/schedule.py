@@ -29,7 +29,8 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib
-from .ops import gdn_scan_hip
+from .ops import gdn_scan_deferred, gdn_scan_hip
+from .ops import read_supported as late_read_supported
 from .level import level_mix
 from .level import supported as fused_level_supported
 from .route import route_reader
@@ -141,7 +142,7 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
 
 class _Level:
     __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "logits", "a_final", "b_final",
-                 "a_starts", "b_starts")
+                 "a_starts", "b_starts", "b_read")
 
 
 def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, position_ids: Tensor,
@@ -166,10 +167,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         lv = _Level()
         slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
         g_in, b_in, g_out, b_out = _gates(model, key, j, control)
-        (raw, a_starts, a_final), (_, b_starts, b_final) = _concurrent([
+        # The outer read of this level (below) runs the B recurrence with the
+        # same keys, values, gates and initial state: where the kernels allow,
+        # the B scan keeps its intermediates for that read instead.
+        deferred = _DEFER_OUTER_READ[0] and late_read_supported(slot, value)
+        b_scan = gdn_scan_deferred if deferred else (lambda *a, **kw: gdn_scan_hip(None, *a, **kw)[1:] + (None,))
+        (raw, a_starts, a_final), (b_starts, b_final, lv.b_read) = _concurrent([
             (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan),
              (q, key, slot, g_in, b_in, old.inner)),
-            (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **scan),
+            (lambda: b_scan(slot, value, g_out, b_out, old.outer, **scan),
              (slot, value, g_out, b_out, old.outer))])
         # Snapshots: block 0 uses the cached ones, which are the scans' own
         # initial states unless the call starts inside a block.
@@ -203,6 +209,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     weights = model.output_logits.softmax(0)
 
     def outer_read(lv, qo, s0):
+        if lv.b_read is not None:
+            return lambda: lv.b_read(qo)
         return lambda: gdn_scan_hip(qo, lv.slot, lv.value, lv.g_out, lv.b_out, s0, **scan)[0]
 
     reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
@@ -360,6 +368,7 @@ def _residual_eta(key, value, rk, rv, eta):
 
 
 _FUSED_LEVEL = [True]  # the fused level write and residual (level.py)
+_DEFER_OUTER_READ = [True]  # outer reads as late reads of the B scans (ops.gdn_scan_deferred)
 
 
 def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):

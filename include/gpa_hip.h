@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 6
+#define GPA_HIP_ABI_VERSION 7
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -136,6 +136,24 @@ int gpa_gdn_forward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
  * ops.py:49-85 in the reference, plus chunk-start state injections). */
 int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
                      const gpa_gdn_grads *grads, gpa_timing *timing, hipStream_t stream);
+
+/* A late read: `out` = u(q_t)^T S_t for a query that arrives after the scan.
+ * `saved` holds the intermediates of a gpa_gdn_forward that ran with
+ * problem.q = NULL (same k, v, g, beta, s0, chunk, offset); this call fills
+ * saved.qn and saved.qcol for the new query (problem.q) and runs the read.
+ * The result equals gpa_gdn_forward with that query, without repeating the
+ * state recurrence.  Needs bf16, K a multiple of 16 up to 256, V a multiple
+ * of 8 up to 256.  Replaces the second pass of the same recurrence that the
+ * reference makes for a level's outer read (src/gpa/attention.py:333-341
+ * reads the B memory that :318-329 updates). */
+int gpa_gdn_read(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa_operand out,
+                 hipStream_t stream);
+
+/* The query gradient of a late read alone: dq (f32 operand, [B,T,H,K]) from
+ * dout.  The read's other gradients are those of gpa_gdn_backward with the
+ * same problem (query set), saved (qn, qcol filled) and dout. */
+int gpa_gdn_read_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa_operand dout,
+                          gpa_operand dq, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Batched single-token decode step of the whole DenseGPA core (the reference's

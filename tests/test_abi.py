@@ -18,7 +18,8 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
-                     "gpa_gdn_forward", "gpa_gdn_backward", "gpa_decode_step", "gpa_route_forward",
+                     "gpa_gdn_forward", "gpa_gdn_backward", "gpa_gdn_read", "gpa_gdn_read_backward",
+                     "gpa_decode_step", "gpa_route_forward",
                      "gpa_route_backward", "gpa_route_weight_grads", "gpa_level_forward", "gpa_level_backward"):
         assert expected in names
 

@@ -170,3 +170,68 @@ def test_gdn_rejects_bad_geometry_before_launch():
     big = torch.zeros(1, 4, 1, 300, device=DEV)
     with pytest.raises(ValueError):
         gdn_scan_hip(big, big, v.to(DEV), g.to(DEV), beta.to(DEV), None, chunk=4)
+
+
+LATE_CASES = [
+    # (B, T, H, K, V, chunk, offset)
+    (1, 130, 2, 128, 128, 64, 0),
+    (1, 96, 1, 256, 128, 64, 30),
+    (2, 70, 2, 64, 48, 64, 17),
+    (1, 20, 2, 32, 16, 8, 3),
+    (1, 64, 1, 128, 256, 64, 0),
+]
+
+
+@pytest.mark.parametrize("case", LATE_CASES, ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}K{c[3]}V{c[4]}C{c[5]}o{c[6]}")
+def test_late_read_matches_scan_with_query(case):
+    """gdn_scan_deferred + read(q) against gdn_scan_hip(q, ...) and the float64
+    recurrence: outputs, states and every input gradient (bf16 bar 2e-2; the
+    two HIP paths agree far more closely)."""
+    from gpa_amd.ops import gdn_scan_deferred, gdn_scan_hip
+    b, t, h, kd, vd, chunk, offset = case
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, torch.bfloat16, seed=31 + kd + vd)
+    gen = torch.Generator().manual_seed(4)
+    nch = (offset + t + chunk - 1) // chunk
+    w_out = torch.randn(b, t, h, vd, generator=gen, dtype=torch.float64).to(DEV)
+    w_states = (torch.randn(b, h, nch, kd, vd, generator=gen, dtype=torch.float64) * .1).to(DEV)
+    w_final = torch.randn(b, h, kd, vd, generator=gen, dtype=torch.float64).to(DEV)
+
+    def run(deferred):
+        xs = [x.to(DEV).requires_grad_() for x in (q, k, v, g, beta, s0)]
+        if deferred:
+            states, final, read = gdn_scan_deferred(*xs[1:], chunk=chunk, offset=offset)
+            out = read(xs[0])
+        else:
+            out, states, final = gdn_scan_hip(*xs, chunk=chunk, offset=offset)
+        loss = ((out.double() * w_out).sum() + (states.double() * w_states).sum()
+                + (final.double() * w_final).sum())
+        loss.backward()
+        return out, states, final, [x.grad for x in xs]
+
+    out_d, st_d, fin_d, grads_d = run(True)
+    out_p, st_p, fin_p, grads_p = run(False)
+    assert torch.equal(st_d, st_p) and torch.equal(fin_d, fin_p)
+    assert _rel(out_d, out_p) < 1e-6, _rel(out_d, out_p)
+    names = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
+    close = {n: _rel(a, r) for n, a, r in zip(names, grads_d, grads_p)}
+    print(case, "deferred vs plain", close)
+    assert all(e < 5e-3 for e in close.values()), close
+    # the float64 oracle
+    ref_leaves = [x.detach().double().requires_grad_() for x in (q, k, v)]
+    g_r, b_r, s_r = (x.double().requires_grad_() for x in (g, beta, s0))
+    ro, rs, rf = _oracle_segments_autograd(ref_leaves, g_r, b_r, s_r, chunk, offset)
+    ((ro * w_out.cpu()).sum() + (rs * w_states.cpu()).sum() + (rf * w_final.cpu()).sum()).backward()
+    assert _rel(out_d, ro) < 2e-2
+    refs = [ref_leaves[0].grad, ref_leaves[1].grad, ref_leaves[2].grad, g_r.grad, b_r.grad, s_r.grad]
+    errs = {n: _rel(a, r) for n, a, r in zip(names, grads_d, refs)}
+    print(case, "deferred vs oracle", errs)
+    assert all(e < 2e-2 for e in errs.values()), errs
+
+
+def test_late_read_taken_once():
+    from gpa_amd.ops import gdn_scan_deferred
+    q, k, v, g, beta, s0 = _inputs(1, 8, 1, 32, 16, torch.bfloat16, seed=2)
+    _, _, read = gdn_scan_deferred(*(x.to(DEV) for x in (k, v, g, beta, s0)), chunk=4)
+    read(q.to(DEV))
+    with pytest.raises(ValueError):
+        read(q.to(DEV))
