@@ -531,6 +531,366 @@ __global__ __launch_bounds__(LNT, 1) void level_bwd(gpa_level_problem p, gpa_lev
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 activations: the same step on the bf16 MFMA (32x32x16).  u(key), the
+// write w and the reconstructions' incoming gradients are exact in bf16 (the
+// reference rounds them to the activation type); the fp32 snapshots and
+// gradients are split into bf16 hi + lo, each product taking hi*hi + hi*lo +
+// lo*hi (the hi*lo terms vanish against an exact operand).  Snapshot
+// fragments are read straight from global memory (eight contraction indices
+// per lane: 32 contiguous bytes where the layout allows, else eight
+// coalesced scalars), so nothing but the block's rows is staged in LDS and
+// two or three workgroups share a CU.  Row phases run one wave per row with
+// the lanes along the row.
+
+__host__ __device__ constexpr int pad16(int x) { return (x + 15) & ~15; }
+__host__ __device__ constexpr int pad32(int x) { return (x + 31) & ~31; }
+
+struct Lds16 {
+  int ldu, ldw, lde;       // bf16 pitch of u(key) and w rows, float pitch of the fp32 row buffer
+  int u_off, w_off, e_off;  // byte offsets
+  int bytes;
+  __host__ __device__ Lds16(int Dk, int Dv, int M) {
+    ldu = pad16(Dk) + 8;
+    ldw = pad16(M) + 8;
+    int wide = pad32(M) > pad32(Dk) ? pad32(M) : pad32(Dk);
+    wide = wide > pad32(Dv) ? wide : pad32(Dv);
+    lde = wide + 4;
+    u_off = 0;
+    w_off = u_off + LROWS * ldu * 2;
+    e_off = w_off + LROWS * ldw * 2;
+    bytes = e_off + LROWS * lde * 4;
+  }
+};
+
+// A snapshot column seen along its contraction axis: element i of the column
+// is base[i * st], i < count; `ok` is false for a padding column.
+struct Col {
+  const float* base;
+  int st, count;
+  bool ok;
+};
+
+// Eight consecutive elements first .. first+7 of a column (zero past `count`
+// or in a padding column), without branches: indices are clamped for the
+// load and masked after it.  With FAST (count a multiple of 16) and a unit
+// stride they are two 16-byte loads.
+template <bool FAST>
+__device__ __forceinline__ void raw8(const Col& c, int first, float (&v)[8]) {
+  if (FAST && c.st == 1) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(c.base + first);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(c.base + first + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = c.ok ? v[e] : 0.f;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = first + e < c.count ? first + e : c.count - 1;
+      const float x = c.base[(int64_t)i * c.st];
+      v[e] = (c.ok && first + e < c.count) ? x : 0.f;
+    }
+  }
+}
+
+__device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hi[e] = (__bf16)v[e];
+    lo[e] = (__bf16)(v[e] - (float)hi[e]);
+  }
+}
+
+__device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Snapshot columns (the out-of-range column index is clamped for the loads).
+// A^ along k, column m (a slot): A^[.][m].
+__device__ __forceinline__ Col ahat_k(const Block& q, int m) {
+  const int mc = m < q.M ? m : q.M - 1;
+  return q.a_first ? Col{q.a_fs + mc, q.M, q.Dk, m < q.M} : Col{q.a_st + (int64_t)mc * q.Dk, 1, q.Dk, m < q.M};
+}
+// A^ along m, column k: A^[k][.].
+__device__ __forceinline__ Col ahat_m(const Block& q, int k) {
+  const int kc = k < q.Dk ? k : q.Dk - 1;
+  return q.a_first ? Col{q.a_fs + (int64_t)kc * q.M, 1, q.M, k < q.Dk} : Col{q.a_st + kc, q.Dk, q.M, k < q.Dk};
+}
+// B^ along m, column v: B^[.][v].
+__device__ __forceinline__ Col bhat_m(const Block& q, int v) {
+  const int vc = v < q.Dv ? v : q.Dv - 1;
+  return q.b_first ? Col{q.b_fs + vc, q.Dv, q.M, v < q.Dv} : Col{q.b_st + (int64_t)vc * q.M, 1, q.M, v < q.Dv};
+}
+
+// acc[rt] += A_rt B (rt = 0, 1: the block's two 32-row tiles) over `steps`
+// 16-wide contraction steps, B split into hi / lo; each B fragment is loaded
+// once for both row tiles, and the fragments of FGROUP steps are loaded
+// before their MFMAs so that their global loads overlap.  A fragments come
+// from LDS.
+constexpr int FGROUP = 8;
+template <typename LB, typename LA>
+__device__ __forceinline__ void tile2_split_b(f32x16 (&acc)[2], int steps, LB&& load_b, LA&& frag_a) {
+  f32x16 c[4] = {};
+#pragma unroll 1
+  for (int s0 = 0; s0 < steps; s0 += FGROUP) {
+    float v[FGROUP][8];
+#pragma unroll
+    for (int j = 0; j < FGROUP; ++j)
+      if (s0 + j < steps) load_b(s0 + j, v[j]);
+#pragma unroll
+    for (int j = 0; j < FGROUP; ++j)
+      if (s0 + j < steps) {
+        bf16x8 hi, lo;
+        split8(v[j], hi, lo);
+        const bf16x8 a0 = frag_a(0, s0 + j), a1 = frag_a(1, s0 + j);
+        c[0] = mfma16(a0, hi, c[0]);
+        c[2] = mfma16(a1, hi, c[2]);
+        c[1] = mfma16(a0, lo, c[1]);
+        c[3] = mfma16(a1, lo, c[3]);
+      }
+  }
+  acc[0] = c[0] + c[1];
+  acc[1] = c[2] + c[3];
+}
+
+// Row phases with whole rows per 32 lanes: thread -> (row, columns 8 c32 ..
+// 8 c32 + 7), 8 rows per pass of the workgroup, 8 passes; every global load
+// of a thread is issued before its first use.  Needs widths that are
+// multiples of 8 and at most 256.
+constexpr int RPASS = LROWS / (LNT / 32);  // passes of 8 rows
+
+__device__ __forceinline__ float sum32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+  return x;
+}
+__device__ __forceinline__ float max32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 32));
+  return x;
+}
+
+__device__ __forceinline__ void bf8_to_f32(const uint4& u, float (&x)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint4 f32_to_bf8(const float (&x)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(x[2 * i]).bits | ((uint32_t)f32_to_bf16(x[2 * i + 1]).bits << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <bool FAST>
+__global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
+  HIP_DYNAMIC_SHARED(float, lds_f)
+  unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
+  const Block q(p);
+  const int Dk = q.Dk, Dv = q.Dv, M = q.M;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
+  const Lds16 L(Dk, Dv, M);
+  __bf16* U = reinterpret_cast<__bf16*>(lds + L.u_off);  // u(key) [64][ldu]
+  __bf16* W = reinterpret_cast<__bf16*>(lds + L.w_off);  // w [64][ldw]
+  float* E = reinterpret_cast<float*>(lds + L.e_off);    // logits, then rk / rv [64][lde]
+  const int ldu = L.ldu, ldw = L.ldw, lde = L.lde;
+  const bf16_t* key = reinterpret_cast<const bf16_t*>(p.key.ptr);
+
+  // u(key)
+  if (FAST) {
+    const int c32 = tid & 31, c = 8 * c32, r0 = tid >> 5;
+    const bool on = c < Dk;
+    uint4 raw[RPASS];
+#pragma unroll
+    for (int i = 0; i < RPASS; ++i) {
+      const int t = q.token(r0 + 8 * i);
+      raw[i] = (on && t >= 0) ? *reinterpret_cast<const uint4*>(key + q.at(p.key, t) + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < RPASS; ++i) {
+      float x[8];
+      bf8_to_f32(raw[i], x);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      const float den = fmaxf(sqrtf(sum32(ss)), 1e-6f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = x[e] / den;
+      if (on) *reinterpret_cast<uint4*>(&U[(r0 + 8 * i) * ldu + c]) = f32_to_bf8(x);
+    }
+  } else
+  for (int r = wave; r < LROWS; r += LW) {
+    const int t = q.token(r);
+    float x[GPA_LEVEL_MAX_WIDTH / 64];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < GPA_LEVEL_MAX_WIDTH / 64; ++i) {
+      const int c = lane + 64 * i;
+      x[i] = (t >= 0 && c < Dk) ? to_f32(key[q.at(p.key, t) + c]) : 0.f;
+      ss += x[i] * x[i];
+    }
+    const float den = fmaxf(sqrtf(sum64(ss)), 1e-6f);
+#pragma unroll
+    for (int i = 0; i < GPA_LEVEL_MAX_WIDTH / 64; ++i) {
+      const int c = lane + 64 * i;
+      if (c < ldu) U[r * ldu + c] = (__bf16)(x[i] / den);  // exact: bf16 rounding of the unit key
+    }
+  }
+  __syncthreads();
+
+  // logits = u(key) A^ -> E
+  const int K16 = pad16(Dk) / 16, M16 = pad16(M) / 16, MT = pad32(M) / 32;
+#pragma unroll 1
+  for (int mt = wave; mt < MT; mt += LW) {
+    const int m = 32 * mt + li;
+    f32x16 acc[2];
+    const Col col = ahat_k(q, m);
+    tile2_split_b(
+        acc, K16, [&](int ks, float(&v)[8]) { raw8<FAST>(col, 16 * ks + 8 * hh, v); },
+        [&](int rt, int ks) { return *reinterpret_cast<const bf16x8*>(&U[(32 * rt + li) * ldu + 16 * ks + 8 * hh]); });
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) E[(32 * rt + acc_row(r, hh)) * lde + m] = acc[rt][r];
+  }
+  __syncthreads();
+
+  // w = softmax; the row max and sum are saved.
+  if (FAST) {
+    const int c32 = tid & 31, c = 8 * c32, r0 = tid >> 5;
+    const bool on = c < M;
+#pragma unroll 2
+    for (int i = 0; i < RPASS; ++i) {
+      const int r = r0 + 8 * i, t = q.token(r);
+      float x[8];
+      float mx = -INFINITY;
+      if (on) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&E[r * lde + c]);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&E[r * lde + c + 4]);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      }
+      mx = max32(mx);
+      float sm = 0.f;
+      if (on)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm += __expf(x[e] - mx);
+      sm = sum32(sm);
+      if (t >= 0 && c32 < 2) p.stats[q.saved(t, 2) + c32] = c32 ? sm : mx;
+      if (on) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = t >= 0 ? round_as<bf16_t>(__expf(x[e] - mx) / sm) : 0.f;
+        const uint4 w8 = f32_to_bf8(x);
+        *reinterpret_cast<uint4*>(&W[r * ldw + c]) = w8;
+        if (t >= 0) *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.write.ptr) + q.at(p.write, t) + c) = w8;
+      }
+    }
+  } else
+  for (int r = wave; r < LROWS; r += LW) {
+    const int t = q.token(r);
+    float x[GPA_LEVEL_MAX_WIDTH / 64];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < GPA_LEVEL_MAX_WIDTH / 64; ++i) {
+      const int m = lane + 64 * i;
+      x[i] = m < M ? E[r * lde + m] : -INFINITY;
+      mx = fmaxf(mx, x[i]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < GPA_LEVEL_MAX_WIDTH / 64; ++i) sm += lane + 64 * i < M ? __expf(x[i] - mx) : 0.f;
+    sm = sum64(sm);
+    if (t >= 0 && lane < 2) p.stats[q.saved(t, 2) + lane] = lane ? sm : mx;
+    bf16_t* wo = reinterpret_cast<bf16_t*>(p.write.ptr) + (t >= 0 ? q.at(p.write, t) : 0);
+#pragma unroll
+    for (int i = 0; i < GPA_LEVEL_MAX_WIDTH / 64; ++i) {
+      const int m = lane + 64 * i;
+      float w = 0.f;
+      if (t >= 0 && m < M) {
+        w = round_as<bf16_t>(__expf(x[i] - mx) / sm);
+        wo[m] = from_f32<bf16_t>(w);
+      }
+      if (m < ldw) W[r * ldw + m] = (__bf16)w;
+    }
+  }
+  __syncthreads();
+
+  // rk = A^ w (then key' = key - eta0 rk) and rv = w^T B^ (then value' = value - eta1 rv):
+  // tiles -> E, then a wave per row writes the rounded results.
+  const float eta0 = p.eta[2 * q.h], eta1 = p.eta[2 * q.h + 1];
+  for (int part = 0; part < 2; ++part) {
+    const int D = part ? Dv : Dk, DT = pad32(D) / 32;
+#pragma unroll 1
+    for (int dt = wave; dt < DT; dt += LW) {
+      const int c = 32 * dt + li;
+      f32x16 acc[2];
+      const Col col = part ? bhat_m(q, c) : ahat_m(q, c);
+      tile2_split_b(
+          acc, M16, [&](int ms, float(&v)[8]) { raw8<FAST>(col, 16 * ms + 8 * hh, v); },
+          [&](int rt, int ms) {
+            return *reinterpret_cast<const bf16x8*>(&W[(32 * rt + li) * ldw + 16 * ms + 8 * hh]);
+          });
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) E[(32 * rt + acc_row(r, hh)) * lde + c] = acc[rt][r];
+    }
+    __syncthreads();
+    const gpa_operand& src = part ? p.value : p.key;
+    const gpa_operand& dst = part ? p.value_out : p.key_out;
+    bf16_t* saved = reinterpret_cast<bf16_t*>(part ? p.rv : p.rk);
+    const float eta = part ? eta1 : eta0;
+    if (FAST) {
+      const int c32 = tid & 31, c = 8 * c32, r0 = tid >> 5;
+      const bool on = c < D;
+      uint4 raw[RPASS];
+#pragma unroll
+      for (int i = 0; i < RPASS; ++i) {
+        const int t = q.token(r0 + 8 * i);
+        raw[i] = (on && t >= 0) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(src.ptr) +
+                                                                   q.at(src, t) + c)
+                                : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < RPASS; ++i) {
+        const int r = r0 + 8 * i, t = q.token(r);
+        if (!on || t < 0) continue;
+        float x[8], rc[8];
+        bf8_to_f32(raw[i], x);
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&E[r * lde + c]);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&E[r * lde + c + 4]);
+        rc[0] = a.x; rc[1] = a.y; rc[2] = a.z; rc[3] = a.w; rc[4] = b.x; rc[5] = b.y; rc[6] = b.z; rc[7] = b.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rc[e] = round_as<bf16_t>(rc[e]);
+          x[e] = x[e] - eta * rc[e];
+        }
+        *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(dst.ptr) + q.at(dst, t) + c) = f32_to_bf8(x);
+        *reinterpret_cast<uint4*>(saved + q.saved(t, D) + c) = f32_to_bf8(rc);
+      }
+    } else
+    for (int r = wave; r < LROWS; r += LW) {
+      const int t = q.token(r);
+      if (t < 0) continue;
+      const bf16_t* x = reinterpret_cast<const bf16_t*>(src.ptr) + q.at(src, t);
+      bf16_t* y = reinterpret_cast<bf16_t*>(dst.ptr) + q.at(dst, t);
+      bf16_t* sv = saved + q.saved(t, D);
+      for (int c = lane; c < D; c += 64) {
+        const float rc = round_as<bf16_t>(E[r * lde + c]);
+        y[c] = from_f32<bf16_t>(round_as<bf16_t>(to_f32(x[c]) - eta * rc));
+        sv[c] = from_f32<bf16_t>(rc);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 int check_level(const gpa_level_problem* p) {
   if (!p) return fail(GPA_HIP_EINVAL, "level: null problem");
   if (p->batch < 1 || p->tokens < 1 || p->heads < 1) return fail(GPA_HIP_EINVAL, "level: empty shape");
@@ -572,6 +932,30 @@ int launch_level_fwd(const gpa_level_problem& p, dim3 grid, hipStream_t stream) 
   hipLaunchKernelGGL((level_fwd<E, SR>), grid, dim3(LNT), lds, stream, p);
   return GPA_HIP_OK;
 }
+// Vector fragment loads need whole 16-wide contraction steps (and so 32-byte
+// aligned snapshot rows).
+// Rows of the activation operands are read and written as 16-byte vectors.
+bool rows_aligned(const gpa_operand& o) {
+  return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.sb % 8 == 0 && o.st % 8 == 0 && o.sh % 8 == 0;
+}
+
+bool level_fast(const gpa_level_problem& p) {
+  return p.key_dim % 16 == 0 && p.value_dim % 16 == 0 && p.slots % 16 == 0 && rows_aligned(p.key) &&
+         rows_aligned(p.value) && rows_aligned(p.write) && rows_aligned(p.key_out) && rows_aligned(p.value_out);
+}
+
+int launch_level_fwd16(const gpa_level_problem& p, dim3 grid, hipStream_t stream) {
+  const size_t lds = Lds16(p.key_dim, p.value_dim, p.slots).bytes;
+  if (level_fast(p)) {
+    if (int rc = level_lds(level_fwd16<true>, lds)) return rc;
+    hipLaunchKernelGGL((level_fwd16<true>), grid, dim3(LNT), lds, stream, p);
+  } else {
+    if (int rc = level_lds(level_fwd16<false>, lds)) return rc;
+    hipLaunchKernelGGL((level_fwd16<false>), grid, dim3(LNT), lds, stream, p);
+  }
+  return GPA_HIP_OK;
+}
+
 template <typename E, int SR>
 int launch_level_bwd(const gpa_level_problem& p, const gpa_level_grads& g, dim3 grid, hipStream_t stream) {
   const size_t lds = sizeof(float) * LevelLds(p.key_dim, p.value_dim, p.slots, SR).bwd_floats();
@@ -591,8 +975,7 @@ extern "C" int gpa_level_forward(const gpa_level_problem* problem, hipStream_t s
   const int N = (problem->offset + problem->tokens + problem->chunk - 1) / problem->chunk;
   const dim3 grid(N, problem->batch * problem->heads);
   const bool bf = problem->dtype == GPA_DTYPE_BF16, big = slab_rows(*problem, false) == 64;
-  int rc = bf ? (big ? launch_level_fwd<bf16_t, 64>(*problem, grid, stream)
-                     : launch_level_fwd<bf16_t, 32>(*problem, grid, stream))
+  int rc = bf ? launch_level_fwd16(*problem, grid, stream)
               : (big ? launch_level_fwd<float, 64>(*problem, grid, stream)
                      : launch_level_fwd<float, 32>(*problem, grid, stream));
   if (rc) return rc;

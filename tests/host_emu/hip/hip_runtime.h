@@ -35,6 +35,11 @@ struct uint2 {
 struct uint4 {
   unsigned x, y, z, w;
 };
+inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
+struct float4 {
+  float x, y, z, w;
+};
+inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
 struct EmuIdx {
   unsigned x, y, z;
 };
