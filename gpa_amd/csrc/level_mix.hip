@@ -587,7 +587,7 @@ __device__ __forceinline__ void raw8(const Col& c, int first, float (&v)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int i = first + e < c.count ? first + e : c.count - 1;
-      const float x = c.base[(int64_t)i * c.st];
+      const float x = c.base[i * c.st];
       v[e] = (c.ok && first + e < c.count) ? x : 0.f;
     }
   }
@@ -620,6 +620,12 @@ __device__ __forceinline__ Col ahat_m(const Block& q, int k) {
 __device__ __forceinline__ Col bhat_m(const Block& q, int v) {
   const int vc = v < q.Dv ? v : q.Dv - 1;
   return q.b_first ? Col{q.b_fs + vc, q.Dv, q.M, v < q.Dv} : Col{q.b_st + (int64_t)vc * q.M, 1, q.M, v < q.Dv};
+}
+
+// B^ along v, column m: B^[m][.].
+__device__ __forceinline__ Col bhat_v(const Block& q, int m) {
+  const int mc = m < q.M ? m : q.M - 1;
+  return q.b_first ? Col{q.b_fs + (int64_t)mc * q.Dv, 1, q.Dv, m < q.M} : Col{q.b_st + mc, q.M, q.Dv, m < q.M};
 }
 
 // acc[rt] += A_rt B (rt = 0, 1: the block's two 32-row tiles) over `steps`
@@ -891,6 +897,400 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// The backward for bf16 activations on bf16 MFMA, for aligned widths (all
+// multiples of 16, 16-byte aligned rows); other shapes keep level_bwd.
+// 8 waves.  Per block (rows t, slots m, keys k, values v):
+//   drk = round(-eta0 dkey'), drv = round(-eta1 dvalue')           (exact bf16)
+//   dB^T = drv^T w                                                 -> db
+//   dw   = round(dwrite + round(drk A^^T... + drv B^^T))  (drk A^ + drv B^T)
+//   p    = softmax(u A^) from the saved row max and sum
+//   dl   = p (dw - <p, dw>)
+//   dA^T = w^T drk + dl^T u                                        -> da
+//   du   = dl A^T;  dkey = round(dkey' + round(unit backward of round(du)))
+// Products contracting over the block's rows read token-contiguous LDS
+// copies (w^T, drk^T, drv^T, u^T, dl^T), written with the lanes along the
+// rows; the one product contracting over slots (du) gathers its dl rows from
+// dl^T.  Snapshot fragments come from global memory as in the forward.
+constexpr int BW = 8, BNT = 64 * BW;  // waves, threads
+constexpr int TP = LROWS + 8;         // bf16 pitch of token-contiguous rows
+
+struct Lds16b {
+  int wt, drkt, ut, drvt, dlt_hi, dlt_lo, du, bytes;  // byte offsets
+  int lde;                                            // float pitch of du rows
+  __host__ __device__ Lds16b(int Dk, int Dv, int M) {
+    const int x = LROWS > 0 ? 2 * TP : 0;             // bytes per token-contiguous row
+    wt = 0;
+    drkt = wt + M * x;
+    ut = drkt + Dk * x;
+    dlt_hi = ut + Dk * x;
+    dlt_lo = dlt_hi + M * x;
+    drvt = dlt_hi;                                    // dead before dl^T is written
+    lde = Dk + 4;
+    const int need_du = LROWS * lde * 4, need_drvt = Dv * x;
+    bytes = dlt_lo + M * x;
+    if (dlt_hi + need_drvt > bytes) bytes = dlt_hi + need_drvt;
+    // du replaces w^T .. u^T (dead by then) when it fits below dl^T, which is
+    // still being read while du is written; else it goes after everything.
+    du = need_du <= dlt_hi ? 0 : bytes;
+    if (du) bytes += need_du;
+  }
+};
+
+template <int TW>  // (row tile, slot tile) pairs per wave in the dw / logits phase: 2 M / 32 / BW
+__global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_level_grads g) {
+  HIP_DYNAMIC_SHARED(float, lds_f)
+  unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
+  __shared__ float den_s[LROWS], mx_s[LROWS], sm_s[LROWS], dot_s[LROWS];
+  __shared__ float red[BW][2];
+  const Block q(p);
+  const int Dk = q.Dk, Dv = q.Dv, M = q.M, H = q.H, N = q.N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
+  const Lds16b L(Dk, Dv, M);
+  __bf16* WT = reinterpret_cast<__bf16*>(lds + L.wt);     // w^T     [M][TP]
+  __bf16* DRKT = reinterpret_cast<__bf16*>(lds + L.drkt); // drk^T   [Dk][TP]
+  __bf16* UT = reinterpret_cast<__bf16*>(lds + L.ut);     // u^T     [Dk][TP]
+  __bf16* DRVT = reinterpret_cast<__bf16*>(lds + L.drvt); // drv^T   [Dv][TP]
+  __bf16* DLH = reinterpret_cast<__bf16*>(lds + L.dlt_hi); // dl^T hi [M][TP]
+  __bf16* DLL = reinterpret_cast<__bf16*>(lds + L.dlt_lo); // dl^T lo
+  float* DU = reinterpret_cast<float*>(lds + L.du);        // du      [64][lde]
+  const float eta0 = p.eta[2 * q.h], eta1 = p.eta[2 * q.h + 1];
+  const bf16_t* key = reinterpret_cast<const bf16_t*>(p.key.ptr);
+  const int MT = M / 32, KT = Dk / 32, VT = Dv / 32, K16 = Dk / 16, V16 = Dv / 16, M16 = M / 16;
+
+  // ---- rows: norms of the keys (16 rows per pass, 32 lanes per row) and the
+  // saved softmax statistics.
+  {
+    const int c = 8 * (tid & 31), r0 = tid >> 5;
+    uint4 raw[LROWS / 16];
+#pragma unroll
+    for (int i = 0; i < LROWS / 16; ++i) {
+      const int t = q.token(r0 + 16 * i);
+      raw[i] = (c < Dk && t >= 0) ? *reinterpret_cast<const uint4*>(key + q.at(p.key, t) + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LROWS / 16; ++i) {
+      float x[8];
+      bf8_to_f32(raw[i], x);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      ss = sum32(ss);
+      const int r = r0 + 16 * i, t = q.token(r);
+      if ((tid & 31) == 0) {
+        den_s[r] = fmaxf(sqrtf(ss), 1e-6f);
+        mx_s[r] = t >= 0 ? p.stats[q.saved(t, 2)] : 0.f;
+        sm_s[r] = t >= 0 ? p.stats[q.saved(t, 2) + 1] : 1.f;
+        dot_s[r] = 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- token-contiguous copies: lane = row, wave = group of 8 columns.
+  float d_eta0 = 0.f, d_eta1 = 0.f;
+  {
+    const int t = q.token(lane);
+    auto load8 = [&](const gpa_operand& o, int c) {
+      return t >= 0 ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(o.ptr) + q.at(o, t) + c)
+                    : make_uint4(0, 0, 0, 0);
+    };
+    auto saved8 = [&](const void* base, int D, int c) {
+      return t >= 0 ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(base) + q.saved(t, D) + c)
+                    : make_uint4(0, 0, 0, 0);
+    };
+    auto put_t = [&](__bf16* dst, int c, const float (&x)[8]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[(c + e) * TP + lane] = (__bf16)x[e];
+    };
+    for (int c = 8 * wave; c < M; c += 8 * BW) {  // w^T
+      float x[8];
+      bf8_to_f32(load8(p.write, c), x);
+      put_t(WT, c, x);
+    }
+    for (int c = 8 * wave; c < Dk; c += 8 * BW) {  // drk^T, u^T, d eta0
+      const uint4 a = load8(g.dkey_out, c), b = saved8(p.rk, Dk, c), kk = load8(p.key, c);
+      float d[8], r[8], x[8];
+      bf8_to_f32(a, d);
+      bf8_to_f32(b, r);
+      bf8_to_f32(kk, x);
+      const float den = den_s[lane];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        d_eta0 -= d[e] * r[e];
+        d[e] = round_as<bf16_t>(-eta0 * d[e]);
+        x[e] = x[e] / den;
+      }
+      put_t(DRKT, c, d);
+      put_t(UT, c, x);
+    }
+    for (int c = 8 * wave; c < Dv; c += 8 * BW) {  // drv^T, d eta1
+      const uint4 a = load8(g.dvalue_out, c), b = saved8(p.rv, Dv, c);
+      float d[8], r[8];
+      bf8_to_f32(a, d);
+      bf8_to_f32(b, r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        d_eta1 -= d[e] * r[e];
+        d[e] = round_as<bf16_t>(-eta1 * d[e]);
+      }
+      put_t(DRVT, c, d);
+    }
+  }
+  __syncthreads();
+
+  auto frag_t = [&](const __bf16* X, int row, int ts) {  // 8 tokens of row `row` of a token-contiguous copy
+    return *reinterpret_cast<const bf16x8*>(&X[row * TP + 16 * ts + 8 * hh]);
+  };
+
+  // ---- dB^T[v][m] = sum_t drv[t][v] w[t][m]  -> db
+  for (int i = wave; i < VT * MT; i += BW) {
+    const int vt = i % VT, mt = i / VT;
+    f32x16 acc = {};
+#pragma unroll
+    for (int ts = 0; ts < LROWS / 16; ++ts)
+      acc = mfma16(frag_t(DRVT, 32 * vt + li, ts), frag_t(WT, 32 * mt + li, ts), acc);
+    const int m = 32 * mt + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int v = 32 * vt + acc_row(r, hh);
+      if (q.b_first) g.db_first[((int64_t)q.b * H + q.h) * M * Dv + (int64_t)m * Dv + v] = acc[r];
+      else g.db_states[(((int64_t)q.b * H + q.h) * N + q.n) * Dv * M + (int64_t)v * M + m] = acc[r];
+    }
+  }
+
+  // ---- dw and the recomputed logits per (row tile i & 1, slot tile i >> 1):
+  // p and dw of the tile, in accumulator layout.
+  auto dw_logits = [&](int i, float (&pk)[16], float (&dk)[16]) {
+    const int rt = i & 1, mt = i >> 1;
+      const int m = 32 * mt + li, row = 32 * rt + li, trow = q.token(row);
+      // A fragments from global: drk and u (contraction k), drv (contraction v).
+      const bf16_t* dkr = reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + (trow >= 0 ? q.at(g.dkey_out, trow) : 0);
+      const bf16_t* dvr = reinterpret_cast<const bf16_t*>(g.dvalue_out.ptr) + (trow >= 0 ? q.at(g.dvalue_out, trow) : 0);
+      const bf16_t* kr = key + (trow >= 0 ? q.at(p.key, trow) : 0);
+      const float den = den_s[row];
+      auto a_frag = [&](const uint4& raw, float scale, bool unit) {
+        float x[8];
+        bf8_to_f32(raw, x);
+        bf16x8 f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (__bf16)(unit ? x[e] / den : round_as<bf16_t>(scale * x[e]));
+        return f;
+      };
+      f32x16 cw[2] = {}, cl[2] = {};
+      const Col ak = ahat_k(q, m);
+      constexpr int G = 4;
+#pragma unroll 1
+      for (int s0 = 0; s0 < K16; s0 += G) {
+        float v[G][8];
+        uint4 rd[G], rk[G];
+#pragma unroll
+        for (int jj = 0; jj < G; ++jj)
+          if (s0 + jj < K16) {
+            const int c0 = 16 * (s0 + jj) + 8 * hh;
+            raw8<true>(ak, c0, v[jj]);
+            rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dkr + c0) : make_uint4(0, 0, 0, 0);
+            rk[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
+          }
+#pragma unroll
+        for (int jj = 0; jj < G; ++jj)
+          if (s0 + jj < K16) {
+            bf16x8 bh, bl;
+            split8(v[jj], bh, bl);
+            const bf16x8 ad = a_frag(rd[jj], -eta0, false), au = a_frag(rk[jj], 1.f, true);
+            cw[0] = mfma16(ad, bh, cw[0]);
+            cl[0] = mfma16(au, bh, cl[0]);
+            cw[1] = mfma16(ad, bl, cw[1]);
+            cl[1] = mfma16(au, bl, cl[1]);
+          }
+      }
+      const Col bv = bhat_v(q, m);
+#pragma unroll 1
+      for (int s0 = 0; s0 < V16; s0 += G) {
+        float v[G][8];
+        uint4 rd[G];
+#pragma unroll
+        for (int jj = 0; jj < G; ++jj)
+          if (s0 + jj < V16) {
+            const int c0 = 16 * (s0 + jj) + 8 * hh;
+            raw8<true>(bv, c0, v[jj]);
+            rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dvr + c0) : make_uint4(0, 0, 0, 0);
+          }
+#pragma unroll
+        for (int jj = 0; jj < G; ++jj)
+          if (s0 + jj < V16) {
+            bf16x8 bh, bl;
+            split8(v[jj], bh, bl);
+            const bf16x8 ad = a_frag(rd[jj], -eta1, false);
+            cw[0] = mfma16(ad, bh, cw[0]);
+            cw[1] = mfma16(ad, bl, cw[1]);
+          }
+      }
+      const f32x16 dwa = cw[0] + cw[1], lga = cl[0] + cl[1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * rt + acc_row(r, hh), tk = q.token(t);
+      float dw = 0.f;
+      if (tk >= 0) {
+        const float dwr = to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m]);
+        dw = round_as<bf16_t>(dwr + round_as<bf16_t>(dwa[r]));
+      }
+      pk[r] = __expf(lga[r] - mx_s[t]) / sm_s[t];
+      dk[r] = dw;
+    }
+  };
+  auto add_dot = [&](int i, const float (&pk)[16], const float (&dk)[16]) {
+    float part[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[r] = pk[r] * dk[r];
+    const float tot = tile_row_sum(part, lane);
+    if ((lane & 1) == 0) atomicAdd(&dot_s[32 * (i & 1) + acc_row(sum_index(lane), hh)], tot);
+  };
+  auto put_dl = [&](int i, const float (&pk)[16], const float (&dk)[16]) {  // dl = p (dw - dot) -> dl^T
+    const int rt = i & 1, m = 32 * (i >> 1) + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * rt + acc_row(r, hh);
+      const float x = pk[r] * (dk[r] - dot_s[t]);
+      const __bf16 hi = (__bf16)x;
+      DLH[m * TP + t] = hi;
+      DLL[m * TP + t] = (__bf16)(x - (float)hi);
+    }
+  };
+  if (TW == 1) {  // one tile per wave: p and dw stay in registers across the row-dot barrier
+    const int i = wave;
+    float pk[16], dk[16];
+    const bool mine = (i >> 1) < MT;
+    if (mine) {
+      dw_logits(i, pk, dk);
+      add_dot(i, pk, dk);
+    }
+    __syncthreads();
+    if (mine) put_dl(i, pk, dk);
+  } else {  // several tiles per wave: the row dots first, then the tiles again
+#pragma unroll 1
+    for (int i = wave; i < 2 * MT; i += BW) {
+      float pk[16], dk[16];
+      dw_logits(i, pk, dk);
+      add_dot(i, pk, dk);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int i = wave; i < 2 * MT; i += BW) {
+      float pk[16], dk[16];
+      dw_logits(i, pk, dk);
+      put_dl(i, pk, dk);
+    }
+  }
+  __syncthreads();
+
+  // ---- dA^T[m][k] = sum_t w[t][m] drk[t][k] + dl[t][m] u[t][k]  -> da
+  auto da_at = [&](int m, int k) -> float* {
+    return q.a_first ? g.da_first + ((int64_t)q.b * H + q.h) * Dk * M + (int64_t)k * M + m
+                     : g.da_states + (((int64_t)q.b * H + q.h) * N + q.n) * M * Dk + (int64_t)m * Dk + k;
+  };
+  for (int i = wave; i < MT * KT; i += BW) {
+    const int mt = i % MT, kt = i / MT;
+    f32x16 a1 = {}, a2 = {};
+#pragma unroll
+    for (int ts = 0; ts < LROWS / 16; ++ts) {
+      const bf16x8 drk = frag_t(DRKT, 32 * kt + li, ts), u = frag_t(UT, 32 * kt + li, ts);
+      a1 = mfma16(frag_t(WT, 32 * mt + li, ts), drk, a1);
+      a2 = mfma16(frag_t(DLH, 32 * mt + li, ts), u, a2);
+      a1 = mfma16(frag_t(DLL, 32 * mt + li, ts), u, a1);
+    }
+    const int k = 32 * kt + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) *da_at(32 * mt + acc_row(r, hh), k) = a1[r] + a2[r];
+  }
+  __syncthreads();  // w^T, drk^T and u^T are dead: du reuses their memory
+
+  // ---- du[t][k] = sum_m dl[t][m] A^[k][m], dl rows gathered from dl^T.
+  for (int i = wave; i < 2 * KT; i += BW) {
+    const int rt = i & 1, kt = i >> 1, k = 32 * kt + li;
+    const Col am = ahat_m(q, k);
+    f32x16 c1 = {}, c2 = {};
+    constexpr int G = 4;
+#pragma unroll 1
+    for (int s0 = 0; s0 < M16; s0 += G) {
+      float v[G][8];
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj)
+        if (s0 + jj < M16) raw8<true>(am, 16 * (s0 + jj) + 8 * hh, v[jj]);
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj)
+        if (s0 + jj < M16) {
+          bf16x8 bh, bl, ah, al;
+          split8(v[jj], bh, bl);
+          const int m0 = 16 * (s0 + jj) + 8 * hh, t = 32 * rt + li;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            ah[e] = DLH[(m0 + e) * TP + t];
+            al[e] = DLL[(m0 + e) * TP + t];
+          }
+          c1 = mfma16(ah, bh, c1);
+          c2 = mfma16(ah, bl, c2);
+          c1 = mfma16(al, bh, c1);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) DU[(32 * rt + acc_row(r, hh)) * L.lde + k] = round_as<bf16_t>(c1[r] + c2[r]);
+  }
+  __syncthreads();
+
+  // ---- dkey = round(dkey' + round(unit backward of du)), 16 rows per pass.
+  {
+    const int c = 8 * (tid & 31), r0 = tid >> 5;
+    const bool on = c < Dk;
+#pragma unroll
+    for (int i = 0; i < LROWS / 16; ++i) {
+      const int r = r0 + 16 * i, t = q.token(r);
+      float x[8], du[8];
+      if (on && t >= 0) bf8_to_f32(*reinterpret_cast<const uint4*>(key + q.at(p.key, t) + c), x);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+      const float den = den_s[r];
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        du[e] = on ? DU[r * L.lde + c + e] : 0.f;
+        x[e] = x[e] / den;
+        dot += x[e] * du[e];
+      }
+      dot = sum32(dot);
+      if (!on || t < 0) continue;
+      float dko[8];
+      bf8_to_f32(*reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + q.at(g.dkey_out, t) + c), dko);
+      const bool clamped = den <= 1e-6f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ub = clamped ? du[e] / den : (du[e] - x[e] * dot) / den;
+        dko[e] = round_as<bf16_t>(dko[e] + round_as<bf16_t>(ub));
+      }
+      *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(g.dkey.ptr) + q.at(g.dkey, t) + c) = f32_to_bf8(dko);
+    }
+  }
+
+  {  // per-block sums of d eta
+    float a = d_eta0, c = d_eta1;
+    for (int o = 32; o >= 1; o >>= 1) {
+      a += __shfl_xor(a, o);
+      c += __shfl_xor(c, o);
+    }
+    if (lane == 0) {
+      red[wave][0] = a;
+      red[wave][1] = c;
+    }
+    __syncthreads();
+    if (tid < 2) {
+      float x = 0.f;
+      for (int w = 0; w < BW; ++w) x += red[w][tid];
+      g.deta[(((int64_t)q.b * H + q.h) * N + q.n) * 2 + tid] = x;
+    }
+  }
+}
+
 int check_level(const gpa_level_problem* p) {
   if (!p) return fail(GPA_HIP_EINVAL, "level: null problem");
   if (p->batch < 1 || p->tokens < 1 || p->heads < 1) return fail(GPA_HIP_EINVAL, "level: empty shape");
@@ -944,6 +1344,14 @@ bool level_fast(const gpa_level_problem& p) {
          rows_aligned(p.value) && rows_aligned(p.write) && rows_aligned(p.key_out) && rows_aligned(p.value_out);
 }
 
+// level_bwd16: widths multiples of 32, 16-byte aligned rows, LDS within the CU.
+bool level_bwd16_ok(const gpa_level_problem& p, const gpa_level_grads& g) {
+  const size_t statics = 4 * LROWS * sizeof(float) + BW * 2 * sizeof(float);
+  return p.key_dim % 32 == 0 && p.value_dim % 32 == 0 && p.slots % 32 == 0 && level_fast(p) &&
+         rows_aligned(g.dkey_out) && rows_aligned(g.dvalue_out) && rows_aligned(g.dkey) &&
+         Lds16b(p.key_dim, p.value_dim, p.slots).bytes + statics <= LDS_MAX;
+}
+
 int launch_level_fwd16(const gpa_level_problem& p, dim3 grid, hipStream_t stream) {
   const size_t lds = Lds16(p.key_dim, p.value_dim, p.slots).bytes;
   if (level_fast(p)) {
@@ -993,6 +1401,17 @@ extern "C" int gpa_level_backward(const gpa_level_problem* problem, const gpa_le
   const int N = (problem->offset + problem->tokens + problem->chunk - 1) / problem->chunk;
   const dim3 grid(N, problem->batch * problem->heads);
   const bool bf = problem->dtype == GPA_DTYPE_BF16, big = slab_rows(*problem, true) == 64;
+  if (bf && level_bwd16_ok(*problem, *grads)) {
+    const size_t lds = Lds16b(problem->key_dim, problem->value_dim, problem->slots).bytes;
+    if (problem->slots <= 128) {
+      if (int rc = level_lds(level_bwd16<1>, lds)) return rc;
+      hipLaunchKernelGGL((level_bwd16<1>), grid, dim3(BNT), lds, stream, *problem, *grads);
+    } else {
+      if (int rc = level_lds(level_bwd16<2>, lds)) return rc;
+      hipLaunchKernelGGL((level_bwd16<2>), grid, dim3(BNT), lds, stream, *problem, *grads);
+    }
+    return check_launch("gpa_level_backward");
+  }
   int rc = bf ? (big ? launch_level_bwd<bf16_t, 64>(*problem, *grads, grid, stream)
                      : launch_level_bwd<bf16_t, 32>(*problem, *grads, grid, stream))
               : (big ? launch_level_bwd<float, 64>(*problem, *grads, grid, stream)

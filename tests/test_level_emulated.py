@@ -23,6 +23,7 @@ CASES = {
     "broadcast_first": dict(b=2, t=5, h=1, dk=8, dv=6, m=4, c=4, offset=2, first="broadcast"),
     "no_first": dict(b=1, t=9, h=2, dk=16, dv=8, m=12, c=4, offset=0, first=None),
     "c3_widths": dict(b=1, t=70, h=1, dk=128, dv=128, m=256, c=64, offset=0, first=None),
+    "aligned_first": dict(b=2, t=40, h=1, dk=64, dv=32, m=96, c=16, offset=5, first="full"),
 }
 
 
