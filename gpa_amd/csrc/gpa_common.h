@@ -13,12 +13,13 @@ struct bf16_t {
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float((uint32_t)x.bits << 16); }
 
-// Round-to-nearest-even float -> bfloat16 (NaN kept quiet).
+// Round-to-nearest-even float -> bfloat16 (a NaN stays a NaN): the hardware
+// conversion (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return bf16_t{(uint16_t)((u >> 16) | 0x40u)};
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bf16_t{(uint16_t)(u >> 16)};
+  const __bf16 h = (__bf16)f;
+  bf16_t r;
+  __builtin_memcpy(&r, &h, sizeof r);
+  return r;
 }
 
 template <typename E> __device__ __forceinline__ E from_f32(float x);

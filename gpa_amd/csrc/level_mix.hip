@@ -1063,80 +1063,76 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
   // p and dw of the tile, in accumulator layout.
   auto dw_logits = [&](int i, float (&pk)[16], float (&dk)[16]) {
     const int rt = i & 1, mt = i >> 1;
-      const int m = 32 * mt + li, row = 32 * rt + li, trow = q.token(row);
-      // A fragments from global: drk and u (contraction k), drv (contraction v).
-      const bf16_t* dkr = reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + (trow >= 0 ? q.at(g.dkey_out, trow) : 0);
-      const bf16_t* dvr = reinterpret_cast<const bf16_t*>(g.dvalue_out.ptr) + (trow >= 0 ? q.at(g.dvalue_out, trow) : 0);
-      const bf16_t* kr = key + (trow >= 0 ? q.at(p.key, trow) : 0);
-      const float den = den_s[row];
-      auto a_frag = [&](const uint4& raw, float scale, bool unit) {
-        float x[8];
-        bf8_to_f32(raw, x);
-        bf16x8 f;
+    const int m = 32 * mt + li, row = 32 * rt + li, trow = q.token(row);
+    // dwrite of the tile's elements, loaded first so that it arrives meanwhile.
+    float dwr[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (__bf16)(unit ? x[e] / den : round_as<bf16_t>(scale * x[e]));
-        return f;
-      };
-      f32x16 cw[2] = {}, cl[2] = {};
-      const Col ak = ahat_k(q, m);
-      constexpr int G = 4;
+    for (int r = 0; r < 16; ++r) {
+      const int tk = q.token(32 * rt + acc_row(r, hh));
+      dwr[r] = tk >= 0 ? to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m]) : 0.f;
+    }
+    // A fragments from global: drk and u (contraction k), drv (contraction v).
+    const bf16_t* dkr = reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + (trow >= 0 ? q.at(g.dkey_out, trow) : 0);
+    const bf16_t* dvr = reinterpret_cast<const bf16_t*>(g.dvalue_out.ptr) + (trow >= 0 ? q.at(g.dvalue_out, trow) : 0);
+    const bf16_t* kr = key + (trow >= 0 ? q.at(p.key, trow) : 0);
+    const float den = den_s[row];
+    auto a_frag = [&](const uint4& raw, float scale, bool unit) {
+      float x[8];
+      bf8_to_f32(raw, x);
+      bf16x8 f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (__bf16)(unit ? x[e] / den : round_as<bf16_t>(scale * x[e]));
+      return f;
+    };
+    // The key-side (A^, contraction k) and value-side (B^^T, contraction v)
+    // products run in one loop, so the loads of both are in flight together.
+    f32x16 cw[2] = {}, cl[2] = {};
+    const Col ak = ahat_k(q, m), bv = bhat_v(q, m);
+    constexpr int G = 4;
+    const int S16 = K16 > V16 ? K16 : V16;
 #pragma unroll 1
-      for (int s0 = 0; s0 < K16; s0 += G) {
-        float v[G][8];
-        uint4 rd[G], rk[G];
+    for (int s0 = 0; s0 < S16; s0 += G) {
+      float va[G][8], vb[G][8];
+      uint4 rd[G], rk[G], rv[G];
 #pragma unroll
-        for (int jj = 0; jj < G; ++jj)
-          if (s0 + jj < K16) {
-            const int c0 = 16 * (s0 + jj) + 8 * hh;
-            raw8<true>(ak, c0, v[jj]);
-            rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dkr + c0) : make_uint4(0, 0, 0, 0);
-            rk[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
-          }
-#pragma unroll
-        for (int jj = 0; jj < G; ++jj)
-          if (s0 + jj < K16) {
-            bf16x8 bh, bl;
-            split8(v[jj], bh, bl);
-            const bf16x8 ad = a_frag(rd[jj], -eta0, false), au = a_frag(rk[jj], 1.f, true);
-            cw[0] = mfma16(ad, bh, cw[0]);
-            cl[0] = mfma16(au, bh, cl[0]);
-            cw[1] = mfma16(ad, bl, cw[1]);
-            cl[1] = mfma16(au, bl, cl[1]);
-          }
+      for (int jj = 0; jj < G; ++jj) {
+        const int c0 = 16 * (s0 + jj) + 8 * hh;
+        if (s0 + jj < K16) {
+          raw8<true>(ak, c0, va[jj]);
+          rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dkr + c0) : make_uint4(0, 0, 0, 0);
+          rk[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
+        }
+        if (s0 + jj < V16) {
+          raw8<true>(bv, c0, vb[jj]);
+          rv[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dvr + c0) : make_uint4(0, 0, 0, 0);
+        }
       }
-      const Col bv = bhat_v(q, m);
-#pragma unroll 1
-      for (int s0 = 0; s0 < V16; s0 += G) {
-        float v[G][8];
-        uint4 rd[G];
 #pragma unroll
-        for (int jj = 0; jj < G; ++jj)
-          if (s0 + jj < V16) {
-            const int c0 = 16 * (s0 + jj) + 8 * hh;
-            raw8<true>(bv, c0, v[jj]);
-            rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dvr + c0) : make_uint4(0, 0, 0, 0);
-          }
-#pragma unroll
-        for (int jj = 0; jj < G; ++jj)
-          if (s0 + jj < V16) {
-            bf16x8 bh, bl;
-            split8(v[jj], bh, bl);
-            const bf16x8 ad = a_frag(rd[jj], -eta1, false);
-            cw[0] = mfma16(ad, bh, cw[0]);
-            cw[1] = mfma16(ad, bl, cw[1]);
-          }
+      for (int jj = 0; jj < G; ++jj) {
+        if (s0 + jj < K16) {
+          bf16x8 bh, bl;
+          split8(va[jj], bh, bl);
+          const bf16x8 ad = a_frag(rd[jj], -eta0, false), au = a_frag(rk[jj], 1.f, true);
+          cw[0] = mfma16(ad, bh, cw[0]);
+          cl[0] = mfma16(au, bh, cl[0]);
+          cw[1] = mfma16(ad, bl, cw[1]);
+          cl[1] = mfma16(au, bl, cl[1]);
+        }
+        if (s0 + jj < V16) {
+          bf16x8 bh, bl;
+          split8(vb[jj], bh, bl);
+          const bf16x8 ad = a_frag(rv[jj], -eta1, false);
+          cw[0] = mfma16(ad, bh, cw[0]);
+          cw[1] = mfma16(ad, bl, cw[1]);
+        }
       }
-      const f32x16 dwa = cw[0] + cw[1], lga = cl[0] + cl[1];
+    }
+    const f32x16 dwa = cw[0] + cw[1], lga = cl[0] + cl[1];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 32 * rt + acc_row(r, hh), tk = q.token(t);
-      float dw = 0.f;
-      if (tk >= 0) {
-        const float dwr = to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m]);
-        dw = round_as<bf16_t>(dwr + round_as<bf16_t>(dwa[r]));
-      }
+      dk[r] = tk >= 0 ? round_as<bf16_t>(dwr[r] + round_as<bf16_t>(dwa[r])) : 0.f;
       pk[r] = __expf(lga[r] - mx_s[t]) / sm_s[t];
-      dk[r] = dw;
     }
   };
   auto add_dot = [&](int i, const float (&pk)[16], const float (&dk)[16]) {

@@ -153,7 +153,38 @@ __device__ __forceinline__ void row_softmax(int M, int part, const float (&v)[RP
   for (int i = 0; i < RPER; ++i) pr[i] /= s;
 }
 
-template <typename E>
+// VEC (bf16 activations, widths multiples of 8, 16-byte aligned rows): the
+// row phases run with 32 lanes per row, 8 columns each, every 16-byte load of
+// a thread issued before its first use.
+constexpr int VPASS = RR / (RNT / 32);  // row passes of 8 rows
+
+__device__ __forceinline__ float vsum32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+  return x;
+}
+__device__ __forceinline__ float vmax32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 32));
+  return x;
+}
+__device__ __forceinline__ void unpack_bf8(const uint4& u, float (&x)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint4 pack_bf8(const float (&x)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(x[2 * i]).bits | ((uint32_t)f32_to_bf16(x[2 * i + 1]).bits << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <typename E, bool VEC>
 __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   using W = typename Wt<E>::type;
   HIP_DYNAMIC_SHARED(float, lds)
@@ -170,7 +201,79 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   E* shd = reinterpret_cast<E*>(p.hd) + (int64_t)h * R * M;
 
   // ---- r0 = softmax(base + gain tanh z)
-  {
+  if constexpr (VEC) {
+    const int c = 8 * (tid & 31), rsub = tid >> 5;
+    const bool on = c < M;
+    float bv[VPASS][8];
+    uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
+      if (on) {
+        const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
+        bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
+        bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
+#pragma unroll
+        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+          if (e < p.incoming)
+            mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
+                                                       rows.at(p.msg[e], rr, h) + c);
+      }
+    }
+    const float gain = p.gain[h];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int row = rsub + 8 * i, r = row0 + row;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
+      if (p.incoming > 0) {
+        float z[8] = {};
+#pragma unroll
+        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+          if (e < p.incoming && on) {
+            const float w = p.edge_weight[e * p.heads + h];
+            float x[8];
+            unpack_bf8(mv[i][e], x);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) z[j] += w * x[j];
+          }
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += z[j];
+        const float mean = vsum32(s) / M;
+        float qq = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          z[j] = on ? z[j] - mean : 0.f;
+          qq += z[j] * z[j];
+        }
+        const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] += gain * tanhf(z[j] / sig);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
+      mx = vmax32(mx);
+      float sm = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[j] = on ? __expf(v[j] - mx) : 0.f;
+        sm += v[j];
+      }
+      sm = vsum32(sm);
+      const bool valid = r < R;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (valid && on) ? round_as<E>(v[j] / sm) : 0.f;
+      if (c < kM) {
+        *reinterpret_cast<f32x4*>(&A[row * lda + c]) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(&A[row * lda + c + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+      }
+      if (valid && on) *reinterpret_cast<uint4*>(sr0 + (int64_t)r * M + c) = pack_bf8(v);
+    }
+  } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
     float v[RPER], z[RPER], pr[RPER], inv;
@@ -235,7 +338,27 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   __syncthreads();
 
   // ---- q -> Hs
-  {
+  if constexpr (VEC) {
+    const int c = 8 * (tid & 31), rsub = tid >> 5;
+    uint4 qv[VPASS];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int r = row0 + rsub + 8 * i;
+      qv[i] = (c < Dk && r < R) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.q.ptr) +
+                                                                   rows.at(p.q, r, h) + c)
+                                : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int row = rsub + 8 * i;
+      float x[8];
+      unpack_bf8(qv[i], x);
+      if (c < kD) {
+        *reinterpret_cast<f32x4*>(&Hs[row * ldh + c]) = f32x4{x[0], x[1], x[2], x[3]};
+        *reinterpret_cast<f32x4*>(&Hs[row * ldh + c + 4]) = f32x4{x[4], x[5], x[6], x[7]};
+      }
+    }
+  } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
     const E* q = reinterpret_cast<const E*>(p.q.ptr) + rows.at(p.q, valid ? r : R - 1, h);
@@ -268,7 +391,7 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   }
 }
 
-template <typename E>
+template <typename E, bool VEC>
 __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_grads g) {
   using W = typename Wt<E>::type;
   HIP_DYNAMIC_SHARED(float, lds)
@@ -290,7 +413,27 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   float part_mg = 0.f, part_gain = 0.f, part_w[GPA_ROUTE_MAX_INCOMING] = {0.f, 0.f, 0.f};
 
   // ---- dqo -> G
-  {
+  if constexpr (VEC) {
+    const int c = 8 * (tid & 31), rsub = tid >> 5;
+    uint4 dv[VPASS];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int r = row0 + rsub + 8 * i;
+      dv[i] = (c < M && r < R) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(g.dqo.ptr) +
+                                                                  rows.at(g.dqo, r, h) + c)
+                               : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int row = rsub + 8 * i;
+      float x[8];
+      unpack_bf8(dv[i], x);
+      if (c < kM) {
+        *reinterpret_cast<f32x4*>(&G[row * lda + c]) = f32x4{x[0], x[1], x[2], x[3]};
+        *reinterpret_cast<f32x4*>(&G[row * lda + c + 4]) = f32x4{x[4], x[5], x[6], x[7]};
+      }
+    }
+  } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
     const E* dqo = reinterpret_cast<const E*>(g.dqo.ptr) + rows.at(g.dqo, valid ? r : R - 1, h);
@@ -338,7 +481,23 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   __syncthreads();
 
   // ---- G <- round(query_scale dqo) (the gradient of q W_qs)
-  {
+  if constexpr (VEC) {
+    const int c = 8 * (tid & 31), rsub = tid >> 5;
+    if (c < M) {
+#pragma unroll
+      for (int i = 0; i < VPASS; ++i) {
+        const int row = rsub + 8 * i, r = row0 + row;
+        float* gr = &G[row * lda + c];
+        const f32x4 a = *reinterpret_cast<const f32x4*>(gr), b = *reinterpret_cast<const f32x4*>(gr + 4);
+        float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = round_as<E>(p.query_scale * x[e]);
+        *reinterpret_cast<f32x4*>(gr) = f32x4{x[0], x[1], x[2], x[3]};
+        *reinterpret_cast<f32x4*>(gr + 4) = f32x4{x[4], x[5], x[6], x[7]};
+        if (r < R) *reinterpret_cast<uint4*>(gdqs + (int64_t)r * M + c) = pack_bf8(x);
+      }
+    }
+  } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
 #pragma unroll
     for (int i = 0; i < RPER; ++i) {
@@ -406,7 +565,130 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   __syncthreads();
 
   // ---- softmax and relation-read backward of each row
-  {
+  if constexpr (VEC) {
+    const int c = 8 * (tid & 31), rsub = tid >> 5;
+    const bool on = c < M;
+    float bv[VPASS][8];
+    uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
+      if (on) {
+        const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
+        bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
+        bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
+#pragma unroll
+        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+          if (e < NI)
+            mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
+                                                       rows.at(p.msg[e], rr, h) + c);
+      }
+    }
+    const float gain = p.gain[h];
+#pragma unroll
+    for (int i = 0; i < VPASS; ++i) {
+      const int row = rsub + 8 * i, r = row0 + row;
+      const bool valid = r < R;
+      float v[8], z[8] = {}, msgf[GPA_ROUTE_MAX_INCOMING][8], inv = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
+      if (NI > 0) {
+#pragma unroll
+        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+          if (e < NI && on) {
+            const float w = p.edge_weight[e * H + h];
+            unpack_bf8(mv[i][e], msgf[e]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) z[j] += w * msgf[e][j];
+          }
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += z[j];
+        const float mean = vsum32(s) / M;
+        float qq = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          z[j] = on ? z[j] - mean : 0.f;
+          qq += z[j] * z[j];
+        }
+        const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
+        inv = 1.f / sig;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          z[j] = z[j] / sig;
+          v[j] += gain * tanhf(z[j]);
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
+      mx = vmax32(mx);
+      float pr[8], sm = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pr[j] = on ? __expf(v[j] - mx) : 0.f;
+        sm += pr[j];
+      }
+      sm = vsum32(sm);
+      float d0[8] = {};
+      if (on) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&A2[row * lda + c]);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&A2[row * lda + c + 4]);
+        d0[0] = a.x; d0[1] = a.y; d0[2] = a.z; d0[3] = a.w; d0[4] = b.x; d0[5] = b.y; d0[6] = b.z; d0[7] = b.w;
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pr[j] /= sm;
+        s += pr[j] * d0[j];
+      }
+      s = vsum32(s);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = on ? pr[j] * (d0[j] - s) : 0.f;  // d base'
+      if (valid && on) {
+        float* db = reinterpret_cast<float*>(g.dbase.ptr) + rows.at(g.dbase, r, h) + c;
+        *reinterpret_cast<f32x4*>(db) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(db + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      }
+      if (NI > 0) {
+        float dz[8], szz = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float th = tanhf(z[j]);
+          if (valid && on) part_gain += v[j] * th;
+          dz[j] = on ? gain * v[j] * (1.f - th * th) : 0.f;
+          szz += dz[j] * z[j];
+        }
+        const float mzz = vsum32(szz) / M;
+        float sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          dz[j] = on ? (dz[j] - z[j] * mzz) * inv : 0.f;  // d centred
+          sc += dz[j];
+        }
+        const float mc = vsum32(sc) / M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dz[j] -= mc;  // d incoming
+#pragma unroll
+        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+          if (e < NI && on) {
+            const float w = p.edge_weight[e * H + h];
+            float sw = 0.f, dm[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              sw += dz[j] * msgf[e][j];
+              dm[j] = round_as<E>(w * dz[j]);
+            }
+            if (valid) {
+              part_w[e] += sw;
+              *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(g.dmsg[e].ptr) + rows.at(g.dmsg[e], r, h) + c) =
+                  pack_bf8(dm);
+            }
+          }
+      }
+    }
+  } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
     const int rc = valid ? r : R - 1;
@@ -637,6 +919,29 @@ int set_lds(K kernel, size_t bytes) {
 }  // namespace
 }  // namespace gpa
 
+namespace gpa {
+namespace {
+// Rows read and written as 16-byte vectors: element strides multiples of 8
+// (4 for float32 rows, whose 8-column pieces are two 16-byte halves).
+bool vec_rows(const gpa_operand& o, int align_elems) {
+  return reinterpret_cast<uintptr_t>(o.ptr) % 16 == 0 && o.sb % align_elems == 0 && o.st % align_elems == 0 &&
+         o.sh % align_elems == 0;
+}
+bool route_vec(const gpa_route_problem& p) {
+  if (p.slots % 8 || p.key_dim % 8 || !vec_rows(p.base, 4) || !vec_rows(p.q, 8)) return false;
+  for (int e = 0; e < p.incoming; ++e)
+    if (!vec_rows(p.msg[e], 8)) return false;
+  return true;
+}
+bool route_bwd_vec(const gpa_route_problem& p, const gpa_route_grads& g) {
+  if (!route_vec(p) || !vec_rows(g.dqo, 8) || !vec_rows(g.dbase, 4)) return false;
+  for (int e = 0; e < p.incoming; ++e)
+    if (!vec_rows(g.dmsg[e], 8)) return false;
+  return true;
+}
+}  // namespace
+}  // namespace gpa
+
 extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_route(problem)) return rc;
@@ -646,12 +951,15 @@ extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t s
   const int R = problem->batch * problem->tokens;
   const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
   const size_t lds = fwd_lds(*problem);
-  if (problem->dtype == GPA_DTYPE_BF16) {
-    if (int rc = set_lds(route_fwd<bf16_t>, lds)) return rc;
-    hipLaunchKernelGGL(route_fwd<bf16_t>, grid, block, lds, stream, *problem);
+  if (problem->dtype == GPA_DTYPE_BF16 && route_vec(*problem)) {
+    if (int rc = set_lds(route_fwd<bf16_t, true>, lds)) return rc;
+    hipLaunchKernelGGL((route_fwd<bf16_t, true>), grid, block, lds, stream, *problem);
+  } else if (problem->dtype == GPA_DTYPE_BF16) {
+    if (int rc = set_lds(route_fwd<bf16_t, false>, lds)) return rc;
+    hipLaunchKernelGGL((route_fwd<bf16_t, false>), grid, block, lds, stream, *problem);
   } else {
-    if (int rc = set_lds(route_fwd<float>, lds)) return rc;
-    hipLaunchKernelGGL(route_fwd<float>, grid, block, lds, stream, *problem);
+    if (int rc = set_lds(route_fwd<float, false>, lds)) return rc;
+    hipLaunchKernelGGL((route_fwd<float, false>), grid, block, lds, stream, *problem);
   }
   return check_launch("gpa_route_forward");
 }
@@ -668,12 +976,15 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
   const int R = problem->batch * problem->tokens;
   const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
   const size_t lds = bwd_lds(*problem);
-  if (problem->dtype == GPA_DTYPE_BF16) {
-    if (int rc = set_lds(route_bwd<bf16_t>, lds)) return rc;
-    hipLaunchKernelGGL(route_bwd<bf16_t>, grid, block, lds, stream, *problem, *grads);
+  if (problem->dtype == GPA_DTYPE_BF16 && route_bwd_vec(*problem, *grads)) {
+    if (int rc = set_lds(route_bwd<bf16_t, true>, lds)) return rc;
+    hipLaunchKernelGGL((route_bwd<bf16_t, true>), grid, block, lds, stream, *problem, *grads);
+  } else if (problem->dtype == GPA_DTYPE_BF16) {
+    if (int rc = set_lds(route_bwd<bf16_t, false>, lds)) return rc;
+    hipLaunchKernelGGL((route_bwd<bf16_t, false>), grid, block, lds, stream, *problem, *grads);
   } else {
-    if (int rc = set_lds(route_bwd<float>, lds)) return rc;
-    hipLaunchKernelGGL(route_bwd<float>, grid, block, lds, stream, *problem, *grads);
+    if (int rc = set_lds(route_bwd<float, false>, lds)) return rc;
+    hipLaunchKernelGGL((route_bwd<float, false>), grid, block, lds, stream, *problem, *grads);
   }
   return check_launch("gpa_route_backward");
 }
