@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -113,6 +113,17 @@ class LevelGrads(ctypes.Structure):
                [(n, c_vp) for n in ("da_states", "db_states", "da_first", "db_first", "deta")]
 
 
+class CountProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "slots", "dtype")] + \
+               [("raw", Operand), ("write", Operand), ("count0", c_vp), ("count0_sb", c_i64)] + \
+               [(n, c_vp) for n in ("gain", "scale", "logits", "final_count", "prefix")]
+
+
+class CountGrads(ctypes.Structure):
+    _fields_ = [("dlogits", c_vp), ("dfinal", c_vp), ("draw", Operand), ("dwrite", Operand)] + \
+               [(n, c_vp) for n in ("dcount0", "partials", "tsum")]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -132,6 +143,9 @@ EXPORTS = {
                                 c_vp, c_vp], ctypes.c_int),
     "gpa_level_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
     "gpa_level_backward": ([ctypes.POINTER(LevelProblem), ctypes.POINTER(LevelGrads), c_vp], ctypes.c_int),
+    "gpa_count_logits_forward": ([ctypes.POINTER(CountProblem), c_vp], ctypes.c_int),
+    "gpa_count_logits_backward": ([ctypes.POINTER(CountProblem), ctypes.POINTER(CountGrads), c_vp],
+                                  ctypes.c_int),
 }
 
 _lib = None

@@ -31,6 +31,8 @@ from torch import Tensor
 from . import _lib
 from .ops import gdn_scan_deferred, gdn_scan_hip
 from .ops import read_supported as late_read_supported
+from .counts import count_logits
+from .counts import supported as fused_counts_supported
 from .level import level_mix
 from .level import supported as fused_level_supported
 from .route import route_reader
@@ -141,8 +143,8 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
 
 
 class _Level:
-    __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "logits", "a_final", "b_final",
-                 "a_starts", "b_starts", "b_read")
+    __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "final_count", "logits", "a_final",
+                 "b_final", "a_starts", "b_starts", "b_read")
 
 
 def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, position_ids: Tensor,
@@ -190,10 +192,16 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         else:
             write, key_next, value_next = _level_mix_torch(key, value, a_starts, b_starts, snap.inner, snap.outer,
                                                            eta, blocks, write)
-        counts = old.count[:, None] + _cumsum_tokens(write.float())
         lv.slot, lv.value, lv.g_out, lv.b_out = slot, value, g_out, b_out
-        lv.write, lv.counts = write, counts
-        lv.logits = _base_logits(model, raw, counts, j)
+        lv.write = write
+        if _FUSED_COUNTS[0] and fused_counts_supported(cfg, raw.dtype, write.shape[-1]):
+            gain, scale = _count_scalars(model, j, raw)
+            lv.logits, lv.final_count = count_logits(raw, write, old.count, gain, scale)
+            lv.counts = None  # not needed past the logits on this path
+        else:
+            lv.counts = old.count[:, None] + _cumsum_tokens(write.float())
+            lv.final_count = lv.counts[:, -1]
+            lv.logits = _base_logits(model, raw, lv.counts, j)
         lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, a_starts, b_starts
         levels.append(lv)
         key, value = key_next, value_next
@@ -228,7 +236,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         last = blocks.n - 1
         frozen = frozen0 if last == 0 else tuple(
             ResidualSnapshot(lv.a_starts[:, :, last], lv.b_starts[:, :, last]) for lv in levels)
-    new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.counts[:, -1], None) for lv in levels)
+    new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.final_count, None) for lv in levels)
     new_state = GPAState(new_levels, relations, state.position + tokens, chunk, new_offset, frozen)
     return out, new_state, (tuple(routes) if want_routes else None)
 
@@ -353,6 +361,20 @@ def _base_logits(model, raw: Tensor, counts: Tensor, j: int) -> Tensor:
     else:
         scale = cfg.read_scale
     return scale * raw.float() + gain * counts.log1p()
+
+
+def _count_scalars(model, j: int, like: Tensor):
+    """Per-head count gain and read scale of level j, as [H] tensors."""
+    cfg = model.config
+    gain = F.softplus(model.count_gain_raw[j])
+    if cfg.learn_read_scale:
+        scale = model.read_log_scale[j].clamp(math.log(.25), math.log(64.)).exp()
+    else:
+        scale = torch.full((cfg.heads,), float(cfg.read_scale), device=like.device)
+    return gain, scale
+
+
+_FUSED_COUNTS = [True]  # counts and base logits in HIP (counts.py)
 
 
 def _residual(model, key, value, rk, rv, j):

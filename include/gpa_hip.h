@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 7
+#define GPA_HIP_ABI_VERSION 8
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -305,6 +305,39 @@ typedef struct gpa_level_grads {
  * glue at attention.py:314-329, autograd through it for the backward). */
 int gpa_level_forward(const gpa_level_problem *problem, hipStream_t stream);
 int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *grads, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Slot counts and base logits of one level (reference attention.py:196-204,
+ * with the counts of :318-319, for the default flags):
+ *   counts[t] = count0 + sum_{t' <= t} write[t']              (float32)
+ *   logits[t] = scale[h] raw[t] + gain[h] log1p(counts[t])
+ * The counts are not materialised: the forward writes the logits, the final
+ * counts and the counts before every 64-token tile (`prefix`, kept for the
+ * backward).  Widths up to 256 slots.
+ */
+typedef struct gpa_count_problem {
+    int32_t batch, tokens, heads, slots, dtype;   /* dtype of raw and write */
+    gpa_operand raw, write;                       /* [B,T,H,M] */
+    const float *count0;                          /* [B,H,M] at count0[b*count0_sb + h*M + m] */
+    int64_t count0_sb;
+    const float *gain, *scale;                    /* [H]: softplus(count gain), read scale */
+    float *logits;                                /* out [B,T,H,M] float32, contiguous */
+    float *final_count;                           /* out [B,H,M] */
+    float *prefix;                                /* out/saved [B,H,ceil(T/64),M] */
+} gpa_count_problem;
+
+typedef struct gpa_count_grads {
+    const float *dlogits;                         /* [B,T,H,M] float32, contiguous */
+    const float *dfinal;                          /* [B,H,M] or NULL */
+    gpa_operand draw, dwrite;                     /* out [B,T,H,M] (problem dtype) */
+    float *dcount0;                               /* out [B,H,M], or NULL */
+    float *partials;                              /* out [B*H*ceil(T/64)][2]: d gain, d scale per tile */
+    float *tsum;                                  /* scratch [B,H,ceil(T/64),M] */
+} gpa_count_grads;
+
+int gpa_count_logits_forward(const gpa_count_problem *problem, hipStream_t stream);
+int gpa_count_logits_backward(const gpa_count_problem *problem, const gpa_count_grads *grads,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

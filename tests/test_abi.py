@@ -19,7 +19,8 @@ def test_header_declares_the_entry_points():
     names = _declared()
     for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
                      "gpa_gdn_forward", "gpa_gdn_backward", "gpa_gdn_read", "gpa_gdn_read_backward",
-                     "gpa_decode_step", "gpa_route_forward",
+                     "gpa_decode_step", "gpa_route_forward", "gpa_count_logits_forward",
+                     "gpa_count_logits_backward",
                      "gpa_route_backward", "gpa_route_weight_grads", "gpa_level_forward", "gpa_level_backward"):
         assert expected in names
 
@@ -69,6 +70,9 @@ def test_ctypes_structs_match_c_layout():
     # 9 int32 (+pad), 2 operands, 4 pointers, 2 int64, 1 pointer, 3 operands, 3 pointers
     assert ctypes.sizeof(_lib.LevelProblem) == 40 + 2 * 32 + 4 * 8 + 2 * 8 + 8 + 3 * 32 + 3 * 8
     assert ctypes.sizeof(_lib.LevelGrads) == 4 * 32 + 5 * 8
+    # 5 int32 (+pad), 2 operands, count0 + its stride, 5 pointers
+    assert ctypes.sizeof(_lib.CountProblem) == 24 + 2 * 32 + 2 * 8 + 5 * 8
+    assert ctypes.sizeof(_lib.CountGrads) == 2 * 8 + 2 * 32 + 3 * 8
 
 
 def test_backend_refuses_cpu_tensors():
