@@ -295,7 +295,7 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
           const int t = t0 + 4 * q + r;
           const int tok = tok_s[t];
           if (tok >= 0 && v < V)
-            reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)tok * gr.dv.st + v] = bet_s[t] * y[r];
+            reinterpret_cast<E*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)tok * gr.dv.st + v] = from_f32<E>(bet_s[t] * y[r]);
           part[r] = to_f32(vv_s[t * LDO + 16 * j + tq]) * y[r];
         }
 #pragma unroll
@@ -542,8 +542,8 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
   // ---- part 2: dX = (g - x^ (x^ . g)) / |x|.
   if (own) {
     const int k = 32 * kt + li;
-    float* dqo = gr.dq.ptr && p.q.ptr ? reinterpret_cast<float*>(gr.dq.ptr) + op_base(gr.dq, b, h) : nullptr;
-    float* dko = reinterpret_cast<float*>(gr.dk.ptr) + op_base(gr.dk, b, h);
+    E* dqo = gr.dq.ptr && p.q.ptr ? reinterpret_cast<E*>(gr.dq.ptr) + op_base(gr.dq, b, h) : nullptr;
+    E* dko = reinterpret_cast<E*>(gr.dk.ptr) + op_base(gr.dk, b, h);
     if (k < K) {
 #pragma unroll
       for (int m = 0; m < NTW; ++m)
@@ -553,12 +553,12 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
           const int tok = tok_s[t];
           if (tok < 0) continue;
           dko[(int64_t)tok * gr.dk.st + k] =
-              (knrm_s[t] > 1e-6f ? dka[m][r] - xe[m][r] * kdot_s[t] : dka[m][r]) * krd_s[t];
+              from_f32<E>((knrm_s[t] > 1e-6f ? dka[m][r] - xe[m][r] * kdot_s[t] : dka[m][r]) * krd_s[t]);
           if (has_q) {
             dqo[(int64_t)tok * gr.dq.st + k] =
-                (qnrm_s[t] > 1e-6f ? dq[m][r] - qe[m][r] * qdot_s[t] : dq[m][r]) * qrd_s[t];
+                from_f32<E>((qnrm_s[t] > 1e-6f ? dq[m][r] - qe[m][r] * qdot_s[t] : dq[m][r]) * qrd_s[t]);
           } else if (dqo) {
-            dqo[(int64_t)tok * gr.dq.st + k] = 0.f;
+            dqo[(int64_t)tok * gr.dq.st + k] = from_f32<E>(0.f);
           }
         }
     }

@@ -770,8 +770,8 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
         const int v = v0 + tx + 16 * j;
         rdot += b_s[sr * LDS_ + tx + 16 * j] * acc[i][j];
         if (t >= 0 && v < V)
-          reinterpret_cast<float*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)t * gr.dv.st + v] =
-              bet_s[sr] * acc[i][j];
+          reinterpret_cast<E*>(gr.dv.ptr)[op_base(gr.dv, b, h) + (int64_t)t * gr.dv.st + v] =
+              from_f32<E>(bet_s[sr] * acc[i][j]);
       }
       rdot = sum16(rdot);
       if (tx == 0) atomicAdd(&dbet_s[sr], rdot);
@@ -800,7 +800,7 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
         if (p.q.ptr && gr.dq.ptr && t >= 0)
           for (int j = 0; j < NJ; ++j) {
             const int k = tx + 16 * j;
-            if (k < K) reinterpret_cast<float*>(gr.dq.ptr)[op_base(gr.dq, b, h) + (int64_t)t * gr.dq.st + k] = 0.f;
+            if (k < K) reinterpret_cast<E*>(gr.dq.ptr)[op_base(gr.dq, b, h) + (int64_t)t * gr.dq.st + k] = from_f32<E>(0.f);
           }
         continue;
       }
@@ -820,13 +820,13 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
       for (int j = 0; j < NJ; ++j) dot += (xs[j] / den) * (which == 0 ? dq[i][j] : dk[i][j]);
       dot = sum16(dot);
       if (t < 0) continue;
-      float* out = reinterpret_cast<float*>(dst.ptr) + op_base(dst, b, h) + (int64_t)t * dst.st;
+      E* out = reinterpret_cast<E*>(dst.ptr) + op_base(dst, b, h) + (int64_t)t * dst.st;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int k = tx + 16 * j;
         if (k >= K) continue;
         const float g = which == 0 ? dq[i][j] : dk[i][j];
-        out[k] = nrm > 1e-6f ? (g - (xs[j] / den) * dot) / den : g / 1e-6f;
+        out[k] = from_f32<E>(nrm > 1e-6f ? (g - (xs[j] / den) * dot) / den : g / 1e-6f);
       }
     }
   }

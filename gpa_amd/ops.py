@@ -128,9 +128,10 @@ class _GDNScan(torch.autograd.Function):
         ddelta = torch.empty(rows * vd, **f32)
         dhend = torch.empty(bsz * heads * nch * kd * vd, **f32)
         dw = torch.empty(rows * kd, **f32)
-        dq = torch.zeros(bsz, tokens, heads, kd, **f32) if has_q else None
-        dk = torch.empty(bsz, tokens, heads, kd, **f32)
-        dv = torch.empty(bsz, tokens, heads, vd, **f32)
+        act = dict(device=dev, dtype=k.dtype)  # the kernels round dq, dk, dv to the activation type
+        dq = torch.empty(bsz, tokens, heads, kd, **act) if has_q else None
+        dk = torch.empty(bsz, tokens, heads, kd, **act)
+        dv = torch.empty(bsz, tokens, heads, vd, **act)
         dg = torch.empty(bsz, tokens, heads, **f32)
         db = torch.empty(bsz, tokens, heads, **f32)
         ds0 = torch.empty(bsz, heads, kd, vd, **f32)
@@ -146,8 +147,8 @@ class _GDNScan(torch.autograd.Function):
         _lib.check(lib.gpa_gdn_backward(prob, saved, grads, timing, _lib.stream_handle(dev)), "gpa_gdn_backward")
         if late:  # dq of the late read was returned by the read itself
             box.release()
-        dq_out = dq.to(q.dtype) if (has_q and not late and ctx.needs_input_grad[0]) else None
-        return (dq_out, dk.to(k.dtype), dv.to(v.dtype), dg, db,
+        dq_out = dq if (has_q and not late and ctx.needs_input_grad[0]) else None
+        return (dq_out, dk, dv, dg, db,
                 ds0 if has_s0 else None, None, None, None)
 
 

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 8
+#define GPA_HIP_ABI_VERSION 9
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -96,9 +96,10 @@ typedef struct gpa_gdn_saved {
  * NULL (no read gradient); dstates f32 [S,N,V,K] (value-major, like states)
  * injects gradients of the chunk-start states (NULL = none); dfinal f32
  * [S,K,V] (NULL = none).  Caller-owned f32 scratch: dd0, o, ddelta
- * [S,N,V,64], dhend [S,N,V,K], dw [S,N,64,K].  Gradient outputs are f32
- * operands: dq (skipped when q was NULL), dk [.. K], dv [.. V], dg, dbeta per
- * token; ds0 [S,K,V] contiguous. */
+ * [S,N,V,64], dhend [S,N,V,K], dw [S,N,64,K].  Gradient outputs: dq
+ * (skipped when q was NULL), dk [.. K], dv [.. V] in the problem dtype
+ * (rounded once from fp32); dg, dbeta f32 per token; ds0 [S,K,V] f32
+ * contiguous. */
 typedef struct gpa_gdn_grads {
     gpa_operand dout;
     const float *dstates, *dfinal;
