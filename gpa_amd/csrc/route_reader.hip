@@ -83,12 +83,26 @@ __device__ __forceinline__ float gelu_grad(float x) {
   return .5f * (1.f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-.5f * x * x);
 }
 
+// Offsets of a workgroup's rows r = b*T + t: the (b, t) split of each of its
+// RR rows is computed once (rows past the end repeat the last one).
 struct Rows {
-  int tokens, heads;
+  int row0;
+  const int *rb, *rt;
   __device__ __forceinline__ int64_t at(const gpa_operand& o, int r, int h) const {
-    return (int64_t)(r / tokens) * o.sb + (int64_t)(r % tokens) * o.st + (int64_t)h * o.sh;
+    const int i = r - row0;
+    return (int64_t)rb[i] * o.sb + (int64_t)rt[i] * o.st + (int64_t)h * o.sh;
   }
 };
+
+__device__ __forceinline__ Rows make_rows(int* rb, int* rt, int row0, int R, int T) {
+  if (threadIdx.x < RR) {
+    const int r = row0 + threadIdx.x < R ? row0 + threadIdx.x : R - 1;
+    rb[threadIdx.x] = r / T;
+    rt[threadIdx.x] = r % T;
+  }
+  __syncthreads();
+  return Rows{row0, rb, rt};
+}
 
 // Relation read and softmax of one row (8 threads, columns part + 8 i):
 // returns base' = base + gain tanh z in v[], and fills z[] / inc[] when asked.
@@ -195,7 +209,8 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   const int lda = kM + 4, ldh = (k2M > kD ? k2M : kD) + 4;
   float* A = lds;             // r0, then r1        [RR][lda]
   float* Hs = lds + RR * lda; // gelu(h1), then q   [RR][ldh]
-  const Rows rows{p.tokens, p.heads};
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, row0, R, p.tokens);
   E* sr0 = reinterpret_cast<E*>(p.r0) + (int64_t)h * R * M;
   E* sh1 = reinterpret_cast<E*>(p.h1) + (int64_t)h * R * 2 * M;
   E* shd = reinterpret_cast<E*>(p.hd) + (int64_t)h * R * M;
@@ -404,7 +419,8 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   float* G = lds;                // dqo, then round(qs dqo)   [RR][lda]
   float* A2 = lds + RR * lda;    // d hd, then d r0           [RR][lda]
   float* H2 = A2 + RR * lda;     // d h1                      [RR][ldh]
-  const Rows rows{p.tokens, p.heads};
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, row0, R, p.tokens);
   const E* sh1 = reinterpret_cast<const E*>(p.h1) + (int64_t)h * R * 2 * M;
   const E* shd = reinterpret_cast<const E*>(p.hd) + (int64_t)h * R * M;
   E* gdh1 = reinterpret_cast<E*>(g.dh1) + (int64_t)h * R * 2 * M;
@@ -590,7 +606,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
     for (int i = 0; i < VPASS; ++i) {
       const int row = rsub + 8 * i, r = row0 + row;
       const bool valid = r < R;
-      float v[8], z[8] = {}, msgf[GPA_ROUTE_MAX_INCOMING][8], inv = 0.f;
+      float v[8], z[8] = {}, thz[8] = {}, msgf[GPA_ROUTE_MAX_INCOMING][8], inv = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
       if (NI > 0) {
@@ -617,7 +633,8 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           z[j] = z[j] / sig;
-          v[j] += gain * tanhf(z[j]);
+          thz[j] = tanhf(z[j]);
+          v[j] += gain * thz[j];
         }
       }
       float mx = -INFINITY;
@@ -655,7 +672,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
         float dz[8], szz = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float th = tanhf(z[j]);
+          const float th = thz[j];
           if (valid && on) part_gain += v[j] * th;
           dz[j] = on ? gain * v[j] * (1.f - th * th) : 0.f;
           szz += dz[j] * z[j];
