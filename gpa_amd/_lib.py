@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -92,7 +92,7 @@ class RouteProblem(ctypes.Structure):
 class RouteGrads(ctypes.Structure):
     _fields_ = [(n, Operand) for n in ("dqo", "droute", "dbase")] + \
                [("dmsg", Operand * ROUTE_MAX_INCOMING), ("dq", Operand)] + \
-               [(n, c_vp) for n in ("dh1", "dhd", "dqs", "partials")]
+               [(n, c_vp) for n in ("dh1", "dhd", "dqs", "hg", "partials")]
 
 
 LEVEL_MAX_WIDTH = 256

@@ -424,6 +424,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   const E* sh1 = reinterpret_cast<const E*>(p.h1) + (int64_t)h * R * 2 * M;
   const E* shd = reinterpret_cast<const E*>(p.hd) + (int64_t)h * R * M;
   E* gdh1 = reinterpret_cast<E*>(g.dh1) + (int64_t)h * R * 2 * M;
+  E* ghg = reinterpret_cast<E*>(g.hg) + (int64_t)h * R * 2 * M;
   E* gdhd = reinterpret_cast<E*>(g.dhd) + (int64_t)h * R * M;
   E* gdqs = reinterpret_cast<E*>(g.dqs) + (int64_t)h * R * M;
   float part_mg = 0.f, part_gain = 0.f, part_w[GPA_ROUTE_MAX_INCOMING] = {0.f, 0.f, 0.f};
@@ -541,6 +542,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
             const float x = to_f32(sh1[(int64_t)r * 2 * M + col]);
             d = round_as<E>(round_as<E>(acc[i]) * gelu_grad(x));
             gdh1[(int64_t)r * 2 * M + col] = from_f32<E>(d);
+            ghg[(int64_t)r * 2 * M + col] = from_f32<E>(gelu(x));  // shares gelu_grad's erf
           }
           H2[row * ldh + col] = d;
         } else if (col < k2M) {
@@ -791,7 +793,6 @@ struct TnOperand {
   const void* ptr;
   int64_t rs, hs;  // row and head strides (elements)
   int width;
-  int gelu;        // A mapped through round(gelu(.)) on load (d D from h1)
 };
 
 constexpr int WT = 64;     // output tile
@@ -822,10 +823,6 @@ __device__ __forceinline__ void load8(const TnOperand& o, int h, int r, int c, i
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       if (c + s < o.width) x[s] = to_f32(p[s]);
-  }
-  if (o.gelu) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) x[s] = round_as<E>(gelu(x[s]));
   }
 }
 
@@ -886,6 +883,156 @@ template <typename E>
 __global__ void round_in_place(float* c, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     c[i] = round_as<E>(c[i]);
+}
+
+// bf16 weight gradients, all four products in one launch.  A workgroup owns
+// a 128x128 tile of one product's C for one head and a span of rows; the
+// span is walked in slabs of 64 rows.  Waves 0-1 stage A, waves 2-3 stage B:
+// each lane reads an 8x8 block (8 rows of 16 bytes), transposes it in
+// registers and writes its 8 columns to LDS as 16-byte rows of 8 tokens, so
+// that LDS holds [column][token] and each MFMA operand is one 16-byte read.
+// With a 72-element pitch and lanes ordered row block first, the writes and
+// the reads both touch 16 distinct 4-bank groups per 16 lanes.  Partial tiles
+// of the spans are added into C (cleared first) with float atomics.
+constexpr int GT = 128;         // output tile
+constexpr int GK = 64;          // rows per slab
+constexpr int GP = GK + 8;      // LDS pitch (bf16)
+constexpr int GNT = 256;
+constexpr int G_WGS = 512;      // workgroups the row spans aim for
+constexpr size_t G_LDS = 2 * GT * GP * sizeof(uint16_t);  // A and B slabs
+
+struct WJob {
+  TnOperand a, b;
+  float* c;
+  int tj, tiles;  // column tiles of C, tiles of C
+};
+struct WJobs {
+  WJob j0, j1, j2, j3;
+  int span, R, tiles, heads, n;  // tiles of all four products, workgroups
+};
+
+// Workgroups go to the 8 XCDs round robin (id % 8).  Renumber them so that
+// each XCD runs a contiguous range of logical ids: the tiles of one product,
+// head and span, which read the same rows of A or B, then share an L2.
+__device__ __forceinline__ int xcd_logical(int id, int n) {
+  const int q = n / 8, r = n % 8, x = id % 8, local = id / 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+
+__global__ __launch_bounds__(GNT, 4) void route_wgrad16(WJobs js) {
+  HIP_DYNAMIC_SHARED(uint16_t, glds)
+  const int logical = xcd_logical(blockIdx.x, js.n);
+  int t = logical % js.tiles;
+  const int h = (logical / js.tiles) % js.heads, span_idx = logical / (js.tiles * js.heads);
+  const bool in0 = t < js.j0.tiles;
+  t -= in0 ? 0 : js.j0.tiles;
+  const bool in1 = !in0 && t < js.j1.tiles;
+  t -= (in0 || in1) ? 0 : js.j1.tiles;
+  const bool in2 = !in0 && !in1 && t < js.j2.tiles;
+  t -= (in0 || in1 || in2) ? 0 : js.j2.tiles;
+  const WJob& J = in0 ? js.j0 : in1 ? js.j1 : in2 ? js.j2 : js.j3;
+  const int i0 = GT * (t / J.tj), j0 = GT * (t % J.tj);
+  const int rbeg = span_idx * js.span, rend = rbeg + js.span < js.R ? rbeg + js.span : js.R;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // staging role: 8x8 block (row block rb, column block cb) of A or B; the
+  // operand is chosen per wave and held in scalar registers
+  const bool isb = wave >= 2;
+  const TnOperand O = isb ? J.b : J.a;
+  const int rb = 8 * (tid & 7), cb = 8 * ((tid & 127) >> 3);
+  const int col = (isb ? j0 : i0) + cb;
+  const bool col_ok = col < O.width;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(O.ptr) + (int64_t)h * O.hs + (col_ok ? col : 0);
+  uint16_t* const stage = glds + (isb ? GT * GP : 0) + cb * GP + rb;
+
+  // Loads are unconditional (clamped to a valid row and column) so that all
+  // eight are in flight together; rows out of range are zeroed at the store.
+  uint4 x[8];
+  unsigned live = 0;
+  auto load = [&](int k0) {
+    live = 0;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int r = k0 + rb + s;
+      x[s] = *reinterpret_cast<const uint4*>(src + (int64_t)(r < rend ? r : rend - 1) * O.rs);
+      live |= (col_ok && r < rend) ? 1u << s : 0u;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (!((live >> s) & 1)) x[s] = make_uint4(0, 0, 0, 0);
+    uint16_t* const dst = stage;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const unsigned r0 = (&x[0].x)[d], r1 = (&x[1].x)[d], r2 = (&x[2].x)[d], r3 = (&x[3].x)[d];
+      const unsigned r4 = (&x[4].x)[d], r5 = (&x[5].x)[d], r6 = (&x[6].x)[d], r7 = (&x[7].x)[d];
+      const uint4 even = make_uint4((r0 & 0xffffu) | (r1 << 16), (r2 & 0xffffu) | (r3 << 16),
+                                    (r4 & 0xffffu) | (r5 << 16), (r6 & 0xffffu) | (r7 << 16));
+      const uint4 odd = make_uint4((r0 >> 16) | (r1 & 0xffff0000u), (r2 >> 16) | (r3 & 0xffff0000u),
+                                   (r4 >> 16) | (r5 & 0xffff0000u), (r6 >> 16) | (r7 & 0xffff0000u));
+      *reinterpret_cast<uint4*>(dst + (2 * d) * GP) = even;
+      *reinterpret_cast<uint4*>(dst + (2 * d + 1) * GP) = odd;
+    }
+  };
+
+  // compute role: a 64x64 quadrant of C per wave, 2x2 MFMA tiles
+  const int wi = 64 * (wave & 1), wj = 64 * (wave >> 1);
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  f32x16 acc[2][2] = {};
+
+  // One LDS slab (four workgroups fit a CU); the next slab's loads are in
+  // flight while this one is multiplied.
+  load(rbeg);
+  for (int k0 = rbeg; k0 < rend; k0 += GK) {
+    store();
+    __syncthreads();
+    if (k0 + GK < rend) load(k0 + GK);
+    const uint16_t* As = glds;
+    const uint16_t* Bs = As + GT * GP;
+#pragma unroll
+    for (int kk = 0; kk < GK; kk += 16) {
+      bf16x8 af[2], bfr[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        af[u] = *reinterpret_cast<const bf16x8*>(As + (wi + 32 * u + fr) * GP + kk + fk);
+        bfr[u] = *reinterpret_cast<const bf16x8*>(Bs + (wj + 32 * u + fr) * GP + kk + fk);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+          acc[u][v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[u], bfr[v], acc[u][v], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  float* c = J.c + (int64_t)h * J.a.width * J.b.width;
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wi + 32 * u + acc_row(r, lane >> 5), j = j0 + wj + 32 * v + fr;
+        if (i < J.a.width && j < J.b.width) atomicAdd(&c[(int64_t)i * J.b.width + j], acc[u][v][r]);
+      }
+}
+
+struct FourBufs {
+  float* c[4];
+  int64_t n[4];
+};
+template <bool ROUND>
+__global__ void fill_or_round4(FourBufs b) {
+  const int64_t step = (int64_t)gridDim.x * blockDim.x, first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    for (int64_t i = first; i < b.n[q]; i += step) b.c[q][i] = ROUND ? round_as<bf16_t>(b.c[q][i]) : 0.f;
+}
+
+// 16-byte loads need 8-element aligned columns, strides and base.
+bool wgrad16_ok(const TnOperand& o) {
+  return o.width % 8 == 0 && o.rs % 8 == 0 && o.hs % 8 == 0 && (reinterpret_cast<uintptr_t>(o.ptr) & 15) == 0;
 }
 
 int check_route(const gpa_route_problem* p) {
@@ -986,7 +1133,7 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
   using namespace gpa;
   if (int rc = check_route(problem)) return rc;
   if (!grads || !grads->dqo.ptr || !grads->dbase.ptr || !grads->dq.ptr || !grads->dh1 || !grads->dhd ||
-      !grads->dqs || !grads->partials || !problem->up || !problem->down || !problem->rs || !problem->qs)
+      !grads->dqs || !grads->hg || !grads->partials || !problem->up || !problem->down || !problem->rs || !problem->qs)
     return fail(GPA_HIP_EINVAL, "route: null gradient buffer or backward weight");
   for (int e = 0; e < problem->incoming; ++e)
     if (!grads->dmsg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message gradient");
@@ -1010,7 +1157,7 @@ extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gp
                                       float* d_down, float* d_rs, float* d_qs, hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_route(problem)) return rc;
-  if (!grads || !grads->dqo.ptr || !grads->dh1 || !grads->dhd || !grads->dqs || !problem->route.ptr || !d_up ||
+  if (!grads || !grads->dqo.ptr || !grads->dh1 || !grads->dhd || !grads->dqs || !grads->hg || !problem->route.ptr || !d_up ||
       !d_down || !d_rs || !d_qs)
     return fail(GPA_HIP_EINVAL, "route: null weight-gradient buffer");
   const int M = problem->slots, Dk = problem->key_dim, R = problem->batch * problem->tokens, H = problem->heads;
@@ -1021,17 +1168,46 @@ extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gp
       !row_stride(problem->q, problem->batch, problem->tokens, rs_q))
     return fail(GPA_HIP_EINVAL, "route: route, dqo and q rows must be uniformly strided");
   const int64_t R64 = R;
-  const TnOperand r0{problem->r0, M, R64 * M, M, 0};
-  const TnOperand hid{problem->h1, 2 * M, R64 * 2 * M, 2 * M, 1};
-  const TnOperand dh1{grads->dh1, 2 * M, R64 * 2 * M, 2 * M, 0};
-  const TnOperand dhd{grads->dhd, M, R64 * M, M, 0};
-  const TnOperand dqs{grads->dqs, M, R64 * M, M, 0};
-  const TnOperand r1{problem->route.ptr, rs_route, problem->route.sh, M, 0};
-  const TnOperand dqo{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M, 0};
-  const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk, 0};
+  const TnOperand r0{problem->r0, M, R64 * M, M};
+  const TnOperand hid{grads->hg, 2 * M, R64 * 2 * M, 2 * M};
+  const TnOperand dh1{grads->dh1, 2 * M, R64 * 2 * M, 2 * M};
+  const TnOperand dhd{grads->dhd, M, R64 * M, M};
+  const TnOperand dqs{grads->dqs, M, R64 * M, M};
+  const TnOperand r1{problem->route.ptr, rs_route, problem->route.sh, M};
+  const TnOperand dqo{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M};
+  const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk};
   struct Job { TnOperand a, b; float* c; } jobs[4] = {{r0, dh1, d_up}, {hid, dhd, d_down}, {r1, dqo, d_rs},
                                                         {q, dqs, d_qs}};
   const bool bf = problem->dtype == GPA_DTYPE_BF16;
+  bool fast = bf;
+  for (const Job& j : jobs) fast = fast && wgrad16_ok(j.a) && wgrad16_ok(j.b);
+  if (fast) {
+    WJob w[4];
+    FourBufs fb;
+    int tiles = 0;
+    for (int q = 0; q < 4; ++q) {
+      const int ti = (jobs[q].a.width + GT - 1) / GT, tj = (jobs[q].b.width + GT - 1) / GT;
+      w[q] = {jobs[q].a, jobs[q].b, jobs[q].c, tj, ti * tj};
+      fb.c[q] = jobs[q].c;
+      fb.n[q] = (int64_t)H * jobs[q].a.width * jobs[q].b.width;
+      tiles += ti * tj;
+    }
+    // Row spans: enough workgroups for the whole chip, each span whole slabs.
+    const int slabs = (R + GK - 1) / GK, per_span_wgs = tiles * H;
+    int spans = (G_WGS + per_span_wgs - 1) / per_span_wgs;
+    spans = spans < 1 ? 1 : spans > slabs ? slabs : spans;
+    const int span = GK * ((slabs + spans - 1) / spans);
+    spans = (R + span - 1) / span;
+    const int n = tiles * H * spans;
+    const WJobs js{w[0], w[1], w[2], w[3], span, R, tiles, H, n};
+    if (int rc = set_lds(route_wgrad16, G_LDS)) return rc;
+    const int64_t total = fb.n[0] + fb.n[1] + fb.n[2] + fb.n[3];
+    const dim3 fgrid((unsigned)((total + 1023) / 1024 < 2048 ? (total + 1023) / 1024 : 2048));
+    hipLaunchKernelGGL(fill_or_round4<false>, fgrid, dim3(256), 0, stream, fb);
+    hipLaunchKernelGGL(route_wgrad16, dim3(n), dim3(GNT), G_LDS, stream, js);
+    hipLaunchKernelGGL(fill_or_round4<true>, fgrid, dim3(256), 0, stream, fb);
+    return check_launch("gpa_route_weight_grads");
+  }
   for (const Job& j : jobs) {
     const int64_t n = (int64_t)H * j.a.width * j.b.width;
     const dim3 fill_grid((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64));

@@ -8,8 +8,8 @@ together with each launch's algorithmic FLOP count:
 
   gdn_prep       (4CK + 2CV + C^2/3)      per token: K K^T, W, U, triangular solve
   gdn_state_fwd  4KV                      W S, K^T D
-  gdn_out_fwd    2KV + 2CK + 2CV          Q S, Q K^T, P D
-  gdn_dd0        2CK + 2CV                Q K^T, P^T dO
+  gdn_out_*      2KV + 2CK + 2CV          Q S, Q K^T, P D
+  gdn_dd0*       2CK + 2CV                Q K^T, P^T dO
   gdn_state_bwd  4KV (+2KV with a read)   K dS, W^T dD (+ Q^T dO)
   gdn_chunk_bwd  4KV + 4CV + 4CK + 2C^2   D dS^T, Y S^T, dD D^T, T^T dD, K K^T, T^T X,
                  (+2KV + 2CV + 6CK)       dKK K (+ dO S^T, dO D^T, Q K^T, dQK K, dQK^T Q)
@@ -119,7 +119,8 @@ def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
                 (4 * c * k + 2 * c * v + c * c / 3) * tokens),
                (state, 4 * k * v * tokens)]
     if read:
-        kernels.append((f"gdn_out_fwd<{e},{km}>", (2 * k * v + 2 * c * k + 2 * c * v) * tokens))
+        out = f"gdn_out_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_out_fwd<{e},{km}>"
+        kernels.append((out, (2 * k * v + 2 * c * k + 2 * c * v) * tokens))
     return _active.timing(kernels)
 
 
@@ -129,7 +130,8 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     e, km = _tag(dtype), _kmax(k)
     kernels = []
     if read:
-        kernels.append((f"gdn_dd0<{e},{km}>", (2 * c * k + 2 * c * v) * tokens))
+        dd0 = f"gdn_dd0_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_dd0<{e},{km}>"
+        kernels.append((dd0, (2 * c * k + 2 * c * v) * tokens))
     state = f"gdn_state_bwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_bwd<{e},{km}>"
     kernels.append((state, (6 if read else 4) * k * v * tokens))
     chunk = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c

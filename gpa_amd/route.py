@@ -120,6 +120,7 @@ class _RouteReader(torch.autograd.Function):
         dh1 = torch.empty(heads, rows, 2 * m, device=dev, dtype=dtype)
         dhd = torch.empty(heads, rows, m, device=dev, dtype=dtype)
         dqs = torch.empty(heads, rows, m, device=dev, dtype=dtype)
+        hg = torch.empty(heads, rows, 2 * m, device=dev, dtype=dtype)
         blocks = (rows + _lib.ROUTE_ROWS - 1) // _lib.ROUTE_ROWS
         partials = torch.empty(blocks, heads, 2 + len(msgs), device=dev, dtype=torch.float32)
         gr = _lib.RouteGrads()
@@ -127,6 +128,7 @@ class _RouteReader(torch.autograd.Function):
         for e, x in enumerate(dmsgs):
             gr.dmsg[e] = _operand(x)
         gr.dh1, gr.dhd, gr.dqs, gr.partials = dh1.data_ptr(), dhd.data_ptr(), dqs.data_ptr(), partials.data_ptr()
+        gr.hg = hg.data_ptr()
         stream = _lib.stream_handle(dev)
         _lib.check(lib.gpa_route_backward(prob, gr, stream), "gpa_route_backward")
         d_up = torch.empty(heads, m, 2 * m, device=dev, dtype=torch.float32)

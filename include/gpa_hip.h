@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 9
+#define GPA_HIP_ABI_VERSION 10
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -252,6 +252,7 @@ typedef struct gpa_route_grads {
     gpa_operand dmsg[GPA_ROUTE_MAX_INCOMING];     /* out */
     gpa_operand dq;                               /* out [B,T,H,Dk] */
     void *dh1, *dhd, *dqs;                        /* out rows [H][R][2M | M | M]: grads of h1, hd and of q W_qs */
+    void *hg;                                     /* out rows [H][R][2M]: round(gelu(h1)), read by the weight gradients */
     float *partials;                              /* out [ceil(R/32)][H][2 + incoming]:
                                                      d mlp_gain, d gain, d w_e summed over the block's rows */
 } gpa_route_grads;
@@ -265,7 +266,8 @@ int gpa_route_forward(const gpa_route_problem *problem, hipStream_t stream);
 int gpa_route_backward(const gpa_route_problem *problem, const gpa_route_grads *grads, hipStream_t stream);
 /* Weight gradients summed over rows, float32 [H][K][N] in the parameters'
  * own layouts: d U [M][2M], d D [2M][M], d W_rs [M][M], d W_qs [Dk][M]
- * (each rounded to the activation type, as the reference's typed products are). */
+ * (each rounded to the activation type, as the reference's typed products are).
+ * Reads the rows dh1, dhd, dqs and hg that gpa_route_backward wrote. */
 int gpa_route_weight_grads(const gpa_route_problem *problem, const gpa_route_grads *grads, float *d_up,
                            float *d_down, float *d_rs, float *d_qs, hipStream_t stream);
 

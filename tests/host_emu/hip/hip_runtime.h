@@ -117,6 +117,8 @@ inline emu_f32x4 emu_mfma_16x16x4_f32(float a, float b, emu_f32x4 c) {
   return c;
 }
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, x, y, z) emu_mfma_32x32x16_bf16(a, b, c)
+// Only used on values that are uniform over the wave, where it is the identity.
+#define __builtin_amdgcn_readfirstlane(x) (x)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu_mfma_32x32x2_f32(a, b, c)
 #define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) emu_mfma_16x16x4_f32(a, b, c)
 
