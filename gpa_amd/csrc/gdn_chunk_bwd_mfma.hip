@@ -35,6 +35,9 @@ template <typename E, int KM>
 struct ChunkBwdLayout {
   static constexpr bool XR = KM > 128;
   static constexpr int VS = 16;                   // value slice
+  // bf16 activations: the value slice runs as one 32x32x16 step (BFV), with
+  // dO rows read as 8-byte pairs (LDO a multiple of 4)
+  static constexpr bool BFV = std::is_same<E, bf16_t>::value && VS == 16;
   static constexpr int LDO = VS + 4, LT = R + 4, LS = KM + 4;
   static constexpr int LX = XR ? KM + 8 : KM + 4;  // row stride of x/|x| (bf16 elements when XR)
   static constexpr int XF = XR ? R * LX / 2 : R * LX;
@@ -60,6 +63,7 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
   constexpr bool XR = L::XR;
   static_assert(!XR || std::is_same<E, bf16_t>::value, "rounded x/|x| needs bf16 activations");
   constexpr int VS = L::VS, LDO = L::LDO, LT = L::LT, LS = L::LS, LX = L::LX;
+  constexpr bool BFV = L::BFV;
   constexpr int NW = CB_WAVES, NTH = CB_NT, KT = KM / 32;
   constexpr int NTW = KT >= 4 ? KT / 4 : 1;  // R x K output tiles per owning wave
   // Per-slice staging counts (float4 of S/dS, of D/dD; elements of dO/V) and
@@ -309,6 +313,27 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
         }
       }
       __syncthreads();
+      if constexpr (BFV) {
+        // One 32x32x16 bf16 step per slice; fp32 operands split (mfma_tiles.h).
+        const int c0 = 8 * hh;
+        if (own) {
+          const SplitBf8 bs = col_split_bf8(s_s, LS, 32 * kt + li, c0);
+          const SplitBf8 bds = col_split_bf8(ds_s, LS, 32 * kt + li, c0);
+#pragma unroll
+          for (int m = 0; m < NTW; ++m) {
+            const int row = 32 * tile_rt(m) + li;
+            if (has_q) mma_exact_split(dq[m], row_bf8(do_s, LDO, row, c0), bs);
+            mma_split(dka[m], col_split_bf8(d_s, LT, row, c0), bds);
+            mma_split(dkw[m], col_split_bf8(y_s, LT, row, c0), bs);
+          }
+        }
+        const SplitBf8 bu = col_split_bf8(d_s, LT, 32 * ru + li, c0);
+        if (grp_p) {
+          if (has_q) mma_exact_split(dp, row_bf8(do_s, LDO, 32 * rr + li, c0), bu);
+        } else {
+          mma_split(dp, col_split_bf8(dd_s, LT, 32 * rr + li, c0), bu);
+        }
+      } else {
 #pragma unroll
       for (int g = 0; g < VS / 8; ++g) {
         const int c0 = 8 * g + 4 * hh;
@@ -328,6 +353,7 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
         } else {
           mma8(dp, ld_x(dd_s, LT, 32 * rr + li, c0), bu);
         }
+      }
       }
       __syncthreads();
       if (sl + 1 < nsl) {

@@ -104,6 +104,50 @@ __device__ __forceinline__ bf16x8 pack8(const float* x) {
   return r;
 }
 
+// Split bf16 operands of v_mfma_f32_32x32x16_bf16 (lane l: row or column
+// l%32, contraction 8 (l/32) .. +7).  An fp32 value x is carried as hi + lo,
+// hi = bf16(x), lo = bf16(x - hi); a product keeps hi*hi + hi*lo + lo*hi,
+// about 16 significant bits.  Values exact in bf16 go in unsplit.
+struct SplitBf8 {
+  bf16x8 hi, lo;
+};
+__device__ __forceinline__ SplitBf8 split_bf8(const float (&x)[8]) {
+  SplitBf8 s;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s.hi[e] = (__bf16)x[e];
+    s.lo[e] = (__bf16)(x[e] - (float)s.hi[e]);
+  }
+  return s;
+}
+// Elements (c0 + e, x), e = 0..7, of an fp32 matrix stored with x contiguous.
+__device__ __forceinline__ SplitBf8 col_split_bf8(const float* m, int ld, int x, int c0) {
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = m[(c0 + e) * ld + x];
+  return split_bf8(v);
+}
+// Elements (x, c0 + e) of a bf16 matrix stored with c contiguous (8-byte aligned rows).
+__device__ __forceinline__ bf16x8 row_bf8(const bf16_t* m, int ld, int x, int c0) {
+  const uint2 a = *reinterpret_cast<const uint2*>(m + x * ld + c0), b = *reinterpret_cast<const uint2*>(m + x * ld + c0 + 4);
+  const uint4 w = make_uint4(a.x, a.y, b.x, b.y);
+  bf16x8 r;
+  __builtin_memcpy(&r, &w, 16);
+  return r;
+}
+__device__ __forceinline__ void mma_bf16(f32x16& c, bf16x8 a, bf16x8 b) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mma_split(f32x16& c, const SplitBf8& a, const SplitBf8& b) {
+  mma_bf16(c, a.hi, b.hi);
+  mma_bf16(c, a.hi, b.lo);
+  mma_bf16(c, a.lo, b.hi);
+}
+__device__ __forceinline__ void mma_exact_split(f32x16& c, bf16x8 a, const SplitBf8& b) {
+  mma_bf16(c, a, b.hi);
+  mma_bf16(c, a, b.lo);
+}
+
 template <typename E>
 __device__ __forceinline__ f32x4 round4(f32x4 x) {
   return f32x4{round_as<E>(x.x), round_as<E>(x.y), round_as<E>(x.z), round_as<E>(x.w)};
