@@ -455,7 +455,13 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
     __syncthreads();
     // ---- dA = -(T^T X), strictly lower (waves 4-7): b, gate and dKK.
     f32x16 da = {};
-    if (!grp_p) {
+    if (!grp_p && BFV) {
+#pragma unroll
+      for (int g = 0; g < R / 16; ++g) {
+        const int c0 = 16 * g + 8 * hh;
+        mma_split(da, col_split_bf8(tm, LT, 32 * rr + li, c0), col_split_bf8(xm, LT, 32 * ru + li, c0));
+      }
+    } else if (!grp_p) {
 #pragma unroll
       for (int g = 0; g < R / 8; ++g) {
         const int c0 = 8 * g + 4 * hh;
@@ -495,6 +501,31 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
   float xe[NTW][16], qe[NTW][16];
   if (own) {
     const int k = 32 * kt + li;
+    if constexpr (BFV) {
+    // bf16: Kn, Qn rows exact, dQK and dKK + dKK^T split.
+#pragma unroll 2
+    for (int g = 0; g < R / 16; ++g) {
+      const int c0 = 16 * g + 8 * hh;
+      bf16x8 bk, bq;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bk[e] = (__bf16)kr(c0 + e, k);
+        bq[e] = (__bf16)qr(c0 + e, k);
+      }
+#pragma unroll
+      for (int m = 0; m < NTW; ++m) {
+        const int row = 32 * tile_rt(m) + li;
+        if (has_q) {
+          mma_split_exact(dq[m], row_split_bf8(dqk, LT, row, c0), bk);
+          mma_split_exact(dka[m], col_split_bf8(dqk, LT, row, c0), bq);
+        }
+        float kk[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kk[e] = dkk[row * LT + c0 + e] + dkk[(c0 + e) * LT + row];
+        mma_split_exact(dka[m], split_bf8(kk), bk);
+      }
+    }
+    } else {
 #pragma unroll 2
     for (int g = 0; g < R / 8; ++g) {
       const int c0 = 8 * g + 4 * hh;
@@ -509,6 +540,7 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
         }
         mma8(dka[m], ld_c(dkk, LT, row, c0) + ld_x(dkk, LT, row, c0), bk);
       }
+    }
     }
     if (XR) {
       const bool kin = k < K;

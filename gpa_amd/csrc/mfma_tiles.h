@@ -127,6 +127,12 @@ __device__ __forceinline__ SplitBf8 col_split_bf8(const float* m, int ld, int x,
   for (int e = 0; e < 8; ++e) v[e] = m[(c0 + e) * ld + x];
   return split_bf8(v);
 }
+// Elements (x, c0 + e) of an fp32 matrix stored with c contiguous (16-byte aligned rows).
+__device__ __forceinline__ SplitBf8 row_split_bf8(const float* m, int ld, int x, int c0) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(m + x * ld + c0), b = *reinterpret_cast<const f32x4*>(m + x * ld + c0 + 4);
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  return split_bf8(v);
+}
 // Elements (x, c0 + e) of a bf16 matrix stored with c contiguous (8-byte aligned rows).
 __device__ __forceinline__ bf16x8 row_bf8(const bf16_t* m, int ld, int x, int c0) {
   const uint2 a = *reinterpret_cast<const uint2*>(m + x * ld + c0), b = *reinterpret_cast<const uint2*>(m + x * ld + c0 + 4);
@@ -146,6 +152,10 @@ __device__ __forceinline__ void mma_split(f32x16& c, const SplitBf8& a, const Sp
 __device__ __forceinline__ void mma_exact_split(f32x16& c, bf16x8 a, const SplitBf8& b) {
   mma_bf16(c, a, b.hi);
   mma_bf16(c, a, b.lo);
+}
+__device__ __forceinline__ void mma_split_exact(f32x16& c, const SplitBf8& a, bf16x8 b) {
+  mma_bf16(c, a.hi, b);
+  mma_bf16(c, a.lo, b);
 }
 
 template <typename E>
