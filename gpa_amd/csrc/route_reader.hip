@@ -83,6 +83,23 @@ __device__ __forceinline__ float gelu_grad(float x) {
   return .5f * (1.f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-.5f * x * x);
 }
 
+// Workgroups go to the 8 XCDs round robin (id % 8).  xcd_logical renumbers
+// them so that each XCD runs a contiguous range of logical ids, and
+// workgroups that read the same data (one head's weights; the tiles of one
+// weight-gradient product, head and span) share that XCD's L2.
+__device__ __forceinline__ int xcd_logical(int id, int n) {
+  const int q = n / 8, r = n % 8, x = id % 8, local = id / 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+// Row tile and head of a route workgroup (grid: row tiles x heads).
+struct RouteTile {
+  int tile, h;
+};
+__device__ __forceinline__ RouteTile route_tile() {
+  const int nt = gridDim.x, id = xcd_logical(blockIdx.x + nt * blockIdx.y, nt * gridDim.y);
+  return RouteTile{id % nt, id / nt};
+}
+
 // Offsets of a workgroup's rows r = b*T + t: the (b, t) split of each of its
 // RR rows is computed once (rows past the end repeat the last one).
 struct Rows {
@@ -203,7 +220,8 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   using W = typename Wt<E>::type;
   HIP_DYNAMIC_SHARED(float, lds)
   const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens;
-  const int h = blockIdx.y, row0 = blockIdx.x * RR;
+  const RouteTile rtile = route_tile();
+  const int h = rtile.h, row0 = rtile.tile * RR;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kM = pad16(M), k2M = pad16(2 * M), kD = pad16(Dk);
   const int lda = kM + 4, ldh = (k2M > kD ? k2M : kD) + 4;
@@ -412,7 +430,8 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   HIP_DYNAMIC_SHARED(float, lds)
   __shared__ float red[RW][2 + GPA_ROUTE_MAX_INCOMING];
   const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens, H = p.heads, NI = p.incoming;
-  const int h = blockIdx.y, row0 = blockIdx.x * RR;
+  const RouteTile rtile = route_tile();
+  const int h = rtile.h, row0 = rtile.tile * RR;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kM = pad16(M), k2M = pad16(2 * M);
   const int lda = kM + 4, ldh = k2M + 4;
@@ -779,7 +798,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
     if (tid < 2 + NI) {
       float x = 0.f;
       for (int w = 0; w < RW; ++w) x += red[w][tid];
-      g.partials[((int64_t)blockIdx.x * H + h) * (2 + NI) + tid] = x;
+      g.partials[((int64_t)rtile.tile * H + h) * (2 + NI) + tid] = x;
     }
   }
 }
@@ -911,13 +930,6 @@ struct WJobs {
   int span, R, tiles, heads, n;  // tiles of all four products, workgroups
 };
 
-// Workgroups go to the 8 XCDs round robin (id % 8).  Renumber them so that
-// each XCD runs a contiguous range of logical ids: the tiles of one product,
-// head and span, which read the same rows of A or B, then share an L2.
-__device__ __forceinline__ int xcd_logical(int id, int n) {
-  const int q = n / 8, r = n % 8, x = id % 8, local = id / 8;
-  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
-}
 
 __global__ __launch_bounds__(GNT, 4) void route_wgrad16(WJobs js) {
   HIP_DYNAMIC_SHARED(uint16_t, glds)
