@@ -494,18 +494,31 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
       if (t >= pad32(M) / 32) continue;
       f32x16 acc = {};
       tile_gemm(acc, G, lda, rs, kM, kM, 32 * t, lane);
+      // The row operands are all loaded (at clamped addresses) before the
+      // first store, so that their latencies overlap.
+      // Without d route the same loads read the saved hd rows (always valid).
+      float dro[16], hdv[16];
+      const E* drp = droute ? droute : shd;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int col = 32 * t + (lane & 31), r = row0 + acc_row(i, lane >> 5);
+        const bool ok = col < M && r < R;
+        const int rc = ok ? r : 0, cc = ok ? col : 0;
+        dro[i] = to_f32(drp[droute ? rows.at(g.droute, rc, h) + cc : (int64_t)rc * M + cc]);
+        hdv[i] = to_f32(shd[(int64_t)rc * M + cc]);
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
         if (col < M) {
           float d = round_as<E>(acc[i]);
-          if (droute && r < R) d = round_as<E>(d + to_f32(droute[rows.at(g.droute, r, h) + col]));
+          if (droute && r < R) d = round_as<E>(d + dro[i]);
           if (r >= R) d = 0.f;
           dr1[s][i] = d;
           const float dhd = round_as<E>(gm * d);
           A2[row * lda + col] = dhd;
           if (r < R) {
-            part_mg += d * to_f32(shd[(int64_t)r * M + col]);
+            part_mg += d * hdv[i];
             gdhd[(int64_t)r * M + col] = from_f32<E>(dhd);
           }
         } else if (col < kM) {
@@ -552,13 +565,20 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
     for (int t = wave; t < pad32(2 * M) / 32; t += RW) {
       f32x16 acc = {};
       tile_gemm(acc, A2, lda, down, kM, kM, 32 * t, lane);
+      float h1v[16];  // loaded before the first store (see above)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int col = 32 * t + (lane & 31), r = row0 + acc_row(i, lane >> 5);
+        const bool ok = col < 2 * M && r < R;
+        h1v[i] = to_f32(sh1[(int64_t)(ok ? r : 0) * 2 * M + (ok ? col : 0)]);
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
         if (col < 2 * M) {
           float d = 0.f;
           if (r < R) {
-            const float x = to_f32(sh1[(int64_t)r * 2 * M + col]);
+            const float x = h1v[i];
             d = round_as<E>(round_as<E>(acc[i]) * gelu_grad(x));
             gdh1[(int64_t)r * 2 * M + col] = from_f32<E>(d);
             ghg[(int64_t)r * 2 * M + col] = from_f32<E>(gelu(x));  // shares gelu_grad's erf
