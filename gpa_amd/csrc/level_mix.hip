@@ -571,26 +571,30 @@ struct Col {
   bool ok;
 };
 
-// Eight consecutive elements first .. first+7 of a column (zero past `count`
-// or in a padding column), without branches: indices are clamped for the
-// load and masked after it.  With FAST (count a multiple of 16) and a unit
-// stride they are two 16-byte loads.
+// Eight consecutive elements first .. first+7 of a column, loads only:
+// indices are clamped to the column, and mask8 zeroes what lies past `count`
+// or in a padding column once the loads of a group are all issued (a mask
+// next to its load would make the wave wait for each load in turn).  With
+// FAST (count a multiple of 16) and a unit stride they are two 16-byte
+// loads; the stride is one per operand, so the branch is uniform.
 template <bool FAST>
 __device__ __forceinline__ void raw8(const Col& c, int first, float (&v)[8]) {
-  if (FAST && c.st == 1) {
+  const int st = __builtin_amdgcn_readfirstlane(c.st);
+  if (FAST && st == 1) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(c.base + first);
     const f32x4 b = *reinterpret_cast<const f32x4*>(c.base + first + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = c.ok ? v[e] : 0.f;
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int i = first + e < c.count ? first + e : c.count - 1;
-      const float x = c.base[i * c.st];
-      v[e] = (c.ok && first + e < c.count) ? x : 0.f;
+      v[e] = c.base[i * st];
     }
   }
+}
+__device__ __forceinline__ void mask8(const Col& c, int first, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (c.ok && first + e < c.count) ? v[e] : 0.f;
 }
 
 __device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
@@ -634,18 +638,18 @@ __device__ __forceinline__ Col bhat_v(const Block& q, int m) {
 // before their MFMAs so that their global loads overlap.  A fragments come
 // from LDS.
 constexpr int FGROUP = 8;
-template <typename LB, typename LA>
-__device__ __forceinline__ void tile2_split_b(f32x16 (&acc)[2], int steps, LB&& load_b, LA&& frag_a) {
+template <bool FAST, typename LA>
+__device__ __forceinline__ void tile2_split_b(f32x16 (&acc)[2], int steps, const Col& col, int sub, LA&& frag_a) {
   f32x16 c[4] = {};
 #pragma unroll 1
   for (int s0 = 0; s0 < steps; s0 += FGROUP) {
     float v[FGROUP][8];
 #pragma unroll
-    for (int j = 0; j < FGROUP; ++j)
-      if (s0 + j < steps) load_b(s0 + j, v[j]);
+    for (int j = 0; j < FGROUP; ++j) raw8<FAST>(col, 16 * (s0 + j < steps ? s0 + j : steps - 1) + sub, v[j]);
 #pragma unroll
     for (int j = 0; j < FGROUP; ++j)
       if (s0 + j < steps) {
+        mask8(col, 16 * (s0 + j) + sub, v[j]);
         bf16x8 hi, lo;
         split8(v[j], hi, lo);
         const bf16x8 a0 = frag_a(0, s0 + j), a1 = frag_a(1, s0 + j);
@@ -755,8 +759,8 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
     const int m = 32 * mt + li;
     f32x16 acc[2];
     const Col col = ahat_k(q, m);
-    tile2_split_b(
-        acc, K16, [&](int ks, float(&v)[8]) { raw8<FAST>(col, 16 * ks + 8 * hh, v); },
+    tile2_split_b<FAST>(
+        acc, K16, col, 8 * hh,
         [&](int rt, int ks) { return *reinterpret_cast<const bf16x8*>(&U[(32 * rt + li) * ldu + 16 * ks + 8 * hh]); });
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -837,8 +841,8 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
       const int c = 32 * dt + li;
       f32x16 acc[2];
       const Col col = part ? bhat_m(q, c) : ahat_m(q, c);
-      tile2_split_b(
-          acc, M16, [&](int ms, float(&v)[8]) { raw8<FAST>(col, 16 * ms + 8 * hh, v); },
+      tile2_split_b<FAST>(
+          acc, M16, col, 8 * hh,
           [&](int rt, int ms) {
             return *reinterpret_cast<const bf16x8*>(&W[(32 * rt + li) * ldw + 16 * ms + 8 * hh]);
           });
@@ -1097,19 +1101,20 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
 #pragma unroll
       for (int jj = 0; jj < G; ++jj) {
         const int c0 = 16 * (s0 + jj) + 8 * hh;
+        raw8<true>(ak, s0 + jj < K16 ? c0 : 16 * (K16 - 1) + 8 * hh, va[jj]);
+        raw8<true>(bv, s0 + jj < V16 ? c0 : 16 * (V16 - 1) + 8 * hh, vb[jj]);
         if (s0 + jj < K16) {
-          raw8<true>(ak, c0, va[jj]);
           rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dkr + c0) : make_uint4(0, 0, 0, 0);
           rk[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
         }
         if (s0 + jj < V16) {
-          raw8<true>(bv, c0, vb[jj]);
           rv[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dvr + c0) : make_uint4(0, 0, 0, 0);
         }
       }
 #pragma unroll
       for (int jj = 0; jj < G; ++jj) {
         if (s0 + jj < K16) {
+          mask8(ak, 16 * (s0 + jj) + 8 * hh, va[jj]);
           bf16x8 bh, bl;
           split8(va[jj], bh, bl);
           const bf16x8 ad = a_frag(rd[jj], -eta0, false), au = a_frag(rk[jj], 1.f, true);
@@ -1119,6 +1124,7 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
           cl[1] = mfma16(au, bl, cl[1]);
         }
         if (s0 + jj < V16) {
+          mask8(bv, 16 * (s0 + jj) + 8 * hh, vb[jj]);
           bf16x8 bh, bl;
           split8(vb[jj], bh, bl);
           const bf16x8 ad = a_frag(rv[jj], -eta1, false);
@@ -1211,11 +1217,11 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
     for (int s0 = 0; s0 < M16; s0 += G) {
       float v[G][8];
 #pragma unroll
-      for (int jj = 0; jj < G; ++jj)
-        if (s0 + jj < M16) raw8<true>(am, 16 * (s0 + jj) + 8 * hh, v[jj]);
+      for (int jj = 0; jj < G; ++jj) raw8<true>(am, 16 * (s0 + jj < M16 ? s0 + jj : M16 - 1) + 8 * hh, v[jj]);
 #pragma unroll
       for (int jj = 0; jj < G; ++jj)
         if (s0 + jj < M16) {
+          mask8(am, 16 * (s0 + jj) + 8 * hh, v[jj]);
           bf16x8 bh, bl, ah, al;
           split8(v[jj], bh, bl);
           const int m0 = 16 * (s0 + jj) + 8 * hh, t = 32 * rt + li;
