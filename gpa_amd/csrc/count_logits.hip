@@ -157,13 +157,26 @@ __global__ __launch_bounds__(CNT) void count_bwd_write(gpa_count_problem p, gpa_
   const float gain = p.gain[h];
   float dc[CT];
   float run = p.prefix[c.tile(b, h, n, m)];
+  // Groups of 16 tokens: the loads of a group (at clamped tokens) are all
+  // issued before the running sum uses them.
+  constexpr int CG = 16;
 #pragma unroll
-  for (int i = 0; i < CT; ++i) {
-    dc[i] = 0.f;
-    if (i < len) {
-      const int t = t0 + i;
-      run += ld<E>(p.write, c.at(p.write, b, t, h) + m);
-      dc[i] = gain * g.dlogits[c.row(b, t, h, m)] / (1.f + run);
+  for (int i0 = 0; i0 < CT; i0 += CG) {
+    float wv[CG], dl[CG];
+#pragma unroll
+    for (int j = 0; j < CG; ++j) {
+      const int t = t0 + (i0 + j < len ? i0 + j : 0);
+      wv[j] = ld<E>(p.write, c.at(p.write, b, t, h) + m);
+      dl[j] = g.dlogits[c.row(b, t, h, m)];
+    }
+#pragma unroll
+    for (int j = 0; j < CG; ++j) {
+      const int i = i0 + j;
+      dc[i] = 0.f;
+      if (i < len) {
+        run += wv[j];
+        dc[i] = gain * dl[j] / (1.f + run);
+      }
     }
   }
   float acc = g.tsum[c.tile(b, h, n, m)];

@@ -39,6 +39,35 @@ __device__ __forceinline__ void frag_split(const float* x, bf16x8& hi, bf16x8& l
   }
 }
 
+// Eight contiguous floats kept raw: a group's loads are all issued before the
+// first conversion, so that the wave waits once per group, not per load.
+struct Raw8 {
+  f32x4 a, b;
+};
+__device__ __forceinline__ Raw8 ld_raw8(const float* x) {
+  return Raw8{*reinterpret_cast<const f32x4*>(x), *reinterpret_cast<const f32x4*>(x + 4)};
+}
+__device__ __forceinline__ bf16x8 exact_of(const Raw8& r) {
+  bf16x8 o;
+  o[0] = (__bf16)r.a.x; o[1] = (__bf16)r.a.y; o[2] = (__bf16)r.a.z; o[3] = (__bf16)r.a.w;
+  o[4] = (__bf16)r.b.x; o[5] = (__bf16)r.b.y; o[6] = (__bf16)r.b.z; o[7] = (__bf16)r.b.w;
+  return o;
+}
+__device__ __forceinline__ void split_of(const Raw8& r, bf16x8& hi, bf16x8& lo) {
+  const float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hi[e] = (__bf16)v[e];
+    lo[e] = (__bf16)(v[e] - (float)hi[e]);
+  }
+}
+// Fragments loaded per group (fewer with 256 keys, whose Qn fragments
+// already hold 64 registers).
+template <int KM>
+constexpr int lgroup() {
+  return KM > 128 ? 4 : 8;
+}
+
 // The (rt, ct) 32x32 tile of P = causal e^{G_t-G_u} Qn Kn^T, with qa the Qn
 // fragments of row tile rt (K16 k steps).  Lane l ends with column
 // u = 32 ct + l%32 and rows t = 32 rt + acc_row(r, l/32).
@@ -49,8 +78,14 @@ __device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const floa
   f32x16 acc = {};
   const float* krow = kn + (32 * ct + li) * K + 8 * hh;
 #pragma unroll
-  for (int ks = 0; ks < KM / 16; ++ks)
-    if (ks < K16) acc = mfma_bf16(qa[ks], frag_exact(krow + 16 * ks), acc);
+  for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
+    Raw8 raw[lgroup<KM>()];
+#pragma unroll
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_raw8(krow + 16 * (k0 + j < K16 ? k0 + j : 0));
+#pragma unroll
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j)
+      if (k0 + j < K16) acc = mfma_bf16(qa[k0 + j], exact_of(raw[j]), acc);
+  }
   const int u = 32 * ct + li;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -64,14 +99,20 @@ template <int KM>
 __device__ __forceinline__ void load_q(bf16x8 (&qa)[KM / 16], const float* qn, int K16, int K, int rt, int l) {
   const float* qrow = qn + (32 * rt + (l & 31)) * K + 8 * (l >> 5);
 #pragma unroll
-  for (int ks = 0; ks < KM / 16; ++ks) qa[ks] = ks < K16 ? frag_exact(qrow + 16 * ks) : bf16x8{};
+  for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
+    Raw8 raw[lgroup<KM>()];
+#pragma unroll
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_raw8(qrow + 16 * (k0 + j < K16 ? k0 + j : 0));
+#pragma unroll
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) qa[k0 + j] = k0 + j < K16 ? exact_of(raw[j]) : bf16x8{};
+  }
 }
 
 }  // namespace
 
 // O = diag(e^G) Qn S_n + P D for one (chunk n, stream s); V <= 256.
 template <int KM>
-__global__ __launch_bounds__(ONT) void gdn_out_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_operand out, int nch) {
+__global__ __launch_bounds__(ONT, 2) void gdn_out_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_operand out, int nch) {
   __shared__ __align__(16) __bf16 ph[R * PLD], pl[R * PLD];  // P hi / lo, [t][u]
   __shared__ float gam_s[R];
   const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
@@ -100,22 +141,31 @@ __global__ __launch_bounds__(ONT) void gdn_out_mfma(gpa_gdn_problem p, gpa_gdn_s
     const int v = 32 * vt + li, vc = v < V ? v : V - 1;  // clamped column: loads stay in bounds
     f32x16 a1 = {}, a2 = {};
     const float* srow = st + (int64_t)vc * K + 8 * hh;
+    const float* drow = dl + (int64_t)vc * R + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KM / 16; ++ks)
-      if (ks < K16) {
-        bf16x8 bh, bl;
-        frag_split(srow + 16 * ks, bh, bl);
-        a1 = mfma_bf16(qa[ks], bh, a1);
-        a2 = mfma_bf16(qa[ks], bl, a2);
-      }
+    for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
+      Raw8 raw[lgroup<KM>()];
+#pragma unroll
+      for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_raw8(srow + 16 * (k0 + j < K16 ? k0 + j : 0));
+#pragma unroll
+      for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j)
+        if (k0 + j < K16) {
+          bf16x8 bh, bl;
+          split_of(raw[j], bh, bl);
+          a1 = mfma_bf16(qa[k0 + j], bh, a1);
+          a2 = mfma_bf16(qa[k0 + j], bl, a2);
+        }
+    }
+    Raw8 draw[R / 16];
+#pragma unroll
+    for (int us = 0; us < R / 16; ++us) draw[us] = ld_raw8(drow + 16 * us);
     f32x16 acc = a1 + a2;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] *= __expf(gam_s[32 * rt + acc_row(r, hh)]);
-    const float* drow = dl + (int64_t)vc * R + 8 * hh;
 #pragma unroll
     for (int us = 0; us < R / 16; ++us) {
       bf16x8 dh, dlo;
-      frag_split(drow + 16 * us, dh, dlo);
+      split_of(draw[us], dh, dlo);
       const int off = (32 * rt + li) * PLD + 16 * us + 8 * hh;
       const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&ph[off]);
       const bf16x8 pb = *reinterpret_cast<const bf16x8*>(&pl[off]);
@@ -137,7 +187,7 @@ __global__ __launch_bounds__(ONT) void gdn_out_mfma(gpa_gdn_problem p, gpa_gdn_s
 // dd0 = P^T dO and o = diag(e^G) dO (value-major [V][R]) for one (chunk n,
 // stream s); V <= 256.
 template <int KM>
-__global__ __launch_bounds__(ONT) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
+__global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
                                                      int nch) {
   __shared__ __align__(16) __bf16 ph[R * PLD], pl[R * PLD];  // P^T hi / lo, [u][t]
   __shared__ __align__(16) __bf16 dot[GPA_OUT_MFMA_MAX_V * PLD];  // dO^T, [v][t] (exact)
@@ -152,11 +202,13 @@ __global__ __launch_bounds__(ONT) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gdn_s
     const int t = idx / V8, v0 = 8 * (idx - t * V8), tok = token_at(p, n, t);
     const bf16_t* src = reinterpret_cast<const bf16_t*>(gr.dout.ptr) + op_base(gr.dout, b, h) +
                         (int64_t)(tok >= 0 ? tok : 0) * gr.dout.st;
+    bf16_t x[8];  // clamped loads first, masks at the stores
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = src[v0 + e < V ? v0 + e : V - 1];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int v = v0 + e;
-      const bf16_t x = (tok >= 0 && v < V) ? src[v] : bf16_t{0};
-      if (v < V) reinterpret_cast<bf16_t*>(dot)[v * PLD + t] = x;
+      if (v < V) reinterpret_cast<bf16_t*>(dot)[v * PLD + t] = tok >= 0 ? x[e] : bf16_t{0};
     }
   }
   bf16x8 qa[KM / 16];
@@ -318,14 +370,17 @@ __global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_g
     gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
     qdot_s[tid] = 0.f;
   }
-  {  // query row norms, 4 threads per row
+  {  // query row norms, 4 threads per row; loads first (clamped), then the sum
     const int row = tid >> 2, part = tid & 3, tok = token_at(p, n, row);
+    float xs[KM / 4];
+#pragma unroll
+    for (int i = 0; i < KM / 4; ++i) {
+      const int c = part + 4 * i;
+      xs[i] = op_load<bf16_t>(p.q, b, h, tok >= 0 ? tok : 0, c < K ? c : 0);
+    }
     float ss = 0.f;
-    if (tok >= 0)
-      for (int c = part; c < K; c += 4) {
-        const float x = op_load<bf16_t>(p.q, b, h, tok, c);
-        ss += x * x;
-      }
+#pragma unroll
+    for (int i = 0; i < KM / 4; ++i) ss += (tok >= 0 && part + 4 * i < K) ? xs[i] * xs[i] : 0.f;
     ss += __shfl_xor(ss, 1);
     ss += __shfl_xor(ss, 2);
     if (part == 0) {
@@ -346,30 +401,44 @@ __global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_g
   const int pc = w >> 1;  // dO D^T tile (rt, pc)
   for (int v0 = 0; v0 < V; v0 += VSL) {
     __syncthreads();
-    // S_n^T slice: thread -> (value v, 4 keys), split into hi / lo.
-    for (int idx = tid; idx < VSL * (KM / 4); idx += ONT) {
-      const int vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (v < V && k < K) x = *reinterpret_cast<const float4*>(st + (int64_t)v * K + k);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
+    // S_n^T slice: thread -> (value v, 4 keys), split into hi / lo; D^T
+    // slice: thread -> (value v, 4 positions).  All loads of the thread are
+    // issued (at clamped addresses) before the first store.
+    constexpr int SN = VSL * (KM / 4) / ONT, DN = VSL * (R / 4) / ONT;
+    static_assert(SN * ONT == VSL * (KM / 4) && DN * ONT == VSL * (R / 4), "staging shares");
+    float4 xs[SN], xd[DN];
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const int idx = tid + ONT * i, vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
+      xs[i] = *reinterpret_cast<const float4*>(st + ((v < V && k < K) ? (int64_t)v * K + k : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < DN; ++i) {
+      const int idx = tid + ONT * i, vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
+      xd[i] = *reinterpret_cast<const float4*>(dl + (v < V ? (int64_t)v * R + u : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const int idx = tid + ONT * i, vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
+      const bool ok = v < V && k < K;
+      const float x4[4] = {ok ? xs[i].x : 0.f, ok ? xs[i].y : 0.f, ok ? xs[i].z : 0.f, ok ? xs[i].w : 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const __bf16 hi = (__bf16)xs[e];
+        const __bf16 hi = (__bf16)x4[e];
         sth[(k + e) * PLD + vl] = hi;
-        stl[(k + e) * PLD + vl] = (__bf16)(xs[e] - (float)hi);
+        stl[(k + e) * PLD + vl] = (__bf16)(x4[e] - (float)hi);
       }
     }
-    // D^T slice: thread -> (value v, 4 positions).
-    for (int idx = tid; idx < VSL * (R / 4); idx += ONT) {
-      const int vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (v < V) x = *reinterpret_cast<const float4*>(dl + (int64_t)v * R + u);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < DN; ++i) {
+      const int idx = tid + ONT * i, vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
+      const bool ok = v < V;
+      const float x4[4] = {ok ? xd[i].x : 0.f, ok ? xd[i].y : 0.f, ok ? xd[i].z : 0.f, ok ? xd[i].w : 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const __bf16 hi = (__bf16)xs[e];
+        const __bf16 hi = (__bf16)x4[e];
         dth[(u + e) * PLD + vl] = hi;
-        dtl[(u + e) * PLD + vl] = (__bf16)(xs[e] - (float)hi);
+        dtl[(u + e) * PLD + vl] = (__bf16)(x4[e] - (float)hi);
       }
     }
     __syncthreads();
@@ -430,10 +499,16 @@ __global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_g
     const int kt = pc + 2 * j, k = 32 * kt + li;
     float c[16];
 #pragma unroll
+    for (int r = 0; r < 16; ++r) {  // clamped loads first, masks after
+      const int t = 32 * rt + acc_row(r, hh), tok = token_at(p, n, t);
+      const bool ok = kt < KT && k < K && tok >= 0;
+      qe[j][r] = op_load<bf16_t>(p.q, b, h, ok ? tok : 0, ok ? k : 0);
+    }
+#pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 32 * rt + acc_row(r, hh), tok = token_at(p, n, t);
       const bool ok = kt < KT && k < K && tok >= 0;
-      qe[j][r] = ok ? op_load<bf16_t>(p.q, b, h, tok, k) * qrd_s[t] : 0.f;
+      qe[j][r] = ok ? qe[j][r] * qrd_s[t] : 0.f;
       c[r] = qe[j][r] * aq[j][r];
     }
     const float sq = tile_row_sum(c, l);

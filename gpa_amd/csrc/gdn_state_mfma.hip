@@ -140,11 +140,24 @@ __device__ __forceinline__ void load_gates(float (&g16)[16], float& gc, const fl
 }
 
 // Key-major [K][V] state (initial state, final state and its gradient).
+// The 16 loads are unconditional (out-of-range elements read element (0, 0))
+// and masked afterwards, so that they are in flight together.
 __device__ __forceinline__ void load_km(f32x16& x, const float* m, int64_t base, int v, int V, int K, int k0, int l) {
+  if (!m) {
+    x = f32x16{};
+    return;
+  }
+  float t[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int k = k0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    x[r] = (m && k < K && v < V) ? m[base + (int64_t)k * V + v] : 0.f;
+    const bool ok = k < K && v < V;
+    t[r] = m[base + (ok ? (int64_t)k * V + v : 0)];
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int k = k0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    x[r] = (k < K && v < V) ? t[r] : 0.f;
   }
 }
 
