@@ -255,6 +255,10 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
       }
     }
     const float gain = p.gain[h];
+    // edge weights read once (a load inside the row loop would wait behind the stores)
+    float ew[GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+    for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < p.incoming ? p.edge_weight[e * p.heads + h] : 0.f;
 #pragma unroll
     for (int i = 0; i < VPASS; ++i) {
       const int row = rsub + 8 * i, r = row0 + row;
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
 #pragma unroll
         for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
           if (e < p.incoming && on) {
-            const float w = p.edge_weight[e * p.heads + h];
+            const float w = ew[e];
             float x[8];
             unpack_bf8(mv[i][e], x);
 #pragma unroll
@@ -502,8 +506,10 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int col = 32 * t + (lane & 31), r = row0 + acc_row(i, lane >> 5);
+        // Masked entries read the tile's first row (rows.at only knows this
+        // tile's rows; row0 < R always).
         const bool ok = col < M && r < R;
-        const int rc = ok ? r : 0, cc = ok ? col : 0;
+        const int rc = ok ? r : row0, cc = ok ? col : 0;
         dro[i] = to_f32(drp[droute ? rows.at(g.droute, rc, h) + cc : (int64_t)rc * M + cc]);
         hdv[i] = to_f32(shd[(int64_t)rc * M + cc]);
       }
@@ -643,6 +649,9 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
       }
     }
     const float gain = p.gain[h];
+    float ew[GPA_ROUTE_MAX_INCOMING];  // read once, as in the forward
+#pragma unroll
+    for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < NI ? p.edge_weight[e * H + h] : 0.f;
 #pragma unroll
     for (int i = 0; i < VPASS; ++i) {
       const int row = rsub + 8 * i, r = row0 + row;
@@ -654,7 +663,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
 #pragma unroll
         for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
           if (e < NI && on) {
-            const float w = p.edge_weight[e * H + h];
+            const float w = ew[e];
             unpack_bf8(mv[i][e], msgf[e]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) z[j] += w * msgf[e][j];
@@ -731,7 +740,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
 #pragma unroll
         for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
           if (e < NI && on) {
-            const float w = p.edge_weight[e * H + h];
+            const float w = ew[e];
             float sw = 0.f, dm[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
