@@ -1072,8 +1072,8 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
     float dwr[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int tk = q.token(32 * rt + acc_row(r, hh));
-      dwr[r] = tk >= 0 ? to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m]) : 0.f;
+      const int tk = q.token(32 * rt + acc_row(r, hh));  // void rows: token 0, masked at use
+      dwr[r] = to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk >= 0 ? tk : 0) + m]);
     }
     // A fragments from global: drk and u (contraction k), drv (contraction v).
     const bf16_t* dkr = reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + (trow >= 0 ? q.at(g.dkey_out, trow) : 0);
