@@ -37,9 +37,10 @@ SHAPE = dict(heads=16, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), c
 # HBM bytes per launch of a kernel in this workload, from rocprofv3 FETCH_SIZE
 # (x2.0) and WRITE_SIZE (x1.0) passes calibrated on a 1 GiB copy
 # (profiles/dense_gpa_layer_T8192_pmc_traffic.md).  Used for `roofline.traffic`
-# when that kernel is the dominant one.
-MEASURED_TRAFFIC = {"gdn_state_bwd_mfma<128>": (303177.3 * 2.0 + 239238.7) * 1024,
-                    "gdn_chunk_bwd_mfma<bf16,128>": (368116.2 * 2.0 + 212254.3) * 1024}
+# when that kernel is the dominant one.  The state backward's figure is the
+# dispatch-weighted mean of its two instantiations (with and without a query).
+MEASURED_TRAFFIC = {"gdn_state_bwd_mfma<128>": (279254.2 * 2.0 + 247040.0) * 1024,
+                    "gdn_chunk_bwd_mfma<bf16,128>": (386136.3 * 2.0 + 136162.6) * 1024}
 BATCH, TOKENS = 1, 8192
 
 
