@@ -403,23 +403,26 @@ __global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_g
     __syncthreads();
     // S_n^T slice: thread -> (value v, 4 keys), split into hi / lo; D^T
     // slice: thread -> (value v, 4 positions).  All loads of the thread are
-    // issued (at clamped addresses) before the first store.
+    // issued (at clamped addresses) before the first store.  Lanes take
+    // consecutive values, so that a wave's transposed 2-byte stores go to
+    // consecutive addresses of one LDS row (lanes along the keys would hit
+    // the same few banks).
     constexpr int SN = VSL * (KM / 4) / ONT, DN = VSL * (R / 4) / ONT;
     static_assert(SN * ONT == VSL * (KM / 4) && DN * ONT == VSL * (R / 4), "staging shares");
     float4 xs[SN], xd[DN];
 #pragma unroll
     for (int i = 0; i < SN; ++i) {
-      const int idx = tid + ONT * i, vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
+      const int idx = tid + ONT * i, vl = idx % VSL, k = 4 * (idx / VSL), v = v0 + vl;
       xs[i] = *reinterpret_cast<const float4*>(st + ((v < V && k < K) ? (int64_t)v * K + k : 0));
     }
 #pragma unroll
     for (int i = 0; i < DN; ++i) {
-      const int idx = tid + ONT * i, vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
+      const int idx = tid + ONT * i, vl = idx % VSL, u = 4 * (idx / VSL), v = v0 + vl;
       xd[i] = *reinterpret_cast<const float4*>(dl + (v < V ? (int64_t)v * R + u : 0));
     }
 #pragma unroll
     for (int i = 0; i < SN; ++i) {
-      const int idx = tid + ONT * i, vl = idx / (KM / 4), k = 4 * (idx - vl * (KM / 4)), v = v0 + vl;
+      const int idx = tid + ONT * i, vl = idx % VSL, k = 4 * (idx / VSL), v = v0 + vl;
       const bool ok = v < V && k < K;
       const float x4[4] = {ok ? xs[i].x : 0.f, ok ? xs[i].y : 0.f, ok ? xs[i].z : 0.f, ok ? xs[i].w : 0.f};
 #pragma unroll
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(ONT) void gdn_read_dq_mfma(gpa_gdn_problem p, gpa_g
     }
 #pragma unroll
     for (int i = 0; i < DN; ++i) {
-      const int idx = tid + ONT * i, vl = idx / (R / 4), u = 4 * (idx - vl * (R / 4)), v = v0 + vl;
+      const int idx = tid + ONT * i, vl = idx % VSL, u = 4 * (idx / VSL), v = v0 + vl;
       const bool ok = v < V;
       const float x4[4] = {ok ? xd[i].x : 0.f, ok ? xd[i].y : 0.f, ok ? xd[i].z : 0.f, ok ? xd[i].w : 0.f};
 #pragma unroll

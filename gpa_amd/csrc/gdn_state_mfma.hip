@@ -129,6 +129,22 @@ __device__ __forceinline__ void add_state(f32x16& x, const float* m, int v, int 
   }
 }
 
+// The same elements, loaded (not added): nothing uses them here, so a
+// prefetch stays in flight until its first use.
+template <bool GUARD>
+__device__ __forceinline__ void get_state(f32x16& x, const float* m, int v, int V, int K, int k0, int l) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int k = k0 + 8 * g + 4 * (l >> 5);
+    if (!GUARD || (v < V && k < K)) {
+      const float4 q = *reinterpret_cast<const float4*>(m + (int64_t)v * K + k);
+      x[4 * g] = q.x; x[4 * g + 1] = q.y; x[4 * g + 2] = q.z; x[4 * g + 3] = q.w;
+    } else {
+      x[4 * g] = x[4 * g + 1] = x[4 * g + 2] = x[4 * g + 3] = 0.f;
+    }
+  }
+}
+
 // Gates of the 16 accumulator rows of lane l (row block row0) and G_C.
 __device__ __forceinline__ void load_gates(float (&g16)[16], float& gc, const float* gm, int row0, int l) {
 #pragma unroll
@@ -373,10 +389,11 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
       for (int i = 0; i < NRB; ++i)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-          inj[i][cb] = f32x16{};
           if (owns && sp.rows(w + 4 * i))
-            add_state<!FAST>(inj[i][cb], gr.dstates + state_off(s, n, nch, K, V), v0 + 32 * cb + (l & 31), V, K,
-                      32 * (w + 4 * i), l);
+            get_state<!FAST>(inj[i][cb], gr.dstates + state_off(s, n, nch, K, V), v0 + 32 * cb + (l & 31), V, K,
+                             32 * (w + 4 * i), l);
+          else
+            inj[i][cb] = f32x16{};
         }
     }
   };
