@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -124,6 +124,16 @@ class CountGrads(ctypes.Structure):
                [(n, c_vp) for n in ("dcount0", "partials", "tsum")]
 
 
+class SlotProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "key_dim", "slots", "dtype")] + \
+               [("key", Operand), ("center", c_vp), ("center_t", c_vp), ("gate_w", c_vp), ("slot", Operand),
+                ("raw", Operand)]
+
+
+class SlotGrads(ctypes.Structure):
+    _fields_ = [(n, Operand) for n in ("dslot", "draw", "dkey")] + [(n, c_vp) for n in ("dcenter", "dgate_w")]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -146,6 +156,8 @@ EXPORTS = {
     "gpa_count_logits_forward": ([ctypes.POINTER(CountProblem), c_vp], ctypes.c_int),
     "gpa_count_logits_backward": ([ctypes.POINTER(CountProblem), ctypes.POINTER(CountGrads), c_vp],
                                   ctypes.c_int),
+    "gpa_slot_gates_forward": ([ctypes.POINTER(SlotProblem), c_vp], ctypes.c_int),
+    "gpa_slot_gates_backward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(SlotGrads), c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -39,3 +39,20 @@ int check_launch(const char* what);
 // Records timing->events[timing->launched++] on `stream` (no-op without timing).
 struct gpa_timing;
 void mark(gpa_timing* timing, hipStream_t stream);
+
+namespace gpa {
+// Up to four products C[h] = sum over the R rows r of A[h][r]^T B[h][r]
+// (float32 [heads][a_width][b_width], cleared first), rounded to bf16 values
+// when bf16: row r of head h of A sits at a + h * a_hs + r * a_rs (elements).
+// The bf16 path runs them as one MFMA launch (route_reader.hip).
+struct TnProduct {
+  const void* a;
+  int64_t a_rs, a_hs;
+  int a_width;
+  const void* b;
+  int64_t b_rs, b_hs;
+  int b_width;
+  float* c;
+};
+int launch_tn_products(const TnProduct* products, int n, int heads, int rows, bool bf16, hipStream_t stream);
+}  // namespace gpa

@@ -1194,6 +1194,62 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
   return check_launch("gpa_route_backward");
 }
 
+namespace gpa {
+int launch_tn_products(const TnProduct* products, int np, int H, int R, bool bf, hipStream_t stream) {
+  if (np < 1 || np > 4) return fail(GPA_HIP_EINVAL, "tn products: 1 to 4 products");
+  struct Job {
+    TnOperand a, b;
+    float* c;
+  } jobs[4];
+  for (int q = 0; q < np; ++q)
+    jobs[q] = {{products[q].a, products[q].a_rs, products[q].a_hs, products[q].a_width},
+               {products[q].b, products[q].b_rs, products[q].b_hs, products[q].b_width},
+               products[q].c};
+  bool fast = bf;
+  for (int q = 0; q < np; ++q) fast = fast && wgrad16_ok(jobs[q].a) && wgrad16_ok(jobs[q].b);
+  if (fast) {
+    WJob w[4] = {};  // unused products have no tiles
+    FourBufs fb = {};
+    int tiles = 0;
+    for (int q = 0; q < np; ++q) {
+      const int ti = (jobs[q].a.width + GT - 1) / GT, tj = (jobs[q].b.width + GT - 1) / GT;
+      w[q] = {jobs[q].a, jobs[q].b, jobs[q].c, tj, ti * tj};
+      fb.c[q] = jobs[q].c;
+      fb.n[q] = (int64_t)H * jobs[q].a.width * jobs[q].b.width;
+      tiles += ti * tj;
+    }
+    // Row spans: enough workgroups for the whole chip, each span whole slabs.
+    const int slabs = (R + GK - 1) / GK, per_span_wgs = tiles * H;
+    int spans = (G_WGS + per_span_wgs - 1) / per_span_wgs;
+    spans = spans < 1 ? 1 : spans > slabs ? slabs : spans;
+    const int span = GK * ((slabs + spans - 1) / spans);
+    spans = (R + span - 1) / span;
+    const int n = tiles * H * spans;
+    const WJobs js{w[0], w[1], w[2], w[3], span, R, tiles, H, n};
+    if (int rc = set_lds(route_wgrad16, G_LDS)) return rc;
+    const int64_t total = fb.n[0] + fb.n[1] + fb.n[2] + fb.n[3];
+    const dim3 fgrid((unsigned)((total + 1023) / 1024 < 2048 ? (total + 1023) / 1024 : 2048));
+    hipLaunchKernelGGL(fill_or_round4<false>, fgrid, dim3(256), 0, stream, fb);
+    hipLaunchKernelGGL(route_wgrad16, dim3(n), dim3(GNT), G_LDS, stream, js);
+    hipLaunchKernelGGL(fill_or_round4<true>, fgrid, dim3(256), 0, stream, fb);
+    return GPA_HIP_OK;
+  }
+  for (int q = 0; q < np; ++q) {
+    const Job& j = jobs[q];
+    const int64_t n = (int64_t)H * j.a.width * j.b.width;
+    const dim3 fill_grid((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64));
+    hipLaunchKernelGGL(fill_zero, fill_grid, dim3(256), 0, stream, j.c, n);
+    const dim3 grid(((j.a.width + WT - 1) / WT) * ((j.b.width + WT - 1) / WT), H, (R + WKC - 1) / WKC);
+    if (bf)
+      hipLaunchKernelGGL(route_wgrad<bf16_t>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
+    else
+      hipLaunchKernelGGL(route_wgrad<float>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
+    if (bf) hipLaunchKernelGGL(round_in_place<bf16_t>, fill_grid, dim3(256), 0, stream, j.c, n);
+  }
+  return GPA_HIP_OK;
+}
+}  // namespace gpa
+
 extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gpa_route_grads* grads, float* d_up,
                                       float* d_down, float* d_rs, float* d_qs, hipStream_t stream) {
   using namespace gpa;
@@ -1217,48 +1273,10 @@ extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gp
   const TnOperand r1{problem->route.ptr, rs_route, problem->route.sh, M};
   const TnOperand dqo{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M};
   const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk};
-  struct Job { TnOperand a, b; float* c; } jobs[4] = {{r0, dh1, d_up}, {hid, dhd, d_down}, {r1, dqo, d_rs},
-                                                        {q, dqs, d_qs}};
-  const bool bf = problem->dtype == GPA_DTYPE_BF16;
-  bool fast = bf;
-  for (const Job& j : jobs) fast = fast && wgrad16_ok(j.a) && wgrad16_ok(j.b);
-  if (fast) {
-    WJob w[4];
-    FourBufs fb;
-    int tiles = 0;
-    for (int q = 0; q < 4; ++q) {
-      const int ti = (jobs[q].a.width + GT - 1) / GT, tj = (jobs[q].b.width + GT - 1) / GT;
-      w[q] = {jobs[q].a, jobs[q].b, jobs[q].c, tj, ti * tj};
-      fb.c[q] = jobs[q].c;
-      fb.n[q] = (int64_t)H * jobs[q].a.width * jobs[q].b.width;
-      tiles += ti * tj;
-    }
-    // Row spans: enough workgroups for the whole chip, each span whole slabs.
-    const int slabs = (R + GK - 1) / GK, per_span_wgs = tiles * H;
-    int spans = (G_WGS + per_span_wgs - 1) / per_span_wgs;
-    spans = spans < 1 ? 1 : spans > slabs ? slabs : spans;
-    const int span = GK * ((slabs + spans - 1) / spans);
-    spans = (R + span - 1) / span;
-    const int n = tiles * H * spans;
-    const WJobs js{w[0], w[1], w[2], w[3], span, R, tiles, H, n};
-    if (int rc = set_lds(route_wgrad16, G_LDS)) return rc;
-    const int64_t total = fb.n[0] + fb.n[1] + fb.n[2] + fb.n[3];
-    const dim3 fgrid((unsigned)((total + 1023) / 1024 < 2048 ? (total + 1023) / 1024 : 2048));
-    hipLaunchKernelGGL(fill_or_round4<false>, fgrid, dim3(256), 0, stream, fb);
-    hipLaunchKernelGGL(route_wgrad16, dim3(n), dim3(GNT), G_LDS, stream, js);
-    hipLaunchKernelGGL(fill_or_round4<true>, fgrid, dim3(256), 0, stream, fb);
-    return check_launch("gpa_route_weight_grads");
-  }
-  for (const Job& j : jobs) {
-    const int64_t n = (int64_t)H * j.a.width * j.b.width;
-    const dim3 fill_grid((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64));
-    hipLaunchKernelGGL(fill_zero, fill_grid, dim3(256), 0, stream, j.c, n);
-    const dim3 grid(((j.a.width + WT - 1) / WT) * ((j.b.width + WT - 1) / WT), H, (R + WKC - 1) / WKC);
-    if (bf)
-      hipLaunchKernelGGL(route_wgrad<bf16_t>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
-    else
-      hipLaunchKernelGGL(route_wgrad<float>, grid, dim3(RNT), 0, stream, j.a, j.b, j.c, R);
-    if (bf) hipLaunchKernelGGL(round_in_place<bf16_t>, fill_grid, dim3(256), 0, stream, j.c, n);
-  }
+  auto prod = [](const TnOperand& a, const TnOperand& b, float* c) {
+    return TnProduct{a.ptr, a.rs, a.hs, a.width, b.ptr, b.rs, b.hs, b.width, c};
+  };
+  const TnProduct products[4] = {prod(r0, dh1, d_up), prod(hid, dhd, d_down), prod(r1, dqo, d_rs), prod(q, dqs, d_qs)};
+  if (int rc = launch_tn_products(products, 4, H, R, problem->dtype == GPA_DTYPE_BF16, stream)) return rc;
   return check_launch("gpa_route_weight_grads");
 }

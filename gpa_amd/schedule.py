@@ -32,6 +32,8 @@ from . import _lib
 from .ops import gdn_scan_deferred, gdn_scan_hip
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
+from .slots import slot_gates
+from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
 from .level import level_mix
 from .level import supported as fused_level_supported
@@ -167,8 +169,13 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     levels: list[_Level] = []
     for j, (old, snap) in enumerate(zip(state.levels, frozen0)):
         lv = _Level()
-        slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
-        g_in, b_in, g_out, b_out = _gates(model, key, j, control)
+        if _FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]):
+            proj, raw = slot_gates(key, model.center[j], model.gate_weight[j])
+            slot = _slot_feature(cfg, proj)
+            g_in, b_in, g_out, b_out = _gates(model, key, j, control, raw)
+        else:
+            slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
+            g_in, b_in, g_out, b_out = _gates(model, key, j, control)
         # The outer read of this level (below) runs the B recurrence with the
         # same keys, values, gates and initial state: where the kernels allow,
         # the B scan keeps its intermediates for that read instead.
@@ -331,11 +338,14 @@ def _assignment(cfg, slot: Tensor):
     return (slot / .25).softmax(-1) if cfg.rsa_update else None
 
 
-def _gates(model, key: Tensor, j: int, control: Tensor | None):
-    """Scalar decay/strength gates per token and head (attention.py:161-174)."""
+def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | None = None):
+    """Scalar decay/strength gates per token and head (attention.py:161-174);
+    `raw` is the gate input product when the caller has it already."""
     cfg = model.config
     w = model.gate_weight[j]
-    if cfg.control_dim:
+    if raw is not None:
+        pass
+    elif cfg.control_dim:
         raw = _mm(control, w, "btd,hdc->bthc", control.dtype)
     else:
         src = key if cfg.rsa_update else _unit(key)
@@ -375,6 +385,7 @@ def _count_scalars(model, j: int, like: Tensor):
 
 
 _FUSED_COUNTS = [True]  # counts and base logits in HIP (counts.py)
+_FUSED_SLOTS = [True]  # slot products and gate inputs in HIP (slots.py)
 
 
 def _residual(model, key, value, rk, rv, j):

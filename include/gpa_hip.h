@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 10
+#define GPA_HIP_ABI_VERSION 11
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -341,6 +341,35 @@ typedef struct gpa_count_grads {
 int gpa_count_logits_forward(const gpa_count_problem *problem, hipStream_t stream);
 int gpa_count_logits_backward(const gpa_count_problem *problem, const gpa_count_grads *grads,
                               hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Slot products and gate inputs of one level (bf16 activations):
+ *   slot = k C^T                 reference attention.py:176-177 (_slot; the
+ *                                linear slot feature is the identity)
+ *   raw  = unit(k) W_g           attention.py:165 (_gates without control
+ *                                input or rsa_update; unit as ops.py:14-17)
+ * C = center[level] and W_g = gate_weight[level] rounded to bf16; products
+ * accumulate in float32 and round to bf16.  The gate nonlinearities stay with
+ * the caller.  Key width a multiple of 16 up to 256, slots a multiple of 32 up
+ * to 256, key and dslot rows 16-byte aligned. */
+typedef struct gpa_slot_problem {
+    int batch, tokens, heads, key_dim, slots, dtype;
+    gpa_operand key;                              /* [B,T,H,Dk] */
+    const void *center;                           /* [H][M][Dk] bf16 */
+    const void *center_t;                         /* [H][Dk][M] bf16 (backward only) */
+    const void *gate_w;                           /* [H][Dk][4] bf16 */
+    gpa_operand slot, raw;                        /* out [B,T,H,M], [B,T,H,4] (forward) */
+} gpa_slot_problem;
+
+typedef struct gpa_slot_grads {
+    gpa_operand dslot, draw;                      /* incoming [B,T,H,M], [B,T,H,4] bf16 */
+    gpa_operand dkey;                             /* out [B,T,H,Dk]: both terms, added */
+    float *dcenter;                               /* out [H][M][Dk], sums rounded to bf16 values */
+    float *dgate_w;                               /* out [H][Dk][4], sums rounded to bf16 values */
+} gpa_slot_grads;
+
+int gpa_slot_gates_forward(const gpa_slot_problem *problem, hipStream_t stream);
+int gpa_slot_gates_backward(const gpa_slot_problem *problem, const gpa_slot_grads *grads, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -20,7 +20,7 @@ def test_header_declares_the_entry_points():
     for expected in ("gpa_hip_abi_version", "gpa_hip_last_error", "gpa_gdn_nchunks", "gpa_gdn_path",
                      "gpa_gdn_forward", "gpa_gdn_backward", "gpa_gdn_read", "gpa_gdn_read_backward",
                      "gpa_decode_step", "gpa_route_forward", "gpa_count_logits_forward",
-                     "gpa_count_logits_backward",
+                     "gpa_count_logits_backward", "gpa_slot_gates_forward", "gpa_slot_gates_backward",
                      "gpa_route_backward", "gpa_route_weight_grads", "gpa_level_forward", "gpa_level_backward"):
         assert expected in names
 
@@ -73,6 +73,9 @@ def test_ctypes_structs_match_c_layout():
     # 5 int32 (+pad), 2 operands, count0 + its stride, 5 pointers
     assert ctypes.sizeof(_lib.CountProblem) == 24 + 2 * 32 + 2 * 8 + 5 * 8
     assert ctypes.sizeof(_lib.CountGrads) == 2 * 8 + 2 * 32 + 3 * 8
+    # 6 int32, key operand, 3 pointers, 2 operands; 3 operands, 2 pointers
+    assert ctypes.sizeof(_lib.SlotProblem) == 24 + 32 + 3 * 8 + 2 * 32
+    assert ctypes.sizeof(_lib.SlotGrads) == 3 * 32 + 2 * 8
 
 
 def test_backend_refuses_cpu_tensors():
