@@ -40,7 +40,7 @@ SHAPE = dict(heads=16, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), c
 # when that kernel is the dominant one.  The state backward's figure is the
 # dispatch-weighted mean of its two instantiations (with and without a query).
 MEASURED_TRAFFIC = {"gdn_state_bwd_mfma<128>": (279254.2 * 2.0 + 247040.0) * 1024,
-                    "gdn_chunk_bwd_mfma<bf16,128>": (386136.3 * 2.0 + 136162.6) * 1024}
+                    "gdn_chunk_bwd_mfma<bf16,128>": (392730.9 * 2.0 + 129279.9) * 1024}
 BATCH, TOKENS = 1, 8192
 
 
