@@ -6,7 +6,7 @@ chunk_size=64; q,k,v ~ N(0,1) in bf16 with K L2-normalised per head; fp32
 master parameters; loss = mean(out.float()^2).  Inputs are resident in HBM
 before the timed region.
 
-    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu] [--no-decode]
 
 Prints ONE JSON line.  `value` is tokens/s of the whole job over the timed
 steps (independent scans overlap on side streams).  `roofline` is the dominant
@@ -15,8 +15,10 @@ kernel's achieved rate against the bf16 MFMA peak: algorithmic FLOP per launch
 extra step in which the schedule runs on one stream (no kernel overlaps
 another, so the interval is the kernel's own run time and agrees with a rocprof
 kernel trace of that step).  `step_roofline` is the whole step's algorithmic
-FLOP over the timed step time; `cpu_baseline` times the CPU oracle (the
-reference's per-token torch algorithm) on a bounded sample.
+FLOP over the timed step time; `decode` is the batched one-token decode rate
+(B=64 streams of the same layer) with its HBM roofline from the state bytes a
+token step must move; `cpu_baseline` times the CPU oracle (the reference's
+per-token torch algorithm) on a bounded sample.
 """
 from __future__ import annotations
 
@@ -64,6 +66,54 @@ def f_forward_per_token_head(dk: int, dv: int, slots, c: int) -> float:
     return total
 
 
+DECODE_BATCH = 64
+
+
+def decode_state_bytes(dk: int, dv: int, slots) -> int:
+    """HBM bytes one stream (b, h) must move per decoded token: every fp32
+    state read and written once (A_j [Dk,M_j] and B_j [M_j,Dv], R_ij [M_i,M_j],
+    counts [M_j]) and the block-start snapshots of A_j, B_j read once."""
+    s = sum(slots)
+    rel = sum(mi * mj for i, mi in enumerate(slots) for j, mj in enumerate(slots) if i != j)
+    return 4 * (3 * (dk * s + s * dv) + 2 * rel + 2 * s)
+
+
+def decode_rate(model, steps: int = 24, warmup: int = 8) -> dict:
+    """Batched one-token decode through the model's cache (chunk mode, T=1 per
+    call), B=64 streams of the same layer, bf16; the rate of the path that
+    serves it (the schedule's T=1 segments)."""
+    import torch
+    cfg = model.config
+    dev = next(model.parameters()).device
+    h, dk, dv = cfg.heads, cfg.key_dim, cfg.value_dim
+    gen = torch.Generator(device=dev).manual_seed(1)
+
+    def token():
+        q = torch.randn(DECODE_BATCH, 1, h, dk, device=dev, generator=gen).bfloat16()
+        k = torch.nn.functional.normalize(torch.randn(DECODE_BATCH, 1, h, dk, device=dev, generator=gen), dim=-1)
+        v = torch.randn(DECODE_BATCH, 1, h, dv, device=dev, generator=gen).bfloat16()
+        return q, k.bfloat16(), v
+
+    toks = [token() for _ in range(warmup + steps)]
+    with torch.no_grad():
+        state = model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)
+        for i in range(warmup):
+            _, state = model(*toks[i], state)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            _, state = model(*toks[i], state)
+        torch.cuda.synchronize()
+        seconds = (time.perf_counter() - start) / steps
+    moved = decode_state_bytes(dk, dv, cfg.slots) * DECODE_BATCH * h
+    gbs = moved / seconds / 1e9
+    return {"value": DECODE_BATCH / seconds, "unit": "tokens/s", "batch": DECODE_BATCH,
+            "ms_per_token_step": seconds * 1e3, "steps": steps,
+            "path": "schedule T=1 segments (the fused one-kernel step is switched off)",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
+
+
 def cpu_baseline(sample_tokens: int = 512) -> dict:
     """The oracle (per-token reference algorithm, fp32) timed on this host."""
     import torch
@@ -104,6 +154,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the batched decode measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build", file=sys.stderr)
@@ -175,6 +226,8 @@ def main() -> int:
         "step_roofline": {"bound": "mfma", "achieved": step_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                           "frac": step_tflops / PEAK_BF16_TFLOPS, "flop_per_step": flop_step},
     }
+    if not args.no_decode:
+        result["decode"] = decode_rate(model)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
