@@ -80,8 +80,9 @@ def decode_state_bytes(dk: int, dv: int, slots) -> int:
 
 def decode_rate(model, steps: int = 24, warmup: int = 8) -> dict:
     """Batched one-token decode through the model's cache (chunk mode, T=1 per
-    call), B=64 streams of the same layer, bf16; the rate of the path that
-    serves it (the schedule's T=1 segments)."""
+    call), B=64 streams of the same layer, bf16, under no_grad; the rate of
+    the path that serves it (the schedule's T=1 segments, whose recurrences
+    are one-token steps that read and write each state once)."""
     import torch
     cfg = model.config
     dev = next(model.parameters()).device
@@ -109,7 +110,8 @@ def decode_rate(model, steps: int = 24, warmup: int = 8) -> dict:
     gbs = moved / seconds / 1e9
     return {"value": DECODE_BATCH / seconds, "unit": "tokens/s", "batch": DECODE_BATCH,
             "ms_per_token_step": seconds * 1e3, "steps": steps,
-            "path": "schedule T=1 segments (the fused one-kernel step is switched off)",
+            "path": "schedule T=1 segments: one-token scan steps (gdn_token_step) and the block-snapshot "
+                    "level mix; the fused one-kernel step is switched off",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 

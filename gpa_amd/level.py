@@ -119,6 +119,41 @@ class _LevelMix(torch.autograd.Function):
         return dkey, dvalue_out, da, db, da_first, db_first, deta, None, None
 
 
+def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
+                    offset: int) -> tuple[Tensor, Tensor, Tensor]:
+    """`level_mix` of a call that stays inside one block (offset + T <= chunk)
+    whose snapshots A^ [B,H,Dk,M] and B^ [B,H,M,Dv] are given: the scans'
+    chunk-start states are not needed (inference decode); no autograd."""
+    _lib.require_device(key)
+    bsz, tokens, heads, dk = key.shape
+    if offset + tokens > chunk:
+        raise ValueError("level_mix_block: the call must stay inside one block")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (key, value, a_first, b_first, eta)):
+        raise RuntimeError("level_mix_block has no backward: call it under torch.no_grad() or inference_mode()")
+    lib = _lib.load()
+    dtype, dv, m = key.dtype, value.shape[-1], a_first.shape[-1]
+    key, value = key.contiguous(), value.contiguous()
+    (af, asb), (bf, bsb) = _snapshot(a_first), _snapshot(b_first)
+    eta = eta.detach().float().contiguous()
+    write = torch.empty(bsz, tokens, heads, m, device=key.device, dtype=dtype)
+    key_out, value_out = torch.empty_like(key), torch.empty_like(value)
+    rk, rv = torch.empty_like(key), torch.empty_like(value)
+    stats = torch.empty(bsz, tokens, heads, 2, device=key.device, dtype=torch.float32)
+    p = _lib.LevelProblem()
+    p.batch, p.tokens, p.heads, p.key_dim, p.value_dim = bsz, tokens, heads, dk, dv
+    p.slots, p.chunk, p.offset, p.dtype = m, chunk, offset, _lib.DTYPE_CODES[dtype]
+    p.key, p.value = _lib.operand(key), _lib.operand(value)
+    # One block, taken from the snapshots: the kernels read the start states
+    # only for later blocks, so the snapshots stand in for the (unused) pointers.
+    p.a_states, p.b_states = af.data_ptr(), bf.data_ptr()
+    p.a_first, p.a_first_sb, p.b_first, p.b_first_sb = af.data_ptr(), asb, bf.data_ptr(), bsb
+    p.eta = eta.data_ptr()
+    p.write, p.key_out, p.value_out = (_lib.operand(t) for t in (write, key_out, value_out))
+    p.rk, p.rv, p.stats = rk.data_ptr(), rv.data_ptr(), stats.data_ptr()
+    _lib.check(lib.gpa_level_forward(p, _lib.stream_handle(key.device)), "gpa_level_forward")
+    return write, key_out, value_out
+
+
 def level_mix(key: Tensor, value: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: Tensor | None,
               b_first: Tensor | None, eta: Tensor, chunk: int, offset: int):
     """(write, key', value') of one level.  key [B,T,H,Dk], value [B,T,H,Dv];

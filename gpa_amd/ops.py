@@ -274,6 +274,82 @@ def gdn_scan_deferred(k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor 
     return states_vk.transpose(-1, -2), final, read
 
 
+def token_step_supported(k: Tensor, v: Tensor) -> bool:
+    """Whether `gdn_token_hip` takes these keys/values: one token, float32 or
+    bfloat16, K and V up to 256, V a multiple of 4."""
+    return (k.dtype in _lib.DTYPE_CODES and k.ndim == 4 and k.shape[1] == 1 and k.shape[-1] <= 256
+            and v.shape[-1] <= 256 and v.shape[-1] % 4 == 0)
+
+
+def _token_state(s: Tensor) -> Tensor:
+    """A float32 [B,H,K,V] state the token kernel reads in 16-byte vectors."""
+    s = _f32_state(s)
+    if s.data_ptr() % 16 or s.stride(0) % 4 or s.stride(1) % 4:
+        s = s.contiguous()
+    return s
+
+
+def _no_autograd(name: str, *tensors) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise RuntimeError(f"{name} has no backward: call it under torch.no_grad() or inference_mode()")
+
+
+def gdn_token_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                  s0: Tensor | None) -> tuple[Tensor | None, Tensor]:
+    """One token of B*H GDN streams without autograd (inference decode):
+    `gdn_update` then `memory_read` of the reference (src/gpa/ops.py:29-46),
+    i.e. `gdn_scan_hip` at T = 1 without the intermediates a backward needs.
+    q (may be None), k [B,1,H,K], v [B,1,H,V], g/beta [B,1,H] (any strides),
+    s0 [B,H,K,V] or None = zeros.  Returns (out [B,1,H,V] or None, final
+    [B,H,K,V] float32).  Keys/values must pass `token_step_supported`."""
+    _lib.require_device(k)
+    if not token_step_supported(k, v) or v.dtype != k.dtype or (q is not None and q.dtype != k.dtype):
+        raise ValueError("gdn_token_hip: needs one float32/bfloat16 token, K, V <= 256 and V % 4 == 0")
+    if v.shape[:3] != k.shape[:3] or (q is not None and q.shape != k.shape):
+        raise ValueError("gdn_token_hip: expected q,k [B,1,H,K] and v [B,1,H,V]")
+    if g.shape != k.shape[:3] or beta.shape != k.shape[:3]:
+        raise ValueError("gdn_token_hip: g and beta must be [B,1,H]")
+    bsz, _, heads, kd = k.shape
+    vd = v.shape[-1]
+    if s0 is not None and s0.shape != (bsz, heads, kd, vd):
+        raise ValueError("gdn_token_hip: s0 must be [B,H,K,V]")
+    _no_autograd("gdn_token_hip", q, k, v, g, beta, s0)
+    lib = _lib.load()
+    q = _contig_last(q) if q is not None else None
+    k, v = _contig_last(k), _contig_last(v)
+    g, beta = g.float(), beta.float()
+    s0f = _token_state(s0) if s0 is not None else None
+    final = torch.empty(bsz, heads, kd, vd, device=k.device, dtype=torch.float32)
+    out = torch.empty(bsz, 1, heads, vd, device=k.device, dtype=k.dtype) if q is not None else None
+    prob = _problem(q, k, v, g, beta, s0f, 1, 0)
+    _lib.check(lib.gpa_gdn_token_step(prob, final.data_ptr(), _lib.operand(out), _lib.stream_handle(k.device)),
+               "gpa_gdn_token_step")
+    return out, final
+
+
+def gdn_token_read(q: Tensor, state: Tensor) -> Tensor:
+    """u(q)^T S of one token per stream (reference ops.py:45-46): q [B,1,H,K],
+    S [B,H,K,V] float32 -> [B,1,H,V] in q's dtype; no autograd."""
+    _lib.require_device(q)
+    bsz, tokens, heads, kd = q.shape
+    if tokens != 1 or state.shape != (bsz, heads, kd, state.shape[-1]):
+        raise ValueError("gdn_token_read: expected q [B,1,H,K] and S [B,H,K,V]")
+    if q.dtype not in _lib.DTYPE_CODES or kd > 256 or state.shape[-1] > 256 or state.shape[-1] % 4:
+        raise ValueError("gdn_token_read: needs float32/bfloat16, K, V <= 256 and V % 4 == 0")
+    _no_autograd("gdn_token_read", q, state)
+    lib = _lib.load()
+    q = _contig_last(q)
+    sf = _token_state(state)
+    vd = sf.shape[-1]
+    out = torch.empty(bsz, 1, heads, vd, device=q.device, dtype=q.dtype)
+    prob = _lib.Problem(bsz, heads, 1, 0, 1, kd, vd, _lib.DTYPE_CODES[q.dtype], _lib.operand(q), _lib.operand(None),
+                        _lib.operand(None), _lib.operand(None), _lib.operand(None), sf.data_ptr(), sf.stride(0),
+                        sf.stride(1))
+    _lib.check(lib.gpa_gdn_token_step(prob, None, _lib.operand(out), _lib.stream_handle(q.device)),
+               "gpa_gdn_token_step")
+    return out
+
+
 # --------------------------------------------------------------------------- reference-signature operators
 def _check_scan_args(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor) -> None:
     """The reference's argument checks and messages (src/gpa/ops.py:52-55)."""

@@ -29,13 +29,13 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib
-from .ops import gdn_scan_deferred, gdn_scan_hip
+from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_token_hip, gdn_token_read, token_step_supported
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
 from .slots import slot_gates
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
-from .level import level_mix
+from .level import level_mix, level_mix_block
 from .level import supported as fused_level_supported
 from .route import route_reader
 from .route import supported as fused_route_supported
@@ -163,6 +163,10 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     blocks = _Blocks(tokens, offset, chunk)
     frozen0 = state.frozen or tuple(ResidualSnapshot(lv.inner, lv.outer) for lv in state.levels)
     scan = dict(chunk=chunk, offset=offset)
+    # Inference on one token (decode): each recurrence is a single token step
+    # that reads and writes its state once, and the level mix reads the cached
+    # block snapshots, so no chunk-start states are kept.
+    token = _TOKEN_STEP[0] and tokens == 1 and not torch.is_grad_enabled()
 
     # ---- level pass (storage + inner reads), attention.py:309-329
     key, value = k, v
@@ -176,6 +180,21 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         else:
             slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
             g_in, b_in, g_out, b_out = _gates(model, key, j, control)
+        eta = 1 + .25 * model.residual_raw[j].tanh()
+        write = _assignment(cfg, slot)
+        fused_level = write is None and _FUSED_LEVEL[0] and fused_level_supported(
+            cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
+        if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
+            raw, a_final = gdn_token_hip(q, key, slot, g_in, b_in, old.inner)
+            b_final = gdn_token_hip(None, slot, value, g_out, b_out, old.outer)[1]
+            lv.b_read = lambda qo, s=b_final: gdn_token_read(qo, s)
+            write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
+            lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
+            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, None, None
+            _level_logits(model, lv, j, raw, old)
+            levels.append(lv)
+            key, value = key_next, value_next
+            continue
         # The outer read of this level (below) runs the B recurrence with the
         # same keys, values, gates and initial state: where the kernels allow,
         # the B scan keeps its intermediates for that read instead.
@@ -190,10 +209,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         # initial states unless the call starts inside a block.
         first_a = None if snap.inner is old.inner else snap.inner
         first_b = None if snap.outer is old.outer else snap.outer
-        eta = 1 + .25 * model.residual_raw[j].tanh()
-        write = _assignment(cfg, slot)
-        if write is None and _FUSED_LEVEL[0] and fused_level_supported(cfg, dtype, key.shape[-1], value.shape[-1],
-                                                                       slot.shape[-1]):
+        if fused_level:
             write, key_next, value_next = level_mix(key, value, a_starts.transpose(-1, -2),
                                                     b_starts.transpose(-1, -2), first_a, first_b, eta, chunk, offset)
         else:
@@ -201,21 +217,14 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                                                            eta, blocks, write)
         lv.slot, lv.value, lv.g_out, lv.b_out = slot, value, g_out, b_out
         lv.write = write
-        if _FUSED_COUNTS[0] and fused_counts_supported(cfg, raw.dtype, write.shape[-1]):
-            gain, scale = _count_scalars(model, j, raw)
-            lv.logits, lv.final_count = count_logits(raw, write, old.count, gain, scale)
-            lv.counts = None  # not needed past the logits on this path
-        else:
-            lv.counts = old.count[:, None] + _cumsum_tokens(write.float())
-            lv.final_count = lv.counts[:, -1]
-            lv.logits = _base_logits(model, raw, lv.counts, j)
+        _level_logits(model, lv, j, raw, old)
         lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, a_starts, b_starts
         levels.append(lv)
         key, value = key_next, value_next
 
     # ---- relations, attention.py:206-223
     local = [lv.logits.softmax(-1).to(dtype) for lv in levels]
-    incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan)
+    incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan, token)
 
     # ---- route reader, attention.py:225-262
     routes, queries = _bridge(model, q, [lv.logits for lv in levels], incoming, [lv.counts for lv in levels])
@@ -402,6 +411,7 @@ def _residual_eta(key, value, rk, rv, eta):
 
 _FUSED_LEVEL = [True]  # the fused level write and residual (level.py)
 _DEFER_OUTER_READ = [True]  # outer reads as late reads of the B scans (ops.gdn_scan_deferred)
+_TOKEN_STEP = [True]  # one-token inference calls as token steps (ops.gdn_token_hip)
 
 
 def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):
@@ -422,8 +432,23 @@ def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta
     return (write, *_residual_eta(key, value, rk, rv, eta))
 
 
-def _relations(model, local, writes, rel_states, scan):
-    """Every ordered edge's R_ij scan (attention.py:206-223)."""
+def _level_logits(model, lv, j: int, raw: Tensor, old: LevelState) -> None:
+    """Counts after every token and the level's base logits (attention.py:
+    319-323 and :165-175) into lv."""
+    cfg = model.config
+    if _FUSED_COUNTS[0] and fused_counts_supported(cfg, raw.dtype, lv.write.shape[-1]):
+        gain, scale = _count_scalars(model, j, raw)
+        lv.logits, lv.final_count = count_logits(raw, lv.write, old.count, gain, scale)
+        lv.counts = None  # not needed past the logits on this path
+    else:
+        lv.counts = old.count[:, None] + _cumsum_tokens(lv.write.float())
+        lv.final_count = lv.counts[:, -1]
+        lv.logits = _base_logits(model, raw, lv.counts, j)
+
+
+def _relations(model, local, writes, rel_states, scan, token=False):
+    """Every ordered edge's R_ij scan (attention.py:206-223); one token step
+    per edge when `token` (inference on one token)."""
     cfg = model.config
 
     def edge(e, i, j, old):
@@ -438,6 +463,8 @@ def _relations(model, local, writes, rel_states, scan):
                 norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
                 target = (target / norm[..., None]).to(target.dtype)
                 beta = (beta * norm.square()).clamp_max(.9)
+            if token and token_step_supported(writes[i], target):
+                return gdn_token_hip(local[i], writes[i], target, g, beta, old.memory)
             msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
             return msg, memory
         return run, (local[i], writes[i], writes[j], old.memory)

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 11
+#define GPA_HIP_ABI_VERSION 12
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -155,6 +155,18 @@ int gpa_gdn_read(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa
  * same problem (query set), saved (qn, qcol filled) and dout. */
 int gpa_gdn_read_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa_operand dout,
                           gpa_operand dq, hipStream_t stream);
+
+/* One token of every stream without saved intermediates (inference decode;
+ * problem->tokens must be 1, chunk and offset are not used):
+ *   final = a S0 + beta u(k) (v - u(k)^T a S0)^T with a = exp(g),
+ *   out   = u(q)^T final when q.ptr != NULL,
+ * final contiguous [batch,heads,K,V] float32.  With k.ptr == NULL the call
+ * only reads: out = u(q)^T S0 (v, g, beta and final unused; q and s0
+ * required).  Needs V a multiple of 4, K and V up to 256, s0 and final 16-byte
+ * aligned with s0 strides a multiple of 4.  Replaces reference
+ * src/gpa/ops.py:29-46 (gdn_update, memory_read), the scan at T = 1 of
+ * ops.py:49-85 without the intermediates a backward would need. */
+int gpa_gdn_token_step(const gpa_gdn_problem *problem, float *final_state, gpa_operand out, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Batched single-token decode step of the whole DenseGPA core (the reference's

@@ -1,0 +1,124 @@
+"""One-token inference steps (gpa_amd/ops.py gdn_token_hip / gdn_token_read,
+csrc/gdn_token.hip) and the decode path of the schedule that uses them.
+
+Operators: against the oracle's gdn_step then gdn_read (reference
+src/gpa/ops.py:29-46) on the CPU, for float32 (relative L2 1e-5) and bfloat16
+(2e-2), several widths (K not a multiple of 16, K = V = 256), no initial state,
+a batch-broadcast initial state (stride 0) and calls without a query.
+Module: DenseGPA one-token calls from a fresh cache across block boundaries
+(offsets 0..3 of a 4-token block) at C3 widths, against the oracle (1e-4 in
+float32, 2e-2 in bfloat16) and against the chunked-scan path of the same
+schedule: output and every cache tensor.
+"""
+import copy
+
+import pytest
+import torch
+
+import oracle
+from oracle import reference as ref
+from gpa_amd import DenseGPA, GPAConfig, schedule
+from gpa_amd.ops import gdn_token_hip, gdn_token_read
+from gpa_amd.state import tensors
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / max(b.norm().item(), 1e-30)).item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("b,h,k,v,s0,query", [(3, 2, 128, 128, "full", True), (2, 3, 64, 96, "broadcast", True),
+                                              (1, 2, 256, 256, "full", True), (2, 1, 20, 12, None, True),
+                                              (2, 2, 128, 256, "full", False), (1, 1, 200, 4, "broadcast", True)])
+def test_token_step_matches_reference_step_and_read(b, h, k, v, s0, query, dtype):
+    g = torch.Generator().manual_seed(b * 100 + k + v)
+    q = torch.randn(b, 1, h, k, generator=g).to(dtype)
+    key = torch.randn(b, 1, h, k, generator=g).to(dtype)
+    val = torch.randn(b, 1, h, v, generator=g).to(dtype)
+    lg = -torch.rand(b, 1, h, generator=g)
+    beta = torch.rand(b, 1, h, generator=g)
+    if s0 == "full":
+        state = torch.randn(b, h, k, v, generator=g) * .2
+    elif s0 == "broadcast":
+        state = (torch.randn(1, h, k, v, generator=g) * .2).expand(b, h, k, v)
+    else:
+        state = None
+    with torch.no_grad():
+        out, final = gdn_token_hip(q.to(DEV) if query else None, key.to(DEV), val.to(DEV), lg.to(DEV),
+                                   beta.to(DEV), state.to(DEV) if state is not None else None)
+    s_ref = ref.gdn_step(state if state is not None else torch.zeros(b, h, k, v), key[:, 0], val[:, 0],
+                         lg[:, 0], beta[:, 0])
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert final.dtype == torch.float32 and final.shape == (b, h, k, v)
+    assert _rel(final, s_ref) < tol
+    if query:
+        o_ref = ref.gdn_read(q[:, 0], s_ref)
+        assert out.dtype == dtype and out.shape == (b, 1, h, v)
+        assert _rel(out[:, 0], o_ref) < tol
+    else:
+        assert out is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_token_read_matches_reference_read(dtype):
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(2, 1, 3, 96, generator=g).to(dtype)
+    state = torch.randn(2, 3, 96, 64, generator=g)
+    with torch.no_grad():
+        out = gdn_token_read(q.to(DEV), state.to(DEV))
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert out.dtype == dtype and _rel(out[:, 0], ref.gdn_read(q[:, 0], state)) < tol
+
+
+def test_token_step_refuses_autograd():
+    k = torch.randn(1, 1, 1, 8, device=DEV, requires_grad=True)
+    v = torch.randn(1, 1, 1, 8, device=DEV)
+    g, beta = torch.zeros(1, 1, 1, device=DEV), torch.ones(1, 1, 1, device=DEV)
+    with pytest.raises(RuntimeError, match="no backward"):
+        gdn_token_hip(None, k, v, g, beta, None)
+
+
+C3 = dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_decode_token_steps_match_oracle_and_chunk_path(dtype, monkeypatch):
+    torch.manual_seed(21)
+    model = DenseGPA(GPAConfig(**C3))
+    oracle_run = oracle.OracleRun(copy.deepcopy(model))
+    hip = model.to(DEV)
+    b, steps = 2, 7
+    g = torch.Generator().manual_seed(5)
+    toks = []
+    for _ in range(steps):
+        q = torch.randn(b, 1, 2, 128, generator=g)
+        k = torch.nn.functional.normalize(torch.randn(b, 1, 2, 128, generator=g), dim=-1)
+        toks.append((q.to(dtype), k.to(dtype), torch.randn(b, 1, 2, 128, generator=g).to(dtype)))
+
+    def decode(token_path):
+        monkeypatch.setattr(schedule, "_TOKEN_STEP", [token_path])
+        outs, state = [], None
+        with torch.no_grad():
+            for x in toks:
+                y, state = hip(*(t.to(DEV) for t in x), state)
+                outs.append(y)
+        return torch.cat(outs, 1), state
+
+    y_tok, s_tok = decode(True)
+    y_chunk, s_chunk = decode(False)
+    ref_outs, ref_state = [], None
+    with torch.no_grad():
+        for x in toks:
+            y, ref_state = oracle_run(*x, ref_state)
+            ref_outs.append(y)
+    y_ref = torch.cat(ref_outs, 1)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert y_tok.dtype == dtype and _rel(y_tok, y_ref) < tol
+    assert _rel(y_tok, y_chunk) < tol
+    assert s_tok.chunk_offset == ref_state.chunk_offset == steps % 4
+    for a, r, c in zip(tensors(s_tok), tensors(ref_state), tensors(s_chunk)):
+        assert _rel(a, r) < tol and _rel(a, c) < tol

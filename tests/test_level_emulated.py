@@ -106,3 +106,25 @@ def test_host_built_level_mix_matches_device_glue(name, dtype, runner, tmp_path,
     print(name, dtype, "worst", worst)
     bad = {k: v for k, v in errors.items() if v > tol}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("first", ["full", "broadcast"])
+def test_host_built_level_mix_block_matches_level_mix(first, runner, tmp_path, monkeypatch):
+    """One token inside a block (the inference decode call): `level_mix_block`,
+    which passes no start states, gives exactly what `level_mix` gives with
+    start states and the same block-0 snapshots, and reads nothing else."""
+    b, h, dk, dv, m, c, off = 3, 2, 16, 8, 12, 4, 2
+    g = torch.Generator().manual_seed(5)
+    key = torch.randn(b, 1, h, dk, generator=g).to(torch.bfloat16)
+    value = torch.randn(b, 1, h, dv, generator=g).to(torch.bfloat16)
+    a_vm, b_vm = torch.randn(b, h, 1, m, dk, generator=g), torch.randn(b, h, 1, dv, m, generator=g)
+    lead = (b,) if first == "full" else (1,)
+    fa = (torch.randn(*lead, h, dk, m, generator=g) * .3).expand(b, h, dk, m)
+    fb = (torch.randn(*lead, h, m, dv, generator=g) * .3).expand(b, h, m, dv)
+    eta = 1 + .25 * torch.randn(h, 2, generator=g).tanh()
+    harness.use_host(monkeypatch, harness.HostLib(runner, str(tmp_path)))
+    with torch.no_grad():
+        ref = level.level_mix(key, value, a_vm, b_vm, fa, fb, eta, c, off)
+        got = level.level_mix_block(key, value, fa, fb, eta, c, off)
+    for a, r in zip(got, ref):
+        assert torch.equal(a, r)
