@@ -78,12 +78,17 @@ def decode_state_bytes(dk: int, dv: int, slots) -> int:
     return 4 * (3 * (dk * s + s * dv) + 2 * rel + 2 * s)
 
 
-def decode_rate(model, steps: int = 24, warmup: int = 8) -> dict:
+def decode_rate(model, steps: int = 64, warmup: int = 8) -> dict:
     """Batched one-token decode through the model's cache (chunk mode, T=1 per
-    call), B=64 streams of the same layer, bf16, under no_grad; the rate of
-    the path that serves it (the schedule's T=1 segments, whose recurrences
-    are one-token steps that read and write each state once)."""
+    call), B=64 streams of the same layer, bf16, under no_grad, on the path
+    that serves it: the schedule's T=1 segments (one-token steps that read
+    and write each state once), replayed from one HIP graph per block
+    position (`DecodeGraph`).  The timed steps span a whole block, so the
+    once-per-block state copy of the graph cycle is included.  The eager
+    rate of the same steps is reported beside it."""
     import torch
+
+    from gpa_amd import DecodeGraph
     cfg = model.config
     dev = next(model.parameters()).device
     h, dk, dv = cfg.heads, cfg.key_dim, cfg.value_dim
@@ -96,22 +101,32 @@ def decode_rate(model, steps: int = 24, warmup: int = 8) -> dict:
         return q, k.bfloat16(), v
 
     toks = [token() for _ in range(warmup + steps)]
-    with torch.no_grad():
-        state = model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)
+
+    def timed(run):
         for i in range(warmup):
-            _, state = model(*toks[i], state)
+            run(toks[i])
         torch.cuda.synchronize()
         start = time.perf_counter()
         for i in range(warmup, warmup + steps):
-            _, state = model(*toks[i], state)
+            run(toks[i])
         torch.cuda.synchronize()
-        seconds = (time.perf_counter() - start) / steps
+        return (time.perf_counter() - start) / steps
+
+    with torch.no_grad():
+        box = [model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)]
+
+        def eager(x):
+            _, box[0] = model(*x, box[0])
+        eager_s = timed(eager)
+        graphed = DecodeGraph(model, model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16), *toks[0])
+        seconds = timed(lambda x: graphed.step(*x))
+        del graphed
     moved = decode_state_bytes(dk, dv, cfg.slots) * DECODE_BATCH * h
     gbs = moved / seconds / 1e9
     return {"value": DECODE_BATCH / seconds, "unit": "tokens/s", "batch": DECODE_BATCH,
-            "ms_per_token_step": seconds * 1e3, "steps": steps,
-            "path": "schedule T=1 segments: one-token scan steps (gdn_token_step) and the block-snapshot "
-                    "level mix; the fused one-kernel step is switched off",
+            "ms_per_token_step": seconds * 1e3, "eager_ms_per_token_step": eager_s * 1e3, "steps": steps,
+            "path": "schedule T=1 segments (one-token scan steps gdn_token_step, block-snapshot level mix) "
+                    "replayed from one HIP graph per block position; the fused one-kernel step is switched off",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 

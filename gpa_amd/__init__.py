@@ -6,11 +6,11 @@ hand-written HIP library `libgpa_hip.so` (C ABI declared in include/gpa_hip.h)
 driven from PyTorch-ROCm; there is no CPU or eager fallback.
 """
 from .config import GPAConfig
-from .graph import GradientGraph
+from .graph import DecodeGraph, GradientGraph
 from .module import DenseGPA, QuadraticFeatures
 from .ops import TwoStageState, two_stage_gdn
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 
 __all__ = ["DenseGPA", "GPAConfig", "GPAState", "LevelState", "RelationState", "ResidualSnapshot",
-           "TwoStageState", "two_stage_gdn", "GradientGraph", "QuadraticFeatures"]
+           "TwoStageState", "two_stage_gdn", "GradientGraph", "DecodeGraph", "QuadraticFeatures"]
 __version__ = "0.1.0"

@@ -47,3 +47,86 @@ class GradientGraph:
                 static.copy_(value)
         self.graph.replay()
         return self.loss, self.output
+
+
+class DecodeGraph:
+    """One-token decode of a fixed batch on HIP graphs (inference, no autograd).
+
+    A one-token call of the chunk model depends on its position in the block
+    (which snapshots it reads, the offset it carries), so there is one graph
+    per position: `chunk_size` graphs, captured in the order they replay and
+    sharing one memory pool.  Each graph's output state lives in pool memory
+    that a later graph of the same block reuses once the state has been read,
+    so the graphs hold about two states, not one per position.
+
+    The cache must start at a block boundary (chunk_offset 0).  Its tensors
+    are copied into static buffers that the first graph reads and that every
+    later graph of the block reads as the block snapshots; after the last
+    position of a block the new cache is copied back into them (one state
+    copy per block).
+
+    `step(q, k, v)` ([B,1,H,D] like the captured token) copies the token into
+    the static inputs, replays the graph of the current position and returns
+    that graph's output buffer, which holds until the same position replays
+    `chunk_size` steps later.  `state` is the cache after the last step, at a
+    block boundary (its tensors are the static buffers: clone to keep them).
+    """
+
+    def __init__(self, model, state, q, k, v, warmups: int = 2):
+        if state.chunk_offset != 0:
+            raise ValueError("DecodeGraph: the cache must start at a block boundary (chunk_offset 0)")
+        if q.shape[1] != 1:
+            raise ValueError("DecodeGraph: one token per call")
+        from .state import _apply, tensors
+        self._tensors = tensors
+        self.chunk = state.chunk_size
+        self.position = state.position
+        self.offset = 0
+        self.inputs = tuple(x.detach().clone() for x in (q, k, v))
+        self.start = _apply(state, lambda t: t.detach().clone(memory_format=torch.contiguous_format))
+        current = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(current)
+        with torch.no_grad(), torch.cuda.stream(side):
+            s = self.start
+            for _ in range(warmups):
+                _, s = model(*self.inputs, s)
+        current.wait_stream(side)
+        del s
+        self.pool = torch.cuda.graph_pool_handle()
+        self.graphs, self.outputs = [], []
+        s = self.start
+        with torch.no_grad():
+            for _ in range(self.chunk):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=self.pool):
+                    out, s = model(*self.inputs, s)
+                self.graphs.append(graph)
+                self.outputs.append(out)
+        self.last = s  # the cache after a whole block
+        pairs = list(zip(tensors(self.start), tensors(self.last)))
+        if s.chunk_offset != 0 or len(pairs) != len(list(tensors(self.start))) or any(
+                a.shape != b.shape for a, b in pairs):
+            raise RuntimeError("DecodeGraph: the cache after a block does not match the cache it started from")
+
+    def step(self, q, k, v):
+        for static, value in zip(self.inputs, (q, k, v)):
+            if static.shape != value.shape or static.dtype != value.dtype:
+                raise ValueError("DecodeGraph replays only the captured token shape/dtype")
+            static.copy_(value)
+        o = self.offset
+        self.graphs[o].replay()
+        self.offset = (o + 1) % self.chunk
+        self.position += 1
+        if self.offset == 0:
+            with torch.no_grad():
+                for dst, src in zip(self._tensors(self.start), self._tensors(self.last)):
+                    dst.copy_(src)
+        return self.outputs[o]
+
+    @property
+    def state(self):
+        if self.offset != 0:
+            raise RuntimeError("DecodeGraph.state is available at block boundaries")
+        import dataclasses
+        return dataclasses.replace(self.start, position=self.position)

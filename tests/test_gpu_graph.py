@@ -62,3 +62,37 @@ def test_captured_step_replays_match_eager(dtype):
             assert err < tol, (seed, n, err)
         for a, b in zip(got_in, ex):
             assert _rel(a, b.grad) < tol, seed
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_decode_graph_matches_eager_decode(dtype):
+    """DecodeGraph: one graph per block position; three blocks of one-token
+    steps (every graph replays three times, with the block-boundary state copy
+    and eager checks in between) give the eager decode's outputs and cache."""
+    from gpa_amd.graph import DecodeGraph
+    from gpa_amd.state import tensors
+    torch.manual_seed(3)
+    cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=4)
+    model = DenseGPA(cfg).to(DEV)
+    b = 3
+    g = torch.Generator(device=DEV).manual_seed(9)
+
+    def token():
+        q = torch.randn(b, 1, 2, 32, device=DEV, generator=g).to(dtype)
+        k = torch.nn.functional.normalize(torch.randn(b, 1, 2, 32, device=DEV, generator=g), dim=-1).to(dtype)
+        return q, k, torch.randn(b, 1, 2, 48, device=DEV, generator=g).to(dtype)
+
+    toks = [token() for _ in range(12)]
+    with torch.no_grad():
+        state = model.initial_state(b, device=DEV, dtype=dtype)
+        graphed = DecodeGraph(model, state, *toks[0])
+        for i, x in enumerate(toks):
+            y_graph = graphed.step(*x).clone()
+            torch.cuda.synchronize()
+            y_eager, state = model(*x, state)
+            assert _rel(y_graph, y_eager) < 1e-6, i
+            if (i + 1) % cfg.chunk_size == 0:
+                got = graphed.state
+                assert got.position == state.position == i + 1
+                for a, r in zip(tensors(got), tensors(state)):
+                    assert _rel(a, r) < 1e-6, i
