@@ -450,14 +450,17 @@ def _relations(model, local, writes, rel_states, scan, token=False):
     """Every ordered edge's R_ij scan (attention.py:206-223); one token step
     per edge when `token` (inference on one token)."""
     cfg = model.config
+    # Every edge's decay and write strength [E,H], in three launches.
+    decay = -F.softplus(model.relation_decay_raw)
+    if cfg.positional_mode == "none":
+        decay = decay * 0
+    strength = model.relation_beta_raw.sigmoid()
 
     def edge(e, i, j, old):
         def run():
             lead = writes[i].shape[:-1]
-            g = (-F.softplus(model.relation_decay_raw[e])).expand(lead)
-            if cfg.positional_mode == "none":
-                g = g * 0
-            beta = model.relation_beta_raw[e].sigmoid().expand(lead)
+            g = decay[e].expand(lead)
+            beta = strength[e].expand(lead)
             target = writes[j]
             if cfg.rsa_update:
                 norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
@@ -467,7 +470,7 @@ def _relations(model, local, writes, rel_states, scan, token=False):
                 return gdn_token_hip(local[i], writes[i], target, g, beta, old.memory)
             msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
             return msg, memory
-        return run, (local[i], writes[i], writes[j], old.memory)
+        return run, (local[i], writes[i], writes[j], old.memory, decay, strength)
 
     done = _concurrent([edge(e, i, j, old) for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))])
     incoming = [[] for _ in local]
