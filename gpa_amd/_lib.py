@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -146,6 +146,7 @@ EXPORTS = {
     "gpa_gdn_read": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, c_vp], ctypes.c_int),
     "gpa_gdn_read_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, Operand, c_vp],
                               ctypes.c_int),
+    "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
     "gpa_gdn_token_step": ([ctypes.POINTER(Problem), c_vp, Operand, c_vp], ctypes.c_int),
     "gpa_decode_step": ([ctypes.POINTER(DecodeProblem), c_vp], ctypes.c_int),
     "gpa_route_forward": ([ctypes.POINTER(RouteProblem), c_vp], ctypes.c_int),

@@ -150,8 +150,14 @@ def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor
     p.eta = eta.data_ptr()
     p.write, p.key_out, p.value_out = (_lib.operand(t) for t in (write, key_out, value_out))
     p.rk, p.rv, p.stats = rk.data_ptr(), rv.data_ptr(), stats.data_ptr()
-    _lib.check(lib.gpa_level_forward(p, _lib.stream_handle(key.device)), "gpa_level_forward")
+    if tokens == 1 and _TOKEN_KERNEL[0]:
+        _lib.check(lib.gpa_level_token_forward(p, _lib.stream_handle(key.device)), "gpa_level_token_forward")
+    else:
+        _lib.check(lib.gpa_level_forward(p, _lib.stream_handle(key.device)), "gpa_level_forward")
     return write, key_out, value_out
+
+
+_TOKEN_KERNEL = [True]  # one-token calls of level_mix_block on gpa_level_token_forward
 
 
 def level_mix(key: Tensor, value: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: Tensor | None,

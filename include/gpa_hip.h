@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 12
+#define GPA_HIP_ABI_VERSION 13
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -320,6 +320,14 @@ typedef struct gpa_level_grads {
  * glue at attention.py:314-329, autograd through it for the backward). */
 int gpa_level_forward(const gpa_level_problem *problem, hipStream_t stream);
 int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *grads, hipStream_t stream);
+
+/* The level write and residual of ONE token of every stream (inference
+ * decode; problem->tokens must be 1) from the block snapshots a_first and
+ * b_first, which are required (a_states, b_states, rk, rv and stats are not
+ * used): write = softmax(u(key) A^) rounded to the activation type,
+ * key_out = key - eta0 round(A^ write), value_out = value - eta1 round(write^T B^).
+ * Replaces reference src/gpa/attention.py:314-329 and :190-194 at T = 1. */
+int gpa_level_token_forward(const gpa_level_problem *problem, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Slot counts and base logits of one level (reference attention.py:196-204,

@@ -122,3 +122,28 @@ def test_decode_token_steps_match_oracle_and_chunk_path(dtype, monkeypatch):
     assert s_tok.chunk_offset == ref_state.chunk_offset == steps % 4
     for a, r, c in zip(tensors(s_tok), tensors(ref_state), tensors(s_chunk)):
         assert _rel(a, r) < tol and _rel(a, c) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("b,h,dk,dv,m,first", [(3, 2, 128, 128, 128, "full"), (2, 2, 128, 128, 256, "broadcast"),
+                                               (2, 1, 20, 8, 12, "full"), (1, 3, 256, 96, 64, "broadcast")])
+def test_level_token_kernel_matches_block_kernel(b, h, dk, dv, m, first, dtype, monkeypatch):
+    """gpa_level_token_forward (one token from the block snapshots) against the
+    block kernel gpa_level_forward on the same call: write, key', value'."""
+    from gpa_amd import level
+    g = torch.Generator().manual_seed(b + dk + m)
+    key = torch.randn(b, 1, h, dk, generator=g).to(dtype).to(DEV)
+    value = torch.randn(b, 1, h, dv, generator=g).to(dtype).to(DEV)
+    lead = b if first == "full" else 1
+    fa = (torch.randn(lead, h, dk, m, generator=g) * .3).to(DEV).expand(b, h, dk, m)
+    fb = (torch.randn(lead, h, m, dv, generator=g) * .3).to(DEV).expand(b, h, m, dv)
+    eta = (1 + .25 * torch.randn(h, 2, generator=g).tanh()).to(DEV)
+    outs = {}
+    for token_kernel in (True, False):
+        monkeypatch.setattr(level, "_TOKEN_KERNEL", [token_kernel])
+        with torch.no_grad():
+            outs[token_kernel] = level.level_mix_block(key, value, fa, fb, eta, 4, 2)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for name, a, r in zip(("write", "key'", "value'"), outs[True], outs[False]):
+        assert a.dtype == r.dtype == dtype and a.shape == r.shape, name
+        assert _rel(a, r) < tol, (name, _rel(a, r))
