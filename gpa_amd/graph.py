@@ -67,9 +67,13 @@ class DecodeGraph:
 
     `step(q, k, v)` ([B,1,H,D] like the captured token) copies the token into
     the static inputs, replays the graph of the current position and returns
-    that graph's output buffer, which holds until the same position replays
-    `chunk_size` steps later.  `state` is the cache after the last step, at a
-    block boundary (its tensors are the static buffers: clone to keep them).
+    that position's output buffer.  The buffers are allocated outside the
+    graphs' pool (each graph ends by copying its output into its own buffer),
+    because the pool memory of one graph's output is free space to the graphs
+    captured before it and is overwritten when they replay.  An output buffer
+    holds until the same position replays `chunk_size` steps later.  `state`
+    is the cache after the last step, at a block boundary (its tensors are the
+    static buffers: clone to keep them).
     """
 
     def __init__(self, model, state, q, k, v, warmups: int = 2):
@@ -94,15 +98,18 @@ class DecodeGraph:
         current.wait_stream(side)
         del s
         self.pool = torch.cuda.graph_pool_handle()
-        self.graphs, self.outputs = [], []
+        self.graphs = []
+        # One output buffer per position, from the ordinary allocator.
+        self.outputs = [torch.empty_like(self.inputs[2]) for _ in range(self.chunk)]
         s = self.start
         with torch.no_grad():
-            for _ in range(self.chunk):
+            for o in range(self.chunk):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=self.pool):
                     out, s = model(*self.inputs, s)
+                    self.outputs[o].copy_(out)
+                del out
                 self.graphs.append(graph)
-                self.outputs.append(out)
         self.last = s  # the cache after a whole block
         pairs = list(zip(tensors(self.start), tensors(self.last)))
         if s.chunk_offset != 0 or len(pairs) != len(list(tensors(self.start))) or any(

@@ -153,15 +153,19 @@ class OracleRun:
         self.edges = cfg_edges(self.cfg)
 
     # -- level glue ---------------------------------------------------------
-    def gates(self, key, j, control):
-        """(g_in, beta_in, g_out, beta_out), each [B,T,H] (attention.py:161-174)."""
+    def gate_inputs(self, key, j, control):
+        """The gate product before its bias, [B,T,H,4] in the activation type
+        (attention.py:162-165)."""
         cfg, w = self.cfg, self.p.gate_weight[j]
         if cfg.control_dim:
-            raw = torch.einsum("...d,hdc->...hc", control, w.to(control.dtype))
-        else:
-            src = key if cfg.rsa_update else unit(key)
-            raw = torch.einsum("...hd,hdc->...hc", src, w.to(key.dtype))
-        raw = raw.to(_work(key)) + self.p.gate_bias[j]
+            return torch.einsum("...d,hdc->...hc", control, w.to(control.dtype))
+        src = key if cfg.rsa_update else unit(key)
+        return torch.einsum("...hd,hdc->...hc", src, w.to(key.dtype))
+
+    def gates(self, key, j, control):
+        """(g_in, beta_in, g_out, beta_out), each [B,T,H] (attention.py:161-174)."""
+        cfg = self.cfg
+        raw = self.gate_inputs(key, j, control).to(_work(key)) + self.p.gate_bias[j]
         g_in, b_in, g_out, b_out = raw.unbind(-1)
         g_in = -F.softplus(g_in).clamp(max=10.)
         g_out = -F.softplus(g_out).clamp(max=10.)
@@ -197,6 +201,11 @@ class OracleRun:
         new_key = (key - eta[:, 0, None] * rk.to(key.dtype)).to(key.dtype)
         new_value = (value - eta[:, 1, None] * rv.to(value.dtype)).to(value.dtype)
         return new_key, new_value
+
+    @staticmethod
+    def counts(count0, write):
+        """Soft slot counts after every token, n0 + cumsum_t(write) (attention.py:316)."""
+        return count0[:, None] + write.to(count0.dtype).cumsum(1)
 
     def base_logits(self, raw, count, moment, j):
         """read_scale*raw + softplus(c_j) log1p(n) [+ moment term] (attention.py:196-204)."""
@@ -338,7 +347,7 @@ class OracleRun:
             if write is None:
                 write = torch.einsum("bthd,bhdm->bthm", unit(key).to(snap.inner.dtype), snap.inner).softmax(-1)
             write = write.to(q.dtype)
-            counts = old.count[:, None] + write.to(old.count.dtype).cumsum(1)
+            counts = self.counts(old.count, write)
             history.append(counts)
             moment, correction = old.position, None
             if moment is not None:

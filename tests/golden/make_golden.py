@@ -173,13 +173,66 @@ CASES = {
 }
 
 
+def run_two_stage(name, *, seed, batch, length, heads, key_dim, slots, value_dim, dtype, weights=True):
+    """The reference's two_stage_gdn (ops.py:146-163) on seeded inputs: output,
+    both final states and the gradient of every input of out.square().mean()."""
+    from gpa import TwoStageState, two_stage_gdn
+    g = torch.Generator().manual_seed(seed)
+    b, t, h, dk, m, dv = batch, length, heads, key_dim, slots, value_dim
+    raw = {"q": torch.randn(b, t, h, dk, generator=g, dtype=torch.float64),
+           "k": torch.randn(b, t, h, dk, generator=g, dtype=torch.float64),
+           "slots": torch.randn(b, t, h, m, generator=g, dtype=torch.float64),
+           "v": torch.randn(b, t, h, dv, generator=g, dtype=torch.float64),
+           "gi": -torch.rand(b, t, h, generator=g, dtype=torch.float64) * .3,
+           "bi": torch.rand(b, t, h, generator=g, dtype=torch.float64),
+           "go": -torch.rand(b, t, h, generator=g, dtype=torch.float64) * .3,
+           "bo": torch.rand(b, t, h, generator=g, dtype=torch.float64),
+           "inner": torch.randn(b, h, dk, m, generator=g, dtype=torch.float64) * .1,
+           "outer": torch.randn(b, h, m, dv, generator=g, dtype=torch.float64) * .1}
+    if weights:
+        raw["route_weight"] = torch.randn(m, m, generator=g, dtype=torch.float64) / m ** .5
+        raw["query_weight"] = torch.randn(m, dk, generator=g, dtype=torch.float64) / dk ** .5
+    act = ("q", "k", "slots", "v")
+    work = torch.float64 if dtype == torch.float64 else torch.float32
+    x = {n: t_.to(dtype if n in act else work).requires_grad_() for n, t_ in raw.items()}
+    state = TwoStageState(x["inner"], x["outer"])
+    out, new = two_stage_gdn(x["q"], x["k"], x["slots"], x["v"], x["gi"], x["bi"], x["go"], x["bo"], state,
+                             route_weight=x.get("route_weight"), query_weight=x.get("query_weight"))
+    out.float().square().mean().backward()
+    store = {"dtype": np.array(str(dtype).replace("torch.", ""))}
+    for n, t_ in x.items():
+        store["in/" + n] = t_.detach().float().numpy() if t_.dtype == torch.bfloat16 else t_.detach().numpy()
+        store["grad/" + n] = (t_.grad.float() if t_.grad.dtype == torch.bfloat16 else t_.grad).numpy()
+    store["out"] = out.detach().float().numpy() if out.dtype == torch.bfloat16 else out.detach().numpy()
+    store["inner"] = new.inner.detach().numpy()
+    store["outer"] = new.outer.detach().numpy()
+    np.savez_compressed(os.path.join(HERE, name + ".npz"), **store)
+    print(name, "arrays:", len(store), flush=True)
+
+
+# Operator-level fixtures (names start with "ops_"; not DenseGPA cases).
+OPS_CASES = {
+    "ops_two_stage_fp64": dict(seed=21, batch=2, length=37, heads=2, key_dim=8, slots=6, value_dim=5,
+                               dtype=torch.float64),
+    "ops_two_stage_fp32": dict(seed=22, batch=1, length=70, heads=2, key_dim=16, slots=12, value_dim=10,
+                               dtype=torch.float32),
+    "ops_two_stage_plain_fp32": dict(seed=23, batch=2, length=20, heads=3, key_dim=8, slots=5, value_dim=7,
+                                     dtype=torch.float32, weights=False),
+    "ops_two_stage_bf16": dict(seed=24, batch=1, length=70, heads=2, key_dim=16, slots=12, value_dim=10,
+                               dtype=torch.bfloat16),
+}
+
+
 def main(names):
     if not os.path.isdir(REFERENCE):
         raise SystemExit("reference package not found; golden vectors are written in the build container")
     sys.path.insert(0, REFERENCE)
     torch.set_num_threads(min(8, os.cpu_count() or 1))
-    for name in names or CASES:
-        run_case(name, **CASES[name])
+    for name in names or [*CASES, *OPS_CASES]:
+        if name in OPS_CASES:
+            run_two_stage(name, **OPS_CASES[name])
+        else:
+            run_case(name, **CASES[name])
 
 
 if __name__ == "__main__":

@@ -22,7 +22,38 @@ DTYPES = {"float32": torch.float32, "float64": torch.float64, "bfloat16": torch.
 
 
 def names():
-    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+    """The DenseGPA fixtures (operator fixtures start with "ops_")."""
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith("ops_"))
+
+
+def ops_names(prefix: str):
+    """The operator fixtures whose names start with `prefix` (e.g. "ops_two_stage")."""
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and f.startswith(prefix))
+
+
+class TwoStageCase:
+    """A two_stage_gdn fixture (reference src/gpa/ops.py:146-163): inputs, output,
+    final states and the input gradients of out.square().mean()."""
+
+    ACT = ("q", "k", "slots", "v")
+    ORDER = ("q", "k", "slots", "v", "gi", "bi", "go", "bo", "inner", "outer", "route_weight", "query_weight")
+
+    def __init__(self, name: str):
+        self.name = name
+        with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+            self.z = {k: z[k] for k in z.files}
+        self.dtype = DTYPES[str(self.z["dtype"])]
+
+    def inputs(self, dtype=None):
+        """Input tensors by name, activations in `dtype` (default: the fixture's),
+        the rest in its work type (float64 for a float64 case, else float32)."""
+        dtype = dtype or self.dtype
+        work = torch.float64 if dtype == torch.float64 else torch.float32
+        return {n: torch.from_numpy(self.z["in/" + n]).to(dtype if n in self.ACT else work)
+                for n in self.ORDER if "in/" + n in self.z}
+
+    def ref(self, name: str) -> torch.Tensor:
+        return torch.from_numpy(self.z[name]).double()
 
 
 class Case:

@@ -60,6 +60,8 @@ CONFIGS = {
                                    slot_feature="softmax"), b=2, t=5),
     "c2_dims": dict(cfg=dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=64),
                     b=1, t=130),
+    "c2_dims_b8": dict(cfg=dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=64),
+                       b=8, t=130),
     "c3_dims": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64),
                     b=1, t=130, normalize_k=True),
     # the tokenwise model (chunk_size 1)
@@ -92,7 +94,8 @@ def _run_both(name, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
-    if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "tiny_unequal_c3", "lm_flags", "tokenwise"):
+    if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "c2_dims_b8", "tiny_unequal_c3", "lm_flags",
+                                                "tokenwise"):
         pytest.skip("bf16 covered on the configuration-shaped cases")
     tol = TOL[dtype]
     (hm, xs, c_hip, out, state), (rm, rs, c_ref, ref_out, ref_state) = _run_both(name, dtype)
@@ -117,23 +120,33 @@ def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("name", ["tiny_unequal_c3", "c2_dims", "tokenwise"])
+@pytest.mark.parametrize("name", ["tiny_unequal_c3", "tiny_none_c4", "lm_flags", "c2_dims", "c3_dims",
+                                  "tokenwise"])
 def test_cached_partitions_and_decode_match_oracle(name):
+    """Cached calls cut at block-unaligned points, then three one-token decode
+    calls (the T = 1 inference path: one-token scan steps, the one-token level
+    kernel and the relation token steps, with the configuration's flags and
+    control input), against the oracle's cached calls, in float32."""
     spec = CONFIGS[name]
-    model, q, k, v, ctrl = _setup(spec["cfg"], spec["b"], spec["t"], torch.float32, seed=9)
+    model, q, k, v, ctrl = _setup(spec["cfg"], spec["b"], spec["t"], torch.float32, seed=9,
+                                  normalize_k=spec.get("normalize_k", False), gate_noise=spec.get("gate_noise", 0.),
+                                  control_dim=spec.get("control_dim", 0))
     ref = oracle.OracleRun(copy.deepcopy(model))
     hip = model.to(DEV)
     t = spec["t"]
     cuts = [0, 2, 3, t // 2, t - 1, t]
+    part = (lambda x, lo, hi: x[:, lo:hi]) if ctrl is not None else (lambda x, lo, hi: None)
+    dev = (lambda x: x.to(DEV) if x is not None else None)
     with torch.no_grad():
-        full, full_state = hip(q.to(DEV), k.to(DEV), v.to(DEV))
+        full, full_state = hip(q.to(DEV), k.to(DEV), v.to(DEV), control_input=dev(ctrl))
         state, parts = None, []
         for lo, hi in zip(cuts[:-1], cuts[1:]):
-            y, state = hip(q[:, lo:hi].to(DEV), k[:, lo:hi].to(DEV), v[:, lo:hi].to(DEV), state)
+            y, state = hip(q[:, lo:hi].to(DEV), k[:, lo:hi].to(DEV), v[:, lo:hi].to(DEV), state,
+                           control_input=dev(part(ctrl, lo, hi)))
             parts.append(y)
         ref_state, ref_parts = None, []
         for lo, hi in zip(cuts[:-1], cuts[1:]):
-            y, ref_state = ref(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], ref_state)
+            y, ref_state = ref(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], ref_state, control_input=part(ctrl, lo, hi))
             ref_parts.append(y)
         hip_cat, ref_cat = torch.cat(parts, 1), torch.cat(ref_parts, 1)
         assert _rel(hip_cat, full) < 1e-5
@@ -145,9 +158,11 @@ def test_cached_partitions_and_decode_match_oracle(name):
         g = torch.Generator().manual_seed(3)
         for _ in range(3):
             dq = torch.randn(q.shape[0], 1, *q.shape[2:], generator=g)
+            dk = torch.nn.functional.normalize(torch.randn(dq.shape, generator=g), dim=-1)
             dv = torch.randn(v.shape[0], 1, *v.shape[2:], generator=g)
-            y, state = hip(dq.to(DEV), dq.to(DEV), dv.to(DEV), state)
-            y_ref, ref_state = ref(dq, dq, dv, ref_state)
+            dc = torch.randn(q.shape[0], 1, ctrl.shape[-1], generator=g) if ctrl is not None else None
+            y, state = hip(dq.to(DEV), dk.to(DEV), dv.to(DEV), state, control_input=dev(dc))
+            y_ref, ref_state = ref(dq, dk, dv, ref_state, control_input=dc)
             assert _rel(y, y_ref) < 1e-4
         for a, b in zip(tensors(state), tensors(ref_state)):
             assert _rel(a, b) < 1e-4

@@ -8,8 +8,9 @@ inputs run through the HIP backend and every entry is compared by relative L2
 error: 1e-4 in float32, 2e-2 in bfloat16.  Entries stored as fingerprints (sum,
 sum|x|, sum x^2 and 64 evenly spaced samples) are compared through sum|x|,
 sum x^2 and the samples.  Gradients that vanish at initialisation are floored
-at 1e-3 of the largest gradient norm of the case.  The float64 fixtures are
-not run: the HIP backend computes in float32 or bfloat16.
+at 1e-3 of the largest gradient norm of the case.  The HIP backend computes in
+float32 or bfloat16, so a float64 fixture runs in float32 (the seeded float64
+model and inputs rounded to float32) at the float32 bar, 1e-4.
 """
 import math
 
@@ -23,7 +24,7 @@ from tests.golden_cases import Case, fingerprint, names
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
-CASES = [n for n in names() if not n.endswith("fp64")]
+CASES = names()
 
 
 def _norm(case, name):
@@ -51,11 +52,16 @@ def _rel(case, name, x, floor=0.):
 @pytest.mark.parametrize("name", CASES)
 def test_hip_backend_reproduces_reference_fixture(name):
     case = Case(name)
-    tol = TOL[case.dtype]
+    dtype = torch.float32 if case.dtype == torch.float64 else case.dtype
+    tol = TOL[dtype]
     model, q, k, v, ctrl = case.build()
-    model = model.to(DEV)
-    xs = [x.to(DEV).requires_grad_() for x in (q, k, v)]
-    c = ctrl.to(DEV).requires_grad_() if ctrl is not None else None
+    model = model.float().to(DEV)
+    xs = [x.to(DEV, dtype).requires_grad_() for x in (q, k, v)]
+    c = ctrl.to(DEV, torch.float32).requires_grad_() if ctrl is not None else None
+    if case.cfg.get("positional_mode") == "moments":
+        with pytest.raises(ValueError, match="moments"):
+            model(*xs, control_input=c)
+        return
     out, state = model(*xs, control_input=c)
     errors = {"out": _rel(case, "out", out)}
     meta = list(case.z["state/meta"])
@@ -83,7 +89,7 @@ def test_hip_backend_reproduces_reference_fixture(name):
                 parts.append(y)
             errors["partition_out"] = _rel(case, "partition_out", torch.cat(parts, 1))
         if case.steps():
-            dq, dk, dv = (x.to(DEV) for x in case.regen_decode_inputs())
+            dq, dk, dv = (x.to(DEV, dtype) for x in case.regen_decode_inputs())
             running, ys = state, []
             for t in range(case.steps()):
                 y, running = model(dq[:, t:t + 1], dk[:, t:t + 1], dv[:, t:t + 1], running)

@@ -96,3 +96,118 @@ def test_decode_graph_matches_eager_decode(dtype):
                 assert got.position == state.position == i + 1
                 for a, r in zip(tensors(got), tensors(state)):
                     assert _rel(a, r) < 1e-6, i
+
+
+def test_gradient_graph_replays_match_oracle():
+    """Replays of a captured float32 forward+backward (C2 widths, two heads,
+    two blocks and a partial one) against the oracle's forward and autograd on
+    the CPU: output, loss, every parameter gradient and the input gradients,
+    for two different inputs."""
+    import oracle
+    torch.manual_seed(1)
+    cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=64)
+    cpu_model = DenseGPA(cfg)
+    model = copy.deepcopy(cpu_model).to(DEV)
+    shape_q, shape_v = (2, 130, 2, 32), (2, 130, 2, 48)
+
+    def inputs(seed):
+        g = torch.Generator().manual_seed(seed)
+        return [torch.randn(shape_q, generator=g), torch.randn(shape_q, generator=g),
+                torch.randn(shape_v, generator=g)]
+
+    def loss_fn(q, k, v):
+        out, _ = model(q, k, v)
+        return out.float().square().mean(), out
+
+    graph = GradientGraph(model, [x.to(DEV).requires_grad_() for x in inputs(100)], loss_fn, warmups=2)
+    for seed in (7, 8):
+        xs = inputs(seed)
+        loss, out = graph.replay(*(x.to(DEV) for x in xs))
+        torch.cuda.synchronize()
+        ref_model = copy.deepcopy(cpu_model)
+        rs = [x.clone().requires_grad_() for x in xs]
+        r_out, _ = oracle.OracleRun(ref_model)(*rs)
+        r_loss = r_out.float().square().mean()
+        r_loss.backward()
+        assert _rel(out, r_out) < 1e-4 and _rel(loss, r_loss) < 1e-4, seed
+        top = max(p.grad.norm().item() for p in ref_model.parameters() if p.grad is not None)
+        for (n, p), (_, r) in zip(model.named_parameters(), ref_model.named_parameters()):
+            if r.grad is None:
+                continue
+            err = (p.grad.cpu() - r.grad).norm().item() / max(r.grad.norm().item(), 1e-3 * top)
+            assert err < 1e-4, (seed, n, err)
+        for a, b in zip(graph.inputs, rs):
+            assert _rel(a.grad, b.grad) < 1e-4, seed
+
+
+def test_decode_graph_outputs_hold_until_their_position_replays():
+    """The output of position o stays valid while the following positions of
+    the block and the first positions of the next block replay (until o
+    itself replays): kept without copies, it equals the eager decode's."""
+    from gpa_amd.graph import DecodeGraph
+    torch.manual_seed(4)
+    cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=4)
+    model = DenseGPA(cfg).to(DEV)
+    b = 2
+    g = torch.Generator(device=DEV).manual_seed(5)
+    toks = [(torch.randn(b, 1, 2, 32, device=DEV, generator=g),
+             torch.nn.functional.normalize(torch.randn(b, 1, 2, 32, device=DEV, generator=g), dim=-1),
+             torch.randn(b, 1, 2, 48, device=DEV, generator=g)) for _ in range(6)]
+    with torch.no_grad():
+        state = model.initial_state(b, device=DEV, dtype=torch.float32)
+        graphed = DecodeGraph(model, state, *toks[0])
+        kept = [graphed.step(*x) for x in toks[:4]]        # one whole block, no clones
+        later = [graphed.step(*x).clone() for x in toks[4:6]]  # positions 0 and 1 of the next block
+        torch.cuda.synchronize()
+        eager = []
+        for x in toks:
+            y, state = model(*x, state)
+            eager.append(y)
+    for o in (2, 3):  # not replayed since
+        assert _rel(kept[o], eager[o]) < 1e-6, o
+    for i, y in enumerate(later):
+        assert _rel(y, eager[4 + i]) < 1e-6, i
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_decode_graph_matches_oracle_at_c3_widths(dtype):
+    """The graphed decode the benchmark times, at config-3 widths (Dk = Dv =
+    128, slots (128,128,128,256), chunk 64) with two heads and two sequences:
+    a 64-token prefill, then 65 graphed one-token steps (a whole block and one
+    step into the next), against the oracle's cached calls on the CPU: every
+    step's output and the whole cache at the block boundary."""
+    import oracle
+    from gpa_amd.graph import DecodeGraph
+    from gpa_amd.state import tensors
+    torch.manual_seed(6)
+    cfg = GPAConfig(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64)
+    cpu_model = DenseGPA(cfg)
+    model = copy.deepcopy(cpu_model).to(DEV)
+    ref = oracle.OracleRun(cpu_model)
+    b, steps = 2, 65
+    g = torch.Generator().manual_seed(7)
+
+    def draw(t):
+        q = torch.randn(b, t, 2, 128, generator=g)
+        k = torch.nn.functional.normalize(torch.randn(b, t, 2, 128, generator=g), dim=-1)
+        return q.to(dtype), k.to(dtype), torch.randn(b, t, 2, 128, generator=g).to(dtype)
+
+    pre = draw(64)
+    toks = [draw(1) for _ in range(steps)]
+    tol = TOL_DEC[dtype]
+    with torch.no_grad():
+        _, state = model(*(x.to(DEV) for x in pre))
+        _, r_state = ref(*pre)
+        graphed = DecodeGraph(model, state, *(x.to(DEV) for x in toks[0]))
+        for i, x in enumerate(toks):
+            y = graphed.step(*(t.to(DEV) for t in x))
+            y_ref, r_state = ref(*x, r_state)
+            assert _rel(y, y_ref) < tol, (i, _rel(y, y_ref))
+            if i == 63:
+                got = graphed.state
+                assert got.position == r_state.position == 128 and r_state.chunk_offset == 0
+                for n, (a, r) in enumerate(zip(tensors(got), tensors(r_state))):
+                    assert _rel(a, r) < tol, (n, _rel(a, r))
+
+
+TOL_DEC = {torch.float32: 1e-4, torch.bfloat16: 2e-2}

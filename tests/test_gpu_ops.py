@@ -7,6 +7,7 @@ import torch
 import oracle
 from gpa_amd import TwoStageState, two_stage_gdn
 from gpa_amd.ops import gdn_scan, gdn_update, memory_read
+from tests.golden_cases import TwoStageCase, ops_names
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -76,3 +77,25 @@ def test_two_stage_gdn_matches_oracle(dtype):
                                              query_weight=qw)
     tol = TOL[dtype]
     assert _rel(out, ref_out) < tol and _rel(st.inner, ref_a) < tol and _rel(st.outer, ref_b) < tol
+
+
+@pytest.mark.parametrize("name", ops_names("ops_two_stage"))
+def test_two_stage_gdn_reproduces_reference_fixture(name):
+    """HIP two_stage_gdn against the reference's own two_stage_gdn results
+    (tests/golden/ops_two_stage_*.npz): output, both final states and the
+    gradient of every input.  A float64 fixture runs in float32 at 1e-4."""
+    case = TwoStageCase(name)
+    dtype = torch.float32 if case.dtype == torch.float64 else case.dtype
+    tol = TOL[dtype]
+    x = {n: t.to(DEV).requires_grad_() for n, t in case.inputs(dtype).items()}
+    out, st = two_stage_gdn(x["q"], x["k"], x["slots"], x["v"], x["gi"], x["bi"], x["go"], x["bo"],
+                            TwoStageState(x["inner"], x["outer"]), route_weight=x.get("route_weight"),
+                            query_weight=x.get("query_weight"))
+    out.float().square().mean().backward()
+    errors = {label: _rel(got, case.ref(label)) for label, got in (("out", out), ("inner", st.inner),
+                                                                  ("outer", st.outer))}
+    for n, t in x.items():
+        errors["grad/" + n] = _rel(t.grad, case.ref("grad/" + n))
+    print(name, "worst", max(errors.items(), key=lambda kv: kv[1]))
+    bad = {k: e for k, e in errors.items() if e > tol}
+    assert not bad, bad

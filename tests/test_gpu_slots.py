@@ -1,7 +1,7 @@
 """Fused slot products and gate inputs (gpa_amd/slots.py, csrc/slot_gates.hip)
-against the reference's typed einsums (attention.py:176-177 and :165, emulated
-as fp32 products of bf16-rounded operands, rounded to bf16, on the CPU): slot,
-raw and the gradients of key, center and gate_weight, at the bf16 bar 2e-2.
+against the oracle's restatement of the reference's bf16 einsums on the CPU
+(`OracleRun.slot`, attention.py:176-177, and `OracleRun.gate_inputs`, :162-165):
+slot, raw and the gradients of key, center and gate_weight, at the bf16 bar 2e-2.
 Also the row tails (T not a multiple of 64), several heads and batches, and
 the widest shapes (Dk = M = 256)."""
 import pytest
@@ -17,10 +17,15 @@ def _rel(a, b):
 
 
 def _reference(key, center, gate_w):
-    from gpa_amd import schedule
-    slot = schedule._mm(key, center, "bthd,hmd->bthm", key.dtype)
-    raw = schedule._mm(schedule._unit(key), gate_w, "bthd,hdc->bthc", key.dtype)
-    return slot, raw
+    """The oracle's slot product and gate input of one level with these weights."""
+    from types import SimpleNamespace
+
+    import oracle
+    from gpa_amd import GPAConfig
+    h, m, d = center.shape
+    cfg = GPAConfig(heads=h, key_dim=d, value_dim=8, slots=(m,), chunk_size=64)
+    run = oracle.OracleRun(SimpleNamespace(config=cfg, center=[center], gate_weight=[gate_w]))
+    return run.slot(key, 0), run.gate_inputs(key, 0, None)
 
 
 @pytest.mark.parametrize("b,t,h,d,m", [(1, 130, 2, 128, 128), (2, 64, 3, 64, 96), (1, 200, 1, 256, 256),

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from tests.golden_cases import Case, compare, compare_state, grad_scale, names
+from tests.golden_cases import Case, TwoStageCase, compare, compare_state, grad_scale, names, ops_names
 
 # Same arithmetic in a different association order: fp64 agrees to ~1e-12,
 # fp32 to ~1e-6; bf16 activations agree except where an fp32 difference of
@@ -72,4 +72,29 @@ def test_oracle_forward_state_and_gradients_match_reference(name):
             errors.append(compare(case, "decode/out", torch.cat(ys, 1), rtol))
             errors += compare_state(case, "decode/state", running, rtol)
     errors = [e for e in errors if e]
+    assert not errors, errors
+
+
+@pytest.mark.parametrize("name", ops_names("ops_two_stage"))
+def test_oracle_two_stage_matches_reference(name):
+    """oracle.two_stage against the reference's two_stage_gdn on the same inputs:
+    output, both final states and the gradient of every input."""
+    case = TwoStageCase(name)
+    rtol = RTOL[case.dtype]
+    x = {n: t.requires_grad_() for n, t in case.inputs().items()}
+    out, a, b = oracle.two_stage(x["q"], x["k"], x["slots"], x["v"], x["gi"], x["bi"], x["go"], x["bo"],
+                                 x["inner"], x["outer"], route_weight=x.get("route_weight"),
+                                 query_weight=x.get("query_weight"))
+    out.float().square().mean().backward()
+    errors = []
+    for label, got in (("out", out), ("inner", a), ("outer", b)):
+        rel = ((got.detach().double() - case.ref(label)).norm() / case.ref(label).norm()).item()
+        if rel > rtol:
+            errors.append(f"{label}: {rel:.3e}")
+    g_rtol = rtol if case.dtype != torch.bfloat16 else 5e-2
+    for n, t in x.items():
+        ref = case.ref("grad/" + n)
+        rel = ((t.grad.double() - ref).norm() / ref.norm()).item()
+        if rel > g_rtol:
+            errors.append(f"grad/{n}: {rel:.3e}")
     assert not errors, errors
