@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -144,6 +144,7 @@ EXPORTS = {
     "gpa_gdn_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads),
                           ctypes.POINTER(Timing), c_vp], ctypes.c_int),
     "gpa_gdn_read": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, c_vp], ctypes.c_int),
+    "gpa_gdn_scan_noalloc": ([ctypes.POINTER(Problem), Operand, c_vp, c_vp], ctypes.c_int),
     "gpa_gdn_read_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, Operand, c_vp],
                               ctypes.c_int),
     "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),

@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <stdio.h>
 #include <type_traits>
 
 #include "gpa_hip.h"
@@ -1016,4 +1018,103 @@ extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_sa
   if (timing) timing->launched = 0;
   return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, timing, stream, nch)
                                           : dispatch_backward<float>(*problem, *saved, *grads, timing, stream, nch);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward (gpa_gdn_scan_noalloc).  The intermediates that
+// gpa_gdn_forward takes from its caller live in `scratch`, a static device
+// array of GPA_NOALLOC_SCRATCH_BYTES that every device the library runs on
+// holds until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, taken once per device, with
+// that device current, on the first call there.  The forward kernels write
+// every element of the intermediates they later read, so nothing needs
+// clearing between calls.  All calls on one device share its array: calls
+// that overlap in time on one device (two streams, two threads) race.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[GPA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // per device, set once under the mutex
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(GPA_HIP_EHIP, "gdn_scan_noalloc: hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(GPA_HIP_EUNSUPPORTED, "gdn_scan_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      char buf[160];
+      snprintf(buf, sizeof buf, "gdn_scan_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(err));
+      return fail(GPA_HIP_EHIP, buf);
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GPA_HIP_OK;
+}
+
+// Carve the forward's intermediates (the sizes gpa_gdn_saved documents in
+// include/gpa_hip.h) from `base` in 256-byte aligned pieces; returns the bytes
+// used.  With base == 0 it only measures.
+uint64_t carve_saved(const gpa_gdn_problem& p, uintptr_t base, gpa_gdn_saved* sv) {
+  const uint64_t nch = gpa_gdn_nchunks(p.tokens, p.offset, p.chunk);
+  const uint64_t chunks = (uint64_t)p.batch * p.heads * nch, rows = chunks * R;
+  const uint64_t K = p.kdim, V = p.vdim, k16 = K / 16, rb = (K + 31) / 32;
+  const bool mfma = path_of(&p) == 1, has_q = p.q.ptr != nullptr;
+  uint64_t at = 0;
+  auto take = [&](uint64_t bytes) -> void* {
+    if (!bytes) return nullptr;
+    void* ptr = reinterpret_cast<void*>(base + at);
+    at += (bytes + 255) / 256 * 256;
+    return ptr;
+  };
+  const uint64_t f = sizeof(float), h = 2;  // float32, bf16 element sizes
+  sv->kn = static_cast<float*>(take(rows * K * f));
+  sv->qn = static_cast<float*>(take(has_q ? rows * K * f : 0));
+  sv->w = static_cast<float*>(take(mfma ? 0 : rows * K * f));
+  sv->u = static_cast<float*>(take(rows * V * f));
+  sv->delta = static_cast<float*>(take(rows * V * f));
+  sv->tri = static_cast<float*>(take(rows * R * f));
+  sv->gam = static_cast<float*>(take(rows * f));
+  sv->beta = static_cast<float*>(take(rows * f));
+  sv->states = static_cast<float*>(take(chunks * V * K * f));
+  sv->final = nullptr;  // the caller's output
+  sv->wrow = take(mfma ? chunks * 2 * k16 * 64 * 16 * h : 0);
+  sv->wcol = take(mfma ? chunks * rb * 4 * 64 * 16 * h : 0);
+  sv->krow = take(mfma ? chunks * 2 * k16 * 64 * 8 * h : 0);
+  sv->kcol = take(mfma ? chunks * rb * 4 * 64 * 8 * h : 0);
+  sv->qcol = take(mfma && has_q ? chunks * rb * 4 * 64 * 8 * h : 0);
+  return at;
+}
+
+}  // namespace
+
+extern "C" int gpa_gdn_scan_noalloc(const gpa_gdn_problem* problem, gpa_operand out, float* final_state,
+                                    hipStream_t stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (!final_state) return fail(GPA_HIP_EINVAL, "gdn_scan_noalloc: final_state is null");
+  if (problem->q.ptr && !out.ptr) return fail(GPA_HIP_EINVAL, "gdn_scan_noalloc: q given without out");
+  gpa_gdn_saved sv{};
+  const uint64_t need = carve_saved(*problem, 0, &sv);
+  if (need > (uint64_t)GPA_NOALLOC_SCRATCH_BYTES) {
+    char buf[200];
+    snprintf(buf, sizeof buf,
+             "gdn_scan_noalloc: the problem needs %llu bytes of scratch, above the %llu-byte maximum "
+             "(fewer streams or tokens per call)",
+             (unsigned long long)need, (unsigned long long)GPA_NOALLOC_SCRATCH_BYTES);
+    return fail(GPA_HIP_EINVAL, buf);
+  }
+  void* base = nullptr;
+  if ((rc = scratch_address(&base))) return rc;
+  carve_saved(*problem, reinterpret_cast<uintptr_t>(base), &sv);
+  sv.final = final_state;
+  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
+  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, sv, out, nullptr, stream, nch)
+                                          : dispatch_forward<float>(*problem, sv, out, nullptr, stream, nch);
 }

@@ -246,6 +246,48 @@ def gdn_scan_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor
     return out, states_vk.transpose(-1, -2), final
 
 
+def gdn_scan_noalloc(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor | None,
+                     *, chunk: int, offset: int = 0, out: Tensor | None = None,
+                     final: Tensor | None = None) -> tuple[Tensor | None, Tensor]:
+    """Inference forward of `gdn_scan_hip` through the library's allocation-free
+    entry point (gpa_gdn_scan_noalloc): the library allocates nothing; its
+    intermediates live in a fixed per-device scratch array (64 MiB), and
+    problems that need more are rejected.  Pass `out` ([B,T,H,V], the input
+    dtype) and `final` ([B,H,K,V] float32, contiguous) to allocate nothing
+    here either (e.g. under graph capture).  No autograd.  Calls overlapping
+    on one device share the scratch array and must not run concurrently."""
+    _lib.require_device(k)
+    if k.dtype not in _lib.DTYPE_CODES or v.dtype != k.dtype or (q is not None and q.dtype != k.dtype):
+        raise ValueError("gdn_scan_noalloc: q/k/v must share float32 or bfloat16")
+    if k.ndim != 4 or v.ndim != 4 or v.shape[:3] != k.shape[:3] or (q is not None and q.shape != k.shape):
+        raise ValueError("gdn_scan_noalloc: expected q,k [B,T,H,K] and v [B,T,H,V]")
+    if g.shape != k.shape[:3] or beta.shape != k.shape[:3]:
+        raise ValueError("gdn_scan_noalloc: g and beta must be [B,T,H]")
+    if not 1 <= chunk <= _lib.CHUNK_ROWS or not 0 <= offset < chunk:
+        raise ValueError("gdn_scan_noalloc: need 1 <= chunk <= 64 and 0 <= offset < chunk")
+    _no_autograd("gdn_scan_noalloc", q, k, v, g, beta, s0)
+    bsz, tokens, heads, kd = k.shape
+    vd = v.shape[-1]
+    if s0 is not None and s0.shape != (bsz, heads, kd, vd):
+        raise ValueError("gdn_scan_noalloc: s0 must be [B,H,K,V]")
+    q = _contig_last(q) if q is not None else None
+    k, v = _contig_last(k), _contig_last(v)
+    g, beta = g.float(), beta.float()
+    s0f = _f32_state(s0) if s0 is not None else None
+    if final is None:
+        final = torch.empty(bsz, heads, kd, vd, device=k.device, dtype=torch.float32)
+    elif final.shape != (bsz, heads, kd, vd) or final.dtype != torch.float32 or not final.is_contiguous():
+        raise ValueError("gdn_scan_noalloc: final must be a contiguous float32 [B,H,K,V] tensor")
+    if q is not None and out is None:
+        out = torch.empty(bsz, tokens, heads, vd, device=k.device, dtype=k.dtype)
+    elif q is not None and (out.shape != (bsz, tokens, heads, vd) or out.dtype != k.dtype or out.stride(-1) != 1):
+        raise ValueError("gdn_scan_noalloc: out must be [B,T,H,V] in the input dtype with a contiguous last axis")
+    prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+    _lib.check(_lib.load().gpa_gdn_scan_noalloc(prob, _lib.operand(out if q is not None else None), final.data_ptr(),
+                             _lib.stream_handle(k.device)), "gpa_gdn_scan_noalloc")
+    return (out if q is not None else None), final
+
+
 def read_supported(k: Tensor, v: Tensor) -> bool:
     """Whether gdn_scan_deferred can take a late read of these keys/values
     (bf16, K a multiple of 16 up to 256, V a multiple of 8 up to 256)."""

@@ -8,7 +8,9 @@
  * (per calling thread).  The library never allocates device memory, never
  * synchronises and keeps no mutable global state: every buffer (inputs,
  * outputs, the intermediates a backward pass needs) is owned by the caller,
- * so calls are reentrant and may be captured into a HIP graph.
+ * so calls are reentrant and may be captured into a HIP graph.  The one
+ * exception is gpa_gdn_scan_noalloc, which keeps its intermediates in a
+ * static per-device array (see there).
  *
  * Operand convention.  A scan runs `batch*heads` independent streams.  Element
  * (stream s = b*heads + h, token t, feature d) of a gpa_operand lives at
@@ -33,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 13
+#define GPA_HIP_ABI_VERSION 14
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -155,6 +157,22 @@ int gpa_gdn_read(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa
  * same problem (query set), saved (qn, qcol filled) and dout. */
 int gpa_gdn_read_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved, gpa_operand dout,
                           gpa_operand dq, hipStream_t stream);
+
+/* Allocation-free forward scan.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  It computes what
+ * gpa_gdn_forward computes -- `out` (problem dtype) when q.ptr != NULL and the
+ * final state, contiguous [batch,heads,K,V] float32 -- with the forward's
+ * intermediates in a static device array of GPA_NOALLOC_SCRATCH_BYTES that
+ * each device holds until the process ends, instead of caller buffers (no
+ * backward follows).  A problem whose intermediates exceed the array is
+ * rejected with GPA_HIP_EINVAL; at K = V = 128 in bf16 that is about 190
+ * stream-chunks (e.g. 16 streams of 704 tokens).  It calls no hipMalloc or
+ * hipFree.  Every call on a device shares that device's array: calls that
+ * overlap in time on one device (two streams, two threads) race. */
+#define GPA_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int gpa_gdn_scan_noalloc(const gpa_gdn_problem *problem, gpa_operand out, float *final_state,
+                         hipStream_t stream);
 
 /* One token of every stream without saved intermediates (inference decode;
  * problem->tokens must be 1, chunk and offset are not used):
