@@ -55,6 +55,30 @@ __device__ __forceinline__ int64_t state_off(int s, int n, int nch, int K, int V
 __device__ __forceinline__ int64_t vc_off(int s, int n, int nch, int V) {
   return ((int64_t)s * nch + n) * V * R;
 }
+// MFMA path: U in fragment order, per chunk [ceil(V/32)][2][4][64][4]: for
+// 32-column strip c, row tile rt and group g, lane l holds U rows
+// 32 rt + 8 g + 4 (l/32) + 0..3 of column 32 c + l%32 (the accumulator layout
+// of a 32 x 32 MFMA tile), so a wave reads 1 KB contiguous per instruction.
+__host__ __device__ __forceinline__ int ufrag_v(int V) { return (V + 31) / 32 * 32; }  // padded width
+__device__ __forceinline__ int64_t ufrag_off(int s, int n, int nch, int V) { return ((int64_t)s * nch + n) * ufrag_v(V) * R; }
+__device__ __forceinline__ int ufrag_idx(int c, int rt, int g, int l) { return (((c * 2 + rt) * 4 + g) * 64 + l) * 4; }
+// Position of element (row r < 64, column v) in a fragment-order block.
+__device__ __forceinline__ int ufrag_elem(int v, int r) {
+  return ufrag_idx(v >> 5, r >> 5, (r >> 3) & 3, (v & 31) + 32 * ((r >> 2) & 1)) + (r & 3);
+}
+// Lane l's 16 accumulator values of strip c, row tile rt of one chunk's U
+// block uc (zeros when the strip does not exist, c >= nstrip).
+template <bool GUARD>
+__device__ __forceinline__ void load_ufrag(float (&x)[16], const float* uc, int c, int nstrip, int rt, int l) {
+  const bool ok = !GUARD || c < nstrip;
+  const float* src = uc + ufrag_idx(ok ? c : 0, rt, 0, l);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 q = *reinterpret_cast<const float4*>(src + 256 * g);
+    x[4 * g] = ok ? q.x : 0.f; x[4 * g + 1] = ok ? q.y : 0.f; x[4 * g + 2] = ok ? q.z : 0.f; x[4 * g + 3] = ok ? q.w : 0.f;
+  }
+}
+
 // Per-chunk sizes (bf16 elements) of the MFMA fragment buffers.
 __host__ __device__ __forceinline__ int frag_row_elems(int K, int per_lane) { return 2 * (K / 16) * 64 * per_lane; }
 __host__ __device__ __forceinline__ int frag_col_elems(int K, int per_lane) { return ((K + 31) / 32) * 4 * 64 * per_lane; }

@@ -225,17 +225,20 @@ __global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gd
       pl[u * PLD + t] = (__bf16)(pt[r] - (float)hi);
     }
   }
-  // o = diag(e^G) dO, value-major: thread -> (v, 4 consecutive rows).
-  float* om = gr.o + vc_off(s, n, nch, V);
-  for (int idx = tid; idx < V * (R / 4); idx += ONT) {
-    const int v = idx / (R / 4), t0 = 4 * (idx - v * (R / 4));
-    const bf16_t* x = reinterpret_cast<const bf16_t*>(dot) + v * PLD + t0;
-    *reinterpret_cast<float4*>(om + (int64_t)v * R + t0) =
-        make_float4(__expf(gam_s[t0]) * to_f32(x[0]), __expf(gam_s[t0 + 1]) * to_f32(x[1]),
-                    __expf(gam_s[t0 + 2]) * to_f32(x[2]), __expf(gam_s[t0 + 3]) * to_f32(x[3]));
+  // o = diag(e^G) dO in fragment order (ufrag_idx): thread -> (strip, row
+  // tile, group, lane), four consecutive rows of one column; zero past V.
+  float* om = gr.o + ufrag_off(s, n, nch, V);
+  for (int idx = tid; idx < ((V + 31) / 32) * 512; idx += ONT) {
+    const int ln = idx & 63, g = (idx >> 6) & 3, r2 = (idx >> 8) & 1, c = idx >> 9;
+    const int v = 32 * c + (ln & 31), t0 = 32 * r2 + 8 * g + 4 * (ln >> 5);
+    const bf16_t* x = reinterpret_cast<const bf16_t*>(dot) + (v < V ? v : 0) * PLD + t0;
+    *reinterpret_cast<float4*>(om + ufrag_idx(c, r2, g, ln)) =
+        v < V ? make_float4(__expf(gam_s[t0]) * to_f32(x[0]), __expf(gam_s[t0 + 1]) * to_f32(x[1]),
+                            __expf(gam_s[t0 + 2]) * to_f32(x[2]), __expf(gam_s[t0 + 3]) * to_f32(x[3]))
+              : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   __syncthreads();
-  float* d0 = gr.dd0 + vc_off(s, n, nch, V);
+  float* d0 = gr.dd0 + ufrag_off(s, n, nch, V);
   const int VT = (V + 31) / 32, ut = rt;
   for (int vt = w >> 1; vt < VT; vt += 2) {
     const int v = 32 * vt + li, vc = v < V ? v : V - 1;
@@ -250,12 +253,11 @@ __global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gd
       a2 = mfma_bf16(pb, bo, a2);
     }
     const f32x16 acc = a1 + a2;
-    if (v < V) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(d0 + (int64_t)v * R + 32 * ut + 8 * g + 4 * hh) =
-            make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]);
-    }
+    for (int g = 0; g < 4; ++g)  // fragment order, zero past V
+      *reinterpret_cast<float4*>(d0 + ufrag_idx(vt, ut, g, l)) =
+          v < V ? make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3])
+                : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 

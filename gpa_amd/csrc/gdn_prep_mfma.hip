@@ -246,7 +246,8 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
   }
   __syncthreads();
   if (MF) {
-    // Row fragments: piece (t/32, k/16, lane t%32 + 32 ((k/8) % 2)), hi then lo.
+    // Row fragments: piece (t/32, k/16, lane t%32 + 32 ((k/8) % 2)); fragment f
+    // = piece / 64 holds the 64 lanes' hi parts, then their lo parts.
     __bf16* wrow = reinterpret_cast<__bf16*>(sv.wrow) + chunk_id * frag_row_elems(K, 16);
     __bf16* wcol = reinterpret_cast<__bf16*>(sv.wcol) + chunk_id * frag_col_elems(K, 16);
     for (int piece = tid; piece < 2 * K16 * 64; piece += NTH) {
@@ -258,10 +259,12 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
         hi[e] = (__bf16)src[e];
         lo[e] = (__bf16)(src[e] - (float)hi[e]);
       }
-      *reinterpret_cast<bf16x8v*>(wrow + (int64_t)piece * 16) = hi;
-      *reinterpret_cast<bf16x8v*>(wrow + (int64_t)piece * 16 + 8) = lo;
+      __bf16* dst = wrow + (int64_t)(piece >> 6) * 1024 + ln * 8;
+      *reinterpret_cast<bf16x8v*>(dst) = hi;
+      *reinterpret_cast<bf16x8v*>(dst + 512) = lo;
     }
-    // Column fragments: piece (k/32, t/16, lane k%32 + 32 ((t/8) % 2)), rows t..t+7, hi then lo.
+    // Column fragments: piece (k/32, t/16, lane k%32 + 32 ((t/8) % 2)), rows t..t+7,
+    // planar like the row fragments.
     const int RB = (K + 31) / 32;
     for (int piece = tid; piece < RB * 4 * 64; piece += NTH) {
       const int ln = piece & 63, cs = (piece >> 6) & 3, rb = piece >> 8;
@@ -273,13 +276,15 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
         hi[e] = (__bf16)x;
         lo[e] = (__bf16)(x - (float)hi[e]);
       }
-      *reinterpret_cast<bf16x8v*>(wcol + (int64_t)piece * 16) = hi;
-      *reinterpret_cast<bf16x8v*>(wcol + (int64_t)piece * 16 + 8) = lo;
+      __bf16* dst = wcol + (int64_t)(piece >> 6) * 1024 + ln * 8;
+      *reinterpret_cast<bf16x8v*>(dst) = hi;
+      *reinterpret_cast<bf16x8v*>(dst + 512) = lo;
     }
   }
 
   // ---- U = T diag(b) V in slices of 128 values; every wave owns one 32x32 tile.
-  float* um = sv.u + vc_off(s, n, nch, V);
+  // Value-major on the FMA path, fragment order (ufrag_idx) on the MFMA path.
+  float* um = sv.u + (MF ? ufrag_off(s, n, nch, V) : vc_off(s, n, nch, V));
   const int urt = wave >> 2, uvt = wave & 3;
   for (int v0 = 0; v0 < V; v0 += VC) {
     __syncthreads();  // W fragments (or the previous slice) are done with the region
@@ -308,7 +313,16 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
       mma8(acc, ld_c(t_s, LT, 32 * urt + li, c0), ld_x(v_s, LV, 32 * uvt + li, c0));
     }
     const int v = v0 + 32 * uvt + li;
-    if (v < V) {
+    if (MF) {
+      // Whole 32-column strips, zero past V (the padded strip is read too).
+      const int c = (v0 + 32 * uvt) >> 5;
+      if (v0 + 32 * uvt < V) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(um + ufrag_idx(c, urt, q, lane)) =
+              v < V ? f32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]} : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    } else if (v < V) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<f32x4*>(um + (int64_t)v * R + 32 * urt + 8 * q + 4 * hh) =

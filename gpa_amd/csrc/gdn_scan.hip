@@ -27,6 +27,7 @@
 #include "gpa_hip.h"
 #include "gpa_common.h"
 #include "gdn_common.h"
+#include "gdn_strip.h"
 
 namespace gpa {
 
@@ -233,8 +234,12 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
   if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
   __syncthreads();
   build_p<KM>(p_s, a_s, b_s, sv.qn + rows_off(s, n, nch, 0, K), sv.kn + rows_off(s, n, nch, 0, K), gam_s, K);
-  float* d0 = gr.dd0 + vc_off(s, n, nch, V);
-  float* om = gr.o + vc_off(s, n, nch, V);
+  // dd0 and o are value-major for the FMA state kernels and in fragment order
+  // (ufrag_idx) for the MFMA ones (bf16, K a multiple of 16).
+  const bool frag = std::is_same<E, bf16_t>::value && K % 16 == 0;
+  float* d0 = gr.dd0 + (frag ? ufrag_off(s, n, nch, V) : vc_off(s, n, nch, V));
+  float* om = gr.o + (frag ? ufrag_off(s, n, nch, V) : vc_off(s, n, nch, V));
+  auto at = [&](int v, int r) -> int64_t { return frag ? ufrag_elem(v, r) : (int64_t)v * R + r; };
   for (int v0 = 0; v0 < V; v0 += 64) {
     __syncthreads();
     for (int idx = tid; idx < R * 64; idx += NT) {
@@ -245,7 +250,8 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
     __syncthreads();
     for (int idx = tid; idx < R * 64; idx += NT) {
       const int r = idx % R, c = idx / R;
-      if (v0 + c < V) om[(int64_t)(v0 + c) * R + r] = __expf(gam_s[r]) * b_s[r * LDS_ + c];
+      if (v0 + c < V) om[at(v0 + c, r)] = __expf(gam_s[r]) * b_s[r * LDS_ + c];
+      else if (frag && v0 + c < ufrag_v(V)) om[at(v0 + c, r)] = 0.f;
     }
     float acc[4][4] = {};
     for (int u = 0; u < R; ++u) {  // acc[t'][v] += P[u][t'] dO[u][v]
@@ -261,9 +267,11 @@ __global__ __launch_bounds__(NT) void gdn_dd0(gpa_gdn_problem p, gpa_gdn_saved s
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int v = v0 + tx + 16 * j;
+      const int v = v0 + tx + 16 * j;  // four consecutive rows are contiguous in both layouts
       if (v < V)
-        *reinterpret_cast<float4*>(&d0[(int64_t)v * R + 4 * ty]) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+        *reinterpret_cast<float4*>(&d0[at(v, 4 * ty)]) = make_float4(acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+      else if (frag && v < ufrag_v(V))
+        *reinterpret_cast<float4*>(&d0[at(v, 4 * ty)]) = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
 }
@@ -883,7 +891,13 @@ int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operan
   mark(tm, st);
   if (int rc = launch_prep_mfma<E, KM>(p, sv, mf, nch, st)) return rc;
   mark(tm, st);
-  if (mf) {
+  if (mf && KM <= 128) {
+    StripFwdPack pk{};
+    pk.n = 1;
+    pk.p[0] = strip_fwd_one(p, sv, nch, 0);
+    const bool fast = p.kdim == KM && p.vdim % 64 == 0;
+    if (int rc = launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, st)) return rc;
+  } else if (mf) {
     if (int rc = launch_state_fwd_mfma<KM>(p, sv, nch, st)) return rc;
   } else {
     const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -922,7 +936,15 @@ int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_g
     gr.o = nullptr;
   }
   mark(tm, st);
-  if (use_mfma<E>(p)) {
+  if (use_mfma<E>(p) && KM <= 128) {
+    StripBwdPack pk{};
+    pk.n = 1;
+    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q);
+    const bool fast = p.kdim == KM && p.vdim % 64 == 0;
+    if (int rc = launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, has_q,
+                                                              gr.dstates != nullptr, st))
+      return rc;
+  } else if (use_mfma<E>(p)) {
     if (int rc = launch_state_bwd_mfma<KM>(p, sv, gr, nch, st)) return rc;
   } else {
     const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -1077,7 +1099,7 @@ uint64_t carve_saved(const gpa_gdn_problem& p, uintptr_t base, gpa_gdn_saved* sv
   sv->kn = static_cast<float*>(take(rows * K * f));
   sv->qn = static_cast<float*>(take(has_q ? rows * K * f : 0));
   sv->w = static_cast<float*>(take(mfma ? 0 : rows * K * f));
-  sv->u = static_cast<float*>(take(rows * V * f));
+  sv->u = static_cast<float*>(take(rows * (mfma ? (uint64_t)ufrag_v(p.vdim) : V) * f));
   sv->delta = static_cast<float*>(take(rows * V * f));
   sv->tri = static_cast<float*>(take(rows * R * f));
   sv->gam = static_cast<float*>(take(rows * f));

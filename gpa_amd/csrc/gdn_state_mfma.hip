@@ -52,10 +52,12 @@ struct Split8 {
   bf16x8 hi, lo;
 };
 
+// One lane's part of a planar split fragment (hi parts of the 64 lanes, then
+// their lo parts): p points at the lane's hi part.
 __device__ __forceinline__ Split8 load_split(const __bf16* p) {
   Split8 s;
   s.hi = *reinterpret_cast<const bf16x8*>(p);
-  s.lo = *reinterpret_cast<const bf16x8*>(p + 8);
+  s.lo = *reinterpret_cast<const bf16x8*>(p + 512);
   return s;
 }
 
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
 
   const __bf16* wrow = reinterpret_cast<const __bf16*>(sv.wrow) + (int64_t)s * nch * frag_row;
   const __bf16* kcol = reinterpret_cast<const __bf16*>(sv.kcol) + (int64_t)s * nch * frag_col;
-  auto w_at = [&](int n, int ks) { return wrow + (int64_t)n * frag_row + ((rt * sp.K16 + ks) * 64 + l) * 16; };
+  auto w_at = [&](int n, int ks) { return wrow + (int64_t)n * frag_row + (rt * sp.K16 + ks) * 1024 + l * 8; };
   auto k_at = [&](int n, int rb, int cs) { return kcol + (int64_t)n * frag_col + ((rb * 4 + cs) * 64 + l) * 8; };
   Split8 wr[KM / 16];
   bf16x8 kf[NRB][R / 16];
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
 #pragma unroll
     for (int cs = 0; cs < R / 16; ++cs)
       kf[i][cs] = owns && sp.rows(w + 4 * i) ? *reinterpret_cast<const bf16x8*>(k_at(0, w + 4 * i, cs)) : bf16x8{};
-  load_acc_vc<!FAST>(ur, sv.u + vc_off(s, 0, nch, V), vd, V, 32 * rt, l);
+  load_ufrag<!FAST>(ur, sv.u + ufrag_off(s, 0, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
   load_gates(gr_, gcr, sv.gam + rows_off(s, 0, nch, 0, 1), 32 * rt, l);
 
   for (int n = 0; n < nch; ++n) {
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) d[r] = ur[r] - d[r];
-    load_acc_vc<!FAST>(ur, sv.u + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
+    load_ufrag<!FAST>(ur, sv.u + ufrag_off(s, nn, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
     store_acc_vc<!FAST>(sv.delta + vc_off(s, n, nch, V), vd, V, 32 * rt, d, l);
 #pragma unroll
     for (int r = 0; r < 16; ++r) d[r] *= __expf(gcr - gr_[r]);
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
   const __bf16* wcol = reinterpret_cast<const __bf16*>(sv.wcol) + (int64_t)s * nch * frag_wcol;
   const __bf16* qcol = HAS_Q ? reinterpret_cast<const __bf16*>(sv.qcol) + (int64_t)s * nch * frag_col : nullptr;
   auto k_at = [&](int n, int ks) { return krow + (int64_t)n * frag_row + ((rt * sp.K16 + ks) * 64 + l) * 8; };
-  auto w_at = [&](int n, int rb, int cs) { return wcol + (int64_t)n * frag_wcol + ((rb * 4 + cs) * 64 + l) * 16; };
+  auto w_at = [&](int n, int rb, int cs) { return wcol + (int64_t)n * frag_wcol + (rb * 4 + cs) * 1024 + l * 8; };
   auto q_at = [&](int n, int rb, int cs) { return qcol + (int64_t)n * frag_col + ((rb * 4 + cs) * 64 + l) * 8; };
   bf16x8 kr[KM / 16];
   Split8 wf[NRB][R / 16];
@@ -412,8 +414,8 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
       }
     }
     if constexpr (HAS_Q) {
-      load_acc_vc<!FAST>(d0r, gr.dd0 + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
-      load_acc_vc<!FAST>(orr, gr.o + vc_off(s, n, nch, V), vd, V, 32 * rt, l);
+      load_ufrag<!FAST>(d0r, gr.dd0 + ufrag_off(s, n, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
+      load_ufrag<!FAST>(orr, gr.o + ufrag_off(s, n, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
     }
     load_gates(gr_, gcr, sv.gam + rows_off(s, n, nch, 0, 1), 32 * rt, l);
     load_inj(n);
@@ -468,8 +470,8 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[r] = orr[r];
       put_split_t(oh, ol, CT, 32 * rt, 32 * ct, o, l);
-      load_acc_vc<!FAST>(d0r, gr.dd0 + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
-      load_acc_vc<!FAST>(orr, gr.o + vc_off(s, nn, nch, V), vd, V, 32 * rt, l);
+      load_ufrag<!FAST>(d0r, gr.dd0 + ufrag_off(s, nn, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
+      load_ufrag<!FAST>(orr, gr.o + ufrag_off(s, nn, nch, V), (v0 + 32 * ct) >> 5, ufrag_v(V) >> 5, rt, l);
     }
     lds_barrier();
     // (e) dS = e^{G_C} dS + Qn^T o - W^T dD + dstates[n]; fragments are reloaded once

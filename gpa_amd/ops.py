@@ -72,7 +72,9 @@ class _GDNScan(torch.autograd.Function):
         kn = torch.empty(rows * kd, **f32)
         qn = torch.empty(rows * kd, **f32) if q is not None else None
         w = torch.empty(rows * kd, **f32) if not mfma else None
-        u = torch.empty(rows * vd, **f32)
+        # U: value-major [S,N,V,64] on the FMA path; on the MFMA path fragment
+        # order over ceil(V/32) whole 32-column strips (include/gpa_hip.h).
+        u = torch.empty(rows * (-(-vd // 32) * 32 if mfma else vd), **f32)
         delta = torch.empty(rows * vd, **f32)
         tri = torch.empty(rows * _lib.CHUNK_ROWS, **f32)
         gam = torch.empty(rows, **f32)
@@ -123,8 +125,11 @@ class _GDNScan(torch.autograd.Function):
         want_read = has_q and dout is not None
         if want_read:
             dout = _contig_last(dout.to(k.dtype))
-        dd0 = torch.empty(rows * vd, **f32) if want_read else None
-        obuf = torch.empty(rows * vd, **f32) if want_read else None
+        # dd0 and o: value-major on the FMA path, fragment order over whole
+        # 32-column strips on the MFMA path (like u).
+        vcols = -(-vd // 32) * 32 if mfma else vd
+        dd0 = torch.empty(rows * vcols, **f32) if want_read else None
+        obuf = torch.empty(rows * vcols, **f32) if want_read else None
         ddelta = torch.empty(rows * vd, **f32)
         dhend = torch.empty(bsz * heads * nch * kd * vd, **f32)
         dw = torch.empty(rows * kd, **f32)

@@ -72,7 +72,11 @@ typedef struct gpa_gdn_problem {
  * N = nchunks, per chunk):
  *   kn, qn         f32 [S,N,64,K]   normalised keys / queries (rows = positions)
  *   w              f32 [S,N,64,K]   W = T diag(b e^G) Kn  (FMA path only)
- *   u, delta       f32 [S,N,V,64]   U = T diag(b) V, D = U - W S_n  (value-major)
+ *   u, delta       f32 [S,N,V,64]   U = T diag(b) V, D = U - W S_n  (value-major; on the
+ *                                   MFMA path u is in fragment order instead, per chunk
+ *                                   [ceil(V/32)][2][4][64][4]: strip c, row tile rt, group
+ *                                   g, lane l holds U rows 32rt + 8g + 4(l/32) + 0..3 of
+ *                                   column 32c + l%32, zero past V)
  *   tri            f32 [S,N,64,64]  T = (I + A)^-1
  *   gam, beta      f32 [S,N,64]     in-chunk cumulative log decay, beta (void rows 0)
  *   states         f32 [S,N,V,K]    state at the start of every chunk, value-major
@@ -81,10 +85,11 @@ typedef struct gpa_gdn_problem {
  * On the MFMA path (gpa_gdn_path() == 1) the sequential kernels read their
  * matrix operands as bf16 MFMA fragments written by the chunk kernel; with
  * K16 = K/16 and RB = ceil(K/32), per chunk:
- *   wrow  [2][K16][64][16]  W rows:     lane l of fragment (rt,ks) holds
- *                           W[32rt + l%32][16ks + 8(l/32) + e], e<8, as hi then lo
- *   wcol  [RB][4][64][16]   W^T rows:   fragment (rb,cs), lane l, element e is
- *                           W[16cs + 8(l/32) + e][32rb + l%32], hi then lo
+ *   wrow  [2][K16][2][64][8] W rows:    lane l of fragment (rt,ks) holds
+ *                           W[32rt + l%32][16ks + 8(l/32) + e], e<8, split
+ *                           into bf16 hi (plane 0) and lo = x - hi (plane 1)
+ *   wcol  [RB][4][2][64][8]  W^T rows:   fragment (rb,cs), lane l, element e is
+ *                           W[16cs + 8(l/32) + e][32rb + l%32], hi / lo planes
  *   krow  [2][K16][64][8]   Kn rows (exact in bf16), same placement as wrow
  *   kcol  [RB][4][64][8]    Kn^T rows, same placement as wcol
  *   qcol  [RB][4][64][8]    Qn^T rows (only with a query)
@@ -98,7 +103,8 @@ typedef struct gpa_gdn_saved {
  * NULL (no read gradient); dstates f32 [S,N,V,K] (value-major, like states)
  * injects gradients of the chunk-start states (NULL = none); dfinal f32
  * [S,K,V] (NULL = none).  Caller-owned f32 scratch: dd0, o, ddelta
- * [S,N,V,64], dhend [S,N,V,K], dw [S,N,64,K].  Gradient outputs: dq
+ * [S,N,V,64], dhend [S,N,V,K], dw [S,N,64,K]; on the MFMA path dd0 and o are
+ * in the fragment order of u (ceil(V/32) whole strips per chunk).  Gradient outputs: dq
  * (skipped when q was NULL), dk [.. K], dv [.. V] in the problem dtype
  * (rounded once from fp32); dg, dbeta f32 per token; ds0 [S,K,V] f32
  * contiguous. */
