@@ -36,13 +36,6 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 METRIC = "GPA attn fwd+bwd tokens/s @T=8192 bf16; decode tok/s; % of roofline"
 SHAPE = dict(heads=16, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64)
-# HBM bytes per launch of a kernel in this workload, from rocprofv3 FETCH_SIZE
-# (x2.0) and WRITE_SIZE (x1.0) passes calibrated on a 1 GiB copy
-# (profiles/dense_gpa_layer_T8192_pmc_traffic.md).  Used for `roofline.traffic`
-# when that kernel is the dominant one.  The state backward's figure is the
-# dispatch-weighted mean of its two instantiations (with and without a query).
-MEASURED_TRAFFIC = {"gdn_state_bwd_mfma<128>": (279254.2 * 2.0 + 247040.0) * 1024,
-                    "gdn_chunk_bwd_mfma<bf16,128>": (392730.9 * 2.0 + 129279.9) * 1024}
 BATCH, TOKENS = 1, 8192
 
 
@@ -131,8 +124,23 @@ def decode_rate(model, steps: int = 64, warmup: int = 8) -> dict:
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 
 
-def cpu_baseline(sample_tokens: int = 512) -> dict:
-    """The oracle (per-token reference algorithm, fp32) timed on this host."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline() -> dict:
+    """The oracle (per-token reference algorithm, fp32) timed on this host with
+    the reference benchmark's protocol (scripts/benchmark.py:44-54): 2 warm-up
+    runs, then 3 timed runs each at T=128 and T=256 (fwd+bwd of the training
+    workload's layer at B=1); and batched decode of the same layer at B=64
+    after a one-block (64-token) prefill, 8 timed one-token steps."""
     import torch
 
     import oracle
@@ -140,29 +148,66 @@ def cpu_baseline(sample_tokens: int = 512) -> dict:
     cores = len(os.sched_getaffinity(0))
     old = torch.get_num_threads()
     torch.set_num_threads(cores)
+    h, dk, dv = SHAPE["heads"], SHAPE["key_dim"], SHAPE["value_dim"]
+
+    def inputs(b, t):
+        q = torch.randn(b, t, h, dk)
+        k = torch.nn.functional.normalize(torch.randn_like(q), dim=-1)
+        return q, k, torch.randn(b, t, h, dv)
+
     try:
         torch.manual_seed(0)
         model = DenseGPA(GPAConfig(**SHAPE))
         run = oracle.OracleRun(model)
 
         def once(t):
-            q = torch.randn(BATCH, t, SHAPE["heads"], SHAPE["key_dim"])
-            k = torch.nn.functional.normalize(torch.randn_like(q), dim=-1)
-            v = torch.randn(BATCH, t, SHAPE["heads"], SHAPE["value_dim"])
-            xs = [x.requires_grad_() for x in (q, k, v)]
+            xs = [x.requires_grad_() for x in inputs(BATCH, t)]
             model.zero_grad(set_to_none=True)
             start = time.perf_counter()
             out, _ = run(*xs)
             out.float().square().mean().backward()
             return time.perf_counter() - start
 
-        once(8)  # page in
-        seconds = once(sample_tokens)
+        for _ in range(2):
+            once(32)
+        rates = {}
+        for t in (128, 256):
+            secs = [once(t) for _ in range(3)]
+            rates[t] = BATCH * t * len(secs) / sum(secs)
+        with torch.no_grad():
+            _, state = run(*inputs(DECODE_BATCH, 64))
+            toks = [inputs(DECODE_BATCH, 1) for _ in range(10)]
+            for x in toks[:2]:
+                _, state = run(*x, state)
+            start = time.perf_counter()
+            for x in toks[2:]:
+                _, state = run(*x, state)
+            step_s = (time.perf_counter() - start) / (len(toks) - 2)
     finally:
         torch.set_num_threads(old)
-    return {"value": BATCH * sample_tokens / seconds, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"oracle fwd+bwd of the same layer, fp32, B=1 T={sample_tokens} (1 timed run, "
-                      f"{seconds:.1f} s), {platform.processor() or platform.machine()}"}
+    return {"value": rates[256], "unit": "tokens/s", "cores": cores, "kind": "port",
+            "tokens_per_s_T128": rates[128], "tokens_per_s_T256": rates[256],
+            "decode": {"value": DECODE_BATCH / step_s, "unit": "tokens/s", "ms_per_token_step": step_s * 1e3,
+                       "batch": DECODE_BATCH},
+            "sample": f"oracle fwd+bwd of the same layer, fp32, B=1: 2 warm-ups (T=32), 3 timed runs at T=128 "
+                      f"and at T=256 (value = T=256); decode B=64 after a 64-token prefill, 8 timed steps; "
+                      f"{_cpu_model()}, {cores} threads"}
+
+
+def _measured_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (FETCH_SIZE x its copy-calibrated factor + WRITE_SIZE, KiB per dispatch),
+    or None when the summary has no row for it."""
+    path = os.path.join(ROOT, "profiles", "dense_gpa_layer_T8192_pmc_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 6 and cells[0].strip("`") == kernel:
+                    return (float(cells[4].replace(",", "")) + float(cells[5].replace(",", ""))) * 1e6
+    except OSError:
+        pass
+    return None
 
 
 def main() -> int:
@@ -226,9 +271,12 @@ def main() -> int:
     dominant = timer.dominant()
     roofline = None
     if dominant is not None:
+        chain = "_state_" in dominant["name"]
         roofline = {"bound": "mfma", "kernel": dominant["name"], "achieved": dominant["tflops"],
                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": dominant["tflops"] / PEAK_BF16_TFLOPS,
-                    "traffic": MEASURED_TRAFFIC.get(dominant["name"]),
+                    "traffic": _measured_traffic(dominant["name"]),
+                    "limited_by": ("latency of the sequential chunk chain (one state step per 64 tokens)"
+                                   if chain else "issue latency at one workgroup per CU"),
                     "avg_launch_us": dominant["avg_us"], "launches": dominant["launches"],
                     "share_of_step": dominant["total_ms"] / serial_ms,
                     "timed_in": f"one extra step on one stream ({serial_ms:.1f} ms)"}

@@ -4,7 +4,8 @@
 
 Compiles every gpa_amd/csrc/*.hip to an object under gpa_amd/_build/ and links
 gpa_amd/libgpa_hip.so.  Packed-FP32 instructions are disabled on purpose
-(`-packed-fp32-ops`): float arithmetic is emitted as scalar VALU ops.
+(`-packed-fp32-ops`): float arithmetic is emitted as scalar VALU ops.  MFMA
+results are kept in VGPRs (`-amdgpu-mfma-vgpr-form`).
 """
 from __future__ import annotations
 
@@ -22,6 +23,9 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include"),
          "-I", CSRC, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA accumulators in VGPRs: the element-wise work on accumulator
+         # tiles then needs no v_accvgpr_read/write copies.
+         "-mllvm", "-amdgpu-mfma-vgpr-form=1",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
 

@@ -215,6 +215,225 @@ __device__ __forceinline__ uint4 pack_bf8(const float (&x)[8]) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// r0 = softmax(base + gain tanh z) of a workgroup's RR rows, rounded to E,
+// with 32 lanes per row (8 columns each) and 8 rows per pass (VEC rows):
+// written to the saved rows sr0 and, when A is given, to the LDS tile
+// A [RR][lda] (zero beyond M, up to kM).
+template <typename E>
+__device__ __forceinline__ void rows_r0_vec(const gpa_route_problem& p, const Rows& rows, int row0, int h,
+                                            E* sr0, float* A, int lda, int kM) {
+  const int M = p.slots, R = p.batch * p.tokens, tid = threadIdx.x;
+  const int c = 8 * (tid & 31), rsub = tid >> 5;
+  const bool on = c < M;
+  float bv[VPASS][8];
+  uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+  for (int i = 0; i < VPASS; ++i) {
+    const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
+    if (on) {
+      const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
+      bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
+      bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
+#pragma unroll
+      for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+        if (e < p.incoming)
+          mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
+                                                     rows.at(p.msg[e], rr, h) + c);
+    }
+  }
+  const float gain = p.gain[h];
+  // edge weights read once (a load inside the row loop would wait behind the stores)
+  float ew[GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+  for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < p.incoming ? p.edge_weight[e * p.heads + h] : 0.f;
+#pragma unroll
+  for (int i = 0; i < VPASS; ++i) {
+    const int row = rsub + 8 * i, r = row0 + row;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
+    if (p.incoming > 0) {
+      float z[8] = {};
+#pragma unroll
+      for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+        if (e < p.incoming && on) {
+          const float w = ew[e];
+          float x[8];
+          unpack_bf8(mv[i][e], x);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) z[j] += w * x[j];
+        }
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += z[j];
+      const float mean = vsum32(s) / M;
+      float qq = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        z[j] = on ? z[j] - mean : 0.f;
+        qq += z[j] * z[j];
+      }
+      const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] += gain * tanhf(z[j] / sig);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
+    mx = vmax32(mx);
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = on ? __expf(v[j] - mx) : 0.f;
+      sm += v[j];
+    }
+    sm = vsum32(sm);
+    const bool valid = r < R;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (valid && on) ? round_as<E>(v[j] / sm) : 0.f;
+    if (A && c < kM) {
+      *reinterpret_cast<f32x4*>(&A[row * lda + c]) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(&A[row * lda + c + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+    }
+    if (valid && on) *reinterpret_cast<uint4*>(sr0 + (int64_t)r * M + c) = pack_bf8(v);
+  }
+}
+
+// Softmax and relation-read backward of a workgroup's RR rows (VEC rows: 32
+// lanes per row, 8 columns each, 8 rows per pass) from d r0 (d0v[pass][j],
+// the lane's columns of row rsub + 8 pass): writes d base and the message
+// gradients, and adds the lane's shares of d gain and d w_e.
+template <typename E>
+__device__ __forceinline__ void rows_bwd_vec(const gpa_route_problem& p, const gpa_route_grads& g, const Rows& rows,
+                                             int row0, int h, const float (&d0v)[VPASS][8], float& part_gain,
+                                             float (&part_w)[GPA_ROUTE_MAX_INCOMING]) {
+  const int M = p.slots, R = p.batch * p.tokens, H = p.heads, NI = p.incoming, tid = threadIdx.x;
+  const int c = 8 * (tid & 31), rsub = tid >> 5;
+  const bool on = c < M;
+  float bv[VPASS][8];
+  uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
+#pragma unroll
+  for (int i = 0; i < VPASS; ++i) {
+    const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
+    if (on) {
+      const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
+      bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
+      bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
+#pragma unroll
+      for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+        if (e < NI)
+          mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
+                                                     rows.at(p.msg[e], rr, h) + c);
+    }
+  }
+  const float gain = p.gain[h];
+  float ew[GPA_ROUTE_MAX_INCOMING];  // read once, as in the forward
+#pragma unroll
+  for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < NI ? p.edge_weight[e * H + h] : 0.f;
+#pragma unroll
+  for (int i = 0; i < VPASS; ++i) {
+    const int row = rsub + 8 * i, r = row0 + row;
+    const bool valid = r < R;
+    float v[8], z[8] = {}, thz[8] = {}, msgf[GPA_ROUTE_MAX_INCOMING][8], inv = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
+    if (NI > 0) {
+#pragma unroll
+      for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+        if (e < NI && on) {
+          const float w = ew[e];
+          unpack_bf8(mv[i][e], msgf[e]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) z[j] += w * msgf[e][j];
+        }
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += z[j];
+      const float mean = vsum32(s) / M;
+      float qq = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        z[j] = on ? z[j] - mean : 0.f;
+        qq += z[j] * z[j];
+      }
+      const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
+      inv = 1.f / sig;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        z[j] = z[j] / sig;
+        thz[j] = tanhf(z[j]);
+        v[j] += gain * thz[j];
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
+    mx = vmax32(mx);
+    float pr[8], sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = on ? __expf(v[j] - mx) : 0.f;
+      sm += pr[j];
+    }
+    sm = vsum32(sm);
+    float d0[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d0[j] = on ? d0v[i][j] : 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] /= sm;
+      s += pr[j] * d0[j];
+    }
+    s = vsum32(s);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = on ? pr[j] * (d0[j] - s) : 0.f;  // d base'
+    if (valid && on) {
+      float* db = reinterpret_cast<float*>(g.dbase.ptr) + rows.at(g.dbase, r, h) + c;
+      *reinterpret_cast<f32x4*>(db) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(db + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    }
+    if (NI > 0) {
+      float dz[8], szz = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float th = thz[j];
+        if (valid && on) part_gain += v[j] * th;
+        dz[j] = on ? gain * v[j] * (1.f - th * th) : 0.f;
+        szz += dz[j] * z[j];
+      }
+      const float mzz = vsum32(szz) / M;
+      float sc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        dz[j] = on ? (dz[j] - z[j] * mzz) * inv : 0.f;  // d centred
+        sc += dz[j];
+      }
+      const float mc = vsum32(sc) / M;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dz[j] -= mc;  // d incoming
+#pragma unroll
+      for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
+        if (e < NI && on) {
+          const float w = ew[e];
+          float sw = 0.f, dm[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            sw += dz[j] * msgf[e][j];
+            dm[j] = round_as<E>(w * dz[j]);
+          }
+          if (valid) {
+            part_w[e] += sw;
+            *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(g.dmsg[e].ptr) + rows.at(g.dmsg[e], r, h) + c) =
+                pack_bf8(dm);
+          }
+        }
+    }
+  }
+}
+
 template <typename E, bool VEC>
 __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
   using W = typename Wt<E>::type;
@@ -235,81 +454,7 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
 
   // ---- r0 = softmax(base + gain tanh z)
   if constexpr (VEC) {
-    const int c = 8 * (tid & 31), rsub = tid >> 5;
-    const bool on = c < M;
-    float bv[VPASS][8];
-    uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
-#pragma unroll
-    for (int i = 0; i < VPASS; ++i) {
-      const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
-      if (on) {
-        const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
-        bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
-        bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
-#pragma unroll
-        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-          if (e < p.incoming)
-            mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
-                                                       rows.at(p.msg[e], rr, h) + c);
-      }
-    }
-    const float gain = p.gain[h];
-    // edge weights read once (a load inside the row loop would wait behind the stores)
-    float ew[GPA_ROUTE_MAX_INCOMING];
-#pragma unroll
-    for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < p.incoming ? p.edge_weight[e * p.heads + h] : 0.f;
-#pragma unroll
-    for (int i = 0; i < VPASS; ++i) {
-      const int row = rsub + 8 * i, r = row0 + row;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
-      if (p.incoming > 0) {
-        float z[8] = {};
-#pragma unroll
-        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-          if (e < p.incoming && on) {
-            const float w = ew[e];
-            float x[8];
-            unpack_bf8(mv[i][e], x);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) z[j] += w * x[j];
-          }
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s += z[j];
-        const float mean = vsum32(s) / M;
-        float qq = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          z[j] = on ? z[j] - mean : 0.f;
-          qq += z[j] * z[j];
-        }
-        const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] += gain * tanhf(z[j] / sig);
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
-      mx = vmax32(mx);
-      float sm = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[j] = on ? __expf(v[j] - mx) : 0.f;
-        sm += v[j];
-      }
-      sm = vsum32(sm);
-      const bool valid = r < R;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = (valid && on) ? round_as<E>(v[j] / sm) : 0.f;
-      if (c < kM) {
-        *reinterpret_cast<f32x4*>(&A[row * lda + c]) = f32x4{v[0], v[1], v[2], v[3]};
-        *reinterpret_cast<f32x4*>(&A[row * lda + c + 4]) = f32x4{v[4], v[5], v[6], v[7]};
-      }
-      if (valid && on) *reinterpret_cast<uint4*>(sr0 + (int64_t)r * M + c) = pack_bf8(v);
-    }
+    rows_r0_vec<E>(p, rows, row0, h, sr0, A, lda, kM);
   } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
@@ -425,6 +570,452 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------- tiled products
+// The bf16 route reader with widths that are multiples of 64 runs the row
+// phases as their own kernels and each product as a tiled GEMM over all the
+// rows of a head (128 rows x BN columns per workgroup, operands staged
+// through LDS in 32-deep slabs, the weights read once per tile instead of
+// once per 32 rows), with the element-wise work of the product fused into the
+// epilogue.  The products are the fused kernel's, with the same operand and
+// result roundings and the same contraction order (ascending 16-deep steps
+// into one float32 accumulator), so both give the same bits.
+
+__global__ __launch_bounds__(RNT) void route_rows16(gpa_route_problem p) {
+  const int M = p.slots, R = p.batch * p.tokens;
+  const RouteTile rtile = route_tile();
+  const int h = rtile.h, row0 = rtile.tile * RR;
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, row0, R, p.tokens);
+  rows_r0_vec<bf16_t>(p, rows, row0, h, reinterpret_cast<bf16_t*>(p.r0) + (int64_t)h * R * M, nullptr, 0, 0);
+}
+
+constexpr int GM_BM = 128;           // rows per tile
+constexpr int GM_KS = 32;            // contraction slab
+constexpr int GM_LD = GM_KS + 8;     // LDS row pitch (bf16): 80 bytes
+constexpr int GM_NT = 256;
+
+// Row operand: element (h, r, k) at p + h * sh + r * sr + k.
+struct RowOp {
+  const bf16_t* p;
+  int64_t sh, sr;
+};
+// One product: rows of `a` (K wide) times a packed weight b [H][nb][ldb]
+// (output column n, contraction k contiguous: the layout route.py packs).
+struct Prod {
+  RowOp a;
+  const bf16_t* b;
+  int64_t nb, ldb;
+  int K;
+};
+struct GemmShape {
+  int R, N, H;
+};
+
+__device__ __forceinline__ float gelu_round(float x) { return round_as<bf16_t>(gelu(x)); }
+typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4n gelu_pack(u32x4n u) {
+  float x[8];
+  unpack_bf8(make_uint4(u.x, u.y, u.z, u.w), x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = gelu_round(x[e]);
+  const uint4 r = pack_bf8(x);
+  return u32x4n{r.x, r.y, r.z, r.w};
+}
+
+// acc[rt][ct] += A(rows) B over one product; the workgroup's tile is rows
+// row0 .. +127, columns col0 .. +BN-1 of head h; wave w computes rows
+// 64 (w / 2) .. +63 and columns (BN / 2)(w % 2) .. as 32x32 MFMA tiles.
+// GELU: the A operand is round(gelu(a)) of the stored rows.
+template <int BN, bool GELU>
+__device__ __forceinline__ void gemm_run(const Prod& pr, const GemmShape& sh, int h, int row0, int col0,
+                                         bf16_t (*As)[GM_BM * GM_LD], bf16_t (*Bs)[BN * GM_LD],
+                                         f32x16 (&acc)[2][BN / 64]) {
+  constexpr int TN = BN / 64, BP = BN * GM_KS / 8 / GM_NT;  // B pieces per thread (2 or 1)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wr = w >> 1, wc = w & 1;
+  const bf16_t* ap = pr.a.p + (int64_t)h * pr.a.sh;
+  const bf16_t* bp = pr.b + (int64_t)h * pr.nb * pr.ldb + (int64_t)col0 * pr.ldb;
+  // This thread's 16-byte pieces of each slab: A rows ar[i] (clamped to the
+  // last row), B rows br[i]; column offsets kq.
+  const bf16_t* ar[2];
+  const bf16_t* br[BP];
+  int alds[2], blds[BP];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int piece = tid + GM_NT * i, r = row0 + (piece >> 2);
+    ar[i] = ap + (int64_t)(r < sh.R ? r : sh.R - 1) * pr.a.sr + 8 * (piece & 3);
+    alds[i] = (piece >> 2) * GM_LD + 8 * (piece & 3);
+  }
+#pragma unroll
+  for (int i = 0; i < BP; ++i) {
+    const int piece = tid + GM_NT * i;
+    br[i] = bp + (int64_t)(piece >> 2) * pr.ldb + 8 * (piece & 3);
+    blds[i] = (piece >> 2) * GM_LD + 8 * (piece & 3);
+  }
+  const int steps = pr.K / GM_KS;
+  // (register arrays of a native vector type: arrays of HIP's uint4 struct
+  // are not always promoted to registers)
+  u32x4n ra[2], rb[BP];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) ra[i] = *reinterpret_cast<const u32x4n*>(ar[i]);
+#pragma unroll
+  for (int i = 0; i < BP; ++i) rb[i] = *reinterpret_cast<const u32x4n*>(br[i]);
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4n*>(&As[buf][alds[i]]) = GELU ? gelu_pack(ra[i]) : ra[i];
+#pragma unroll
+    for (int i = 0; i < BP; ++i) *reinterpret_cast<u32x4n*>(&Bs[buf][blds[i]]) = rb[i];
+    __syncthreads();
+    // the next slab's pieces (the last slab loads itself again, unused)
+    const int kn = (s + 1 < steps ? s + 1 : s) * GM_KS;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[i] = *reinterpret_cast<const u32x4n*>(ar[i] + kn);
+#pragma unroll
+    for (int i = 0; i < BP; ++i) rb[i] = *reinterpret_cast<const u32x4n*>(br[i] + kn);
+#pragma unroll
+    for (int ks = 0; ks < GM_KS / 16; ++ks) {
+      bf16x8 af[2], bf[TN];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        af[rt] = *reinterpret_cast<const bf16x8*>(&As[buf][(64 * wr + 32 * rt + (lane & 31)) * GM_LD + 16 * ks +
+                                                         8 * (lane >> 5)]);
+#pragma unroll
+      for (int ct = 0; ct < TN; ++ct)
+        bf[ct] = *reinterpret_cast<const bf16x8*>(&Bs[buf][((BN / 2) * wc + 32 * ct + (lane & 31)) * GM_LD +
+                                                           16 * ks + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < TN; ++ct) mma_bf16(acc[rt][ct], af[rt], bf[ct]);
+    }
+  }
+  // every wave is done with the slabs before the caller reuses the LDS
+  __syncthreads();
+}
+
+// Tile of a workgroup: heads slowest, so that each XCD serves a contiguous
+// run of heads and keeps their weights in its L2.
+struct GemmTile {
+  int h, row0, col0;
+};
+template <int BN>
+__device__ __forceinline__ GemmTile gemm_tile(const GemmShape& sh) {
+  const int ntn = sh.N / BN, ntr = (sh.R + GM_BM - 1) / GM_BM, per_head = ntn * ntr;
+  const int id = xcd_logical(blockIdx.x, gridDim.x);
+  const int h = id / per_head, rem = id % per_head;
+  return GemmTile{h, GM_BM * (rem / ntn), BN * (rem % ntn)};
+}
+
+// Eight consecutive bf16 / float32 values.
+__device__ __forceinline__ void ld8(const bf16_t* p, float (&x)[8]) { unpack_bf8(*reinterpret_cast<const uint4*>(p), x); }
+__device__ __forceinline__ void st8(bf16_t* p, const float (&x)[8]) { *reinterpret_cast<uint4*>(p) = pack_bf8(x); }
+__device__ __forceinline__ void ld8(const float* p, float (&x)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+__device__ __forceinline__ void st8(float* p, const float (&x)[8]) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+}
+
+// LDS of a product workgroup: the operand slabs, reused by the epilogue as a
+// float32 staging tile of PR rows.
+template <int BN>
+struct GemmLds {
+  static constexpr int PR = BN <= 128 ? 64 : 32, LDT = BN + 4;
+  static constexpr int SLABS = 2 * (GM_BM + BN) * GM_LD * 2, STAGE = PR * LDT * 4;
+  static constexpr int BYTES = SLABS > STAGE ? SLABS : STAGE;
+};
+
+// The epilogue: Epi::combine(acc, acc2) per element in registers; then, PR
+// rows at a time, the values go through LDS so that every thread handles
+// whole 8-column row pieces: pre = epi.load(h, r, c) for all of a thread's
+// pieces first, then epi.store(h, r, c, v, pre, epi.head(h)), whose return
+// values summed over each 32-row block go to epi.block_sum (Epi::kPart).
+template <int BN, bool GELU, bool DUAL, typename Epi>
+__global__ __launch_bounds__(GM_NT) void route_gemm16(Prod p1, Prod p2, GemmShape sh, Epi epi) {
+  constexpr int TN = BN / 64, PR = GemmLds<BN>::PR, LDT = GemmLds<BN>::LDT;
+  constexpr int VPR = BN / 8, NVT = PR * VPR / GM_NT;  // pieces per row, per thread and pass
+  __shared__ __align__(16) unsigned char smem[GemmLds<BN>::BYTES];
+  auto As = reinterpret_cast<bf16_t(*)[GM_BM * GM_LD]>(smem);
+  auto Bs = reinterpret_cast<bf16_t(*)[BN * GM_LD]>(smem + 2 * GM_BM * GM_LD * 2);
+  float* stage = reinterpret_cast<float*>(smem);
+  const GemmTile t = gemm_tile<BN>(sh);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wr = w >> 1, wc = w & 1;
+  f32x16 acc[2][TN], acc2[2][TN];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < TN; ++ct) acc[rt][ct] = acc2[rt][ct] = f32x16{};
+  gemm_run<BN, GELU>(p1, sh, t.h, t.row0, t.col0, As, Bs, acc);
+  if constexpr (DUAL) gemm_run<BN, false>(p2, sh, t.h, t.row0, t.col0, As, Bs, acc2);
+  const float hs = epi.head(t.h);
+  __shared__ float red[GM_NT / 64][2];
+#pragma unroll
+  for (int pass = 0; pass < GM_BM / PR; ++pass) {
+    // the 32-row tiles of this pass: rows 64 wr + 32 rt in [pass PR, pass PR + PR)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int rbase = 64 * wr + 32 * rt - pass * PR;
+      if (rbase >= 0 && rbase < PR) {
+#pragma unroll
+        for (int ct = 0; ct < TN; ++ct)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            stage[(rbase + acc_row(i, lane >> 5)) * LDT + (BN / 2) * wc + 32 * ct + (lane & 31)] =
+                epi.combine(acc[rt][ct][i], acc2[rt][ct][i]);
+      }
+    }
+    __syncthreads();
+    typename Epi::Pre pre[NVT];
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const int v = tid + GM_NT * j, r = t.row0 + pass * PR + v / VPR;
+      pre[j] = epi.load(t.h, r < sh.R ? r : t.row0, t.col0 + 8 * (v % VPR));  // the tile's first row is valid
+    }
+    float part0 = 0.f, part1 = 0.f;  // rows below / from 32 of the pass (registers, not a private array)
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const int v = tid + GM_NT * j, row = v / VPR, r = t.row0 + pass * PR + row;
+      float x[8];
+      ld8(stage + row * LDT + 8 * (v % VPR), x);
+      if (r < sh.R) {
+        const float y = epi.store(t.h, r, t.col0 + 8 * (v % VPR), x, pre[j], hs);
+        if (row < 32) part0 += y;
+        else part1 += y;
+      }
+    }
+    if constexpr (Epi::kPart) {
+      // A tile spans all N columns (BN == N), so a block's sum is complete here.
+#pragma unroll
+      for (int k = 0; k < PR / 32; ++k) {
+        float x = k ? part1 : part0;
+        for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+        if (lane == 0) red[w][k] = x;
+      }
+    }
+    __syncthreads();
+    if constexpr (Epi::kPart) {
+      if (tid < PR / 32) {
+        const int r0 = t.row0 + pass * PR + 32 * tid;
+        if (r0 < sh.R) epi.block_sum(t.h, r0 / RR, red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid]);
+      }
+    }
+  }
+}
+
+// h1 = round(r0 U), saved.
+struct EpiH1 {
+  static constexpr bool kPart = false;
+  bf16_t* h1;
+  int64_t sh, sr;
+  typedef int Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return a; }
+  __device__ Pre load(int, int, int) const { return 0; }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre, float) const {
+    st8(h1 + h * sh + r * sr + c, v);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+// hd = round(gelu(h1) D), saved; r1 = round(r0 + mlp_gain hd), the route output.
+struct EpiHd {
+  static constexpr bool kPart = false;
+  bf16_t* hd;
+  const bf16_t* r0;
+  int64_t sh, sr;  // of hd and r0: [H][R][M]
+  const float* mlp_gain;
+  bf16_t* route;
+  int64_t route_sh, route_sr;
+  typedef uint4 Pre;
+  __device__ float head(int h) const { return mlp_gain[h]; }
+  __device__ float combine(float a, float) const { return round_as<bf16_t>(a); }
+  __device__ Pre load(int h, int r, int c) const { return *reinterpret_cast<const uint4*>(r0 + h * sh + r * sr + c); }
+  __device__ float store(int h, int r, int c, const float (&d)[8], Pre r0v, float g) const {
+    st8(hd + h * sh + r * sr + c, d);
+    float x[8];
+    unpack_bf8(r0v, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] += g * d[j];
+    st8(route + h * route_sh + r * route_sr + c, x);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+// qo = round(round(r1 W_rs) + round(query_scale round(q W_qs))).
+struct EpiQo {
+  static constexpr bool kPart = false;
+  bf16_t* qo;
+  int64_t sh, sr;
+  float query_scale;
+  typedef int Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float a2) const {
+    return round_as<bf16_t>(a) + round_as<bf16_t>(query_scale * round_as<bf16_t>(a2));
+  }
+  __device__ Pre load(int, int, int) const { return 0; }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre, float) const {
+    st8(qo + h * sh + r * sr + c, v);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+
+// Backward.  d r1 = round(dqo W_rs^T) (+ d route, rounded) is kept in the
+// float32 d base buffer until the row kernel overwrites it; d hd = round(mlp_gain
+// d r1) and round(query_scale dqo) are saved rows; each 32-row block's
+// sum of d r1 . hd is d mlp_gain's partial.
+struct EpiDr1 {
+  static constexpr bool kPart = true;
+  const bf16_t* dqo;
+  const bf16_t* droute;  // may be null
+  int64_t io_sh, io_sr;  // dqo and d route rows ([B,T,H,M], uniformly strided)
+  const bf16_t* hd;
+  bf16_t *dhd, *dqs;
+  int64_t sh, sr;        // hd, dhd, dqs: [H][R][M]
+  float* dr1;            // d base [B,T,H,M] float32
+  int64_t dr_sh, dr_sr;
+  const float* mlp_gain;
+  float query_scale;
+  float* partials;       // [R / 32][H][2 + incoming], slot 0
+  int heads, nparts;
+  struct Pre {
+    uint4 dro, hd, dqo;
+  };
+  __device__ float head(int h) const { return mlp_gain[h]; }
+  __device__ float combine(float a, float) const { return round_as<bf16_t>(a); }
+  __device__ Pre load(int h, int r, int c) const {
+    const int64_t io = h * io_sh + r * io_sr + c;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    return Pre{droute ? *reinterpret_cast<const uint4*>(droute + io) : z,
+               *reinterpret_cast<const uint4*>(hd + h * sh + r * sr + c), *reinterpret_cast<const uint4*>(dqo + io)};
+  }
+  __device__ float store(int h, int r, int c, const float (&v)[8], const Pre& x, float gm) const {
+    float d[8], dro[8], hv[8], dq[8], dh[8];
+    unpack_bf8(x.dro, dro);
+    unpack_bf8(x.hd, hv);
+    unpack_bf8(x.dqo, dq);
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      d[j] = droute ? round_as<bf16_t>(v[j] + dro[j]) : v[j];
+      dh[j] = gm * d[j];
+      dq[j] *= query_scale;
+      part += d[j] * hv[j];
+    }
+    const int64_t o = h * sh + r * sr + c;
+    st8(dhd + o, dh);
+    st8(dqs + o, dq);
+    st8(dr1 + h * dr_sh + r * dr_sr + c, d);
+    return part;
+  }
+  __device__ void block_sum(int h, int blk, float x) const { partials[((int64_t)blk * heads + h) * nparts] = x; }
+};
+// d h1 = round(round(d hd D^T) gelu'(h1)), and round(gelu(h1)) for the weight
+// gradients (it shares gelu'(h1)'s erf).
+struct EpiDh1 {
+  static constexpr bool kPart = false;
+  const bf16_t* h1;
+  bf16_t *dh1, *hg;
+  int64_t sh, sr;  // [H][R][2M]
+  typedef uint4 Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return round_as<bf16_t>(a); }
+  __device__ Pre load(int h, int r, int c) const { return *reinterpret_cast<const uint4*>(h1 + h * sh + r * sr + c); }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre hv, float) const {
+    float x[8], d[8], gl[8];
+    unpack_bf8(hv, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      d[j] = v[j] * gelu_grad(x[j]);
+      gl[j] = gelu(x[j]);
+    }
+    const int64_t o = h * sh + r * sr + c;
+    st8(dh1 + o, d);
+    st8(hg + o, gl);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+// d r0 = round(d r1 + round(d h1 U^T)), in place of d r1.
+struct EpiDr0 {
+  static constexpr bool kPart = false;
+  float* dr;
+  int64_t sh, sr;
+  struct Pre {
+    float x[8];
+  };
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return round_as<bf16_t>(a); }
+  __device__ Pre load(int h, int r, int c) const {
+    Pre p;
+    ld8(dr + h * sh + r * sr + c, p.x);
+    return p;
+  }
+  __device__ float store(int h, int r, int c, const float (&v)[8], const Pre& d1, float) const {
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = round_as<bf16_t>(d1.x[j] + v[j]);
+    st8(dr + h * sh + r * sr + c, y);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+// d q = round(round(query_scale dqo) W_qs^T).
+struct EpiDq {
+  static constexpr bool kPart = false;
+  bf16_t* dq;
+  int64_t sh, sr;
+  typedef int Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return a; }
+  __device__ Pre load(int, int, int) const { return 0; }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre, float) const {
+    st8(dq + h * sh + r * sr + c, v);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+
+// Row backward of the tiled path: d r0 from the d base buffer (float32,
+// written by the products), then rows_bwd_vec; partial slots 1 and 2 + e.
+__global__ __launch_bounds__(RNT) void route_rows16_bwd(gpa_route_problem p, gpa_route_grads g) {
+  __shared__ float red[RW][1 + GPA_ROUTE_MAX_INCOMING];
+  const int M = p.slots, R = p.batch * p.tokens, H = p.heads, NI = p.incoming;
+  const RouteTile rtile = route_tile();
+  const int h = rtile.h, row0 = rtile.tile * RR, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, row0, R, p.tokens);
+  const int c = 8 * (tid & 31), rsub = tid >> 5, cc = c < M ? c : 0;
+  float d0v[VPASS][8];
+#pragma unroll
+  for (int i = 0; i < VPASS; ++i) {
+    const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
+    const float* src = reinterpret_cast<const float*>(g.dbase.ptr) + rows.at(g.dbase, rr, h) + cc;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src), b = *reinterpret_cast<const f32x4*>(src + 4);
+    d0v[i][0] = a.x; d0v[i][1] = a.y; d0v[i][2] = a.z; d0v[i][3] = a.w;
+    d0v[i][4] = b.x; d0v[i][5] = b.y; d0v[i][6] = b.z; d0v[i][7] = b.w;
+  }
+  // every lane has its d r0 values before any row of the workgroup is overwritten
+  __syncthreads();
+  float part_gain = 0.f, part_w[GPA_ROUTE_MAX_INCOMING] = {0.f, 0.f, 0.f};
+  rows_bwd_vec<bf16_t>(p, g, rows, row0, h, d0v, part_gain, part_w);
+  float vals[1 + GPA_ROUTE_MAX_INCOMING] = {part_gain, part_w[0], part_w[1], part_w[2]};
+#pragma unroll
+  for (int k = 0; k < 1 + GPA_ROUTE_MAX_INCOMING; ++k) {
+    float x = vals[k];
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    if (lane == 0) red[wave][k] = x;
+  }
+  __syncthreads();
+  if (tid < 1 + NI) {
+    float x = 0.f;
+    for (int w = 0; w < RW; ++w) x += red[w][tid];
+    g.partials[((int64_t)rtile.tile * H + h) * (2 + NI) + 1 + tid] = x;
   }
 }
 
@@ -630,131 +1221,16 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   // ---- softmax and relation-read backward of each row
   if constexpr (VEC) {
     const int c = 8 * (tid & 31), rsub = tid >> 5;
-    const bool on = c < M;
-    float bv[VPASS][8];
-    uint4 mv[VPASS][GPA_ROUTE_MAX_INCOMING];
+    float d0v[VPASS][8];
 #pragma unroll
     for (int i = 0; i < VPASS; ++i) {
-      const int r = row0 + rsub + 8 * i, rr = r < R ? r : R - 1;
-      if (on) {
-        const float* bp = reinterpret_cast<const float*>(p.base.ptr) + rows.at(p.base, rr, h) + c;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp), x1 = *reinterpret_cast<const f32x4*>(bp + 4);
-        bv[i][0] = x0.x; bv[i][1] = x0.y; bv[i][2] = x0.z; bv[i][3] = x0.w;
-        bv[i][4] = x1.x; bv[i][5] = x1.y; bv[i][6] = x1.z; bv[i][7] = x1.w;
-#pragma unroll
-        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-          if (e < NI)
-            mv[i][e] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.msg[e].ptr) +
-                                                       rows.at(p.msg[e], rr, h) + c);
-      }
+      const int row = rsub + 8 * i;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&A2[row * lda + (c < M ? c : 0)]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&A2[row * lda + (c < M ? c : 0) + 4]);
+      d0v[i][0] = a.x; d0v[i][1] = a.y; d0v[i][2] = a.z; d0v[i][3] = a.w;
+      d0v[i][4] = b.x; d0v[i][5] = b.y; d0v[i][6] = b.z; d0v[i][7] = b.w;
     }
-    const float gain = p.gain[h];
-    float ew[GPA_ROUTE_MAX_INCOMING];  // read once, as in the forward
-#pragma unroll
-    for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) ew[e] = e < NI ? p.edge_weight[e * H + h] : 0.f;
-#pragma unroll
-    for (int i = 0; i < VPASS; ++i) {
-      const int row = rsub + 8 * i, r = row0 + row;
-      const bool valid = r < R;
-      float v[8], z[8] = {}, thz[8] = {}, msgf[GPA_ROUTE_MAX_INCOMING][8], inv = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = on ? bv[i][e] : 0.f;
-      if (NI > 0) {
-#pragma unroll
-        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-          if (e < NI && on) {
-            const float w = ew[e];
-            unpack_bf8(mv[i][e], msgf[e]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) z[j] += w * msgf[e][j];
-          }
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s += z[j];
-        const float mean = vsum32(s) / M;
-        float qq = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          z[j] = on ? z[j] - mean : 0.f;
-          qq += z[j] * z[j];
-        }
-        const float sig = sqrtf(vsum32(qq) / M + 1e-5f);
-        inv = 1.f / sig;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          z[j] = z[j] / sig;
-          thz[j] = tanhf(z[j]);
-          v[j] += gain * thz[j];
-        }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mx = on ? fmaxf(mx, v[j]) : mx;
-      mx = vmax32(mx);
-      float pr[8], sm = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pr[j] = on ? __expf(v[j] - mx) : 0.f;
-        sm += pr[j];
-      }
-      sm = vsum32(sm);
-      float d0[8] = {};
-      if (on) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&A2[row * lda + c]);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(&A2[row * lda + c + 4]);
-        d0[0] = a.x; d0[1] = a.y; d0[2] = a.z; d0[3] = a.w; d0[4] = b.x; d0[5] = b.y; d0[6] = b.z; d0[7] = b.w;
-      }
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pr[j] /= sm;
-        s += pr[j] * d0[j];
-      }
-      s = vsum32(s);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = on ? pr[j] * (d0[j] - s) : 0.f;  // d base'
-      if (valid && on) {
-        float* db = reinterpret_cast<float*>(g.dbase.ptr) + rows.at(g.dbase, r, h) + c;
-        *reinterpret_cast<f32x4*>(db) = f32x4{v[0], v[1], v[2], v[3]};
-        *reinterpret_cast<f32x4*>(db + 4) = f32x4{v[4], v[5], v[6], v[7]};
-      }
-      if (NI > 0) {
-        float dz[8], szz = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float th = thz[j];
-          if (valid && on) part_gain += v[j] * th;
-          dz[j] = on ? gain * v[j] * (1.f - th * th) : 0.f;
-          szz += dz[j] * z[j];
-        }
-        const float mzz = vsum32(szz) / M;
-        float sc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          dz[j] = on ? (dz[j] - z[j] * mzz) * inv : 0.f;  // d centred
-          sc += dz[j];
-        }
-        const float mc = vsum32(sc) / M;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dz[j] -= mc;  // d incoming
-#pragma unroll
-        for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-          if (e < NI && on) {
-            const float w = ew[e];
-            float sw = 0.f, dm[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              sw += dz[j] * msgf[e][j];
-              dm[j] = round_as<E>(w * dz[j]);
-            }
-            if (valid) {
-              part_w[e] += sw;
-              *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(g.dmsg[e].ptr) + rows.at(g.dmsg[e], r, h) + c) =
-                  pack_bf8(dm);
-            }
-          }
-      }
-    }
+    rows_bwd_vec<E>(p, g, rows, row0, h, d0v, part_gain, part_w);
   } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
@@ -1147,12 +1623,107 @@ bool route_bwd_vec(const gpa_route_problem& p, const gpa_route_grads& g) {
 }  // namespace
 }  // namespace gpa
 
+namespace gpa {
+namespace {
+template <int BN, bool GELU, bool DUAL, typename Epi>
+void launch_gemm16(const Prod& a, const Prod& b, const GemmShape& sh, const Epi& epi, hipStream_t stream) {
+  const int n = sh.H * (sh.N / BN) * ((sh.R + GM_BM - 1) / GM_BM);
+  hipLaunchKernelGGL((route_gemm16<BN, GELU, DUAL, Epi>), dim3(n), dim3(GM_NT), 0, stream, a, b, sh, epi);
+}
+
+// The tiled bf16 path: widths multiples of 64, 16-byte rows, and the q, route
+// and qo rows uniformly strided (their row strides in rs_*).
+bool route_tiled(const gpa_route_problem& p, int64_t& rs_q, int64_t& rs_route, int64_t& rs_qo) {
+  return p.dtype == GPA_DTYPE_BF16 && p.slots % 64 == 0 && p.key_dim % 64 == 0 && route_vec(p) &&
+         vec_rows(p.route, 8) && vec_rows(p.qo, 8) && row_stride(p.q, p.batch, p.tokens, rs_q) &&
+         row_stride(p.route, p.batch, p.tokens, rs_route) && row_stride(p.qo, p.batch, p.tokens, rs_qo);
+}
+
+int route_forward_tiled(const gpa_route_problem& p, int64_t rs_q, int64_t rs_route, int64_t rs_qo,
+                        hipStream_t stream) {
+  const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens, H = p.heads;
+  const int64_t R64 = R;
+  hipLaunchKernelGGL(route_rows16, dim3((R + RR - 1) / RR, H), dim3(RNT), 0, stream, p);
+  const bf16_t* r0 = static_cast<const bf16_t*>(p.r0);
+  bf16_t* h1 = static_cast<bf16_t*>(p.h1);
+  bf16_t* hd = static_cast<bf16_t*>(p.hd);
+  bf16_t* route = static_cast<bf16_t*>(p.route.ptr);
+  // h1 = r0 U
+  const Prod up{RowOp{r0, R64 * M, M}, static_cast<const bf16_t*>(p.up_t), pad32(2 * M), pad16(M), M};
+  launch_gemm16<128, false, false>(up, up, GemmShape{R, 2 * M, H}, EpiH1{h1, R64 * 2 * M, 2 * M}, stream);
+  // hd = gelu(h1) D, r1 = r0 + mlp_gain hd
+  const Prod down{RowOp{h1, R64 * 2 * M, 2 * M}, static_cast<const bf16_t*>(p.down_t), pad32(M), pad16(2 * M),
+                  2 * M};
+  const EpiHd ehd{hd, r0, R64 * M, M, p.mlp_gain, route, p.route.sh, rs_route};
+  // qo = r1 W_rs + query_scale q W_qs
+  const Prod rs{RowOp{route, p.route.sh, rs_route}, static_cast<const bf16_t*>(p.rs_t), pad32(M), pad16(M), M};
+  const Prod qs{RowOp{static_cast<const bf16_t*>(p.q.ptr), p.q.sh, rs_q}, static_cast<const bf16_t*>(p.qs_t),
+                pad32(M), pad16(Dk), Dk};
+  const EpiQo eqo{static_cast<bf16_t*>(p.qo.ptr), p.qo.sh, rs_qo, p.query_scale};
+  if (M % 128 == 0) {
+    launch_gemm16<128, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
+    launch_gemm16<128, false, true>(rs, qs, GemmShape{R, M, H}, eqo, stream);
+  } else {
+    launch_gemm16<64, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
+    launch_gemm16<64, false, true>(rs, qs, GemmShape{R, M, H}, eqo, stream);
+  }
+  return check_launch("gpa_route_forward");
+}
+}  // namespace
+}  // namespace gpa
+
+namespace gpa {
+namespace {
+bool same_rows(const gpa_operand& a, const gpa_operand& b) { return a.sb == b.sb && a.st == b.st && a.sh == b.sh; }
+
+int route_backward_tiled(const gpa_route_problem& p, const gpa_route_grads& g, int64_t rs_dqo, int64_t rs_db,
+                         hipStream_t stream) {
+  const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens, H = p.heads;
+  const int64_t R64 = R;
+  const bf16_t* dqo = static_cast<const bf16_t*>(g.dqo.ptr);
+  bf16_t* dhd = static_cast<bf16_t*>(g.dhd);
+  bf16_t* dqs = static_cast<bf16_t*>(g.dqs);
+  bf16_t* dh1 = static_cast<bf16_t*>(g.dh1);
+  float* dr = static_cast<float*>(g.dbase.ptr);
+  // d r1 (into d base), d hd, round(query_scale dqo), d mlp_gain partials: BN = N = M
+  const Prod prs{RowOp{dqo, g.dqo.sh, rs_dqo}, static_cast<const bf16_t*>(p.rs), pad32(M), pad16(M), M};
+  const EpiDr1 e1{dqo, static_cast<const bf16_t*>(g.droute.ptr), g.dqo.sh, rs_dqo,
+                  static_cast<const bf16_t*>(p.hd), dhd, dqs, R64 * M, M, dr, g.dbase.sh, rs_db,
+                  p.mlp_gain, p.query_scale, g.partials, H, 2 + p.incoming};
+  const GemmShape sm{R, M, H};
+  if (M == 64) launch_gemm16<64, false, false>(prs, prs, sm, e1, stream);
+  else if (M == 128) launch_gemm16<128, false, false>(prs, prs, sm, e1, stream);
+  else launch_gemm16<256, false, false>(prs, prs, sm, e1, stream);
+  // d h1 = (d hd D^T) gelu'(h1), and round(gelu(h1))
+  const Prod pdown{RowOp{dhd, R64 * M, M}, static_cast<const bf16_t*>(p.down), pad32(2 * M), pad16(M), M};
+  const EpiDh1 e3{static_cast<const bf16_t*>(p.h1), dh1, static_cast<bf16_t*>(g.hg), R64 * 2 * M, 2 * M};
+  launch_gemm16<128, false, false>(pdown, pdown, GemmShape{R, 2 * M, H}, e3, stream);
+  // d r0 = d r1 + d h1 U^T (in place), d q = round(query_scale dqo) W_qs^T
+  const Prod pup{RowOp{dh1, R64 * 2 * M, 2 * M}, static_cast<const bf16_t*>(p.up), pad32(M), pad16(2 * M), 2 * M};
+  const EpiDr0 e4{dr, g.dbase.sh, rs_db};
+  const Prod pqs{RowOp{dqs, R64 * M, M}, static_cast<const bf16_t*>(p.qs), pad32(Dk), pad16(M), M};
+  int64_t rs_dq;
+  row_stride(g.dq, p.batch, p.tokens, rs_dq);
+  const EpiDq e5{static_cast<bf16_t*>(g.dq.ptr), g.dq.sh, rs_dq};
+  if (M % 128 == 0) launch_gemm16<128, false, false>(pup, pup, sm, e4, stream);
+  else launch_gemm16<64, false, false>(pup, pup, sm, e4, stream);
+  if (Dk % 128 == 0) launch_gemm16<128, false, false>(pqs, pqs, GemmShape{R, Dk, H}, e5, stream);
+  else launch_gemm16<64, false, false>(pqs, pqs, GemmShape{R, Dk, H}, e5, stream);
+  // softmax and relation-read backward of every row
+  hipLaunchKernelGGL(route_rows16_bwd, dim3((R + RR - 1) / RR, H), dim3(RNT), 0, stream, p, g);
+  return check_launch("gpa_route_backward");
+}
+}  // namespace
+}  // namespace gpa
+
 extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_route(problem)) return rc;
   if (!problem->up_t || !problem->down_t || !problem->rs_t || !problem->qs_t || !problem->qo.ptr ||
       !problem->route.ptr)
     return fail(GPA_HIP_EINVAL, "route: null forward weight or output");
+  int64_t rs_q, rs_route, rs_qo;
+  if (route_tiled(*problem, rs_q, rs_route, rs_qo)) return route_forward_tiled(*problem, rs_q, rs_route, rs_qo, stream);
   const int R = problem->batch * problem->tokens;
   const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
   const size_t lds = fwd_lds(*problem);
@@ -1178,6 +1749,16 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
     return fail(GPA_HIP_EINVAL, "route: null gradient buffer or backward weight");
   for (int e = 0; e < problem->incoming; ++e)
     if (!grads->dmsg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message gradient");
+  {
+    int64_t rs_q, rs_route, rs_qo, rs_dqo, rs_db, rs_dq;
+    if (route_tiled(*problem, rs_q, rs_route, rs_qo) && route_bwd_vec(*problem, *grads) &&
+        row_stride(grads->dqo, problem->batch, problem->tokens, rs_dqo) &&
+        row_stride(grads->dbase, problem->batch, problem->tokens, rs_db) &&
+        row_stride(grads->dq, problem->batch, problem->tokens, rs_dq) &&
+        vec_rows(grads->dq, 8) && (!grads->droute.ptr || (same_rows(grads->droute, grads->dqo) &&
+                                                           vec_rows(grads->droute, 8))))
+      return route_backward_tiled(*problem, *grads, rs_dqo, rs_db, stream);
+  }
   const int R = problem->batch * problem->tokens;
   const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
   const size_t lds = bwd_lds(*problem);

@@ -114,7 +114,10 @@ def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     if _active is None:
         return None
     e, km = _tag(dtype), _kmax(k)
-    state = f"gdn_state_fwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_fwd<{km}>"
+    if _mfma(k, dtype):
+        state = f"gdn_state_fwd_strip<{km}>" if km <= 128 else f"gdn_state_fwd_mfma<{km}>"
+    else:
+        state = f"gdn_state_fwd<{km}>"
     kernels = [(f"gdn_prep_mfma<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
                 (4 * c * k + 2 * c * v + c * c / 3) * tokens),
                (state, 4 * k * v * tokens)]
@@ -132,7 +135,10 @@ def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
     if read:
         dd0 = f"gdn_dd0_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_dd0<{e},{km}>"
         kernels.append((dd0, (2 * c * k + 2 * c * v) * tokens))
-    state = f"gdn_state_bwd_mfma<{km}>" if _mfma(k, dtype) else f"gdn_state_bwd<{e},{km}>"
+    if _mfma(k, dtype):
+        state = f"gdn_state_bwd_strip<{km}>" if km <= 128 else f"gdn_state_bwd_mfma<{km}>"
+    else:
+        state = f"gdn_state_bwd<{e},{km}>"
     kernels.append((state, (6 if read else 4) * k * v * tokens))
     chunk = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c
     if read:
@@ -204,21 +210,103 @@ def summarize_trace(path: str, gap_ms: float = 100.0, top: int = 25) -> str:
     return out
 
 
-def summarize_counters(path: str) -> str:
-    """Markdown table of a rocprofv3 `--pmc` counter_collection.csv: per kernel
-    and counter, the dispatch count and the mean value per dispatch."""
+def _kernel_name(raw: str) -> str:
+    return raw.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+
+
+def _read_counters(path: str) -> dict:
+    """{(kernel, counter): (dispatches, total)} of a rocprofv3 counter_collection.csv."""
     import csv
 
     stats: dict = {}
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
-            key = (r["Kernel_Name"].split("(")[0].replace("void ", "").replace("(anonymous namespace)::", ""),
-                   r["Counter_Name"])
+            key = (_kernel_name(r["Kernel_Name"]), r["Counter_Name"])
             c, t = stats.get(key, (0, 0.0))
             stats[key] = (c + 1, t + float(r["Counter_Value"]))
+    return stats
+
+
+def summarize_counters(path: str) -> str:
+    """Markdown table of a rocprofv3 `--pmc` counter_collection.csv: per kernel
+    and counter, the dispatch count and the mean value per dispatch."""
+    stats = _read_counters(path)
     lines = ["| kernel | counter | dispatches | mean per dispatch |", "|---|---|---:|---:|"]
     for (n, ctr), (c, t) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
         lines.append(f"| `{n[:90]}` | {ctr} | {c} | {t / c:.1f} |")
+    return "\n".join(lines) + "\n"
+
+
+def timer_name(kernel: str) -> str:
+    """The name `kernel_timer` gives a kernel of a trace: the namespace and
+    spaces dropped, bf16_t written bf16, and the state recurrences grouped by
+    their key width alone (their other template flags select variants)."""
+    n = kernel.replace("gpa::", "").replace("bf16_t", "bf16").replace(" ", "")
+    if n.startswith("gdn_state_") and "<" in n:
+        n = n.split(",")[0].rstrip(">") + ">"
+    return n
+
+
+def summarize_traffic(fetch: str, write: str, copy_fetch: str, copy_write: str, copy_bytes: int) -> str:
+    """HBM bytes per dispatch of every gdn kernel from a FETCH_SIZE and a
+    WRITE_SIZE pass (KiB per dispatch), each scaled by what the same counter
+    reads for a plain copy of `copy_bytes` bytes."""
+    f, w = _read_counters(fetch), _read_counters(write)
+    cf, cw = _read_counters(copy_fetch), _read_counters(copy_write)
+
+    def per_dispatch(stats, kernel, ctr):
+        c, t = stats[(kernel, ctr)]
+        return t / c
+
+    copy = "__amd_rocclr_copyBuffer"
+    kib = copy_bytes / 1024
+    sf = kib / per_dispatch(cf, copy, "FETCH_SIZE")
+    sw = kib / per_dispatch(cw, copy, "WRITE_SIZE")
+    groups: dict = {}
+    for (kernel, ctr), (c, t) in f.items():
+        if ctr != "FETCH_SIZE" or "gdn_" not in kernel or (kernel, "WRITE_SIZE") not in w:
+            continue
+        wc, wt = w[(kernel, "WRITE_SIZE")]
+        g = groups.setdefault(timer_name(kernel), [0, 0.0, 0.0])
+        g[0] += c
+        g[1] += t
+        g[2] += wt * c / wc  # the write pass may count dispatches differently; weight by the fetch pass
+    lines = [f"Copy calibration ({copy_bytes} bytes read and written): FETCH_SIZE x {sf:.3f}, WRITE_SIZE x {sw:.3f}.",
+             "", "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB read | HBM MB written |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for name, (c, ft, wt) in sorted(groups.items(), key=lambda kv: -(kv[1][1] * sf + kv[1][2] * sw) / kv[1][0]):
+        fk, wk = ft / c, wt / c
+        lines.append(f"| `{name}` | {c} | {fk:,.1f} | {wk:,.1f} | {fk * sf * 1.024e-3:,.1f} | {wk * sw * 1.024e-3:,.1f} |")
+    return "\n".join(lines) + "\n"
+
+
+def summarize_mfma(path: str, clock_mhz: float = 2400.0, xcds: int = 8, simds: int = 1024) -> str:
+    """MFMA use per gdn kernel from one `--pmc` pass holding GRBM_GUI_ACTIVE,
+    SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16/_F32 (512 FLOP per
+    unit), SQ_WAVE_CYCLES, SQ_WAIT_ANY and SQ_WAIT_INST_ANY: the kernel's
+    duration (GRBM_GUI_ACTIVE counts every XCD), the share of all SIMD cycles
+    in which an MFMA was busy, and the executed bf16 MFMA rate against the
+    2.5 PFLOP/s dense peak."""
+    s = _read_counters(path)
+    kernels = sorted({k for k, c in s if c == "SQ_VALU_MFMA_BUSY_CYCLES" and "gdn_" in k})
+    lines = ["| kernel | dispatches | us per dispatch | MFMA busy (% of SIMD cycles) | executed bf16 MFMA TFLOP/s "
+             "| % of bf16 peak | executed fp32 MFMA TFLOP/s | waves waiting (% of wave cycles) |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    rows = []
+    for k in kernels:
+        def mean(ctr):
+            c, t = s.get((k, ctr), (1, 0.0))
+            return t / c
+        n = s[(k, "SQ_VALU_MFMA_BUSY_CYCLES")][0]
+        cycles = mean("GRBM_GUI_ACTIVE") / xcds
+        us = cycles / clock_mhz
+        busy = mean("SQ_VALU_MFMA_BUSY_CYCLES") / (cycles * simds)
+        bf = mean("SQ_INSTS_VALU_MFMA_MOPS_BF16") * 512 / (us * 1e-6) / 1e12
+        f32 = mean("SQ_INSTS_VALU_MFMA_MOPS_F32") * 512 / (us * 1e-6) / 1e12
+        wait = mean("SQ_WAIT_ANY") / max(mean("SQ_WAVE_CYCLES"), 1.0)
+        rows.append((n * us, f"| `{timer_name(k)}` ({k.split('<')[-1].rstrip('>')}) | {n} | {us:,.1f} | "
+                             f"{100 * busy:.1f} | {bf:,.1f} | {100 * bf / 2500:.2f} | {f32:,.1f} | {100 * wait:.0f} |"))
+    lines += [r for _, r in sorted(rows, key=lambda x: -x[0])]
     return "\n".join(lines) + "\n"
 
 
@@ -238,12 +326,17 @@ def copy_kernel(nbytes: int, reps: int = 3) -> None:
 if __name__ == "__main__":
     import sys
 
-    cmd, arg = sys.argv[1], sys.argv[2]
+    cmd, args = sys.argv[1], sys.argv[2:]
     if cmd == "trace":
-        print(summarize_trace(arg))
+        print(summarize_trace(args[0]))
     elif cmd == "counters":
-        print(summarize_counters(arg))
+        print(summarize_counters(args[0]))
+    elif cmd == "traffic":
+        print(summarize_traffic(*args[:4], int(args[4])))
+    elif cmd == "mfma":
+        print(summarize_mfma(args[0]))
     elif cmd == "copy":
-        copy_kernel(int(arg))
+        copy_kernel(int(args[0]))
     else:
-        raise SystemExit("usage: python -m gpa_amd.profiling trace|counters <csv> | copy <bytes>")
+        raise SystemExit("usage: python -m gpa_amd.profiling trace|counters|mfma <csv> | "
+                         "traffic <fetch csv> <write csv> <copy fetch csv> <copy write csv> <copy bytes> | copy <bytes>")

@@ -1,0 +1,129 @@
+"""Route reader (gpa_route_forward / gpa_route_backward / gpa_route_weight_grads,
+csrc/route_reader.hip) through the C ABI: the tiled bf16 path (row kernels
+and 128-row MFMA products, taken when the widths are multiples of 64 and the
+q, route and qo rows are uniformly strided) against the one-kernel path of the
+same library on the same values (taken when q's rows are not uniformly
+strided: a [B, T+1, H, Dk] buffer viewed as [B, T, H, Dk]).  Both round where
+the reference's bf16 einsums round and contract in the same order, so every
+output and saved row must agree bit for bit.  The one-kernel path is itself
+pinned to the oracle by the module tests (test_gpu_dense_gpa.py) and the
+host-built kernel tests (test_route_emulated.py)."""
+import pytest
+import torch
+
+from gpa_amd import _lib
+from gpa_amd import route as rt
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _inputs(b, t, h, m, dk, n_in, seed):
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randn(b, t, h, m, generator=g)
+    q = torch.randn(b, t, h, dk, generator=g).to(BF)
+    msgs = [torch.randn(b, t, h, m, generator=g).to(BF) for _ in range(n_in)]
+    ew = torch.softmax(torch.randn(n_in, h, generator=g), 0) if n_in else torch.zeros(0, h)
+    gain = torch.rand(h, generator=g) + .5
+    mg = torch.rand(h, generator=g) + .5
+    up = torch.randn(h, m, 2 * m, generator=g) / m ** .5
+    down = torch.randn(h, 2 * m, m, generator=g) / (2 * m) ** .5
+    rs = torch.eye(m).expand(h, m, m) + .05 * torch.randn(h, m, m, generator=g)
+    qs = torch.randn(h, dk, m, generator=g) / dk ** .5
+    return [x.to(DEV) for x in (base, q, ew, gain, mg, up, down, rs, qs)], [x.to(DEV) for x in msgs]
+
+
+def _strided_copy(x):
+    """The same values in a [B, T+1, ...] buffer, viewed as [B, T, ...]: the
+    rows are then not uniformly strided when B > 1."""
+    big = torch.zeros(x.shape[0], x.shape[1] + 1, *x.shape[2:], device=x.device, dtype=x.dtype)
+    big[:, :x.shape[1]] = x
+    return big[:, :x.shape[1]]
+
+
+def _forward(args, msgs, q, query_scale=1 / 16):
+    base, _, ew, gain, mg, up, down, rs, qs = args
+    lib = _lib.load()
+    b, t, h, _ = q.shape
+    m = base.shape[-1]
+    weights = {"up_t": rt._pack(up, BF, True), "down_t": rt._pack(down, BF, True),
+               "rs_t": rt._pack(rs, BF, True), "qs_t": rt._pack(qs, BF, True)}
+    qo = torch.empty(b, t, h, m, device=DEV, dtype=BF)
+    route = torch.empty_like(qo)
+    saved = tuple(torch.empty(h, b * t, w, device=DEV, dtype=BF) for w in (m, 2 * m, m))
+    prob = rt._problem(base.contiguous(), q, ew.contiguous(), gain, mg, msgs, query_scale, weights,
+                       (qo, route), saved)
+    _lib.check(lib.gpa_route_forward(prob, _lib.stream_handle(q.device)), "gpa_route_forward")
+    torch.cuda.synchronize()
+    return {"qo": qo, "route": route, "r0": saved[0], "h1": saved[1], "hd": saved[2]}
+
+
+@pytest.mark.parametrize("b,t,h,m,dk,n_in", [(2, 100, 3, 128, 128, 3), (2, 70, 2, 256, 128, 3),
+                                             (2, 129, 2, 64, 64, 1), (2, 33, 1, 128, 64, 0)])
+def test_tiled_route_forward_matches_one_kernel_path(b, t, h, m, dk, n_in):
+    args, msgs = _inputs(b, t, h, m, dk, n_in, seed=b * 100 + t + m)
+    q = args[1]
+    tiled = _forward(args, msgs, q)
+    fused = _forward(args, msgs, _strided_copy(q))
+    for name, x in tiled.items():
+        y = fused[name]
+        assert torch.equal(x, y), f"{name}: max |diff| {(x.float() - y.float()).abs().max().item()}"
+    assert torch.isfinite(tiled["qo"].float()).all()
+
+
+def _backward(args, msgs, q, fwd, dqo, droute, query_scale=1 / 16):
+    base, _, ew, gain, mg, up, down, rs, qs = args
+    lib = _lib.load()
+    b, t, h, dk = q.shape
+    m = base.shape[-1]
+    rows = b * t
+    weights = {"up": rt._pack(up, BF, False), "down": rt._pack(down, BF, False),
+               "rs": rt._pack(rs, BF, False), "qs": rt._pack(qs, BF, False)}
+    saved = (fwd["r0"], fwd["h1"], fwd["hd"])
+    prob = rt._problem(base.contiguous(), q, ew.contiguous(), gain, mg, msgs, query_scale, weights,
+                       (fwd["route"], fwd["route"]), saved)
+    out = {"dbase": torch.empty(b, t, h, m, device=DEV), "dq": torch.empty(b, t, h, dk, device=DEV, dtype=BF),
+           "dh1": torch.empty(h, rows, 2 * m, device=DEV, dtype=BF),
+           "dhd": torch.empty(h, rows, m, device=DEV, dtype=BF),
+           "dqs": torch.empty(h, rows, m, device=DEV, dtype=BF),
+           "hg": torch.empty(h, rows, 2 * m, device=DEV, dtype=BF),
+           "partials": torch.full(((rows + _lib.ROUTE_ROWS - 1) // _lib.ROUTE_ROWS, h, 2 + len(msgs)), float("nan"),
+                                  device=DEV)}
+    dmsgs = [torch.empty_like(x) for x in msgs]
+    gr = _lib.RouteGrads()
+    gr.dqo, gr.droute = _lib.operand(dqo), _lib.operand(droute)
+    gr.dbase, gr.dq = _lib.operand(out["dbase"]), _lib.operand(out["dq"])
+    for e, x in enumerate(dmsgs):
+        gr.dmsg[e] = _lib.operand(x)
+    gr.dh1, gr.dhd, gr.dqs = out["dh1"].data_ptr(), out["dhd"].data_ptr(), out["dqs"].data_ptr()
+    gr.hg, gr.partials = out["hg"].data_ptr(), out["partials"].data_ptr()
+    _lib.check(lib.gpa_route_backward(prob, gr, _lib.stream_handle(q.device)), "gpa_route_backward")
+    torch.cuda.synchronize()
+    for e, x in enumerate(dmsgs):
+        out[f"dmsg{e}"] = x
+    return out
+
+
+@pytest.mark.parametrize("b,t,h,m,dk,n_in,with_droute", [(2, 100, 3, 128, 128, 3, True), (2, 70, 2, 256, 128, 3, False),
+                                                         (2, 129, 2, 64, 64, 1, True), (2, 33, 1, 128, 64, 0, False)])
+def test_tiled_route_backward_matches_one_kernel_path(b, t, h, m, dk, n_in, with_droute):
+    """d base, d messages, d q, the saved gradient rows and every partial sum
+    agree bit for bit, except d mlp_gain's partials (slot 0), which the tiled
+    path sums over a block's rows in another order (relative 1e-5)."""
+    args, msgs = _inputs(b, t, h, m, dk, n_in, seed=7 * b + t + m)
+    q = args[1]
+    fwd = _forward(args, msgs, q)
+    g = torch.Generator().manual_seed(t)
+    dqo = torch.randn(b, t, h, m, generator=g).to(BF).to(DEV)
+    droute = torch.randn(b, t, h, m, generator=g).to(BF).to(DEV) if with_droute else None
+    tiled = _backward(args, msgs, q, fwd, dqo, droute)
+    fused = _backward(args, msgs, _strided_copy(q), fwd, dqo, droute)
+    for name, x in tiled.items():
+        y = fused[name]
+        if name == "partials":
+            assert torch.equal(x[..., 1:], y[..., 1:]), "partials of d gain / d w_e"
+            assert torch.allclose(x[..., 0], y[..., 0], rtol=1e-5, atol=1e-6 * y[..., 0].abs().max().item())
+            assert torch.isfinite(x).all()
+        else:
+            assert torch.equal(x, y), f"{name}: max |diff| {(x.float() - y.float()).abs().max().item()}"
