@@ -1631,10 +1631,14 @@ void launch_gemm16(const Prod& a, const Prod& b, const GemmShape& sh, const Epi&
   hipLaunchKernelGGL((route_gemm16<BN, GELU, DUAL, Epi>), dim3(n), dim3(GM_NT), 0, stream, a, b, sh, epi);
 }
 
-// The tiled bf16 path: widths multiples of 64, 16-byte rows, and the q, route
-// and qo rows uniformly strided (their row strides in rs_*).
+// The tiled bf16 path: widths multiples of 64, 16-byte rows, the q, route and
+// qo rows uniformly strided (their row strides in rs_*), and enough rows per
+// head to fill 128-row tiles (a few rows, as in one-token decode, stay on the
+// one-kernel path).
+constexpr int TILED_MIN_ROWS = 1024;
 bool route_tiled(const gpa_route_problem& p, int64_t& rs_q, int64_t& rs_route, int64_t& rs_qo) {
-  return p.dtype == GPA_DTYPE_BF16 && p.slots % 64 == 0 && p.key_dim % 64 == 0 && route_vec(p) &&
+  return p.dtype == GPA_DTYPE_BF16 && p.slots % 64 == 0 && p.key_dim % 64 == 0 &&
+         p.batch * p.tokens >= TILED_MIN_ROWS && route_vec(p) &&
          vec_rows(p.route, 8) && vec_rows(p.qo, 8) && row_stride(p.q, p.batch, p.tokens, rs_q) &&
          row_stride(p.route, p.batch, p.tokens, rs_route) && row_stride(p.qo, p.batch, p.tokens, rs_qo);
 }
