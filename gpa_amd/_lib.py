@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -134,6 +134,26 @@ class SlotGrads(ctypes.Structure):
     _fields_ = [(n, Operand) for n in ("dslot", "draw", "dkey")] + [(n, c_vp) for n in ("dcenter", "dgate_w")]
 
 
+class GateProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "dtype")] + \
+               [("raw", Operand), ("bias", c_vp), ("beta_max", ctypes.c_float), ("decay_scale", ctypes.c_float)] + \
+               [(n, c_vp) for n in ("g_in", "b_in", "g_out", "b_out")]
+
+
+TOKEN_LOGITS_MAX_SLOTS = 256
+
+
+class TokenLogitsProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "heads", "slots", "dtype")] + \
+               [("raw", Operand), ("write", Operand), ("count0", c_vp), ("count0_sb", c_i64)] + \
+               [(n, c_vp) for n in ("gain", "scale", "logits", "count", "local")]
+
+
+class MixProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "value_dim", "levels", "dtype")] + \
+               [("read", Operand * DECODE_MAX_LEVELS), ("weights", c_vp), ("out", Operand)]
+
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -161,6 +181,9 @@ EXPORTS = {
                                   ctypes.c_int),
     "gpa_slot_gates_forward": ([ctypes.POINTER(SlotProblem), c_vp], ctypes.c_int),
     "gpa_slot_gates_backward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(SlotGrads), c_vp], ctypes.c_int),
+    "gpa_gate_act_forward": ([ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
+    "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
+    "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
 }
 
 _lib = None

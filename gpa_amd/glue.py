@@ -1,0 +1,60 @@
+"""Element-wise glue of the inference path in one launch each
+(`gpa_gate_act_forward`, `gpa_token_logits_forward`, `gpa_output_mix_forward`,
+csrc/token_glue.hip): the gate nonlinearities of a level (reference
+attention.py:161-174), one token's counts, base logits and local read
+distribution (:316-323, :196-204, :330) and the output mix (:340-341).  They
+carry no autograd: the schedule uses them when no gradient is recorded."""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def gate_act(raw: Tensor, bias: Tensor, beta_max: float, decay_scale: float):
+    """(g_in, b_in, g_out, b_out), each float32 [B,T,H], from the gate inputs
+    raw [B,T,H,4] and the bias [H,4]."""
+    lib = _lib.load()
+    b, t, h, _ = raw.shape
+    outs = [torch.empty(b, t, h, device=raw.device, dtype=torch.float32) for _ in range(4)]
+    bias = bias.detach().float().contiguous()
+    p = _lib.GateProblem(b, t, h, _lib.DTYPE_CODES[raw.dtype], _lib.operand(raw), bias.data_ptr(),
+                         float(beta_max), float(decay_scale), *(o.data_ptr() for o in outs))
+    _lib.check(lib.gpa_gate_act_forward(p, _lib.stream_handle(raw.device)), "gpa_gate_act_forward")
+    return tuple(outs)
+
+
+def token_logits(raw: Tensor, write: Tensor, count0: Tensor, gain: Tensor, scale: Tensor):
+    """(logits [B,1,H,M] float32, counts [B,H,M] float32, local [B,1,H,M] in
+    raw's dtype) of one token of one level."""
+    lib = _lib.load()
+    b, _, h, m = raw.shape
+    c0 = count0.float()
+    if c0.stride(2) != 1 or c0.stride(1) != m:
+        c0 = c0.contiguous()
+    gain, scale = gain.detach().float().contiguous(), scale.detach().float().contiguous()
+    logits = torch.empty(b, 1, h, m, device=raw.device, dtype=torch.float32)
+    count = torch.empty(b, h, m, device=raw.device, dtype=torch.float32)
+    local = torch.empty(b, 1, h, m, device=raw.device, dtype=raw.dtype)
+    p = _lib.TokenLogitsProblem(b, h, m, _lib.DTYPE_CODES[raw.dtype], _lib.operand(raw), _lib.operand(write),
+                                c0.data_ptr(), c0.stride(0), gain.data_ptr(), scale.data_ptr(),
+                                logits.data_ptr(), count.data_ptr(), local.data_ptr())
+    _lib.check(lib.gpa_token_logits_forward(p, _lib.stream_handle(raw.device)), "gpa_token_logits_forward")
+    return logits, count, local
+
+
+def output_mix(reads, weights: Tensor) -> Tensor:
+    """sum_j weights[j][h] reads[j], rounded to the reads' dtype."""
+    lib = _lib.load()
+    b, t, h, dv = reads[0].shape
+    out = torch.empty_like(reads[0])
+    w = weights.detach().float().contiguous()
+    p = _lib.MixProblem()
+    p.batch, p.tokens, p.heads, p.value_dim, p.levels = b, t, h, dv, len(reads)
+    p.dtype = _lib.DTYPE_CODES[reads[0].dtype]
+    for j, r in enumerate(reads):
+        p.read[j] = _lib.operand(r)
+    p.weights, p.out = w.data_ptr(), _lib.operand(out)
+    _lib.check(lib.gpa_output_mix_forward(p, _lib.stream_handle(out.device)), "gpa_output_mix_forward")
+    return out

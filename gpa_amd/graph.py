@@ -16,6 +16,8 @@ from __future__ import annotations
 
 import torch
 
+from . import params
+
 
 class GradientGraph:
     def __init__(self, model, inputs, loss_fn, warmups: int = 3):
@@ -65,6 +67,11 @@ class DecodeGraph:
     position of a block the new cache is copied back into them (one state
     copy per block).
 
+    Tensors derived from the parameters alone (packed weight layouts, gate
+    constants) are computed once and read by the graphs (`params.frozen`), so
+    the parameters must not change while the graphs are in use: `step` raises
+    if one has.
+
     `step(q, k, v)` ([B,1,H,D] like the captured token) copies the token into
     the static inputs, replays the graph of the current position and returns
     that position's output buffer.  The buffers are allocated outside the
@@ -91,7 +98,8 @@ class DecodeGraph:
         current = torch.cuda.current_stream()
         side = torch.cuda.Stream()
         side.wait_stream(current)
-        with torch.no_grad(), torch.cuda.stream(side):
+        self._params = [(p, p._version) for p in model.parameters()]
+        with torch.no_grad(), torch.cuda.stream(side), params.frozen():
             s = self.start
             for _ in range(warmups):
                 _, s = model(*self.inputs, s)
@@ -102,7 +110,7 @@ class DecodeGraph:
         # One output buffer per position, from the ordinary allocator.
         self.outputs = [torch.empty_like(self.inputs[2]) for _ in range(self.chunk)]
         s = self.start
-        with torch.no_grad():
+        with torch.no_grad(), params.frozen():
             for o in range(self.chunk):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=self.pool):
@@ -117,6 +125,8 @@ class DecodeGraph:
             raise RuntimeError("DecodeGraph: the cache after a block does not match the cache it started from")
 
     def step(self, q, k, v):
+        if any(p._version != ver for p, ver in self._params):
+            raise RuntimeError("DecodeGraph: a parameter changed after capture; build a new DecodeGraph")
         for static, value in zip(self.inputs, (q, k, v)):
             if static.shape != value.shape or static.dtype != value.dtype:
                 raise ValueError("DecodeGraph replays only the captured token shape/dtype")

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, params
 
 
 def supported(cfg, dtype: torch.dtype, slots: int) -> bool:
@@ -33,7 +33,12 @@ def _pad(x: int, m: int) -> int:
 def _pack(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
     """[H,K,N] weight -> [H,N32,K16] rows of the contraction for each output
     column (transpose=True), or [H,K,N] -> [H,K32,N16] (transpose=False:
-    output column = K, contraction = N); rounded to `dtype`, zero padded."""
+    output column = K, contraction = N); rounded to `dtype`, zero padded.
+    Cached while the weight is unchanged (params.derived)."""
+    return params.derived(("route_pack", id(w), dtype, transpose), (w,), lambda: _pack_now(w, dtype, transpose))
+
+
+def _pack_now(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
     w = w.detach().to(dtype)
     if transpose:
         w = w.transpose(1, 2)

@@ -28,7 +28,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from . import _lib
+from . import _lib, glue, params
 from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_token_hip, gdn_token_read, token_step_supported
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
@@ -146,7 +146,10 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
 
 class _Level:
     __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "final_count", "logits", "a_final",
-                 "b_final", "a_starts", "b_starts", "b_read")
+                 "b_final", "a_starts", "b_starts", "b_read", "local")
+
+    def __init__(self):
+        self.local = None  # the local read distribution, when the counts kernel gave it
 
 
 def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, position_ids: Tensor,
@@ -180,7 +183,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         else:
             slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
             g_in, b_in, g_out, b_out = _gates(model, key, j, control)
-        eta = 1 + .25 * model.residual_raw[j].tanh()
+        eta = _etas(model)[j]
         write = _assignment(cfg, slot)
         fused_level = write is None and _FUSED_LEVEL[0] and fused_level_supported(
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
@@ -223,14 +226,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         key, value = key_next, value_next
 
     # ---- relations, attention.py:206-223
-    local = [lv.logits.softmax(-1).to(dtype) for lv in levels]
+    local = [lv.local if lv.local is not None else lv.logits.softmax(-1).to(dtype) for lv in levels]
     incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan, token)
 
     # ---- route reader, attention.py:225-262
     routes, queries = _bridge(model, q, [lv.logits for lv in levels], incoming, [lv.counts for lv in levels])
 
     # ---- outer reads and level mix, attention.py:333-341
-    weights = model.output_logits.softmax(0)
+    ol = model.output_logits
+    weights = params.derived(("out_w", id(ol)), (ol,), lambda: ol.softmax(0), differentiable=True)
 
     def outer_read(lv, qo, s0):
         if lv.b_read is not None:
@@ -240,10 +244,14 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
                           (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
                          for j, (lv, qo) in enumerate(zip(levels, queries))])
-    out = 0
-    for j, read in enumerate(reads):
-        out = out + weights[j][..., None] * read
-    out = out.to(v.dtype)
+    if _GLUE[0] and not torch.is_grad_enabled() and all(r.dtype == v.dtype for r in reads) \
+            and len(reads) <= _lib.DECODE_MAX_LEVELS:
+        out = glue.output_mix(reads, weights)
+    else:
+        out = 0
+        for j, read in enumerate(reads):
+            out = out + weights[j][..., None] * read
+        out = out.to(v.dtype)
 
     # ---- new cache, attention.py:342-344
     new_offset = (offset + tokens) % chunk
@@ -359,12 +367,15 @@ def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | Non
     else:
         src = key if cfg.rsa_update else _unit(key)
         raw = _mm(src, w, "bthd,hdc->bthc", key.dtype)
+    tier = ((1., .1, .01, .001)[j] if cfg.levels == 4 else .1 ** j) if cfg.rsa_update else 1.
+    if _GLUE[0] and not torch.is_grad_enabled() and raw.dtype in _lib.DTYPE_CODES:
+        return glue.gate_act(raw, model.gate_bias[j], cfg.beta_max,
+                             0. if cfg.positional_mode == "none" else tier)
     raw = raw.float() + model.gate_bias[j]
     g_in, b_in, g_out, b_out = raw.unbind(-1)
     g_in = -F.softplus(g_in).clamp(max=10.)
     g_out = -F.softplus(g_out).clamp(max=10.)
     if cfg.rsa_update:
-        tier = (1., .1, .01, .001)[j] if cfg.levels == 4 else .1 ** j
         g_in, g_out = g_in * tier, g_out * tier
     if cfg.positional_mode == "none":
         g_in, g_out = g_in * 0, g_out * 0
@@ -385,22 +396,30 @@ def _base_logits(model, raw: Tensor, counts: Tensor, j: int) -> Tensor:
 def _count_scalars(model, j: int, like: Tensor):
     """Per-head count gain and read scale of level j, as [H] tensors."""
     cfg = model.config
-    gain = F.softplus(model.count_gain_raw[j])
+    raw = model.count_gain_raw
+    gain = params.derived(("count_gain", id(raw)), (raw,), lambda: F.softplus(raw), differentiable=True)[j]
     if cfg.learn_read_scale:
         scale = model.read_log_scale[j].clamp(math.log(.25), math.log(64.)).exp()
     else:
-        scale = torch.full((cfg.heads,), float(cfg.read_scale), device=like.device)
+        scale = params.derived(("read_scale", cfg.heads, float(cfg.read_scale), like.device), (),
+                               lambda: torch.full((cfg.heads,), float(cfg.read_scale), device=like.device))
     return gain, scale
 
 
 _FUSED_COUNTS = [True]  # counts and base logits in HIP (counts.py)
+_GLUE = [True]  # one-launch gate, one-token logits and output-mix kernels without autograd (glue.py)
 _FUSED_SLOTS = [True]  # slot products and gate inputs in HIP (slots.py)
+
+
+def _etas(model) -> Tensor:
+    """1 + .25 tanh(residual_raw), [L,H,2] (attention.py:192)."""
+    raw = model.residual_raw
+    return params.derived(("eta", id(raw)), (raw,), lambda: 1 + .25 * raw.tanh(), differentiable=True)
 
 
 def _residual(model, key, value, rk, rv, j):
     """attention.py:190-194."""
-    eta = 1 + .25 * model.residual_raw[j].tanh()
-    return _residual_eta(key, value, rk, rv, eta)
+    return _residual_eta(key, value, rk, rv, _etas(model)[j])
 
 
 def _residual_eta(key, value, rk, rv, eta):
@@ -436,6 +455,12 @@ def _level_logits(model, lv, j: int, raw: Tensor, old: LevelState) -> None:
     """Counts after every token and the level's base logits (attention.py:
     319-323 and :165-175) into lv."""
     cfg = model.config
+    if (_GLUE[0] and not torch.is_grad_enabled() and raw.shape[1] == 1 and raw.dtype in _lib.DTYPE_CODES
+            and lv.write.dtype == raw.dtype and lv.write.shape[-1] <= _lib.TOKEN_LOGITS_MAX_SLOTS):
+        gain, scale = _count_scalars(model, j, raw)
+        lv.logits, lv.final_count, lv.local = glue.token_logits(raw, lv.write, old.count, gain, scale)
+        lv.counts = lv.final_count[:, None]
+        return
     if _FUSED_COUNTS[0] and fused_counts_supported(cfg, raw.dtype, lv.write.shape[-1]):
         gain, scale = _count_scalars(model, j, raw)
         lv.logits, lv.final_count = count_logits(raw, lv.write, old.count, gain, scale)
@@ -450,11 +475,12 @@ def _relations(model, local, writes, rel_states, scan, token=False):
     """Every ordered edge's R_ij scan (attention.py:206-223); one token step
     per edge when `token` (inference on one token)."""
     cfg = model.config
-    # Every edge's decay and write strength [E,H], in three launches.
-    decay = -F.softplus(model.relation_decay_raw)
-    if cfg.positional_mode == "none":
-        decay = decay * 0
-    strength = model.relation_beta_raw.sigmoid()
+    # Every edge's decay and write strength [E,H].
+    rd, rb = model.relation_decay_raw, model.relation_beta_raw
+    decay = params.derived(("rel_decay", id(rd), cfg.positional_mode == "none"), (rd,),
+                           lambda: -F.softplus(rd) * (0. if cfg.positional_mode == "none" else 1.),
+                           differentiable=True)
+    strength = params.derived(("rel_beta", id(rb)), (rb,), lambda: rb.sigmoid(), differentiable=True)
 
     def edge(e, i, j, old):
         def run():
@@ -485,7 +511,16 @@ def _incoming_index(model, j: int) -> Tensor:
     """Device index of the edges into level j (i-major order), built from the
     module's edge-target buffer so that no host copy happens inside a graph
     capture."""
-    return (model._edge_target == j).nonzero_static(size=model.config.levels - 1)[:, 0]
+    target = model._edge_target
+    return params.derived(("edge_in", id(target), j), (target,),
+                          lambda: (target == j).nonzero_static(size=model.config.levels - 1)[:, 0])
+
+
+def _incoming_weights(model, j: int) -> Tensor:
+    """Softmax of the logits of the edges into level j over those edges, [n_in,H]."""
+    logits = model.edge_logits
+    return params.derived(("edge_w", id(logits), j), (logits, model._edge_target),
+                          lambda: logits.index_select(0, _incoming_index(model, j)).softmax(0), differentiable=True)
 
 
 _FUSED_ROUTE = [True]  # the fused route reader for the default read (route.py)
@@ -498,8 +533,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
     routes, queries = [], []
     for j, base in enumerate(logits):
         if _FUSED_ROUTE[0] and fused_route_supported(cfg, dtype, base.shape[-1]):
-            w = (model.edge_logits.index_select(0, _incoming_index(model, j)).softmax(0)
-                 if incoming[j] else None)
+            w = _incoming_weights(model, j) if incoming[j] else None
             qo, route = route_reader(base, q, w, model.relation_gain[j], model.route_mlp_gain[j],
                                      model.route_up[j], model.route_down[j], model.route_weight[j],
                                      model.query_weight[j], cfg.query_scale, [msg for _, msg in incoming[j]])
@@ -507,7 +541,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
             queries.append(qo)
             continue
         if incoming[j]:
-            w = model.edge_logits.index_select(0, _incoming_index(model, j)).softmax(0)
+            w = _incoming_weights(model, j)
             total = 0
             if cfg.paper_product_read:
                 for wt, (e, msg) in zip(w, incoming[j]):

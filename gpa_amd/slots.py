@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, params
 
 
 def supported(cfg, key: Tensor, slots: int) -> bool:
@@ -50,8 +50,10 @@ class _SlotGates(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         lib = _lib.load()
         b, t, h, _ = key.shape
-        cb = center.detach().to(key.dtype).contiguous()
-        wg = gate_w.detach().to(key.dtype).contiguous()
+        cb = params.derived(("slot_center", id(center), key.dtype), (center,),
+                            lambda: center.detach().to(key.dtype).contiguous())
+        wg = params.derived(("slot_gate_w", id(gate_w), key.dtype), (gate_w,),
+                            lambda: gate_w.detach().to(key.dtype).contiguous())
         slot = key.new_empty(b, t, h, cb.shape[1])
         raw = key.new_empty(b, t, h, 4)
         prob = _problem(key, cb, None, wg, slot, raw)

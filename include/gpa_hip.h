@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 14
+#define GPA_HIP_ABI_VERSION 15
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -414,6 +414,52 @@ typedef struct gpa_slot_grads {
 
 int gpa_slot_gates_forward(const gpa_slot_problem *problem, hipStream_t stream);
 int gpa_slot_gates_backward(const gpa_slot_problem *problem, const gpa_slot_grads *grads, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Element-wise glue of the inference path (no autograd), one launch each.
+ *
+ * Gate nonlinearities of one level for every token (reference _gates,
+ * attention.py:166-174, after the gate-input product):
+ *   x = float(raw) + bias;   g_in  = -min(softplus(x0), 10) * decay_scale
+ *   b_in  = beta_max sigmoid(x1);   g_out = -min(softplus(x2), 10) * decay_scale
+ *   b_out = beta_max sigmoid(x3)
+ * decay_scale: 0 for positional_mode "none", the rsa tier, otherwise 1.
+ * Outputs: float32 [B,T,H], contiguous. */
+typedef struct gpa_gate_problem {
+    int32_t batch, tokens, heads, dtype;
+    gpa_operand raw;                              /* [B,T,H,4] gate inputs */
+    const float *bias;                            /* [H][4] */
+    float beta_max, decay_scale;
+    float *g_in, *b_in, *g_out, *b_out;           /* out [B,T,H] */
+} gpa_gate_problem;
+int gpa_gate_act_forward(const gpa_gate_problem *problem, hipStream_t stream);
+
+/* One token (T = 1) of one level's slot counts, base logits and local read
+ * distribution (attention.py:316-317, _base_logits :196-204, the softmax of
+ * :330): n = count0 + write;  logits = scale raw + gain log1p(n);
+ * local = softmax(logits) rounded to the activation type. */
+#define GPA_TOKEN_LOGITS_MAX_SLOTS 256
+typedef struct gpa_token_logits_problem {
+    int32_t batch, heads, slots, dtype;
+    gpa_operand raw, write;                       /* [B,1,H,M] */
+    const float *count0;                          /* [B,H,M] (head slices contiguous) */
+    int64_t count0_sb;                            /* its batch stride (0: broadcast) */
+    const float *gain, *scale;                    /* [H] */
+    float *logits;                                /* out [B,1,H,M] float32, contiguous */
+    float *count;                                 /* out [B,H,M], contiguous */
+    void *local;                                  /* out [B,1,H,M], contiguous */
+} gpa_token_logits_problem;
+int gpa_token_logits_forward(const gpa_token_logits_problem *problem, hipStream_t stream);
+
+/* Output mix (attention.py:340-341): out = sum_j w[j][h] read_j, in level
+ * order, rounded to the activation type. */
+typedef struct gpa_mix_problem {
+    int32_t batch, tokens, heads, value_dim, levels, dtype;
+    gpa_operand read[GPA_DECODE_MAX_LEVELS];      /* [B,T,H,Dv] per level */
+    const float *weights;                         /* [L][H] float32 */
+    gpa_operand out;                              /* [B,T,H,Dv] */
+} gpa_mix_problem;
+int gpa_output_mix_forward(const gpa_mix_problem *problem, hipStream_t stream);
 
 #ifdef __cplusplus
 }
