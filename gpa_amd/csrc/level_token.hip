@@ -126,6 +126,148 @@ __global__ __launch_bounds__(QNT) void level_token(gpa_level_problem p) {
   }
 }
 
+
+// The same step with every snapshot value in registers: all loads of the
+// workgroup (A^ and B^ as float4 pieces) are issued before the first sum, so
+// each stream costs one memory round trip.  Thread t holds the float4 column
+// group t % (M/4) of A^ rows t / (M/4) + i NT/(M/4) and the group t % (Dv/4) of
+// B^ rows t / (Dv/4) + i NT/(Dv/4) (i < 16).  Widths multiples of 4 with
+// (M/4) and (Dv/4) dividing NT, Dk M / 4 and M Dv / 4 at most 16 NT.
+constexpr int RQ = 16;  // float4 pieces of A^ (and of B^) per thread
+
+template <typename E, int NT>
+__global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
+  constexpr int NW = NT / 64;
+  __shared__ float uk[256], wf[256], zp[NT * 4], rks[256];
+  __shared__ float red[NW], soft[2];
+  const int s = blockIdx.x, b = s / p.heads, h = s - b * p.heads;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int Dk = p.key_dim, Dv = p.value_dim, M = p.slots;
+  const int ga = M / 4, gb = Dv / 4;          // float4 groups per row
+  const int ra = NT / ga, rb = NT / gb;       // rows per pass
+  const int ca = t % ga, cb = t % gb;
+  const float4* A = reinterpret_cast<const float4*>(p.a_first + (int64_t)b * p.a_first_sb + (int64_t)h * Dk * M);
+  const float4* Bh = reinterpret_cast<const float4*>(p.b_first + (int64_t)b * p.b_first_sb + (int64_t)h * M * Dv);
+  const E* key = reinterpret_cast<const E*>(p.key.ptr) + op_base(p.key, b, h);
+  const E* val = reinterpret_cast<const E*>(p.value.ptr) + op_base(p.value, b, h);
+  const int na = Dk * ga, nb = M * gb;       // float4 pieces of each snapshot
+  float4 av[RQ], bv[RQ];
+#pragma unroll
+  for (int i = 0; i < RQ; ++i) {
+    const int fa = t + NT * i, fb = t + NT * i;
+    av[i] = A[fa < na ? fa : 0];
+    bv[i] = Bh[fb < nb ? fb : 0];
+  }
+  const float xk = t < Dk ? to_f32(key[t < Dk ? t : 0]) : 0.f;
+  const float xv = t < Dv ? to_f32(val[t < Dv ? t : 0]) : 0.f;
+  const float eta0 = p.eta[2 * h], eta1 = p.eta[2 * h + 1];
+
+  // u(key) = key / max(||key||, 1e-6) in float32, rounded to the activation type.
+  const float sk = sum64(xk * xk);
+  if (lane == 0) red[wave] = sk;
+  __syncthreads();
+  float nk2 = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) nk2 += red[w];
+  const float nk = fmaxf(sqrtf(nk2), 1e-6f);
+  if (t < Dk) uk[t] = round_as<E>(xk / nk);
+  __syncthreads();
+
+  // Logits z[m] = sum_k u(key)[k] A^[k][m]: partials over the thread's rows,
+  // then over the ra threads of a column group.
+  {
+    float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+      const int row = t / ga + ra * i;
+      if (row < Dk) {
+        const float u = uk[row];
+        z0 += u * av[i].x; z1 += u * av[i].y; z2 += u * av[i].z; z3 += u * av[i].w;
+      }
+    }
+    const int part = t / ga;
+    *reinterpret_cast<float4*>(&zp[part * M + 4 * ca]) = make_float4(z0, z1, z2, z3);
+    __syncthreads();
+    if (t < M) {
+      float zt = 0.f;
+      for (int q = 0; q < ra; ++q) zt += zp[q * M + t];
+      wf[t] = zt;
+    }
+    __syncthreads();
+  }
+
+  // Softmax over the M logits; the write is rounded to the activation type.
+  if (wave == 0) {
+    float mx = -INFINITY;
+    for (int m = lane; m < M; m += 64) mx = fmaxf(mx, wf[m]);
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sm = 0.f;
+    for (int m = lane; m < M; m += 64) sm += expf(wf[m] - mx);
+    sm = sum64(sm);
+    if (lane == 0) {
+      soft[0] = mx;
+      soft[1] = sm;
+    }
+  }
+  __syncthreads();
+  float wt = 0.f;
+  if (t < M) {
+    wt = round_as<E>(expf(wf[t] - soft[0]) / soft[1]);
+    reinterpret_cast<E*>(p.write.ptr)[op_base(p.write, b, h) + t] = from_f32<E>(wt);
+  }
+  __syncthreads();  // every thread has read wf[t] for the softmax before it is overwritten
+  if (t < M) wf[t] = wt;
+  __syncthreads();
+
+  // rk[k] = sum_m A^[k][m] w[m]: each row's ga column groups are ga
+  // consecutive lanes (32 or 64) of one wave.
+  {
+    const float4 w4 = *reinterpret_cast<const float4*>(&wf[4 * ca]);
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+      float d = av[i].x * w4.x + av[i].y * w4.y + av[i].z * w4.z + av[i].w * w4.w;
+      for (int o = ga >> 1; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
+      const int row = t / ga + ra * i;
+      if (ca == 0 && row < Dk) rks[row] = d;
+    }
+  }
+  // rv[v] = sum_m w[m] B^[m][v]: partials over the thread's rows, then over
+  // the rb threads of a column group.
+  {
+    float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+      const int row = t / gb + rb * i;
+      if (row < M) {
+        const float w = wf[row];
+        r0 += w * bv[i].x; r1 += w * bv[i].y; r2 += w * bv[i].z; r3 += w * bv[i].w;
+      }
+    }
+    __syncthreads();  // zp's logit partials are no longer read
+    *reinterpret_cast<float4*>(&zp[(t / gb) * Dv + 4 * cb]) = make_float4(r0, r1, r2, r3);
+  }
+  __syncthreads();
+  if (t < Dv) {
+    float rv = 0.f;
+    for (int q = 0; q < rb; ++q) rv += zp[q * Dv + t];
+    reinterpret_cast<E*>(p.value_out.ptr)[op_base(p.value_out, b, h) + t] = from_f32<E>(xv - eta1 * round_as<E>(rv));
+  }
+  if (t < Dk)
+    reinterpret_cast<E*>(p.key_out.ptr)[op_base(p.key_out, b, h) + t] = from_f32<E>(xk - eta0 * round_as<E>(rks[t]));
+}
+
+// Threads for the register kernel (0: the shape is not covered).
+int reg_threads(const gpa_level_problem& p) {
+  const int Dk = p.key_dim, Dv = p.value_dim, M = p.slots;
+  if (M % 4 || Dv % 4 || (reinterpret_cast<uintptr_t>(p.a_first) | reinterpret_cast<uintptr_t>(p.b_first)) % 16 ||
+      p.a_first_sb % 4 || p.b_first_sb % 4)
+    return 0;
+  for (int nt : {256, 512}) {
+    if (nt % (M / 4) || nt % (Dv / 4)) continue;
+    if ((int64_t)Dk * M / 4 <= (int64_t)RQ * nt && (int64_t)M * Dv / 4 <= (int64_t)RQ * nt) return nt;
+  }
+  return 0;
+}
 }  // namespace
 }  // namespace gpa
 
@@ -142,7 +284,19 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
       !p.value_out.ptr)
     return fail(GPA_HIP_EINVAL, "level token: null pointer (the snapshots a_first and b_first are required)");
   const dim3 grid((unsigned)((int64_t)p.batch * p.heads));
-  if (p.dtype == GPA_DTYPE_BF16) hipLaunchKernelGGL(level_token<bf16_t>, grid, dim3(QNT), 0, stream, p);
-  else hipLaunchKernelGGL(level_token<float>, grid, dim3(QNT), 0, stream, p);
+  const bool bf = p.dtype == GPA_DTYPE_BF16;
+  switch (reg_threads(p)) {
+    case 256:
+      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 256>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((level_token_reg<float, 256>), grid, dim3(256), 0, stream, p);
+      break;
+    case 512:
+      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 512>), grid, dim3(512), 0, stream, p);
+      else hipLaunchKernelGGL((level_token_reg<float, 512>), grid, dim3(512), 0, stream, p);
+      break;
+    default:
+      if (bf) hipLaunchKernelGGL(level_token<bf16_t>, grid, dim3(QNT), 0, stream, p);
+      else hipLaunchKernelGGL(level_token<float>, grid, dim3(QNT), 0, stream, p);
+  }
   return check_launch("gpa_level_token_forward");
 }
