@@ -144,6 +144,15 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
     return torch.cat((first.unsqueeze(2).to(starts.dtype), starts[:, :, 1:]), dim=2)
 
 
+def _outer_token(lv, slot, value, g_out, b_out, s0):
+    """The read of a level's one-token outer step: the B_j step and its read
+    with the route query in one kernel; the new state goes to lv.b_final."""
+    def read(qo):
+        out, lv.b_final = gdn_token_hip(qo, slot, value, g_out, b_out, s0)
+        return out
+    return read
+
+
 class _Level:
     __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "final_count", "logits", "a_final",
                  "b_final", "a_starts", "b_starts", "b_read", "local")
@@ -189,11 +198,12 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
         if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
             raw, a_final = gdn_token_hip(q, key, slot, g_in, b_in, old.inner)
-            b_final = gdn_token_hip(None, slot, value, g_out, b_out, old.outer)[1]
-            lv.b_read = lambda qo, s=b_final: gdn_token_read(qo, s)
+            # The B_j step runs at its read, after the route reader (nothing
+            # before needs the new B_j): one pass over the state for both.
+            lv.b_read = _outer_token(lv, slot, value, g_out, b_out, old.outer)
             write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
-            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, None, None
+            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
             _level_logits(model, lv, j, raw, old)
             levels.append(lv)
             key, value = key_next, value_next
@@ -244,6 +254,10 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
                           (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
                          for j, (lv, qo) in enumerate(zip(levels, queries))])
+    if not (_SERIAL[0] or torch.cuda.is_current_stream_capturing()):
+        for lv in levels:  # states made by a one-token outer step on a side stream
+            if lv.b_starts is None and lv.b_final is not None:
+                lv.b_final.record_stream(torch.cuda.current_stream())
     if _GLUE[0] and not torch.is_grad_enabled() and all(r.dtype == v.dtype for r in reads) \
             and len(reads) <= _lib.DECODE_MAX_LEVELS:
         out = glue.output_mix(reads, weights)
