@@ -118,8 +118,9 @@ def decode_rate(model, steps: int = 64, warmup: int = 8) -> dict:
     gbs = moved / seconds / 1e9
     return {"value": DECODE_BATCH / seconds, "unit": "tokens/s", "batch": DECODE_BATCH,
             "ms_per_token_step": seconds * 1e3, "eager_ms_per_token_step": eager_s * 1e3, "steps": steps,
-            "path": "schedule T=1 segments (one-token scan steps gdn_token_step, block-snapshot level mix) "
-                    "replayed from one HIP graph per block position; the fused one-kernel step is switched off",
+            "path": "schedule T=1 segments (one-token scan steps gdn_token_step, register-resident block-snapshot "
+                    "level kernel, one-launch gate/logit/mix glue, cached parameter layouts) replayed from one HIP "
+                    "graph per block position; the fused one-kernel step is switched off",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 

@@ -237,6 +237,11 @@ def summarize_counters(path: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+def _ours(kernel: str) -> bool:
+    """A kernel of this library's scans or route reader."""
+    return "gdn_" in kernel or "route_" in kernel
+
+
 def timer_name(kernel: str) -> str:
     """The name `kernel_timer` gives a kernel of a trace: the namespace and
     spaces dropped, bf16_t written bf16, and the state recurrences grouped by
@@ -264,7 +269,7 @@ def summarize_traffic(fetch: str, write: str, copy_fetch: str, copy_write: str, 
     sw = kib / per_dispatch(cw, copy, "WRITE_SIZE")
     groups: dict = {}
     for (kernel, ctr), (c, t) in f.items():
-        if ctr != "FETCH_SIZE" or "gdn_" not in kernel or (kernel, "WRITE_SIZE") not in w:
+        if ctr != "FETCH_SIZE" or not _ours(kernel) or (kernel, "WRITE_SIZE") not in w:
             continue
         wc, wt = w[(kernel, "WRITE_SIZE")]
         g = groups.setdefault(timer_name(kernel), [0, 0.0, 0.0])
@@ -288,7 +293,7 @@ def summarize_mfma(path: str, clock_mhz: float = 2400.0, xcds: int = 8, simds: i
     in which an MFMA was busy, and the executed bf16 MFMA rate against the
     2.5 PFLOP/s dense peak."""
     s = _read_counters(path)
-    kernels = sorted({k for k, c in s if c == "SQ_VALU_MFMA_BUSY_CYCLES" and "gdn_" in k})
+    kernels = sorted({k for k, c in s if c == "SQ_VALU_MFMA_BUSY_CYCLES" and _ours(k)})
     lines = ["| kernel | dispatches | us per dispatch | MFMA busy (% of SIMD cycles) | executed bf16 MFMA TFLOP/s "
              "| % of bf16 peak | executed fp32 MFMA TFLOP/s | waves waiting (% of wave cycles) |",
              "|---|---:|---:|---:|---:|---:|---:|---:|"]
