@@ -15,8 +15,8 @@ kernel's achieved rate against the bf16 MFMA peak: algorithmic FLOP per launch
 extra step in which the schedule runs on one stream (no kernel overlaps
 another, so the interval is the kernel's own run time and agrees with a rocprof
 kernel trace of that step).  `step_roofline` is the whole step's algorithmic
-FLOP over the timed step time; `decode` is the batched one-token decode rate
-(B=64 streams of the same layer) with its HBM roofline from the state bytes a
+FLOP over the timed step time; `decode` is the batched one-token decode rate (B=64 streams of the same layer, 2048-token
+prefill, 256 graph-replayed steps) with its HBM roofline from the state bytes a
 token step must move; `cpu_baseline` times the CPU oracle (the reference's
 per-token torch algorithm) on a bounded sample.
 """
@@ -71,14 +71,17 @@ def decode_state_bytes(dk: int, dv: int, slots) -> int:
     return 4 * (3 * (dk * s + s * dv) + 2 * rel + 2 * s)
 
 
-def decode_rate(model, steps: int = 64, warmup: int = 8) -> dict:
+def decode_rate(model, steps: int = 256, warmup: int = 64, prefill: int = 2048) -> dict:
     """Batched one-token decode through the model's cache (chunk mode, T=1 per
     call), B=64 streams of the same layer, bf16, under no_grad, on the path
     that serves it: the schedule's T=1 segments (one-token steps that read
     and write each state once), replayed from one HIP graph per block
-    position (`DecodeGraph`).  The timed steps span a whole block, so the
-    once-per-block state copy of the graph cycle is included.  The eager
-    rate of the same steps is reported beside it."""
+    position (`DecodeGraph`).  The cache is first prefilled over `prefill`
+    tokens of N(0,1) q, k (k normalised), v, in 512-token calls (chunk mode
+    carries the cache exactly across calls that end on block boundaries);
+    after one untimed cycle of replays (`warmup`) the timed steps span whole
+    blocks, so the once-per-block state copy of the graph cycle is included.
+    The eager rate of 64 steps from the same cache is reported beside it."""
     import torch
 
     from gpa_amd import DecodeGraph
@@ -87,42 +90,55 @@ def decode_rate(model, steps: int = 64, warmup: int = 8) -> dict:
     h, dk, dv = cfg.heads, cfg.key_dim, cfg.value_dim
     gen = torch.Generator(device=dev).manual_seed(1)
 
-    def token():
-        q = torch.randn(DECODE_BATCH, 1, h, dk, device=dev, generator=gen).bfloat16()
-        k = torch.nn.functional.normalize(torch.randn(DECODE_BATCH, 1, h, dk, device=dev, generator=gen), dim=-1)
-        v = torch.randn(DECODE_BATCH, 1, h, dv, device=dev, generator=gen).bfloat16()
+    def tokens(t):
+        q = torch.randn(DECODE_BATCH, t, h, dk, device=dev, generator=gen).bfloat16()
+        k = torch.nn.functional.normalize(torch.randn(DECODE_BATCH, t, h, dk, device=dev, generator=gen), dim=-1)
+        v = torch.randn(DECODE_BATCH, t, h, dv, device=dev, generator=gen).bfloat16()
         return q, k.bfloat16(), v
 
-    toks = [token() for _ in range(warmup + steps)]
-
-    def timed(run):
-        for i in range(warmup):
-            run(toks[i])
-        torch.cuda.synchronize()
-        start = time.perf_counter()
-        for i in range(warmup, warmup + steps):
-            run(toks[i])
-        torch.cuda.synchronize()
-        return (time.perf_counter() - start) / steps
-
+    _progress(f"decode: {prefill}-token prefill at B={DECODE_BATCH}")
     with torch.no_grad():
-        box = [model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)]
+        state = model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)
+        for _ in range(prefill // 512):
+            _, state = model(*tokens(512), state)
+        torch.cuda.synchronize()
+        toks = [tokens(1) for _ in range(warmup + steps)]
+
+        def timed(run, n_warm, n_timed):
+            for i in range(n_warm):
+                run(toks[i])
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            for i in range(n_warm, n_warm + n_timed):
+                run(toks[i])
+            torch.cuda.synchronize()
+            return (time.perf_counter() - start) / n_timed
+
+        box = [state]
 
         def eager(x):
             _, box[0] = model(*x, box[0])
-        eager_s = timed(eager)
-        graphed = DecodeGraph(model, model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16), *toks[0])
-        seconds = timed(lambda x: graphed.step(*x))
+        _progress("decode: eager token steps")
+        eager_s = timed(eager, 8, 64)
+        del box
+        _progress("decode: graph capture and replays")
+        graphed = DecodeGraph(model, state, *toks[0])
+        seconds = timed(lambda x: graphed.step(*x), warmup, steps)
         del graphed
     moved = decode_state_bytes(dk, dv, cfg.slots) * DECODE_BATCH * h
     gbs = moved / seconds / 1e9
     return {"value": DECODE_BATCH / seconds, "unit": "tokens/s", "batch": DECODE_BATCH,
-            "ms_per_token_step": seconds * 1e3, "eager_ms_per_token_step": eager_s * 1e3, "steps": steps,
+            "ms_per_token_step": seconds * 1e3, "eager_ms_per_token_step": eager_s * 1e3,
+            "prefill_tokens": prefill, "warmup_steps": warmup, "steps": steps,
             "path": "schedule T=1 segments (one-token scan steps gdn_token_step, register-resident block-snapshot "
                     "level kernel, one-launch gate/logit/mix glue, cached parameter layouts) replayed from one HIP "
                     "graph per block position; the fused one-kernel step is switched off",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
+
+
+def _progress(what: str) -> None:
+    print(f"bench: {what}", file=sys.stderr, flush=True)
 
 
 def _cpu_model() -> str:
@@ -141,7 +157,8 @@ def cpu_baseline() -> dict:
     the reference benchmark's protocol (scripts/benchmark.py:44-54): 2 warm-up
     runs, then 3 timed runs each at T=128 and T=256 (fwd+bwd of the training
     workload's layer at B=1); and batched decode of the same layer at B=64
-    after a one-block (64-token) prefill, 8 timed one-token steps."""
+    after a one-block (64-token) prefill, 8 timed one-token steps (the step
+    cost does not depend on the prefill length: the cache is fixed-size)."""
     import torch
 
     import oracle
@@ -243,6 +260,7 @@ def main() -> int:
         out, _ = model(*xs)
         out.float().square().mean().backward()
 
+    _progress("training step: warm-up and timed steps")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -260,6 +278,7 @@ def main() -> int:
     # big-grid kernel also waits for CUs held by its neighbours).  The idle gap
     # before it marks the step in a rocprof kernel trace
     # (`python -m gpa_amd.profiling trace <kernel_trace.csv>` summarises it).
+    _progress("training step: one-stream step with kernel timers")
     time.sleep(0.3)
     with schedule.one_stream(), profiling.kernel_timer() as timer:
         serial_start = time.perf_counter()
@@ -295,6 +314,7 @@ def main() -> int:
     if not args.no_decode:
         result["decode"] = decode_rate(model)
     if not args.no_cpu:
+        _progress("CPU baseline")
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
     return 0

@@ -7,6 +7,8 @@ and replays.  The optimizer step stays outside the graph.  Parameters and the
 input buffers keep their addresses; replay overwrites the captured gradient
 buffers, so `.grad` must not be reset to None while the graph is in use.
 
+Steps over `MAX_CAPTURE_ROWS` rows or more are refused (see there).
+
 The HIP library is capture-safe: it never allocates, synchronises or writes
 memory with hipMemset, and it enqueues on the current (capturing) stream.
 While capturing, the schedule issues its independent scans in order on the
@@ -14,24 +16,47 @@ capturing stream instead of on side streams, so the graph is single-stream.
 """
 from __future__ import annotations
 
+import gc
+
 import torch
 
 from . import params
 
 
+# Captures of steps over this many rows (batch x tokens) or more are refused:
+# the capture of a B=1, T=8192 training step of the Qwen3-0.6B-shaped layer
+# ended in a host segfault on ROCm 7.2 (whose cause is not known), and no
+# capture at or above this size has passed.  Steps this large are launch-light
+# anyway (a few hundred launches over tens of milliseconds).
+MAX_CAPTURE_ROWS = 1024
+
+
 class GradientGraph:
     def __init__(self, model, inputs, loss_fn, warmups: int = 3):
+        rows = max((x.shape[0] * x.shape[1] for x in inputs if x.dim() >= 2), default=0)
+        if rows >= MAX_CAPTURE_ROWS:
+            raise NotImplementedError(
+                f"GradientGraph: capture of steps over {rows} rows (batch x tokens) is switched off "
+                f"(limit {MAX_CAPTURE_ROWS}); run such steps eagerly")
         self.inputs = tuple(x.detach().clone().requires_grad_(x.requires_grad) for x in inputs)
         current = torch.cuda.current_stream()
         stream = torch.cuda.Stream()
         stream.wait_stream(current)
+        # Autograd graphs of earlier steps must be gone before the warm-up and
+        # before the capture: a parameter's gradient-accumulation node is
+        # reused while any graph holding it is alive, and it keeps the stream
+        # it was created on, so the captured backward would accumulate on a
+        # stream outside the capture (a cross-stream capture).
+        gc.collect()
         with torch.cuda.stream(stream):
             for _ in range(warmups):
                 model.zero_grad(set_to_none=True)
                 for x in self.inputs:
                     x.grad = None
-                loss, _ = loss_fn(*self.inputs)
+                loss, out = loss_fn(*self.inputs)
                 loss.backward()
+                del loss, out
+                gc.collect()
         current.wait_stream(stream)
         model.zero_grad(set_to_none=True)
         for x in self.inputs:

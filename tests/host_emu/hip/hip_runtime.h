@@ -24,6 +24,7 @@
 #define __forceinline__ inline
 #define __shared__ static
 #define __launch_bounds__(...)
+#define __align__(n) __attribute__((aligned(n)))
 
 struct dim3 {
   unsigned x = 1, y = 1, z = 1;

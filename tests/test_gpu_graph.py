@@ -211,3 +211,71 @@ def test_decode_graph_matches_oracle_at_c3_widths(dtype):
 
 
 TOL_DEC = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def test_capture_keeps_the_schedule_on_the_capturing_stream(monkeypatch):
+    """Graphs are captured single-stream: while a GradientGraph or a
+    DecodeGraph captures, the schedule runs its independent scans in order on
+    the capturing stream and never takes its side streams (no cross-stream
+    fork/join or allocator stream records inside a capture), while the eager
+    warm-up calls of the same objects do take them."""
+    from gpa_amd import schedule
+    from gpa_amd.graph import DecodeGraph
+    seen = []
+    real = schedule._side_streams
+
+    def spy(device):
+        seen.append(torch.cuda.is_current_stream_capturing())
+        return real(device)
+
+    monkeypatch.setattr(schedule, "_side_streams", spy)
+    monkeypatch.setattr(schedule, "_SERIAL", [False])
+    torch.manual_seed(2)
+    cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=4)
+    model = DenseGPA(cfg).to(DEV)
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(2, 9, 2, d, generator=g).to(DEV).requires_grad_() for d in (32, 32, 48)]
+
+    def loss_fn(q, k, v):
+        out, _ = model(q, k, v)
+        return out.float().square().mean(), out
+
+    GradientGraph(model, xs, loss_fn, warmups=1)
+    assert seen and not any(seen), "side streams taken while capturing the training step"
+    eager_calls = len(seen)
+    seen.clear()
+    with torch.no_grad():
+        tok = [x[:, :1].detach() for x in xs]
+        DecodeGraph(model, model.initial_state(2, device=DEV, dtype=torch.float32), *tok, warmups=1)
+    assert seen and not any(seen), "side streams taken while capturing a decode step"
+    assert eager_calls > 0
+
+
+def test_gradient_graph_capture_accumulates_on_the_capturing_stream(monkeypatch):
+    """The warm-up's autograd graph is released before the capture, so the
+    captured backward creates its own gradient-accumulation nodes on the
+    capturing stream.  A node reused from the warm-up keeps the warm-up
+    stream, which would put the captured accumulation on a stream outside
+    the capture; torch reports that reuse as a stream-mismatch warning.  (The
+    warm-up runs on one stream here, so the capture is the only place such a
+    mismatch can come from.)"""
+    import warnings
+
+    from gpa_amd import schedule
+    monkeypatch.setattr(schedule, "_SERIAL", [True])
+    torch.manual_seed(5)
+    cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=4)
+    model = DenseGPA(cfg).to(DEV)
+    g = torch.Generator().manual_seed(6)
+    xs = [torch.randn(1, 10, 2, d, generator=g).to(DEV).requires_grad_() for d in (32, 32, 48)]
+
+    def loss_fn(q, k, v):
+        out, _ = model(q, k, v)
+        return out.float().square().mean(), out
+
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        graph = GradientGraph(model, xs, loss_fn, warmups=2)
+        graph.replay(*xs)
+        torch.cuda.synchronize()
+    assert not [w for w in rec if "AccumulateGrad" in str(w.message)], [str(w.message)[:120] for w in rec]

@@ -81,3 +81,15 @@ def test_reference_signature_ops_validate_like_the_reference():
     assert out.shape == (1, 0, 2, 4) and final is s0
     with pytest.raises(ValueError, match="unknown backend"):
         gdn_scan(x, x, x, torch.zeros(1, 3, 2), torch.zeros(1, 3, 2), s0, backend="torch")
+
+
+def test_gradient_graph_refuses_captures_over_the_row_limit():
+    """GradientGraph refuses steps of MAX_CAPTURE_ROWS rows (batch x tokens)
+    or more before it touches the device: captures that large are switched
+    off (the B=1, T=8192 training step's capture ended in a host segfault)."""
+    from gpa_amd import GradientGraph
+    from gpa_amd.graph import MAX_CAPTURE_ROWS
+    model = DenseGPA(GPAConfig(heads=1, key_dim=8, value_dim=8, slots=(4, 4)))
+    xs = [torch.zeros(2, MAX_CAPTURE_ROWS // 2, 1, 8) for _ in range(3)]
+    with pytest.raises(NotImplementedError, match="switched off"):
+        GradientGraph(model, xs, lambda *a: None)
