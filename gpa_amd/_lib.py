@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -78,6 +78,7 @@ class DecodeProblem(ctypes.Structure):
 ROUTE_MAX_WIDTH = 256
 ROUTE_MAX_INCOMING = 3
 ROUTE_ROWS = 32
+ROUTE_MAX_PACK = 4
 
 
 class RouteProblem(ctypes.Structure):
@@ -171,6 +172,7 @@ EXPORTS = {
     "gpa_gdn_token_step": ([ctypes.POINTER(Problem), c_vp, Operand, c_vp], ctypes.c_int),
     "gpa_decode_step": ([ctypes.POINTER(DecodeProblem), c_vp], ctypes.c_int),
     "gpa_route_forward": ([ctypes.POINTER(RouteProblem), c_vp], ctypes.c_int),
+    "gpa_route_forward_many": ([ctypes.POINTER(RouteProblem), c_i32, c_vp], ctypes.c_int),
     "gpa_route_backward": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp], ctypes.c_int),
     "gpa_route_weight_grads": ([ctypes.POINTER(RouteProblem), ctypes.POINTER(RouteGrads), c_vp, c_vp, c_vp,
                                 c_vp, c_vp], ctypes.c_int),

@@ -12,6 +12,7 @@
 // einsums do; the gradients round where the reference's bf16 tensors do.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mfma_tiles.h"
@@ -434,13 +435,12 @@ __device__ __forceinline__ void rows_bwd_vec(const gpa_route_problem& p, const g
   }
 }
 
+// The forward of RR rows (row0 ..) of head h of one problem.
 template <typename E, bool VEC>
-__global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
+__device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h, int row0) {
   using W = typename Wt<E>::type;
   HIP_DYNAMIC_SHARED(float, lds)
   const int M = p.slots, Dk = p.key_dim, R = p.batch * p.tokens;
-  const RouteTile rtile = route_tile();
-  const int h = rtile.h, row0 = rtile.tile * RR;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kM = pad16(M), k2M = pad16(2 * M), kD = pad16(Dk);
   const int lda = kM + 4, ldh = (k2M > kD ? k2M : kD) + 4;
@@ -571,6 +571,47 @@ __global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
       }
     }
   }
+}
+
+template <typename E, bool VEC>
+__global__ __launch_bounds__(RNT) void route_fwd(gpa_route_problem p) {
+  const RouteTile rtile = route_tile();
+  route_fwd_run<E, VEC>(p, rtile.h, rtile.tile * RR);
+}
+
+// Several problems (the target levels of one call) in one launch: workgroups
+// wg0[i] .. wg0[i+1]-1 run problem i, head-major over its row tiles.  The
+// problem is read through the kernel-argument pointer with a uniform offset
+// (indexing the by-value argument would copy it to scratch).
+struct RoutePack {
+  int n;
+  int wg0[GPA_ROUTE_MAX_PACK], tiles[GPA_ROUTE_MAX_PACK];
+  gpa_route_problem p[GPA_ROUTE_MAX_PACK];
+};
+
+typedef const __attribute__((address_space(4))) RoutePack* RoutePackPtr;
+
+// The pack entry of this workgroup, copied word by word from the argument segment.
+__device__ __forceinline__ int route_pack_entry(RoutePackPtr kp, gpa_route_problem& p) {
+  int pi = 0;
+#pragma unroll 1
+  for (int i = 1; i < kp->n; ++i)
+    if ((int)blockIdx.x >= kp->wg0[i]) pi = i;
+  const __attribute__((address_space(4))) uint32_t* src =
+      (const __attribute__((address_space(4))) uint32_t*)&kp->p[pi];
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&p);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(gpa_route_problem) / 4); ++i) dst[i] = src[i];
+  return pi;
+}
+
+// bf16 with 16-byte rows (the one-token decode path).
+__global__ __launch_bounds__(RNT) void route_fwd_pack(RoutePack pk) {
+  const RoutePackPtr kp = (RoutePackPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  gpa_route_problem p;
+  const int pi = route_pack_entry(kp, p);
+  const int local = (int)blockIdx.x - kp->wg0[pi], nt = kp->tiles[pi];
+  route_fwd_run<bf16_t, true>(p, local / nt, (local % nt) * RR);
 }
 
 // ---------------------------------------------------------------- tiled products
@@ -1742,6 +1783,41 @@ extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t s
     hipLaunchKernelGGL((route_fwd<float, false>), grid, block, lds, stream, *problem);
   }
   return check_launch("gpa_route_forward");
+}
+
+extern "C" int gpa_route_forward_many(const gpa_route_problem* problems, int32_t n, hipStream_t stream) {
+  using namespace gpa;
+  if (!problems || n < 1 || n > GPA_ROUTE_MAX_PACK) return fail(GPA_HIP_EINVAL, "route: 1 to 4 problems");
+  bool pack = n > 1;
+  for (int i = 0; i < n; ++i) {
+    const gpa_route_problem& p = problems[i];
+    if (int rc = check_route(&p)) return rc;
+    if (!p.up_t || !p.down_t || !p.rs_t || !p.qs_t || !p.qo.ptr || !p.route.ptr)
+      return fail(GPA_HIP_EINVAL, "route: null forward weight or output");
+    int64_t rs_q, rs_route, rs_qo;
+    // (the packed kernel is instantiated for the bf16 16-byte row path only)
+    if (route_tiled(p, rs_q, rs_route, rs_qo) || p.dtype != GPA_DTYPE_BF16 || !route_vec(p)) pack = false;
+  }
+  if (!pack) {
+    for (int i = 0; i < n; ++i)
+      if (int rc = gpa_route_forward(&problems[i], stream)) return rc;
+    return GPA_HIP_OK;
+  }
+  RoutePack pk{};
+  pk.n = n;
+  int total = 0;
+  size_t lds = 0;
+  for (int i = 0; i < n; ++i) {
+    const gpa_route_problem& p = problems[i];
+    pk.p[i] = p;
+    pk.wg0[i] = total;
+    pk.tiles[i] = (p.batch * p.tokens + RR - 1) / RR;
+    total += pk.tiles[i] * p.heads;
+    lds = std::max(lds, fwd_lds(p));
+  }
+  if (int rc = set_lds(route_fwd_pack, lds)) return rc;
+  hipLaunchKernelGGL(route_fwd_pack, dim3(total), dim3(RNT), lds, stream, pk);
+  return check_launch("gpa_route_forward_many");
 }
 
 extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_route_grads* grads,

@@ -69,29 +69,37 @@ def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, 
     return p
 
 
+def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs):
+    """The forward problem of one target level and every tensor it points
+    into: (problem, (base, q, edge_w, g, mg, msgs), (qo, route), saved rows)."""
+    dtype = q.dtype
+    bsz, tokens, heads, _ = q.shape
+    m = base.shape[-1]
+    rows = bsz * tokens
+    base = base.float().contiguous()
+    q = q.contiguous()
+    msgs = tuple(x.to(dtype).contiguous() for x in msgs)
+    edge_w = edge_w.detach().float().contiguous() if msgs else None
+    g, mg = gain.detach().float().contiguous(), mlp_gain.detach().float().contiguous()
+    weights = {"up_t": _pack(up, dtype, True), "down_t": _pack(down, dtype, True),
+               "rs_t": _pack(rs, dtype, True), "qs_t": _pack(qs, dtype, True)}
+    qo = torch.empty(bsz, tokens, heads, m, device=q.device, dtype=dtype)
+    route = torch.empty_like(qo)
+    saved = (torch.empty(heads, rows, m, device=q.device, dtype=dtype),
+             torch.empty(heads, rows, 2 * m, device=q.device, dtype=dtype),
+             torch.empty(heads, rows, m, device=q.device, dtype=dtype))
+    prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved)
+    return prob, (base, q, edge_w, g, mg, msgs), (qo, route), saved
+
+
 class _RouteReader(torch.autograd.Function):
     @staticmethod
     def forward(ctx, base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs):
         _lib.require_device(q)
         ctx.set_materialize_grads(False)
         lib = _lib.load()
-        dtype = q.dtype
-        bsz, tokens, heads, _ = q.shape
-        m = base.shape[-1]
-        rows = bsz * tokens
-        base = base.float().contiguous()
-        q = q.contiguous()
-        msgs = tuple(x.to(dtype).contiguous() for x in msgs)
-        edge_w = edge_w.detach().float().contiguous() if msgs else None
-        g, mg = gain.detach().float().contiguous(), mlp_gain.detach().float().contiguous()
-        weights = {"up_t": _pack(up, dtype, True), "down_t": _pack(down, dtype, True),
-                   "rs_t": _pack(rs, dtype, True), "qs_t": _pack(qs, dtype, True)}
-        qo = torch.empty(bsz, tokens, heads, m, device=q.device, dtype=dtype)
-        route = torch.empty_like(qo)
-        saved = (torch.empty(heads, rows, m, device=q.device, dtype=dtype),
-                 torch.empty(heads, rows, 2 * m, device=q.device, dtype=dtype),
-                 torch.empty(heads, rows, m, device=q.device, dtype=dtype))
-        prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved)
+        prob, (base, q, edge_w, g, mg, msgs), (qo, route), saved = _forward_problem(
+            base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs)
         _lib.check(lib.gpa_route_forward(prob, _lib.stream_handle(q.device)), "gpa_route_forward")
         ctx.query_scale = query_scale
         ctx.n_in = len(msgs)
@@ -147,6 +155,34 @@ class _RouteReader(torch.autograd.Function):
         d_edge = sums[:, 2:].t().contiguous().to(dt[0]) if msgs else None
         return (dbase, dq, d_edge, sums[:, 1].to(dt[1]), sums[:, 0].to(dt[2]), d_up.to(dt[3]), d_down.to(dt[4]),
                 d_rs.to(dt[5]), d_qs.to(dt[6]), None, *dmsgs)
+
+
+def route_reader_many(reads) -> list[tuple[Tensor, Tensor]]:
+    """`route_reader` of several target levels, for inference (no autograd):
+    one launch where the library can pack them (`gpa_route_forward_many`:
+    bf16 one-token calls), else one per level.  `reads` holds route_reader's
+    argument tuples; returns [(qo, route)] in the same order."""
+    if not reads:
+        return []
+    if torch.is_grad_enabled():
+        raise RuntimeError("route_reader_many is for inference: call it under torch.no_grad()")
+    if len(reads) > _lib.ROUTE_MAX_PACK:
+        raise ValueError(f"route_reader_many: at most {_lib.ROUTE_MAX_PACK} levels")
+    lib = _lib.load()
+    probs = (_lib.RouteProblem * len(reads))()
+    keep, outs = [], []
+    for i, (base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs) in enumerate(reads):
+        _lib.require_device(q)
+        if not msgs:
+            edge_w = gain.new_zeros(0, gain.shape[0])
+        prob, inputs, out, saved = _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs,
+                                                    query_scale, msgs)
+        probs[i] = prob
+        keep.append((inputs, saved))
+        outs.append(out)
+    _lib.check(lib.gpa_route_forward_many(probs, len(reads), _lib.stream_handle(reads[0][1].device)),
+               "gpa_route_forward_many")
+    return outs
 
 
 def route_reader(base: Tensor, q: Tensor, edge_w: Tensor | None, gain: Tensor, mlp_gain: Tensor, up: Tensor,

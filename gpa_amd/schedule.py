@@ -37,7 +37,7 @@ from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
 from .level import level_mix, level_mix_block
 from .level import supported as fused_level_supported
-from .route import route_reader
+from .route import route_reader, route_reader_many
 from .route import supported as fused_route_supported
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 
@@ -545,6 +545,15 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
     cfg = model.config
     dtype = q.dtype
     routes, queries = [], []
+    if (_FUSED_ROUTE[0] and not torch.is_grad_enabled() and 1 < len(logits) <= _lib.ROUTE_MAX_PACK
+            and all(fused_route_supported(cfg, dtype, base.shape[-1]) for base in logits)):
+        # inference: every level's read in one launch where the library can pack them
+        reads = [(base, q, _incoming_weights(model, j) if incoming[j] else None, model.relation_gain[j],
+                  model.route_mlp_gain[j], model.route_up[j], model.route_down[j], model.route_weight[j],
+                  model.query_weight[j], cfg.query_scale, [msg for _, msg in incoming[j]])
+                 for j, base in enumerate(logits)]
+        done = route_reader_many(reads)
+        return [route for _, route in done], [qo for qo, _ in done]
     for j, base in enumerate(logits):
         if _FUSED_ROUTE[0] and fused_route_supported(cfg, dtype, base.shape[-1]):
             w = _incoming_weights(model, j) if incoming[j] else None

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 15
+#define GPA_HIP_ABI_VERSION 16
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -297,6 +297,13 @@ typedef struct gpa_route_grads {
  * (reference attention.py:225-262) and the fused Triton route
  * (triton_route.py:11-151, packed.py:130-136). */
 int gpa_route_forward(const gpa_route_problem *problem, hipStream_t stream);
+/* The forwards of up to GPA_ROUTE_MAX_PACK problems (the target levels of one
+ * call: the same _bridge loop, attention.py:225-262) in one launch where they
+ * all take the one-kernel path with the same element type and row access
+ * (fewer than 1024 rows each, as in one-token decode); otherwise one
+ * gpa_route_forward per problem.  Results are those of gpa_route_forward. */
+#define GPA_ROUTE_MAX_PACK 4
+int gpa_route_forward_many(const gpa_route_problem *problems, int32_t n, hipStream_t stream);
 /* Backward: input and row gradients, plus per-block partial sums of the scalar
  * parameter gradients.  Needs the forward's saved rows and outputs. */
 int gpa_route_backward(const gpa_route_problem *problem, const gpa_route_grads *grads, hipStream_t stream);

@@ -24,7 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 CLANG = "/opt/rocm/llvm/bin/clang++"
 ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3,
-           "gpa_level_forward": 4, "gpa_level_backward": 5}
+           "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6}
 SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip"]
 
 
@@ -47,6 +47,10 @@ def build(out_dir: str, sources=None) -> str:
 
 def _pointer_fields(ctype, base=0):
     out = []
+    if issubclass(ctype, ctypes.Array):  # an array of structs passed as one blob
+        for i in range(ctype._length_):
+            out += _pointer_fields(ctype._type_, base + i * ctypes.sizeof(ctype._type_))
+        return out
     for name, t in ctype._fields_:
         off = base + getattr(ctype, name).offset
         if t is ctypes.c_void_p:
@@ -124,6 +128,10 @@ class HostLib:
 
     def gpa_route_forward(self, prob, stream):
         return self._call("gpa_route_forward", [prob])
+
+    def gpa_route_forward_many(self, probs, n, stream):
+        assert n == len(probs)
+        return self._call("gpa_route_forward_many", [probs])
 
     def gpa_route_backward(self, prob, grads, stream):
         return self._call("gpa_route_backward", [prob, grads])

@@ -16,6 +16,7 @@
 #include <cstring>
 #include <memory>
 #include <thread>
+#include <tuple>
 #include <vector>
 
 #define __global__
@@ -141,6 +142,11 @@ inline uint32_t __float_as_uint(float f) {
   return u;
 }
 
+// The kernel-argument segment: the address of the running kernel's first
+// argument (each emulated thread holds its own copy of the arguments).
+extern thread_local const void* emu_kernarg;
+#define __builtin_amdgcn_kernarg_segment_ptr() (emu_kernarg)
+
 template <typename K, typename... A>
 void emu_launch(K kernel, dim3 grid, dim3 block, size_t lds_bytes, A... args) {
   // One team of blockDim.x threads runs the workgroups one after another; a
@@ -155,6 +161,8 @@ void emu_launch(K kernel, dim3 grid, dim3 block, size_t lds_bytes, A... args) {
   std::vector<std::thread> threads;
   for (unsigned t = 0; t < nt; ++t)
     threads.emplace_back([&, t] {
+      const std::tuple<A...> targs(args...);
+      emu_kernarg = &std::get<0>(targs);
       threadIdx = {t, 0, 0};
       blockDim = {block.x, block.y, block.z};
       gridDim = {grid.x, grid.y, grid.z};
@@ -162,7 +170,7 @@ void emu_launch(K kernel, dim3 grid, dim3 block, size_t lds_bytes, A... args) {
         for (unsigned by = 0; by < grid.y; ++by)
           for (unsigned bx = 0; bx < grid.x; ++bx) {
             blockIdx = {bx, by, bz};
-            kernel(args...);
+            std::apply(kernel, targs);
             between.arrive_and_wait();
           }
     });

@@ -18,6 +18,7 @@ std::vector<std::unique_ptr<std::barrier<>>> emu_wave_barrier;
 float emu_xchg[16][64];
 float emu_ma[16][64][8], emu_mb[16][64][8];
 char* emu_dynamic_lds;
+thread_local const void* emu_kernarg;
 static std::string last_error;
 int fail(int code, const char* message) {
   last_error = message;
@@ -87,6 +88,10 @@ int main(int argc, char** argv) {
     case 5:
       rc = gpa_level_backward(reinterpret_cast<gpa_level_problem*>(blobs.at(0).data()),
                               reinterpret_cast<gpa_level_grads*>(blobs.at(1).data()), nullptr);
+      break;
+    case 6:
+      rc = gpa_route_forward_many(reinterpret_cast<gpa_route_problem*>(blobs.at(0).data()),
+                                  (int32_t)(blobs.at(0).size() / sizeof(gpa_route_problem)), nullptr);
       break;
   }
   if (rc) {

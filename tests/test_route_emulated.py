@@ -100,3 +100,24 @@ def test_host_built_route_reader_matches_device_glue(name, dtype, runner, tmp_pa
     print(name, dtype, "worst", worst)
     bad = {k: v for k, v in errors.items() if v > tol}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("name", ["c3_widths", "two_tiles", "tiny"])
+def test_host_built_route_pack_matches_one_launch_per_level(name, runner, tmp_path, monkeypatch):
+    """Inference reads of every target level in one call (gpa_route_forward_many,
+    which packs the levels into one launch for bf16 rows of 16-byte pieces and
+    launches them one by one otherwise, as for "tiny") give the bits of one
+    gpa_route_forward per level."""
+    from gpa_amd.route import route_reader
+    model, logits, incoming, q = _inputs(CASES[name], torch.bfloat16)
+    harness.use_host(monkeypatch, harness.HostLib(runner, str(tmp_path)))
+    cfg = model.config
+    with torch.no_grad():
+        routes, queries = schedule._bridge(model, q, logits, incoming, [None] * len(logits))
+        for j, base in enumerate(logits):
+            w = schedule._incoming_weights(model, j) if incoming[j] else None
+            qo, route = route_reader(base, q, w, model.relation_gain[j], model.route_mlp_gain[j],
+                                     model.route_up[j], model.route_down[j], model.route_weight[j],
+                                     model.query_weight[j], cfg.query_scale, [m for _, m in incoming[j]])
+            assert torch.equal(qo, queries[j]), j
+            assert torch.equal(route, routes[j]), j
