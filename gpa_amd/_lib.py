@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -79,6 +79,7 @@ ROUTE_MAX_WIDTH = 256
 ROUTE_MAX_INCOMING = 3
 ROUTE_ROWS = 32
 ROUTE_MAX_PACK = 4
+TOKEN_MAX_PACK = 12
 
 
 class RouteProblem(ctypes.Structure):
@@ -170,6 +171,8 @@ EXPORTS = {
                               ctypes.c_int),
     "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
     "gpa_gdn_token_step": ([ctypes.POINTER(Problem), c_vp, Operand, c_vp], ctypes.c_int),
+    "gpa_gdn_token_step_many": ([ctypes.POINTER(Problem), ctypes.POINTER(c_vp), ctypes.POINTER(Operand), c_i32,
+                                 c_vp], ctypes.c_int),
     "gpa_decode_step": ([ctypes.POINTER(DecodeProblem), c_vp], ctypes.c_int),
     "gpa_route_forward": ([ctypes.POINTER(RouteProblem), c_vp], ctypes.c_int),
     "gpa_route_forward_many": ([ctypes.POINTER(RouteProblem), c_i32, c_vp], ctypes.c_int),

@@ -41,14 +41,14 @@ __device__ __forceinline__ float4 column_sums(float4 x, float4 (*part)[16], int 
   return s;
 }
 
-// NI rows per thread: K <= 16 NI.
+// Workgroup wg of one problem; NI rows per thread: K <= 16 NI.
 template <typename E, int NI>
-__global__ __launch_bounds__(SNT) void gdn_token_step(gpa_gdn_problem p, float* fin, gpa_operand out) {
+__device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, const gpa_operand& out, int wg) {
   __shared__ float kh[16 * NI], qh[16 * NI];
   __shared__ float norms[2][4];
   __shared__ float4 part[2][4][16];
   const int ncb = (p.vdim + SCOL - 1) / SCOL;
-  const int s = blockIdx.x / ncb, cb = blockIdx.x - s * ncb;
+  const int s = wg / ncb, cb = wg - s * ncb;
   const int b = s / p.heads, h = s - b * p.heads;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int c4 = t & 15, rg = t >> 4;
@@ -157,23 +157,76 @@ __global__ __launch_bounds__(SNT) void gdn_token_step(gpa_gdn_problem p, float* 
   }
 }
 
+template <typename E, int NI>
+__global__ __launch_bounds__(SNT) void gdn_token_step(gpa_gdn_problem p, float* fin, gpa_operand out) {
+  token_run<E, NI>(p, fin, out, blockIdx.x);
+}
+
+// Several problems with the same element type and row class in one launch:
+// workgroups wg0[i] .. wg0[i+1]-1 run problem i.
+struct TokenPack {
+  int n;
+  int wg0[GPA_TOKEN_MAX_PACK];
+  float* fin[GPA_TOKEN_MAX_PACK];
+  gpa_operand out[GPA_TOKEN_MAX_PACK];
+  gpa_gdn_problem p[GPA_TOKEN_MAX_PACK];
+};
+
+// A struct in the kernel-argument segment copied word by word (scalar loads).
+template <typename T>
+__device__ __forceinline__ void kernarg_copy(T& dst, const __attribute__((address_space(4))) T* src) {
+  static_assert(sizeof(T) % 4 == 0, "word copy");
+  const __attribute__((address_space(4))) uint32_t* s = (const __attribute__((address_space(4))) uint32_t*)src;
+  uint32_t* d = reinterpret_cast<uint32_t*>(&dst);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = s[i];
+}
+
+// The pack is the kernel's only argument: its entries are read through the
+// kernel-argument pointer with a uniform index, as scalar loads (indexing the
+// by-value argument would copy it to scratch).
+template <typename E, int NI>
+__global__ __launch_bounds__(SNT) void gdn_token_step_pack(TokenPack pk) {
+  typedef const __attribute__((address_space(4))) TokenPack* KernargPtr;
+  const KernargPtr kp = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  int pi = 0;
+#pragma unroll 1
+  for (int i = 1; i < kp->n; ++i)
+    if ((int)blockIdx.x >= kp->wg0[i]) pi = i;
+  gpa_gdn_problem p;
+  gpa_operand out;
+  kernarg_copy(p, &kp->p[pi]);
+  kernarg_copy(out, &kp->out[pi]);
+  token_run<E, NI>(p, kp->fin[pi], out, (int)blockIdx.x - kp->wg0[pi]);
+}
+
+int64_t token_workgroups(const gpa_gdn_problem& p) {
+  return (int64_t)p.batch * p.heads * ((p.vdim + SCOL - 1) / SCOL);
+}
+int token_rows(const gpa_gdn_problem& p) { return p.kdim <= 64 ? 4 : (p.kdim <= 128 ? 8 : 16); }
+
 template <typename E>
 void launch_token(const gpa_gdn_problem& p, float* fin, gpa_operand out, hipStream_t stream) {
-  const int64_t ncb = (p.vdim + SCOL - 1) / SCOL;
-  const dim3 grid((unsigned)((int64_t)p.batch * p.heads * ncb));
-  if (p.kdim <= 64) hipLaunchKernelGGL((gdn_token_step<E, 4>), grid, dim3(SNT), 0, stream, p, fin, out);
-  else if (p.kdim <= 128) hipLaunchKernelGGL((gdn_token_step<E, 8>), grid, dim3(SNT), 0, stream, p, fin, out);
-  else hipLaunchKernelGGL((gdn_token_step<E, 16>), grid, dim3(SNT), 0, stream, p, fin, out);
+  const dim3 grid((unsigned)token_workgroups(p));
+  switch (token_rows(p)) {
+    case 4: hipLaunchKernelGGL((gdn_token_step<E, 4>), grid, dim3(SNT), 0, stream, p, fin, out); break;
+    case 8: hipLaunchKernelGGL((gdn_token_step<E, 8>), grid, dim3(SNT), 0, stream, p, fin, out); break;
+    default: hipLaunchKernelGGL((gdn_token_step<E, 16>), grid, dim3(SNT), 0, stream, p, fin, out);
+  }
+}
+
+template <typename E>
+void launch_token_pack(const TokenPack& pk, int rows, unsigned grid, hipStream_t stream) {
+  switch (rows) {
+    case 4: hipLaunchKernelGGL((gdn_token_step_pack<E, 4>), dim3(grid), dim3(SNT), 0, stream, pk); break;
+    case 8: hipLaunchKernelGGL((gdn_token_step_pack<E, 8>), dim3(grid), dim3(SNT), 0, stream, pk); break;
+    default: hipLaunchKernelGGL((gdn_token_step_pack<E, 16>), dim3(grid), dim3(SNT), 0, stream, pk);
+  }
 }
 
 bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
 
-}  // namespace
-}  // namespace gpa
-
-extern "C" int gpa_gdn_token_step(const gpa_gdn_problem* problem, float* final_state, gpa_operand out,
-                                  hipStream_t stream) {
-  using namespace gpa;
+int check_token(const gpa_gdn_problem* problem, const float* final_state, const gpa_operand& out) {
   if (!problem) return fail(GPA_HIP_EINVAL, "token step: null problem");
   const gpa_gdn_problem& p = *problem;
   if (p.tokens != 1) return fail(GPA_HIP_EINVAL, "token step: needs tokens == 1");
@@ -189,7 +242,49 @@ extern "C" int gpa_gdn_token_step(const gpa_gdn_problem* problem, float* final_s
   if (p.s0 && (!aligned16(p.s0) || p.s0_sb % 4 || p.s0_sh % 4))
     return fail(GPA_HIP_EINVAL, "token step: s0 must be 16-byte aligned with strides a multiple of 4");
   if (final_state && !aligned16(final_state)) return fail(GPA_HIP_EINVAL, "token step: final must be 16-byte aligned");
+  if (token_workgroups(p) > INT32_MAX / 2) return fail(GPA_HIP_EINVAL, "token step: too many streams");
+  return GPA_HIP_OK;
+}
+
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_gdn_token_step(const gpa_gdn_problem* problem, float* final_state, gpa_operand out,
+                                  hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_token(problem, final_state, out)) return rc;
+  const gpa_gdn_problem& p = *problem;
   if (p.dtype == GPA_DTYPE_BF16) launch_token<bf16_t>(p, final_state, out, stream);
   else launch_token<float>(p, final_state, out, stream);
   return check_launch("gpa_gdn_token_step");
+}
+
+extern "C" int gpa_gdn_token_step_many(const gpa_gdn_problem* problems, float* const* final_states,
+                                       const gpa_operand* outs, int32_t n, hipStream_t stream) {
+  using namespace gpa;
+  if (!problems || !final_states || !outs || n < 1 || n > GPA_TOKEN_MAX_PACK)
+    return fail(GPA_HIP_EINVAL, "token step many: 1 to GPA_TOKEN_MAX_PACK problems with finals and outs");
+  for (int i = 0; i < n; ++i)
+    if (int rc = check_token(&problems[i], final_states[i], outs[i])) return rc;
+  // One launch per (element type, row class) present, problems in call order.
+  for (int dt = 0; dt < 2; ++dt)
+    for (int rows = 4; rows <= 16; rows *= 2) {
+      TokenPack pk{};
+      int64_t total = 0;
+      for (int i = 0; i < n; ++i) {
+        const gpa_gdn_problem& p = problems[i];
+        if (p.dtype != (dt ? GPA_DTYPE_BF16 : GPA_DTYPE_F32) || token_rows(p) != rows) continue;
+        pk.p[pk.n] = p;
+        pk.fin[pk.n] = final_states[i];
+        pk.out[pk.n] = outs[i];
+        pk.wg0[pk.n] = (int)total;
+        total += token_workgroups(p);
+        ++pk.n;
+      }
+      if (!pk.n) continue;
+      if (total > INT32_MAX / 2) return fail(GPA_HIP_EINVAL, "token step many: too many workgroups");
+      if (dt) launch_token_pack<bf16_t>(pk, rows, (unsigned)total, stream);
+      else launch_token_pack<float>(pk, rows, (unsigned)total, stream);
+    }
+  return check_launch("gpa_gdn_token_step_many");
 }

@@ -8,6 +8,8 @@ offset that aligns chunks with blocks that began in an earlier call.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch import Tensor
 
@@ -341,14 +343,8 @@ def _no_autograd(name: str, *tensors) -> None:
         raise RuntimeError(f"{name} has no backward: call it under torch.no_grad() or inference_mode()")
 
 
-def gdn_token_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
-                  s0: Tensor | None) -> tuple[Tensor | None, Tensor]:
-    """One token of B*H GDN streams without autograd (inference decode):
-    `gdn_update` then `memory_read` of the reference (src/gpa/ops.py:29-46),
-    i.e. `gdn_scan_hip` at T = 1 without the intermediates a backward needs.
-    q (may be None), k [B,1,H,K], v [B,1,H,V], g/beta [B,1,H] (any strides),
-    s0 [B,H,K,V] or None = zeros.  Returns (out [B,1,H,V] or None, final
-    [B,H,K,V] float32).  Keys/values must pass `token_step_supported`."""
+def _token_call(q, k, v, g, beta, s0):
+    """Checked arguments of one token step: (problem, final, out, tensors kept alive)."""
     _lib.require_device(k)
     if not token_step_supported(k, v) or v.dtype != k.dtype or (q is not None and q.dtype != k.dtype):
         raise ValueError("gdn_token_hip: needs one float32/bfloat16 token, K, V <= 256 and V % 4 == 0")
@@ -361,14 +357,49 @@ def gdn_token_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tenso
     if s0 is not None and s0.shape != (bsz, heads, kd, vd):
         raise ValueError("gdn_token_hip: s0 must be [B,H,K,V]")
     _no_autograd("gdn_token_hip", q, k, v, g, beta, s0)
-    lib = _lib.load()
     q = _contig_last(q) if q is not None else None
     k, v = _contig_last(k), _contig_last(v)
     g, beta = g.float(), beta.float()
     s0f = _token_state(s0) if s0 is not None else None
     final = torch.empty(bsz, heads, kd, vd, device=k.device, dtype=torch.float32)
     out = torch.empty(bsz, 1, heads, vd, device=k.device, dtype=k.dtype) if q is not None else None
-    prob = _problem(q, k, v, g, beta, s0f, 1, 0)
+    return _problem(q, k, v, g, beta, s0f, 1, 0), final, out, (q, k, v, g, beta, s0f)
+
+
+def gdn_token_many(calls) -> list[tuple[Tensor | None, Tensor]]:
+    """`gdn_token_hip` of several independent groups, for inference: one
+    launch per element type and key-width class (`gpa_gdn_token_step_many`)
+    instead of one per group.  `calls` holds gdn_token_hip's argument tuples
+    (q, k, v, g, beta, s0), at most `_lib.TOKEN_MAX_PACK` of them, on one
+    device; returns [(out, final)] in the same order."""
+    if not calls:
+        return []
+    if len(calls) > _lib.TOKEN_MAX_PACK:
+        raise ValueError(f"gdn_token_many: at most {_lib.TOKEN_MAX_PACK} groups per call")
+    lib = _lib.load()
+    n = len(calls)
+    probs, finals, outs = (_lib.Problem * n)(), (ctypes.c_void_p * n)(), (_lib.Operand * n)()
+    keep, results = [], []
+    for i, call in enumerate(calls):
+        prob, final, out, alive = _token_call(*call)
+        probs[i], finals[i], outs[i] = prob, final.data_ptr(), _lib.operand(out)
+        keep.append(alive)
+        results.append((out, final))
+    _lib.check(lib.gpa_gdn_token_step_many(probs, finals, outs, n, _lib.stream_handle(calls[0][1].device)),
+               "gpa_gdn_token_step_many")
+    return results
+
+
+def gdn_token_hip(q: Tensor | None, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                  s0: Tensor | None) -> tuple[Tensor | None, Tensor]:
+    """One token of B*H GDN streams without autograd (inference decode):
+    `gdn_update` then `memory_read` of the reference (src/gpa/ops.py:29-46),
+    i.e. `gdn_scan_hip` at T = 1 without the intermediates a backward needs.
+    q (may be None), k [B,1,H,K], v [B,1,H,V], g/beta [B,1,H] (any strides),
+    s0 [B,H,K,V] or None = zeros.  Returns (out [B,1,H,V] or None, final
+    [B,H,K,V] float32).  Keys/values must pass `token_step_supported`."""
+    lib = _lib.load()
+    prob, final, out, alive = _token_call(q, k, v, g, beta, s0)
     _lib.check(lib.gpa_gdn_token_step(prob, final.data_ptr(), _lib.operand(out), _lib.stream_handle(k.device)),
                "gpa_gdn_token_step")
     return out, final

@@ -29,7 +29,8 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib, glue, params
-from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_token_hip, gdn_token_read, token_step_supported
+from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_token_hip, gdn_token_many, gdn_token_read
+from .ops import token_step_supported
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
 from .slots import slot_gates
@@ -144,21 +145,19 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
     return torch.cat((first.unsqueeze(2).to(starts.dtype), starts[:, :, 1:]), dim=2)
 
 
-def _outer_token(lv, slot, value, g_out, b_out, s0):
-    """The read of a level's one-token outer step: the B_j step and its read
-    with the route query in one kernel; the new state goes to lv.b_final."""
-    def read(qo):
-        out, lv.b_final = gdn_token_hip(qo, slot, value, g_out, b_out, s0)
-        return out
-    return read
-
-
 class _Level:
     __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "final_count", "logits", "a_final",
-                 "b_final", "a_starts", "b_starts", "b_read", "local")
+                 "b_final", "a_starts", "b_starts", "b_read", "local", "b_token")
 
     def __init__(self):
         self.local = None  # the local read distribution, when the counts kernel gave it
+        # A one-token outer step deferred to its read: (slot, value, g, beta, s0)
+        # of the B_j step, which runs with the route query in one kernel.
+        self.b_token = None
+
+
+def _chunks(items, n):
+    return [items[i:i + n] for i in range(0, len(items), n)]
 
 
 def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, position_ids: Tensor,
@@ -200,7 +199,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             raw, a_final = gdn_token_hip(q, key, slot, g_in, b_in, old.inner)
             # The B_j step runs at its read, after the route reader (nothing
             # before needs the new B_j): one pass over the state for both.
-            lv.b_read = _outer_token(lv, slot, value, g_out, b_out, old.outer)
+            lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
             write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
             lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
@@ -251,9 +250,20 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             return lambda: lv.b_read(qo)
         return lambda: gdn_scan_hip(qo, lv.slot, lv.value, lv.g_out, lv.b_out, s0, **scan)[0]
 
-    reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
-                          (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
-                         for j, (lv, qo) in enumerate(zip(levels, queries))])
+    if all(lv.b_token is not None for lv in levels):
+        # one-token outer steps of every level, packed into as few launches as the library takes
+        reads = []
+        for part in _chunks(list(zip(levels, queries)), _lib.TOKEN_MAX_PACK):
+            done = gdn_token_many([(qo,) + lv.b_token for lv, qo in part])
+            for (lv, _), (out_j, lv.b_final) in zip(part, done):
+                reads.append(out_j)
+    else:
+        for lv in levels:
+            if lv.b_token is not None:
+                lv.b_read = _outer_token(lv)
+        reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
+                              (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
+                             for j, (lv, qo) in enumerate(zip(levels, queries))])
     if not (_SERIAL[0] or torch.cuda.is_current_stream_capturing()):
         for lv in levels:  # states made by a one-token outer step on a side stream
             if lv.b_starts is None and lv.b_final is not None:
@@ -277,6 +287,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.final_count, None) for lv in levels)
     new_state = GPAState(new_levels, relations, state.position + tokens, chunk, new_offset, frozen)
     return out, new_state, (tuple(routes) if want_routes else None)
+
+
+def _outer_token(lv):
+    """The read of a level's deferred one-token outer step on its own; the new
+    state goes to lv.b_final."""
+    def read(qo):
+        out, lv.b_final = gdn_token_hip(qo, *lv.b_token)
+        return out
+    return read
 
 
 def run_tokens(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, control: Tensor | None, *,
@@ -512,7 +531,14 @@ def _relations(model, local, writes, rel_states, scan, token=False):
             return msg, memory
         return run, (local[i], writes[i], writes[j], old.memory, decay, strength)
 
-    done = _concurrent([edge(e, i, j, old) for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))])
+    if token and not cfg.rsa_update and all(token_step_supported(writes[i], writes[j]) for i, j in model.edges):
+        # every edge's one-token step, packed into as few launches as the library takes
+        lead = writes[0].shape[:-1]
+        calls = [(local[i], writes[i], writes[j], decay[e].expand(lead), strength[e].expand(lead), old.memory)
+                 for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))]
+        done = [r for part in _chunks(calls, _lib.TOKEN_MAX_PACK) for r in gdn_token_many(part)]
+    else:
+        done = _concurrent([edge(e, i, j, old) for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))])
     incoming = [[] for _ in local]
     finals = []
     for e, ((i, j), (msg, memory)) in enumerate(zip(model.edges, done)):

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 16
+#define GPA_HIP_ABI_VERSION 17
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -191,6 +191,16 @@ int gpa_gdn_scan_noalloc(const gpa_gdn_problem *problem, gpa_operand out, float 
  * src/gpa/ops.py:29-46 (gdn_update, memory_read), the scan at T = 1 of
  * ops.py:49-85 without the intermediates a backward would need. */
 int gpa_gdn_token_step(const gpa_gdn_problem *problem, float *final_state, gpa_operand out, hipStream_t stream);
+/* gpa_gdn_token_step of up to GPA_TOKEN_MAX_PACK independent problems
+ * (final_states[i], outs[i] belong to problems[i]) in one launch per element
+ * type and key-width class (K <= 64, <= 128, <= 256) present: the one-token
+ * steps of every relation edge (the _relations loop, attention.py:206-223)
+ * or of every level's outer memory (attention.py:333-339) at once.  Results
+ * are those of one gpa_gdn_token_step per problem; the problems must not
+ * write a state another one reads. */
+#define GPA_TOKEN_MAX_PACK 12
+int gpa_gdn_token_step_many(const gpa_gdn_problem *problems, float *const *final_states, const gpa_operand *outs,
+                            int32_t n, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Batched single-token decode step of the whole DenseGPA core (the reference's

@@ -18,7 +18,7 @@ import torch
 import oracle
 from oracle import reference as ref
 from gpa_amd import DenseGPA, GPAConfig, schedule
-from gpa_amd.ops import gdn_token_hip, gdn_token_read
+from gpa_amd.ops import gdn_token_hip, gdn_token_many, gdn_token_read
 from gpa_amd.state import tensors
 
 pytestmark = pytest.mark.gpu
@@ -61,6 +61,47 @@ def test_token_step_matches_reference_step_and_read(b, h, k, v, s0, query, dtype
         assert _rel(out[:, 0], o_ref) < tol
     else:
         assert out is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_token_many_matches_one_call_per_group_and_reference(dtype):
+    """gdn_token_many (one launch per key-width class) gives the bits of one
+    gdn_token_hip per group, for groups of three key-width classes in mixed
+    order, with and without a query and an initial state, and each matches the
+    oracle's step and read."""
+    g = torch.Generator().manual_seed(5)
+    shapes = [(64, 1, 128, 128, True, "full"), (64, 1, 256, 128, True, "full"), (2, 3, 20, 12, False, None),
+              (64, 1, 128, 256, True, "broadcast"), (2, 3, 256, 4, True, "full"), (64, 1, 128, 128, True, "full")]
+    calls = []
+    for b, h, k, v, query, s0 in shapes:
+        q = torch.randn(b, 1, h, k, generator=g).to(dtype) if query else None
+        key = torch.randn(b, 1, h, k, generator=g).to(dtype)
+        val = torch.randn(b, 1, h, v, generator=g).to(dtype)
+        lg, beta = -torch.rand(b, 1, h, generator=g), torch.rand(b, 1, h, generator=g)
+        st = {"full": torch.randn(b, h, k, v, generator=g) * .2,
+              "broadcast": (torch.randn(1, h, k, v, generator=g) * .2).expand(b, h, k, v), None: None}[s0]
+        calls.append(tuple(x.to(DEV) if x is not None else None for x in (q, key, val, lg, beta, st)))
+    with torch.no_grad():
+        many = gdn_token_many(calls)
+        one = [gdn_token_hip(*c) for c in calls]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for (out_m, fin_m), (out_1, fin_1), (q, key, val, lg, beta, st) in zip(many, one, calls):
+        assert torch.equal(fin_m, fin_1)
+        assert (out_m is None) == (out_1 is None)
+        b, _, h, k = key.shape
+        s_ref = ref.gdn_step(st.cpu() if st is not None else torch.zeros(b, h, k, val.shape[-1]), key[:, 0].cpu(),
+                             val[:, 0].cpu(), lg[:, 0].cpu(), beta[:, 0].cpu())
+        assert _rel(fin_m, s_ref) < tol
+        if out_m is not None:
+            assert torch.equal(out_m, out_1)
+            assert _rel(out_m[:, 0], ref.gdn_read(q[:, 0].cpu(), s_ref)) < tol
+
+
+def test_token_many_refuses_too_many_groups():
+    k = torch.randn(1, 1, 1, 8, device=DEV)
+    g, beta = torch.zeros(1, 1, 1, device=DEV), torch.ones(1, 1, 1, device=DEV)
+    with pytest.raises(ValueError):
+        gdn_token_many([(None, k, k, g, beta, None)] * 13)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
@@ -126,10 +167,12 @@ def test_decode_token_steps_match_oracle_and_chunk_path(dtype, monkeypatch):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("b,h,dk,dv,m,first", [(3, 2, 128, 128, 128, "full"), (2, 2, 128, 128, 256, "broadcast"),
-                                               (2, 1, 20, 8, 12, "full"), (1, 3, 256, 96, 64, "broadcast")])
+                                               (2, 1, 20, 8, 12, "full"), (1, 3, 256, 96, 64, "broadcast"),
+                                               (64, 16, 128, 128, 128, "full"), (64, 16, 128, 128, 256, "full")])
 def test_level_token_kernel_matches_block_kernel(b, h, dk, dv, m, first, dtype, monkeypatch):
     """gpa_level_token_forward (one token from the block snapshots) against the
-    block kernel gpa_level_forward on the same call: write, key', value'."""
+    block kernel gpa_level_forward on the same call: write, key', value'; the
+    last two cases have the decode batch's 1024 streams."""
     from gpa_amd import level
     g = torch.Generator().manual_seed(b + dk + m)
     key = torch.randn(b, 1, h, dk, generator=g).to(dtype).to(DEV)
