@@ -12,11 +12,11 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
-MAX_TIMED = 4
+MAX_TIMED = 40
 CHUNK_ROWS = 64
 MAX_KDIM = 256
 MAX_VDIM = 1024
@@ -80,6 +80,7 @@ ROUTE_MAX_INCOMING = 3
 ROUTE_ROWS = 32
 ROUTE_MAX_PACK = 4
 TOKEN_MAX_PACK = 12
+GDN_MAX_PACK = 12
 
 
 class RouteProblem(ctypes.Structure):
@@ -170,6 +171,10 @@ EXPORTS = {
     "gpa_gdn_read_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, Operand, c_vp],
                               ctypes.c_int),
     "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
+    "gpa_gdn_forward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Operand), c_i32,
+                              ctypes.POINTER(Timing), c_vp], ctypes.c_int),
+    "gpa_gdn_backward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads), c_i32,
+                               ctypes.POINTER(Timing), c_vp], ctypes.c_int),
     "gpa_gdn_token_step": ([ctypes.POINTER(Problem), c_vp, Operand, c_vp], ctypes.c_int),
     "gpa_gdn_token_step_many": ([ctypes.POINTER(Problem), ctypes.POINTER(c_vp), ctypes.POINTER(Operand), c_i32,
                                  c_vp], ctypes.c_int),

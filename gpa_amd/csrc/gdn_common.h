@@ -109,6 +109,18 @@ __device__ __forceinline__ void stage_rows(float* dst, const float* src, int wid
 }
 
 
+// A struct in the kernel-argument segment copied word by word (scalar loads):
+// the pack kernels read their entry this way (indexing a by-value argument
+// would copy the whole argument to scratch).
+template <typename T>
+__device__ __forceinline__ void kernarg_copy(T& dst, const __attribute__((address_space(4))) T* src) {
+  static_assert(sizeof(T) % 4 == 0, "word copy");
+  const __attribute__((address_space(4))) uint32_t* s = (const __attribute__((address_space(4))) uint32_t*)src;
+  uint32_t* d = reinterpret_cast<uint32_t*>(&dst);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = s[i];
+}
+
 // MFMA launchers for the bf16 state recurrences (gdn_state_mfma.hip); they
 // return nonzero if the width is not built.
 template <int KM>
@@ -116,6 +128,23 @@ int launch_state_fwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int
 template <int KM>
 int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
                           hipStream_t st);
+// Several problems of these kernels in one launch: workgroups wg0[i] ..
+// wg0[i+1]-1 run problem i (mfma_state_workgroups(problem) of them).  `fast`
+// when every problem has K == KM and V a multiple of 64; the backward's read
+// gradient and state injections must be present in all problems or in none.
+constexpr int GPA_MFMA_MAXP = 5;
+struct MfmaPack {
+  int n;
+  int wg0[GPA_MFMA_MAXP], nvb[GPA_MFMA_MAXP], nch[GPA_MFMA_MAXP];
+  gpa_gdn_problem p[GPA_MFMA_MAXP];
+  gpa_gdn_saved sv[GPA_MFMA_MAXP];
+  gpa_gdn_grads gr[GPA_MFMA_MAXP];
+};
+int mfma_state_workgroups(const gpa_gdn_problem& p);
+template <int KM>
+int launch_state_fwd_mfma_pack(const MfmaPack& pk, int total, bool fast, hipStream_t st);
+template <int KM>
+int launch_state_bwd_mfma_pack(const MfmaPack& pk, int total, bool fast, bool has_q, bool has_inj, hipStream_t st);
 // MFMA chunk preparation (gdn_prep_mfma.hip); mf: write the bf16 fragments.
 template <typename E, int KM>
 int launch_prep_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, bool mf, int nch, hipStream_t st);

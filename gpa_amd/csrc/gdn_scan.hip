@@ -883,110 +883,266 @@ int allow_lds(F kernel, size_t bytes) {
   return err == hipSuccess ? GPA_HIP_OK : fail(GPA_HIP_EHIP, "hipFuncSetAttribute(max dynamic LDS) failed");
 }
 
+// ---- the phases of a forward and a backward (each launches one kernel) ----
+
 template <typename E, int KM>
-int launch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, gpa_timing* tm,
-                   hipStream_t st, int nch) {
-  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
-  const bool mf = use_mfma<E>(p);
-  mark(tm, st);
-  if (int rc = launch_prep_mfma<E, KM>(p, sv, mf, nch, st)) return rc;
-  mark(tm, st);
-  if (mf && KM <= 128) {
+int fwd_prep(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStream_t st) {
+  return launch_prep_mfma<E, KM>(p, sv, use_mfma<E>(p), nch, st);
+}
+
+// A problem whose state recurrence runs on the strip kernels (bf16 MFMA, K <= 128).
+template <typename E>
+bool strip_path(const gpa_gdn_problem& p) {
+  return use_mfma<E>(p) && p.kdim <= 128;
+}
+
+// The state recurrence of one problem outside a pack.
+template <typename E, int KM>
+int fwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStream_t st) {
+  const dim3 block(NT);
+  if (strip_path<E>(p)) {
     StripFwdPack pk{};
     pk.n = 1;
     pk.p[0] = strip_fwd_one(p, sv, nch, 0);
     const bool fast = p.kdim == KM && p.vdim % 64 == 0;
-    if (int rc = launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, st)) return rc;
-  } else if (mf) {
-    if (int rc = launch_state_fwd_mfma<KM>(p, sv, nch, st)) return rc;
-  } else {
-    const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
-    const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
-    if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
-    hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
+    return launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, st);
   }
-  if (p.q.ptr && out.ptr) {
+  if (use_mfma<E>(p)) return launch_state_fwd_mfma<KM>(p, sv, nch, st);
+  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + R * LDS_ + R * (VT + 1) + 2 * R);
+  if (int rc = allow_lds(gdn_state_fwd<KM>, lds_state)) return rc;
+  hipLaunchKernelGGL((gdn_state_fwd<KM>), grid_s, block, lds_state, st, p, sv, nch);
+  return GPA_HIP_OK;
+}
+
+template <typename E, int KM>
+int fwd_out(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, int nch, hipStream_t st) {
+  if (use_mfma<E>(p) && p.vdim <= GPA_OUT_MFMA_MAX_V) return launch_out_mfma<KM>(p, sv, out, nch, st);
+  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
+  const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+  hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
+  return GPA_HIP_OK;
+}
+
+bool has_read(const gpa_gdn_problem& p, const gpa_gdn_grads& gr) { return p.q.ptr && gr.dout.ptr; }
+
+// The grads as the kernels see them: no read gradient, no dd0 / o.
+gpa_gdn_grads effective_grads(const gpa_gdn_problem& p, gpa_gdn_grads gr) {
+  if (!has_read(p, gr)) {
+    gr.dd0 = nullptr;
+    gr.o = nullptr;
+  }
+  return gr;
+}
+
+template <typename E, int KM>
+int bwd_dd0(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch, hipStream_t st) {
+  if (use_mfma<E>(p) && p.vdim <= GPA_OUT_MFMA_MAX_V) return launch_dd0_mfma<KM>(p, sv, gr, nch, st);
+  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
+  const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
+  hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
+  return GPA_HIP_OK;
+}
+
+template <typename E, int KM>
+int bwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch, hipStream_t st) {
+  const dim3 block(NT);
+  if (strip_path<E>(p)) {
+    const bool has_q = has_read(p, gr);
+    StripBwdPack pk{};
+    pk.n = 1;
+    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q);
+    const bool fast = p.kdim == KM && p.vdim % 64 == 0;
+    return launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, has_q, gr.dstates != nullptr,
+                                                        st);
+  }
+  if (use_mfma<E>(p)) return launch_state_bwd_mfma<KM>(p, sv, gr, nch, st);
+  const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
+  const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
+  if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
+  return GPA_HIP_OK;
+}
+
+template <typename E, int KM>
+int bwd_chunk(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch, hipStream_t st) {
+  // The MFMA chunk kernel keeps 64 x 256 fp32 rows in LDS only for bf16.
+  constexpr bool mfma_chunk = !(std::is_same<E, float>::value && KM == 256);
+  if (mfma_chunk && p.kdim % 4 == 0) {
+    if constexpr (mfma_chunk) return launch_chunk_bwd_mfma<E, KM>(p, sv, gr, nch, st);
+  }
+  constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
+  constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
+  const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
+  if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
+  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
+  hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  return GPA_HIP_OK;
+}
+
+// A phase of problem i, dispatched on its element type and key-width class.
+enum class Phase { prep, state, out, dd0, state_bwd, chunk_bwd };
+
+template <typename E, int KM>
+int run_phase_km(Phase ph, const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out,
+                 const gpa_gdn_grads& gr, int nch, hipStream_t st) {
+  switch (ph) {
+    case Phase::prep: return fwd_prep<E, KM>(p, sv, nch, st);
+    case Phase::state: return fwd_state<E, KM>(p, sv, nch, st);
+    case Phase::out: return fwd_out<E, KM>(p, sv, out, nch, st);
+    case Phase::dd0: return bwd_dd0<E, KM>(p, sv, gr, nch, st);
+    case Phase::state_bwd: return bwd_state<E, KM>(p, sv, gr, nch, st);
+    default: return bwd_chunk<E, KM>(p, sv, gr, nch, st);
+  }
+}
+
+template <typename E>
+int run_phase(Phase ph, const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, const gpa_gdn_grads& gr,
+              int nch, hipStream_t st) {
+  switch (kmax_for(p.kdim)) {
+    case 64: return run_phase_km<E, 64>(ph, p, sv, out, gr, nch, st);
+    case 128: return run_phase_km<E, 128>(ph, p, sv, out, gr, nch, st);
+    default: return run_phase_km<E, 256>(ph, p, sv, out, gr, nch, st);
+  }
+}
+
+int phase(Phase ph, const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, const gpa_gdn_grads& gr,
+          hipStream_t st) {
+  const int nch = gpa_gdn_nchunks(p.tokens, p.offset, p.chunk);
+  return p.dtype == GPA_DTYPE_BF16 ? run_phase<bf16_t>(ph, p, sv, out, gr, nch, st)
+                                   : run_phase<float>(ph, p, sv, out, gr, nch, st);
+}
+
+bool on_strips(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && p.kdim % 16 == 0 && p.kdim <= 128; }
+// The 256-key bf16 MFMA state kernels (packed up to GPA_MFMA_MAXP problems).
+bool on_mfma256(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && p.kdim % 16 == 0 && p.kdim > 128; }
+
+// Forward of n problems: every prep, the state recurrences (the problems on
+// the strip kernels of one key-width class in one packed launch, at the
+// position of the first of them), every read.
+int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_operand* outs, int n,
+                        gpa_timing* tm, hipStream_t st) {
+  const gpa_gdn_grads none{};
+  for (int i = 0; i < n; ++i) {
     mark(tm, st);
-    if (mf && p.vdim <= GPA_OUT_MFMA_MAX_V) {
-      if (int rc = launch_out_mfma<KM>(p, sv, out, nch, st)) return rc;
-    } else {
-      const size_t lds_out = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
-      hipLaunchKernelGGL((gdn_out_fwd<E, KM>), grid_c, block, lds_out, st, p, sv, out, nch);
+    if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, st)) return rc;
+  }
+  bool done[GPA_GDN_MAX_PACK] = {};
+  for (int i = 0; i < n; ++i) {
+    if (done[i]) continue;
+    mark(tm, st);
+    if (on_mfma256(ps[i])) {
+      MfmaPack pk{};
+      int total = 0;
+      bool fast = true;
+      for (int j = i; j < n && pk.n < GPA_MFMA_MAXP; ++j) {
+        if (done[j] || !on_mfma256(ps[j])) continue;
+        pk.p[pk.n] = ps[j];
+        pk.sv[pk.n] = svs[j];
+        pk.nch[pk.n] = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+        pk.nvb[pk.n] = (ps[j].vdim + 63) / 64;
+        pk.wg0[pk.n++] = total;
+        total += mfma_state_workgroups(ps[j]);
+        fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
+        done[j] = true;
+      }
+      if (int rc = launch_state_fwd_mfma_pack<256>(pk, total, fast, st)) return rc;
+      continue;
     }
+    if (!on_strips(ps[i])) {
+      if (int rc = phase(Phase::state, ps[i], svs[i], outs[i], none, st)) return rc;
+      continue;
+    }
+    const int km = kmax_for(ps[i].kdim);
+    StripFwdPack pk{};
+    int total = 0;
+    bool fast = true;
+    for (int j = i; j < n; ++j) {
+      if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km) continue;
+      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+      pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total);
+      total += strip_workgroups(ps[j]);
+      fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
+      done[j] = true;
+    }
+    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, st)
+                            : launch_state_fwd_strip<128>(pk, total, fast, st);
+    if (rc) return rc;
+  }
+  for (int i = 0; i < n; ++i) {
+    if (!ps[i].q.ptr || !outs[i].ptr) continue;
+    mark(tm, st);
+    if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, st)) return rc;
   }
   mark(tm, st);
   return check_launch("gdn_forward");
 }
 
-template <typename E, int KM>
-int launch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_gdn_grads gr, gpa_timing* tm,
-                    hipStream_t st, int nch) {
-  const dim3 grid_c(nch, p.batch * p.heads), block(NT);
-  const bool has_q = p.q.ptr && gr.dout.ptr;
-  if (has_q) {
+// Backward of n problems: every dd0, the state recurrences (packed per
+// key-width class, read gradient and state injection), every chunk kernel.
+int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_gdn_grads* grs, int n,
+                         gpa_timing* tm, hipStream_t st) {
+  const gpa_operand none{};
+  gpa_gdn_grads gr[GPA_GDN_MAX_PACK];
+  for (int i = 0; i < n; ++i) gr[i] = effective_grads(ps[i], grs[i]);
+  for (int i = 0; i < n; ++i) {
+    if (!has_read(ps[i], gr[i])) continue;
     mark(tm, st);
-    if (use_mfma<E>(p) && p.vdim <= GPA_OUT_MFMA_MAX_V) {
-      if (int rc = launch_dd0_mfma<KM>(p, sv, gr, nch, st)) return rc;
-    } else {
-      const size_t lds = sizeof(float) * (R * LDR + 2 * R * LDS_ + R);
-      hipLaunchKernelGGL((gdn_dd0<E, KM>), grid_c, block, lds, st, p, sv, gr, nch);
+    if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], st)) return rc;
+  }
+  bool done[GPA_GDN_MAX_PACK] = {};
+  for (int i = 0; i < n; ++i) {
+    if (done[i]) continue;
+    mark(tm, st);
+    const bool hq = has_read(ps[i], gr[i]), hi = gr[i].dstates != nullptr;
+    if (on_mfma256(ps[i])) {
+      MfmaPack pk{};
+      int total = 0;
+      bool fast = true;
+      for (int j = i; j < n && pk.n < GPA_MFMA_MAXP; ++j) {
+        if (done[j] || !on_mfma256(ps[j]) || has_read(ps[j], gr[j]) != hq || (gr[j].dstates != nullptr) != hi)
+          continue;
+        pk.p[pk.n] = ps[j];
+        pk.sv[pk.n] = svs[j];
+        pk.gr[pk.n] = gr[j];
+        pk.nch[pk.n] = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+        pk.nvb[pk.n] = (ps[j].vdim + 63) / 64;
+        pk.wg0[pk.n++] = total;
+        total += mfma_state_workgroups(ps[j]);
+        fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
+        done[j] = true;
+      }
+      if (int rc = launch_state_bwd_mfma_pack<256>(pk, total, fast, hq, hi, st)) return rc;
+      continue;
     }
-  } else {
-    gr.dd0 = nullptr;
-    gr.o = nullptr;
-  }
-  mark(tm, st);
-  if (use_mfma<E>(p) && KM <= 128) {
+    if (!on_strips(ps[i])) {
+      if (int rc = phase(Phase::state_bwd, ps[i], svs[i], none, gr[i], st)) return rc;
+      continue;
+    }
+    const int km = kmax_for(ps[i].kdim);
     StripBwdPack pk{};
-    pk.n = 1;
-    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q);
-    const bool fast = p.kdim == KM && p.vdim % 64 == 0;
-    if (int rc = launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, has_q,
-                                                              gr.dstates != nullptr, st))
-      return rc;
-  } else if (use_mfma<E>(p)) {
-    if (int rc = launch_state_bwd_mfma<KM>(p, sv, gr, nch, st)) return rc;
-  } else {
-    const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
-    const size_t lds_state = sizeof(float) * (KM * (VT + 1) + 2 * R * LDS_ + 2 * R * (VT + 1) + 2 * R);
-    if (int rc = allow_lds(gdn_state_bwd<E, KM>, lds_state)) return rc;
-    hipLaunchKernelGGL((gdn_state_bwd<E, KM>), grid_s, block, lds_state, st, p, sv, gr, nch);
+    int total = 0;
+    bool fast = true;
+    for (int j = i; j < n; ++j) {
+      if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || has_read(ps[j], gr[j]) != hq ||
+          (gr[j].dstates != nullptr) != hi)
+        continue;
+      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+      pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq);
+      total += strip_workgroups(ps[j]);
+      fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
+      done[j] = true;
+    }
+    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, st)
+                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, st);
+    if (rc) return rc;
   }
-  mark(tm, st);
-  // The MFMA chunk kernel keeps 64 x 256 fp32 rows in LDS only for bf16.
-  constexpr bool mfma_chunk = !(std::is_same<E, float>::value && KM == 256);
-  if (mfma_chunk && p.kdim % 4 == 0) {
-    if constexpr (mfma_chunk)
-      if (int rc = launch_chunk_bwd_mfma<E, KM>(p, sv, gr, nch, st)) return rc;
-  } else {
-    constexpr int PHASE_A = 3 * R * (VT + 1) + 2 * KM * (VT + 1);
-    constexpr int PHASE_BC = 5 * R * LDR + 2 * R * LDS_;
-    const size_t lds_chunk = sizeof(float) * ((PHASE_A > PHASE_BC ? PHASE_A : PHASE_BC) + 4 * R + 4);
-    if (int rc = allow_lds(gdn_chunk_bwd<E, KM>, lds_chunk)) return rc;
-    hipLaunchKernelGGL((gdn_chunk_bwd<E, KM>), grid_c, block, lds_chunk, st, p, sv, gr, nch);
+  for (int i = 0; i < n; ++i) {
+    mark(tm, st);
+    if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], st)) return rc;
   }
   mark(tm, st);
   return check_launch("gdn_backward");
-}
-
-template <typename E>
-int dispatch_forward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, gpa_timing* tm,
-                     hipStream_t st, int nch) {
-  switch (kmax_for(p.kdim)) {
-    case 64: return launch_forward<E, 64>(p, sv, out, tm, st, nch);
-    case 128: return launch_forward<E, 128>(p, sv, out, tm, st, nch);
-    default: return launch_forward<E, 256>(p, sv, out, tm, st, nch);
-  }
-}
-
-template <typename E>
-int dispatch_backward(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr,
-                      gpa_timing* tm, hipStream_t st, int nch) {
-  switch (kmax_for(p.kdim)) {
-    case 64: return launch_backward<E, 64>(p, sv, gr, tm, st, nch);
-    case 128: return launch_backward<E, 128>(p, sv, gr, tm, st, nch);
-    default: return launch_backward<E, 256>(p, sv, gr, tm, st, nch);
-  }
 }
 
 }  // namespace
@@ -1019,10 +1175,21 @@ extern "C" int gpa_gdn_forward(const gpa_gdn_problem* problem, const gpa_gdn_sav
   if (rc) return rc;
   if (int rc2 = check_saved(problem, saved)) return rc2;
   if (problem->q.ptr && !out.ptr) return fail(GPA_HIP_EINVAL, "gdn_forward: q given without out");
-  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
   if (timing) timing->launched = 0;
-  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, *saved, out, timing, stream, nch)
-                                          : dispatch_forward<float>(*problem, *saved, out, timing, stream, nch);
+  return launch_forward_many(problem, saved, &out, 1, timing, stream);
+}
+
+extern "C" int gpa_gdn_forward_many(const gpa_gdn_problem* problems, const gpa_gdn_saved* saved,
+                                    const gpa_operand* outs, int32_t n, gpa_timing* timing, hipStream_t stream) {
+  if (!problems || !saved || !outs || n < 1 || n > GPA_GDN_MAX_PACK)
+    return fail(GPA_HIP_EINVAL, "gdn_forward_many: 1 to GPA_GDN_MAX_PACK problems with saved buffers and outs");
+  for (int i = 0; i < n; ++i) {
+    if (int rc = check_problem(&problems[i])) return rc;
+    if (int rc = check_saved(&problems[i], &saved[i])) return rc;
+    if (problems[i].q.ptr && !outs[i].ptr) return fail(GPA_HIP_EINVAL, "gdn_forward_many: q given without out");
+  }
+  if (timing) timing->launched = 0;
+  return launch_forward_many(problems, saved, outs, n, timing, stream);
 }
 
 extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_saved* saved,
@@ -1036,10 +1203,26 @@ extern "C" int gpa_gdn_backward(const gpa_gdn_problem* problem, const gpa_gdn_sa
     return fail(GPA_HIP_EINVAL, "gdn_backward: a gradient buffer is null");
   if (problem->q.ptr && grads->dout.ptr && (!grads->dd0 || !grads->o || !grads->dq.ptr))
     return fail(GPA_HIP_EINVAL, "gdn_backward: read gradient needs dd0, o and dq");
-  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
   if (timing) timing->launched = 0;
-  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_backward<bf16_t>(*problem, *saved, *grads, timing, stream, nch)
-                                          : dispatch_backward<float>(*problem, *saved, *grads, timing, stream, nch);
+  return launch_backward_many(problem, saved, grads, 1, timing, stream);
+}
+
+extern "C" int gpa_gdn_backward_many(const gpa_gdn_problem* problems, const gpa_gdn_saved* saved,
+                                     const gpa_gdn_grads* grads, int32_t n, gpa_timing* timing, hipStream_t stream) {
+  if (!problems || !saved || !grads || n < 1 || n > GPA_GDN_MAX_PACK)
+    return fail(GPA_HIP_EINVAL, "gdn_backward_many: 1 to GPA_GDN_MAX_PACK problems with saved buffers and grads");
+  for (int i = 0; i < n; ++i) {
+    const gpa_gdn_problem* problem = &problems[i];
+    const gpa_gdn_grads* g = &grads[i];
+    if (int rc = check_problem(problem)) return rc;
+    if (int rc = check_saved(problem, &saved[i])) return rc;
+    if (!g->ddelta || !g->dhend || !g->dw || !g->dk.ptr || !g->dv.ptr || !g->dg.ptr || !g->dbeta.ptr || !g->ds0)
+      return fail(GPA_HIP_EINVAL, "gdn_backward_many: a gradient buffer is null");
+    if (problem->q.ptr && g->dout.ptr && (!g->dd0 || !g->o || !g->dq.ptr))
+      return fail(GPA_HIP_EINVAL, "gdn_backward_many: read gradient needs dd0, o and dq");
+  }
+  if (timing) timing->launched = 0;
+  return launch_backward_many(problems, saved, grads, n, timing, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1136,7 +1319,5 @@ extern "C" int gpa_gdn_scan_noalloc(const gpa_gdn_problem* problem, gpa_operand 
   if ((rc = scratch_address(&base))) return rc;
   carve_saved(*problem, reinterpret_cast<uintptr_t>(base), &sv);
   sv.final = final_state;
-  const int nch = gpa_gdn_nchunks(problem->tokens, problem->offset, problem->chunk);
-  return problem->dtype == GPA_DTYPE_BF16 ? dispatch_forward<bf16_t>(*problem, sv, out, nullptr, stream, nch)
-                                          : dispatch_forward<float>(*problem, sv, out, nullptr, stream, nch);
+  return launch_forward_many(problem, &sv, &out, 1, nullptr, stream);
 }

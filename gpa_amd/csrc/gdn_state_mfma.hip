@@ -207,7 +207,8 @@ struct Shape {
 // current one: with every operand reloaded as soon as it is dead, each load
 // has a whole chunk step to arrive, and no extra registers are needed.
 template <int KM, bool FAST>
-__global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
+__device__ __forceinline__ void state_fwd_mfma_run(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int bx,
+                                                   int s) {
   constexpr int KLD = KM + TPAD;
   constexpr int NRB = KM / 32 >= 4 ? KM / 128 : 1;  // 32-row blocks of the state per wave
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -216,9 +217,9 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
   __bf16* dh = sl + MV * KLD;                        // [MV][CT]   (e^{G_C-G} D)^T hi
   __bf16* dl = dh + MV * CT;                         // [MV][CT]   lo
   const Shape<KM, FAST> sp(p);
-  const int s = blockIdx.y, b = s / p.heads, h = s % p.heads;
+  const int b = s / p.heads, h = s % p.heads;
   const int K = sp.K, V = sp.V, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int v0 = blockIdx.x * MV;
+  const int v0 = bx * MV;
   const bool owns = (KM / 32 >= 4) || w < KM / 32;  // row blocks rb = w + 4*i
   const int rt = w >> 1, ct = w & 1;               // this wave's D tile
   const int vd = v0 + 32 * ct + (l & 31);          // D tile column
@@ -347,8 +348,8 @@ __global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_
 }
 
 template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
-__global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
-                                                          int nch) {
+__device__ __forceinline__ void state_bwd_mfma_run(const gpa_gdn_problem& p, const gpa_gdn_saved& sv,
+                                                   const gpa_gdn_grads& gr, int nch, int bx, int s) {
   constexpr int KLD = KM + TPAD;
   constexpr int NRB = KM / 32 >= 4 ? KM / 128 : 1;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -359,9 +360,8 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
   __bf16* oh = dl + MV * CT;                         // [MV][CT]   o^T hi
   __bf16* ol = oh + MV * CT;                         // [MV][CT]   lo
   const Shape<KM, FAST> sp(p);
-  const int s = blockIdx.y;
   const int K = sp.K, V = sp.V, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int v0 = blockIdx.x * MV;
+  const int v0 = bx * MV;
   const bool owns = (KM / 32 >= 4) || w < KM / 32;
   const int rt = w >> 1, ct = w & 1;
   const int vd = v0 + 32 * ct + (l & 31);
@@ -544,6 +544,54 @@ __global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_
   }
 }
 
+template <int KM, bool FAST>
+__global__ __launch_bounds__(NT) void gdn_state_fwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, int nch) {
+  state_fwd_mfma_run<KM, FAST>(p, sv, nch, blockIdx.x, blockIdx.y);
+}
+
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+__global__ __launch_bounds__(NT) void gdn_state_bwd_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
+                                                          int nch) {
+  state_bwd_mfma_run<KM, FAST, HAS_Q, HAS_INJ>(p, sv, gr, nch, blockIdx.x, blockIdx.y);
+}
+
+typedef const __attribute__((address_space(4))) MfmaPack* MfmaPackPtr;
+
+// The pack entry of this workgroup (the pack is the kernel's only argument).
+__device__ __forceinline__ int mfma_pack_entry(MfmaPackPtr kp) {
+  int pi = 0;
+#pragma unroll 1
+  for (int i = 1; i < kp->n; ++i)
+    if ((int)blockIdx.x >= kp->wg0[i]) pi = i;
+  return pi;
+}
+
+template <int KM, bool FAST>
+__global__ __launch_bounds__(NT) void gdn_state_fwd_mfma_pack(MfmaPack pk) {
+  const MfmaPackPtr kp = (MfmaPackPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  const int pi = mfma_pack_entry(kp);
+  gpa_gdn_problem p;
+  gpa_gdn_saved sv;
+  kernarg_copy(p, &kp->p[pi]);
+  kernarg_copy(sv, &kp->sv[pi]);
+  const int local = (int)blockIdx.x - kp->wg0[pi], nvb = kp->nvb[pi];
+  state_fwd_mfma_run<KM, FAST>(p, sv, kp->nch[pi], local % nvb, local / nvb);
+}
+
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+__global__ __launch_bounds__(NT) void gdn_state_bwd_mfma_pack(MfmaPack pk) {
+  const MfmaPackPtr kp = (MfmaPackPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  const int pi = mfma_pack_entry(kp);
+  gpa_gdn_problem p;
+  gpa_gdn_saved sv;
+  gpa_gdn_grads gr;
+  kernarg_copy(p, &kp->p[pi]);
+  kernarg_copy(sv, &kp->sv[pi]);
+  kernarg_copy(gr, &kp->gr[pi]);
+  const int local = (int)blockIdx.x - kp->wg0[pi], nvb = kp->nvb[pi];
+  state_bwd_mfma_run<KM, FAST, HAS_Q, HAS_INJ>(p, sv, gr, kp->nch[pi], local % nvb, local / nvb);
+}
+
 namespace {
 
 template <typename F>
@@ -597,6 +645,47 @@ int launch_state_bwd_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
                                           : launch_bwd_flags<KM, false>(p, sv, gr, nch, st);
 }
 
+int mfma_state_workgroups(const gpa_gdn_problem& p) { return ((p.vdim + MV - 1) / MV) * p.batch * p.heads; }
+
+template <int KM>
+int launch_state_fwd_mfma_pack(const MfmaPack& pk, int total, bool fast, hipStream_t st) {
+  const size_t lds = sizeof(__bf16) * (2 * MV * (KM + TPAD) + 2 * MV * CT);
+  if (fast) {
+    if (int rc = allow_lds_mfma(gdn_state_fwd_mfma_pack<KM, true>, lds)) return rc;
+    hipLaunchKernelGGL((gdn_state_fwd_mfma_pack<KM, true>), dim3(total), dim3(NT), lds, st, pk);
+  } else {
+    if (int rc = allow_lds_mfma(gdn_state_fwd_mfma_pack<KM, false>, lds)) return rc;
+    hipLaunchKernelGGL((gdn_state_fwd_mfma_pack<KM, false>), dim3(total), dim3(NT), lds, st, pk);
+  }
+  return GPA_HIP_OK;
+}
+
+namespace {
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+int launch_bwd_pack(const MfmaPack& pk, int total, hipStream_t st) {
+  const size_t lds = sizeof(__bf16) * (2 * MV * (KM + TPAD) + 4 * MV * CT);
+  if (int rc = allow_lds_mfma(gdn_state_bwd_mfma_pack<KM, FAST, HAS_Q, HAS_INJ>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd_mfma_pack<KM, FAST, HAS_Q, HAS_INJ>), dim3(total), dim3(NT), lds, st, pk);
+  return GPA_HIP_OK;
+}
+template <int KM, bool FAST>
+int launch_bwd_pack_flags(const MfmaPack& pk, int total, bool has_q, bool has_inj, hipStream_t st) {
+  if (has_q)
+    return has_inj ? launch_bwd_pack<KM, FAST, true, true>(pk, total, st)
+                   : launch_bwd_pack<KM, FAST, true, false>(pk, total, st);
+  return has_inj ? launch_bwd_pack<KM, FAST, false, true>(pk, total, st)
+                 : launch_bwd_pack<KM, FAST, false, false>(pk, total, st);
+}
+}  // namespace
+
+template <int KM>
+int launch_state_bwd_mfma_pack(const MfmaPack& pk, int total, bool fast, bool has_q, bool has_inj, hipStream_t st) {
+  return fast ? launch_bwd_pack_flags<KM, true>(pk, total, has_q, has_inj, st)
+              : launch_bwd_pack_flags<KM, false>(pk, total, has_q, has_inj, st);
+}
+
+template int launch_state_fwd_mfma_pack<256>(const MfmaPack&, int, bool, hipStream_t);
+template int launch_state_bwd_mfma_pack<256>(const MfmaPack&, int, bool, bool, bool, hipStream_t);
 template int launch_state_fwd_mfma<64>(const gpa_gdn_problem&, const gpa_gdn_saved&, int, hipStream_t);
 template int launch_state_fwd_mfma<128>(const gpa_gdn_problem&, const gpa_gdn_saved&, int, hipStream_t);
 template int launch_state_fwd_mfma<256>(const gpa_gdn_problem&, const gpa_gdn_saved&, int, hipStream_t);

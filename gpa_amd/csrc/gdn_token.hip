@@ -172,16 +172,6 @@ struct TokenPack {
   gpa_gdn_problem p[GPA_TOKEN_MAX_PACK];
 };
 
-// A struct in the kernel-argument segment copied word by word (scalar loads).
-template <typename T>
-__device__ __forceinline__ void kernarg_copy(T& dst, const __attribute__((address_space(4))) T* src) {
-  static_assert(sizeof(T) % 4 == 0, "word copy");
-  const __attribute__((address_space(4))) uint32_t* s = (const __attribute__((address_space(4))) uint32_t*)src;
-  uint32_t* d = reinterpret_cast<uint32_t*>(&dst);
-#pragma unroll
-  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = s[i];
-}
-
 // The pack is the kernel's only argument: its entries are read through the
 // kernel-argument pointer with a uniform index, as scalar loads (indexing the
 // by-value argument would copy it to scratch).

@@ -48,16 +48,12 @@ def _in_use_here(*tensors):
             t.record_stream(stream)
 
 
-class _GDNScan(torch.autograd.Function):
-    """One group of GDN scans; saved intermediates per include/gpa_hip.h."""
+class _Group:
+    """One scan group's forward: its problem, saved intermediates (layouts of
+    include/gpa_hip.h) and outputs."""
 
-    @staticmethod
-    def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int, box=None):
-        lib = _lib.load()
+    def __init__(self, lib, q, k, v, g, beta, s0, chunk: int, offset: int, box=None):
         _in_use_here(q, k, v, g, beta, s0)
-        # Outputs nobody differentiates (often the chunk-start states) reach the
-        # backward as None, so it neither fills nor streams zero gradients.
-        ctx.set_materialize_grads(False)
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
         dev = k.device
@@ -65,8 +61,8 @@ class _GDNScan(torch.autograd.Function):
         if nch <= 0:
             raise ValueError("gdn_scan_hip: invalid chunk geometry")
         s0f = _f32_state(s0) if s0 is not None else None
-        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
-        mfma = lib.gpa_gdn_path(prob) == 1
+        self.prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        mfma = lib.gpa_gdn_path(self.prob) == 1
         chunks = bsz * heads * nch
         rows = chunks * _lib.CHUNK_ROWS
         f32 = dict(device=dev, dtype=torch.float32)
@@ -81,8 +77,8 @@ class _GDNScan(torch.autograd.Function):
         tri = torch.empty(rows * _lib.CHUNK_ROWS, **f32)
         gam = torch.empty(rows, **f32)
         bet = torch.empty(rows, **f32)
-        states = torch.empty(bsz, heads, nch, vd, kd, **f32)   # value-major chunk-start states
-        final = torch.empty(bsz, heads, kd, vd, **f32)
+        self.states = torch.empty(bsz, heads, nch, vd, kd, **f32)   # value-major chunk-start states
+        self.final = torch.empty(bsz, heads, kd, vd, **f32)
         frags = [None] * 5
         if mfma:
             k16, rb = kd // 16, (kd + 31) // 32
@@ -91,30 +87,35 @@ class _GDNScan(torch.autograd.Function):
                      torch.empty(chunks * 2 * k16 * 64 * 8, **b16),    # krow
                      torch.empty(chunks * rb * 4 * 64 * 8, **b16),     # kcol
                      torch.empty(chunks * rb * 4 * 64 * 8, **b16) if q is not None else None]  # qcol
-        out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype) if q is not None else None
-        saved = _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
-        timing = profiling.forward_timing(kd, vd, chunk, tokens * bsz * heads, k.dtype, q is not None)
-        _lib.check(lib.gpa_gdn_forward(prob, saved, _lib.operand(out), timing, _lib.stream_handle(dev)),
-                   "gpa_gdn_forward")
-        ctx.geom = (chunk, offset, nch, q is not None, s0 is not None, mfma)
-        ctx.box = box
-        ctx.save_for_backward(q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)
-        token = None
+        self.out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype) if q is not None else None
+        self.inter = (kn, qn, w, u, delta, tri, gam, bet, self.states, self.final, *frags)
+        self.saved = _lib.Saved(*(_ptr(t) for t in self.inter))
+        self.geom = (chunk, offset, nch, q is not None, s0 is not None, mfma)
+        self.timing_args = (kd, vd, chunk, tokens * bsz * heads, k.dtype, q is not None)
+        self.tensors = (q, k, v, g, beta, s0f) + self.inter
+        self.token = None
         if box is not None:  # a late read will use these intermediates
             box.args = (k, v, g, beta, s0f, chunk, offset, nch)
-            box.saved = (kn, w, u, delta, tri, gam, bet, states, final, *frags)
-            token = torch.zeros(1, device=dev)
-        return out, states, final, token
+            box.saved = (kn, w, u, delta, tri, gam, bet, self.states, self.final, *frags)
+            self.token = torch.zeros(1, device=dev)
 
-    @staticmethod
-    def backward(ctx, dout, dstates, dfinal, dtoken=None):
-        lib = _lib.load()
+    def outputs(self):
+        return self.out, self.states, self.final, self.token
+
+
+_N_SAVED = 21  # tensors a group saves: q, k, v, g, beta, s0 and its 15 intermediates
+
+
+class _GroupGrad:
+    """One scan group's backward: gradient buffers and the library structs."""
+
+    def __init__(self, saved_tensors, geom, box, dout, dstates, dfinal, needs_dq: bool):
         _in_use_here(dout, dstates, dfinal)
-        chunk, offset, nch, has_q, has_s0, mfma = ctx.geom
-        (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags) = ctx.saved_tensors
-        box = ctx.box
-        late = box is not None and box.dout is not None
-        if late:  # the late read's gradient joins this backward as its read
+        chunk, offset, nch, has_q, has_s0, mfma = geom
+        (q, k, v, g, beta, s0f, kn, qn, w, u, delta, tri, gam, bet, states, final, *frags) = saved_tensors
+        self.box = box
+        self.late = box is not None and box.dout is not None
+        if self.late:  # the late read's gradient joins this backward as its read
             q, qn, dout = box.q, box.qn, box.dout
             frags[4] = box.qcol
             has_q = True
@@ -144,19 +145,98 @@ class _GDNScan(torch.autograd.Function):
         ds0 = torch.empty(bsz, heads, kd, vd, **f32)
         dstates = dstates.float().contiguous() if dstates is not None else None
         dfinal = dfinal.float().contiguous() if dfinal is not None else None
-        prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
-        saved = _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
-        grads = _lib.Grads(_lib.operand(dout if want_read else None), _ptr(dstates), _ptr(dfinal),
-                           _ptr(dd0), _ptr(obuf), ddelta.data_ptr(), dhend.data_ptr(), dw.data_ptr(),
-                           _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
-                           _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
-        timing = profiling.backward_timing(kd, vd, chunk, tokens * bsz * heads, k.dtype, want_read)
-        _lib.check(lib.gpa_gdn_backward(prob, saved, grads, timing, _lib.stream_handle(dev)), "gpa_gdn_backward")
-        if late:  # dq of the late read was returned by the read itself
-            box.release()
-        dq_out = dq if (has_q and not late and ctx.needs_input_grad[0]) else None
-        return (dq_out, dk, dv, dg, db,
-                ds0 if has_s0 else None, None, None, None)
+        self.prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
+        self.saved = _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))
+        self.grads = _lib.Grads(_lib.operand(dout if want_read else None), _ptr(dstates), _ptr(dfinal),
+                                _ptr(dd0), _ptr(obuf), ddelta.data_ptr(), dhend.data_ptr(), dw.data_ptr(),
+                                _lib.operand(dq), _lib.operand(dk), _lib.operand(dv),
+                                _lib.operand(dg), _lib.operand(db), ds0.data_ptr())
+        # Every buffer the library reads or writes stays referenced until the
+        # call is enqueued and the record is released: a gradient this group
+        # does not return (ds0 without an initial state, dq of a late read) is
+        # still written, and memory dropped early would be handed to the next
+        # group's buffers of a packed call before the kernels run.
+        self.keep = (dout, dstates, dfinal, dd0, obuf, ddelta, dhend, dw, q, qn, frags[4], dq, ds0)
+        self.timing_args = (kd, vd, chunk, tokens * bsz * heads, k.dtype, want_read)
+        self.inj = dstates is not None
+        dq_out = dq if (has_q and not self.late and needs_dq) else None
+        self.result = (dq_out, dk, dv, dg, db, ds0 if has_s0 else None)
+
+    def done(self):
+        """The gradients to return; the record (and so its buffers) must live
+        until the library call that uses it has been enqueued."""
+        if self.late:  # dq of the late read was returned by the read itself
+            self.box.release()
+        return self.result
+
+
+class _GDNScan(torch.autograd.Function):
+    """One group of GDN scans; saved intermediates per include/gpa_hip.h."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, s0, chunk: int, offset: int, box=None):
+        lib = _lib.load()
+        # Outputs nobody differentiates (often the chunk-start states) reach the
+        # backward as None, so it neither fills nor streams zero gradients.
+        ctx.set_materialize_grads(False)
+        grp = _Group(lib, q, k, v, g, beta, s0, chunk, offset, box)
+        timing = profiling.forward_timing(*grp.timing_args)
+        _lib.check(lib.gpa_gdn_forward(grp.prob, grp.saved, _lib.operand(grp.out), timing,
+                                       _lib.stream_handle(k.device)), "gpa_gdn_forward")
+        ctx.geom, ctx.box = grp.geom, box
+        ctx.save_for_backward(*grp.tensors)
+        return grp.outputs()
+
+    @staticmethod
+    def backward(ctx, dout, dstates, dfinal, dtoken=None):
+        lib = _lib.load()
+        gg = _GroupGrad(ctx.saved_tensors, ctx.geom, ctx.box, dout, dstates, dfinal, ctx.needs_input_grad[0])
+        timing = profiling.backward_timing(*gg.timing_args)
+        _lib.check(lib.gpa_gdn_backward(gg.prob, gg.saved, gg.grads, timing,
+                                        _lib.stream_handle(ctx.saved_tensors[1].device)), "gpa_gdn_backward")
+        return gg.done() + (None, None, None)
+
+
+class _GDNScanMany(torch.autograd.Function):
+    """Several independent groups of GDN scans in one library call
+    (gpa_gdn_forward_many / gpa_gdn_backward_many): their state recurrences
+    advance together in packed launches.  Inputs: a spec of (chunk, offset,
+    box) per group, then q, k, v, g, beta, s0 of every group; outputs: out,
+    states, final, token of every group."""
+
+    @staticmethod
+    def forward(ctx, spec, *flat):
+        lib = _lib.load()
+        ctx.set_materialize_grads(False)
+        groups = [_Group(lib, *flat[6 * i:6 * i + 6], chunk, offset, box)
+                  for i, (chunk, offset, box) in enumerate(spec)]
+        n = len(groups)
+        probs, saved, outs = (_lib.Problem * n)(), (_lib.Saved * n)(), (_lib.Operand * n)()
+        for i, grp in enumerate(groups):
+            probs[i], saved[i], outs[i] = grp.prob, grp.saved, _lib.operand(grp.out)
+        timing = profiling.forward_timing_many([grp.timing_args for grp in groups])
+        _lib.check(lib.gpa_gdn_forward_many(probs, saved, outs, n, timing, _lib.stream_handle(flat[1].device)),
+                   "gpa_gdn_forward_many")
+        ctx.geoms = [grp.geom for grp in groups]
+        ctx.boxes = [box for _, _, box in spec]
+        ctx.save_for_backward(*(t for grp in groups for t in grp.tensors))
+        return tuple(x for grp in groups for x in grp.outputs())
+
+    @staticmethod
+    def backward(ctx, *douts):
+        lib = _lib.load()
+        saved_t = ctx.saved_tensors
+        n = len(ctx.geoms)
+        groups = [_GroupGrad(saved_t[_N_SAVED * i:_N_SAVED * (i + 1)], ctx.geoms[i], ctx.boxes[i],
+                             douts[4 * i], douts[4 * i + 1], douts[4 * i + 2], ctx.needs_input_grad[1 + 6 * i])
+                  for i in range(n)]
+        probs, saved, grads = (_lib.Problem * n)(), (_lib.Saved * n)(), (_lib.Grads * n)()
+        for i, gg in enumerate(groups):
+            probs[i], saved[i], grads[i] = gg.prob, gg.saved, gg.grads
+        timing = profiling.backward_timing_many([gg.timing_args + (gg.inj,) for gg in groups])
+        _lib.check(lib.gpa_gdn_backward_many(probs, saved, grads, n, timing,
+                                             _lib.stream_handle(saved_t[1].device)), "gpa_gdn_backward_many")
+        return (None,) + tuple(x for gg in groups for x in gg.done())
 
 
 class _ReadBox:
@@ -321,6 +401,66 @@ def gdn_scan_deferred(k: Tensor, v: Tensor, g: Tensor, beta: Tensor, s0: Tensor 
         return _GDNRead.apply(_contig_last(q), token, box)
 
     return states_vk.transpose(-1, -2), final, read
+
+
+def _check_group(q, k, v, g, beta, s0, chunk, offset, name):
+    _lib.require_device(k)
+    if k.dtype not in _lib.DTYPE_CODES or v.dtype != k.dtype or (q is not None and q.dtype != k.dtype):
+        raise ValueError(f"{name}: q/k/v must share float32 or bfloat16")
+    if k.ndim != 4 or v.ndim != 4 or v.shape[:3] != k.shape[:3] or (q is not None and q.shape != k.shape):
+        raise ValueError(f"{name}: expected q,k [B,T,H,K] and v [B,T,H,V]")
+    if g.shape != k.shape[:3] or beta.shape != k.shape[:3]:
+        raise ValueError(f"{name}: g and beta must be [B,T,H]")
+    if k.shape[-1] > _lib.MAX_KDIM or v.shape[-1] > _lib.MAX_VDIM:
+        raise ValueError(f"{name}: widths above K={_lib.MAX_KDIM}, V={_lib.MAX_VDIM} are not built")
+    if s0 is not None and s0.shape != (k.shape[0], k.shape[2], k.shape[3], v.shape[3]):
+        raise ValueError(f"{name}: s0 must be [B,H,K,V]")
+    if not 1 <= chunk <= _lib.CHUNK_ROWS or not 0 <= offset < chunk:
+        raise ValueError(f"{name}: need 1 <= chunk <= 64 and 0 <= offset < chunk")
+
+
+def gdn_scan_many(groups):
+    """Several independent groups of `gdn_scan_hip` / `gdn_scan_deferred` in
+    one library call whose state recurrences advance together (the packed
+    level and edge scans of the reference, packed.py:77, 121, 155, and the
+    paired A/B scans of a level, staged.py:14-35).  `groups` holds dicts with
+    q (None for a deferred group), k, v, g, beta, s0, chunk, offset and
+    optionally deferred=True (then q must be None); at most
+    `_lib.GDN_MAX_PACK` groups on one device.  Returns, in order, (out, states
+    [B,H,N,K,V], final) of each plain group and (states, final, read) of each
+    deferred group, exactly as the one-group functions."""
+    if not groups:
+        return []
+    if len(groups) > _lib.GDN_MAX_PACK:
+        raise ValueError(f"gdn_scan_many: at most {_lib.GDN_MAX_PACK} groups per call")
+    spec, flat, deferred = [], [], []
+    for grp in groups:
+        q, k, v, g, beta, s0 = (grp.get(x) for x in ("q", "k", "v", "g", "beta", "s0"))
+        chunk, offset, late = grp["chunk"], grp.get("offset", 0), grp.get("deferred", False)
+        _check_group(q, k, v, g, beta, s0, chunk, offset, "gdn_scan_many")
+        if late and (q is not None or not read_supported(k, v)):
+            raise ValueError("gdn_scan_many: a deferred group takes no query and needs read_supported keys/values")
+        box = _ReadBox() if late else None
+        spec.append((chunk, offset, box))
+        deferred.append(late)
+        flat += [_contig_last(q) if q is not None else None, _contig_last(k), _contig_last(v), g.float(),
+                 beta.float(), s0]
+    res = _GDNScanMany.apply(tuple(spec), *flat)
+    outs = []
+    for i, late in enumerate(deferred):
+        out, states_vk, final, token = res[4 * i:4 * i + 4]
+        if not late:
+            outs.append((out, states_vk.transpose(-1, -2), final))
+            continue
+        k = flat[6 * i + 1]
+        box = spec[i][2]
+
+        def read(q: Tensor, k=k, token=token, box=box) -> Tensor:
+            if q.shape != k.shape or q.dtype != k.dtype:
+                raise ValueError("gdn_scan_deferred: the query must match the keys' shape and dtype")
+            return _GDNRead.apply(_contig_last(q), token, box)
+        outs.append((states_vk.transpose(-1, -2), final, read))
+    return outs
 
 
 def token_step_supported(k: Tensor, v: Tensor) -> bool:

@@ -110,42 +110,109 @@ def kernel_timer():
         timer.collect()
 
 
-def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
-    if _active is None:
-        return None
+def _prep(k, v, c, tokens, dtype):
     e, km = _tag(dtype), _kmax(k)
+    return (f"gdn_prep_mfma<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
+            (4 * c * k + 2 * c * v + c * c / 3) * tokens)
+
+
+def _on_strips(k, dtype) -> bool:
+    """Mirror of the library's choice of the strip state kernels (packable)."""
+    return _mfma(k, dtype) and k <= 128
+
+
+def _state_fwd_name(k, dtype) -> str:
+    km = _kmax(k)
     if _mfma(k, dtype):
-        state = f"gdn_state_fwd_strip<{km}>" if km <= 128 else f"gdn_state_fwd_mfma<{km}>"
-    else:
-        state = f"gdn_state_fwd<{km}>"
-    kernels = [(f"gdn_prep_mfma<{e},{km},{'true' if _mfma(k, dtype) else 'false'}>",
-                (4 * c * k + 2 * c * v + c * c / 3) * tokens),
-               (state, 4 * k * v * tokens)]
+        return f"gdn_state_fwd_strip<{km}>" if km <= 128 else f"gdn_state_fwd_mfma<{km}>"
+    return f"gdn_state_fwd<{km}>"
+
+
+def _state_bwd_name(k, dtype) -> str:
+    km = _kmax(k)
+    if _mfma(k, dtype):
+        return f"gdn_state_bwd_strip<{km}>" if km <= 128 else f"gdn_state_bwd_mfma<{km}>"
+    return f"gdn_state_bwd<{_tag(dtype)},{km}>"
+
+
+def _out(k, v, c, tokens, dtype):
+    e, km = _tag(dtype), _kmax(k)
+    name = f"gdn_out_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_out_fwd<{e},{km}>"
+    return name, (2 * k * v + 2 * c * k + 2 * c * v) * tokens
+
+
+def _dd0(k, v, c, tokens, dtype):
+    e, km = _tag(dtype), _kmax(k)
+    name = f"gdn_dd0_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_dd0<{e},{km}>"
+    return name, (2 * c * k + 2 * c * v) * tokens
+
+
+def _chunk_bwd(k, v, c, tokens, dtype, read):
+    e, km = _tag(dtype), _kmax(k)
+    flop = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c
     if read:
-        out = f"gdn_out_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_out_fwd<{e},{km}>"
-        kernels.append((out, (2 * k * v + 2 * c * k + 2 * c * v) * tokens))
-    return _active.timing(kernels)
+        flop += 2 * k * v + 2 * c * v + 6 * c * k
+    mfma_chunk = k % 4 == 0 and not (km == 256 and e == "f32")
+    return f"{'gdn_chunk_bwd_mfma' if mfma_chunk else 'gdn_chunk_bwd'}<{e},{km}>", flop * tokens
+
+
+def forward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
+    return forward_timing_many([(k, v, c, tokens, dtype, read)])
 
 
 def backward_timing(k: int, v: int, c: int, tokens: int, dtype, read: bool):
+    return backward_timing_many([(k, v, c, tokens, dtype, read, None)])
+
+
+_MFMA_MAXP = 5  # problems per packed launch of the 256-key MFMA state kernels
+
+
+def _state_launches(groups, key, name, flop):
+    """The state launches of a many-call in the library's order: the groups on
+    the strip kernels with equal `key` share one launch, at the position of the
+    first of them, and so do up to five 256-key MFMA groups; the others launch
+    alone."""
+    kernels, done = [], [False] * len(groups)
+    for i, gi in enumerate(groups):
+        if done[i]:
+            continue
+        strips, wide = _on_strips(gi[0], gi[4]), _mfma(gi[0], gi[4]) and gi[0] > 128
+        if not (strips or wide):
+            kernels.append((name(gi[0], gi[4]), flop(gi)))
+            continue
+        total, count = 0.0, 0
+        for j in range(i, len(groups)):
+            gj = groups[j]
+            same = _on_strips(gj[0], gj[4]) if strips else (_mfma(gj[0], gj[4]) and gj[0] > 128)
+            if done[j] or not same or key(gj) != key(gi) or (wide and count == _MFMA_MAXP):
+                continue
+            total += flop(gj)
+            count += 1
+            done[j] = True
+        kernels.append((name(gi[0], gi[4]), total))
+    return kernels
+
+
+def forward_timing_many(groups):
+    """Kernel list of gpa_gdn_forward_many over groups (k, v, c, tokens, dtype,
+    read): every prep, the state launches, every read."""
     if _active is None:
         return None
-    e, km = _tag(dtype), _kmax(k)
-    kernels = []
-    if read:
-        dd0 = f"gdn_dd0_mfma<{km}>" if _mfma(k, dtype) and v <= 256 else f"gdn_dd0<{e},{km}>"
-        kernels.append((dd0, (2 * c * k + 2 * c * v) * tokens))
-    if _mfma(k, dtype):
-        state = f"gdn_state_bwd_strip<{km}>" if km <= 128 else f"gdn_state_bwd_mfma<{km}>"
-    else:
-        state = f"gdn_state_bwd<{e},{km}>"
-    kernels.append((state, (6 if read else 4) * k * v * tokens))
-    chunk = 4 * k * v + 4 * c * v + 4 * c * k + 2 * c * c
-    if read:
-        chunk += 2 * k * v + 2 * c * v + 6 * c * k
-    mfma_chunk = k % 4 == 0 and not (km == 256 and e == "f32")
-    name = "gdn_chunk_bwd_mfma" if mfma_chunk else "gdn_chunk_bwd"
-    kernels.append((f"{name}<{e},{km}>", chunk * tokens))
+    kernels = [_prep(*g[:5]) for g in groups]
+    kernels += _state_launches(groups, lambda g: _kmax(g[0]), _state_fwd_name, lambda g: 4 * g[0] * g[1] * g[3])
+    kernels += [_out(*g[:5]) for g in groups if g[5]]
+    return _active.timing(kernels)
+
+
+def backward_timing_many(groups):
+    """Kernel list of gpa_gdn_backward_many over groups (k, v, c, tokens,
+    dtype, read, injected): every dd0, the state launches, every chunk kernel."""
+    if _active is None:
+        return None
+    kernels = [_dd0(*g[:5]) for g in groups if g[5]]
+    kernels += _state_launches(groups, lambda g: (_kmax(g[0]), g[5], g[6]), _state_bwd_name,
+                               lambda g: (6 if g[5] else 4) * g[0] * g[1] * g[3])
+    kernels += [_chunk_bwd(*g[:6]) for g in groups]
     return _active.timing(kernels)
 
 

@@ -29,7 +29,8 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib, glue, params
-from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_token_hip, gdn_token_many, gdn_token_read
+from .ops import gdn_scan_deferred, gdn_scan_hip, gdn_scan_many, gdn_token_hip, gdn_token_many
+from .ops import gdn_token_read
 from .ops import token_step_supported
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
@@ -211,12 +212,20 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         # same keys, values, gates and initial state: where the kernels allow,
         # the B scan keeps its intermediates for that read instead.
         deferred = _DEFER_OUTER_READ[0] and late_read_supported(slot, value)
-        b_scan = gdn_scan_deferred if deferred else (lambda *a, **kw: gdn_scan_hip(None, *a, **kw)[1:] + (None,))
-        (raw, a_starts, a_final), (b_starts, b_final, lv.b_read) = _concurrent([
-            (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan),
-             (q, key, slot, g_in, b_in, old.inner)),
-            (lambda: b_scan(slot, value, g_out, b_out, old.outer, **scan),
-             (slot, value, g_out, b_out, old.outer))])
+        if _PACKED[0]:
+            # the A_j and B_j scans in one call: their state recurrences advance together
+            (raw, a_starts, a_final), b = gdn_scan_many([
+                dict(q=q, k=key, v=slot, g=g_in, beta=b_in, s0=old.inner, **scan),
+                dict(q=None, k=slot, v=value, g=g_out, beta=b_out, s0=old.outer, deferred=deferred, **scan)])
+            b_starts, b_final, lv.b_read = b if deferred else b[1:] + (None,)
+        else:
+            b_scan = gdn_scan_deferred if deferred else (
+                lambda *a, **kw: gdn_scan_hip(None, *a, **kw)[1:] + (None,))
+            (raw, a_starts, a_final), (b_starts, b_final, lv.b_read) = _concurrent([
+                (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan),
+                 (q, key, slot, g_in, b_in, old.inner)),
+                (lambda: b_scan(slot, value, g_out, b_out, old.outer, **scan),
+                 (slot, value, g_out, b_out, old.outer))])
         # Snapshots: block 0 uses the cached ones, which are the scans' own
         # initial states unless the call starts inside a block.
         first_a = None if snap.inner is old.inner else snap.inner
@@ -261,9 +270,11 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         for lv in levels:
             if lv.b_token is not None:
                 lv.b_read = _outer_token(lv)
-        reads = _concurrent([(outer_read(lv, qo, state.levels[j].outer),
-                              (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
-                             for j, (lv, qo) in enumerate(zip(levels, queries))])
+        jobs = [(outer_read(lv, qo, state.levels[j].outer),
+                 (qo, lv.slot, lv.value, lv.g_out, lv.b_out, state.levels[j].outer))
+                for j, (lv, qo) in enumerate(zip(levels, queries))]
+        # with packed scans everything runs in order on the current stream
+        reads = [fn() for fn, _ in jobs] if _PACKED[0] else _concurrent(jobs)
     if not (_SERIAL[0] or torch.cuda.is_current_stream_capturing()):
         for lv in levels:  # states made by a one-token outer step on a side stream
             if lv.b_starts is None and lv.b_final is not None:
@@ -464,6 +475,7 @@ def _residual_eta(key, value, rk, rv, eta):
 _FUSED_LEVEL = [True]  # the fused level write and residual (level.py)
 _DEFER_OUTER_READ = [True]  # outer reads as late reads of the B scans (ops.gdn_scan_deferred)
 _TOKEN_STEP = [True]  # one-token inference calls as token steps (ops.gdn_token_hip)
+_PACKED = [True]  # a level's A/B scans and all edge scans as packed calls (ops.gdn_scan_many)
 
 
 def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):
@@ -537,6 +549,20 @@ def _relations(model, local, writes, rel_states, scan, token=False):
         calls = [(local[i], writes[i], writes[j], decay[e].expand(lead), strength[e].expand(lead), old.memory)
                  for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))]
         done = [r for part in _chunks(calls, _lib.TOKEN_MAX_PACK) for r in gdn_token_many(part)]
+    elif _PACKED[0]:
+        # every edge's scan in as few library calls as it takes: the state
+        # recurrences of all edges advance together
+        lead = writes[0].shape[:-1]
+        groups = []
+        for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
+            g, beta, target = decay[e].expand(lead), strength[e].expand(lead), writes[j]
+            if cfg.rsa_update:
+                norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
+                target = (target / norm[..., None]).to(target.dtype)
+                beta = (beta * norm.square()).clamp_max(.9)
+            groups.append(dict(q=local[i], k=writes[i], v=target, g=g, beta=beta, s0=old.memory, **scan))
+        done = [(msg, final) for part in _chunks(groups, _lib.GDN_MAX_PACK)
+                for msg, _, final in gdn_scan_many(part)]
     else:
         done = _concurrent([edge(e, i, j, old) for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))])
     incoming = [[] for _ in local]

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 17
+#define GPA_HIP_ABI_VERSION 18
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -120,7 +120,7 @@ typedef struct gpa_gdn_grads {
  * before the i-th kernel an entry point launches and events[n] after the
  * last one (n = *launched on return, at most GPA_MAX_TIMED).  The events are
  * created and read by the caller (hipEventCreate / hipEventElapsedTime). */
-#define GPA_MAX_TIMED 4
+#define GPA_MAX_TIMED 40
 typedef struct gpa_timing {
     hipEvent_t events[GPA_MAX_TIMED + 1];
     int32_t launched;
@@ -145,6 +145,25 @@ int gpa_gdn_forward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
  * ops.py:49-85 in the reference, plus chunk-start state injections). */
 int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
                      const gpa_gdn_grads *grads, gpa_timing *timing, hipStream_t stream);
+
+/* Forward / backward of up to GPA_GDN_MAX_PACK independent scan groups in one
+ * call (saved[i], outs[i], grads[i] belong to problems[i]): the packed level
+ * and edge launches of the reference (packed.py:77, 121, 155 pack the levels
+ * or the edges into one scan over L*H or E*H heads; staged.py:14-35 pairs the
+ * A and B scans of a level).  The chunk-parallel kernels run once per group;
+ * the sequential state recurrences of all groups on the bf16 strip kernels
+ * (K <= 128) advance together in one launch per key-width class (and, in the
+ * backward, per presence of a read gradient and of state injections).
+ * Results are those of one gpa_gdn_forward / gpa_gdn_backward per group; the
+ * groups must not write a buffer another one reads.  timing (may be NULL)
+ * marks every launch in order: the preps, the state launches, the reads
+ * (forward); the dd0 kernels, the state launches, the chunk kernels
+ * (backward). */
+#define GPA_GDN_MAX_PACK 12
+int gpa_gdn_forward_many(const gpa_gdn_problem *problems, const gpa_gdn_saved *saved, const gpa_operand *outs,
+                         int32_t n, gpa_timing *timing, hipStream_t stream);
+int gpa_gdn_backward_many(const gpa_gdn_problem *problems, const gpa_gdn_saved *saved,
+                          const gpa_gdn_grads *grads, int32_t n, gpa_timing *timing, hipStream_t stream);
 
 /* A late read: `out` = u(q_t)^T S_t for a query that arrives after the scan.
  * `saved` holds the intermediates of a gpa_gdn_forward that ran with

@@ -56,7 +56,7 @@ def test_ctypes_structs_match_c_layout():
     assert ctypes.sizeof(_lib.Problem) == 32 + 5 * 32 + 24
     assert ctypes.sizeof(_lib.Saved) == 15 * 8
     assert ctypes.sizeof(_lib.Grads) == 32 + 7 * 8 + 5 * 32 + 8
-    assert ctypes.sizeof(_lib.Timing) == 5 * 8 + 8
+    assert ctypes.sizeof(_lib.Timing) == (_lib.MAX_TIMED + 1) * 8 + 8 and _lib.MAX_TIMED == 40
     assert ctypes.sizeof(_lib.DecodeState) == 16
     # slots (+pad), 7 parameter pointers, 5 states, 3 output pointers
     assert ctypes.sizeof(_lib.DecodeLevel) == 8 + 7 * 8 + 5 * 16 + 3 * 8

@@ -181,3 +181,32 @@ def test_empty_call_returns_same_state_and_state_is_query_independent():
     for a, b in zip(s1.levels, s2.levels):
         assert torch.equal(a.inner, b.inner) and torch.equal(a.outer, b.outer)
     assert not torch.allclose(y1, y2)
+
+
+@pytest.mark.parametrize("name", ["c2_dims", "lm_flags", "c3_dims"])
+def test_packed_scans_match_the_stream_schedule(name, monkeypatch):
+    """The packed scan calls (a level's A/B pair and every edge in one library
+    call, schedule._PACKED) against the same schedule with one call per scan
+    group on side streams: output, every cache tensor and every gradient."""
+    from gpa_amd import schedule
+    spec = CONFIGS[name]
+    dtype = torch.bfloat16 if name == "c3_dims" else torch.float32
+    runs = {}
+    for packed in (True, False):
+        monkeypatch.setattr(schedule, "_PACKED", [packed])
+        model, q, k, v, ctrl = _setup(spec["cfg"], spec["b"], spec["t"], dtype, seed=9,
+                                      normalize_k=spec.get("normalize_k", False),
+                                      gate_noise=spec.get("gate_noise", 0.), control_dim=spec.get("control_dim", 0))
+        model = model.to(DEV)
+        xs = [x.to(DEV).requires_grad_() for x in (q, k, v)]
+        c = ctrl.to(DEV) if ctrl is not None else None
+        out, state = model(*xs, control_input=c)
+        out.float().square().mean().backward()
+        runs[packed] = ([out] + list(tensors(state)), [p.grad for p in model.parameters()] + [x.grad for x in xs])
+    tol = 1e-5 if dtype == torch.float32 else 5e-3
+    for kind, a_list, b_list in (("forward", runs[True][0], runs[False][0]), ("grad", runs[True][1], runs[False][1])):
+        for i, (a, b) in enumerate(zip(a_list, b_list)):
+            if a is None or b is None:
+                assert a is None and b is None, (kind, i)
+                continue
+            assert _rel(a, b) < tol, (kind, i, _rel(a, b))

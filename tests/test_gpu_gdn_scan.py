@@ -235,3 +235,86 @@ def test_late_read_taken_once():
     read(q.to(DEV))
     with pytest.raises(ValueError):
         read(q.to(DEV))
+
+
+# Packed groups (gpa_gdn_forward_many / gpa_gdn_backward_many): K <= 128 bf16
+# groups share their strip state launches, the 256-key bf16 groups share the
+# MFMA state launches, the fp32 and non-multiple-of-16 groups launch alone.
+# Offsets and chunk lengths differ between groups; some groups have no
+# initial state (their ds0 is written but not returned).
+MANY = [
+    # (B, T, H, K, V, chunk, offset, dtype, query, s0, deferred)
+    (1, 130, 2, 128, 128, 64, 0, torch.bfloat16, True, True, False),
+    (1, 130, 2, 128, 256, 64, 0, torch.bfloat16, False, True, True),
+    (2, 70, 2, 64, 96, 64, 17, torch.bfloat16, True, False, False),
+    (1, 129, 1, 256, 128, 64, 1, torch.bfloat16, True, True, False),
+    (1, 100, 2, 128, 64, 32, 5, torch.bfloat16, True, True, False),
+    (1, 96, 2, 256, 256, 64, 30, torch.bfloat16, True, False, False),
+    (1, 130, 1, 256, 96, 64, 0, torch.bfloat16, True, True, False),
+    (1, 40, 2, 40, 24, 16, 5, torch.bfloat16, True, True, False),
+    (1, 70, 2, 32, 48, 64, 17, torch.float32, True, True, False),
+]
+
+
+def _many_groups(seed):
+    groups = []
+    for i, (b, t, h, kd, vd, chunk, offset, dtype, query, s0, deferred) in enumerate(MANY):
+        q, k, v, g, beta, st = _inputs(b, t, h, kd, vd, dtype, seed + i, q=query, s0=s0)
+        if deferred:
+            qr = torch.randn(b, t, h, kd, generator=torch.Generator().manual_seed(seed + 50 + i)).to(dtype)
+        else:
+            qr = None
+        leaves = [x.to(DEV).requires_grad_() if x is not None else None for x in (q, k, v, g, beta, st, qr)]
+        groups.append((leaves, chunk, offset, deferred))
+    return groups
+
+
+def _many_loss(results, groups, seed):
+    """A loss over every output, every chunk-start state (state injections) and
+    every final state, with fixed random weights."""
+    gen = torch.Generator().manual_seed(seed)
+    loss = 0.
+    for (leaves, _, _, deferred), res in zip(groups, results):
+        if deferred:
+            states, final, read = res
+            out = read(leaves[6])
+        else:
+            out, states, final = res
+        parts = [x for x in (out, states, final) if x is not None]
+        for x in parts:
+            wgt = torch.randn(x.shape, generator=gen).to(DEV)
+            loss = loss + (x.float() * wgt).sum()
+    return loss
+
+
+def test_scan_many_matches_one_call_per_group():
+    from gpa_amd.ops import gdn_scan_deferred, gdn_scan_hip, gdn_scan_many
+    results = {}
+    for packed in (True, False):
+        groups = _many_groups(300)
+        if packed:
+            res = gdn_scan_many([dict(q=lv[0], k=lv[1], v=lv[2], g=lv[3], beta=lv[4], s0=lv[5], chunk=c, offset=o,
+                                      deferred=d) for lv, c, o, d in groups])
+        else:
+            res = [gdn_scan_deferred(lv[1], lv[2], lv[3], lv[4], lv[5], chunk=c, offset=o) if d else
+                   gdn_scan_hip(lv[0], lv[1], lv[2], lv[3], lv[4], lv[5], chunk=c, offset=o)
+                   for lv, c, o, d in groups]
+        loss = _many_loss(res, groups, 7)
+        loss.backward()
+        fwd = [x.detach() for r, (_, _, _, d) in zip(res, groups) for x in (r[:2] if d else r) if x is not None]
+        grads = [x.grad for lv, _, _, _ in groups for x in lv if x is not None]
+        results[packed] = (fwd, grads)
+    (fa, ga), (fb, gb) = results[True], results[False]
+    assert len(fa) == len(fb) and len(ga) == len(gb)
+    for i, (a, b) in enumerate(zip(fa, fb)):
+        assert _rel(a, b) < 1e-6, ("forward", i, _rel(a, b))
+    for i, (a, b) in enumerate(zip(ga, gb)):
+        assert a is not None and b is not None, ("grad", i)
+        assert _rel(a, b) < 1e-5, ("grad", i, _rel(a, b))
+
+
+def test_scan_many_refuses_too_many_groups():
+    from gpa_amd.ops import gdn_scan_many
+    q, k, v, g, beta, st = (x.to(DEV) if x is not None else None for x in _inputs(1, 8, 1, 16, 16, torch.bfloat16, 1))
+    with pytest.raises(ValueError):
+        gdn_scan_many([dict(q=q, k=k, v=v, g=g, beta=beta, s0=st, chunk=8)] * 13)

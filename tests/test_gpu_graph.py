@@ -213,12 +213,14 @@ def test_decode_graph_matches_oracle_at_c3_widths(dtype):
 TOL_DEC = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
 
-def test_capture_keeps_the_schedule_on_the_capturing_stream(monkeypatch):
+@pytest.mark.parametrize("packed", [False, True], ids=["streams", "packed"])
+def test_capture_keeps_the_schedule_on_the_capturing_stream(packed, monkeypatch):
     """Graphs are captured single-stream: while a GradientGraph or a
     DecodeGraph captures, the schedule runs its independent scans in order on
     the capturing stream and never takes its side streams (no cross-stream
-    fork/join or allocator stream records inside a capture), while the eager
-    warm-up calls of the training step do take them."""
+    fork/join or allocator stream records inside a capture).  With one call
+    per scan group the eager warm-up calls of the training step do take them;
+    with packed scan calls (the default) no call takes a side stream."""
     from gpa_amd import schedule
     from gpa_amd.graph import DecodeGraph
     seen = []
@@ -230,6 +232,7 @@ def test_capture_keeps_the_schedule_on_the_capturing_stream(monkeypatch):
 
     monkeypatch.setattr(schedule, "_side_streams", spy)
     monkeypatch.setattr(schedule, "_SERIAL", [False])
+    monkeypatch.setattr(schedule, "_PACKED", [packed])
     torch.manual_seed(2)
     cfg = GPAConfig(heads=2, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=4)
     model = DenseGPA(cfg).to(DEV)
@@ -241,7 +244,8 @@ def test_capture_keeps_the_schedule_on_the_capturing_stream(monkeypatch):
         return out.float().square().mean(), out
 
     GradientGraph(model, xs, loss_fn, warmups=1)
-    assert seen and not any(seen), "side streams taken while capturing the training step"
+    assert not any(seen), "side streams taken while capturing the training step"
+    assert packed or seen, "the eager warm-up of the stream schedule took no side stream"
     eager_calls = len(seen)
     seen.clear()
     with torch.no_grad():
@@ -250,7 +254,7 @@ def test_capture_keeps_the_schedule_on_the_capturing_stream(monkeypatch):
     # (one-token decode packs its independent steps into single launches and
     # may take no side stream at all)
     assert not any(seen), "side streams taken while capturing a decode step"
-    assert eager_calls > 0
+    assert packed or eager_calls > 0
 
 
 def test_gradient_graph_capture_accumulates_on_the_capturing_stream(monkeypatch):
