@@ -300,6 +300,20 @@ def main() -> int:
                     "avg_launch_us": dominant["avg_us"], "launches": dominant["launches"],
                     "share_of_step": dominant["total_ms"] / serial_ms,
                     "timed_in": f"one extra step on one stream ({serial_ms:.1f} ms)"}
+    # The sequential state recurrences: every state launch of the step together
+    # (packed launches advance several scan groups at once), algorithmic FLOP
+    # over their summed launch time.
+    state_rows = [r for r in timer.table() if "_state_" in r["name"]]
+    state_roofline = None
+    if state_rows:
+        st_ms = sum(r["total_ms"] for r in state_rows)
+        st_flop = sum(r["tflops"] * r["total_ms"] * 1e-3 * 1e12 for r in state_rows)
+        st_tf = st_flop / (st_ms * 1e-3) / 1e12
+        state_roofline = {"bound": "latency", "achieved": st_tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                          "frac": st_tf / PEAK_BF16_TFLOPS, "launches": sum(r["launches"] for r in state_rows),
+                          "total_ms": st_ms, "share_of_step": st_ms / serial_ms,
+                          "limited_by": "one dependent chunk step after another (128 per launch at T=8192)"}
+    kernels = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in timer.table()[:12]]
     result = {
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -308,6 +322,8 @@ def main() -> int:
                                "C=64, bf16 activations", "global_batch": BATCH, "seq_len": TOKENS,
                    "parallelism": "single GPU"},
         "roofline": roofline,
+        "state_roofline": state_roofline,
+        "kernels_one_stream_step": kernels,
         "step_roofline": {"bound": "mfma", "achieved": step_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                           "frac": step_tflops / PEAK_BF16_TFLOPS, "flop_per_step": flop_step},
     }

@@ -113,6 +113,10 @@ class DecodeGraph:
             raise ValueError("DecodeGraph: the cache must start at a block boundary (chunk_offset 0)")
         if q.shape[1] != 1:
             raise ValueError("DecodeGraph: one token per call")
+        if model.config.positional_mode == "moments":
+            # the rotary embedding reads the absolute position, which a
+            # replayed graph would keep at its captured value
+            raise ValueError("DecodeGraph: positional_mode='moments' depends on the position; decode eagerly")
         from .state import _apply, tensors
         self._tensors = tensors
         self.chunk = state.chunk_size

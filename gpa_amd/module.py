@@ -166,7 +166,7 @@ class DenseGPA(nn.Module):
             out, new_state, routes = v.new_empty(v.shape), state, None
         elif cfg.chunk_size == 1:
             out, new_state, routes = run_tokens(self, q, k, v, state, control_input,
-                                                want_routes=return_diagnostics)
+                                                want_routes=return_diagnostics, position_ids=position_ids)
         elif not return_diagnostics and decode_supported(self, q, k, v, state, control_input):
             (out, new_state), routes = decode_step(self, q, k, v, state), None
         else:

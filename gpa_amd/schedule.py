@@ -41,6 +41,7 @@ from .level import level_mix, level_mix_block
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
 from .route import supported as fused_route_supported
+from .positional import additive_scan, rope
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
 
 _F32 = torch.float32
@@ -148,10 +149,12 @@ def _snapshots(starts: Tensor, first: Tensor) -> Tensor:
 
 class _Level:
     __slots__ = ("slot", "value", "g_out", "b_out", "write", "counts", "final_count", "logits", "a_final",
-                 "b_final", "a_starts", "b_starts", "b_read", "local", "b_token")
+                 "b_final", "a_starts", "b_starts", "b_read", "local", "b_token", "correction", "moment")
 
     def __init__(self):
         self.local = None  # the local read distribution, when the counts kernel gave it
+        # positional moments: the read of the moment state and the new state
+        self.correction = self.moment = None
         # A one-token outer step deferred to its read: (slot, value, g, beta, s0)
         # of the B_j step, which runs with the route query in one kernel.
         self.b_token = None
@@ -167,8 +170,6 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     _lib.require_device(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("backend='hip' computes in float32 or bfloat16 activations")
-    if cfg.positional_mode == "moments":
-        raise ValueError("positional_mode='moments' is not built for backend='hip'")
     bsz, tokens, heads, dk = q.shape
     dtype = q.dtype
     chunk, offset = cfg.chunk_size, state.chunk_offset
@@ -179,6 +180,9 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     # that reads and writes its state once, and the level mix reads the cached
     # block snapshots, so no chunk-start states are kept.
     token = _TOKEN_STEP[0] and tokens == 1 and not torch.is_grad_enabled()
+    # positional moments: the inner reads and the route reader take the rotated
+    # query (attention.py:305)
+    qr = rope(q, position_ids) if cfg.positional_mode == "moments" else q
 
     # ---- level pass (storage + inner reads), attention.py:309-329
     key, value = k, v
@@ -197,13 +201,14 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         fused_level = write is None and _FUSED_LEVEL[0] and fused_level_supported(
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
         if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
-            raw, a_final = gdn_token_hip(q, key, slot, g_in, b_in, old.inner)
+            raw, a_final = gdn_token_hip(qr, key, slot, g_in, b_in, old.inner)
             # The B_j step runs at its read, after the route reader (nothing
             # before needs the new B_j): one pass over the state for both.
             lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
             write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
             lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
+            _moments(lv, key, qr, position_ids, old)
             _level_logits(model, lv, j, raw, old)
             levels.append(lv)
             key, value = key_next, value_next
@@ -215,15 +220,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         if _PACKED[0]:
             # the A_j and B_j scans in one call: their state recurrences advance together
             (raw, a_starts, a_final), b = gdn_scan_many([
-                dict(q=q, k=key, v=slot, g=g_in, beta=b_in, s0=old.inner, **scan),
+                dict(q=qr, k=key, v=slot, g=g_in, beta=b_in, s0=old.inner, **scan),
                 dict(q=None, k=slot, v=value, g=g_out, beta=b_out, s0=old.outer, deferred=deferred, **scan)])
             b_starts, b_final, lv.b_read = b if deferred else b[1:] + (None,)
         else:
             b_scan = gdn_scan_deferred if deferred else (
                 lambda *a, **kw: gdn_scan_hip(None, *a, **kw)[1:] + (None,))
             (raw, a_starts, a_final), (b_starts, b_final, lv.b_read) = _concurrent([
-                (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **scan),
-                 (q, key, slot, g_in, b_in, old.inner)),
+                (lambda: gdn_scan_hip(qr, key, slot, g_in, b_in, old.inner, **scan),
+                 (qr, key, slot, g_in, b_in, old.inner)),
                 (lambda: b_scan(slot, value, g_out, b_out, old.outer, **scan),
                  (slot, value, g_out, b_out, old.outer))])
         # Snapshots: block 0 uses the cached ones, which are the scans' own
@@ -238,6 +243,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                                                            eta, blocks, write)
         lv.slot, lv.value, lv.g_out, lv.b_out = slot, value, g_out, b_out
         lv.write = write
+        _moments(lv, key, qr, position_ids, old)
         _level_logits(model, lv, j, raw, old)
         lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, b_final, a_starts, b_starts
         levels.append(lv)
@@ -248,7 +254,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan, token)
 
     # ---- route reader, attention.py:225-262
-    routes, queries = _bridge(model, q, [lv.logits for lv in levels], incoming, [lv.counts for lv in levels])
+    routes, queries = _bridge(model, qr, [lv.logits for lv in levels], incoming, [lv.counts for lv in levels])
 
     # ---- outer reads and level mix, attention.py:333-341
     ol = model.output_logits
@@ -295,7 +301,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         last = blocks.n - 1
         frozen = frozen0 if last == 0 else tuple(
             ResidualSnapshot(lv.a_starts[:, :, last], lv.b_starts[:, :, last]) for lv in levels)
-    new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.final_count, None) for lv in levels)
+    new_levels = tuple(LevelState(lv.a_final, lv.b_final, lv.final_count, lv.moment) for lv in levels)
     new_state = GPAState(new_levels, relations, state.position + tokens, chunk, new_offset, frozen)
     return out, new_state, (tuple(routes) if want_routes else None)
 
@@ -310,7 +316,7 @@ def _outer_token(lv):
 
 
 def run_tokens(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, control: Tensor | None, *,
-               want_routes: bool = False):
+               want_routes: bool = False, position_ids: Tensor | None = None):
     """The tokenwise model (`chunk_size == 1`, attention.py:264-297, the loop at
     :385-393).  Each token passes through every level with the updated states:
     the write reads the updated inner state, the residuals use the updated
@@ -322,12 +328,13 @@ def run_tokens(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, control:
     _lib.require_device(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("backend='hip' computes in float32 or bfloat16 activations")
-    if cfg.positional_mode == "moments":
-        raise ValueError("positional_mode='moments' is not built for backend='hip'")
+    if position_ids is None:
+        position_ids = torch.arange(state.position, state.position + q.shape[1], device=q.device)
     outs, routes = [], []
     for t in range(q.shape[1]):
         ctl = control[:, t:t + 1] if control is not None else None
-        out, state, r = _token(model, q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], state, ctl)
+        pos = position_ids[t] if position_ids.ndim == 1 else position_ids[:, t:t + 1]
+        out, state, r = _token(model, q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], state, ctl, pos)
         outs.append(out)
         routes.append(r)
     routes = tuple(torch.cat(r, 1) for r in zip(*routes)) if want_routes else None
@@ -340,10 +347,11 @@ def _read(x: Tensor, s: Tensor) -> Tensor:
     return torch.einsum("bthk,bhkv->bthv", _unit(x).float(), s.float()).to(x.dtype)
 
 
-def _token(model, q, k, v, state: GPAState, control):
+def _token(model, q, k, v, state: GPAState, control, position=None):
     """One token of the tokenwise model (attention.py:264-297), on [B,1,H,.] views."""
     cfg = model.config
     dtype = q.dtype
+    qr = rope(q, position) if cfg.positional_mode == "moments" else q
     step = dict(chunk=1, offset=0)
     key, value = k, v
     new_levels, writes, logits = [], [], []
@@ -351,23 +359,29 @@ def _token(model, q, k, v, state: GPAState, control):
         slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
         g_in, b_in, g_out, b_out = _gates(model, key, j, control)
         (raw, _, a), (_, _, b) = _concurrent([
-            (lambda: gdn_scan_hip(q, key, slot, g_in, b_in, old.inner, **step),
-             (q, key, slot, g_in, b_in, old.inner)),
+            (lambda: gdn_scan_hip(qr, key, slot, g_in, b_in, old.inner, **step),
+             (qr, key, slot, g_in, b_in, old.inner)),
             (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **step),
              (slot, value, g_out, b_out, old.outer))])
         write = _assignment(cfg, slot)
         if write is None:
             write = _read(key, a).softmax(-1)
         count = old.count + write[:, 0].to(old.count.dtype)
-        logits.append(_base_logits(model, raw, count[:, None], j))
+        moment, correction = old.position, None
+        if moment is not None:  # attention.py:276-281
+            kh = _unit(key)
+            delta = (rope(kh, position) - kh).to(moment.dtype)
+            moment = moment + delta[:, 0, :, :, None] * write[:, 0].to(delta.dtype)[..., None, :]
+            correction = _read(qr, moment)
+        logits.append(_base_logits(model, raw, count[:, None], j, correction))
         writes.append(write)
-        new_levels.append(LevelState(a, b, count, None))
+        new_levels.append(LevelState(a, b, count, moment))
         rk = torch.einsum("bhdm,bthm->bthd", a, write.float())
         rv = torch.einsum("bthm,bhmv->bthv", write.float(), b)
         key, value = _residual(model, key, value, rk, rv, j)
     local = [lg.softmax(-1).to(dtype) for lg in logits]
     incoming, relations = _relations(model, local, writes, state.relations, step)
-    routes, queries = _bridge(model, q, logits, incoming, [lv.count[:, None] for lv in new_levels])
+    routes, queries = _bridge(model, qr, logits, incoming, [lv.count[:, None] for lv in new_levels])
     weights = model.output_logits.softmax(0)
     out = 0
     for j, qo in enumerate(queries):
@@ -426,15 +440,29 @@ def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | Non
     return g_in, cfg.beta_max * b_in.sigmoid(), g_out, cfg.beta_max * b_out.sigmoid()
 
 
-def _base_logits(model, raw: Tensor, counts: Tensor, j: int) -> Tensor:
-    """read_scale*raw + softplus(c_j) log1p(n) (attention.py:196-204)."""
+def _base_logits(model, raw: Tensor, counts: Tensor, j: int, moment: Tensor | None = None) -> Tensor:
+    """read_scale*raw + softplus(c_j) log1p(n) [+ moment_gain_j tanh(moment / (1 + n))]
+    (attention.py:196-204)."""
     cfg = model.config
     gain = F.softplus(model.count_gain_raw[j])[..., None]
     if cfg.learn_read_scale:
         scale = model.read_log_scale[j].clamp(math.log(.25), math.log(64.)).exp()[..., None]
     else:
         scale = cfg.read_scale
-    return scale * raw.float() + gain * counts.log1p()
+    logits = scale * raw.float() + gain * counts.log1p()
+    if moment is not None:
+        logits = logits + model.moment_gain[j][..., None] * torch.tanh(moment / (1 + counts))
+    return logits
+
+
+def _moments(lv, key: Tensor, qr: Tensor, positions, old: LevelState) -> None:
+    """The level's positional moments (attention.py:318-323): the additive scan
+    of rope(u(key)) - u(key) against the write, read by u(rope(q)); sets
+    lv.correction and lv.moment (both None without moments)."""
+    if old.position is None:
+        return
+    kh = _unit(key)
+    lv.correction, lv.moment = additive_scan(_unit(qr), rope(kh, positions) - kh, lv.write, old.position)
 
 
 def _count_scalars(model, j: int, like: Tensor):
@@ -500,6 +528,11 @@ def _level_logits(model, lv, j: int, raw: Tensor, old: LevelState) -> None:
     """Counts after every token and the level's base logits (attention.py:
     319-323 and :165-175) into lv."""
     cfg = model.config
+    if lv.correction is not None:  # positional moments: the logits take the moment term
+        lv.counts = old.count[:, None] + _cumsum_tokens(lv.write.float())
+        lv.final_count = lv.counts[:, -1]
+        lv.logits = _base_logits(model, raw, lv.counts, j, lv.correction)
+        return
     if (_GLUE[0] and not torch.is_grad_enabled() and raw.shape[1] == 1 and raw.dtype in _lib.DTYPE_CODES
             and lv.write.dtype == raw.dtype and lv.write.shape[-1] <= _lib.TOKEN_LOGITS_MAX_SLOTS):
         gain, scale = _count_scalars(model, j, raw)

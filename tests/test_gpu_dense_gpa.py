@@ -64,6 +64,13 @@ CONFIGS = {
                        b=8, t=130),
     "c3_dims": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64),
                     b=1, t=130, normalize_k=True),
+    # positional moments (rotary query, additive moment state and its logit term)
+    "moments": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(5, 7, 5), chunk_size=4,
+                             positional_mode="moments"), b=2, t=11),
+    "moments_c3": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64,
+                                positional_mode="moments"), b=1, t=130, normalize_k=True),
+    "tokenwise_moments": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(5, 4), chunk_size=1,
+                                       positional_mode="moments"), b=2, t=6),
     # the tokenwise model (chunk_size 1)
     "tokenwise": dict(cfg=dict(heads=2, key_dim=16, value_dim=8, slots=(6, 4, 5), chunk_size=1), b=2, t=8),
     "tokenwise_lm": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1, control_dim=5,
@@ -95,7 +102,7 @@ def _run_both(name, dtype):
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
     if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "c2_dims_b8", "tiny_unequal_c3", "lm_flags",
-                                                "tokenwise"):
+                                                "tokenwise", "moments_c3"):
         pytest.skip("bf16 covered on the configuration-shaped cases")
     tol = TOL[dtype]
     (hm, xs, c_hip, out, state), (rm, rs, c_ref, ref_out, ref_state) = _run_both(name, dtype)
@@ -121,7 +128,7 @@ def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
 
 
 @pytest.mark.parametrize("name", ["tiny_unequal_c3", "tiny_none_c4", "lm_flags", "c2_dims", "c3_dims",
-                                  "tokenwise"])
+                                  "tokenwise", "moments", "tokenwise_moments"])
 def test_cached_partitions_and_decode_match_oracle(name):
     """Cached calls cut at block-unaligned points, then three one-token decode
     calls (the T = 1 inference path: one-token scan steps, the one-token level

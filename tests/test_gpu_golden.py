@@ -58,10 +58,6 @@ def test_hip_backend_reproduces_reference_fixture(name):
     model = model.float().to(DEV)
     xs = [x.to(DEV, dtype).requires_grad_() for x in (q, k, v)]
     c = ctrl.to(DEV, torch.float32).requires_grad_() if ctrl is not None else None
-    if case.cfg.get("positional_mode") == "moments":
-        with pytest.raises(ValueError, match="moments"):
-            model(*xs, control_input=c)
-        return
     out, state = model(*xs, control_input=c)
     errors = {"out": _rel(case, "out", out)}
     meta = list(case.z["state/meta"])
