@@ -131,9 +131,9 @@ __global__ __launch_bounds__(QNT) void level_token(gpa_level_problem p) {
 // workgroup (A^ and B^ as float4 pieces) are issued before the first sum, so
 // each stream costs one memory round trip.  Thread t holds the float4 column
 // group t % (M/4) of A^ rows t / (M/4) + i NT/(M/4) and the group t % (Dv/4) of
-// B^ rows t / (Dv/4) + i NT/(Dv/4) (i < 16).  Widths multiples of 4 with
-// (M/4) and (Dv/4) dividing NT, Dk M / 4 and M Dv / 4 at most 16 NT.
-constexpr int RQ = 16;  // float4 pieces of A^ (and of B^) per thread
+// B^ rows t / (Dv/4) + i NT/(Dv/4) (i < RQ).  Widths multiples of 4 with
+// (M/4) and (Dv/4) dividing NT, Dk M / 4 and M Dv / 4 at most RQ NT.
+constexpr int RQ = 8;  // float4 pieces of A^ (and of B^) per thread
 
 template <typename E, int NT>
 __global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
@@ -262,7 +262,8 @@ int reg_threads(const gpa_level_problem& p) {
   if (M % 4 || Dv % 4 || (reinterpret_cast<uintptr_t>(p.a_first) | reinterpret_cast<uintptr_t>(p.b_first)) % 16 ||
       p.a_first_sb % 4 || p.b_first_sb % 4)
     return 0;
-  for (int nt : {256, 512}) {
+  // (more threads with fewer pieces each: more waves in flight per compute unit)
+  for (int nt : {256, 512, 1024}) {
     if (nt % (M / 4) || nt % (Dv / 4)) continue;
     if ((int64_t)Dk * M / 4 <= (int64_t)RQ * nt && (int64_t)M * Dv / 4 <= (int64_t)RQ * nt) return nt;
   }
@@ -293,6 +294,10 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
     case 512:
       if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 512>), grid, dim3(512), 0, stream, p);
       else hipLaunchKernelGGL((level_token_reg<float, 512>), grid, dim3(512), 0, stream, p);
+      break;
+    case 1024:
+      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 1024>), grid, dim3(1024), 0, stream, p);
+      else hipLaunchKernelGGL((level_token_reg<float, 1024>), grid, dim3(1024), 0, stream, p);
       break;
     default:
       if (bf) hipLaunchKernelGGL(level_token<bf16_t>, grid, dim3(QNT), 0, stream, p);

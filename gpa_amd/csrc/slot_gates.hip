@@ -81,7 +81,9 @@ __global__ __launch_bounds__(SNT) void slot_fwd(gpa_slot_problem p) {
 
   const bf16_t* cen = reinterpret_cast<const bf16_t*>(p.center) + (int64_t)h * M * D;
   bf16_t* slot = reinterpret_cast<bf16_t*>(p.slot.ptr) + (int64_t)h * p.slot.sh;
-  for (int ct = ch; ct < M / 32; ct += 2) {
+  // blockIdx.z splits the slot column tiles between workgroups (calls with few
+  // rows, such as one-token decode); the gate inputs are done by z == 0.
+  for (int ct = ch + 2 * (int)blockIdx.z; ct < M / 32; ct += 2 * (int)gridDim.z) {
     const bf16_t* cp = cen + (int64_t)(32 * ct + li) * D + 8 * hh;
     bf16x8 bfr[KM / 16];
 #pragma unroll
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(SNT) void slot_fwd(gpa_slot_problem p) {
     }
   }
 
-  if (ch == 0) {
+  if (ch == 0 && blockIdx.z == 0) {
     float ss = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KM / 16; ++ks)
@@ -287,7 +289,10 @@ extern "C" int gpa_slot_gates_forward(const gpa_slot_problem* problem, hipStream
   using namespace gpa;
   if (int rc = check_slot(problem)) return rc;
   if (!problem->slot.ptr || !problem->raw.ptr) return fail(GPA_HIP_EINVAL, "slot: null output");
-  const dim3 grid((problem->batch * problem->tokens + SR - 1) / SR, problem->heads);
+  const int tiles = (problem->batch * problem->tokens + SR - 1) / SR;
+  // Few row tiles (one-token decode): one workgroup per 64 slot columns.
+  const int zsplit = tiles * problem->heads < 256 ? (problem->slots + 63) / 64 : 1;
+  const dim3 grid(tiles, problem->heads, zsplit);
   if (problem->key_dim <= 128)
     hipLaunchKernelGGL(slot_fwd<128>, grid, dim3(SNT), 0, stream, *problem);
   else

@@ -29,7 +29,7 @@ def _reference(key, center, gate_w):
 
 
 @pytest.mark.parametrize("b,t,h,d,m", [(1, 130, 2, 128, 128), (2, 64, 3, 64, 96), (1, 200, 1, 256, 256),
-                                       (3, 5, 2, 32, 32)])
+                                       (3, 5, 2, 32, 32), (64, 1, 16, 128, 256), (1, 2048, 16, 128, 128)])
 def test_slot_gates_match_typed_einsums(b, t, h, d, m):
     from gpa_amd.slots import slot_gates
     g = torch.Generator().manual_seed(b * 1000 + t + d)
