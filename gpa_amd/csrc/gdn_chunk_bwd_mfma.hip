@@ -125,9 +125,21 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
     tok_s[tid] = token_at(p, n, tid);
   }
   if (tid < 4) red_s[tid] = 0.f;
-  for (int i = tid; i < R * R / 4; i += NTH) {
-    const int t = i / (R / 4), c = 4 * (i % (R / 4));
-    *reinterpret_cast<f32x4*>(tm + t * LT + c) = *reinterpret_cast<const f32x4*>(tri + t * R + c);
+  {
+    // the triangular inverse: every load issued before the first store
+    constexpr int TQ = (R * R / 4 + NTH - 1) / NTH;
+    f32x4 tv[TQ];
+#pragma unroll
+    for (int j = 0; j < TQ; ++j) {
+      const int i = tid + NTH * j, ic = i < R * R / 4 ? i : 0;
+      tv[j] = *reinterpret_cast<const f32x4*>(tri + 4 * ic);
+    }
+#pragma unroll
+    for (int j = 0; j < TQ; ++j) {
+      const int i = tid + NTH * j;
+      if ((R * R / 4) % NTH != 0 && i >= R * R / 4) continue;
+      *reinterpret_cast<f32x4*>(tm + (i / (R / 4)) * LT + 4 * (i % (R / 4))) = tv[j];
+    }
   }
   // Row norms of the raw keys and queries, summed in the forward's order, and
   // x/|x| for every key column.  Every load of the wave is issued (at a clamped
@@ -622,13 +634,19 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
     }
   }
   __syncthreads();
-  if (tid < R) {
-    const int tok = tok_s[tid];
+  static_assert(R == 64, "one chunk row per lane of wave 0");
+  if (wave == 0) {
+    // dg_t = sum_{u >= t} dgam_u: a suffix sum across the wave's lanes
+    float acc = dgam_s[lane];
+#pragma unroll
+    for (int off = 1; off < R; off <<= 1) {
+      const float o = __shfl_down(acc, off, 64);
+      if (lane + off < R) acc += o;
+    }
+    const int tok = tok_s[lane];
     if (tok >= 0) {
-      float acc = 0.f;
-      for (int u = tid; u < R; ++u) acc += dgam_s[u];
       reinterpret_cast<float*>(gr.dg.ptr)[op_base(gr.dg, b, h) + (int64_t)tok * gr.dg.st] = acc;
-      reinterpret_cast<float*>(gr.dbeta.ptr)[op_base(gr.dbeta, b, h) + (int64_t)tok * gr.dbeta.st] = dbet_s[tid];
+      reinterpret_cast<float*>(gr.dbeta.ptr)[op_base(gr.dbeta, b, h) + (int64_t)tok * gr.dbeta.st] = dbet_s[lane];
     }
   }
 }
