@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 18
+ABI_VERSION = 19
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -144,6 +144,7 @@ class GateProblem(ctypes.Structure):
 
 
 TOKEN_LOGITS_MAX_SLOTS = 256
+TOKEN_LOGITS_MAX_PACK = 8
 
 
 class TokenLogitsProblem(ctypes.Structure):
@@ -192,6 +193,8 @@ EXPORTS = {
     "gpa_slot_gates_forward": ([ctypes.POINTER(SlotProblem), c_vp], ctypes.c_int),
     "gpa_slot_gates_backward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(SlotGrads), c_vp], ctypes.c_int),
     "gpa_gate_act_forward": ([ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
+    "gpa_slot_gates_act_forward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
+    "gpa_token_logits_many": ([ctypes.POINTER(TokenLogitsProblem), ctypes.c_int32, c_vp], ctypes.c_int),
     "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
 }

@@ -18,6 +18,7 @@
 // backward; both L2-resident per head).
 #include <hip/hip_runtime.h>
 
+#include "glue_rows.h"
 #include "mfma_tiles.h"
 
 namespace gpa {
@@ -54,8 +55,10 @@ __device__ __forceinline__ bf16x8 ld_bf8(const bf16_t* p) {
 // Forward.  Wave w: row tile w & 1; slot column tiles (w >> 1) + 2i.  Waves
 // 0-1 also do the gate inputs of their row tile: lane l holds row l % 32,
 // key columns 16 ks + 8 (l / 32) + 0..7 (its A fragments).
-template <int KM>
-__global__ __launch_bounds__(SNT) void slot_fwd(gpa_slot_problem p) {
+// ACT: the gate nonlinearities of each row follow in the same pass (inference,
+// gpa_slot_gates_act_forward), from the gate inputs as rounded.
+template <int KM, bool ACT>
+__global__ __launch_bounds__(SNT) void slot_fwd(gpa_slot_problem p, gpa_gate_problem gp) {
   __shared__ int64_t key_off[SR], slot_off[SR], raw_off[SR];
   __shared__ float wg[KM * 4];
   const int h = blockIdx.y, row0 = blockIdx.x * SR, D = p.key_dim, M = p.slots, R = p.batch * p.tokens;
@@ -127,6 +130,12 @@ __global__ __launch_bounds__(SNT) void slot_fwd(gpa_slot_problem p) {
       bf16_t* rp = reinterpret_cast<bf16_t*>(p.raw.ptr) + raw_off[lrow] + (int64_t)h * p.raw.sh;
 #pragma unroll
       for (int c = 0; c < 4; ++c) rp[c] = from_f32<bf16_t>(g[c]);
+      if (ACT) {
+        float rr[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rr[c] = round_as<bf16_t>(g[c]);
+        gate_row(gp, h, (int64_t)(row0 + lrow) * p.heads + h, rr);
+      }
     }
   }
 }
@@ -285,19 +294,49 @@ int check_slot(const gpa_slot_problem* p) {
 }  // namespace
 }  // namespace gpa
 
-extern "C" int gpa_slot_gates_forward(const gpa_slot_problem* problem, hipStream_t stream) {
-  using namespace gpa;
-  if (int rc = check_slot(problem)) return rc;
-  if (!problem->slot.ptr || !problem->raw.ptr) return fail(GPA_HIP_EINVAL, "slot: null output");
+namespace gpa {
+namespace {
+int launch_slot_fwd(const gpa_slot_problem* problem, const gpa_gate_problem* gates, hipStream_t stream) {
   const int tiles = (problem->batch * problem->tokens + SR - 1) / SR;
   // Few row tiles (one-token decode): one workgroup per 64 slot columns.
   const int zsplit = tiles * problem->heads < 256 ? (problem->slots + 63) / 64 : 1;
   const dim3 grid(tiles, problem->heads, zsplit);
-  if (problem->key_dim <= 128)
-    hipLaunchKernelGGL(slot_fwd<128>, grid, dim3(SNT), 0, stream, *problem);
-  else
-    hipLaunchKernelGGL(slot_fwd<256>, grid, dim3(SNT), 0, stream, *problem);
+  const gpa_gate_problem none{};
+  if (gates) {
+    if (problem->key_dim <= 128)
+      hipLaunchKernelGGL((slot_fwd<128, true>), grid, dim3(SNT), 0, stream, *problem, *gates);
+    else
+      hipLaunchKernelGGL((slot_fwd<256, true>), grid, dim3(SNT), 0, stream, *problem, *gates);
+  } else {
+    if (problem->key_dim <= 128)
+      hipLaunchKernelGGL((slot_fwd<128, false>), grid, dim3(SNT), 0, stream, *problem, none);
+    else
+      hipLaunchKernelGGL((slot_fwd<256, false>), grid, dim3(SNT), 0, stream, *problem, none);
+  }
+  return GPA_HIP_OK;
+}
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_slot_gates_forward(const gpa_slot_problem* problem, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_slot(problem)) return rc;
+  if (!problem->slot.ptr || !problem->raw.ptr) return fail(GPA_HIP_EINVAL, "slot: null output");
+  launch_slot_fwd(problem, nullptr, stream);
   return check_launch("gpa_slot_gates_forward");
+}
+
+extern "C" int gpa_slot_gates_act_forward(const gpa_slot_problem* problem, const gpa_gate_problem* gates,
+                                          hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_slot(problem)) return rc;
+  if (!problem->slot.ptr || !problem->raw.ptr) return fail(GPA_HIP_EINVAL, "slot: null output");
+  if (!gates || !gates->bias || !gates->g_in || !gates->b_in || !gates->g_out || !gates->b_out)
+    return fail(GPA_HIP_EINVAL, "slot: null gate output");
+  if (gates->batch != problem->batch || gates->tokens != problem->tokens || gates->heads != problem->heads)
+    return fail(GPA_HIP_EINVAL, "slot: the gate outputs must have the problem's batch, tokens and heads");
+  launch_slot_fwd(problem, gates, stream);
+  return check_launch("gpa_slot_gates_act_forward");
 }
 
 extern "C" int gpa_slot_gates_backward(const gpa_slot_problem* problem, const gpa_slot_grads* grads,

@@ -5,19 +5,10 @@
 // and its rounding to the activation type.
 #include <hip/hip_runtime.h>
 
-#include "gdn_common.h"
+#include "glue_rows.h"
 
 namespace gpa {
 namespace {
-
-template <typename E>
-__device__ __forceinline__ float act_at(const gpa_operand& o, int b, int t, int h, int d) {
-  return to_f32(reinterpret_cast<const E*>(o.ptr)[(int64_t)b * o.sb + (int64_t)t * o.st + (int64_t)h * o.sh + d]);
-}
-
-// F.softplus with its default threshold 20.
-__device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoid1(float x) { return 1.f / (1.f + expf(-x)); }
 
 // reference attention.py:161-174 after the gate-input product.
 template <typename E>
@@ -26,13 +17,10 @@ __global__ void gate_act(gpa_gate_problem p) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int h = i % p.heads, bt = i / p.heads, t = bt % p.tokens, b = bt / p.tokens;
-  float x[4];
+  float raw[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) x[c] = act_at<E>(p.raw, b, t, h, c) + p.bias[4 * h + c];
-  p.g_in[i] = __fmul_rn(-fminf(softplus20(x[0]), 10.f), p.decay_scale);
-  p.b_in[i] = __fmul_rn(p.beta_max, sigmoid1(x[1]));
-  p.g_out[i] = __fmul_rn(-fminf(softplus20(x[2]), 10.f), p.decay_scale);
-  p.b_out[i] = __fmul_rn(p.beta_max, sigmoid1(x[3]));
+  for (int c = 0; c < 4; ++c) raw[c] = act_at<E>(p.raw, b, t, h, c);
+  gate_row(p, h, i, raw);
 }
 
 // One token of one level: n = count0 + write; logits = scale raw + gain
@@ -41,40 +29,30 @@ template <typename E>
 __global__ __launch_bounds__(256) void token_logits(gpa_token_logits_problem p) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= p.batch * p.heads) return;
-  const int b = row / p.heads, h = row % p.heads, M = p.slots;
-  constexpr int PER = GPA_TOKEN_LOGITS_MAX_SLOTS / 64;
-  const float* c0 = p.count0 + (int64_t)b * p.count0_sb + (int64_t)h * M;
-  const float gain = p.gain[h], scale = p.scale[h];
-  float lg[PER], mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int m = lane + 64 * i;
-    if (m < M) {
-      const float n = c0[m] + act_at<E>(p.write, b, 0, h, m);
-      p.count[(int64_t)row * M + m] = n;
-      // separate roundings, as the reference's tensor ops (no contraction)
-      lg[i] = __fadd_rn(__fmul_rn(scale, act_at<E>(p.raw, b, 0, h, m)), __fmul_rn(gain, log1pf(n)));
-      p.logits[(int64_t)row * M + m] = lg[i];
-      mx = fmaxf(mx, lg[i]);
-    }
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int m = lane + 64 * i;
-    lg[i] = m < M ? expf(lg[i] - mx) : 0.f;
-    s += lg[i];
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-  E* local = reinterpret_cast<E*>(p.local);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int m = lane + 64 * i;
-    if (m < M) local[(int64_t)row * M + m] = from_f32<E>(lg[i] / s);
-  }
+  token_logits_row<E>(p, row / p.heads, row % p.heads, lane);
+}
+
+// Several levels' token logits in one launch: workgroups wg0[i] .. wg0[i+1]-1
+// take problem i (four rows each), read from the kernel arguments.
+struct LogitsPack {
+  int n;
+  int wg0[GPA_TOKEN_LOGITS_MAX_PACK];
+  gpa_token_logits_problem p[GPA_TOKEN_LOGITS_MAX_PACK];
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void token_logits_pack(LogitsPack pk) {
+  typedef const __attribute__((address_space(4))) LogitsPack* KernargPtr;
+  const KernargPtr kp = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  int pi = 0;
+#pragma unroll 1
+  for (int i = 1; i < kp->n; ++i)
+    if ((int)blockIdx.x >= kp->wg0[i]) pi = i;
+  gpa_token_logits_problem p;
+  kernarg_copy(p, &kp->p[pi]);
+  const int row = ((int)blockIdx.x - kp->wg0[pi]) * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= p.batch * p.heads) return;
+  token_logits_row<E>(p, row / p.heads, row % p.heads, lane);
 }
 
 // out = round(sum_j w[j,h] read_j), summed in level order (attention.py:340-341).
@@ -114,16 +92,26 @@ extern "C" int gpa_gate_act_forward(const gpa_gate_problem* p, hipStream_t strea
   return check_launch("gpa_gate_act_forward");
 }
 
-extern "C" int gpa_token_logits_forward(const gpa_token_logits_problem* p, hipStream_t stream) {
-  using namespace gpa;
+namespace gpa {
+namespace {
+int check_token_logits(const gpa_token_logits_problem* p) {
   if (!p || !p->raw.ptr || !p->write.ptr || !p->count0 || !p->gain || !p->scale || !p->logits || !p->count ||
       !p->local)
     return fail(GPA_HIP_EINVAL, "token logits: null pointer");
   if (p->batch < 1 || p->heads < 1) return fail(GPA_HIP_EINVAL, "token logits: empty shape");
+  if ((int64_t)p->batch * p->heads > 0x7fffffff) return fail(GPA_HIP_EUNSUPPORTED, "token logits: too many rows");
   if (p->slots < 1 || p->slots > GPA_TOKEN_LOGITS_MAX_SLOTS)
     return fail(GPA_HIP_EUNSUPPORTED, "token logits: slots must be in [1, 256]");
   if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16)
     return fail(GPA_HIP_EUNSUPPORTED, "token logits: dtype");
+  return GPA_HIP_OK;
+}
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_token_logits_forward(const gpa_token_logits_problem* p, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_token_logits(p)) return rc;
   const int rows = p->batch * p->heads;
   const dim3 grid((rows + 3) / 4), block(256);
   if (p->dtype == GPA_DTYPE_BF16)
@@ -131,6 +119,30 @@ extern "C" int gpa_token_logits_forward(const gpa_token_logits_problem* p, hipSt
   else
     hipLaunchKernelGGL(token_logits<float>, grid, block, 0, stream, *p);
   return check_launch("gpa_token_logits_forward");
+}
+
+extern "C" int gpa_token_logits_many(const gpa_token_logits_problem* problems, int32_t n, hipStream_t stream) {
+  using namespace gpa;
+  if (n < 0 || n > GPA_TOKEN_LOGITS_MAX_PACK) return fail(GPA_HIP_EINVAL, "token logits: 0 to 8 problems per call");
+  if (n == 0) return GPA_HIP_OK;
+  if (!problems) return fail(GPA_HIP_EINVAL, "token logits: null problems");
+  LogitsPack pk{};
+  int64_t wgs = 0;
+  for (int i = 0; i < n; ++i) {
+    const gpa_token_logits_problem& p = problems[i];
+    if (int rc = check_token_logits(&p)) return rc;
+    if (p.dtype != problems[0].dtype) return fail(GPA_HIP_EINVAL, "token logits: one dtype per call");
+    pk.p[i] = p;
+    pk.wg0[i] = (int)wgs;
+    wgs += ((int64_t)p.batch * p.heads + 3) / 4;
+  }
+  pk.n = n;
+  if (wgs > 0x7fffffff) return fail(GPA_HIP_EUNSUPPORTED, "token logits: too many rows");
+  if (problems[0].dtype == GPA_DTYPE_BF16)
+    hipLaunchKernelGGL(token_logits_pack<bf16_t>, dim3((unsigned)wgs), dim3(256), 0, stream, pk);
+  else
+    hipLaunchKernelGGL(token_logits_pack<float>, dim3((unsigned)wgs), dim3(256), 0, stream, pk);
+  return check_launch("gpa_token_logits_many");
 }
 
 extern "C" int gpa_output_mix_forward(const gpa_mix_problem* p, hipStream_t stream) {

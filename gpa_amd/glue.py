@@ -44,11 +44,46 @@ def token_logits(raw: Tensor, write: Tensor, count0: Tensor, gain: Tensor, scale
     return logits, count, local
 
 
-def output_mix(reads, weights: Tensor) -> Tensor:
-    """sum_j weights[j][h] reads[j], rounded to the reads' dtype."""
+def token_logits_many(calls) -> list[tuple[Tensor, Tensor, Tensor]]:
+    """`token_logits` of several levels in one launch (gpa_token_logits_many);
+    `calls` holds its (raw, write, count0, gain, scale) tuples, all of one
+    dtype.  Returns [(logits, counts, local)] in order, the bits of one call
+    per level."""
+    if not calls:
+        return []
+    if len(calls) > _lib.TOKEN_LOGITS_MAX_PACK:
+        raise ValueError(f"token_logits_many: at most {_lib.TOKEN_LOGITS_MAX_PACK} levels per call")
+    lib = _lib.load()
+    probs = (_lib.TokenLogitsProblem * len(calls))()
+    keep, outs = [], []
+    for i, (raw, write, count0, gain, scale) in enumerate(calls):
+        b, _, h, m = raw.shape
+        c0 = count0.float()
+        if c0.stride(2) != 1 or c0.stride(1) != m:
+            c0 = c0.contiguous()
+        gain, scale = gain.detach().float().contiguous(), scale.detach().float().contiguous()
+        logits = torch.empty(b, 1, h, m, device=raw.device, dtype=torch.float32)
+        count = torch.empty(b, h, m, device=raw.device, dtype=torch.float32)
+        local = torch.empty(b, 1, h, m, device=raw.device, dtype=raw.dtype)
+        probs[i] = _lib.TokenLogitsProblem(b, h, m, _lib.DTYPE_CODES[raw.dtype], _lib.operand(raw),
+                                           _lib.operand(write), c0.data_ptr(), c0.stride(0), gain.data_ptr(),
+                                           scale.data_ptr(), logits.data_ptr(), count.data_ptr(), local.data_ptr())
+        keep.append((c0, gain, scale))
+        outs.append((logits, count, local))
+    _lib.check(lib.gpa_token_logits_many(probs, len(calls), _lib.stream_handle(calls[0][0].device)),
+               "gpa_token_logits_many")
+    return outs
+
+
+def output_mix(reads, weights: Tensor, out: Tensor | None = None) -> Tensor:
+    """sum_j weights[j][h] reads[j], rounded to the reads' dtype; into `out`
+    (a [B,T,H,Dv] tensor of that dtype) when given."""
     lib = _lib.load()
     b, t, h, dv = reads[0].shape
-    out = torch.empty_like(reads[0])
+    if out is None:
+        out = torch.empty_like(reads[0])
+    elif out.shape != reads[0].shape or out.dtype != reads[0].dtype or out.device != reads[0].device:
+        raise ValueError("output_mix: out must match the reads' shape, dtype and device")
     w = weights.detach().float().contiguous()
     p = _lib.MixProblem()
     p.batch, p.tokens, p.heads, p.value_dim, p.levels = b, t, h, dv, len(reads)

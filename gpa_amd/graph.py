@@ -20,7 +20,7 @@ import gc
 
 import torch
 
-from . import params
+from . import params, schedule
 
 
 # Captures of steps over this many rows (batch x tokens) or more are refused:
@@ -143,8 +143,10 @@ class DecodeGraph:
             for o in range(self.chunk):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=self.pool):
-                    out, s = model(*self.inputs, s)
-                    self.outputs[o].copy_(out)
+                    with schedule.output_into(self.outputs[o]):
+                        out, s = model(*self.inputs, s)
+                    if out.data_ptr() != self.outputs[o].data_ptr():
+                        self.outputs[o].copy_(out)
                 del out
                 self.graphs.append(graph)
         self.last = s  # the cache after a whole block

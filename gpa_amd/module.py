@@ -156,9 +156,10 @@ class DenseGPA(nn.Module):
         if (len(state.levels) != cfg.levels
                 or tuple((r.source, r.target) for r in state.relations) != self.edges):
             raise ValueError("cache topology does not match this model")
-        if position_ids is None:
+        if position_ids is None and cfg.positional_mode == "moments":
+            # only the positional moments read positions (attention.py:305, :318-323)
             position_ids = torch.arange(state.position, state.position + q.shape[1], device=q.device)
-        if position_ids.shape not in ((q.shape[1],), (q.shape[0], q.shape[1])):
+        if position_ids is not None and position_ids.shape not in ((q.shape[1],), (q.shape[0], q.shape[1])):
             raise ValueError("position_ids must be [T] or [B,T]")
         from .decode import decode_step, decode_supported
         from .schedule import run_segment, run_tokens

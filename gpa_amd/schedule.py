@@ -34,7 +34,7 @@ from .ops import gdn_token_read
 from .ops import token_step_supported
 from .ops import read_supported as late_read_supported
 from .counts import count_logits
-from .slots import slot_gates
+from .slots import slot_gates, slot_gates_act
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
 from .level import level_mix, level_mix_block
@@ -48,6 +48,22 @@ _F32 = torch.float32
 _LANES = 4          # side streams for independent scans (the device has 4 hardware queues per process)
 _STREAMS: dict = {}
 _SERIAL = [False]   # set by `one_stream()`
+
+
+_OUT_BUFFER = [None]  # set by `output_into()`
+
+
+@contextlib.contextmanager
+def output_into(buffer: Tensor):
+    """Calls of the chunk model inside the block write their output into
+    `buffer` where the output-mix kernel produces it (one-token inference);
+    the caller compares data pointers to know whether it did."""
+    before = _OUT_BUFFER[0]
+    _OUT_BUFFER[0] = buffer
+    try:
+        yield
+    finally:
+        _OUT_BUFFER[0] = before
 
 
 @contextlib.contextmanager
@@ -152,6 +168,7 @@ class _Level:
                  "b_final", "a_starts", "b_starts", "b_read", "local", "b_token", "correction", "moment")
 
     def __init__(self):
+        self.logits = None
         self.local = None  # the local read distribution, when the counts kernel gave it
         # positional moments: the read of the moment state and the new state
         self.correction = self.moment = None
@@ -187,9 +204,15 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     # ---- level pass (storage + inner reads), attention.py:309-329
     key, value = k, v
     levels: list[_Level] = []
+    token_logits = []  # (level, j, inner read, old state) whose one-token logits come after the pass
     for j, (old, snap) in enumerate(zip(state.levels, frozen0)):
         lv = _Level()
-        if _FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]):
+        if (_FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]) and _GLUE[0]
+                and not torch.is_grad_enabled() and cfg.slot_feature == "linear"):
+            # inference: slot products, gate inputs and gate nonlinearities in one launch
+            slot, g_in, b_in, g_out, b_out = slot_gates_act(key, model.center[j], model.gate_weight[j],
+                                                            model.gate_bias[j], cfg.beta_max, _decay_scale(model, j))
+        elif _FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]):
             proj, raw = slot_gates(key, model.center[j], model.gate_weight[j])
             slot = _slot_feature(cfg, proj)
             g_in, b_in, g_out, b_out = _gates(model, key, j, control, raw)
@@ -208,8 +231,12 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
             lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
-            _moments(lv, key, qr, position_ids, old)
-            _level_logits(model, lv, j, raw, old)
+            if old.position is None and _token_logits_supported(raw, write):
+                # nothing in the level pass reads the logits: every level's in one launch after it
+                token_logits.append((lv, j, raw, old))
+            else:
+                _moments(lv, key, qr, position_ids, old)
+                _level_logits(model, lv, j, raw, old)
             levels.append(lv)
             key, value = key_next, value_next
             continue
@@ -249,6 +276,12 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         levels.append(lv)
         key, value = key_next, value_next
 
+    for part in _chunks(token_logits, _lib.TOKEN_LOGITS_MAX_PACK):
+        done = glue.token_logits_many([(raw, lv.write, old.count) + _count_scalars(model, j, raw)
+                                       for lv, j, raw, old in part])
+        for (lv, _, _, _), (lv.logits, lv.final_count, lv.local) in zip(part, done):
+            lv.counts = lv.final_count[:, None]
+
     # ---- relations, attention.py:206-223
     local = [lv.local if lv.local is not None else lv.logits.softmax(-1).to(dtype) for lv in levels]
     incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan, token)
@@ -287,7 +320,9 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                 lv.b_final.record_stream(torch.cuda.current_stream())
     if _GLUE[0] and not torch.is_grad_enabled() and all(r.dtype == v.dtype for r in reads) \
             and len(reads) <= _lib.DECODE_MAX_LEVELS:
-        out = glue.output_mix(reads, weights)
+        buf = _OUT_BUFFER[0]
+        out = glue.output_mix(reads, weights, buf if buf is not None and buf.shape == reads[0].shape
+                              and buf.dtype == reads[0].dtype else None)
     else:
         out = 0
         for j, read in enumerate(reads):
@@ -328,12 +363,13 @@ def run_tokens(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, control:
     _lib.require_device(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("backend='hip' computes in float32 or bfloat16 activations")
-    if position_ids is None:
+    if position_ids is None and cfg.positional_mode == "moments":
         position_ids = torch.arange(state.position, state.position + q.shape[1], device=q.device)
     outs, routes = [], []
     for t in range(q.shape[1]):
         ctl = control[:, t:t + 1] if control is not None else None
-        pos = position_ids[t] if position_ids.ndim == 1 else position_ids[:, t:t + 1]
+        pos = None if position_ids is None else (
+            position_ids[t] if position_ids.ndim == 1 else position_ids[:, t:t + 1])
         out, state, r = _token(model, q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], state, ctl, pos)
         outs.append(out)
         routes.append(r)
@@ -413,6 +449,23 @@ def _assignment(cfg, slot: Tensor):
     return (slot / .25).softmax(-1) if cfg.rsa_update else None
 
 
+def _tier(cfg, j: int) -> float:
+    """The rsa_update decay tier of level j (attention.py:170-171), else 1."""
+    return ((1., .1, .01, .001)[j] if cfg.levels == 4 else .1 ** j) if cfg.rsa_update else 1.
+
+
+def _decay_scale(model, j: int) -> float:
+    """The factor on both decays of level j: 0 without positions, else the tier."""
+    cfg = model.config
+    return 0. if cfg.positional_mode == "none" else _tier(cfg, j)
+
+
+def _token_logits_supported(raw: Tensor, write_like: Tensor) -> bool:
+    """One-token counts / logits / local read by a glue kernel (inference)."""
+    return (_GLUE[0] and not torch.is_grad_enabled() and raw.shape[1] == 1 and raw.dtype in _lib.DTYPE_CODES
+            and write_like.dtype == raw.dtype and raw.shape[-1] <= _lib.TOKEN_LOGITS_MAX_SLOTS)
+
+
 def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | None = None):
     """Scalar decay/strength gates per token and head (attention.py:161-174);
     `raw` is the gate input product when the caller has it already."""
@@ -425,10 +478,9 @@ def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | Non
     else:
         src = key if cfg.rsa_update else _unit(key)
         raw = _mm(src, w, "bthd,hdc->bthc", key.dtype)
-    tier = ((1., .1, .01, .001)[j] if cfg.levels == 4 else .1 ** j) if cfg.rsa_update else 1.
+    tier = _tier(cfg, j)
     if _GLUE[0] and not torch.is_grad_enabled() and raw.dtype in _lib.DTYPE_CODES:
-        return glue.gate_act(raw, model.gate_bias[j], cfg.beta_max,
-                             0. if cfg.positional_mode == "none" else tier)
+        return glue.gate_act(raw, model.gate_bias[j], cfg.beta_max, _decay_scale(model, j))
     raw = raw.float() + model.gate_bias[j]
     g_in, b_in, g_out, b_out = raw.unbind(-1)
     g_in = -F.softplus(g_in).clamp(max=10.)
@@ -533,8 +585,7 @@ def _level_logits(model, lv, j: int, raw: Tensor, old: LevelState) -> None:
         lv.final_count = lv.counts[:, -1]
         lv.logits = _base_logits(model, raw, lv.counts, j, lv.correction)
         return
-    if (_GLUE[0] and not torch.is_grad_enabled() and raw.shape[1] == 1 and raw.dtype in _lib.DTYPE_CODES
-            and lv.write.dtype == raw.dtype and lv.write.shape[-1] <= _lib.TOKEN_LOGITS_MAX_SLOTS):
+    if _token_logits_supported(raw, lv.write):
         gain, scale = _count_scalars(model, j, raw)
         lv.logits, lv.final_count, lv.local = glue.token_logits(raw, lv.write, old.count, gain, scale)
         lv.counts = lv.final_count[:, None]

@@ -87,3 +87,29 @@ def slot_gates(key: Tensor, center: Tensor, gate_w: Tensor) -> tuple[Tensor, Ten
     """(slot [B,T,H,M], raw gate inputs [B,T,H,4]) in key's dtype, from key
     [B,T,H,Dk], center [H,M,Dk] and gate_w [H,Dk,4]."""
     return _SlotGates.apply(key, center, gate_w)
+
+
+def slot_gates_act(key: Tensor, center: Tensor, gate_w: Tensor, bias: Tensor, beta_max: float,
+                   decay_scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """`slot_gates` followed by the gate nonlinearities (`glue.gate_act`) in
+    one launch, for inference (no autograd): (slot [B,T,H,M] in key's dtype,
+    g_in, b_in, g_out, b_out each float32 [B,T,H]), the bits of the two calls."""
+    _lib.require_device(key)
+    if torch.is_grad_enabled() and any(x.requires_grad for x in (key, center, gate_w, bias)):
+        raise RuntimeError("slot_gates_act has no backward: call it under torch.no_grad() or inference_mode()")
+    lib = _lib.load()
+    b, t, h, _ = key.shape
+    cb = params.derived(("slot_center", id(center), key.dtype), (center,),
+                        lambda: center.detach().to(key.dtype).contiguous())
+    wg = params.derived(("slot_gate_w", id(gate_w), key.dtype), (gate_w,),
+                        lambda: gate_w.detach().to(key.dtype).contiguous())
+    slot = key.new_empty(b, t, h, cb.shape[1])
+    raw = key.new_empty(b, t, h, 4)
+    prob = _problem(key, cb, None, wg, slot, raw)
+    outs = [torch.empty(b, t, h, device=key.device, dtype=torch.float32) for _ in range(4)]
+    bias = bias.detach().float().contiguous()
+    gates = _lib.GateProblem(b, t, h, _lib.DTYPE_CODES[key.dtype], _lib.operand(raw), bias.data_ptr(),
+                             float(beta_max), float(decay_scale), *(o.data_ptr() for o in outs))
+    _lib.check(lib.gpa_slot_gates_act_forward(prob, gates, _lib.stream_handle(key.device)),
+               "gpa_slot_gates_act_forward")
+    return (slot, *outs)

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 18
+#define GPA_HIP_ABI_VERSION 19
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -470,6 +470,15 @@ typedef struct gpa_gate_problem {
 } gpa_gate_problem;
 int gpa_gate_act_forward(const gpa_gate_problem *problem, hipStream_t stream);
 
+/* gpa_slot_gates_forward followed by gpa_gate_act_forward on its gate inputs,
+ * in one launch (inference): the slot products and gate inputs of one level
+ * (attention.py:176-177, :165) and the gate nonlinearities of _gates
+ * (attention.py:161-174).  `gates` gives the bias, beta_max, decay_scale and
+ * the four [B,T,H] outputs; its raw operand is not read (the gate inputs are
+ * problem->raw, still written).  Results are those of the two calls. */
+int gpa_slot_gates_act_forward(const gpa_slot_problem *problem, const gpa_gate_problem *gates,
+                               hipStream_t stream);
+
 /* One token (T = 1) of one level's slot counts, base logits and local read
  * distribution (attention.py:316-317, _base_logits :196-204, the softmax of
  * :330): n = count0 + write;  logits = scale raw + gain log1p(n);
@@ -486,6 +495,12 @@ typedef struct gpa_token_logits_problem {
     void *local;                                  /* out [B,1,H,M], contiguous */
 } gpa_token_logits_problem;
 int gpa_token_logits_forward(const gpa_token_logits_problem *problem, hipStream_t stream);
+
+/* gpa_token_logits_forward of up to GPA_TOKEN_LOGITS_MAX_PACK levels in one
+ * launch (every level of one decode step: their logits are read only after
+ * the level pass).  Results are those of one call per problem. */
+#define GPA_TOKEN_LOGITS_MAX_PACK 8
+int gpa_token_logits_many(const gpa_token_logits_problem *problems, int32_t n, hipStream_t stream);
 
 /* Output mix (attention.py:340-341): out = sum_j w[j][h] read_j, in level
  * order, rounded to the activation type. */

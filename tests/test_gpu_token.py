@@ -190,3 +190,46 @@ def test_level_token_kernel_matches_block_kernel(b, h, dk, dv, m, first, dtype, 
     for name, a, r in zip(("write", "key'", "value'"), outs[True], outs[False]):
         assert a.dtype == r.dtype == dtype and a.shape == r.shape, name
         assert _rel(a, r) < tol, (name, _rel(a, r))
+
+
+@pytest.mark.parametrize("b,h,dk,m", [(64, 16, 128, 128), (64, 16, 128, 256), (3, 2, 256, 128), (2, 3, 64, 96)])
+def test_slot_gates_act_matches_slot_gates_then_gate_act(b, h, dk, m):
+    """gpa_slot_gates_act_forward (slot products, gate inputs and gate
+    nonlinearities in one launch) gives the bits of gpa_slot_gates_forward
+    followed by gpa_gate_act_forward."""
+    from gpa_amd import glue
+    from gpa_amd.slots import slot_gates, slot_gates_act
+    g = torch.Generator().manual_seed(b + dk + m)
+    key = torch.randn(b, 1, h, dk, generator=g).bfloat16().to(DEV)
+    center = (torch.randn(h, m, dk, generator=g) * .1).to(DEV)
+    gate_w = (torch.randn(h, dk, 4, generator=g) * .3).to(DEV)
+    bias = torch.randn(h, 4, generator=g).to(DEV)
+    with torch.no_grad():
+        slot, raw = slot_gates(key, center, gate_w)
+        gates = glue.gate_act(raw, bias, .9, .5)
+        fused = slot_gates_act(key, center, gate_w, bias, .9, .5)
+    assert torch.equal(fused[0], slot)
+    for a, r in zip(fused[1:], gates):
+        assert a.dtype == torch.float32 and torch.equal(a, r)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_token_logits_many_matches_one_call_per_level(dtype):
+    """gpa_token_logits_many (the one-token logits of several levels in one
+    launch) gives the bits of one gpa_token_logits_forward per level: slot
+    widths 128, 256, 12 and 96, full and batch-broadcast counts."""
+    from gpa_amd import glue
+    g = torch.Generator().manual_seed(9)
+    calls = []
+    for b, h, m, bcast in [(64, 16, 128, False), (64, 16, 256, True), (3, 2, 12, False), (5, 3, 96, True)]:
+        raw = torch.randn(b, 1, h, m, generator=g).to(dtype).to(DEV)
+        write = torch.rand(b, 1, h, m, generator=g).to(dtype).to(DEV)
+        c0 = (torch.rand(1 if bcast else b, h, m, generator=g) * 5).to(DEV).expand(b, h, m)
+        gain, scale = (torch.rand(h, generator=g) + .5).to(DEV), (torch.rand(h, generator=g) * 4).to(DEV)
+        calls.append((raw, write, c0, gain, scale))
+    with torch.no_grad():
+        many = glue.token_logits_many(calls)
+        one = [glue.token_logits(*c) for c in calls]
+    for got, ref in zip(many, one):
+        for name, a, r in zip(("logits", "counts", "local"), got, ref):
+            assert a.dtype == r.dtype and a.shape == r.shape and torch.equal(a, r), name
