@@ -19,14 +19,16 @@ namespace gpa {
 
 constexpr int PREP_WAVES = 8, PREP_NT = 64 * PREP_WAVES;
 
-// LDS plan (floats): Kn rows; T; one region shared by A (until T is done), W
-// (fragment source) and the b-scaled V slices; per-row scalars.
+// LDS plan (floats): one region holds Kn rows, then W (the fragment source,
+// once the W product has read Kn), then the b-scaled V slices; T; A (until T
+// is done); per-row scalars.  Up to 128 keys this is under 80 KB, so two
+// workgroups share a compute unit.
 template <int KM>
 struct PrepLayout {
   static constexpr int LK = KM + 4, LT = R + 4, VC = 128, LV = VC + 4;
-  static constexpr int KN_OFF = 0, T_OFF = R * LK, X_OFF = T_OFF + R * LT;
-  static constexpr int XS = R * LK > R * LV ? R * LK : R * LV;  // >= R * LT as KM >= 64
-  static constexpr int BLK_OFF = X_OFF + XS;                     // 3 x 16 x 16 block products
+  static constexpr int BIG = R * LK > R * LV ? R * LK : R * LV;
+  static constexpr int KN_OFF = 0, T_OFF = BIG, A_OFF = T_OFF + R * LT;
+  static constexpr int BLK_OFF = A_OFF + R * LT;  // 3 x 16 x 16 block products
   static constexpr int SC_OFF = BLK_OFF + 3 * 256;
   static constexpr int TOTAL = SC_OFF + 4 * R;
   static constexpr size_t BYTES = sizeof(float) * TOTAL;
@@ -38,11 +40,11 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
   constexpr int LK = L::LK, LT = L::LT, VC = L::VC, LV = L::LV, NW = PREP_WAVES, NTH = PREP_NT;
   constexpr int KT = KM / 32, NTW = KT >= 4 ? KT / 4 : 1;
   extern __shared__ __align__(16) float smem[];
-  float* kn_s = smem + L::KN_OFF;  // [R][LK] Kn (rounded)
+  float* kn_s = smem + L::KN_OFF;  // [R][LK] Kn (rounded), then W [R][LK], then b V slices [R][LV]
+  float* w_s = kn_s;
+  float* v_s = kn_s;
   float* t_s = smem + L::T_OFF;    // [R][LT] T
-  float* a_s = smem + L::X_OFF;    // [R][LT] A, then W [R][LK], then b V slices [R][LV]
-  float* w_s = smem + L::X_OFF;
-  float* v_s = smem + L::X_OFF;
+  float* a_s = smem + L::A_OFF;    // [R][LT] A
   float* blk = smem + L::BLK_OFF;  // [3][16][16]
   float* gam_s = smem + L::SC_OFF;
   float* bet_s = gam_s + R;
@@ -218,10 +220,10 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
   const bool own = wave < 2 * KT;
   const int kt = own ? (NTW == 2 ? wave : wave % KT) : 0;
   auto tile_rt = [&](int m) { return NTW == 2 ? m : (own ? wave / KT : 0); };
-  if (own) {
-    f32x16 acc[NTW];
+  f32x16 acc[NTW];
 #pragma unroll
-    for (int m = 0; m < NTW; ++m) acc[m] = f32x16{};
+  for (int m = 0; m < NTW; ++m) acc[m] = f32x16{};
+  if (own) {
 #pragma unroll 4
     for (int g = 0; g < R / 8; ++g) {
       const int c0 = 8 * g + 4 * hh;
@@ -230,9 +232,12 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
 #pragma unroll
       for (int m = 0; m < NTW; ++m) mma8(acc[m], ld_c(t_s, LT, 32 * tile_rt(m) + li, c0) * sc, bk);
     }
+  }
+  if (MF) __syncthreads();  // every wave has read Kn before W takes its place
+  if (own) {
     const int k = 32 * kt + li;
     if (MF) {
-      // W rows to LDS for the fragment writers (A is no longer read).
+      // W rows to LDS for the fragment writers.
 #pragma unroll
       for (int m = 0; m < NTW; ++m)
 #pragma unroll
