@@ -185,12 +185,13 @@ __global__ __launch_bounds__(ONT, 2) void gdn_out_mfma(gpa_gdn_problem p, gpa_gd
 }
 
 // dd0 = P^T dO and o = diag(e^G) dO (value-major [V][R]) for one (chunk n,
-// stream s); V <= 256.
-template <int KM>
+// stream s); V <= VM <= 256 (VM = 128 leaves room for more workgroups per CU).
+template <int KM, int VM>
 __global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gdn_saved sv, gpa_gdn_grads gr,
                                                      int nch) {
+  static_assert(VM <= GPA_OUT_MFMA_MAX_V, "value width");
   __shared__ __align__(16) __bf16 ph[R * PLD], pl[R * PLD];  // P^T hi / lo, [u][t]
-  __shared__ __align__(16) __bf16 dot[GPA_OUT_MFMA_MAX_V * PLD];  // dO^T, [v][t] (exact)
+  __shared__ __align__(16) __bf16 dot[VM * PLD];  // dO^T, [v][t] (exact)
   __shared__ float gam_s[R];
   const int n = blockIdx.x, s = blockIdx.y, b = s / p.heads, h = s % p.heads;
   const int K = p.kdim, V = p.vdim, K16 = K / 16, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
@@ -270,7 +271,11 @@ int launch_out_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_opera
 template <int KM>
 int launch_dd0_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
                     hipStream_t st) {
-  hipLaunchKernelGGL((gdn_dd0_mfma<KM>), dim3(nch, p.batch * p.heads), dim3(ONT), 0, st, p, sv, gr, nch);
+  if (p.vdim <= 128)
+    hipLaunchKernelGGL((gdn_dd0_mfma<KM, 128>), dim3(nch, p.batch * p.heads), dim3(ONT), 0, st, p, sv, gr, nch);
+  else
+    hipLaunchKernelGGL((gdn_dd0_mfma<KM, GPA_OUT_MFMA_MAX_V>), dim3(nch, p.batch * p.heads), dim3(ONT), 0, st, p, sv,
+                       gr, nch);
   return GPA_HIP_OK;
 }
 
