@@ -219,7 +219,10 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
   // ---- value loop: register prefetch of slice sl+1 while slice sl is in LDS.
   // fetch() only issues loads (at a clamped, always valid address); the masks
   // of void or out-of-range entries are applied in stash(), after the MFMA
-  // work of the current slice, so the loads stay in flight meanwhile.
+  // work of the current slice, so the loads stay in flight meanwhile.  With
+  // 256 keys the prefetch registers would spill (their reloads cost more than
+  // the overlap gains): each slice is loaded just before its use.
+  constexpr bool PREFETCH = !XR;
   {
     const gpa_operand& dosrc = has_q ? gr.dout : p.v;  // stand-in of the same shape when there is no read
     f32x4 rs[SQ], rds[SQ], rd[DQ], rdd[DQ];
@@ -288,12 +291,20 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
       }
     };
 
-    fetch(0);
-    stash();
-    __syncthreads();
+    if (PREFETCH) {
+      fetch(0);
+      stash();
+      __syncthreads();
+    }
     for (int sl = 0; sl < nsl; ++sl) {
       const int v0 = sl * VS;
-      if (sl + 1 < nsl) fetch(v0 + VS);
+      if (!PREFETCH) {
+        fetch(v0);
+        stash();
+        __syncthreads();
+      } else if (sl + 1 < nsl) {
+        fetch(v0 + VS);
+      }
       // Y tile (16x16x4): rows 16 (w % 4) .. +15, slice values 16 (w / 4) .. +15.
       if (wave < 4 * (VS / 16)) {
         const int tq = lane & 15, q = lane >> 4, t0 = 16 * (wave & 3), j = wave >> 2;
@@ -368,7 +379,7 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
       }
       }
       __syncthreads();
-      if (sl + 1 < nsl) {
+      if (PREFETCH && sl + 1 < nsl) {
         stash();
         __syncthreads();
       }
