@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 19
+ABI_VERSION = 20
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -96,6 +96,20 @@ class RouteGrads(ctypes.Structure):
     _fields_ = [(n, Operand) for n in ("dqo", "droute", "dbase")] + \
                [("dmsg", Operand * ROUTE_MAX_INCOMING), ("dq", Operand)] + \
                [(n, c_vp) for n in ("dh1", "dhd", "dqs", "hg", "partials")]
+
+
+PRODUCT_ROWS = 4
+
+
+class ProductProblem(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("batch", "tokens", "heads", "slots", "incoming", "dtype", "marginal")] + \
+               [("base", Operand), ("msg", Operand * ROUTE_MAX_INCOMING), ("norm", Operand * ROUTE_MAX_INCOMING),
+                ("counts", Operand)] + [(n, c_vp) for n in ("edge_weight", "gexp", "out")]
+
+
+class ProductGrads(ctypes.Structure):
+    _fields_ = [("dout", c_vp), ("dmsg", Operand * ROUTE_MAX_INCOMING), ("dnorm", c_vp * ROUTE_MAX_INCOMING)] + \
+               [(n, c_vp) for n in ("dcounts", "partials")]
 
 
 LEVEL_MAX_WIDTH = 256
@@ -195,6 +209,8 @@ EXPORTS = {
     "gpa_gate_act_forward": ([ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
     "gpa_slot_gates_act_forward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
     "gpa_token_logits_many": ([ctypes.POINTER(TokenLogitsProblem), ctypes.c_int32, c_vp], ctypes.c_int),
+    "gpa_product_read_forward": ([ctypes.POINTER(ProductProblem), c_vp], ctypes.c_int),
+    "gpa_product_read_backward": ([ctypes.POINTER(ProductProblem), ctypes.POINTER(ProductGrads), c_vp], ctypes.c_int),
     "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
 }

@@ -8,8 +8,13 @@ legacy branch :236-240), for every token of every head of one target level j:
 
 `route_reader` returns (qo, r1) in the activation dtype and is differentiable
 in every input: the base logits, the messages, q, the edge weights, both gains
-and the four weight matrices.  It is used by the schedule for the default
-flags (`supported`); the other read variants keep the device glue.
+and the four weight matrices.  With `paper_product_read` (and
+`relation_marginal`) the relation read is the product form of
+attention.py:231-236 instead: `product_read` (gpa_product_read_forward /
+_backward) forms the base logits from the messages, and `route_reader` then
+runs with no incoming messages.  The schedule uses both where `supported`;
+the remaining flags (rsa_update, shared_query_center, balanced_bridge, slot
+features) keep the device glue.
 """
 from __future__ import annotations
 
@@ -20,7 +25,7 @@ from . import _lib, params
 
 
 def supported(cfg, dtype: torch.dtype, slots: int) -> bool:
-    return (dtype in _lib.DTYPE_CODES and not cfg.paper_product_read and not cfg.rsa_update
+    return (dtype in _lib.DTYPE_CODES and not cfg.rsa_update
             and not cfg.shared_query_center and not cfg.balanced_bridge and cfg.slot_feature == "linear"
             and slots <= _lib.ROUTE_MAX_WIDTH and cfg.key_dim <= _lib.ROUTE_MAX_WIDTH
             and cfg.levels - 1 <= _lib.ROUTE_MAX_INCOMING)
@@ -195,3 +200,89 @@ def route_reader(base: Tensor, q: Tensor, edge_w: Tensor | None, gain: Tensor, m
         # no incoming edges: the relation gain and edge weights are unused (no gradient)
         gain, edge_w = gain.detach(), gain.new_zeros(0, gain.shape[0])
     return _RouteReader.apply(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs)
+
+
+class _ProductRead(torch.autograd.Function):
+    """gpa_product_read_forward / _backward (see product_read)."""
+
+    @staticmethod
+    def forward(ctx, base, gexp, edge_w, counts, *pairs):
+        ni = len(pairs) // 2
+        msgs, norms = pairs[:ni], pairs[ni:]
+        _lib.require_device(base)
+        lib = _lib.load()
+        b, t, h, m = base.shape
+        gexp_f = gexp.detach().float().contiguous()
+        w = edge_w.detach().float().contiguous()
+        out = torch.empty(b, t, h, m, device=base.device, dtype=torch.float32)
+        p = _product_problem(base, gexp_f, w, counts, msgs, norms, out)
+        _lib.check(lib.gpa_product_read_forward(p, _lib.stream_handle(base.device)), "gpa_product_read_forward")
+        ctx.save_for_backward(base, gexp_f, w, counts if counts is not None else base.new_zeros(0), *msgs, *norms)
+        ctx.marginal = counts is not None
+        ctx.ni = ni
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        base, gexp, w, counts, *rest = ctx.saved_tensors
+        ni = ctx.ni
+        msgs, norms = rest[:ni], rest[ni:]
+        counts = counts if ctx.marginal else None
+        lib = _lib.load()
+        b, t, h, m = base.shape
+        dout = dout.float().contiguous()
+        dmsgs = [torch.empty_like(x) for x in msgs]
+        dnorms = [torch.empty(b, t, h, device=base.device, dtype=torch.float32) for _ in range(ni)]
+        dcounts = torch.empty(b, t, h, m, device=base.device, dtype=torch.float32) if ctx.marginal else None
+        nblk = -(-b * t // _lib.PRODUCT_ROWS)
+        partials = torch.empty(nblk, h, 2 + ni, device=base.device, dtype=torch.float32)
+        p = _product_problem(base, gexp, w, counts, msgs, norms, None)
+        g = _lib.ProductGrads()
+        g.dout = dout.data_ptr()
+        for e in range(ni):
+            g.dmsg[e], g.dnorm[e] = _lib.operand(dmsgs[e]), dnorms[e].data_ptr()
+        g.dcounts = dcounts.data_ptr() if dcounts is not None else None
+        g.partials = partials.data_ptr()
+        _lib.check(lib.gpa_product_read_backward(p, g, _lib.stream_handle(base.device)), "gpa_product_read_backward")
+        sums = partials.sum(0)  # [H, 2 + ni]
+        dgexp = m * sums[:, 0] - (sums[:, 1] if ctx.marginal else 0.)
+        dw = sums[:, 2:].transpose(0, 1)  # [ni, H]
+        dnorms = [x[..., None] if n.dim() == 4 else x for x, n in zip(dnorms, norms)]
+        return (dout, dgexp, dw, dcounts, *dmsgs, *dnorms)
+
+
+def _product_problem(base, gexp, w, counts, msgs, norms, out) -> _lib.ProductProblem:
+    b, t, h, m = base.shape
+    p = _lib.ProductProblem()
+    p.batch, p.tokens, p.heads, p.slots, p.incoming = b, t, h, m, len(msgs)
+    p.dtype, p.marginal = _lib.DTYPE_CODES[msgs[0].dtype], int(counts is not None)
+    p.base = _lib.operand(base)
+    for e, (msg, n) in enumerate(zip(msgs, norms)):
+        p.msg[e] = _lib.operand(msg)
+        p.norm[e] = _lib.Operand(n.data_ptr(), n.stride(0), n.stride(1), n.stride(2))
+    if counts is not None:
+        p.counts = _lib.operand(counts)
+    p.edge_weight, p.gexp = w.data_ptr(), gexp.data_ptr()
+    p.out = out.data_ptr() if out is not None else None
+    return p
+
+
+def product_read(base: Tensor, gexp: Tensor, edge_w: Tensor, msgs, norms, counts: Tensor | None) -> Tensor:
+    """The product relation read of one target level (attention.py:231-236):
+    base [B,T,H,M] float32 + (M gexp) sum_e (w_e msg_e) n_e, minus gexp
+    log1p(counts) when `counts` [B,T,H,M] float32 is given (relation_marginal);
+    gexp = e^{clamp(gain, -4, 4)} [H], edge_w [n_in,H] the edge softmax, msgs
+    [B,T,H,M] (one activation dtype) and norms [B,T,H] or [B,T,H,1] float32,
+    |softmax(source logits)| per row.  Returns float32 [B,T,H,M], with autograd
+    to every input."""
+    msgs = [x if x.stride(-1) == 1 else x.contiguous() for x in msgs]
+    if not 1 <= len(msgs) <= _lib.ROUTE_MAX_INCOMING or len(norms) != len(msgs):
+        raise ValueError("product_read: one norm per message, 1 to 3 messages")
+    if any(x.dtype != msgs[0].dtype for x in msgs) or msgs[0].dtype not in _lib.DTYPE_CODES:
+        raise ValueError("product_read: messages of one float32 or bfloat16 dtype")
+    if base.dtype != torch.float32 or base.stride(-1) != 1:
+        raise ValueError("product_read: float32 base logits with contiguous slots")
+    if counts is not None and (counts.dtype != torch.float32 or counts.stride(-1) != 1):
+        raise ValueError("product_read: float32 counts with contiguous slots")
+    norms = [n.float() for n in norms]
+    return _ProductRead.apply(base, gexp, edge_w, counts, *msgs, *norms)

@@ -40,6 +40,7 @@ from .counts import supported as fused_counts_supported
 from .level import level_mix, level_mix_block
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
+from .route import product_read
 from .route import supported as fused_route_supported
 from .positional import additive_scan, rope
 from .state import GPAState, LevelState, RelationState, ResidualSnapshot
@@ -666,6 +667,18 @@ def _incoming_index(model, j: int) -> Tensor:
                           lambda: (target == j).nonzero_static(size=model.config.levels - 1)[:, 0])
 
 
+def _product_base(model, j: int, logits, incoming, counts) -> Tensor:
+    """Level j's base logits after the product relation read (attention.py:
+    231-236) on the HIP kernel (route.product_read): the messages weighted by
+    the edge softmax and by |softmax(source logits)| per row, scaled by
+    M e^{clamp(gain)}, and the marginal term when relation_marginal."""
+    cfg = model.config
+    norms = [logits[model.edges[e][0]].softmax(-1).norm(dim=-1) for e, _ in incoming[j]]
+    gexp = model.relation_gain[j].clamp(-4, 4).exp()
+    return product_read(logits[j].float(), gexp, _incoming_weights(model, j), [msg for _, msg in incoming[j]],
+                        norms, counts[j].float() if cfg.relation_marginal else None)
+
+
 def _incoming_weights(model, j: int) -> Tensor:
     """Softmax of the logits of the edges into level j over those edges, [n_in,H]."""
     logits = model.edge_logits
@@ -681,21 +694,32 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
     cfg = model.config
     dtype = q.dtype
     routes, queries = [], []
+
+    def reader_args(j, base):
+        # the route reader's base logits and incoming messages: the product read
+        # folds the messages into the base logits first (product_read)
+        if not incoming[j]:
+            return base, None, []
+        if cfg.paper_product_read:
+            return _product_base(model, j, logits, incoming, counts), None, []
+        return base, _incoming_weights(model, j), [msg for _, msg in incoming[j]]
+
     if (_FUSED_ROUTE[0] and not torch.is_grad_enabled() and 1 < len(logits) <= _lib.ROUTE_MAX_PACK
             and all(fused_route_supported(cfg, dtype, base.shape[-1]) for base in logits)):
         # inference: every level's read in one launch where the library can pack them
-        reads = [(base, q, _incoming_weights(model, j) if incoming[j] else None, model.relation_gain[j],
-                  model.route_mlp_gain[j], model.route_up[j], model.route_down[j], model.route_weight[j],
-                  model.query_weight[j], cfg.query_scale, [msg for _, msg in incoming[j]])
-                 for j, base in enumerate(logits)]
+        reads = []
+        for j, base in enumerate(logits):
+            base_j, w, msgs = reader_args(j, base)
+            reads.append((base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j], model.route_up[j],
+                          model.route_down[j], model.route_weight[j], model.query_weight[j], cfg.query_scale, msgs))
         done = route_reader_many(reads)
         return [route for _, route in done], [qo for qo, _ in done]
     for j, base in enumerate(logits):
         if _FUSED_ROUTE[0] and fused_route_supported(cfg, dtype, base.shape[-1]):
-            w = _incoming_weights(model, j) if incoming[j] else None
-            qo, route = route_reader(base, q, w, model.relation_gain[j], model.route_mlp_gain[j],
+            base_j, w, msgs = reader_args(j, base)
+            qo, route = route_reader(base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j],
                                      model.route_up[j], model.route_down[j], model.route_weight[j],
-                                     model.query_weight[j], cfg.query_scale, [msg for _, msg in incoming[j]])
+                                     model.query_weight[j], cfg.query_scale, msgs)
             routes.append(route)
             queries.append(qo)
             continue

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 19
+#define GPA_HIP_ABI_VERSION 20
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -342,6 +342,42 @@ int gpa_route_backward(const gpa_route_problem *problem, const gpa_route_grads *
  * Reads the rows dh1, dhd, dqs and hg that gpa_route_backward wrote. */
 int gpa_route_weight_grads(const gpa_route_problem *problem, const gpa_route_grads *grads, float *d_up,
                            float *d_down, float *d_rs, float *d_qs, hipStream_t stream);
+
+/* The product relation read of one target level (reference attention.py:
+ * 231-236, paper_product_read, with the marginal term of relation_marginal),
+ * the part of _bridge before the route softmax; gpa_route_forward then runs
+ * on `out` with no incoming messages:
+ *   inc  = sum_e (w_e msg_e) n_e        in edge order, n_e = |softmax(source logits)| per row
+ *   out  = base + (M gexp) inc  [- gexp log1p(counts)]
+ * gexp = e^{clamp(gain, -4, 4)} per head; each product and sum rounded
+ * separately, in the reference's order. */
+#define GPA_PRODUCT_ROWS 4        /* rows (b, t) of one head per workgroup */
+typedef struct gpa_product_problem {
+    int32_t batch, tokens, heads, slots, incoming, dtype, marginal;
+    gpa_operand base;                             /* float32 [B,T,H,M] */
+    gpa_operand msg[GPA_ROUTE_MAX_INCOMING];      /* [B,T,H,M], activation dtype */
+    gpa_operand norm[GPA_ROUTE_MAX_INCOMING];     /* float32 [B,T,H] (the last stride is unused) */
+    gpa_operand counts;                           /* float32 [B,T,H,M] (marginal only) */
+    const float *edge_weight;                     /* [incoming][H] */
+    const float *gexp;                            /* [H] */
+    float *out;                                   /* float32 [B,T,H,M], contiguous */
+} gpa_product_problem;
+
+typedef struct gpa_product_grads {
+    const float *dout;                            /* float32 [B,T,H,M], contiguous: gradient of out */
+    gpa_operand dmsg[GPA_ROUTE_MAX_INCOMING];     /* out [B,T,H,M], activation dtype */
+    float *dnorm[GPA_ROUTE_MAX_INCOMING];         /* out [B,T,H], contiguous */
+    float *dcounts;                               /* out [B,T,H,M], contiguous (marginal only) */
+    float *partials;                              /* out [ceil(B*T/GPA_PRODUCT_ROWS)][H][2 + incoming]:
+                                                     sum dout inc, sum dout log1p(counts), sum d(w_e msg_e) msg_e
+                                                     over the workgroup's rows */
+} gpa_product_grads;
+
+int gpa_product_read_forward(const gpa_product_problem *problem, hipStream_t stream);
+/* d base = dout (not written); d gexp = M * sum(dout inc) - sum(dout log1p(counts)) and
+ * d w_e = sum(d(w_e msg_e) msg_e) after summing the partials over their first axis. */
+int gpa_product_read_backward(const gpa_product_problem *problem, const gpa_product_grads *grads,
+                              hipStream_t stream);
 
 /* ---------------------------------------------------------------- level mix
  * The block-lagged write and residual of one level (reference _block_segment,

@@ -76,6 +76,9 @@ def test_ctypes_structs_match_c_layout():
     # 6 int32, key operand, 3 pointers, 2 operands; 3 operands, 2 pointers
     assert ctypes.sizeof(_lib.SlotProblem) == 24 + 32 + 3 * 8 + 2 * 32
     assert ctypes.sizeof(_lib.SlotGrads) == 3 * 32 + 2 * 8
+    # 7 int32 (+pad), base, 3 messages, 3 norms, counts, 3 pointers; pointer, 3 operands, 5 pointers
+    assert ctypes.sizeof(_lib.ProductProblem) == 32 + 32 + 3 * 32 + 3 * 32 + 32 + 3 * 8
+    assert ctypes.sizeof(_lib.ProductGrads) == 8 + 3 * 32 + 3 * 8 + 2 * 8
 
 
 def test_backend_refuses_cpu_tensors():

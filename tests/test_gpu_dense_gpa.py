@@ -71,6 +71,16 @@ CONFIGS = {
                                 positional_mode="moments"), b=1, t=130, normalize_k=True),
     "tokenwise_moments": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(5, 4), chunk_size=1,
                                        positional_mode="moments"), b=2, t=6),
+    # the product relation read with and without the marginal term (HIP product_read + route reader)
+    "product": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8, 16), chunk_size=4,
+                             paper_product_read=True), b=2, t=9),
+    "product_marginal": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 16, 8), chunk_size=3,
+                                      paper_product_read=True, relation_marginal=True, read_scale=8.), b=2, t=10),
+    "product_marginal_c3": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256),
+                                         chunk_size=64, paper_product_read=True, relation_marginal=True),
+                                b=1, t=130, normalize_k=True),
+    "tokenwise_product": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1,
+                                       paper_product_read=True, relation_marginal=True), b=2, t=5),
     # the tokenwise model (chunk_size 1)
     "tokenwise": dict(cfg=dict(heads=2, key_dim=16, value_dim=8, slots=(6, 4, 5), chunk_size=1), b=2, t=8),
     "tokenwise_lm": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1, control_dim=5,
@@ -102,7 +112,7 @@ def _run_both(name, dtype):
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
     if dtype == torch.bfloat16 and name not in ("c3_dims", "c2_dims", "c2_dims_b8", "tiny_unequal_c3", "lm_flags",
-                                                "tokenwise", "moments_c3"):
+                                                "tokenwise", "moments_c3", "product_marginal_c3"):
         pytest.skip("bf16 covered on the configuration-shaped cases")
     tol = TOL[dtype]
     (hm, xs, c_hip, out, state), (rm, rs, c_ref, ref_out, ref_state) = _run_both(name, dtype)

@@ -130,3 +130,55 @@ def test_tiled_route_backward_matches_one_kernel_path(b, t, h, m, dk, n_in, with
             assert torch.isfinite(x).all()
         else:
             assert torch.equal(x, y), f"{name}: max |diff| {(x.float() - y.float()).abs().max().item()}"
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / max(b.norm().item(), 1e-30)).item()
+
+
+def _product_ref(base, gexp, w, msgs, norms, counts):
+    """The product relation read as the reference's tensor ops (attention.py:
+    231-236), with the messages promoted from their dtype as there."""
+    total = 0
+    for e, (msg, n) in enumerate(zip(msgs, norms)):
+        total = total + w[e][..., None] * msg * n[..., None]
+    out = base + base.shape[-1] * gexp[..., None] * total
+    if counts is not None:
+        out = out - gexp[..., None] * counts.log1p()
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF], ids=["f32", "bf16"])
+@pytest.mark.parametrize("b,t,h,m,n_in,marginal", [(2, 9, 3, 128, 3, True), (1, 130, 2, 256, 2, False),
+                                                   (3, 5, 2, 12, 1, True), (64, 1, 16, 128, 3, True)])
+def test_product_read_matches_reference_ops_with_gradients(b, t, h, m, n_in, marginal, dtype):
+    """gpa_product_read_forward / _backward against the reference's tensor ops
+    (float32 autograd on the CPU): output to 1e-6, and the gradients of the
+    base, gain factor, edge weights, messages, norms and counts (1e-5 in
+    float32; messages rounded to bfloat16 at 2e-2)."""
+    g = torch.Generator().manual_seed(b * 31 + m + n_in)
+    base = torch.randn(b, t, h, m, generator=g)
+    gexp = torch.rand(h, generator=g) + .5
+    w = torch.softmax(torch.randn(n_in, h, generator=g), 0)
+    msgs = [torch.randn(b, t, h, m, generator=g).to(dtype) for _ in range(n_in)]
+    norms = [torch.rand(b, t, h, generator=g) + .1 for _ in range(n_in)]
+    counts = torch.rand(b, t, h, m, generator=g) * 9 if marginal else None
+    dout = torch.randn(b, t, h, m, generator=g)
+    ins = [base, gexp, w] + msgs + norms + ([counts] if marginal else [])
+    ref_in = [x.clone().requires_grad_() for x in ins]
+    hip_in = [x.to(DEV).requires_grad_() for x in ins]
+
+    def split(xs):
+        return xs[0], xs[1], xs[2], xs[3:3 + n_in], xs[3 + n_in:3 + 2 * n_in], (xs[-1] if marginal else None)
+
+    ref = _product_ref(*split(ref_in))
+    ref.backward(dout)
+    got = rt.product_read(*split(hip_in))
+    got.backward(dout.to(DEV))
+    assert got.dtype == torch.float32 and got.shape == ref.shape
+    assert _rel(got, ref) < 1e-6
+    for i, (a, r) in enumerate(zip(hip_in, ref_in)):
+        tol = 2e-2 if a.dtype == BF else 1e-5
+        assert a.grad is not None and a.grad.dtype == r.grad.dtype, i
+        assert _rel(a.grad, r.grad) < tol, (i, _rel(a.grad, r.grad))
