@@ -13,8 +13,9 @@ and the four weight matrices.  With `paper_product_read` (and
 attention.py:231-236 instead: `product_read` (gpa_product_read_forward /
 _backward) forms the base logits from the messages, and `route_reader` then
 runs with no incoming messages.  The schedule uses both where `supported`;
-the remaining flags (rsa_update, shared_query_center, balanced_bridge, slot
-features) keep the device glue.
+with shared_query_center the query weight is W_qs + center^T / query_scale
+(attention.py:254-256), formed by the caller; the remaining flags
+(rsa_update, balanced_bridge, slot features) keep the device glue.
 """
 from __future__ import annotations
 
@@ -26,7 +27,7 @@ from . import _lib, params
 
 def supported(cfg, dtype: torch.dtype, slots: int) -> bool:
     return (dtype in _lib.DTYPE_CODES and not cfg.rsa_update
-            and not cfg.shared_query_center and not cfg.balanced_bridge and cfg.slot_feature == "linear"
+            and not cfg.balanced_bridge and cfg.slot_feature == "linear"
             and slots <= _lib.ROUTE_MAX_WIDTH and cfg.key_dim <= _lib.ROUTE_MAX_WIDTH
             and cfg.levels - 1 <= _lib.ROUTE_MAX_INCOMING)
 
@@ -39,7 +40,10 @@ def _pack(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
     """[H,K,N] weight -> [H,N32,K16] rows of the contraction for each output
     column (transpose=True), or [H,K,N] -> [H,K32,N16] (transpose=False:
     output column = K, contraction = N); rounded to `dtype`, zero padded.
-    Cached while the weight is unchanged (params.derived)."""
+    Cached while the weight is unchanged (params.derived) when it is a leaf
+    tensor (a parameter); a weight computed in the call is packed afresh."""
+    if not w.is_leaf:
+        return _pack_now(w, dtype, transpose)
     return params.derived(("route_pack", id(w), dtype, transpose), (w,), lambda: _pack_now(w, dtype, transpose))
 
 

@@ -695,6 +695,15 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
     dtype = q.dtype
     routes, queries = [], []
 
+    def query_weight(j):
+        # shared_query_center: W_qs + center^T / query_scale (attention.py:254-256)
+        qw = model.query_weight[j]
+        if not cfg.shared_query_center:
+            return qw
+        c = model.center[j]
+        return params.derived(("query_center", id(qw), id(c), float(cfg.query_scale)), (qw, c),
+                              lambda: qw + c.transpose(-1, -2) / cfg.query_scale, differentiable=True)
+
     def reader_args(j, base):
         # the route reader's base logits and incoming messages: the product read
         # folds the messages into the base logits first (product_read)
@@ -711,7 +720,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
         for j, base in enumerate(logits):
             base_j, w, msgs = reader_args(j, base)
             reads.append((base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j], model.route_up[j],
-                          model.route_down[j], model.route_weight[j], model.query_weight[j], cfg.query_scale, msgs))
+                          model.route_down[j], model.route_weight[j], query_weight(j), cfg.query_scale, msgs))
         done = route_reader_many(reads)
         return [route for _, route in done], [qo for qo, _ in done]
     for j, base in enumerate(logits):
@@ -719,7 +728,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
             base_j, w, msgs = reader_args(j, base)
             qo, route = route_reader(base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j],
                                      model.route_up[j], model.route_down[j], model.route_weight[j],
-                                     model.query_weight[j], cfg.query_scale, msgs)
+                                     query_weight(j), cfg.query_scale, msgs)
             routes.append(route)
             queries.append(qo)
             continue

@@ -79,6 +79,9 @@ CONFIGS = {
     "product_marginal_c3": dict(cfg=dict(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256),
                                          chunk_size=64, paper_product_read=True, relation_marginal=True),
                                 b=1, t=130, normalize_k=True),
+    "product_center": dict(cfg=dict(heads=2, key_dim=16, value_dim=8, slots=(16, 8, 8), chunk_size=4,
+                                    paper_product_read=True, relation_marginal=True, shared_query_center=True,
+                                    read_scale=8.), b=2, t=9),
     "tokenwise_product": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1,
                                        paper_product_read=True, relation_marginal=True), b=2, t=5),
     # the tokenwise model (chunk_size 1)
