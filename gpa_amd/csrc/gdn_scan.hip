@@ -1020,6 +1020,66 @@ bool on_mfma256(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && 
 // Forward of n problems: every prep, the state recurrences (the problems on
 // the strip kernels of one key-width class in one packed launch, at the
 // position of the first of them), every read.
+// The 256-key state packs of a call that also has strip packs run on a second
+// stream of the device: the two classes are independent, and each alone
+// leaves compute units idle (one strip workgroup per CU; 32-96 workgroups of
+// the 256-key kernel).  The side stream and its fork/join events are created
+// on first use per device and kept for the process (default priority).  The
+// enqueue sequence fork -> side launches -> join record -> main launches ->
+// main waits runs under one mutex, so concurrent calls never interleave their
+// event records.  Timed calls and calls under graph capture stay on one stream.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kSideDevices = 64;
+std::mutex g_side_mutex;
+SideStream g_side[kSideDevices];
+
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+}
+
+// Locks g_side_mutex into `lock`, creates the side stream of st's device if
+// needed, and makes it wait for everything st has enqueued so far.
+int side_fork(hipStream_t st, SideStream*& out, std::unique_lock<std::mutex>& lock) {
+  hipDevice_t dev = 0;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess) return fail(GPA_HIP_EHIP, "gdn: hipStreamGetDevice failed");
+  if (dev < 0 || dev >= kSideDevices) return fail(GPA_HIP_EUNSUPPORTED, "gdn: device index above 63");
+  lock = std::unique_lock<std::mutex>(g_side_mutex);
+  SideStream& sd = g_side[dev];
+  if (!sd.s) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(GPA_HIP_EHIP, "gdn: hipGetDevice failed");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return fail(GPA_HIP_EHIP, "gdn: hipSetDevice failed");
+    SideStream made;
+    hipError_t e = hipStreamCreateWithFlags(&made.s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&made.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&made.join, hipEventDisableTiming);
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return fail(GPA_HIP_EHIP, "gdn: creating the side stream failed");
+    sd = made;
+  }
+  if (hipEventRecord(sd.fork, st) != hipSuccess || hipStreamWaitEvent(sd.s, sd.fork, 0) != hipSuccess)
+    return fail(GPA_HIP_EHIP, "gdn: side stream fork failed");
+  out = &sd;
+  return GPA_HIP_OK;
+}
+
+int side_join(hipStream_t st, const SideStream& sd) {
+  if (hipEventRecord(sd.join, sd.s) != hipSuccess || hipStreamWaitEvent(st, sd.join, 0) != hipSuccess)
+    return fail(GPA_HIP_EHIP, "gdn: side stream join failed");
+  return GPA_HIP_OK;
+}
+
+// Whether the state phase of the call overlaps its 256-key packs with the rest.
+bool overlap_state(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStream_t st) {
+  bool mf = false, other = false;
+  for (int i = 0; i < n; ++i) (on_mfma256(ps[i]) ? mf : other) = true;
+  return mf && other && !tm && !capturing(st);
+}
+
 int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_operand* outs, int n,
                         gpa_timing* tm, hipStream_t st) {
   const gpa_gdn_grads none{};
@@ -1027,6 +1087,11 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
     mark(tm, st);
     if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, st)) return rc;
   }
+  SideStream* side = nullptr;
+  std::unique_lock<std::mutex> side_lock;
+  if (overlap_state(ps, n, tm, st))
+    if (int rc = side_fork(st, side, side_lock)) return rc;
+  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key packs
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
     if (done[i]) continue;
@@ -1046,7 +1111,7 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
         fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
         done[j] = true;
       }
-      if (int rc = launch_state_fwd_mfma_pack<256>(pk, total, fast, st)) return rc;
+      if (int rc = launch_state_fwd_mfma_pack<256>(pk, total, fast, sst)) return rc;
       continue;
     }
     if (!on_strips(ps[i])) {
@@ -1069,6 +1134,8 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
                             : launch_state_fwd_strip<128>(pk, total, fast, st);
     if (rc) return rc;
   }
+  if (side)
+    if (int rc = side_join(st, *side)) return rc;
   for (int i = 0; i < n; ++i) {
     if (!ps[i].q.ptr || !outs[i].ptr) continue;
     mark(tm, st);
@@ -1090,6 +1157,11 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
     mark(tm, st);
     if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], st)) return rc;
   }
+  SideStream* side = nullptr;
+  std::unique_lock<std::mutex> side_lock;
+  if (overlap_state(ps, n, tm, st))
+    if (int rc = side_fork(st, side, side_lock)) return rc;
+  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key packs
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
     if (done[i]) continue;
@@ -1112,7 +1184,7 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
         fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
         done[j] = true;
       }
-      if (int rc = launch_state_bwd_mfma_pack<256>(pk, total, fast, hq, hi, st)) return rc;
+      if (int rc = launch_state_bwd_mfma_pack<256>(pk, total, fast, hq, hi, sst)) return rc;
       continue;
     }
     if (!on_strips(ps[i])) {
@@ -1137,6 +1209,8 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
                             : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, st);
     if (rc) return rc;
   }
+  if (side)
+    if (int rc = side_join(st, *side)) return rc;
   for (int i = 0; i < n; ++i) {
     mark(tm, st);
     if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], st)) return rc;
