@@ -1023,7 +1023,8 @@ bool on_mfma256(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && 
 // The 256-key state packs of a call that also has strip packs run on a second
 // stream of the device: the two classes are independent, and each alone
 // leaves compute units idle (one strip workgroup per CU; 32-96 workgroups of
-// the 256-key kernel).  The side stream and its fork/join events are created
+// the 256-key kernel); the out or chunk-backward phase of each group follows
+// its state pack on the same stream.  The side stream and its fork/join events are created
 // on first use per device and kept for the process (default priority).  The
 // enqueue sequence fork -> side launches -> join record -> main launches ->
 // main waits runs under one mutex, so concurrent calls never interleave their
@@ -1134,13 +1135,14 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
                             : launch_state_fwd_strip<128>(pk, total, fast, st);
     if (rc) return rc;
   }
-  if (side)
-    if (int rc = side_join(st, *side)) return rc;
+  // the out phase of each group follows its state pack on the same stream
   for (int i = 0; i < n; ++i) {
     if (!ps[i].q.ptr || !outs[i].ptr) continue;
     mark(tm, st);
-    if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, st)) return rc;
+    if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, on_mfma256(ps[i]) ? sst : st)) return rc;
   }
+  if (side)
+    if (int rc = side_join(st, *side)) return rc;
   mark(tm, st);
   return check_launch("gdn_forward");
 }
@@ -1209,12 +1211,13 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
                             : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, st);
     if (rc) return rc;
   }
-  if (side)
-    if (int rc = side_join(st, *side)) return rc;
+  // the chunk phase of each group follows its state pack on the same stream
   for (int i = 0; i < n; ++i) {
     mark(tm, st);
-    if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], st)) return rc;
+    if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], on_mfma256(ps[i]) ? sst : st)) return rc;
   }
+  if (side)
+    if (int rc = side_join(st, *side)) return rc;
   mark(tm, st);
   return check_launch("gdn_backward");
 }
