@@ -1023,8 +1023,8 @@ bool on_mfma256(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && 
 // The 256-key state packs of a call that also has strip packs run on a second
 // stream of the device: the two classes are independent, and each alone
 // leaves compute units idle (one strip workgroup per CU; 32-96 workgroups of
-// the 256-key kernel); the out or chunk-backward phase of each group follows
-// its state pack on the same stream.  The side stream and its fork/join events are created
+// the 256-key kernel); each group's phases (prep or dd0, state, out or chunk
+// backward) run in order on its stream.  The side stream and its fork/join events are created
 // on first use per device and kept for the process (default priority).  The
 // enqueue sequence fork -> side launches -> join record -> main launches ->
 // main waits runs under one mutex, so concurrent calls never interleave their
@@ -1084,15 +1084,15 @@ bool overlap_state(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipSt
 int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_operand* outs, int n,
                         gpa_timing* tm, hipStream_t st) {
   const gpa_gdn_grads none{};
-  for (int i = 0; i < n; ++i) {
-    mark(tm, st);
-    if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, st)) return rc;
-  }
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
   if (overlap_state(ps, n, tm, st))
     if (int rc = side_fork(st, side, side_lock)) return rc;
-  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key packs
+  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key groups
+  for (int i = 0; i < n; ++i) {
+    mark(tm, st);
+    if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, on_mfma256(ps[i]) ? sst : st)) return rc;
+  }
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
     if (done[i]) continue;
@@ -1154,16 +1154,16 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
   const gpa_operand none{};
   gpa_gdn_grads gr[GPA_GDN_MAX_PACK];
   for (int i = 0; i < n; ++i) gr[i] = effective_grads(ps[i], grs[i]);
-  for (int i = 0; i < n; ++i) {
-    if (!has_read(ps[i], gr[i])) continue;
-    mark(tm, st);
-    if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], st)) return rc;
-  }
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
   if (overlap_state(ps, n, tm, st))
     if (int rc = side_fork(st, side, side_lock)) return rc;
-  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key packs
+  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key groups
+  for (int i = 0; i < n; ++i) {
+    if (!has_read(ps[i], gr[i])) continue;
+    mark(tm, st);
+    if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], on_mfma256(ps[i]) ? sst : st)) return rc;
+  }
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
     if (done[i]) continue;
