@@ -1020,15 +1020,16 @@ bool on_mfma256(const gpa_gdn_problem& p) { return p.dtype == GPA_DTYPE_BF16 && 
 // Forward of n problems: every prep, the state recurrences (the problems on
 // the strip kernels of one key-width class in one packed launch, at the
 // position of the first of them), every read.
-// The 256-key state packs of a call that also has strip packs run on a second
-// stream of the device: the two classes are independent, and each alone
-// leaves compute units idle (one strip workgroup per CU; 32-96 workgroups of
-// the 256-key kernel); each group's phases (prep or dd0, state, out or chunk
-// backward) run in order on its stream.  The side stream and its fork/join events are created
-// on first use per device and kept for the process (default priority).  The
-// enqueue sequence fork -> side launches -> join record -> main launches ->
-// main waits runs under one mutex, so concurrent calls never interleave their
-// event records.  Timed calls and calls under graph capture stay on one stream.
+// Part of the groups of a packed call run on a second stream of the device
+// (which groups: side_groups).  The state chains leave compute units idle
+// (one strip workgroup per CU; 32-96 workgroups of the 256-key kernel), so
+// the other stream's kernels fill them.  Each group's phases (prep or dd0,
+// state, out or chunk backward) run in order on its stream, between a fork
+// event at the start of the call and a join at its end.  The side stream and
+// its events are created on first use per device and kept for the process
+// (default priority).  The enqueue sequence fork -> launches -> join runs
+// under one mutex, so concurrent calls never interleave their event records.
+// Timed calls and calls under graph capture stay on one stream.
 struct SideStream {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
@@ -1074,11 +1075,28 @@ int side_join(hipStream_t st, const SideStream& sd) {
   return GPA_HIP_OK;
 }
 
-// Whether the state phase of the call overlaps its 256-key packs with the rest.
-bool overlap_state(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStream_t st) {
-  bool mf = false, other = false;
-  for (int i = 0; i < n; ++i) (on_mfma256(ps[i]) ? mf : other) = true;
-  return mf && other && !tm && !capturing(st);
+// Which groups of the call run on the side stream: the 256-key groups when
+// the call also has others; else, for a call of strip groups only (a level's
+// A/B pair), the second half of the groups, each half in its own strip pack,
+// so that one half's prep or out phase overlaps the other half's state chain.
+// Returns whether any group goes there (never for timed or captured calls).
+bool side_groups(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStream_t st, bool (&side)[GPA_GDN_MAX_PACK]) {
+  bool mf = false, other = false, strips = true;
+  for (int i = 0; i < n; ++i) {
+    (on_mfma256(ps[i]) ? mf : other) = true;
+    strips = strips && on_strips(ps[i]);
+    side[i] = false;
+  }
+  if (tm || capturing(st)) return false;
+  if (mf && other) {
+    for (int i = 0; i < n; ++i) side[i] = on_mfma256(ps[i]);
+    return true;
+  }
+  if (strips && n >= 2) {
+    for (int i = n / 2; i < n; ++i) side[i] = true;
+    return true;
+  }
+  return false;
 }
 
 int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_operand* outs, int n,
@@ -1086,12 +1104,13 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
   const gpa_gdn_grads none{};
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
-  if (overlap_state(ps, n, tm, st))
+  bool on_side[GPA_GDN_MAX_PACK];
+  if (side_groups(ps, n, tm, st, on_side))
     if (int rc = side_fork(st, side, side_lock)) return rc;
-  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key groups
+  auto stream_of = [&](int i) { return side && on_side[i] ? side->s : st; };
   for (int i = 0; i < n; ++i) {
     mark(tm, st);
-    if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, on_mfma256(ps[i]) ? sst : st)) return rc;
+    if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, stream_of(i))) return rc;
   }
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
@@ -1102,7 +1121,7 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
       int total = 0;
       bool fast = true;
       for (int j = i; j < n && pk.n < GPA_MFMA_MAXP; ++j) {
-        if (done[j] || !on_mfma256(ps[j])) continue;
+        if (done[j] || !on_mfma256(ps[j]) || on_side[j] != on_side[i]) continue;
         pk.p[pk.n] = ps[j];
         pk.sv[pk.n] = svs[j];
         pk.nch[pk.n] = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
@@ -1112,11 +1131,11 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
         fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
         done[j] = true;
       }
-      if (int rc = launch_state_fwd_mfma_pack<256>(pk, total, fast, sst)) return rc;
+      if (int rc = launch_state_fwd_mfma_pack<256>(pk, total, fast, stream_of(i))) return rc;
       continue;
     }
     if (!on_strips(ps[i])) {
-      if (int rc = phase(Phase::state, ps[i], svs[i], outs[i], none, st)) return rc;
+      if (int rc = phase(Phase::state, ps[i], svs[i], outs[i], none, stream_of(i))) return rc;
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
@@ -1124,22 +1143,22 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
     int total = 0;
     bool fast = true;
     for (int j = i; j < n; ++j) {
-      if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km) continue;
+      if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || on_side[j] != on_side[i]) continue;
       const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
       pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total);
       total += strip_workgroups(ps[j]);
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
       done[j] = true;
     }
-    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, st)
-                            : launch_state_fwd_strip<128>(pk, total, fast, st);
+    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, stream_of(i))
+                            : launch_state_fwd_strip<128>(pk, total, fast, stream_of(i));
     if (rc) return rc;
   }
   // the out phase of each group follows its state pack on the same stream
   for (int i = 0; i < n; ++i) {
     if (!ps[i].q.ptr || !outs[i].ptr) continue;
     mark(tm, st);
-    if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, on_mfma256(ps[i]) ? sst : st)) return rc;
+    if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, stream_of(i))) return rc;
   }
   if (side)
     if (int rc = side_join(st, *side)) return rc;
@@ -1156,13 +1175,14 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
   for (int i = 0; i < n; ++i) gr[i] = effective_grads(ps[i], grs[i]);
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
-  if (overlap_state(ps, n, tm, st))
+  bool on_side[GPA_GDN_MAX_PACK];
+  if (side_groups(ps, n, tm, st, on_side))
     if (int rc = side_fork(st, side, side_lock)) return rc;
-  const hipStream_t sst = side ? side->s : st;  // stream of the 256-key groups
+  auto stream_of = [&](int i) { return side && on_side[i] ? side->s : st; };
   for (int i = 0; i < n; ++i) {
     if (!has_read(ps[i], gr[i])) continue;
     mark(tm, st);
-    if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], on_mfma256(ps[i]) ? sst : st)) return rc;
+    if (int rc = phase(Phase::dd0, ps[i], svs[i], none, gr[i], stream_of(i))) return rc;
   }
   bool done[GPA_GDN_MAX_PACK] = {};
   for (int i = 0; i < n; ++i) {
@@ -1174,7 +1194,8 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
       int total = 0;
       bool fast = true;
       for (int j = i; j < n && pk.n < GPA_MFMA_MAXP; ++j) {
-        if (done[j] || !on_mfma256(ps[j]) || has_read(ps[j], gr[j]) != hq || (gr[j].dstates != nullptr) != hi)
+        if (done[j] || !on_mfma256(ps[j]) || has_read(ps[j], gr[j]) != hq || (gr[j].dstates != nullptr) != hi ||
+            on_side[j] != on_side[i])
           continue;
         pk.p[pk.n] = ps[j];
         pk.sv[pk.n] = svs[j];
@@ -1186,11 +1207,11 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
         fast = fast && ps[j].kdim == 256 && ps[j].vdim % 64 == 0;
         done[j] = true;
       }
-      if (int rc = launch_state_bwd_mfma_pack<256>(pk, total, fast, hq, hi, sst)) return rc;
+      if (int rc = launch_state_bwd_mfma_pack<256>(pk, total, fast, hq, hi, stream_of(i))) return rc;
       continue;
     }
     if (!on_strips(ps[i])) {
-      if (int rc = phase(Phase::state_bwd, ps[i], svs[i], none, gr[i], st)) return rc;
+      if (int rc = phase(Phase::state_bwd, ps[i], svs[i], none, gr[i], stream_of(i))) return rc;
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
@@ -1199,7 +1220,7 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
     bool fast = true;
     for (int j = i; j < n; ++j) {
       if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || has_read(ps[j], gr[j]) != hq ||
-          (gr[j].dstates != nullptr) != hi)
+          (gr[j].dstates != nullptr) != hi || on_side[j] != on_side[i])
         continue;
       const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
       pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq);
@@ -1207,14 +1228,14 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
       done[j] = true;
     }
-    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, st)
-                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, st);
+    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, stream_of(i))
+                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, stream_of(i));
     if (rc) return rc;
   }
   // the chunk phase of each group follows its state pack on the same stream
   for (int i = 0; i < n; ++i) {
     mark(tm, st);
-    if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], on_mfma256(ps[i]) ? sst : st)) return rc;
+    if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], stream_of(i))) return rc;
   }
   if (side)
     if (int rc = side_join(st, *side)) return rc;
