@@ -141,7 +141,8 @@ def test_dense_gpa_forward_backward_matches_oracle(name, dtype):
 
 
 @pytest.mark.parametrize("name", ["tiny_unequal_c3", "tiny_none_c4", "lm_flags", "c2_dims", "c3_dims",
-                                  "tokenwise", "moments", "tokenwise_moments"])
+                                  "tokenwise", "moments", "tokenwise_moments", "product_marginal",
+                                  "product_center"])
 def test_cached_partitions_and_decode_match_oracle(name):
     """Cached calls cut at block-unaligned points, then three one-token decode
     calls (the T = 1 inference path: one-token scan steps, the one-token level
