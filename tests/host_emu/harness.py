@@ -24,8 +24,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 CLANG = "/opt/rocm/llvm/bin/clang++"
 ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3,
-           "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6}
-SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip"]
+           "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6, "gpa_gdn_token_step": 7,
+           "gpa_gdn_token_step_many": 8, "gpa_level_token_forward": 9}
+SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip"]
 
 
 def compiler() -> str | None:
@@ -47,9 +48,10 @@ def build(out_dir: str, sources=None) -> str:
 
 def _pointer_fields(ctype, base=0):
     out = []
-    if issubclass(ctype, ctypes.Array):  # an array of structs passed as one blob
+    if issubclass(ctype, ctypes.Array):  # an array of structs or pointers passed as one blob
         for i in range(ctype._length_):
-            out += _pointer_fields(ctype._type_, base + i * ctypes.sizeof(ctype._type_))
+            off = base + i * ctypes.sizeof(ctype._type_)
+            out += [off] if ctype._type_ is ctypes.c_void_p else _pointer_fields(ctype._type_, off)
         return out
     for name, t in ctype._fields_:
         off = base + getattr(ctype, name).offset
@@ -144,6 +146,16 @@ class HostLib:
 
     def gpa_level_backward(self, prob, grads, stream):
         return self._call("gpa_level_backward", [prob, grads])
+
+    def gpa_gdn_token_step(self, prob, final, out, stream):
+        return self._call("gpa_gdn_token_step", [prob, out], [final])
+
+    def gpa_gdn_token_step_many(self, probs, finals, outs, n, stream):
+        assert n == len(probs) == len(finals) == len(outs)
+        return self._call("gpa_gdn_token_step_many", [probs, finals, outs])
+
+    def gpa_level_token_forward(self, prob, stream):
+        return self._call("gpa_level_token_forward", [prob])
 
     def gpa_hip_last_error(self):
         return b""

@@ -142,6 +142,17 @@ inline uint32_t __float_as_uint(float f) {
   return u;
 }
 
+// Inline assembly: the kernels' only statement is `asm volatile("s_waitcnt
+// lgkmcnt(0)\n\ts_barrier" ::: "memory")` (the LDS-only barrier).  Here
+// `asm` vanishes and `volatile(...)` becomes a call that sees the statement's
+// text: a barrier over the workgroup when it holds s_barrier, else nothing (a
+// wait for outstanding memory operations is implicit on the host).
+inline void emu_asm(const char* text) {
+  if (strstr(text, "s_barrier")) __syncthreads();
+}
+#define asm
+#define volatile(...) emu_asm(#__VA_ARGS__)
+
 // The kernel-argument segment: the address of the running kernel's first
 // argument (each emulated thread holds its own copy of the arguments).
 extern thread_local const void* emu_kernarg;

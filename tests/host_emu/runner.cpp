@@ -93,6 +93,19 @@ int main(int argc, char** argv) {
       rc = gpa_route_forward_many(reinterpret_cast<gpa_route_problem*>(blobs.at(0).data()),
                                   (int32_t)(blobs.at(0).size() / sizeof(gpa_route_problem)), nullptr);
       break;
+    case 7:
+      rc = gpa_gdn_token_step(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()), static_cast<float*>(raw.at(0)),
+                              *reinterpret_cast<gpa_operand*>(blobs.at(1).data()), nullptr);
+      break;
+    case 8:
+      rc = gpa_gdn_token_step_many(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                                   reinterpret_cast<float* const*>(blobs.at(1).data()),
+                                   reinterpret_cast<gpa_operand*>(blobs.at(2).data()),
+                                   (int32_t)(blobs.at(0).size() / sizeof(gpa_gdn_problem)), nullptr);
+      break;
+    case 9:
+      rc = gpa_level_token_forward(reinterpret_cast<gpa_level_problem*>(blobs.at(0).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

@@ -123,7 +123,8 @@ def test_host_built_level_mix_block_matches_level_mix(first, runner, tmp_path, m
     fb = (torch.randn(*lead, h, m, dv, generator=g) * .3).expand(b, h, m, dv)
     eta = 1 + .25 * torch.randn(h, 2, generator=g).tanh()
     harness.use_host(monkeypatch, harness.HostLib(runner, str(tmp_path)))
-    monkeypatch.setattr(level, "_TOKEN_KERNEL", [False])  # the block kernel (the host build has no token kernel)
+    # the block kernel; the one-token kernel is compared with it in test_token_emulated.py
+    monkeypatch.setattr(level, "_TOKEN_KERNEL", [False])
     with torch.no_grad():
         ref = level.level_mix(key, value, a_vm, b_vm, fa, fb, eta, c, off)
         got = level.level_mix_block(key, value, fa, fb, eta, c, off)
