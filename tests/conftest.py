@@ -20,3 +20,13 @@ def _few_cpu_threads():
     torch.set_num_threads(min(4, old))
     yield
     torch.set_num_threads(old)
+
+
+@pytest.fixture(scope="session")
+def host_runner(tmp_path_factory):
+    """The AddressSanitizer host build of the kernels (tests/host_emu/), built
+    once per session and shared by the emulated-kernel tests."""
+    from tests.host_emu import harness
+    if harness.compiler() is None:
+        pytest.skip("no host clang")
+    return harness.build(str(tmp_path_factory.mktemp("host_emu")))

@@ -39,11 +39,9 @@ CASES = {
 }
 
 
-@pytest.fixture(scope="module")
-def runner(tmp_path_factory):
-    if harness.compiler() is None:
-        pytest.skip("no host clang")
-    return harness.build(str(tmp_path_factory.mktemp("host_emu")))
+@pytest.fixture
+def runner(host_runner):
+    return host_runner
 
 
 def _rel(a, b):

@@ -22,11 +22,9 @@ from oracle import reference as ref
 from tests.host_emu import harness
 
 
-@pytest.fixture(scope="module")
-def runner(tmp_path_factory):
-    if harness.compiler() is None:
-        pytest.skip("no host clang")
-    return harness.build(str(tmp_path_factory.mktemp("host_emu_token")))
+@pytest.fixture
+def runner(host_runner):
+    return host_runner
 
 
 @pytest.fixture
