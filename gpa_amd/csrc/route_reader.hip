@@ -436,7 +436,10 @@ __device__ __forceinline__ void rows_bwd_vec(const gpa_route_problem& p, const g
 }
 
 // The forward of RR rows (row0 ..) of head h of one problem.
-template <typename E, bool VEC>
+// NW waves: the row phases and the q staging run on the first RNT threads,
+// the product tiles are spread over all NW waves (the packed one-token read
+// uses 8, so that the 32 rows of a wide level walk half as many tiles per wave).
+template <typename E, bool VEC, int NW = RW>
 __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h, int row0) {
   using W = typename Wt<E>::type;
   HIP_DYNAMIC_SHARED(float, lds)
@@ -453,7 +456,9 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
   E* shd = reinterpret_cast<E*>(p.hd) + (int64_t)h * R * M;
 
   // ---- r0 = softmax(base + gain tanh z)
-  if constexpr (VEC) {
+  if (NW > RW && tid >= RNT) {
+    // the row phase runs on the first RNT threads
+  } else if constexpr (VEC) {
     rows_r0_vec<E>(p, rows, row0, h, sr0, A, lda, kM);
   } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
@@ -476,7 +481,7 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
   // ---- h1 = r0 U, gelu(h1) -> Hs
   {
     const W* ut = reinterpret_cast<const W*>(p.up_t) + (int64_t)h * pad32(2 * M) * kM;
-    for (int t = wave; t < pad32(2 * M) / 32; t += RW) {
+    for (int t = wave; t < pad32(2 * M) / 32; t += NW) {
       f32x16 acc = {};
       tile_gemm(acc, A, lda, ut, kM, kM, 32 * t, lane);
 #pragma unroll
@@ -499,7 +504,7 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
     const W* dt = reinterpret_cast<const W*>(p.down_t) + (int64_t)h * pad32(M) * k2M;
     const float g = p.mlp_gain[h];
     E* route = reinterpret_cast<E*>(p.route.ptr);
-    for (int t = wave; t < pad32(M) / 32; t += RW) {
+    for (int t = wave; t < pad32(M) / 32; t += NW) {
       f32x16 acc = {};
       tile_gemm(acc, Hs, ldh, dt, k2M, k2M, 32 * t, lane);
 #pragma unroll
@@ -520,7 +525,9 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
   __syncthreads();
 
   // ---- q -> Hs
-  if constexpr (VEC) {
+  if (NW > RW && tid >= RNT) {
+    // the q staging runs on the first RNT threads
+  } else if constexpr (VEC) {
     const int c = 8 * (tid & 31), rsub = tid >> 5;
     uint4 qv[VPASS];
 #pragma unroll
@@ -557,7 +564,7 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
     const W* rt = reinterpret_cast<const W*>(p.rs_t) + (int64_t)h * pad32(M) * kM;
     const W* qt = reinterpret_cast<const W*>(p.qs_t) + (int64_t)h * pad32(M) * kD;
     E* qo = reinterpret_cast<E*>(p.qo.ptr);
-    for (int t = wave; t < pad32(M) / 32; t += RW) {
+    for (int t = wave; t < pad32(M) / 32; t += NW) {
       f32x16 a3 = {}, a4 = {};
       tile_gemm(a3, A, lda, rt, kM, kM, 32 * t, lane);
       tile_gemm(a4, Hs, ldh, qt, kD, kD, 32 * t, lane);
@@ -605,13 +612,14 @@ __device__ __forceinline__ int route_pack_entry(RoutePackPtr kp, gpa_route_probl
   return pi;
 }
 
-// bf16 with 16-byte rows (the one-token decode path).
-__global__ __launch_bounds__(RNT) void route_fwd_pack(RoutePack pk) {
+// bf16 with 16-byte rows (the one-token decode path), 8 waves per workgroup.
+constexpr int RPACK_W = 8;
+__global__ __launch_bounds__(64 * RPACK_W) void route_fwd_pack(RoutePack pk) {
   const RoutePackPtr kp = (RoutePackPtr)__builtin_amdgcn_kernarg_segment_ptr();
   gpa_route_problem p;
   const int pi = route_pack_entry(kp, p);
   const int local = (int)blockIdx.x - kp->wg0[pi], nt = kp->tiles[pi];
-  route_fwd_run<bf16_t, true>(p, local / nt, (local % nt) * RR);
+  route_fwd_run<bf16_t, true, RPACK_W>(p, local / nt, (local % nt) * RR);
 }
 
 // ---------------------------------------------------------------- tiled products
@@ -1816,7 +1824,7 @@ extern "C" int gpa_route_forward_many(const gpa_route_problem* problems, int32_t
     lds = std::max(lds, fwd_lds(p));
   }
   if (int rc = set_lds(route_fwd_pack, lds)) return rc;
-  hipLaunchKernelGGL(route_fwd_pack, dim3(total), dim3(RNT), lds, stream, pk);
+  hipLaunchKernelGGL(route_fwd_pack, dim3(total), dim3(64 * RPACK_W), lds, stream, pk);
   return check_launch("gpa_route_forward_many");
 }
 
