@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 20
+ABI_VERSION = 21
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -186,6 +186,8 @@ EXPORTS = {
     "gpa_gdn_read_backward": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), Operand, Operand, c_vp],
                               ctypes.c_int),
     "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
+    "gpa_token_level_forward": ([ctypes.POINTER(Problem), c_vp, Operand, ctypes.POINTER(LevelProblem), c_vp],
+                                ctypes.c_int),
     "gpa_gdn_forward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Operand), c_i32,
                               ctypes.POINTER(Timing), c_vp], ctypes.c_int),
     "gpa_gdn_backward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads), c_i32,

@@ -7,159 +7,15 @@
 // (thread t: columns 4 (t % 16) .. +3 of rows t / 16 + 16 i), so the
 // prediction u(k)^T (a S), the update and the read u(q)^T S' all come from the
 // one load.
-#include "gdn_common.h"
+#include "token_step.h"
 
 namespace gpa {
 namespace {
 
-constexpr int SNT = 256;   // threads per workgroup: 16 column quads x 16 row groups
-constexpr int SCOL = 64;   // state columns per workgroup
-
-// Sum of the four row groups that share a wave's column quad (lanes c, c+16,
-// c+32, c+48), then of the four waves through LDS; every thread returns the
-// total of its quad.
-__device__ __forceinline__ float4 column_sums(float4 x, float4 (*part)[16], int wave, int rg, int c4) {
-  x.x += __shfl_xor(x.x, 16, 64);
-  x.y += __shfl_xor(x.y, 16, 64);
-  x.z += __shfl_xor(x.z, 16, 64);
-  x.w += __shfl_xor(x.w, 16, 64);
-  x.x += __shfl_xor(x.x, 32, 64);
-  x.y += __shfl_xor(x.y, 32, 64);
-  x.z += __shfl_xor(x.z, 32, 64);
-  x.w += __shfl_xor(x.w, 32, 64);
-  if ((rg & 3) == 0) part[wave][c4] = x;
-  lds_barrier();
-  float4 s = part[0][c4];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    const float4 y = part[w][c4];
-    s.x += y.x;
-    s.y += y.y;
-    s.z += y.z;
-    s.w += y.w;
-  }
-  return s;
-}
-
-// Workgroup wg of one problem; NI rows per thread: K <= 16 NI.
-template <typename E, int NI>
-__device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, const gpa_operand& out, int wg) {
-  __shared__ float kh[16 * NI], qh[16 * NI];
-  __shared__ float norms[2][4];
-  __shared__ float4 part[2][4][16];
-  const int ncb = (p.vdim + SCOL - 1) / SCOL;
-  const int s = wg / ncb, cb = wg - s * ncb;
-  const int b = s / p.heads, h = s - b * p.heads;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int c4 = t & 15, rg = t >> 4;
-  const int K = p.kdim, V = p.vdim;
-  const int col = SCOL * cb + 4 * c4;
-  const bool cok = col < V;  // V % 4 == 0: a quad is all inside or all outside
-  const int cc = cok ? col : 0;
-  const bool update = p.k.ptr != nullptr, has_q = p.q.ptr != nullptr;
-
-  // Every load first, at clamped addresses; masks afterwards.
-  const float* s0 = p.s0 ? p.s0 + (int64_t)b * p.s0_sb + (int64_t)h * p.s0_sh : nullptr;
-  float4 st[NI];
-  if (s0) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = rg + 16 * i;
-      st[i] = *reinterpret_cast<const float4*>(s0 + (int64_t)(row < K ? row : 0) * V + cc);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  const int tk = t < K ? t : 0;
-  float xk = 0.f, xq = 0.f, vv[4] = {0.f, 0.f, 0.f, 0.f}, g = 0.f, beta = 0.f;
-  if (update) {
-    xk = op_load<E>(p.k, b, h, 0, tk);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = op_load<E>(p.v, b, h, 0, cc + j);
-    g = scalar_load(p.g, b, h, 0);
-    beta = scalar_load(p.beta, b, h, 0);
-  }
-  if (has_q) xq = op_load<E>(p.q, b, h, 0, tk);
-  xk = t < K ? xk : 0.f;
-  xq = t < K ? xq : 0.f;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const bool ok = s0 && cok && rg + 16 * i < K;
-    st[i] = ok ? st[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-
-  // u(k) and u(q): x / max(||x||, 1e-6), rounded to the activation type
-  // (reference ops.py:14-17).
-  const float sk = sum64(xk * xk), sq = sum64(xq * xq);
-  if (lane == 0) {
-    norms[0][wave] = sk;
-    norms[1][wave] = sq;
-  }
-  lds_barrier();
-  const float nk = fmaxf(sqrtf(norms[0][0] + norms[0][1] + norms[0][2] + norms[0][3]), 1e-6f);
-  const float nq = fmaxf(sqrtf(norms[1][0] + norms[1][1] + norms[1][2] + norms[1][3]), 1e-6f);
-  if (t < 16 * NI) {
-    kh[t] = t < K ? round_as<E>(xk / nk) : 0.f;
-    qh[t] = t < K ? round_as<E>(xq / nq) : 0.f;
-  }
-  lds_barrier();
-
-  if (update) {
-    // scaled = exp(g) S; predicted = u(k)^T scaled; S' = scaled + beta (u(k) (v - predicted)^T)
-    const float a = expf(g);
-    float4 pk = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float kr = kh[rg + 16 * i];
-      st[i].x *= a;
-      st[i].y *= a;
-      st[i].z *= a;
-      st[i].w *= a;
-      pk.x += kr * st[i].x;
-      pk.y += kr * st[i].y;
-      pk.z += kr * st[i].z;
-      pk.w += kr * st[i].w;
-    }
-    const float4 pred = column_sums(pk, part[0], wave, rg, c4);
-    const float r0 = vv[0] - pred.x, r1 = vv[1] - pred.y, r2 = vv[2] - pred.z, r3 = vv[3] - pred.w;
-    float* dst = fin + (int64_t)s * K * V;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = rg + 16 * i;
-      const float kr = kh[row];
-      st[i].x += beta * (kr * r0);
-      st[i].y += beta * (kr * r1);
-      st[i].z += beta * (kr * r2);
-      st[i].w += beta * (kr * r3);
-      if (cok && row < K) *reinterpret_cast<float4*>(dst + (int64_t)row * V + col) = st[i];
-    }
-  }
-
-  if (has_q) {
-    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float qr = qh[rg + 16 * i];
-      po.x += qr * st[i].x;
-      po.y += qr * st[i].y;
-      po.z += qr * st[i].z;
-      po.w += qr * st[i].w;
-    }
-    const float4 o = column_sums(po, part[1], wave, rg, c4);
-    if (t < 16 && cok) {
-      E* op = reinterpret_cast<E*>(out.ptr) + op_base(out, b, h) + col;
-      op[0] = from_f32<E>(o.x);
-      op[1] = from_f32<E>(o.y);
-      op[2] = from_f32<E>(o.z);
-      op[3] = from_f32<E>(o.w);
-    }
-  }
-}
-
 template <typename E, int NI>
 __global__ __launch_bounds__(SNT) void gdn_token_step(gpa_gdn_problem p, float* fin, gpa_operand out) {
-  token_run<E, NI>(p, fin, out, blockIdx.x);
+  __shared__ TokenLds<NI> lds;
+  token_run<E, NI>(p, fin, out, blockIdx.x, threadIdx.x, lds);
 }
 
 // Several problems with the same element type and row class in one launch:
@@ -187,13 +43,9 @@ __global__ __launch_bounds__(SNT) void gdn_token_step_pack(TokenPack pk) {
   gpa_operand out;
   kernarg_copy(p, &kp->p[pi]);
   kernarg_copy(out, &kp->out[pi]);
-  token_run<E, NI>(p, kp->fin[pi], out, (int)blockIdx.x - kp->wg0[pi]);
+  __shared__ TokenLds<NI> lds;
+  token_run<E, NI>(p, kp->fin[pi], out, (int)blockIdx.x - kp->wg0[pi], threadIdx.x, lds);
 }
-
-int64_t token_workgroups(const gpa_gdn_problem& p) {
-  return (int64_t)p.batch * p.heads * ((p.vdim + SCOL - 1) / SCOL);
-}
-int token_rows(const gpa_gdn_problem& p) { return p.kdim <= 64 ? 4 : (p.kdim <= 128 ? 8 : 16); }
 
 template <typename E>
 void launch_token(const gpa_gdn_problem& p, float* fin, gpa_operand out, hipStream_t stream) {
@@ -212,28 +64,6 @@ void launch_token_pack(const TokenPack& pk, int rows, unsigned grid, hipStream_t
     case 8: hipLaunchKernelGGL((gdn_token_step_pack<E, 8>), dim3(grid), dim3(SNT), 0, stream, pk); break;
     default: hipLaunchKernelGGL((gdn_token_step_pack<E, 16>), dim3(grid), dim3(SNT), 0, stream, pk);
   }
-}
-
-bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
-
-int check_token(const gpa_gdn_problem* problem, const float* final_state, const gpa_operand& out) {
-  if (!problem) return fail(GPA_HIP_EINVAL, "token step: null problem");
-  const gpa_gdn_problem& p = *problem;
-  if (p.tokens != 1) return fail(GPA_HIP_EINVAL, "token step: needs tokens == 1");
-  if (p.batch < 1 || p.heads < 1 || p.kdim < 1 || p.vdim < 1) return fail(GPA_HIP_EINVAL, "token step: empty shape");
-  if (p.kdim > 256 || p.vdim > 256) return fail(GPA_HIP_EUNSUPPORTED, "token step: widths above 256");
-  if (p.vdim % 4) return fail(GPA_HIP_EUNSUPPORTED, "token step: V must be a multiple of 4");
-  if (p.dtype != GPA_DTYPE_F32 && p.dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "token step: dtype");
-  const bool update = p.k.ptr != nullptr;
-  if (update && (!p.v.ptr || !p.g.ptr || !p.beta.ptr || !final_state))
-    return fail(GPA_HIP_EINVAL, "token step: an update needs v, g, beta and final");
-  if (!update && (!p.q.ptr || !p.s0)) return fail(GPA_HIP_EINVAL, "token step: a read needs q and s0");
-  if (p.q.ptr && !out.ptr) return fail(GPA_HIP_EINVAL, "token step: a query needs out");
-  if (p.s0 && (!aligned16(p.s0) || p.s0_sb % 4 || p.s0_sh % 4))
-    return fail(GPA_HIP_EINVAL, "token step: s0 must be 16-byte aligned with strides a multiple of 4");
-  if (final_state && !aligned16(final_state)) return fail(GPA_HIP_EINVAL, "token step: final must be 16-byte aligned");
-  if (token_workgroups(p) > INT32_MAX / 2) return fail(GPA_HIP_EINVAL, "token step: too many streams");
-  return GPA_HIP_OK;
 }
 
 }  // namespace

@@ -12,7 +12,7 @@
 // split between thread groups and the partial sums meet in LDS); A^ w is a
 // row dot product per wave, eight rows at a time.  HBM bound: A^ is read
 // twice (the second time mostly from cache), B^ once.
-#include "gdn_common.h"
+#include "token_step.h"
 
 namespace gpa {
 namespace {
@@ -136,11 +136,11 @@ __global__ __launch_bounds__(QNT) void level_token(gpa_level_problem p) {
 constexpr int RQ = 8;  // float4 pieces of A^ (and of B^) per thread
 
 template <typename E, int NT>
-__global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
+__device__ __forceinline__ void level_token_reg_run(const gpa_level_problem& p, int s) {
   constexpr int NW = NT / 64;
   __shared__ float uk[256], wf[256], zp[NT * 4], rks[256];
   __shared__ float red[NW], soft[2];
-  const int s = blockIdx.x, b = s / p.heads, h = s - b * p.heads;
+  const int b = s / p.heads, h = s - b * p.heads;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int Dk = p.key_dim, Dv = p.value_dim, M = p.slots;
   const int ga = M / 4, gb = Dv / 4;          // float4 groups per row
@@ -256,6 +256,39 @@ __global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
     reinterpret_cast<E*>(p.key_out.ptr)[op_base(p.key_out, b, h) + t] = from_f32<E>(xk - eta0 * round_as<E>(rks[t]));
 }
 
+template <typename E, int NT>
+__global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
+  level_token_reg_run<E, NT>(p, blockIdx.x);
+}
+
+// A level's inner one-token step (K <= 16 NI, every NT / 256 consecutive
+// step workgroups in one NT-thread workgroup) and its one-token level write
+// (one stream per workgroup) in one launch.  They share no buffers: the step
+// reads the running state and writes a new one, the level write reads the
+// block snapshots.  Step and level workgroups alternate while both last, so
+// that each compute unit streams both kinds of data at once.
+template <typename E, int NI, int NT>
+__global__ __launch_bounds__(NT) void token_level(gpa_gdn_problem sp, float* fin, gpa_operand out,
+                                                  gpa_level_problem lp, int nstep) {
+  __shared__ TokenLds<NI> tl[NT / SNT];
+  const int nlev = lp.batch * lp.heads, blk = blockIdx.x, both = nstep < nlev ? nstep : nlev;
+  bool step;
+  int idx;
+  if (blk < 2 * both) {
+    step = (blk & 1) == 0;
+    idx = blk >> 1;
+  } else {
+    step = nstep > nlev;
+    idx = blk - both;
+  }
+  if (!step) {
+    level_token_reg_run<E, NT>(lp, idx);
+    return;
+  }
+  const int u = threadIdx.x / SNT;
+  token_run<E, NI>(sp, fin, out, idx * (NT / SNT) + u, threadIdx.x % SNT, tl[u]);
+}
+
 // Threads for the register kernel (0: the shape is not covered).
 int reg_threads(const gpa_level_problem& p) {
   const int Dk = p.key_dim, Dv = p.value_dim, M = p.slots;
@@ -269,11 +302,7 @@ int reg_threads(const gpa_level_problem& p) {
   }
   return 0;
 }
-}  // namespace
-}  // namespace gpa
-
-extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStream_t stream) {
-  using namespace gpa;
+int check_level_token(const gpa_level_problem* problem) {
   if (!problem) return fail(GPA_HIP_EINVAL, "level token: null problem");
   const gpa_level_problem& p = *problem;
   if (p.tokens != 1) return fail(GPA_HIP_EINVAL, "level token: needs tokens == 1");
@@ -284,6 +313,16 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
   if (!p.key.ptr || !p.value.ptr || !p.a_first || !p.b_first || !p.eta || !p.write.ptr || !p.key_out.ptr ||
       !p.value_out.ptr)
     return fail(GPA_HIP_EINVAL, "level token: null pointer (the snapshots a_first and b_first are required)");
+  return GPA_HIP_OK;
+}
+
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_level_token(problem)) return rc;
+  const gpa_level_problem& p = *problem;
   const dim3 grid((unsigned)((int64_t)p.batch * p.heads));
   const bool bf = p.dtype == GPA_DTYPE_BF16;
   switch (reg_threads(p)) {
@@ -304,4 +343,34 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
       else hipLaunchKernelGGL(level_token<float>, grid, dim3(QNT), 0, stream, p);
   }
   return check_launch("gpa_level_token_forward");
+}
+
+extern "C" int gpa_token_level_forward(const gpa_gdn_problem* step, float* final_state, gpa_operand out,
+                                       const gpa_level_problem* level, hipStream_t stream) {
+  using namespace gpa;
+  if (int rc = check_token(step, final_state, out)) return rc;
+  if (int rc = check_level_token(level)) return rc;
+  const int nt = reg_threads(*level), ni = token_rows(*step);
+  const int64_t swg = token_workgroups(*step), nlev = (int64_t)level->batch * level->heads;
+  // Only the 512-thread level kernel (M <= 128 at Dk = Dv = 128): at 1024
+  // threads the step role's registers leave room for one workgroup per
+  // compute unit, and the one launch is slower than the two.
+  const bool fused = step->dtype == level->dtype && nt == 512 && (ni == 8 || ni == 16) && swg % (nt / SNT) == 0 &&
+                     swg / (nt / SNT) + nlev <= INT32_MAX / 2;
+  if (!fused) {
+    if (int rc = gpa_gdn_token_step(step, final_state, out, stream)) return rc;
+    return gpa_level_token_forward(level, stream);
+  }
+  const int nstep = (int)(swg / (nt / SNT));
+  const dim3 grid((unsigned)(nstep + nlev));
+  const bool bf = step->dtype == GPA_DTYPE_BF16;
+#define GPA_TOKEN_LEVEL(E, NI) \
+  hipLaunchKernelGGL((token_level<E, NI, 512>), grid, dim3(512), 0, stream, *step, final_state, out, *level, nstep)
+  if (ni == 8) {
+    if (bf) GPA_TOKEN_LEVEL(bf16_t, 8); else GPA_TOKEN_LEVEL(float, 8);
+  } else {
+    if (bf) GPA_TOKEN_LEVEL(bf16_t, 16); else GPA_TOKEN_LEVEL(float, 16);
+  }
+#undef GPA_TOKEN_LEVEL
+  return check_launch("gpa_token_level_forward");
 }

@@ -119,18 +119,16 @@ class _LevelMix(torch.autograd.Function):
         return dkey, dvalue_out, da, db, da_first, db_first, deta, None, None
 
 
-def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
-                    offset: int) -> tuple[Tensor, Tensor, Tensor]:
-    """`level_mix` of a call that stays inside one block (offset + T <= chunk)
-    whose snapshots A^ [B,H,Dk,M] and B^ [B,H,M,Dv] are given: the scans'
-    chunk-start states are not needed (inference decode); no autograd."""
+def _block_problem(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
+                   offset: int):
+    """Checked arguments of a `level_mix_block` call: (problem, write, key',
+    value', tensors kept alive)."""
     _lib.require_device(key)
     bsz, tokens, heads, dk = key.shape
     if offset + tokens > chunk:
         raise ValueError("level_mix_block: the call must stay inside one block")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (key, value, a_first, b_first, eta)):
         raise RuntimeError("level_mix_block has no backward: call it under torch.no_grad() or inference_mode()")
-    lib = _lib.load()
     dtype, dv, m = key.dtype, value.shape[-1], a_first.shape[-1]
     key, value = key.contiguous(), value.contiguous()
     (af, asb), (bf, bsb) = _snapshot(a_first), _snapshot(b_first)
@@ -150,11 +148,41 @@ def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor
     p.eta = eta.data_ptr()
     p.write, p.key_out, p.value_out = (_lib.operand(t) for t in (write, key_out, value_out))
     p.rk, p.rv, p.stats = rk.data_ptr(), rv.data_ptr(), stats.data_ptr()
-    if tokens == 1 and _TOKEN_KERNEL[0]:
+    return p, write, key_out, value_out, (key, value, af, bf, eta, rk, rv, stats)
+
+
+def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
+                    offset: int) -> tuple[Tensor, Tensor, Tensor]:
+    """`level_mix` of a call that stays inside one block (offset + T <= chunk)
+    whose snapshots A^ [B,H,Dk,M] and B^ [B,H,M,Dv] are given: the scans'
+    chunk-start states are not needed (inference decode); no autograd."""
+    lib = _lib.load()
+    p, write, key_out, value_out, alive = _block_problem(key, value, a_first, b_first, eta, chunk, offset)
+    if key.shape[1] == 1 and _TOKEN_KERNEL[0]:
         _lib.check(lib.gpa_level_token_forward(p, _lib.stream_handle(key.device)), "gpa_level_token_forward")
     else:
         _lib.check(lib.gpa_level_forward(p, _lib.stream_handle(key.device)), "gpa_level_forward")
     return write, key_out, value_out
+
+
+def token_step_and_level(step, key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor,
+                         chunk: int, offset: int):
+    """A level's inner one-token step `ops.gdn_token_hip(*step)` and its
+    one-token `level_mix_block(key, value, a_first, b_first, eta, chunk,
+    offset)` in one launch (`gpa_token_level_forward`; inference decode, the
+    two share no buffers).  Returns (out, final, write, key', value') with the
+    results of the two separate calls."""
+    from .ops import _token_call, gdn_token_hip
+    if key.shape[1] != 1:
+        raise ValueError("token_step_and_level: needs one token")
+    if not _TOKEN_KERNEL[0]:
+        return gdn_token_hip(*step) + level_mix_block(key, value, a_first, b_first, eta, chunk, offset)
+    lib = _lib.load()
+    sp, final, out, alive_s = _token_call(*step)
+    lp, write, key_out, value_out, alive_l = _block_problem(key, value, a_first, b_first, eta, chunk, offset)
+    _lib.check(lib.gpa_token_level_forward(sp, final.data_ptr(), _lib.operand(out), lp,
+                                           _lib.stream_handle(key.device)), "gpa_token_level_forward")
+    return out, final, write, key_out, value_out
 
 
 _TOKEN_KERNEL = [True]  # one-token calls of level_mix_block on gpa_level_token_forward

@@ -37,7 +37,7 @@ from .counts import count_logits
 from .slots import slot_gates, slot_gates_act
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
-from .level import level_mix, level_mix_block
+from .level import level_mix, level_mix_block, token_step_and_level
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
 from .route import product_read
@@ -225,11 +225,17 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         fused_level = write is None and _FUSED_LEVEL[0] and fused_level_supported(
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
         if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
-            raw, a_final = gdn_token_hip(qr, key, slot, g_in, b_in, old.inner)
+            step = (qr, key, slot, g_in, b_in, old.inner)
+            if _TOKEN_LEVEL[0]:
+                # the A_j step and the level write in one launch (they share no buffers)
+                raw, a_final, write, key_next, value_next = token_step_and_level(
+                    step, key, value, snap.inner, snap.outer, eta, chunk, offset)
+            else:
+                raw, a_final = gdn_token_hip(*step)
+                write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             # The B_j step runs at its read, after the route reader (nothing
             # before needs the new B_j): one pass over the state for both.
             lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
-            write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
             lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
             if old.position is None and _token_logits_supported(raw, write):
@@ -556,6 +562,7 @@ def _residual_eta(key, value, rk, rv, eta):
 _FUSED_LEVEL = [True]  # the fused level write and residual (level.py)
 _DEFER_OUTER_READ = [True]  # outer reads as late reads of the B scans (ops.gdn_scan_deferred)
 _TOKEN_STEP = [True]  # one-token inference calls as token steps (ops.gdn_token_hip)
+_TOKEN_LEVEL = [True]  # a level's inner token step and its level write in one launch (level.token_step_and_level)
 _PACKED = [True]  # a level's A/B scans and all edge scans as packed calls (ops.gdn_scan_many)
 
 

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 20
+#define GPA_HIP_ABI_VERSION 21
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -424,6 +424,16 @@ int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *
  * key_out = key - eta0 round(A^ write), value_out = value - eta1 round(write^T B^).
  * Replaces reference src/gpa/attention.py:314-329 and :190-194 at T = 1. */
 int gpa_level_token_forward(const gpa_level_problem *problem, hipStream_t stream);
+/* A level's inner one-token step and its one-token level write in one launch
+ * (inference decode, reference attention.py:309-329 at T = 1: the A_j update
+ * and read, ops.py:29-46, beside _block_segment's write and residual).  The
+ * two share no buffers: `step` reads the running state s0 and writes
+ * final_state / out, `level` reads the block snapshots.  Results are those of
+ * gpa_gdn_token_step(step, final_state, out) and gpa_level_token_forward(level);
+ * shapes outside the one-launch kernel (it covers the 512-thread level kernel,
+ * e.g. Dk = M = Dv = 128, and key widths 65..256) take those two launches. */
+int gpa_token_level_forward(const gpa_gdn_problem *step, float *final_state, gpa_operand out,
+                            const gpa_level_problem *level, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Slot counts and base logits of one level (reference attention.py:196-204,

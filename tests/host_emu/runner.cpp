@@ -106,6 +106,11 @@ int main(int argc, char** argv) {
     case 9:
       rc = gpa_level_token_forward(reinterpret_cast<gpa_level_problem*>(blobs.at(0).data()), nullptr);
       break;
+    case 10:
+      rc = gpa_token_level_forward(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                                   static_cast<float*>(raw.at(0)), *reinterpret_cast<gpa_operand*>(blobs.at(1).data()),
+                                   reinterpret_cast<gpa_level_problem*>(blobs.at(2).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

@@ -233,3 +233,33 @@ def test_token_logits_many_matches_one_call_per_level(dtype):
     for got, ref in zip(many, one):
         for name, a, r in zip(("logits", "counts", "local"), got, ref):
             assert a.dtype == r.dtype and a.shape == r.shape and torch.equal(a, r), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("step_shape,lvl", [((8, 16, 128, 128), (8, 16, 128, 128, 128)),
+                                            ((8, 16, 128, 256), (8, 16, 128, 256, 128)),
+                                            ((3, 4, 128, 64), (2, 4, 128, 128, 128)),
+                                            ((4, 4, 100, 128), (1, 4, 128, 128, 128)),
+                                            ((2, 3, 20, 12), (2, 3, 20, 12, 8))],
+                         ids=["m128", "m256", "fewer_steps", "more_steps", "two_launches"])
+def test_token_level_matches_separate_calls(step_shape, lvl, dtype):
+    """A level's inner token step and its level write in one launch
+    (gpa_token_level_forward) give the bits of the two separate calls."""
+    from gpa_amd import level
+    g = torch.Generator().manual_seed(sum(step_shape) + sum(lvl))
+    b, h, k, v = step_shape
+    q, key, val = (torch.randn(b, 1, h, d, generator=g).to(DEV, dtype) for d in (k, k, v))
+    lg, beta = -torch.rand(b, 1, h, generator=g).to(DEV), torch.rand(b, 1, h, generator=g).to(DEV)
+    step = (q, key, val, lg, beta, (torch.randn(b, h, k, v, generator=g) * .2).to(DEV))
+    lb, lh, dk, m, dv = lvl
+    lkey = torch.randn(lb, 1, lh, dk, generator=g).to(DEV, dtype)
+    lval = torch.randn(lb, 1, lh, dv, generator=g).to(DEV, dtype)
+    fa = (torch.randn(lb, lh, dk, m, generator=g) * .3).to(DEV)
+    fb = (torch.randn(lb, lh, m, dv, generator=g) * .3).to(DEV)
+    eta = (1 + .25 * torch.randn(lh, 2, generator=g).tanh()).to(DEV)
+    with torch.no_grad():
+        fused = level.token_step_and_level(step, lkey, lval, fa, fb, eta, 64, 5)
+        apart = gdn_token_hip(*step) + level.level_mix_block(lkey, lval, fa, fb, eta, 64, 5)
+    torch.cuda.synchronize()
+    for name, a, r in zip(("out", "final", "write", "key'", "value'"), fused, apart):
+        assert a.dtype == r.dtype and torch.equal(a, r), name

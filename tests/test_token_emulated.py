@@ -10,7 +10,11 @@ and compared on the CPU:
   arguments) against one call per group, bit for bit;
 - `level_mix_block` at one token on the one-token level kernel against the
   block kernel of the same host build, for register and generic shapes
-  (M = 12, Dv = 8) and batch-broadcast snapshots.
+  (M = 12, Dv = 8) and batch-broadcast snapshots;
+- `token_step_and_level` (a level's inner token step and its level write in
+  one launch) against the two separate calls, bit for bit, with as many, fewer
+  and more step workgroups than level streams, and a shape that takes the
+  two launches.
 
 Every access of these kernels is bounds-checked here before they run on a GPU.
 """
@@ -112,3 +116,25 @@ def test_level_token_kernel_matches_block_kernel(host, monkeypatch, b, h, dk, dv
     for name, a, r in zip(("write", "key'", "value'"), outs[True], outs[False]):
         assert a.dtype == r.dtype == dtype and a.shape == r.shape, name
         assert _rel(a, r) < tol, (name, _rel(a, r))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("step_shape,lvl", [((2, 2, 128, 128), (2, 2, 128, 128, 128)),
+                                            ((1, 2, 128, 256), (1, 2, 128, 256, 128)),
+                                            ((3, 2, 128, 64), (2, 2, 128, 128, 128)),
+                                            ((4, 2, 100, 128), (1, 2, 128, 128, 128)),
+                                            ((2, 1, 20, 12), (2, 1, 20, 12, 8))],
+                         ids=["m128", "m256", "fewer_steps", "more_steps", "two_launches"])
+def test_token_level_matches_separate_calls(host, step_shape, lvl, dtype):
+    g = torch.Generator().manual_seed(sum(step_shape) + sum(lvl))
+    step = _call(g, *step_shape, dtype, "full", True)
+    lb, lh, dk, m, dv = lvl
+    key = torch.randn(lb, 1, lh, dk, generator=g).to(dtype)
+    value = torch.randn(lb, 1, lh, dv, generator=g).to(dtype)
+    fa, fb = torch.randn(lb, lh, dk, m, generator=g) * .3, torch.randn(lb, lh, m, dv, generator=g) * .3
+    eta = 1 + .25 * torch.randn(lh, 2, generator=g).tanh()
+    with torch.no_grad():
+        fused = level.token_step_and_level(step, key, value, fa, fb, eta, 4, 2)
+        apart = ops.gdn_token_hip(*step) + level.level_mix_block(key, value, fa, fb, eta, 4, 2)
+    for name, a, r in zip(("out", "final", "write", "key'", "value'"), fused, apart):
+        assert a.dtype == r.dtype and torch.equal(a, r), name
