@@ -131,8 +131,9 @@ def decode_rate(model, steps: int = 256, warmup: int = 64, prefill: int = 2048) 
             "ms_per_token_step": seconds * 1e3, "eager_ms_per_token_step": eager_s * 1e3,
             "prefill_tokens": prefill, "warmup_steps": warmup, "steps": steps,
             "path": "schedule T=1 segments (one-token scan steps gdn_token_step, register-resident block-snapshot "
-                    "level kernel, one-launch gate/logit/mix glue, cached parameter layouts) replayed from one HIP "
-                    "graph per block position; the fused one-kernel step is switched off",
+                    "level kernel, each 128-slot level's inner step and level write in one launch, one-launch "
+                    "gate/logit/mix glue, cached parameter layouts) replayed from one HIP graph per block position; "
+                    "the fused one-kernel step is switched off",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 
