@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 21
+ABI_VERSION = 22
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -215,6 +215,8 @@ EXPORTS = {
     "gpa_product_read_backward": ([ctypes.POINTER(ProductProblem), ctypes.POINTER(ProductGrads), c_vp], ctypes.c_int),
     "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
+    "gpa_copy_many": ([ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(ctypes.c_int64), c_i32, c_vp],
+                      ctypes.c_int),
 }
 
 _lib = None

@@ -163,3 +163,47 @@ extern "C" int gpa_output_mix_forward(const gpa_mix_problem* p, hipStream_t stre
     hipLaunchKernelGGL(output_mix<float>, grid, block, 0, stream, *p);
   return check_launch("gpa_output_mix_forward");
 }
+
+namespace gpa {
+namespace {
+
+// Up to GPA_COPY_MAX buffers copied in one launch (grid.y = buffer), 16 bytes
+// per thread per step; every buffer and size is a multiple of 16 bytes.
+struct CopyPack {
+  const uint4* src[GPA_COPY_MAX];
+  uint4* dst[GPA_COPY_MAX];
+  int64_t count[GPA_COPY_MAX];
+};
+
+__global__ __launch_bounds__(256) void copy_many(CopyPack pk) {
+  const int i = blockIdx.y;  // uniform: selects, not a dynamic index into the argument
+  const uint4* src = i == 0 ? pk.src[0] : i == 1 ? pk.src[1] : i == 2 ? pk.src[2] : pk.src[3];
+  uint4* dst = i == 0 ? pk.dst[0] : i == 1 ? pk.dst[1] : i == 2 ? pk.dst[2] : pk.dst[3];
+  const int64_t n = i == 0 ? pk.count[0] : i == 1 ? pk.count[1] : i == 2 ? pk.count[2] : pk.count[3];
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) dst[e] = src[e];
+}
+
+}  // namespace
+}  // namespace gpa
+
+extern "C" int gpa_copy_many(void* const* dst, const void* const* src, const int64_t* bytes, int32_t n,
+                             hipStream_t stream) {
+  using namespace gpa;
+  if (!dst || !src || !bytes || n < 1 || n > GPA_COPY_MAX)
+    return fail(GPA_HIP_EINVAL, "copy many: 1 to GPA_COPY_MAX buffers");
+  CopyPack pk{};
+  int64_t most = 0;
+  for (int i = 0; i < n; ++i) {
+    if (bytes[i] < 0 || bytes[i] % 16 || (bytes[i] && (!dst[i] || !src[i])) || (uintptr_t)dst[i] % 16 ||
+        (uintptr_t)src[i] % 16)
+      return fail(GPA_HIP_EINVAL, "copy many: buffers and sizes must be multiples of 16 bytes");
+    pk.src[i] = static_cast<const uint4*>(src[i]);
+    pk.dst[i] = static_cast<uint4*>(dst[i]);
+    pk.count[i] = bytes[i] / 16;
+    most = pk.count[i] > most ? pk.count[i] : most;
+  }
+  if (!most) return GPA_HIP_OK;
+  const int64_t blocks = (most + 255) / 256;
+  hipLaunchKernelGGL(copy_many, dim3((unsigned)(blocks < 1024 ? blocks : 1024), (unsigned)n), dim3(256), 0, stream, pk);
+  return check_launch("gpa_copy_many");
+}

@@ -6,6 +6,8 @@ distribution (:316-323, :196-204, :330) and the output mix (:340-341).  They
 carry no autograd: the schedule uses them when no gradient is recorded."""
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch import Tensor
 
@@ -93,3 +95,28 @@ def output_mix(reads, weights: Tensor, out: Tensor | None = None) -> Tensor:
     p.weights, p.out = w.data_ptr(), _lib.operand(out)
     _lib.check(lib.gpa_output_mix_forward(p, _lib.stream_handle(out.device)), "gpa_output_mix_forward")
     return out
+
+
+COPY_MAX = 4  # buffers per gpa_copy_many launch
+
+
+def copy_many(pairs) -> bool:
+    """dst.copy_(src) for up to COPY_MAX (dst, src) pairs of contiguous device
+    tensors with equal shape and dtype, in one launch (`gpa_copy_many`).  Returns
+    False, copying nothing, when a pair is not 16-byte aligned and sized."""
+    if not 1 <= len(pairs) <= COPY_MAX:
+        raise ValueError("copy_many: 1 to 4 pairs")
+    for d, s in pairs:
+        _lib.require_device(d)
+        if d.shape != s.shape or d.dtype != s.dtype or d.device != s.device:
+            raise ValueError("copy_many: each pair must match in shape, dtype and device")
+        if (not d.is_contiguous() or not s.is_contiguous() or d.data_ptr() % 16 or s.data_ptr() % 16
+                or (d.numel() * d.element_size()) % 16):
+            return False
+    lib = _lib.load()
+    n = len(pairs)
+    dst = (ctypes.c_void_p * n)(*(d.data_ptr() for d, _ in pairs))
+    src = (ctypes.c_void_p * n)(*(s.data_ptr() for _, s in pairs))
+    size = (ctypes.c_int64 * n)(*(d.numel() * d.element_size() for d, _ in pairs))
+    _lib.check(lib.gpa_copy_many(dst, src, size, n, _lib.stream_handle(pairs[0][0].device)), "gpa_copy_many")
+    return True

@@ -20,7 +20,7 @@ import gc
 
 import torch
 
-from . import params, schedule
+from . import glue, params, schedule
 
 
 # Captures of steps over this many rows (batch x tokens) or more are refused:
@@ -161,7 +161,10 @@ class DecodeGraph:
         for static, value in zip(self.inputs, (q, k, v)):
             if static.shape != value.shape or static.dtype != value.dtype:
                 raise ValueError("DecodeGraph replays only the captured token shape/dtype")
-            static.copy_(value)
+        pairs = list(zip(self.inputs, (q, k, v)))
+        if not (all(x.device == self.inputs[0].device for x in (q, k, v)) and glue.copy_many(pairs)):
+            for static, value in pairs:
+                static.copy_(value)
         o = self.offset
         self.graphs[o].replay()
         self.offset = (o + 1) % self.chunk

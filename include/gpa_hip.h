@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 21
+#define GPA_HIP_ABI_VERSION 22
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -557,6 +557,12 @@ typedef struct gpa_mix_problem {
     gpa_operand out;                              /* [B,T,H,Dv] */
 } gpa_mix_problem;
 int gpa_output_mix_forward(const gpa_mix_problem *problem, hipStream_t stream);
+/* Device-to-device copies of up to GPA_COPY_MAX buffers in one launch: dst[i]
+ * <- src[i], bytes[i] each, every pointer and size a multiple of 16 bytes
+ * (GPA_HIP_EINVAL otherwise).  No reference counterpart: it moves a decode
+ * token's q, k and v into the buffers a captured decode graph reads. */
+#define GPA_COPY_MAX 4
+int gpa_copy_many(void *const *dst, const void *const *src, const int64_t *bytes, int32_t n, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -263,3 +263,21 @@ def test_token_level_matches_separate_calls(step_shape, lvl, dtype):
     torch.cuda.synchronize()
     for name, a, r in zip(("out", "final", "write", "key'", "value'"), fused, apart):
         assert a.dtype == r.dtype and torch.equal(a, r), name
+
+
+def test_copy_many_matches_copy():
+    """One launch copies a decode token's q, k and v (gpa_copy_many) with the
+    bytes of Tensor.copy_; an unaligned pair is refused without copying."""
+    from gpa_amd import glue
+    src = [torch.randn(64, 1, 16, 128, device=DEV).bfloat16(), torch.randn(3, 1, 2, 8, device=DEV),
+           torch.randn(0, 4, device=DEV)]
+    dst = [torch.zeros_like(x) for x in src]
+    assert glue.copy_many(list(zip(dst, src)))
+    torch.cuda.synchronize()
+    assert all(torch.equal(d, s) for d, s in zip(dst, src))
+    odd = torch.randn(7, device=DEV)
+    keep = torch.zeros(7, device=DEV)
+    assert not glue.copy_many([(keep, odd)])
+    assert not glue.copy_many([(torch.zeros(8, device=DEV)[1:5], torch.randn(4, device=DEV))])
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(keep) == 0
