@@ -84,7 +84,7 @@ def decode_rate(model, steps: int = 256, warmup: int = 64, prefill: int = 2048) 
     The eager rate of 64 steps from the same cache is reported beside it."""
     import torch
 
-    from gpa_amd import DecodeGraph
+    from gpa_amd import DecodeGraph, params
     cfg = model.config
     dev = next(model.parameters()).device
     h, dk, dv = cfg.heads, cfg.key_dim, cfg.value_dim
@@ -97,7 +97,9 @@ def decode_rate(model, steps: int = 256, warmup: int = 64, prefill: int = 2048) 
         return q, k.bfloat16(), v
 
     _progress(f"decode: {prefill}-token prefill at B={DECODE_BATCH}")
-    with torch.no_grad():
+    # Inference leaves the parameters unchanged, so parameter-derived tensors
+    # (packed weight layouts, gate constants) are computed once (params.frozen).
+    with torch.no_grad(), params.frozen():
         state = model.initial_state(DECODE_BATCH, device=dev, dtype=torch.bfloat16)
         for _ in range(prefill // 512):
             _, state = model(*tokens(512), state)

@@ -2,12 +2,13 @@
 
 Field names, defaults and the `ValueError` contract mirror the reference
 `GPAConfig` (src/gpa/attention.py:17-75) so that configurations and
-checkpoints move between the two packages unchanged.  One difference is
-deliberate: `backend` defaults to and only accepts ``"hip"``.  The
-``torch``/``fla`` backends belong to the reference package; this package is the
-gfx950 backend that drops in beside them.  As in the reference,
-``chunk_size == 1`` selects the tokenwise model (attention.py:264-297) and
-``chunk_size > 1`` the block-lagged chunk model.
+checkpoints move between the two packages unchanged.  Every default equals the
+reference's except one, on purpose: `backend` defaults to and only accepts
+``"hip"``.  The ``torch``/``fla`` backends belong to the reference package;
+this package is the gfx950 backend that drops in beside them.  As in the
+reference, ``chunk_size`` defaults to 1, which selects the tokenwise model
+(attention.py:264-297); ``chunk_size > 1`` selects the block-lagged chunk
+model.
 
 `execution` is accepted for API compatibility and ignored: every reference
 schedule (reference/packed/triton/staged) computes the same function
@@ -36,7 +37,7 @@ class GPAConfig:
     decay_init: float = .001
     relation_beta_init: float = .6
     relation_decay_init: float = .0001
-    chunk_size: int = 64
+    chunk_size: int = 1
     backend: str = "hip"
     execution: str = "reference"
     read_scale: float = 1.

@@ -1075,6 +1075,28 @@ int side_join(hipStream_t st, const SideStream& sd) {
   return GPA_HIP_OK;
 }
 
+// Holds the side stream of one call from its fork to its join.  The join
+// (the caller's stream waits for everything enqueued on the side stream) is
+// recorded on every return path once a fork has happened, so that a call that
+// fails part-way still leaves the side work ordered before later work on the
+// caller's stream; the mutex is released after the join.
+struct SideScope {
+  hipStream_t st;
+  SideStream* sd = nullptr;
+  std::unique_lock<std::mutex> lock;
+  explicit SideScope(hipStream_t s) : st(s) {}
+  SideScope(const SideScope&) = delete;
+  SideScope& operator=(const SideScope&) = delete;
+  ~SideScope() {
+    if (sd) (void)side_join(st, *sd);
+  }
+  int join() {
+    SideStream* s = sd;
+    sd = nullptr;
+    return s ? side_join(st, *s) : GPA_HIP_OK;
+  }
+};
+
 // Which groups of the call run on the side stream: the 256-key groups when
 // the call also has others; else, for a call of strip groups only (a level's
 // A/B pair), the second half of the groups, each half in its own strip pack,
@@ -1102,12 +1124,11 @@ bool side_groups(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStre
 int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, const gpa_operand* outs, int n,
                         gpa_timing* tm, hipStream_t st) {
   const gpa_gdn_grads none{};
-  SideStream* side = nullptr;
-  std::unique_lock<std::mutex> side_lock;
+  SideScope side(st);
   bool on_side[GPA_GDN_MAX_PACK];
   if (side_groups(ps, n, tm, st, on_side))
-    if (int rc = side_fork(st, side, side_lock)) return rc;
-  auto stream_of = [&](int i) { return side && on_side[i] ? side->s : st; };
+    if (int rc = side_fork(st, side.sd, side.lock)) return rc;
+  auto stream_of = [&](int i) { return side.sd && on_side[i] ? side.sd->s : st; };
   for (int i = 0; i < n; ++i) {
     mark(tm, st);
     if (int rc = phase(Phase::prep, ps[i], svs[i], outs[i], none, stream_of(i))) return rc;
@@ -1160,8 +1181,7 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
     mark(tm, st);
     if (int rc = phase(Phase::out, ps[i], svs[i], outs[i], none, stream_of(i))) return rc;
   }
-  if (side)
-    if (int rc = side_join(st, *side)) return rc;
+  if (int rc = side.join()) return rc;
   mark(tm, st);
   return check_launch("gdn_forward");
 }
@@ -1173,12 +1193,11 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
   const gpa_operand none{};
   gpa_gdn_grads gr[GPA_GDN_MAX_PACK];
   for (int i = 0; i < n; ++i) gr[i] = effective_grads(ps[i], grs[i]);
-  SideStream* side = nullptr;
-  std::unique_lock<std::mutex> side_lock;
+  SideScope side(st);
   bool on_side[GPA_GDN_MAX_PACK];
   if (side_groups(ps, n, tm, st, on_side))
-    if (int rc = side_fork(st, side, side_lock)) return rc;
-  auto stream_of = [&](int i) { return side && on_side[i] ? side->s : st; };
+    if (int rc = side_fork(st, side.sd, side.lock)) return rc;
+  auto stream_of = [&](int i) { return side.sd && on_side[i] ? side.sd->s : st; };
   for (int i = 0; i < n; ++i) {
     if (!has_read(ps[i], gr[i])) continue;
     mark(tm, st);
@@ -1237,8 +1256,7 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
     mark(tm, st);
     if (int rc = phase(Phase::chunk_bwd, ps[i], svs[i], none, gr[i], stream_of(i))) return rc;
   }
-  if (side)
-    if (int rc = side_join(st, *side)) return rc;
+  if (int rc = side.join()) return rc;
   mark(tm, st);
   return check_launch("gdn_backward");
 }

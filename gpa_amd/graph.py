@@ -93,9 +93,10 @@ class DecodeGraph:
     copy per block).
 
     Tensors derived from the parameters alone (packed weight layouts, gate
-    constants) are computed once and read by the graphs (`params.frozen`), so
-    the parameters must not change while the graphs are in use: `step` raises
-    if one has.
+    constants) are computed once, kept by this object and read by the graphs
+    (`params.frozen`), so the parameters must not change while the graphs are
+    in use: `step` raises if one has been replaced, moved or updated in place
+    through the parameter itself.
 
     `step(q, k, v)` ([B,1,H,D] like the captured token) copies the token into
     the static inputs, replays the graph of the current position and returns
@@ -127,8 +128,10 @@ class DecodeGraph:
         current = torch.cuda.current_stream()
         side = torch.cuda.Stream()
         side.wait_stream(current)
-        self._params = [(p, p._version) for p in model.parameters()]
-        with torch.no_grad(), torch.cuda.stream(side), params.frozen():
+        self._params = params.fingerprints(list(model.parameters()))
+        # The derived tensors live as long as the graphs that read them.
+        self._derived = params.Store()
+        with torch.no_grad(), torch.cuda.stream(side), params.frozen(self._derived):
             s = self.start
             for _ in range(warmups):
                 _, s = model(*self.inputs, s)
@@ -139,7 +142,7 @@ class DecodeGraph:
         # One output buffer per position, from the ordinary allocator.
         self.outputs = [torch.empty_like(self.inputs[2]) for _ in range(self.chunk)]
         s = self.start
-        with torch.no_grad(), params.frozen():
+        with torch.no_grad(), params.frozen(self._derived):
             for o in range(self.chunk):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=self.pool):
@@ -156,7 +159,7 @@ class DecodeGraph:
             raise RuntimeError("DecodeGraph: the cache after a block does not match the cache it started from")
 
     def step(self, q, k, v):
-        if any(p._version != ver for p, ver in self._params):
+        if not params.unchanged(self._params):
             raise RuntimeError("DecodeGraph: a parameter changed after capture; build a new DecodeGraph")
         for static, value in zip(self.inputs, (q, k, v)):
             if static.shape != value.shape or static.dtype != value.dtype:

@@ -40,8 +40,9 @@ def _pack(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
     """[H,K,N] weight -> [H,N32,K16] rows of the contraction for each output
     column (transpose=True), or [H,K,N] -> [H,K32,N16] (transpose=False:
     output column = K, contraction = N); rounded to `dtype`, zero padded.
-    Cached while the weight is unchanged (params.derived) when it is a leaf
-    tensor (a parameter); a weight computed in the call is packed afresh."""
+    Inside params.frozen() a leaf weight (a parameter) is packed once per
+    scope; otherwise, and for a weight computed in the call, it is packed
+    afresh."""
     if not w.is_leaf:
         return _pack_now(w, dtype, transpose)
     return params.derived(("route_pack", id(w), dtype, transpose), (w,), lambda: _pack_now(w, dtype, transpose))
@@ -80,7 +81,8 @@ def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, 
 
 def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs):
     """The forward problem of one target level and every tensor it points
-    into: (problem, (base, q, edge_w, g, mg, msgs), (qo, route), saved rows)."""
+    into: (problem, (base, q, edge_w, g, mg, msgs, packed weights), (qo,
+    route), saved rows).  The caller keeps these alive until the launch."""
     dtype = q.dtype
     bsz, tokens, heads, _ = q.shape
     m = base.shape[-1]
@@ -98,7 +100,7 @@ def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_sc
              torch.empty(heads, rows, 2 * m, device=q.device, dtype=dtype),
              torch.empty(heads, rows, m, device=q.device, dtype=dtype))
     prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved)
-    return prob, (base, q, edge_w, g, mg, msgs), (qo, route), saved
+    return prob, (base, q, edge_w, g, mg, msgs, weights), (qo, route), saved
 
 
 class _RouteReader(torch.autograd.Function):
@@ -107,9 +109,10 @@ class _RouteReader(torch.autograd.Function):
         _lib.require_device(q)
         ctx.set_materialize_grads(False)
         lib = _lib.load()
-        prob, (base, q, edge_w, g, mg, msgs), (qo, route), saved = _forward_problem(
+        prob, (base, q, edge_w, g, mg, msgs, packed), (qo, route), saved = _forward_problem(
             base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs)
         _lib.check(lib.gpa_route_forward(prob, _lib.stream_handle(q.device)), "gpa_route_forward")
+        del packed
         ctx.query_scale = query_scale
         ctx.n_in = len(msgs)
         ctx.param_dtypes = (edge_w.dtype if msgs else None, gain.dtype, mlp_gain.dtype,

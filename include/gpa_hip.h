@@ -5,12 +5,23 @@
  * Every entry point takes plain device pointers, sizes and element strides,
  * enqueues its kernels on the given HIP stream and returns 0 on success or a
  * negative GPA_HIP_E* code; gpa_hip_last_error() then describes the failure
- * (per calling thread).  The library never allocates device memory, never
- * synchronises and keeps no mutable global state: every buffer (inputs,
- * outputs, the intermediates a backward pass needs) is owned by the caller,
- * so calls are reentrant and may be captured into a HIP graph.  The one
- * exception is gpa_gdn_scan_noalloc, which keeps its intermediates in a
- * static per-device array (see there).
+ * (per calling thread).  The library never allocates device memory and never
+ * synchronises: every buffer (inputs, outputs, the intermediates a backward
+ * pass needs) is owned by the caller, so calls are reentrant and may be
+ * captured into a HIP graph.  Library-held state, all of it per device:
+ *  - gpa_gdn_forward_many / gpa_gdn_backward_many keep one side stream and
+ *    two events per device, created (default priority, hipStreamNonBlocking)
+ *    on the first call that needs them and kept for the process.  When a
+ *    call mixes 256-key groups with narrower ones (or, forward and backward,
+ *    packs two or more strip groups), part of its groups run on that stream:
+ *    the call records a fork event on the caller's stream, makes the side
+ *    stream wait for it, enqueues, and makes the caller's stream wait for a
+ *    join event on every return path, so later work on the caller's stream
+ *    is ordered after all of the call's kernels.  The enqueue sequence runs
+ *    under a process-wide mutex.  Calls under graph capture and timed calls
+ *    never take the side stream (they stay on the caller's stream).
+ *  - gpa_gdn_scan_noalloc keeps its intermediates in a static per-device
+ *    array (see there).
  *
  * Operand convention.  A scan runs `batch*heads` independent streams.  Element
  * (stream s = b*heads + h, token t, feature d) of a gpa_operand lives at

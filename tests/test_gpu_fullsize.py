@@ -10,7 +10,9 @@ properties the model guarantees at any size:
     (attention.py:309-329 never reads it, reference tests/test_gpa.py:107-115);
   * config 4 (the same layer, batch 64, a 2048-token prefill, then one-token
     steps): the prefill split at 1024 equals the whole prefill, and the graphed
-    decode equals eager decode for a block's first steps.
+    decode equals eager decode for a block's first steps;
+  * config 2 (B=8, T=1024, H=4, Dk=32, Dv=48, slots (64,64,64,128), chunk 64,
+    fp32): the same finiteness, partition and Q-independence properties.
 The kernels at these shapes are compared with the oracle at reduced head
 counts and lengths elsewhere (test_gpu_dense_gpa.py, test_gpu_graph.py)."""
 import pytest
@@ -109,3 +111,54 @@ def test_c4_prefill_partition_and_graphed_decode(c3_model):
             y_eager, state = c3_model(*x, state)
             assert torch.isfinite(y_eager).all()
             assert _rel(y_graph, y_eager) < 1e-6, i
+
+
+C2 = dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=64)
+
+
+def _c2_inputs(seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    q = torch.randn(8, 1024, 4, 32, device=DEV, generator=g)
+    k = torch.randn(8, 1024, 4, 32, device=DEV, generator=g)
+    v = torch.randn(8, 1024, 4, 48, device=DEV, generator=g)
+    return q, k, v
+
+
+def test_c2_full_size_properties():
+    """Config 2 at its full size (B=8, T=1024, H=4, Dk=32, Dv=48, slots
+    (64,64,64,128), chunk 64, fp32): forward+backward is finite with a
+    gradient for every parameter; the call split into cached calls at 512
+    (block-aligned) and 515 (inside a block) gives the whole call's output and
+    cache; the level memories do not depend on Q."""
+    print("C2 full size: B=8 T=1024 H=4 fp32 forward+backward", flush=True)
+    torch.manual_seed(0)
+    model = DenseGPA(GPAConfig(**C2)).to(DEV)
+    xs = [x.requires_grad_() for x in _c2_inputs(5)]
+    out, state = model(*xs)
+    loss = out.square().mean()
+    loss.backward()
+    assert out.shape == (8, 1024, 4, 48) and out.dtype == torch.float32
+    assert torch.isfinite(out).all() and torch.isfinite(loss)
+    assert all(torch.isfinite(t).all() for t in tensors(state))
+    for n, p in model.named_parameters():
+        if n == "moment_gain":
+            continue
+        assert p.grad is not None and torch.isfinite(p.grad).all(), n
+    for x in xs:
+        assert torch.isfinite(x.grad).all() and x.grad.abs().sum() > 0
+    q, k, v = (x.detach() for x in xs)
+    with torch.no_grad():
+        whole, s_whole = model(q, k, v)
+        assert _rel(whole, out) < 1e-6
+        for cut in (512, 515):
+            print("C2 full size: partition at", cut, flush=True)
+            y1, s1 = model(q[:, :cut], k[:, :cut], v[:, :cut])
+            y2, s2 = model(q[:, cut:], k[:, cut:], v[:, cut:], s1)
+            assert s2.position == 1024 and s2.chunk_offset == 0
+            assert _rel(torch.cat((y1, y2), 1), whole) < 1e-5
+            for a, b in zip(tensors(s2), tensors(s_whole)):
+                assert _rel(a, b) < 1e-5
+        y3, s3 = model(q * -2 + .5, k, v)
+    for a, b in zip(s_whole.levels, s3.levels):
+        assert torch.equal(a.inner, b.inner) and torch.equal(a.outer, b.outer) and torch.equal(a.count, b.count)
+    assert not torch.equal(y3, whole)

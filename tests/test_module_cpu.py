@@ -22,9 +22,72 @@ def test_config_rejects(bad):
 
 def test_config_defaults_and_edges():
     cfg = GPAConfig()
-    assert cfg.backend == "hip" and cfg.chunk_size == 64
+    assert cfg.backend == "hip" and cfg.chunk_size == 1
     assert cfg.edges == tuple((i, j) for i in range(4) for j in range(4) if i != j)
     replace(cfg, execution="staged")  # accepted and ignored
+
+
+def test_config_defaults_match_the_reference_field_by_field():
+    """Every GPAConfig field, in declaration order, with the reference's
+    default (src/gpa/attention.py:17-42, fixture written by
+    tests/golden/make_config_defaults.py from that source); `backend` is the
+    one deliberate difference ("hip" instead of "torch")."""
+    import json
+    import os
+    from dataclasses import fields
+    with open(os.path.join(os.path.dirname(__file__), "golden", "config_defaults.json")) as f:
+        ref = json.load(f)["fields"]
+    ours = [(fl.name, fl.default) for fl in fields(GPAConfig)]
+    assert [n for n, _ in ours] == [n for n, _ in ref]
+    for (name, mine), (_, theirs) in zip(ours, ref):
+        if name == "backend":
+            assert (mine, theirs) == ("hip", "torch")
+        elif isinstance(mine, tuple):
+            assert list(mine) == theirs, name
+        else:
+            assert mine == theirs and type(mine) is type(theirs), name
+
+
+def test_parameter_derived_tensors_are_cached_only_inside_frozen():
+    """params.derived recomputes on every call unless the caller opts in with
+    params.frozen(store); inside, an entry is dropped when the parameter is
+    replaced (p.data = ...), converted (.double()) or updated in place."""
+    from gpa_amd import params
+    p = torch.nn.Parameter(torch.ones(3))
+    calls = []
+
+    def fn():
+        calls.append(1)
+        return p.detach() * 2
+
+    # outside frozen(): never cached, so in-place and .data updates are seen
+    assert torch.equal(params.derived("k", (p,), fn), torch.full((3,), 2.))
+    p.data.copy_(torch.full((3,), 5.))
+    assert torch.equal(params.derived("k", (p,), fn), torch.full((3,), 10.))
+    p.data = torch.full((3,), 7.)
+    assert torch.equal(params.derived("k", (p,), fn), torch.full((3,), 14.))
+    assert len(calls) == 3
+    with params.frozen() as store:
+        a = params.derived("k", (p,), fn)
+        assert params.derived("k", (p,), fn) is a and len(calls) == 4 and len(store) == 1
+        p.data = torch.full((3,), 1.)           # new storage
+        assert torch.equal(params.derived("k", (p,), fn), torch.full((3,), 2.)) and len(calls) == 5
+        with torch.no_grad():
+            p.add_(1.)                           # version counter
+        assert torch.equal(params.derived("k", (p,), fn), torch.full((3,), 4.)) and len(calls) == 6
+        m = torch.nn.Linear(2, 2)
+        m.weight.requires_grad_(False)
+        w = params.derived("w", (m.weight,), lambda: m.weight * 1)
+        m.double()                               # same Parameter object, new dtype
+        assert params.derived("w", (m.weight,), lambda: m.weight * 1).dtype == torch.float64
+        assert w.dtype == torch.float32
+    # the store belongs to its scope: a new scope starts empty
+    with params.frozen() as again:
+        assert len(again) == 0
+    prints = params.fingerprints([p])
+    assert params.unchanged(prints)
+    p.data = torch.zeros(3)
+    assert not params.unchanged(prints)
 
 
 def test_state_dict_round_trip_and_names():
