@@ -241,7 +241,14 @@ class _GDNScanMany(torch.autograd.Function):
 
 class _ReadBox:
     """What a scan forward without a query hands to its late read, and what
-    the read's backward hands back to the scan's backward."""
+    the read's backward hands back to the scan's backward.
+
+    The box never holds a tensor across a forward/backward gap: the scan's
+    forward leaves its inputs and intermediates here (args, saved), the
+    read's forward takes them into its own saved tensors and empties the box,
+    and the read's backward leaves the query, its normalised forms and dO
+    here for the scan's backward, which releases them.  So activation
+    checkpointing, which drops and recomputes saved tensors, frees all of it."""
 
     def __init__(self):
         self.args = self.saved = None
@@ -260,10 +267,11 @@ class _GDNRead(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, token, box):
         lib = _lib.load()
-        if box.q is not None:
+        if box.args is None:
             raise ValueError("gdn_scan_deferred: the read of a scan can be taken once")
         k, v, g, beta, s0f, chunk, offset, nch = box.args
-        kn, w, u, delta, tri, gam, bet, states, final, *frags = box.saved
+        inter = box.saved
+        kn, w, u, delta, tri, gam, bet, states, final, *frags = inter
         _in_use_here(q, k, v, g, beta, s0f, kn, delta, gam, states, frags[3])
         bsz, tokens, heads, kd = k.shape
         vd = v.shape[-1]
@@ -273,30 +281,34 @@ class _GDNRead(torch.autograd.Function):
         qcol = torch.empty(chunks * ((kd + 31) // 32) * 4 * 64 * 8, device=dev, dtype=torch.bfloat16)
         out = torch.empty(bsz, tokens, heads, vd, device=dev, dtype=k.dtype)
         prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
-        saved = _read_saved(box, qn, qcol)
+        saved = _read_saved(inter, qn, qcol)
         _lib.check(lib.gpa_gdn_read(prob, saved, _lib.operand(out), _lib.stream_handle(dev)), "gpa_gdn_read")
-        box.q, box.qn, box.qcol = q, qn, qcol
-        ctx.box = box
+        ctx.box, ctx.geom = box, (chunk, offset)
+        ctx.save_for_backward(q, qn, qcol, k, v, g, beta, s0f, *inter)
+        box.args = box.saved = None
         return out
 
     @staticmethod
     def backward(ctx, dout):
         lib = _lib.load()
         box = ctx.box
-        k, v, g, beta, s0f, chunk, offset, nch = box.args
-        q = box.q
+        q, qn, qcol, k, v, g, beta, s0f, *inter = ctx.saved_tensors
+        chunk, offset = ctx.geom
         dout = dout.to(k.dtype).contiguous()
         dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
         prob = _problem(q, k, v, g, beta, s0f, chunk, offset)
-        saved = _read_saved(box, box.qn, box.qcol)
+        saved = _read_saved(inter, qn, qcol)
         _lib.check(lib.gpa_gdn_read_backward(prob, saved, _lib.operand(dout), _lib.operand(dq),
                                              _lib.stream_handle(q.device)), "gpa_gdn_read_backward")
-        box.dout = dout
+        # the scan's backward takes the read's gradient as its own read
+        box.q, box.qn, box.qcol, box.dout = q, qn, qcol, dout
         return dq.to(q.dtype), torch.zeros(1, device=q.device), None
 
 
-def _read_saved(box, qn, qcol):
-    kn, w, u, delta, tri, gam, bet, states, final, *frags = box.saved
+def _read_saved(inter, qn, qcol):
+    """The scan's saved intermediates (kn, w, u, delta, tri, gam, bet,
+    states, final, wrow, wcol, krow, kcol, qcol) with the read's qn and qcol."""
+    kn, w, u, delta, tri, gam, bet, states, final, *frags = inter
     frags = list(frags)
     frags[4] = qcol
     return _lib.Saved(*(_ptr(t) for t in (kn, qn, w, u, delta, tri, gam, bet, states, final, *frags)))

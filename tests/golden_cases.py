@@ -22,8 +22,8 @@ DTYPES = {"float32": torch.float32, "float64": torch.float64, "bfloat16": torch.
 
 
 def names():
-    """The DenseGPA fixtures (operator fixtures start with "ops_")."""
-    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith("ops_"))
+    """The DenseGPA fixtures (operator fixtures start with "ops_", LM fixtures with "lm_")."""
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith(("ops_", "lm_")))
 
 
 def ops_names(prefix: str):

@@ -1,0 +1,265 @@
+"""The LM shell (gpa_amd.lm) on the GPU: every attention layer is a HIP DenseGPA core.
+
+* The reference-written tiny checkpoint (tests/golden/lm_tiny, float32): loss
+  and every parameter gradient, logits, a cached prefill with one-token and
+  multi-token continuations and every cache tensor, and the keep_rope
+  variant, against the reference's numbers (tolerance 1e-4).
+* Checkpointed training gives the gradients of plain training.
+* bfloat16 attention at reduced config-5 widths (2 layers, hidden 256, 2
+  query / 1 KV heads of width 128, slots (128,128,128,256), chunk 64, the LM
+  flag set) against the LM oracle at a perturbed parameter point: loss,
+  logits and every parameter gradient (2e-2), and cached decode.
+* Config 5 at full size (tests at the end, long): a T=8192 training step with
+  AdamW, a 4096-token prefill split into cached calls, and greedy decode.
+"""
+import copy
+
+import pytest
+import torch
+
+from gpa_amd.lm import GPALMConfig, GPALMForCausalLM
+from gpa_amd.state import tensors
+from oracle.lm import OracleLM
+from tests.lm_cases import CHECKPOINT, PIECES, LMCase, perturb
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel(a, b, floor=0.):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / max(b.norm().item(), floor, 1e-30)).item()
+
+
+def test_lm_matches_the_reference_checkpoint_numbers():
+    print("LM: tiny reference checkpoint, float32", flush=True)
+    case = LMCase()
+    model = GPALMForCausalLM.from_pretrained(CHECKPOINT, attention_dtype=None).to(DEV)
+    ids = case.ids.to(DEV)
+    model.train()
+    out = model(ids, labels=ids, use_cache=False)
+    out.loss.backward()
+    errors = [case.compare("train/loss", out.loss, 1e-4)]
+    atol = 1e-3 * 1e-4 * case.grad_scale()
+    assert [n for n, p in model.named_parameters() if p.grad is not None] == case.grad_names
+    errors += [case.compare("train/grad/" + n, p.grad, 1e-4, atol) for n, p in model.named_parameters()
+               if p.grad is not None]
+    model.eval()
+    with torch.no_grad():
+        errors.append(case.compare("logits", model(ids, use_cache=False).logits, 1e-4))
+        cache = None
+        for n, (lo, hi) in enumerate(PIECES):
+            res = model(ids[:, lo:hi], past_key_values=cache)
+            cache = res.past_key_values
+            errors.append(case.compare(f"cache/logits{n}", res.logits, 1e-4))
+        assert cache.seen_tokens == int(case.z["full/cache/seen"])
+        for i, mem in enumerate(cache.layers):
+            errors += [case.compare(f"cache/layer{i}/state{n:03d}", t, 1e-4) for n, t in enumerate(tensors(mem.state))]
+            errors += [case.compare(f"cache/layer{i}/ptail", mem.projected_tail, 1e-4),
+                       case.compare(f"cache/layer{i}/ctail", mem.control_tail, 1e-4)]
+        rope = GPALMForCausalLM.from_pretrained(CHECKPOINT, attention_dtype=None, keep_rope=True).to(DEV).eval()
+        errors.append(case.compare("rope/logits", rope(ids, use_cache=False).logits, 1e-4))
+    errors = [e for e in errors if e]
+    assert not errors, errors
+
+
+def test_checkpointed_training_equals_plain_training():
+    print("LM: checkpointed vs plain training", flush=True)
+    grads = []
+    for ckpt in (False, True):
+        model = GPALMForCausalLM.from_pretrained(CHECKPOINT).to(DEV).train()
+        if ckpt:
+            model.gradient_checkpointing_enable()
+        ids = LMCase().ids.to(DEV)
+        loss = model(ids, labels=ids).loss
+        loss.backward()
+        grads.append([loss] + [p.grad for p in model.parameters()])
+    for a, b in zip(*grads):
+        if a is None or b is None:  # moment_gain: read only by positional_mode="moments"
+            assert a is None and b is None
+            continue
+        assert _rel(a, b) < 1e-5
+
+
+C5_SMALL = dict(vocab_size=512, hidden_size=256, intermediate_size=384, num_hidden_layers=2, num_attention_heads=2,
+                num_key_value_heads=1, head_dim=128, gpa=dict(slots=(128, 128, 128, 256), chunk_size=64),
+                attention_dtype="bfloat16", tie_word_embeddings=True, loss_chunk_size=48)
+
+
+def _small_pair(seed=3):
+    torch.manual_seed(seed)
+    model = GPALMForCausalLM(GPALMConfig(**C5_SMALL))
+    perturb(model, seed + 1)
+    ref = copy.deepcopy(model)
+    return model.to(DEV), ref
+
+
+def _train(model, ids, oracle_dtype=None):
+    """(loss, {name: grad}) of one training forward+backward: the HIP model
+    when oracle_dtype is None, else the oracle on a CPU copy."""
+    if oracle_dtype is None:
+        model.train()
+        loss = model(ids.to(DEV), labels=ids.to(DEV)).loss
+    else:
+        loss = OracleLM(model, attention_dtype=oracle_dtype)(ids, labels=ids)[0]
+    loss.backward()
+    return loss, {n: p.grad for n, p in model.named_parameters() if p.grad is not None}
+
+
+def test_lm_at_reduced_config5_widths_matches_the_oracle():
+    """Reduced config-5 widths at a perturbed parameter point.  float32
+    attention: loss and logits against the oracle at 1e-4, every parameter
+    gradient at 2e-4 (layer 0's gradients pass through the backward of both
+    GPA cores, each held to 1e-4 by the module tests; roundoff floor 1e-3 of
+    the largest gradient, which no prefix gradient may need).  bfloat16 attention: loss and logits at 2e-2.  The bf16
+    gradients of this LM are ill-conditioned in the reference algorithm
+    itself: the oracle's bf16 gradients sit 18-40 % from its float32 ones, up
+    to 270 % for per-head scalars whose gradient is a sum over tokens with
+    heavy cancellation.  So the bf16 gradients are held to the float32 oracle
+    by the reference's own bf16 error: the whole gradient vector within 1.25x
+    of the oracle's bf16 error (+1e-2), each parameter within 3x (or 5e-2)."""
+    print("LM: reduced config-5 widths, fp32 and bf16 attention, vs oracle", flush=True)
+    model, ref = _small_pair()
+    g = torch.Generator().manual_seed(11)
+    ids = torch.randint(0, C5_SMALL["vocab_size"], (1, 130), generator=g)
+    results = {}
+    for label, dtype in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        hip, cpu = copy.deepcopy(model), copy.deepcopy(ref)
+        for a, b in zip(hip.model.layers, cpu.model.layers):
+            a.self_attn.attention_dtype = b.self_attn.attention_dtype = dtype
+        results[label] = (_train(hip, ids), _train(cpu, ids, dtype))
+        hip.eval()
+        with torch.no_grad():
+            logits = hip(ids.to(DEV), use_cache=False).logits
+            ref_logits = OracleLM(cpu, attention_dtype=dtype)(ids)[1]
+        assert _rel(logits, ref_logits) < (1e-4 if dtype == torch.float32 else 2e-2), label
+    (loss, grads), (ref_loss, ref_grads) = results["f32"]
+    assert _rel(loss, ref_loss) < 1e-4 and set(grads) == set(ref_grads)
+    top = max(x.norm().item() for x in ref_grads.values())
+    errors, floored = {}, []
+    for n, r in ref_grads.items():
+        errors[n] = _rel(grads[n], r, floor=1e-3 * top)
+        if _rel(grads[n], r) > 2e-4 >= errors[n]:
+            floored.append(n)
+    print("f32 worst", max(errors.items(), key=lambda kv: kv[1]), "floored", floored or "none")
+    assert not {k: v for k, v in errors.items() if v > 2e-4}
+    assert not [n for n in floored if "prefix" in n], floored
+    (loss16, grads16), (ref_loss16, ref_grads16) = results["bf16"]
+    assert _rel(loss16, ref_loss16) < 2e-2
+    names = list(ref_grads)
+    flat = lambda g: torch.cat([g[n].detach().double().cpu().reshape(-1) for n in names])  # noqa: E731
+    ours_all, theirs_all = _rel(flat(grads16), flat(ref_grads)), _rel(flat(ref_grads16), flat(ref_grads))
+    print(f"bf16 gradient vector vs float32 oracle: ours {ours_all:.3e}, the oracle's bf16 {theirs_all:.3e}",
+          flush=True)
+    assert ours_all <= 1.25 * theirs_all + 1e-2
+    worse = {}
+    for n, truth in ref_grads.items():
+        ours, theirs = _rel(grads16[n], truth), _rel(ref_grads16[n], truth)
+        if ours > max(3 * theirs, 5e-2):
+            worse[n] = (ours, theirs)
+    assert not worse, worse
+
+
+def test_lm_cached_decode_matches_the_oracle():
+    """A 67-token prefill and three one-token calls through the cache at
+    reduced config-5 widths.  float32 attention: logits at every call, the
+    convolution tails and every GPA cache tensor against the oracle's cached
+    calls at 1e-4.  bfloat16 attention: the reference's own bf16 logits sit
+    2-4 % from its float32 ones here, so ours must be as close to the float32
+    oracle as the oracle's bf16 logits are (1.25x + 1e-2), and the cache
+    states within 2e-2 of the bf16 oracle's."""
+    print("LM: reduced config-5 widths, cached prefill + decode vs oracle", flush=True)
+    model, ref = _small_pair(5)
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, C5_SMALL["vocab_size"], (2, 70), generator=g)
+    pieces = ((0, 67), (67, 68), (68, 69), (69, 70))
+    logits = {}
+    for label, dtype in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        hip, cpu = copy.deepcopy(model).eval(), copy.deepcopy(ref)
+        for a, b in zip(hip.model.layers, cpu.model.layers):
+            a.self_attn.attention_dtype = b.self_attn.attention_dtype = dtype
+        run = OracleLM(cpu, attention_dtype=dtype)
+        cache, ref_cache, got, want = None, None, [], []
+        with torch.no_grad():
+            for lo, hi in pieces:
+                res = hip(ids[:, lo:hi].to(DEV), past_key_values=cache)
+                cache = res.past_key_values
+                _, ref_logits, ref_cache = run(ids[:, lo:hi], cache=ref_cache)
+                got.append(res.logits)
+                want.append(ref_logits)
+        logits[label] = (got, want)
+        tol = 1e-4 if dtype == torch.float32 else 2e-2
+        assert cache.seen_tokens == ref_cache["seen"] == 70
+        for mem, (state, ptail, ctail) in zip(cache.layers, ref_cache["layers"]):
+            # the tails are projection outputs (GPU and CPU float32 GEMMs round
+            # differently); past layer 0 they carry the earlier cores' outputs
+            tail_tol = 1e-5 if dtype == torch.float32 else tol
+            assert _rel(mem.projected_tail, ptail) < tail_tol and _rel(mem.control_tail, ctail) < tail_tol, label
+            for a, b in zip(tensors(mem.state), tensors(state)):
+                assert _rel(a, b) < tol, label
+    got32, truth = logits["f32"]
+    for a, b in zip(got32, truth):
+        assert _rel(a, b) < 1e-4
+    got16, ref16 = logits["bf16"]
+    for n, (ours, theirs, t) in enumerate(zip(got16, ref16, truth)):
+        e_ours, e_theirs = _rel(ours, t), _rel(theirs, t)
+        print(f"call {n}: bf16 logits vs float32 oracle: ours {e_ours:.3e}, the oracle's bf16 {e_theirs:.3e}")
+        assert e_ours <= 1.25 * e_theirs + 1e-2, n
+
+
+def test_c5_full_size_training_step_prefill_and_greedy_decode():
+    """Config 5 at full size: the Qwen3-0.6B-architecture all-GPA LM (28
+    layers, hidden 1024, 16 query / 8 KV heads of width 128, SwiGLU 3072,
+    vocab 151936, tied embeddings), GPA slots (128,128,128,256), random init,
+    float32 master weights under bfloat16 autocast.  One B=1, T=8192 training
+    step (per-layer checkpointing, chunked CE, AdamW) gives a finite loss near
+    ln(vocab), finite gradients for every parameter the loss reaches, and
+    moves the weights; a 4096-token prefill split into two cached calls gives
+    the whole prefill's cache and next-token logits; greedy decode continues
+    from it with finite logits."""
+    import math
+    from gpa_amd.lm import GPALMCache
+    print("C5 full size: T=8192 training step with AdamW", flush=True)
+    # a leak shows as an allocator OOM with headroom left for the HIP runtime
+    torch.cuda.set_per_process_memory_fraction(0.8)
+    torch.cuda.reset_peak_memory_stats()
+    torch.manual_seed(0)
+    model = GPALMForCausalLM(GPALMConfig(gpa=dict(slots=(128, 128, 128, 256)))).to(DEV)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    model.gradient_checkpointing_enable()
+    model.train()
+    g = torch.Generator(device=DEV).manual_seed(1)
+    ids = torch.randint(0, model.config.vocab_size, (1, 8192), device=DEV, generator=g)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss = model(ids, labels=ids).loss
+    loss.backward()
+    assert torch.isfinite(loss) and abs(loss.item() - math.log(model.config.vocab_size)) < 1.
+    for n, p in model.named_parameters():
+        if n.endswith("moment_gain"):
+            continue
+        assert p.grad is not None and torch.isfinite(p.grad).all(), n
+    before = model.model.layers[0].self_attn.gpa.relation_prefix[0].detach().clone()
+    opt.step()
+    opt.zero_grad(set_to_none=True)
+    assert not torch.equal(before, model.model.layers[0].self_attn.gpa.relation_prefix[0])
+    print(f"C5 full size: peak {torch.cuda.max_memory_allocated() / 2**30:.1f} GiB", flush=True)
+    del opt
+    print("C5 full size: 4096-token prefill (whole vs 2048 + 2048) and greedy decode", flush=True)
+    model.eval()
+    prompt = torch.randint(0, model.config.vocab_size, (1, 4096), device=DEV, generator=g)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        whole = model(prompt, logits_to_keep=1)
+        split = model(prompt[:, :2048])
+        split = model(prompt[:, 2048:], past_key_values=split.past_key_values, logits_to_keep=1)
+        assert _rel(split.logits, whole.logits) < 2e-2
+        for a, b in zip(split.past_key_values.layers, whole.past_key_values.layers):
+            assert _rel(a.projected_tail, b.projected_tail) < 1e-2
+            for x, y in zip(tensors(a.state), tensors(b.state)):
+                assert _rel(x, y) < 1e-2
+        assert isinstance(whole.past_key_values, GPALMCache) and whole.past_key_values.seen_tokens == 4096
+        del whole, split
+        tokens, cache = model.generate_greedy(prompt, 16, prefill_chunk=2048)
+        # the last new token is returned, not yet fed
+        assert tokens.shape == (1, 16) and cache.seen_tokens == 4096 + 15
+        assert ((tokens >= 0) & (tokens < model.config.vocab_size)).all()
+    torch.cuda.set_per_process_memory_fraction(1.0)

@@ -98,3 +98,42 @@ def test_oracle_two_stage_matches_reference(name):
         if rel > g_rtol:
             errors.append(f"grad/{n}: {rel:.3e}")
     assert not errors, errors
+
+
+def test_oracle_lm_matches_the_reference_lm():
+    """oracle.lm.OracleLM (the all-GPA Qwen LM, src/gpa/hf_qwen.py) on the
+    reference-written tiny checkpoint: training loss and every parameter
+    gradient, full logits, a cached prefill with one-token and multi-token
+    continuations (logits and every cache tensor), and the keep_rope variant,
+    against the reference's numbers (float32)."""
+    from gpa_amd.lm import GPALMForCausalLM
+    from gpa_amd.state import tensors
+    from oracle.lm import OracleLM
+    from tests.lm_cases import CHECKPOINT, PIECES, LMCase
+    case = LMCase()
+    model = GPALMForCausalLM.from_pretrained(CHECKPOINT, attention_dtype=None)
+    ids = case.ids
+    run = OracleLM(model)
+    loss, _, _ = run(ids, labels=ids)
+    loss.backward()
+    errors = [case.compare("train/loss", loss, 2e-5)]
+    atol = 1e-3 * 2e-5 * case.grad_scale()
+    got = [n for n, p in model.named_parameters() if p.grad is not None]
+    assert got == case.grad_names
+    errors += [case.compare("train/grad/" + n, p.grad, 2e-5, atol) for n, p in model.named_parameters()
+               if p.grad is not None]
+    with torch.no_grad():
+        errors.append(case.compare("logits", run(ids)[1], 2e-5))
+        cache = None
+        for n, (lo, hi) in enumerate(PIECES):
+            _, logits, cache = run(ids[:, lo:hi], cache=cache)
+            errors.append(case.compare(f"cache/logits{n}", logits, 2e-5))
+        assert cache["seen"] == int(case.z["full/cache/seen"])
+        for i, (state, ptail, ctail) in enumerate(cache["layers"]):
+            errors += [case.compare(f"cache/layer{i}/state{n:03d}", t, 2e-5) for n, t in enumerate(tensors(state))]
+            errors += [case.compare(f"cache/layer{i}/ptail", ptail, 2e-5),
+                       case.compare(f"cache/layer{i}/ctail", ctail, 2e-5)]
+        rope_model = GPALMForCausalLM.from_pretrained(CHECKPOINT, attention_dtype=None, keep_rope=True)
+        errors.append(case.compare("rope/logits", OracleLM(rope_model)(ids)[1], 2e-5))
+    errors = [e for e in errors if e]
+    assert not errors, errors
