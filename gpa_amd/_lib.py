@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 22
+ABI_VERSION = 23
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -89,13 +89,15 @@ class RouteProblem(ctypes.Structure):
                 ("q", Operand)] + \
                [(n, c_vp) for n in ("edge_weight", "gain", "mlp_gain", "up_t", "down_t", "rs_t", "qs_t",
                                     "up", "down", "rs", "qs")] + \
-               [("qo", Operand), ("route", Operand)] + [(n, c_vp) for n in ("r0", "h1", "hd")]
+               [("qo", Operand), ("route", Operand)] + [(n, c_vp) for n in ("r0", "h1", "hd")] + \
+               [("rsa", c_i32), ("balanced", c_i32), ("mix", c_vp), ("qr", c_vp), ("qdir", c_vp)]
 
 
 class RouteGrads(ctypes.Structure):
     _fields_ = [(n, Operand) for n in ("dqo", "droute", "dbase")] + \
                [("dmsg", Operand * ROUTE_MAX_INCOMING), ("dq", Operand)] + \
-               [(n, c_vp) for n in ("dh1", "dhd", "dqs", "hg", "partials")]
+               [(n, c_vp) for n in ("dh1", "dhd", "dqs", "hg", "partials")] + \
+               [("dqr", Operand), ("ddir", Operand), ("mix_partials", c_vp)]
 
 
 PRODUCT_ROWS = 4

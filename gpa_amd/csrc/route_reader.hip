@@ -516,13 +516,36 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
           A[row * lda + col] = r1;
           if (r < R) {
             shd[(int64_t)r * M + col] = from_f32<E>(hd);
-            route[rows.at(p.route, r, h) + col] = from_f32<E>(r1);
+            if (!p.rsa) route[rows.at(p.route, r, h) + col] = from_f32<E>(r1);
           }
         }
       }
     }
   }
   __syncthreads();
+
+  // ---- rsa_update: r1 <- round(r1 / clamp(sum |r1|, .25, 4)) in A and the route output
+  if (p.rsa) {
+    if (!(NW > RW && tid >= RNT)) {
+      const int row = tid >> 3, part = tid & 7, r = row0 + row;
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < RPER; ++i)
+        if (part + 8 * i < M) s += fabsf(A[row * lda + part + 8 * i]);
+      const float l = fminf(fmaxf(sum8(s), .25f), 4.f);
+      E* route = reinterpret_cast<E*>(p.route.ptr);
+#pragma unroll
+      for (int i = 0; i < RPER; ++i) {
+        const int m = part + 8 * i;
+        if (m < M) {
+          const float x = round_as<E>(A[row * lda + m] / l);
+          A[row * lda + m] = x;
+          if (r < R) route[rows.at(p.route, r, h) + m] = from_f32<E>(x);
+        }
+      }
+    }
+    __syncthreads();
+  }
 
   // ---- q -> Hs
   if (NW > RW && tid >= RNT) {
@@ -573,7 +596,12 @@ __device__ __forceinline__ void route_fwd_run(const gpa_route_problem& p, int h,
         const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
         if (col < M && r < R) {
           const float dir = round_as<E>(p.query_scale * round_as<E>(a4[i]));
-          qo[rows.at(p.qo, r, h) + col] = from_f32<E>(round_as<E>(round_as<E>(a3[i]) + dir));
+          if (p.balanced) {  // both halves saved; route_mix_fwd forms qo from their unit rows
+            reinterpret_cast<E*>(p.qr)[((int64_t)h * R + r) * M + col] = from_f32<E>(round_as<E>(a3[i]));
+            reinterpret_cast<E*>(p.qdir)[((int64_t)h * R + r) * M + col] = from_f32<E>(dir);
+          } else {
+            qo[rows.at(p.qo, r, h) + col] = from_f32<E>(round_as<E>(round_as<E>(a3[i]) + dir));
+          }
         }
       }
     }
@@ -620,6 +648,221 @@ __global__ __launch_bounds__(64 * RPACK_W) void route_fwd_pack(RoutePack pk) {
   const int pi = route_pack_entry(kp, p);
   const int local = (int)blockIdx.x - kp->wg0[pi], nt = kp->tiles[pi];
   route_fwd_run<bf16_t, true, RPACK_W>(p, local / nt, (local % nt) * RR);
+}
+
+// ---------------------------------------------------------------- rsa_update and balanced_bridge rows
+// The two reference flags that act on whole rows between the products (sums
+// over the M slots), as row kernels: 8 threads per row, the RR rows of one
+// head per workgroup (grid: row tiles x heads).  Products and sums whose
+// rounding the reference fixes are written with __fmul_rn / __fadd_rn.
+
+struct RowCtx {
+  int M, R, h, tile, row, part, r, rc;
+};
+__device__ __forceinline__ RowCtx row_ctx(const gpa_route_problem& p) {
+  const RouteTile t = route_tile();
+  const int R = p.batch * p.tokens, row = threadIdx.x >> 3, r = t.tile * RR + row;
+  return RowCtx{p.slots, R, t.h, t.tile, row, (int)threadIdx.x & 7, r, r < R ? r : R - 1};
+}
+
+// rsa_update forward (attention.py:251-253), in place on the route rows:
+// r1 <- round(r1 / clamp(sum |r1|, .25, 4)).  (The one-kernel reader does the
+// same in its LDS tile.)
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_rsa_fwd(gpa_route_problem p) {
+  const RowCtx c = row_ctx(p);
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, c.tile * RR, c.R, p.tokens);
+  E* route = reinterpret_cast<E*>(p.route.ptr) + rows.at(p.route, c.rc, c.h);
+  float x[RPER], s = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = c.part + 8 * i;
+    x[i] = m < c.M ? to_f32(route[m]) : 0.f;
+    s += fabsf(x[i]);
+  }
+  const float l = fminf(fmaxf(sum8(s), .25f), 4.f);
+  if (c.r < c.R) {
+#pragma unroll
+    for (int i = 0; i < RPER; ++i)
+      if (c.part + 8 * i < c.M) route[c.part + 8 * i] = from_f32<E>(round_as<E>(x[i] / l));
+  }
+}
+
+// One row's |x| = sqrt(sum x^2) over the thread's columns and its 7 partners.
+__device__ __forceinline__ float row_norm(const float (&x)[RPER]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) s += x[i] * x[i];
+  return sqrtf(sum8(s));
+}
+
+// balanced_bridge forward (attention.py:256-259):
+// qo = round(mix unit(qr) + (1 - mix) unit(qdir)), unit(x) = round(x / max(|x|, 1e-6)).
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_mix_fwd(gpa_route_problem p) {
+  const RowCtx c = row_ctx(p);
+  __shared__ int row_b[RR], row_t[RR];
+  const Rows rows = make_rows(row_b, row_t, c.tile * RR, c.R, p.tokens);
+  const int64_t o = ((int64_t)c.h * c.R + c.rc) * c.M;
+  const E* qr = reinterpret_cast<const E*>(p.qr) + o;
+  const E* qd = reinterpret_cast<const E*>(p.qdir) + o;
+  float a[RPER], b[RPER];
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = c.part + 8 * i;
+    a[i] = m < c.M ? to_f32(qr[m]) : 0.f;
+    b[i] = m < c.M ? to_f32(qd[m]) : 0.f;
+  }
+  const float na = fmaxf(row_norm(a), 1e-6f), nb = fmaxf(row_norm(b), 1e-6f);
+  const float mix = p.mix[c.h], omix = 1.f - mix;
+  E* qo = reinterpret_cast<E*>(p.qo.ptr) + rows.at(p.qo, c.rc, c.h);
+  if (c.r < c.R) {
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = c.part + 8 * i;
+      if (m < c.M) {
+        const float ua = round_as<E>(a[i] / na), ub = round_as<E>(b[i] / nb);
+        qo[m] = from_f32<E>(round_as<E>(__fadd_rn(__fmul_rn(mix, ua), __fmul_rn(omix, ub))));
+      }
+    }
+  }
+}
+
+// Gradient of unit(x) = x / c, c = max(|x|, eps), n = |x| (F.normalize's
+// autograd): dx = du / c + [n >= eps] (-sum(du x) / c^2) x / n.
+__device__ __forceinline__ void unit_bwd(const float (&x)[RPER], const float (&du)[RPER], float n, float (&dx)[RPER]) {
+  const float cl = fmaxf(n, 1e-6f);
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) t += du[i] * x[i];
+  t = sum8(t);
+  const float dn = n >= 1e-6f ? -t / (cl * cl) : 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) dx[i] = du[i] / cl + (n > 0.f ? dn * x[i] / n : 0.f);
+}
+
+// balanced_bridge backward, before the products: from dqo, the gradients of
+// qr and qdir (rounded to E) and the block's sum of dqo . (unit(qr) - unit(qdir))
+// (d mix; the reference's d mix - d (1 - mix)).
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_mix_bwd(gpa_route_problem p, gpa_route_grads g) {
+  const RowCtx c = row_ctx(p);
+  __shared__ int row_b[RR], row_t[RR];
+  __shared__ float red[RW];
+  const Rows rows = make_rows(row_b, row_t, c.tile * RR, c.R, p.tokens);
+  const int64_t o = ((int64_t)c.h * c.R + c.rc) * c.M;
+  const E* qr = reinterpret_cast<const E*>(p.qr) + o;
+  const E* qd = reinterpret_cast<const E*>(p.qdir) + o;
+  const E* dqo = reinterpret_cast<const E*>(g.dqo.ptr) + rows.at(g.dqo, c.rc, c.h);
+  float a[RPER], b[RPER], d[RPER];
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = c.part + 8 * i;
+    a[i] = m < c.M ? to_f32(qr[m]) : 0.f;
+    b[i] = m < c.M ? to_f32(qd[m]) : 0.f;
+    d[i] = m < c.M ? to_f32(dqo[m]) : 0.f;
+  }
+  const float na = row_norm(a), nb = row_norm(b);
+  const float ca = fmaxf(na, 1e-6f), cb = fmaxf(nb, 1e-6f);
+  const float mix = p.mix[c.h], omix = 1.f - mix;
+  float dua[RPER], dub[RPER], part = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const bool on = c.part + 8 * i < c.M;
+    const float ua = on ? round_as<E>(a[i] / ca) : 0.f, ub = on ? round_as<E>(b[i] / cb) : 0.f;
+    part += d[i] * ua - d[i] * ub;
+    dua[i] = on ? round_as<E>(__fmul_rn(d[i], mix)) : 0.f;
+    dub[i] = on ? round_as<E>(__fmul_rn(d[i], omix)) : 0.f;
+  }
+  float dxa[RPER], dxb[RPER];
+  unit_bwd(a, dua, na, dxa);
+  unit_bwd(b, dub, nb, dxb);
+  if (c.r < c.R) {
+    E* gq = reinterpret_cast<E*>(g.dqr.ptr) + rows.at(g.dqr, c.r, c.h);
+    E* gd = reinterpret_cast<E*>(g.ddir.ptr) + rows.at(g.ddir, c.r, c.h);
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = c.part + 8 * i;
+      if (m < c.M) {
+        gq[m] = from_f32<E>(round_as<E>(dxa[i]));
+        gd[m] = from_f32<E>(round_as<E>(dxb[i]));
+      }
+    }
+  } else {
+    part = 0.f;
+  }
+  for (int k = 32; k >= 1; k >>= 1) part += __shfl_xor(part, k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) g.mix_partials[(int64_t)c.tile * p.heads + c.h] = red[0] + red[1] + red[2] + red[3];
+}
+
+// rsa_update backward of one row, given d r1' (the gradient of the rescaled
+// row) and r1: d r1 = round(d r1' / l + [.25 <= s <= 4] (-sum(d r1' r1) / l^2) sign(r1)),
+// s = sum |r1|, l = clamp(s, .25, 4).
+template <typename E>
+__device__ __forceinline__ void rsa_bwd_row(const float (&r1)[RPER], const float (&d)[RPER], int M, int part,
+                                            float (&out)[RPER]) {
+  float s = 0.f, t = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    s += fabsf(r1[i]);
+    t += d[i] * r1[i];
+  }
+  s = sum8(s);
+  t = sum8(t);
+  const float l = fminf(fmaxf(s, .25f), 4.f);
+  const float dl = (s >= .25f && s <= 4.f) ? -t / (l * l) : 0.f;
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const float sg = r1[i] > 0.f ? 1.f : (r1[i] < 0.f ? -1.f : 0.f);
+    out[i] = part + 8 * i < M ? round_as<E>(d[i] / l + dl * sg) : 0.f;
+  }
+}
+
+// rsa_update backward of the tiled path: d r1' (float32 d base rows, written
+// by the d r1 product) -> d r1 in place, d hd = round(mlp_gain d r1), and the
+// block's sum of d r1 . hd (partial slot 0, d mlp_gain).  r1 is recomputed
+// from the saved r0 and hd rows.
+template <typename E>
+__global__ __launch_bounds__(RNT) void route_rsa_bwd(gpa_route_problem p, gpa_route_grads g) {
+  const RowCtx c = row_ctx(p);
+  __shared__ int row_b[RR], row_t[RR];
+  __shared__ float red[RW];
+  const Rows rows = make_rows(row_b, row_t, c.tile * RR, c.R, p.tokens);
+  const int64_t o = ((int64_t)c.h * c.R + c.rc) * c.M;
+  const E* r0 = reinterpret_cast<const E*>(p.r0) + o;
+  const E* hd = reinterpret_cast<const E*>(p.hd) + o;
+  float* dr = reinterpret_cast<float*>(g.dbase.ptr) + rows.at(g.dbase, c.rc, c.h);
+  const float gm = p.mlp_gain[c.h];
+  float r1[RPER], hv[RPER], d[RPER], d1[RPER];
+#pragma unroll
+  for (int i = 0; i < RPER; ++i) {
+    const int m = c.part + 8 * i;
+    hv[i] = m < c.M ? to_f32(hd[m]) : 0.f;
+    r1[i] = m < c.M ? round_as<E>(to_f32(r0[m]) + gm * hv[i]) : 0.f;
+    d[i] = m < c.M ? dr[m] : 0.f;
+  }
+  rsa_bwd_row<E>(r1, d, c.M, c.part, d1);
+  float part = 0.f;
+  if (c.r < c.R) {
+    E* dhd = reinterpret_cast<E*>(g.dhd) + ((int64_t)c.h * c.R + c.r) * c.M;
+#pragma unroll
+    for (int i = 0; i < RPER; ++i) {
+      const int m = c.part + 8 * i;
+      if (m < c.M) {
+        dr[m] = d1[i];
+        dhd[m] = from_f32<E>(round_as<E>(gm * d1[i]));
+        part += d1[i] * hv[i];
+      }
+    }
+  }
+  for (int k = 32; k >= 1; k >>= 1) part += __shfl_xor(part, k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    g.partials[((int64_t)c.tile * p.heads + c.h) * (2 + p.incoming)] = red[0] + red[1] + red[2] + red[3];
 }
 
 // ---------------------------------------------------------------- tiled products
@@ -914,15 +1157,55 @@ struct EpiQo {
   __device__ void block_sum(int, int, float) const {}
 };
 
+// balanced_bridge: qr = round(r1 W_rs) and qdir = round(query_scale round(q W_qs))
+// saved separately (rows [H][R][M]), each by a product of its own;
+// route_mix_fwd forms qo from them.
+struct EpiQr {
+  static constexpr bool kPart = false;
+  bf16_t* qr;
+  int64_t sh, sr;
+  typedef int Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return a; }
+  __device__ Pre load(int, int, int) const { return 0; }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre, float) const {
+    st8(qr + h * sh + r * sr + c, v);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+struct EpiQdir {
+  static constexpr bool kPart = false;
+  bf16_t* qdir;
+  int64_t sh, sr;
+  float query_scale;
+  typedef int Pre;
+  __device__ float head(int) const { return 0.f; }
+  __device__ float combine(float a, float) const { return round_as<bf16_t>(query_scale * round_as<bf16_t>(a)); }
+  __device__ Pre load(int, int, int) const { return 0; }
+  __device__ float store(int h, int r, int c, const float (&v)[8], Pre, float) const {
+    st8(qdir + h * sh + r * sr + c, v);
+    return 0.f;
+  }
+  __device__ void block_sum(int, int, float) const {}
+};
+
 // Backward.  d r1 = round(dqo W_rs^T) (+ d route, rounded) is kept in the
 // float32 d base buffer until the row kernel overwrites it; d hd = round(mlp_gain
 // d r1) and round(query_scale dqo) are saved rows; each 32-row block's
 // sum of d r1 . hd is d mlp_gain's partial.
+// With balanced_bridge the W_rs product reads the gradient of qr and the
+// q W_qs gradient comes from that of qdir (dqo below, rows [H][R][M]).  With
+// rsa_update the product's result is the gradient of the rescaled row: it is
+// stored alone (d r1', rounded) and route_rsa_bwd finishes d r1, d hd and the
+// partial sums.
 struct EpiDr1 {
   static constexpr bool kPart = true;
   const bf16_t* dqo;
   const bf16_t* droute;  // may be null
-  int64_t io_sh, io_sr;  // dqo and d route rows ([B,T,H,M], uniformly strided)
+  int64_t io_sh, io_sr;  // d route rows ([B,T,H,M], uniformly strided)
+  int64_t dq_sh, dq_sr;  // dqo rows
+  int rsa;
   const bf16_t* hd;
   bf16_t *dhd, *dqs;
   int64_t sh, sr;        // hd, dhd, dqs: [H][R][M]
@@ -938,10 +1221,10 @@ struct EpiDr1 {
   __device__ float head(int h) const { return mlp_gain[h]; }
   __device__ float combine(float a, float) const { return round_as<bf16_t>(a); }
   __device__ Pre load(int h, int r, int c) const {
-    const int64_t io = h * io_sh + r * io_sr + c;
     const uint4 z = make_uint4(0, 0, 0, 0);
-    return Pre{droute ? *reinterpret_cast<const uint4*>(droute + io) : z,
-               *reinterpret_cast<const uint4*>(hd + h * sh + r * sr + c), *reinterpret_cast<const uint4*>(dqo + io)};
+    return Pre{droute ? *reinterpret_cast<const uint4*>(droute + h * io_sh + r * io_sr + c) : z,
+               *reinterpret_cast<const uint4*>(hd + h * sh + r * sr + c),
+               *reinterpret_cast<const uint4*>(dqo + h * dq_sh + r * dq_sr + c)};
   }
   __device__ float store(int h, int r, int c, const float (&v)[8], const Pre& x, float gm) const {
     float d[8], dro[8], hv[8], dq[8], dh[8];
@@ -957,10 +1240,10 @@ struct EpiDr1 {
       part += d[j] * hv[j];
     }
     const int64_t o = h * sh + r * sr + c;
-    st8(dhd + o, dh);
+    if (!rsa) st8(dhd + o, dh);
     st8(dqs + o, dq);
     st8(dr1 + h * dr_sh + r * dr_sr + c, d);
-    return part;
+    return rsa ? 0.f : part;
   }
   __device__ void block_sum(int h, int blk, float x) const { partials[((int64_t)blk * heads + h) * nparts] = x; }
 };
@@ -1092,15 +1375,16 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   E* gdqs = reinterpret_cast<E*>(g.dqs) + (int64_t)h * R * M;
   float part_mg = 0.f, part_gain = 0.f, part_w[GPA_ROUTE_MAX_INCOMING] = {0.f, 0.f, 0.f};
 
-  // ---- dqo -> G
+  // ---- dqo (balanced: the gradient of qr) -> G
+  const gpa_operand& d1src = p.balanced ? g.dqr : g.dqo;
   if constexpr (VEC) {
     const int c = 8 * (tid & 31), rsub = tid >> 5;
     uint4 dv[VPASS];
 #pragma unroll
     for (int i = 0; i < VPASS; ++i) {
       const int r = row0 + rsub + 8 * i;
-      dv[i] = (c < M && r < R) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(g.dqo.ptr) +
-                                                                  rows.at(g.dqo, r, h) + c)
+      dv[i] = (c < M && r < R) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(d1src.ptr) +
+                                                                  rows.at(d1src, r, h) + c)
                                : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
@@ -1116,7 +1400,7 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
     const bool valid = r < R;
-    const E* dqo = reinterpret_cast<const E*>(g.dqo.ptr) + rows.at(g.dqo, valid ? r : R - 1, h);
+    const E* dqo = reinterpret_cast<const E*>(d1src.ptr) + rows.at(d1src, valid ? r : R - 1, h);
 #pragma unroll
     for (int i = 0; i < RPER; ++i) {
       const int m = part + 8 * i;
@@ -1161,6 +1445,10 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
           if (droute && r < R) d = round_as<E>(d + dro[i]);
           if (r >= R) d = 0.f;
           dr1[s][i] = d;
+          if (p.rsa) {  // the gradient of the rescaled row; rsa_update's backward follows
+            A2[row * lda + col] = d;
+            continue;
+          }
           const float dhd = round_as<E>(gm * d);
           A2[row * lda + col] = dhd;
           if (r < R) {
@@ -1175,7 +1463,56 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
   }
   __syncthreads();
 
-  // ---- G <- round(query_scale dqo) (the gradient of q W_qs)
+  // ---- rsa_update: d r1 from d r1' (A2) and the recomputed r1; then d hd -> A2
+  if (p.rsa) {
+    {
+      const int row = tid >> 3, part = tid & 7, r = row0 + row, rc = r < R ? r : R - 1;
+      const E* r0v = reinterpret_cast<const E*>(p.r0) + ((int64_t)h * R + rc) * M;
+      const float gm = p.mlp_gain[h];
+      float r1[RPER], d[RPER], d1[RPER];
+#pragma unroll
+      for (int i = 0; i < RPER; ++i) {
+        const int m = part + 8 * i;
+        r1[i] = m < M ? round_as<E>(to_f32(r0v[m]) + gm * to_f32(shd[(int64_t)rc * M + m])) : 0.f;
+        d[i] = m < M ? A2[row * lda + m] : 0.f;
+      }
+      rsa_bwd_row<E>(r1, d, M, part, d1);
+#pragma unroll
+      for (int i = 0; i < RPER; ++i)
+        if (part + 8 * i < M) A2[row * lda + part + 8 * i] = r < R ? d1[i] : 0.f;
+    }
+    __syncthreads();
+    const float gm = p.mlp_gain[h];
+#pragma unroll
+    for (int s = 0; s < RTMAX; ++s) {
+      const int t = wave + RW * s;
+      if (t >= pad32(M) / 32) continue;
+      float hdv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int col = 32 * t + (lane & 31), r = row0 + acc_row(i, lane >> 5);
+        const bool ok = col < M && r < R;
+        hdv[i] = to_f32(shd[(int64_t)(ok ? r : row0) * M + (ok ? col : 0)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = acc_row(i, lane >> 5), col = 32 * t + (lane & 31), r = row0 + row;
+        if (col < M) {
+          const float d = A2[row * lda + col];
+          dr1[s][i] = d;
+          const float dhd = round_as<E>(gm * d);
+          A2[row * lda + col] = dhd;
+          if (r < R) {
+            part_mg += d * hdv[i];
+            gdhd[(int64_t)r * M + col] = from_f32<E>(dhd);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- G <- round(query_scale dqo) (the gradient of q W_qs; balanced: of ddir)
   if constexpr (VEC) {
     const int c = 8 * (tid & 31), rsub = tid >> 5;
     if (c < M) {
@@ -1183,8 +1520,16 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
       for (int i = 0; i < VPASS; ++i) {
         const int row = rsub + 8 * i, r = row0 + row;
         float* gr = &G[row * lda + c];
-        const f32x4 a = *reinterpret_cast<const f32x4*>(gr), b = *reinterpret_cast<const f32x4*>(gr + 4);
-        float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float x[8];
+        if (p.balanced) {
+          const uint4 u = r < R ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(g.ddir.ptr) +
+                                                                  rows.at(g.ddir, r, h) + c)
+                                : make_uint4(0, 0, 0, 0);
+          unpack_bf8(u, x);
+        } else {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(gr), b = *reinterpret_cast<const f32x4*>(gr + 4);
+          x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = round_as<E>(p.query_scale * x[e]);
         *reinterpret_cast<f32x4*>(gr) = f32x4{x[0], x[1], x[2], x[3]};
@@ -1194,11 +1539,14 @@ __global__ __launch_bounds__(RNT) void route_bwd(gpa_route_problem p, gpa_route_
     }
   } else {
     const int row = tid >> 3, part = tid & 7, r = row0 + row;
+    const E* ddir = p.balanced ? reinterpret_cast<const E*>(g.ddir.ptr) + rows.at(g.ddir, r < R ? r : R - 1, h)
+                               : nullptr;
 #pragma unroll
     for (int i = 0; i < RPER; ++i) {
       const int m = part + 8 * i;
       if (m < M) {
-        const float x = round_as<E>(p.query_scale * G[row * lda + m]);
+        const float src = ddir ? (r < R ? to_f32(ddir[m]) : 0.f) : G[row * lda + m];
+        const float x = round_as<E>(p.query_scale * src);
         G[row * lda + m] = x;
         if (r < R) gdqs[(int64_t)r * M + m] = from_f32<E>(x);
       }
@@ -1616,6 +1964,8 @@ int check_route(const gpa_route_problem* p) {
   for (int e = 0; e < p->incoming; ++e)
     if (!p->msg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message");
   if (!p->r0 || !p->h1 || !p->hd) return fail(GPA_HIP_EINVAL, "route: null saved rows");
+  if (p->balanced && (!p->mix || !p->qr || !p->qdir))
+    return fail(GPA_HIP_EINVAL, "route: balanced needs mix and the qr / qdir rows");
   return GPA_HIP_OK;
 }
 
@@ -1665,6 +2015,7 @@ bool route_vec(const gpa_route_problem& p) {
 }
 bool route_bwd_vec(const gpa_route_problem& p, const gpa_route_grads& g) {
   if (!route_vec(p) || !vec_rows(g.dqo, 8) || !vec_rows(g.dbase, 4)) return false;
+  if (p.balanced && (!vec_rows(g.dqr, 8) || !vec_rows(g.ddir, 8))) return false;
   for (int e = 0; e < p.incoming; ++e)
     if (!vec_rows(g.dmsg[e], 8)) return false;
   return true;
@@ -1713,11 +2064,25 @@ int route_forward_tiled(const gpa_route_problem& p, int64_t rs_q, int64_t rs_rou
   const Prod qs{RowOp{static_cast<const bf16_t*>(p.q.ptr), p.q.sh, rs_q}, static_cast<const bf16_t*>(p.qs_t),
                 pad32(M), pad16(Dk), Dk};
   const EpiQo eqo{static_cast<bf16_t*>(p.qo.ptr), p.qo.sh, rs_qo, p.query_scale};
-  if (M % 128 == 0) {
-    launch_gemm16<128, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
+  const dim3 rgrid((R + RR - 1) / RR, H);
+  if (M % 128 == 0) launch_gemm16<128, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
+  else launch_gemm16<64, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
+  // rsa_update: the route rows rescaled in place before the query product reads them
+  if (p.rsa) hipLaunchKernelGGL(route_rsa_fwd<bf16_t>, rgrid, dim3(RNT), 0, stream, p);
+  if (p.balanced) {
+    const EpiQr eqr{static_cast<bf16_t*>(p.qr), R64 * M, M};
+    const EpiQdir eqd{static_cast<bf16_t*>(p.qdir), R64 * M, M, p.query_scale};
+    if (M % 128 == 0) {
+      launch_gemm16<128, false, false>(rs, rs, GemmShape{R, M, H}, eqr, stream);
+      launch_gemm16<128, false, false>(qs, qs, GemmShape{R, M, H}, eqd, stream);
+    } else {
+      launch_gemm16<64, false, false>(rs, rs, GemmShape{R, M, H}, eqr, stream);
+      launch_gemm16<64, false, false>(qs, qs, GemmShape{R, M, H}, eqd, stream);
+    }
+    hipLaunchKernelGGL(route_mix_fwd<bf16_t>, rgrid, dim3(RNT), 0, stream, p);
+  } else if (M % 128 == 0) {
     launch_gemm16<128, false, true>(rs, qs, GemmShape{R, M, H}, eqo, stream);
   } else {
-    launch_gemm16<64, true, false>(down, down, GemmShape{R, M, H}, ehd, stream);
     launch_gemm16<64, false, true>(rs, qs, GemmShape{R, M, H}, eqo, stream);
   }
   return check_launch("gpa_route_forward");
@@ -1738,15 +2103,23 @@ int route_backward_tiled(const gpa_route_problem& p, const gpa_route_grads& g, i
   bf16_t* dqs = static_cast<bf16_t*>(g.dqs);
   bf16_t* dh1 = static_cast<bf16_t*>(g.dh1);
   float* dr = static_cast<float*>(g.dbase.ptr);
+  const dim3 rgrid((R + RR - 1) / RR, H);
+  // balanced_bridge: the gradients of qr and qdir (rows [H][R][M]) and d mix first
+  if (p.balanced) hipLaunchKernelGGL(route_mix_bwd<bf16_t>, rgrid, dim3(RNT), 0, stream, p, g);
+  const bf16_t* d_rs = p.balanced ? static_cast<const bf16_t*>(g.dqr.ptr) : dqo;
+  const bf16_t* d_qs = p.balanced ? static_cast<const bf16_t*>(g.ddir.ptr) : dqo;
+  const int64_t d_sh = p.balanced ? R64 * M : g.dqo.sh, d_sr = p.balanced ? M : rs_dqo;
   // d r1 (into d base), d hd, round(query_scale dqo), d mlp_gain partials: BN = N = M
-  const Prod prs{RowOp{dqo, g.dqo.sh, rs_dqo}, static_cast<const bf16_t*>(p.rs), pad32(M), pad16(M), M};
-  const EpiDr1 e1{dqo, static_cast<const bf16_t*>(g.droute.ptr), g.dqo.sh, rs_dqo,
+  const Prod prs{RowOp{d_rs, d_sh, d_sr}, static_cast<const bf16_t*>(p.rs), pad32(M), pad16(M), M};
+  const EpiDr1 e1{d_qs, static_cast<const bf16_t*>(g.droute.ptr), g.droute.sh, rs_dqo, d_sh, d_sr, p.rsa,
                   static_cast<const bf16_t*>(p.hd), dhd, dqs, R64 * M, M, dr, g.dbase.sh, rs_db,
                   p.mlp_gain, p.query_scale, g.partials, H, 2 + p.incoming};
   const GemmShape sm{R, M, H};
   if (M == 64) launch_gemm16<64, false, false>(prs, prs, sm, e1, stream);
   else if (M == 128) launch_gemm16<128, false, false>(prs, prs, sm, e1, stream);
   else launch_gemm16<256, false, false>(prs, prs, sm, e1, stream);
+  // rsa_update: d r1, d hd and the d mlp_gain partials from d r1'
+  if (p.rsa) hipLaunchKernelGGL(route_rsa_bwd<bf16_t>, rgrid, dim3(RNT), 0, stream, p, g);
   // d h1 = (d hd D^T) gelu'(h1), and round(gelu(h1))
   const Prod pdown{RowOp{dhd, R64 * M, M}, static_cast<const bf16_t*>(p.down), pad32(2 * M), pad16(M), M};
   const EpiDh1 e3{static_cast<const bf16_t*>(p.h1), dh1, static_cast<bf16_t*>(g.hg), R64 * 2 * M, 2 * M};
@@ -1790,6 +2163,12 @@ extern "C" int gpa_route_forward(const gpa_route_problem* problem, hipStream_t s
     if (int rc = set_lds(route_fwd<float, false>, lds)) return rc;
     hipLaunchKernelGGL((route_fwd<float, false>), grid, block, lds, stream, *problem);
   }
+  if (problem->balanced) {
+    if (problem->dtype == GPA_DTYPE_BF16)
+      hipLaunchKernelGGL(route_mix_fwd<bf16_t>, grid, block, 0, stream, *problem);
+    else
+      hipLaunchKernelGGL(route_mix_fwd<float>, grid, block, 0, stream, *problem);
+  }
   return check_launch("gpa_route_forward");
 }
 
@@ -1825,6 +2204,10 @@ extern "C" int gpa_route_forward_many(const gpa_route_problem* problems, int32_t
   }
   if (int rc = set_lds(route_fwd_pack, lds)) return rc;
   hipLaunchKernelGGL(route_fwd_pack, dim3(total), dim3(64 * RPACK_W), lds, stream, pk);
+  for (int i = 0; i < n; ++i)
+    if (problems[i].balanced)
+      hipLaunchKernelGGL(route_mix_fwd<bf16_t>, dim3(pk.tiles[i], problems[i].heads), dim3(RNT), 0, stream,
+                         problems[i]);
   return check_launch("gpa_route_forward_many");
 }
 
@@ -1837,6 +2220,8 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
     return fail(GPA_HIP_EINVAL, "route: null gradient buffer or backward weight");
   for (int e = 0; e < problem->incoming; ++e)
     if (!grads->dmsg[e].ptr) return fail(GPA_HIP_EINVAL, "route: null message gradient");
+  if (problem->balanced && (!grads->dqr.ptr || !grads->ddir.ptr || !grads->mix_partials))
+    return fail(GPA_HIP_EINVAL, "route: balanced needs the qr / qdir gradient rows and mix partials");
   {
     int64_t rs_q, rs_route, rs_qo, rs_dqo, rs_db, rs_dq;
     if (route_tiled(*problem, rs_q, rs_route, rs_qo) && route_bwd_vec(*problem, *grads) &&
@@ -1850,6 +2235,12 @@ extern "C" int gpa_route_backward(const gpa_route_problem* problem, const gpa_ro
   const int R = problem->batch * problem->tokens;
   const dim3 grid((R + RR - 1) / RR, problem->heads), block(RNT);
   const size_t lds = bwd_lds(*problem);
+  if (problem->balanced) {  // the gradients of qr and qdir, which route_bwd reads
+    if (problem->dtype == GPA_DTYPE_BF16)
+      hipLaunchKernelGGL(route_mix_bwd<bf16_t>, grid, block, 0, stream, *problem, *grads);
+    else
+      hipLaunchKernelGGL(route_mix_bwd<float>, grid, block, 0, stream, *problem, *grads);
+  }
   if (problem->dtype == GPA_DTYPE_BF16 && route_bwd_vec(*problem, *grads)) {
     if (int rc = set_lds(route_bwd<bf16_t, true>, lds)) return rc;
     hipLaunchKernelGGL((route_bwd<bf16_t, true>), grid, block, lds, stream, *problem, *grads);
@@ -1940,7 +2331,9 @@ extern "C" int gpa_route_weight_grads(const gpa_route_problem* problem, const gp
   const TnOperand dhd{grads->dhd, M, R64 * M, M};
   const TnOperand dqs{grads->dqs, M, R64 * M, M};
   const TnOperand r1{problem->route.ptr, rs_route, problem->route.sh, M};
-  const TnOperand dqo{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M};
+  // d W_rs = r1^T (the gradient of qr: dqo, or its balanced_bridge form)
+  const TnOperand dqo = problem->balanced ? TnOperand{grads->dqr.ptr, M, R64 * M, M}
+                                          : TnOperand{grads->dqo.ptr, rs_dqo, grads->dqo.sh, M};
   const TnOperand q{problem->q.ptr, rs_q, problem->q.sh, Dk};
   auto prod = [](const TnOperand& a, const TnOperand& b, float* c) {
     return TnProduct{a.ptr, a.rs, a.hs, a.width, b.ptr, b.rs, b.hs, b.width, c};

@@ -12,10 +12,13 @@ and the four weight matrices.  With `paper_product_read` (and
 `relation_marginal`) the relation read is the product form of
 attention.py:231-236 instead: `product_read` (gpa_product_read_forward /
 _backward) forms the base logits from the messages, and `route_reader` then
-runs with no incoming messages.  The schedule uses both where `supported`;
-with shared_query_center the query weight is W_qs + center^T / query_scale
-(attention.py:254-256), formed by the caller; the remaining flags
-(rsa_update, balanced_bridge, slot features) keep the device glue.
+runs with no incoming messages.  With shared_query_center the query weight is
+W_qs + center^T / query_scale (attention.py:254-256), formed by the caller.
+`rsa_update` rescales r1 by its clamped L1 norm before the query product
+(attention.py:251-253) and `balanced_bridge` mixes the unit rows of the two
+query halves with mix = .1 + .8 sigmoid(bridge_mix_raw) (attention.py:256-259),
+both inside the kernels, with gradients to mix.  Only non-linear slot
+features keep the device glue.
 """
 from __future__ import annotations
 
@@ -26,8 +29,7 @@ from . import _lib, params
 
 
 def supported(cfg, dtype: torch.dtype, slots: int) -> bool:
-    return (dtype in _lib.DTYPE_CODES and not cfg.rsa_update
-            and not cfg.balanced_bridge and cfg.slot_feature == "linear"
+    return (dtype in _lib.DTYPE_CODES and cfg.slot_feature == "linear"
             and slots <= _lib.ROUTE_MAX_WIDTH and cfg.key_dim <= _lib.ROUTE_MAX_WIDTH
             and cfg.levels - 1 <= _lib.ROUTE_MAX_INCOMING)
 
@@ -62,7 +64,14 @@ def _operand(t: Tensor | None) -> _lib.Operand:
     return _lib.operand(t)
 
 
-def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, saved):
+def _rows_operand(t: Tensor, tokens: int) -> _lib.Operand:
+    """A [H][R][M] row buffer addressed as [B,T,H,M] (r = b*T + t)."""
+    heads, rows, m = t.shape
+    return _lib.Operand(t.data_ptr(), tokens * m, m, rows * m)
+
+
+def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, saved, flags=(0, 0),
+             mix=None, halves=(None, None)):
     bsz, tokens, heads, dk = q.shape
     p = _lib.RouteProblem()
     p.batch, p.tokens, p.heads, p.slots, p.key_dim = bsz, tokens, heads, base.shape[-1], dk
@@ -76,13 +85,18 @@ def _problem(base, q, edge_w, gain, mlp_gain, msgs, query_scale, weights, outs, 
         setattr(p, name, w.data_ptr())
     p.qo, p.route = _operand(outs[0]), _operand(outs[1])
     p.r0, p.h1, p.hd = (t.data_ptr() for t in saved)
+    p.rsa, p.balanced = flags
+    if flags[1]:
+        p.mix, p.qr, p.qdir = mix.data_ptr(), halves[0].data_ptr(), halves[1].data_ptr()
     return p
 
 
-def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs):
+def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs, flags=(0, 0),
+                     mix=None):
     """The forward problem of one target level and every tensor it points
-    into: (problem, (base, q, edge_w, g, mg, msgs, packed weights), (qo,
-    route), saved rows).  The caller keeps these alive until the launch."""
+    into: (problem, (base, q, edge_w, g, mg, msgs, packed weights, mix), (qo,
+    route), saved rows (r0, h1, hd[, qr, qdir])).  The caller keeps these
+    alive until the launch."""
     dtype = q.dtype
     bsz, tokens, heads, _ = q.shape
     m = base.shape[-1]
@@ -99,31 +113,42 @@ def _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_sc
     saved = (torch.empty(heads, rows, m, device=q.device, dtype=dtype),
              torch.empty(heads, rows, 2 * m, device=q.device, dtype=dtype),
              torch.empty(heads, rows, m, device=q.device, dtype=dtype))
-    prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved)
-    return prob, (base, q, edge_w, g, mg, msgs, weights), (qo, route), saved
+    halves = (None, None)
+    if flags[1]:
+        mix = mix.detach().float().contiguous()
+        halves = tuple(torch.empty(heads, rows, m, device=q.device, dtype=dtype) for _ in range(2))
+    prob = _problem(base, q, edge_w, g, mg, msgs, query_scale, weights, (qo, route), saved, flags, mix, halves)
+    if flags[1]:
+        saved = saved + halves
+    return prob, (base, q, edge_w, g, mg, msgs, weights, mix), (qo, route), saved
 
 
 class _RouteReader(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs):
+    def forward(ctx, base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, flags, mix, *msgs):
         _lib.require_device(q)
         ctx.set_materialize_grads(False)
         lib = _lib.load()
-        prob, (base, q, edge_w, g, mg, msgs, packed), (qo, route), saved = _forward_problem(
-            base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs)
+        prob, (base, q, edge_w, g, mg, msgs, packed, mix_f), (qo, route), saved = _forward_problem(
+            base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs, flags, mix)
         _lib.check(lib.gpa_route_forward(prob, _lib.stream_handle(q.device)), "gpa_route_forward")
         del packed
         ctx.query_scale = query_scale
+        ctx.flags = flags
         ctx.n_in = len(msgs)
         ctx.param_dtypes = (edge_w.dtype if msgs else None, gain.dtype, mlp_gain.dtype,
-                            up.dtype, down.dtype, rs.dtype, qs.dtype)
-        ctx.save_for_backward(base, q, edge_w if msgs else None, g, mg, up, down, rs, qs, route, *saved, *msgs)
+                            up.dtype, down.dtype, rs.dtype, qs.dtype, mix.dtype if flags[1] else None)
+        halves = saved[3:] if flags[1] else (None, None)
+        ctx.save_for_backward(base, q, edge_w if msgs else None, g, mg, up, down, rs, qs, route, *saved[:3],
+                              mix_f, *halves, *msgs)
         return qo, route
 
     @staticmethod
     def backward(ctx, dqo, droute):
         lib = _lib.load()
-        base, q, edge_w, g, mg, up, down, rs, qs, route, r0, h1, hd, *msgs = ctx.saved_tensors
+        (base, q, edge_w, g, mg, up, down, rs, qs, route, r0, h1, hd, mix, qr, qdir,
+         *msgs) = ctx.saved_tensors
+        flags = ctx.flags
         dtype = q.dtype
         bsz, tokens, heads, dk = q.shape
         m = base.shape[-1]
@@ -138,7 +163,7 @@ class _RouteReader(torch.autograd.Function):
                    "rs": _pack(rs, dtype, False), "qs": _pack(qs, dtype, False)}
         prob = _problem(base, q, edge_w, g, mg, msgs, ctx.query_scale,
                         {k: v for k, v in weights.items() if v is not None},
-                        (route, route), (r0, h1, hd))
+                        (route, route), (r0, h1, hd), flags, mix, (qr, qdir))
         dbase = torch.empty_like(base)
         dmsgs = [torch.empty_like(x) for x in msgs]
         dq = torch.empty_like(q)
@@ -154,6 +179,11 @@ class _RouteReader(torch.autograd.Function):
             gr.dmsg[e] = _operand(x)
         gr.dh1, gr.dhd, gr.dqs, gr.partials = dh1.data_ptr(), dhd.data_ptr(), dqs.data_ptr(), partials.data_ptr()
         gr.hg = hg.data_ptr()
+        if flags[1]:
+            dqr, ddir = torch.empty_like(qr), torch.empty_like(qdir)
+            mix_parts = torch.empty(blocks, heads, device=dev, dtype=torch.float32)
+            gr.dqr, gr.ddir = _rows_operand(dqr, tokens), _rows_operand(ddir, tokens)
+            gr.mix_partials = mix_parts.data_ptr()
         stream = _lib.stream_handle(dev)
         _lib.check(lib.gpa_route_backward(prob, gr, stream), "gpa_route_backward")
         d_up = torch.empty(heads, m, 2 * m, device=dev, dtype=torch.float32)
@@ -165,8 +195,9 @@ class _RouteReader(torch.autograd.Function):
         sums = partials.sum(0)
         dt = ctx.param_dtypes
         d_edge = sums[:, 2:].t().contiguous().to(dt[0]) if msgs else None
+        d_mix = mix_parts.sum(0).to(dt[7]) if flags[1] else None
         return (dbase, dq, d_edge, sums[:, 1].to(dt[1]), sums[:, 0].to(dt[2]), d_up.to(dt[3]), d_down.to(dt[4]),
-                d_rs.to(dt[5]), d_qs.to(dt[6]), None, *dmsgs)
+                d_rs.to(dt[5]), d_qs.to(dt[6]), None, None, d_mix, *dmsgs)
 
 
 def route_reader_many(reads) -> list[tuple[Tensor, Tensor]]:
@@ -183,12 +214,14 @@ def route_reader_many(reads) -> list[tuple[Tensor, Tensor]]:
     lib = _lib.load()
     probs = (_lib.RouteProblem * len(reads))()
     keep, outs = [], []
-    for i, (base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs) in enumerate(reads):
+    for i, read in enumerate(reads):
+        base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, msgs = read[:11]
+        rsa, mix = (read[11], read[12]) if len(read) > 11 else (False, None)
         _lib.require_device(q)
         if not msgs:
             edge_w = gain.new_zeros(0, gain.shape[0])
         prob, inputs, out, saved = _forward_problem(base, q, edge_w, gain, mlp_gain, up, down, rs, qs,
-                                                    query_scale, msgs)
+                                                    query_scale, msgs, (int(rsa), int(mix is not None)), mix)
         probs[i] = prob
         keep.append((inputs, saved))
         outs.append(out)
@@ -198,15 +231,18 @@ def route_reader_many(reads) -> list[tuple[Tensor, Tensor]]:
 
 
 def route_reader(base: Tensor, q: Tensor, edge_w: Tensor | None, gain: Tensor, mlp_gain: Tensor, up: Tensor,
-                 down: Tensor, rs: Tensor, qs: Tensor, query_scale: float, msgs) -> tuple[Tensor, Tensor]:
+                 down: Tensor, rs: Tensor, qs: Tensor, query_scale: float, msgs, rsa: bool = False,
+                 mix: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """(qo, route) of one target level; base [B,T,H,M] float32 logits, q
     [B,T,H,Dk], msgs the incoming messages [B,T,H,M] in edge order with their
     softmax weights edge_w [n_in,H]; gain, mlp_gain [H]; U [H,M,2M],
-    D [H,2M,M], W_rs [H,M,M], W_qs [H,Dk,M]."""
+    D [H,2M,M], W_rs [H,M,M], W_qs [H,Dk,M].  rsa: rsa_update's L1 rescale of
+    the route; mix [H] (.1 + .8 sigmoid(bridge_mix_raw)): balanced_bridge."""
     if not msgs:
         # no incoming edges: the relation gain and edge weights are unused (no gradient)
         gain, edge_w = gain.detach(), gain.new_zeros(0, gain.shape[0])
-    return _RouteReader.apply(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, *msgs)
+    flags = (int(rsa), int(mix is not None))
+    return _RouteReader.apply(base, q, edge_w, gain, mlp_gain, up, down, rs, qs, query_scale, flags, mix, *msgs)
 
 
 class _ProductRead(torch.autograd.Function):

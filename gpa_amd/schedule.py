@@ -720,6 +720,10 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
             return _product_base(model, j, logits, incoming, counts), None, []
         return base, _incoming_weights(model, j), [msg for _, msg in incoming[j]]
 
+    def mix(j):
+        # balanced_bridge: .1 + .8 sigmoid(bridge_mix_raw_j), per head (attention.py:257)
+        return .1 + .8 * model.bridge_mix_raw[j].sigmoid() if cfg.balanced_bridge else None
+
     if (_FUSED_ROUTE[0] and not torch.is_grad_enabled() and 1 < len(logits) <= _lib.ROUTE_MAX_PACK
             and all(fused_route_supported(cfg, dtype, base.shape[-1]) for base in logits)):
         # inference: every level's read in one launch where the library can pack them
@@ -727,7 +731,8 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
         for j, base in enumerate(logits):
             base_j, w, msgs = reader_args(j, base)
             reads.append((base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j], model.route_up[j],
-                          model.route_down[j], model.route_weight[j], query_weight(j), cfg.query_scale, msgs))
+                          model.route_down[j], model.route_weight[j], query_weight(j), cfg.query_scale, msgs,
+                          cfg.rsa_update, mix(j)))
         done = route_reader_many(reads)
         return [route for _, route in done], [qo for qo, _ in done]
     for j, base in enumerate(logits):
@@ -735,7 +740,7 @@ def _bridge(model, q: Tensor, logits, incoming, counts):
             base_j, w, msgs = reader_args(j, base)
             qo, route = route_reader(base_j, q, w, model.relation_gain[j], model.route_mlp_gain[j],
                                      model.route_up[j], model.route_down[j], model.route_weight[j],
-                                     query_weight(j), cfg.query_scale, msgs)
+                                     query_weight(j), cfg.query_scale, msgs, cfg.rsa_update, mix(j))
             routes.append(route)
             queries.append(qo)
             continue

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 22
+#define GPA_HIP_ABI_VERSION 23
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -320,6 +320,15 @@ typedef struct gpa_route_problem {
     const void *up, *down, *rs, *qs;              /* backward weights */
     gpa_operand qo, route;                        /* outputs [B,T,H,M] */
     void *r0, *h1, *hd;                           /* saved rows */
+    /* rsa_update (reference attention.py:251-253): r1 <- round(r1 / clamp(sum|r1|, .25, 4)) per row,
+     * in float32, before the query product; the route output is the rescaled row. 0 = off. */
+    int32_t rsa;
+    /* balanced_bridge (attention.py:256-259): qo = round(mix unit(qr) + (1 - mix) unit(qdir)), with
+     * qr = round(r1 W_rs), qdir = round(query_scale round(q W_qs)) and unit(x) = round(x / max(|x|, 1e-6))
+     * per row (float32 sums), instead of qo = round(qr + qdir).  0 = off. */
+    int32_t balanced;
+    const float *mix;                             /* [H]: .1 + .8 sigmoid(bridge_mix_raw) (balanced) */
+    void *qr, *qdir;                              /* saved rows [H][R][M] (balanced) */
 } gpa_route_problem;
 
 typedef struct gpa_route_grads {
@@ -331,6 +340,10 @@ typedef struct gpa_route_grads {
     void *hg;                                     /* out rows [H][R][2M]: round(gelu(h1)), read by the weight gradients */
     float *partials;                              /* out [ceil(R/32)][H][2 + incoming]:
                                                      d mlp_gain, d gain, d w_e summed over the block's rows */
+    gpa_operand dqr, ddir;                        /* balanced: out rows [H][R][M] addressed as [B,T,H,M]
+                                                     (sb = T*M, st = M, sh = R*M): gradients of qr and qdir */
+    float *mix_partials;                          /* balanced: out [ceil(R/32)][H], the block's sum of
+                                                     dqo . (unit(qr) - unit(qdir)) (d mix after summing) */
 } gpa_route_grads;
 
 /* Forward of the route reader.  Replaces the legacy-read body of _bridge

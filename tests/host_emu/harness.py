@@ -26,8 +26,9 @@ CLANG = "/opt/rocm/llvm/bin/clang++"
 ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3,
            "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6, "gpa_gdn_token_step": 7,
            "gpa_gdn_token_step_many": 8, "gpa_level_token_forward": 9,
-           "gpa_token_level_forward": 10}
-SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip"]
+           "gpa_token_level_forward": 10, "gpa_product_read_forward": 11, "gpa_product_read_backward": 12}
+SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip",
+           "product_read.hip"]
 
 
 def compiler() -> str | None:
@@ -160,6 +161,12 @@ class HostLib:
 
     def gpa_token_level_forward(self, step, final, out, level, stream):
         return self._call("gpa_token_level_forward", [step, out, level], [final])
+
+    def gpa_product_read_forward(self, prob, stream):
+        return self._call("gpa_product_read_forward", [prob])
+
+    def gpa_product_read_backward(self, prob, grads, stream):
+        return self._call("gpa_product_read_backward", [prob, grads])
 
     def gpa_hip_last_error(self):
         return b""

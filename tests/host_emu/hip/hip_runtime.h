@@ -131,6 +131,11 @@ extern char* emu_dynamic_lds;
 #define hipFuncAttributeMaxDynamicSharedMemorySize 8
 inline int hipFuncSetAttribute(const void*, int, int) { return 0; }
 inline float __expf(float x) { return expf(x); }
+// correctly rounded single operations (the host build is compiled without FMA contraction)
+inline float __fadd_rn(float a, float b) { return a + b; }
+inline float __fsub_rn(float a, float b) { return a - b; }
+inline float __fmul_rn(float a, float b) { return a * b; }
+inline float __fdiv_rn(float a, float b) { return a / b; }
 inline float __uint_as_float(uint32_t u) {
   float f;
   memcpy(&f, &u, 4);

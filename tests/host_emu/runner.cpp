@@ -111,6 +111,13 @@ int main(int argc, char** argv) {
                                    static_cast<float*>(raw.at(0)), *reinterpret_cast<gpa_operand*>(blobs.at(1).data()),
                                    reinterpret_cast<gpa_level_problem*>(blobs.at(2).data()), nullptr);
       break;
+    case 11:
+      rc = gpa_product_read_forward(reinterpret_cast<gpa_product_problem*>(blobs.at(0).data()), nullptr);
+      break;
+    case 12:
+      rc = gpa_product_read_backward(reinterpret_cast<gpa_product_problem*>(blobs.at(0).data()),
+                                     reinterpret_cast<gpa_product_grads*>(blobs.at(1).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

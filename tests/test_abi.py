@@ -64,9 +64,9 @@ def test_ctypes_structs_match_c_layout():
     assert _lib.DecodeProblem.level.offset == 40 + 4 * 32 + 8 * 8
     assert ctypes.sizeof(_lib.DecodeProblem) == 232 + 4 * 168 + 12 * 16 + 12 * 8
     # 7 int32 + float, 5 operands, 11 pointers, 2 operands, 3 pointers
-    assert ctypes.sizeof(_lib.RouteProblem) == 32 + 5 * 32 + 11 * 8 + 2 * 32 + 3 * 8
+    assert ctypes.sizeof(_lib.RouteProblem) == 32 + 5 * 32 + 11 * 8 + 2 * 32 + 3 * 8 + 8 + 3 * 8
     # 7 operands, 4 pointers
-    assert ctypes.sizeof(_lib.RouteGrads) == 7 * 32 + 5 * 8
+    assert ctypes.sizeof(_lib.RouteGrads) == 7 * 32 + 5 * 8 + 2 * 32 + 8
     # 9 int32 (+pad), 2 operands, 4 pointers, 2 int64, 1 pointer, 3 operands, 3 pointers
     assert ctypes.sizeof(_lib.LevelProblem) == 40 + 2 * 32 + 4 * 8 + 2 * 8 + 8 + 3 * 32 + 3 * 8
     assert ctypes.sizeof(_lib.LevelGrads) == 4 * 32 + 5 * 8

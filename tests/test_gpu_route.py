@@ -182,3 +182,70 @@ def test_product_read_matches_reference_ops_with_gradients(b, t, h, m, n_in, mar
         tol = 2e-2 if a.dtype == BF else 1e-5
         assert a.grad is not None and a.grad.dtype == r.grad.dtype, i
         assert _rel(a.grad, r.grad) < tol, (i, _rel(a.grad, r.grad))
+
+
+LM_FLAGS = dict(rsa_update=True, balanced_bridge=True, paper_product_read=True, shared_query_center=True)
+
+
+def _bridge_run(model, logits, incoming, q):
+    """Routes, query outputs and every gradient of schedule._bridge under a
+    seeded random loss."""
+    from gpa_amd import schedule
+    logits = [x.clone().requires_grad_() for x in logits]
+    incoming = [[(e, m.clone().requires_grad_()) for e, m in group] for group in incoming]
+    q = q.clone().requires_grad_()
+    model.zero_grad(set_to_none=True)
+    routes, queries = schedule._bridge(model, q, logits, incoming, [None] * len(logits))
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    loss = sum((x.float() * torch.randn(x.shape, generator=gen, device=DEV)).sum() for x in routes + queries)
+    loss.backward()
+    grads = {f"logits{j}": x.grad for j, x in enumerate(logits)}
+    grads.update({f"msg{e}": m.grad for group in incoming for e, m in group})
+    grads["q"] = q.grad
+    grads.update({n: p.grad for n, p in model.named_parameters() if p.grad is not None})
+    return list(routes) + list(queries), grads
+
+
+@pytest.mark.parametrize("t", [6, 1040], ids=["one_kernel", "tiled"])
+@pytest.mark.parametrize("flags", [dict(rsa_update=True), dict(balanced_bridge=True), LM_FLAGS],
+                         ids=["rsa", "balanced", "lm_flags"])
+def test_route_flags_match_the_device_glue(flags, t, monkeypatch):
+    """rsa_update's L1 rescale and balanced_bridge's unit mix inside the HIP
+    route reader (attention.py:251-259), alone and with the LM flag set, at
+    C3 widths in bf16, against the schedule's device glue (the reference's
+    typed torch expressions) for the same read: every route and query output
+    and the gradients of the logits, messages, q and every parameter
+    (bridge_mix_raw included), relative L2 2e-2.  6 rows take the one-kernel
+    reader, 1040 rows the tiled products with the flags' row kernels."""
+    from gpa_amd import DenseGPA, GPAConfig, schedule
+    torch.manual_seed(3)
+    cfg = GPAConfig(heads=2, key_dim=128, value_dim=128, slots=(128, 128, 128, 256), chunk_size=64, **flags)
+    model = DenseGPA(cfg).to(DEV)
+    with torch.no_grad():
+        for group in (model.route_weight, model.route_down):
+            for w in group:
+                w.add_(torch.randn_like(w) * .3)
+        model.edge_logits.normal_(0, .7)
+        model.relation_gain.normal_(0, .5)
+        model.route_mlp_gain.normal_(.5, .2)
+        if cfg.balanced_bridge:
+            model.bridge_mix_raw.normal_(0, 1.)
+        for w in model.query_weight:
+            w.normal_(0, .05)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    logits = [torch.randn(1, t, 2, m, generator=g, device=DEV) * 2 for m in cfg.slots]
+    incoming = [[] for _ in cfg.slots]
+    for e, (i, j) in enumerate(model.edges):
+        incoming[j].append((e, torch.randn(1, t, 2, cfg.slots[j], generator=g, device=DEV).to(BF)))
+    q = torch.randn(1, t, 2, 128, generator=g, device=DEV).to(BF)
+    assert schedule.fused_route_supported(cfg, BF, 256)
+    monkeypatch.setattr(schedule, "_FUSED_ROUTE", [False])
+    ref_out, ref_grads = _bridge_run(model, logits, incoming, q)
+    monkeypatch.setattr(schedule, "_FUSED_ROUTE", [True])
+    out, grads = _bridge_run(model, logits, incoming, q)
+    errors = {f"out{i}": _rel(a, b) for i, (a, b) in enumerate(zip(out, ref_out))}
+    assert set(grads) == set(ref_grads)
+    errors.update({"grad/" + n: _rel(grads[n], ref_grads[n]) for n in ref_grads})
+    worst = max(errors.items(), key=lambda kv: kv[1])
+    print(flags, t, "worst", worst)
+    assert not {k: v for k, v in errors.items() if v > 2e-2}, errors

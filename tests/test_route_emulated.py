@@ -16,11 +16,20 @@ import torch
 from gpa_amd import DenseGPA, GPAConfig, schedule
 from tests.host_emu import harness
 
+LM = dict(rsa_update=True, balanced_bridge=True, paper_product_read=True, shared_query_center=True)
 CASES = {
     "tiny": dict(heads=2, key_dim=8, slots=(6, 5, 7), b=2, t=5),
     "one_level": dict(heads=1, key_dim=4, slots=(3,), b=1, t=3),
     "two_tiles": dict(heads=1, key_dim=32, slots=(32, 48), b=1, t=40),
     "c3_widths": dict(heads=1, key_dim=128, slots=(128, 128, 128, 256), b=1, t=6),
+    # rsa_update's L1 rescale and balanced_bridge's unit mix (attention.py:251-259), alone and with
+    # the rest of the LM flag set (product read, shared query centre)
+    "rsa": dict(heads=2, key_dim=8, slots=(6, 5, 7), b=2, t=5, flags=dict(rsa_update=True)),
+    "balanced": dict(heads=2, key_dim=8, slots=(6, 5, 7), b=2, t=5, flags=dict(balanced_bridge=True)),
+    "lm_flags": dict(heads=2, key_dim=8, slots=(8, 8, 16), b=2, t=5, flags=LM),
+    "lm_c3_widths": dict(heads=1, key_dim=128, slots=(128, 128, 128, 256), b=1, t=6, flags=LM),
+    # 1024 rows: the tiled products and the flags' row kernels between them
+    "lm_tiled": dict(heads=1, key_dim=64, slots=(64, 128), b=1, t=1024, flags=LM),
 }
 
 
@@ -36,7 +45,8 @@ def _rel(a, b):
 
 def _inputs(spec, dtype):
     torch.manual_seed(3)
-    cfg = GPAConfig(heads=spec["heads"], key_dim=spec["key_dim"], value_dim=4, slots=spec["slots"], chunk_size=4)
+    cfg = GPAConfig(heads=spec["heads"], key_dim=spec["key_dim"], value_dim=4, slots=spec["slots"], chunk_size=4,
+                    **spec.get("flags", {}))
     model = DenseGPA(cfg)
     with torch.no_grad():
         for group in (model.route_weight, model.route_down):
@@ -45,6 +55,8 @@ def _inputs(spec, dtype):
         model.edge_logits.normal_(0, .7)
         model.relation_gain.normal_(0, .5)
         model.route_mlp_gain.normal_(.5, .2)
+        if cfg.balanced_bridge:
+            model.bridge_mix_raw.normal_(0, 1.)
     b, t, h = spec["b"], spec["t"], spec["heads"]
     logits = [torch.randn(b, t, h, m) * 2 for m in cfg.slots]
     incoming = [[] for _ in cfg.slots]
@@ -73,8 +85,8 @@ def _run(model, logits, incoming, q):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("name", list(CASES))
 def test_host_built_route_reader_matches_device_glue(name, dtype, runner, tmp_path, monkeypatch):
-    if name == "c3_widths" and dtype == torch.float32:
-        pytest.skip("C3 widths covered in bfloat16")
+    if name in ("c3_widths", "lm_c3_widths", "lm_tiled") and dtype == torch.float32:
+        pytest.skip("C3 widths and the tiled path covered in bfloat16")
     model, logits, incoming, q = _inputs(CASES[name], dtype)
     assert schedule.fused_route_supported(model.config, dtype, max(model.config.slots))
     monkeypatch.setattr(schedule, "_FUSED_ROUTE", [False])
@@ -100,7 +112,7 @@ def test_host_built_route_reader_matches_device_glue(name, dtype, runner, tmp_pa
     assert not bad, bad
 
 
-@pytest.mark.parametrize("name", ["c3_widths", "two_tiles", "tiny"])
+@pytest.mark.parametrize("name", ["c3_widths", "two_tiles", "tiny", "lm_flags"])
 def test_host_built_route_pack_matches_one_launch_per_level(name, runner, tmp_path, monkeypatch):
     """Inference reads of every target level in one call (gpa_route_forward_many,
     which packs the levels into one launch for bf16 rows of 16-byte pieces and
@@ -114,8 +126,17 @@ def test_host_built_route_pack_matches_one_launch_per_level(name, runner, tmp_pa
         routes, queries = schedule._bridge(model, q, logits, incoming, [None] * len(logits))
         for j, base in enumerate(logits):
             w = schedule._incoming_weights(model, j) if incoming[j] else None
+            if cfg.paper_product_read and incoming[j]:
+                base = schedule._product_base(model, j, logits, incoming, [None] * len(logits))
+                w, msgs = None, []
+            else:
+                msgs = [m for _, m in incoming[j]]
+            qw = model.query_weight[j]
+            if cfg.shared_query_center:
+                qw = qw + model.center[j].transpose(-1, -2) / cfg.query_scale
+            mix = .1 + .8 * model.bridge_mix_raw[j].sigmoid() if cfg.balanced_bridge else None
             qo, route = route_reader(base, q, w, model.relation_gain[j], model.route_mlp_gain[j],
                                      model.route_up[j], model.route_down[j], model.route_weight[j],
-                                     model.query_weight[j], cfg.query_scale, [m for _, m in incoming[j]])
+                                     qw, cfg.query_scale, msgs, cfg.rsa_update, mix)
             assert torch.equal(qo, queries[j]), j
             assert torch.equal(route, routes[j]), j
