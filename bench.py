@@ -6,7 +6,7 @@ chunk_size=64; q,k,v ~ N(0,1) in bf16 with K L2-normalised per head; fp32
 master parameters; loss = mean(out.float()^2).  Inputs are resident in HBM
 before the timed region.
 
-    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu] [--no-decode]
+    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--no-cpu] [--no-decode] [--no-lm]
 
 Prints ONE JSON line.  `value` is tokens/s of the whole job over the timed
 steps (independent scans overlap on side streams).  `roofline` is the dominant
@@ -17,8 +17,10 @@ another, so the interval is the kernel's own run time and agrees with a rocprof
 kernel trace of that step).  `step_roofline` is the whole step's algorithmic
 FLOP over the timed step time; `decode` is the batched one-token decode rate (B=64 streams of the same layer, 2048-token
 prefill, 256 graph-replayed steps) with its HBM roofline from the state bytes a
-token step must move; `cpu_baseline` times the CPU oracle (the reference's
-per-token torch algorithm) on a bounded sample.
+token step must move; `lm` is the all-GPA Qwen3-0.6B-architecture LM (a T=8192
+training step with AdamW, a 4096-token prefill and 512 graphed greedy tokens);
+`cpu_baseline` times the CPU oracle (the reference's per-token torch algorithm)
+on a bounded sample.
 """
 from __future__ import annotations
 
@@ -140,6 +142,100 @@ def decode_rate(model, steps: int = 256, warmup: int = 64, prefill: int = 2048) 
                          "frac": gbs / PEAK_HBM_GBS, "state_bytes_per_token_step": moved}}
 
 
+LM_SLOTS = (128, 128, 128, 256)
+
+
+def lm_native_flop_per_token(cfg) -> float:
+    """Forward FLOP per token of the LM's native (non-GPA) products: the q, k,
+    v, o projections and the SwiGLU MLP of every layer, and the LM head."""
+    hid, inter, heads, kv, d = (cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads,
+                                cfg.num_key_value_heads, cfg.head_dim)
+    per_layer = 2 * hid * (heads * d + 2 * kv * d) + 2 * heads * d * hid + 2 * 3 * hid * inter
+    return cfg.num_hidden_layers * per_layer + 2 * hid * cfg.vocab_size
+
+
+def lm_rate(train_steps: int = 2, prefill: int = 4096, decode_tokens: int = 512) -> dict:
+    """The Qwen3-0.6B-architecture all-GPA LM (28 layers, hidden 1024, 16 query
+    / 8 KV heads of width 128, SwiGLU 3072, vocab 151936, tied embeddings; GPA
+    slots (128,128,128,256) with the LM wrapper's flag set), random init, fp32
+    master weights under bf16 autocast: a B=1, T=8192 training step (forward,
+    per-layer checkpointed backward, AdamW) on uniform random token ids; then
+    a `prefill`-token prefill and `decode_tokens` greedy tokens, the decode
+    replayed from one HIP graph per block position (LMDecodeGraph, greedy
+    choice inside the graph)."""
+    import torch
+
+    from gpa_amd import params
+    from gpa_amd.lm import GPALMConfig, GPALMForCausalLM, LMDecodeGraph
+    dev = torch.device("cuda:0")
+    torch.cuda.set_per_process_memory_fraction(0.85)
+    torch.manual_seed(0)
+    cfg = GPALMConfig(gpa=dict(slots=LM_SLOTS))
+    model = GPALMForCausalLM(cfg).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    model.gradient_checkpointing_enable()
+    model.train()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    ids = torch.randint(0, cfg.vocab_size, (1, TOKENS), device=dev, generator=gen)
+
+    def train_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(ids, labels=ids).loss
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    _progress("LM: training step warm-up and timed steps")
+    train_step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(train_steps):
+        loss = train_step()
+    torch.cuda.synchronize()
+    train_s = (time.perf_counter() - start) / train_steps
+    peak_gb = torch.cuda.max_memory_allocated() / 2 ** 30
+    del opt
+    model.eval()
+    prompt = torch.randint(0, cfg.vocab_size, (1, prefill), device=dev, generator=gen)
+    _progress("LM: prefill and graphed greedy decode")
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16), params.frozen():
+        model(prompt[:, :64], logits_to_keep=1)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        out = model(prompt, logits_to_keep=1)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - start
+        first = out.logits[:, -1].argmax(-1, keepdim=True)
+        graph = LMDecodeGraph(model, out.past_key_values, first)
+        del out
+        for _ in range(graph.chunk):  # one untimed block of replays
+            graph.step()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        graph.generate(decode_tokens + 1)  # feeds decode_tokens tokens: whole blocks
+        torch.cuda.synchronize()
+        decode_s = (time.perf_counter() - start) / decode_tokens
+        del graph
+    torch.cuda.set_per_process_memory_fraction(1.0)
+    gpa_flop = f_forward_per_token_head(cfg.head_dim, cfg.head_dim, LM_SLOTS, 64) * cfg.num_attention_heads
+    flop_step = 3 * (cfg.num_hidden_layers * gpa_flop + lm_native_flop_per_token(cfg)) * TOKENS
+    tf = flop_step / train_s / 1e12
+    return {"workload": "Qwen3-0.6B-architecture all-GPA LM (28 layers, hidden 1024, heads 16/8, head_dim 128, "
+                        "MLP 3072, vocab 151936), GPA slots (128,128,128,256), random init, bf16 autocast",
+            "train": {"value": TOKENS / train_s, "unit": "tokens/s", "ms_per_step": train_s * 1e3,
+                      "batch": 1, "seq_len": TOKENS, "loss": loss.item(), "peak_gib": peak_gb,
+                      "optimizer": "AdamW (fused)", "checkpointing": "per layer",
+                      "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": tf / PEAK_BF16_TFLOPS, "flop_per_step": flop_step,
+                                   "note": "algorithmic FLOP (no recompute) of the GPA layers and native products"}},
+            "prefill": {"value": prefill / prefill_s, "unit": "tokens/s", "tokens": prefill,
+                        "ms": prefill_s * 1e3},
+            "decode": {"value": 1 / decode_s, "unit": "tokens/s", "ms_per_token": decode_s * 1e3,
+                       "tokens": decode_tokens, "batch": 1,
+                       "path": "LMDecodeGraph: one HIP graph per block position, greedy choice in the graph"}}
+
+
 def _progress(what: str) -> None:
     print(f"bench: {what}", file=sys.stderr, flush=True)
 
@@ -238,6 +334,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the batched decode measurement")
+    ap.add_argument("--no-lm", action="store_true", help="skip the all-GPA LM (config 5) measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build", file=sys.stderr)
@@ -332,6 +429,10 @@ def main() -> int:
     }
     if not args.no_decode:
         result["decode"] = decode_rate(model)
+    if not args.no_lm:
+        del model, xs, q, k, v
+        torch.cuda.empty_cache()
+        result["lm"] = lm_rate()
     if not args.no_cpu:
         _progress("CPU baseline")
         result["cpu_baseline"] = cpu_baseline()

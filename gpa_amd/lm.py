@@ -200,7 +200,12 @@ def causal_conv(x: Tensor, weight: Tensor, tail: Tensor | None) -> tuple[Tensor,
     width = weight.shape[-1] - 1
     prefix = x.new_zeros(x.shape[0], x.shape[-1], width) if tail is None else tail.to(x.dtype)
     joined = torch.cat((prefix, x.transpose(1, 2)), -1)
-    out = F.conv1d(joined, weight.to(x.dtype), groups=x.shape[-1]).transpose(1, 2)
+    if x.shape[1] == 1:
+        # one token (decode): the window's dot product per channel, accumulated
+        # in float32 like the convolution, without a convolution library call
+        out = (joined.float() * weight[:, 0].float()).sum(-1, keepdim=True).to(x.dtype).transpose(1, 2)
+    else:
+        out = F.conv1d(joined, weight.to(x.dtype), groups=x.shape[-1]).transpose(1, 2)
     return out, (joined[:, :, -width:] if width else joined[:, :, :0])
 
 
@@ -302,8 +307,12 @@ class GPALMAttention(nn.Module):
             cos, sin = (x[:, :, None].to(q.dtype) for x in rotary_emb)
             q = q * cos + _rotate_half(q) * sin
             k = k * cos + _rotate_half(k) * sin
+        # each K/V head serves `groups` consecutive query heads (repeat_interleave
+        # on the head axis, written as an expand so that no size is read back)
         groups = self.heads // self.kv_heads
-        k, v = (x.repeat_interleave(groups, dim=2) for x in (k, v))
+        k, v = (x.unsqueeze(3).expand(b, t, self.kv_heads, groups, self.head_dim).reshape(b, t, self.heads,
+                                                                                          self.head_dim)
+                for x in (k, v))
         if self.attention_dtype is not None:
             q, k, v = (x.to(self.attention_dtype) for x in (q, k, v))
         control = F.silu(control)
@@ -537,5 +546,135 @@ class GPALMForCausalLM(nn.Module):
         return model
 
 
+class LMDecodeGraph:
+    """Greedy one-token decode of the LM on HIP graphs (inference, no autograd).
+
+    A one-token call depends on its position in the GPA block (which
+    snapshots it reads), so there is one graph per position: `chunk_size`
+    graphs captured in replay order into one memory pool.  Each runs the
+    whole LM for one token of every stream (embedding; every layer's
+    projections, short convolutions, GPA core and MLP; final norm; LM head),
+    stores the logits in its own buffer and writes the greedy choice into the
+    static token buffer that the next replay reads.  A decode loop is then one
+    replay per token with nothing read back.
+
+    The cache must start at a block boundary of every layer.  Its tensors are
+    copied into static buffers that the first graph reads; after the last
+    position of a block the new cache is copied back into them.  Parameters
+    must not change while the graphs are in use (their derived tensors are
+    computed once, `params.frozen`); `step` raises if one has.  `autocast` is
+    the dtype the graphs run the native layers under (None: none).  The
+    decode depends on positions only through the block offset, so keep_rope
+    and positional moments are refused.
+    """
+
+    def __init__(self, lm: GPALMForCausalLM, cache: GPALMCache, token: Tensor,
+                 autocast: torch.dtype | None = torch.bfloat16, warmups: int = 2):
+        from . import params
+        from .state import _apply
+        cores = [layer.self_attn.gpa.config for layer in lm.model.layers]
+        self.chunk = cores[0].chunk_size
+        if lm.config.keep_rope or any(c.positional_mode == "moments" for c in cores):
+            raise ValueError("LMDecodeGraph: rotary positions depend on the absolute position; decode eagerly")
+        if any(c.chunk_size != self.chunk for c in cores) or any(
+                m is None or m.state.chunk_offset != 0 for m in cache.layers):
+            raise ValueError("LMDecodeGraph: every layer's cache must start at a block boundary of one chunk size")
+        if token.shape != (token.shape[0], 1):
+            raise ValueError("LMDecodeGraph: one token per stream, [B, 1]")
+        self.lm, self.autocast = lm, autocast
+        self.seen = cache.seen_tokens
+        self.offset = 0
+        self.ids = token.detach().clone()
+        clone = lambda t: t.detach().clone(memory_format=torch.contiguous_format)  # noqa: E731
+        self.start = [AttentionMemory(_apply(m.state, clone), clone(m.projected_tail), clone(m.control_tail))
+                      for m in cache.layers]
+        self._params = params.fingerprints(list(lm.parameters()))
+        self._derived = params.Store()
+        current = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(current)
+        with torch.cuda.stream(side), self._context(), params.frozen(self._derived):
+            layers = self.start
+            for _ in range(warmups):
+                c = GPALMCache(len(layers))
+                c.layers = list(layers)
+                lm(self.ids.clone(), past_key_values=c, logits_to_keep=1)
+                layers = c.layers
+            del layers, c
+        current.wait_stream(side)
+        self.pool = torch.cuda.graph_pool_handle()
+        self.graphs = []
+        self.logits = [torch.empty(token.shape[0], lm.config.vocab_size, device=token.device)
+                       for _ in range(self.chunk)]
+        layers = self.start
+        with self._context(), params.frozen(self._derived):
+            for o in range(self.chunk):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=self.pool):
+                    c = GPALMCache(len(layers))
+                    c.layers = list(layers)
+                    logits = lm(self.ids, past_key_values=c, logits_to_keep=1).logits[:, -1]
+                    self.logits[o].copy_(logits)
+                    self.ids.copy_(logits.argmax(-1, keepdim=True))
+                    del logits
+                layers = c.layers
+                self.graphs.append(graph)
+        self.last = layers
+        from .state import tensors
+        for a, b in zip(self.start, self.last):
+            if b.state.chunk_offset != 0 or [t.shape for t in tensors(a.state)] != [t.shape for t in tensors(b.state)]:
+                raise RuntimeError("LMDecodeGraph: the cache after a block does not match the cache it started from")
+
+    def _context(self):
+        import contextlib
+        stack = contextlib.ExitStack()
+        stack.enter_context(torch.no_grad())
+        if self.autocast is not None:
+            stack.enter_context(torch.autocast("cuda", dtype=self.autocast, cache_enabled=False))
+        return stack
+
+    def step(self) -> Tensor:
+        """Feed the current token of every stream; returns the static [B, 1]
+        buffer, which now holds the greedy next token (and `logits[o]` its
+        logits)."""
+        from . import params
+        if not params.unchanged(self._params):
+            raise RuntimeError("LMDecodeGraph: a parameter changed after capture; build a new graph")
+        o = self.offset
+        self.graphs[o].replay()
+        self.offset = (o + 1) % self.chunk
+        self.seen += 1
+        if self.offset == 0:
+            from .state import tensors
+            with torch.no_grad():
+                for a, b in zip(self.start, self.last):
+                    for dst, src in zip(tensors(a.state), tensors(b.state)):
+                        dst.copy_(src)
+                    a.projected_tail.copy_(b.projected_tail)
+                    a.control_tail.copy_(b.control_tail)
+        return self.ids
+
+    def generate(self, steps: int) -> Tensor:
+        """`steps` greedy tokens [B, steps]: the current token of the static
+        buffer first, then one replay per further token (the last one is
+        returned, not fed)."""
+        out = torch.empty(self.ids.shape[0], steps, dtype=self.ids.dtype, device=self.ids.device)
+        for i in range(steps):
+            out[:, i:i + 1].copy_(self.ids)
+            if i + 1 < steps:
+                self.step()
+        return out
+
+    @property
+    def cache(self) -> GPALMCache:
+        """The cache at a block boundary (its tensors are the static buffers: clone to keep them)."""
+        if self.offset != 0:
+            raise RuntimeError("LMDecodeGraph.cache is available at block boundaries")
+        c = GPALMCache(len(self.start))
+        c.layers = list(self.start)
+        c.seen_tokens = self.seen
+        return c
+
+
 __all__ = ["GPALMConfig", "GPALMForCausalLM", "GPALMCache", "AttentionMemory", "RMSNorm", "causal_conv",
-           "LAYER_DEFAULTS", "LMOutput"]
+           "LAYER_DEFAULTS", "LMOutput", "LMDecodeGraph"]

@@ -247,6 +247,23 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             levels.append(lv)
             key, value = key_next, value_next
             continue
+        if token and write is not None and token_step_supported(key, slot) and token_step_supported(slot, value):
+            # a write that does not read the snapshots (rsa_update's softmax(slot / .25), softmax
+            # slot features): the A_j token step, then the residual from the cached block snapshots
+            raw, a_final = gdn_token_hip(qr, key, slot, g_in, b_in, old.inner)
+            write = write.to(dtype)
+            key_next, value_next = _token_residual(key, value, snap.inner, snap.outer, write, eta)
+            lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
+            lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
+            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
+            if old.position is None and _token_logits_supported(raw, write):
+                token_logits.append((lv, j, raw, old))
+            else:
+                _moments(lv, key, qr, position_ids, old)
+                _level_logits(model, lv, j, raw, old)
+            levels.append(lv)
+            key, value = key_next, value_next
+            continue
         # The outer read of this level (below) runs the B recurrence with the
         # same keys, values, gates and initial state: where the kernels allow,
         # the B scan keeps its intermediates for that read instead.
@@ -566,6 +583,16 @@ _TOKEN_LEVEL = [True]  # a level's inner token step and its level write in one l
 _PACKED = [True]  # a level's A/B scans and all edge scans as packed calls (ops.gdn_scan_many)
 
 
+def _token_residual(key, value, snap_inner, snap_outer, write, eta):
+    """The residual of one token per stream from a given write and the block
+    snapshots A^ [B,H,Dk,M], B^ [B,H,M,Dv] (attention.py:327-329): key -
+    eta0 A^ w, value - eta1 w^T B^, the products in float32."""
+    w = write[:, 0].float()                                        # [B,H,M]
+    rk = torch.matmul(snap_inner.float(), w.unsqueeze(-1))[..., 0]  # [B,H,Dk]
+    rv = torch.matmul(w.unsqueeze(-2), snap_outer.float())[..., 0, :]  # [B,H,Dv]
+    return _residual_eta(key, value, rk.unsqueeze(1), rv.unsqueeze(1), eta)
+
+
 def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):
     """The level write and residual as device ops (attention.py:314-329): the
     write (unless given by the slot feature), A^ w, w^T B^ and the residual
@@ -626,20 +653,22 @@ def _relations(model, local, writes, rel_states, scan, token=False):
             beta = strength[e].expand(lead)
             target = writes[j]
             if cfg.rsa_update:
-                norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
-                target = (target / norm[..., None]).to(target.dtype)
-                beta = (beta * norm.square()).clamp_max(.9)
+                target, beta = _rsa_target(writes[i], target, beta)
             if token and token_step_supported(writes[i], target):
                 return gdn_token_hip(local[i], writes[i], target, g, beta, old.memory)
             msg, _, memory = gdn_scan_hip(local[i], writes[i], target, g, beta, old.memory, **scan)
             return msg, memory
         return run, (local[i], writes[i], writes[j], old.memory, decay, strength)
 
-    if token and not cfg.rsa_update and all(token_step_supported(writes[i], writes[j]) for i, j in model.edges):
+    if token and all(token_step_supported(writes[i], writes[j]) for i, j in model.edges):
         # every edge's one-token step, packed into as few launches as the library takes
         lead = writes[0].shape[:-1]
-        calls = [(local[i], writes[i], writes[j], decay[e].expand(lead), strength[e].expand(lead), old.memory)
-                 for e, ((i, j), old) in enumerate(zip(model.edges, rel_states))]
+        calls = []
+        for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
+            g, beta, target = decay[e].expand(lead), strength[e].expand(lead), writes[j]
+            if cfg.rsa_update:
+                target, beta = _rsa_target(writes[i], target, beta)
+            calls.append((local[i], writes[i], target, g, beta, old.memory))
         done = [r for part in _chunks(calls, _lib.TOKEN_MAX_PACK) for r in gdn_token_many(part)]
     elif _PACKED[0]:
         # every edge's scan in as few library calls as it takes: the state
@@ -649,9 +678,7 @@ def _relations(model, local, writes, rel_states, scan, token=False):
         for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
             g, beta, target = decay[e].expand(lead), strength[e].expand(lead), writes[j]
             if cfg.rsa_update:
-                norm = (writes[i].float().square().sum(-1) + 1e-6).sqrt()
-                target = (target / norm[..., None]).to(target.dtype)
-                beta = (beta * norm.square()).clamp_max(.9)
+                target, beta = _rsa_target(writes[i], target, beta)
             groups.append(dict(q=local[i], k=writes[i], v=target, g=g, beta=beta, s0=old.memory, **scan))
         done = [(msg, final) for part in _chunks(groups, _lib.GDN_MAX_PACK)
                 for msg, _, final in gdn_scan_many(part)]
@@ -663,6 +690,13 @@ def _relations(model, local, writes, rel_states, scan, token=False):
         incoming[j].append((e, msg))
         finals.append(RelationState(i, j, memory))
     return incoming, tuple(finals)
+
+
+def _rsa_target(source: Tensor, target: Tensor, beta: Tensor):
+    """rsa_update's relation value and strength (attention.py:215-218): the
+    target write over the source write's norm, beta * norm^2 capped at .9."""
+    norm = (source.float().square().sum(-1) + 1e-6).sqrt()
+    return (target / norm[..., None]).to(target.dtype), (beta * norm.square()).clamp_max(.9)
 
 
 def _incoming_index(model, j: int) -> Tensor:

@@ -207,6 +207,41 @@ def test_lm_cached_decode_matches_the_oracle():
         assert e_ours <= 1.25 * e_theirs + 1e-2, n
 
 
+def test_lm_decode_graph_matches_eager_decode():
+    """LMDecodeGraph (the whole LM's one-token step on one HIP graph per block
+    position, greedy choice inside the graph) against eager one-token calls
+    from the same cache, over 70 steps (across a block boundary, so the
+    once-per-block cache copy is exercised): the logits of every step within
+    1e-5 and the same greedy tokens; then the graph's cache at the boundary
+    equals the eager cache."""
+    from gpa_amd.lm import LMDecodeGraph
+    print("LM: decode graph vs eager, reduced config-5 widths", flush=True)
+    model, _ = _small_pair(7)
+    model.eval()
+    g = torch.Generator().manual_seed(13)
+    ids = torch.randint(0, C5_SMALL["vocab_size"], (2, 64), generator=g).to(DEV)
+    with torch.no_grad():
+        out = model(ids, logits_to_keep=1)
+        cache = out.past_key_values
+        nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+        graph = LMDecodeGraph(model, cache, nxt, autocast=None)
+        for i in range(70):
+            logits = model(nxt, past_key_values=cache, logits_to_keep=1).logits[:, -1]
+            o = graph.offset
+            graph.step()
+            assert _rel(graph.logits[o], logits) < 1e-5, i
+            nxt = logits.argmax(-1, keepdim=True)
+            assert torch.equal(graph.ids, nxt), i
+        for _ in range(58):  # to the next block boundary
+            graph.step()
+            nxt = model(nxt, past_key_values=cache, logits_to_keep=1).logits[:, -1].argmax(-1, keepdim=True)
+        assert torch.equal(graph.ids, nxt) and graph.cache.seen_tokens == cache.seen_tokens
+        for a, b in zip(graph.cache.layers, cache.layers):
+            for x, y in zip(tensors(a.state), tensors(b.state)):
+                assert _rel(x, y) < 1e-5
+            assert _rel(a.projected_tail, b.projected_tail) < 1e-6
+
+
 def test_c5_full_size_training_step_prefill_and_greedy_decode():
     """Config 5 at full size: the Qwen3-0.6B-architecture all-GPA LM (28
     layers, hidden 1024, 16 query / 8 KV heads of width 128, SwiGLU 3072,
@@ -262,4 +297,16 @@ def test_c5_full_size_training_step_prefill_and_greedy_decode():
         # the last new token is returned, not yet fed
         assert tokens.shape == (1, 16) and cache.seen_tokens == 4096 + 15
         assert ((tokens >= 0) & (tokens < model.config.vocab_size)).all()
+        del cache
+        print("C5 full size: graphed greedy decode vs eager", flush=True)
+        from gpa_amd.lm import LMDecodeGraph
+        out = model(prompt, logits_to_keep=1)
+        first = out.logits[:, -1].argmax(-1, keepdim=True)
+        graph = LMDecodeGraph(model, out.past_key_values, first)
+        graphed = graph.generate(16)
+        eager, _ = model.generate_greedy(first, 16, cache=out.past_key_values)
+        assert torch.equal(graphed[:, 0], first[:, 0])
+        # eager starts after `first`; under bf16 autocast the tokens agree while
+        # no near-tie flips one, so compare the first few
+        assert torch.equal(graphed[:, 1:5], eager[:, :4])
     torch.cuda.set_per_process_memory_fraction(1.0)
