@@ -135,7 +135,9 @@ __global__ __launch_bounds__(QNT) void level_token(gpa_level_problem p) {
 // (M/4) and (Dv/4) dividing NT, Dk M / 4 and M Dv / 4 at most RQ NT.
 constexpr int RQ = 8;  // float4 pieces of A^ (and of B^) per thread
 
-template <typename E, int NT>
+// RESID false: the write alone (key_out and value_out null: the last level,
+// whose residual nothing reads): B^ is not loaded and neither product is formed.
+template <typename E, int NT, bool RESID = true>
 __device__ __forceinline__ void level_token_reg_run(const gpa_level_problem& p, int s) {
   constexpr int NW = NT / 64;
   __shared__ float uk[256], wf[256], zp[NT * 4], rks[256];
@@ -156,7 +158,7 @@ __device__ __forceinline__ void level_token_reg_run(const gpa_level_problem& p, 
   for (int i = 0; i < RQ; ++i) {
     const int fa = t + NT * i, fb = t + NT * i;
     av[i] = A[fa < na ? fa : 0];
-    bv[i] = Bh[fb < nb ? fb : 0];
+    if constexpr (RESID) bv[i] = Bh[fb < nb ? fb : 0];
   }
   const float xk = t < Dk ? to_f32(key[t < Dk ? t : 0]) : 0.f;
   const float xv = t < Dv ? to_f32(val[t < Dv ? t : 0]) : 0.f;
@@ -215,6 +217,7 @@ __device__ __forceinline__ void level_token_reg_run(const gpa_level_problem& p, 
     wt = round_as<E>(expf(wf[t] - soft[0]) / soft[1]);
     reinterpret_cast<E*>(p.write.ptr)[op_base(p.write, b, h) + t] = from_f32<E>(wt);
   }
+  if constexpr (!RESID) return;
   __syncthreads();  // every thread has read wf[t] for the softmax before it is overwritten
   if (t < M) wf[t] = wt;
   __syncthreads();
@@ -256,9 +259,9 @@ __device__ __forceinline__ void level_token_reg_run(const gpa_level_problem& p, 
     reinterpret_cast<E*>(p.key_out.ptr)[op_base(p.key_out, b, h) + t] = from_f32<E>(xk - eta0 * round_as<E>(rks[t]));
 }
 
-template <typename E, int NT>
+template <typename E, int NT, bool RESID>
 __global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
-  level_token_reg_run<E, NT>(p, blockIdx.x);
+  level_token_reg_run<E, NT, RESID>(p, blockIdx.x);
 }
 
 // A level's inner one-token step (K <= 16 NI, every NT / 256 consecutive
@@ -267,7 +270,7 @@ __global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
 // reads the running state and writes a new one, the level write reads the
 // block snapshots.  Step and level workgroups alternate while both last, so
 // that each compute unit streams both kinds of data at once.
-template <typename E, int NI, int NT>
+template <typename E, int NI, int NT, bool RESID = true>
 __global__ __launch_bounds__(NT) void token_level(gpa_gdn_problem sp, float* fin, gpa_operand out,
                                                   gpa_level_problem lp, int nstep) {
   __shared__ TokenLds<NI> tl[NT / SNT];
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(NT) void token_level(gpa_gdn_problem sp, float* fin
     idx = blk - both;
   }
   if (!step) {
-    level_token_reg_run<E, NT>(lp, idx);
+    level_token_reg_run<E, NT, RESID>(lp, idx);
     return;
   }
   const int u = threadIdx.x / SNT;
@@ -310,9 +313,10 @@ int check_level_token(const gpa_level_problem* problem) {
   if (p.key_dim < 1 || p.key_dim > QNT || p.value_dim < 1 || p.value_dim > QNT || p.slots < 1 || p.slots > QNT)
     return fail(GPA_HIP_EUNSUPPORTED, "level token: key, value and slot widths must be in [1, 256]");
   if (p.dtype != GPA_DTYPE_F32 && p.dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "level token: dtype");
-  if (!p.key.ptr || !p.value.ptr || !p.a_first || !p.b_first || !p.eta || !p.write.ptr || !p.key_out.ptr ||
-      !p.value_out.ptr)
+  if (!p.key.ptr || !p.value.ptr || !p.a_first || !p.b_first || !p.eta || !p.write.ptr)
     return fail(GPA_HIP_EINVAL, "level token: null pointer (the snapshots a_first and b_first are required)");
+  if (!p.key_out.ptr != !p.value_out.ptr)
+    return fail(GPA_HIP_EINVAL, "level token: key_out and value_out are both given or both null (write only)");
   return GPA_HIP_OK;
 }
 
@@ -324,24 +328,22 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
   if (int rc = check_level_token(problem)) return rc;
   const gpa_level_problem& p = *problem;
   const dim3 grid((unsigned)((int64_t)p.batch * p.heads));
-  const bool bf = p.dtype == GPA_DTYPE_BF16;
-  switch (reg_threads(p)) {
-    case 256:
-      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 256>), grid, dim3(256), 0, stream, p);
-      else hipLaunchKernelGGL((level_token_reg<float, 256>), grid, dim3(256), 0, stream, p);
-      break;
-    case 512:
-      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 512>), grid, dim3(512), 0, stream, p);
-      else hipLaunchKernelGGL((level_token_reg<float, 512>), grid, dim3(512), 0, stream, p);
-      break;
-    case 1024:
-      if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, 1024>), grid, dim3(1024), 0, stream, p);
-      else hipLaunchKernelGGL((level_token_reg<float, 1024>), grid, dim3(1024), 0, stream, p);
-      break;
-    default:
-      if (bf) hipLaunchKernelGGL(level_token<bf16_t>, grid, dim3(QNT), 0, stream, p);
-      else hipLaunchKernelGGL(level_token<float>, grid, dim3(QNT), 0, stream, p);
-  }
+  const bool bf = p.dtype == GPA_DTYPE_BF16, resid = p.key_out.ptr != nullptr;
+  const int nt = reg_threads(p);
+#define GPA_LEVEL_REG(NT)                                                                                   \
+  do {                                                                                                      \
+    if (bf && resid) hipLaunchKernelGGL((level_token_reg<bf16_t, NT, true>), grid, dim3(NT), 0, stream, p);  \
+    else if (bf) hipLaunchKernelGGL((level_token_reg<bf16_t, NT, false>), grid, dim3(NT), 0, stream, p);   \
+    else if (resid) hipLaunchKernelGGL((level_token_reg<float, NT, true>), grid, dim3(NT), 0, stream, p);  \
+    else hipLaunchKernelGGL((level_token_reg<float, NT, false>), grid, dim3(NT), 0, stream, p);            \
+  } while (0)
+  if (nt == 256) GPA_LEVEL_REG(256);
+  else if (nt == 512) GPA_LEVEL_REG(512);
+  else if (nt == 1024) GPA_LEVEL_REG(1024);
+  else if (!resid) return fail(GPA_HIP_EUNSUPPORTED, "level token: the write-only form needs the register kernel");
+  else if (bf) hipLaunchKernelGGL(level_token<bf16_t>, grid, dim3(QNT), 0, stream, p);
+  else hipLaunchKernelGGL(level_token<float>, grid, dim3(QNT), 0, stream, p);
+#undef GPA_LEVEL_REG
   return check_launch("gpa_level_token_forward");
 }
 
@@ -352,11 +354,13 @@ extern "C" int gpa_token_level_forward(const gpa_gdn_problem* step, float* final
   if (int rc = check_level_token(level)) return rc;
   const int nt = reg_threads(*level), ni = token_rows(*step);
   const int64_t swg = token_workgroups(*step), nlev = (int64_t)level->batch * level->heads;
-  // Only the 512-thread level kernel (M <= 128 at Dk = Dv = 128): at 1024
-  // threads the step role's registers leave room for one workgroup per
-  // compute unit, and the one launch is slower than the two.
-  const bool fused = step->dtype == level->dtype && nt == 512 && (ni == 8 || ni == 16) && swg % (nt / SNT) == 0 &&
-                     swg / (nt / SNT) + nlev <= INT32_MAX / 2;
+  // Only the 512-thread level kernel (M <= 128 at Dk = Dv = 128).  At 1024
+  // threads (M = 256) the one launch is slower than the two: with the
+  // residual the step role's registers leave room for one workgroup per
+  // compute unit, and the write-only form measured 12-25 us slower too.
+  const bool resid = level->key_out.ptr != nullptr;
+  const bool fused = step->dtype == level->dtype && nt == 512 && (ni == 8 || ni == 16) &&
+                     swg % (nt / SNT) == 0 && swg / (nt / SNT) + nlev <= INT32_MAX / 2;
   if (!fused) {
     if (int rc = gpa_gdn_token_step(step, final_state, out, stream)) return rc;
     return gpa_level_token_forward(level, stream);
@@ -364,13 +368,16 @@ extern "C" int gpa_token_level_forward(const gpa_gdn_problem* step, float* final
   const int nstep = (int)(swg / (nt / SNT));
   const dim3 grid((unsigned)(nstep + nlev));
   const bool bf = step->dtype == GPA_DTYPE_BF16;
-#define GPA_TOKEN_LEVEL(E, NI) \
-  hipLaunchKernelGGL((token_level<E, NI, 512>), grid, dim3(512), 0, stream, *step, final_state, out, *level, nstep)
-  if (ni == 8) {
-    if (bf) GPA_TOKEN_LEVEL(bf16_t, 8); else GPA_TOKEN_LEVEL(float, 8);
+#define GPA_TOKEN_LEVEL(E, NI, NT, R) \
+  hipLaunchKernelGGL((token_level<E, NI, NT, R>), grid, dim3(NT), 0, stream, *step, final_state, out, *level, nstep)
+#define GPA_TOKEN_LEVEL_E(NI, NT, R) \
+  do { if (bf) GPA_TOKEN_LEVEL(bf16_t, NI, NT, R); else GPA_TOKEN_LEVEL(float, NI, NT, R); } while (0)
+  if (resid) {
+    if (ni == 8) GPA_TOKEN_LEVEL_E(8, 512, true); else GPA_TOKEN_LEVEL_E(16, 512, true);
   } else {
-    if (bf) GPA_TOKEN_LEVEL(bf16_t, 16); else GPA_TOKEN_LEVEL(float, 16);
+    if (ni == 8) GPA_TOKEN_LEVEL_E(8, 512, false); else GPA_TOKEN_LEVEL_E(16, 512, false);
   }
+#undef GPA_TOKEN_LEVEL_E
 #undef GPA_TOKEN_LEVEL
   return check_launch("gpa_token_level_forward");
 }

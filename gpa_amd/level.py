@@ -120,9 +120,10 @@ class _LevelMix(torch.autograd.Function):
 
 
 def _block_problem(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
-                   offset: int):
+                   offset: int, residual: bool = True):
     """Checked arguments of a `level_mix_block` call: (problem, write, key',
-    value', tensors kept alive)."""
+    value', tensors kept alive); key' and value' are None (and not formed)
+    without `residual`."""
     _lib.require_device(key)
     bsz, tokens, heads, dk = key.shape
     if offset + tokens > chunk:
@@ -134,7 +135,7 @@ def _block_problem(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor,
     (af, asb), (bf, bsb) = _snapshot(a_first), _snapshot(b_first)
     eta = eta.detach().float().contiguous()
     write = torch.empty(bsz, tokens, heads, m, device=key.device, dtype=dtype)
-    key_out, value_out = torch.empty_like(key), torch.empty_like(value)
+    key_out, value_out = (torch.empty_like(key), torch.empty_like(value)) if residual else (None, None)
     rk, rv = torch.empty_like(key), torch.empty_like(value)
     stats = torch.empty(bsz, tokens, heads, 2, device=key.device, dtype=torch.float32)
     p = _lib.LevelProblem()
@@ -152,12 +153,17 @@ def _block_problem(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor,
 
 
 def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
-                    offset: int) -> tuple[Tensor, Tensor, Tensor]:
+                    offset: int, residual: bool = True) -> tuple[Tensor, Tensor | None, Tensor | None]:
     """`level_mix` of a call that stays inside one block (offset + T <= chunk)
     whose snapshots A^ [B,H,Dk,M] and B^ [B,H,M,Dv] are given: the scans'
-    chunk-start states are not needed (inference decode); no autograd."""
+    chunk-start states are not needed (inference decode); no autograd.
+    Without `residual` (one token: the last level, whose residual nothing
+    reads) only the write is formed and key', value' are None."""
     lib = _lib.load()
-    p, write, key_out, value_out, alive = _block_problem(key, value, a_first, b_first, eta, chunk, offset)
+    if not residual and key.shape[1] != 1:
+        raise ValueError("level_mix_block: the write-only form takes one token")
+    p, write, key_out, value_out, alive = _block_problem(key, value, a_first, b_first, eta, chunk, offset,
+                                                         residual)
     if key.shape[1] == 1 and _TOKEN_KERNEL[0]:
         _lib.check(lib.gpa_level_token_forward(p, _lib.stream_handle(key.device)), "gpa_level_token_forward")
     else:
@@ -166,26 +172,45 @@ def level_mix_block(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor
 
 
 def token_step_and_level(step, key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor,
-                         chunk: int, offset: int):
+                         chunk: int, offset: int, residual: bool = True):
     """A level's inner one-token step `ops.gdn_token_hip(*step)` and its
     one-token `level_mix_block(key, value, a_first, b_first, eta, chunk,
-    offset)` in one launch (`gpa_token_level_forward`; inference decode, the
-    two share no buffers).  Returns (out, final, write, key', value') with the
-    results of the two separate calls."""
+    offset, residual)` in one launch where the library has it
+    (`gpa_token_level_forward`; inference decode, the two share no buffers).
+    Returns (out, final, write, key', value') with the results of the two
+    separate calls."""
     from .ops import _token_call, gdn_token_hip
     if key.shape[1] != 1:
         raise ValueError("token_step_and_level: needs one token")
     if not _TOKEN_KERNEL[0]:
-        return gdn_token_hip(*step) + level_mix_block(key, value, a_first, b_first, eta, chunk, offset)
+        return gdn_token_hip(*step) + level_mix_block(key, value, a_first, b_first, eta, chunk, offset, residual)
     lib = _lib.load()
     sp, final, out, alive_s = _token_call(*step)
-    lp, write, key_out, value_out, alive_l = _block_problem(key, value, a_first, b_first, eta, chunk, offset)
+    lp, write, key_out, value_out, alive_l = _block_problem(key, value, a_first, b_first, eta, chunk, offset,
+                                                            residual)
     _lib.check(lib.gpa_token_level_forward(sp, final.data_ptr(), _lib.operand(out), lp,
                                            _lib.stream_handle(key.device)), "gpa_token_level_forward")
     return out, final, write, key_out, value_out
 
 
 _TOKEN_KERNEL = [True]  # one-token calls of level_mix_block on gpa_level_token_forward
+
+_REG_PIECES = 8  # float4 pieces of each snapshot per thread in the register level kernel
+
+
+def write_only_supported(key_dim: int, value_dim: int, slots: int) -> bool:
+    """Whether gpa_level_token_forward takes the write-only form for these
+    widths: its register kernel covers them (widths multiples of 4, a thread
+    count of 256, 512 or 1024 that the float4 column groups of A^ and B^
+    divide, and at most 8 float4 pieces of each snapshot per thread)."""
+    if slots % 4 or value_dim % 4:
+        return False
+    for nt in (256, 512, 1024):
+        if nt % (slots // 4) or nt % (value_dim // 4):
+            continue
+        if key_dim * slots // 4 <= _REG_PIECES * nt and slots * value_dim // 4 <= _REG_PIECES * nt:
+            return True
+    return False
 
 
 def level_mix(key: Tensor, value: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: Tensor | None,

@@ -37,7 +37,7 @@ from .counts import count_logits
 from .slots import slot_gates, slot_gates_act
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
-from .level import level_mix, level_mix_block, token_step_and_level
+from .level import level_mix, level_mix_block, token_step_and_level, write_only_supported
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
 from .route import product_read
@@ -226,13 +226,18 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
         if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
             step = (qr, key, slot, g_in, b_in, old.inner)
+            # the last level's residual is never read (attention.py:327-329 after the
+            # loop's last pass): its level kernel forms the write alone
+            residual = j + 1 < len(state.levels) or not write_only_supported(
+                key.shape[-1], value.shape[-1], slot.shape[-1])
             if _TOKEN_LEVEL[0]:
                 # the A_j step and the level write in one launch (they share no buffers)
                 raw, a_final, write, key_next, value_next = token_step_and_level(
-                    step, key, value, snap.inner, snap.outer, eta, chunk, offset)
+                    step, key, value, snap.inner, snap.outer, eta, chunk, offset, residual)
             else:
                 raw, a_final = gdn_token_hip(*step)
-                write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset)
+                write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset,
+                                                              residual)
             # The B_j step runs at its read, after the route reader (nothing
             # before needs the new B_j): one pass over the state for both.
             lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)

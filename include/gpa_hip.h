@@ -446,6 +446,9 @@ int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *
  * b_first, which are required (a_states, b_states, rk, rv and stats are not
  * used): write = softmax(u(key) A^) rounded to the activation type,
  * key_out = key - eta0 round(A^ write), value_out = value - eta1 round(write^T B^).
+ * With key_out and value_out both null the write alone is formed and B^ is
+ * not read (the last level, whose residual nothing reads; shapes of the
+ * register kernel only, e.g. Dk = 128 with M up to 256).
  * Replaces reference src/gpa/attention.py:314-329 and :190-194 at T = 1. */
 int gpa_level_token_forward(const gpa_level_problem *problem, hipStream_t stream);
 /* A level's inner one-token step and its one-token level write in one launch

@@ -138,3 +138,26 @@ def test_token_level_matches_separate_calls(host, step_shape, lvl, dtype):
         apart = ops.gdn_token_hip(*step) + level.level_mix_block(key, value, fa, fb, eta, 4, 2)
     for name, a, r in zip(("out", "final", "write", "key'", "value'"), fused, apart):
         assert a.dtype == r.dtype and torch.equal(a, r), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("b,h,dk,dv,m", [(2, 2, 64, 32, 64), (1, 2, 128, 128, 256), (2, 1, 128, 128, 128)])
+def test_write_only_level_token_gives_the_same_write(host, b, h, dk, dv, m, dtype):
+    """The last level's write-only form (key_out / value_out null: B^ is not
+    read, no residual product) gives the bits of the full form's write, alone
+    and beside the inner token step."""
+    assert level.write_only_supported(dk, dv, m)
+    g = torch.Generator().manual_seed(b + dk + m + 1)
+    key = torch.randn(b, 1, h, dk, generator=g).to(dtype)
+    value = torch.randn(b, 1, h, dv, generator=g).to(dtype)
+    fa, fb = torch.randn(b, h, dk, m, generator=g) * .3, torch.randn(b, h, m, dv, generator=g) * .3
+    eta = 1 + .25 * torch.randn(h, 2, generator=g).tanh()
+    step = _call(g, b, h, dk, m, dtype, "full", True)
+    with torch.no_grad():
+        full = level.level_mix_block(key, value, fa, fb, eta, 4, 2)
+        only = level.level_mix_block(key, value, fa, fb, eta, 4, 2, residual=False)
+        fused = level.token_step_and_level(step, key, value, fa, fb, eta, 4, 2, residual=False)
+        apart = ops.gdn_token_hip(*step)
+    assert only[1] is None and only[2] is None and fused[3] is None and fused[4] is None
+    assert torch.equal(only[0], full[0]) and torch.equal(fused[2], full[0])
+    assert torch.equal(fused[0], apart[0]) and torch.equal(fused[1], apart[1])
