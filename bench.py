@@ -251,13 +251,29 @@ def _cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
+C1 = dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), positional_mode="gated", chunk_size=1)
+C2 = dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=64)
+
+
 def cpu_baseline() -> dict:
     """The oracle (per-token reference algorithm, fp32) timed on this host with
-    the reference benchmark's protocol (scripts/benchmark.py:44-54): 2 warm-up
-    runs, then 3 timed runs each at T=128 and T=256 (fwd+bwd of the training
-    workload's layer at B=1); and batched decode of the same layer at B=64
-    after a one-block (64-token) prefill, 8 timed one-token steps (the step
-    cost does not depend on the prefill length: the cache is fixed-size)."""
+    the reference benchmark's protocol (scripts/benchmark.py:44-54: warm-ups,
+    then timed runs with perf_counter), per workload:
+      * the training workload's layer (B=1, H=16, Dk=Dv=128, slots
+        (128,128,128,256), C=64): fwd+bwd, 2 warm-ups then 3 timed runs each at
+        T=128 and T=256 (`value` = T=256; full T=8192 autograd would hold
+        ~240 GB of per-token states), and forward only (no_grad) at T=1024,
+        1 warm-up then 2 timed runs;
+      * config 1 in full (tokenwise, B=2, T=16, H=4, Dk=32, Dv=48, slots
+        (64,64,64,128)): fwd+bwd of out.square().mean() and a one-token
+        continuation, 2 warm-ups then 3 timed runs;
+      * config 2 (the same widths, C=64, B=8): fwd+bwd at T=128, one 16-token
+        warm-up then 2 timed runs (the full T=1024 takes about a minute a run
+        on 16 cores; the per-token cost does not depend on T, which the two
+        lengths of the training layer check);
+      * batched decode of the training layer at B=64 after a one-block
+        (64-token) prefill, 8 timed one-token steps (the step cost does not
+        depend on the prefill length: the cache is fixed-size)."""
     import torch
 
     import oracle
@@ -265,50 +281,79 @@ def cpu_baseline() -> dict:
     cores = len(os.sched_getaffinity(0))
     old = torch.get_num_threads()
     torch.set_num_threads(cores)
-    h, dk, dv = SHAPE["heads"], SHAPE["key_dim"], SHAPE["value_dim"]
 
-    def inputs(b, t):
-        q = torch.randn(b, t, h, dk)
-        k = torch.nn.functional.normalize(torch.randn_like(q), dim=-1)
-        return q, k, torch.randn(b, t, h, dv)
+    def inputs(shape, b, t, normalize=True):
+        q = torch.randn(b, t, shape["heads"], shape["key_dim"])
+        k = torch.randn_like(q)
+        if normalize:
+            k = torch.nn.functional.normalize(k, dim=-1)
+        return q, k, torch.randn(b, t, shape["heads"], shape["value_dim"])
+
+    def train_rate(run, model, shape, b, t, warm_t, warmups, reps, normalize=True):
+        def once(tt):
+            xs = [x.requires_grad_() for x in inputs(shape, b, tt, normalize)]
+            model.zero_grad(set_to_none=True)
+            start = time.perf_counter()
+            out, state = run(*xs)
+            out.float().square().mean().backward()
+            return time.perf_counter() - start, state
+        for _ in range(warmups):
+            once(warm_t)
+        secs = [once(t)[0] for _ in range(reps)]
+        return b * t * len(secs) / sum(secs)
 
     try:
         torch.manual_seed(0)
         model = DenseGPA(GPAConfig(**SHAPE))
         run = oracle.OracleRun(model)
-
-        def once(t):
-            xs = [x.requires_grad_() for x in inputs(BATCH, t)]
-            model.zero_grad(set_to_none=True)
-            start = time.perf_counter()
-            out, _ = run(*xs)
-            out.float().square().mean().backward()
-            return time.perf_counter() - start
-
-        for _ in range(2):
-            once(32)
-        rates = {}
-        for t in (128, 256):
-            secs = [once(t) for _ in range(3)]
-            rates[t] = BATCH * t * len(secs) / sum(secs)
+        rates = {t: train_rate(run, model, SHAPE, BATCH, t, 32, 2, 3) for t in (128, 256)}
         with torch.no_grad():
-            _, state = run(*inputs(DECODE_BATCH, 64))
-            toks = [inputs(DECODE_BATCH, 1) for _ in range(10)]
+            run(*inputs(SHAPE, BATCH, 32))
+            secs = []
+            for _ in range(2):
+                xs = inputs(SHAPE, BATCH, 1024)
+                start = time.perf_counter()
+                run(*xs)
+                secs.append(time.perf_counter() - start)
+            fwd_rate = BATCH * 1024 * len(secs) / sum(secs)
+            _, state = run(*inputs(SHAPE, DECODE_BATCH, 64))
+            toks = [inputs(SHAPE, DECODE_BATCH, 1) for _ in range(10)]
             for x in toks[:2]:
                 _, state = run(*x, state)
             start = time.perf_counter()
             for x in toks[2:]:
                 _, state = run(*x, state)
             step_s = (time.perf_counter() - start) / (len(toks) - 2)
+        # config 1: tokenwise, fwd+bwd, then a one-token continuation from the returned state
+        torch.manual_seed(0)
+        m1 = DenseGPA(GPAConfig(**C1))
+        r1 = oracle.OracleRun(m1)
+        c1_rate = train_rate(r1, m1, C1, 2, 16, 16, 2, 3, normalize=False)
+        with torch.no_grad():
+            _, s1 = r1(*inputs(C1, 2, 16, False))
+            start = time.perf_counter()
+            r1(*inputs(C1, 2, 1, False), s1)
+            c1_cont_ms = (time.perf_counter() - start) * 1e3
+        # config 2 in full
+        torch.manual_seed(0)
+        m2 = DenseGPA(GPAConfig(**C2))
+        c2_rate = train_rate(oracle.OracleRun(m2), m2, C2, 8, 128, 16, 1, 2, normalize=False)
     finally:
         torch.set_num_threads(old)
     return {"value": rates[256], "unit": "tokens/s", "cores": cores, "kind": "port",
             "tokens_per_s_T128": rates[128], "tokens_per_s_T256": rates[256],
+            "forward_T1024": {"value": fwd_rate, "unit": "tokens/s"},
             "decode": {"value": DECODE_BATCH / step_s, "unit": "tokens/s", "ms_per_token_step": step_s * 1e3,
                        "batch": DECODE_BATCH},
-            "sample": f"oracle fwd+bwd of the same layer, fp32, B=1: 2 warm-ups (T=32), 3 timed runs at T=128 "
-                      f"and at T=256 (value = T=256); decode B=64 after a 64-token prefill, 8 timed steps; "
-                      f"{_cpu_model()}, {cores} threads"}
+            "config1": {"value": c1_rate, "unit": "tokens/s", "continuation_ms": c1_cont_ms,
+                        "workload": "B=2 T=16 H=4 Dk=32 Dv=48 slots (64,64,64,128) C=1, fwd+bwd"},
+            "config2": {"value": c2_rate, "unit": "tokens/s",
+                        "workload": "B=8 H=4 Dk=32 Dv=48 slots (64,64,64,128) C=64, fwd+bwd, timed at T=128"},
+            "sample": f"oracle, fp32, on {_cpu_model()} with {cores} threads: the training layer (B=1) fwd+bwd with "
+                      f"2 warm-ups (T=32) and 3 timed runs at T=128 and at T=256 (value = T=256), forward only at "
+                      f"T=1024 (2 timed runs); config 1 in full (3 timed fwd+bwd runs and a one-token "
+                      f"continuation); config 2 at B=8, T=128 (2 timed fwd+bwd runs); decode B=64 after a 64-token "
+                      f"prefill, 8 timed steps"}
 
 
 def _measured_traffic(kernel: str) -> float | None:
