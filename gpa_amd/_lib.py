@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 23
+ABI_VERSION = 24
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -124,12 +124,14 @@ class LevelProblem(ctypes.Structure):
                [(n, c_vp) for n in ("a_states", "b_states", "a_first", "b_first")] + \
                [("a_first_sb", c_i64), ("b_first_sb", c_i64), ("eta", c_vp)] + \
                [(n, Operand) for n in ("write", "key_out", "value_out")] + [("rk", c_vp), ("rv", c_vp),
-                                                                             ("stats", c_vp)]
+                                                                             ("stats", c_vp)] + \
+               [("given_write", c_i32)]
 
 
 class LevelGrads(ctypes.Structure):
     _fields_ = [(n, Operand) for n in ("dwrite", "dkey_out", "dvalue_out", "dkey")] + \
-               [(n, c_vp) for n in ("da_states", "db_states", "da_first", "db_first", "deta")]
+               [(n, c_vp) for n in ("da_states", "db_states", "da_first", "db_first", "deta")] + \
+               [("dwrite_given", Operand)]
 
 
 class CountProblem(ctypes.Structure):

@@ -183,6 +183,11 @@ __global__ __launch_bounds__(LNT, 1) void level_fwd(gpa_level_problem p) {
   float* SL = S + LROWS * ldm;     // snapshot slab
   const int KT = (Dk + 31) / 32, VT = (Dv + 31) / 32;
 
+  if (p.given_write) {  // the write is given: its rows -> S
+    const int row = tid >> 2, part = tid & 3, t = q.token(row);
+    const E* wi = reinterpret_cast<const E*>(p.write.ptr) + (t >= 0 ? q.at(p.write, t) : 0);
+    for (int m = part; m < pad8(M); m += 4) S[row * ldm + m] = (t >= 0 && m < M) ? to_f32(wi[m]) : 0.f;
+  } else {
   {  // u(key) rows, 4 threads per row
     const int row = tid >> 2, part = tid & 3, t = q.token(row);
     const float den = key_den<E>(p, q, t, part);
@@ -227,6 +232,7 @@ __global__ __launch_bounds__(LNT, 1) void level_fwd(gpa_level_problem p) {
       }
       S[row * ldm + m] = w;
     }
+  }
   }
 
   // rk = A^ w and rv = w^T B^, summed over the slabs
@@ -300,15 +306,16 @@ __global__ __launch_bounds__(LNT, 1) void level_bwd(gpa_level_problem p, gpa_lev
   const int MT = (M + 31) / 32, KT = (Dk + 31) / 32, VT = (Dv + 31) / 32;
   const float eta0 = p.eta[2 * q.h], eta1 = p.eta[2 * q.h + 1];
   const E* key = reinterpret_cast<const E*>(p.key.ptr);
+  const bool given = p.given_write != 0;  // the write is an input: its gradient ends at d w
   float d_eta0 = 0.f, d_eta1 = 0.f;
 
   {  // d rk = -eta0 d key', d rv = -eta1 d value', w; row norms and softmax statistics
     const int row = tid >> 2, part = tid & 3, t = q.token(row);
-    const float den = key_den<E>(p, q, t, part);
+    const float den = given ? 1.f : key_den<E>(p, q, t, part);
     if (part == 0) {
       den_s[row] = den;
-      mx_s[row] = t >= 0 ? p.stats[q.saved(t, 2)] : 0.f;
-      sm_s[row] = t >= 0 ? p.stats[q.saved(t, 2) + 1] : 1.f;
+      mx_s[row] = t >= 0 && !given ? p.stats[q.saved(t, 2)] : 0.f;
+      sm_s[row] = t >= 0 && !given ? p.stats[q.saved(t, 2) + 1] : 1.f;
       dot_s[row] = 0.f;
     }
     const E* dko = reinterpret_cast<const E*>(g.dkey_out.ptr) + (t >= 0 ? q.at(g.dkey_out, t) : 0);
@@ -396,8 +403,10 @@ __global__ __launch_bounds__(LNT, 1) void level_bwd(gpa_level_problem p, gpa_lev
         if (m < M) {
           float d = 0.f;
           if (tk >= 0) {
-            const float dw = to_f32(reinterpret_cast<const E*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m]);
+            const float dw = g.dwrite.ptr ? to_f32(reinterpret_cast<const E*>(g.dwrite.ptr)[q.at(g.dwrite, tk) + m])
+                                          : 0.f;
             d = round_as<E>(dw + round_as<E>(acc[r]));
+            if (given) reinterpret_cast<E*>(g.dwrite_given.ptr)[q.at(g.dwrite_given, tk) + m] = from_f32<E>(d);
           }
           Y[row * ldm + m] = d;
         }
@@ -406,6 +415,7 @@ __global__ __launch_bounds__(LNT, 1) void level_bwd(gpa_level_problem p, gpa_lev
   }
   __syncthreads();
 
+  if (!given) {  // the write's own backward: softmax, u(key) A^ and the unit normalisation
   {  // u(key) -> X
     const int row = tid >> 2, part = tid & 3, t = q.token(row);
     const float den = den_s[row];
@@ -510,6 +520,7 @@ __global__ __launch_bounds__(LNT, 1) void level_bwd(gpa_level_problem p, gpa_lev
         dk[c] = from_f32<E>(round_as<E>(to_f32(dko[c]) + round_as<E>(unit_bwd)));
       }
     }
+  }
   }
 
   {  // per-block sums of d eta
@@ -709,7 +720,26 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
   float* E = reinterpret_cast<float*>(lds + L.e_off);    // logits, then rk / rv [64][lde]
   const int ldu = L.ldu, ldw = L.ldw, lde = L.lde;
   const bf16_t* key = reinterpret_cast<const bf16_t*>(p.key.ptr);
+  const int M16 = pad16(M) / 16;
 
+  if (p.given_write) {  // the write is given: its rows -> W
+    if (FAST) {
+      const int c = 8 * (tid & 31), r0 = tid >> 5;
+      if (c < M)
+#pragma unroll
+        for (int i = 0; i < RPASS; ++i) {
+          const int r = r0 + 8 * i, t = q.token(r);
+          *reinterpret_cast<uint4*>(&W[r * ldw + c]) =
+              t >= 0 ? *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.write.ptr) + q.at(p.write, t) + c)
+                     : make_uint4(0, 0, 0, 0);
+        }
+    } else
+    for (int r = wave; r < LROWS; r += LW) {
+      const int t = q.token(r);
+      const bf16_t* wi = reinterpret_cast<const bf16_t*>(p.write.ptr) + (t >= 0 ? q.at(p.write, t) : 0);
+      for (int m = lane; m < ldw; m += 64) W[r * ldw + m] = (__bf16)((t >= 0 && m < M) ? to_f32(wi[m]) : 0.f);
+    }
+  } else {
   // u(key)
   if (FAST) {
     const int c32 = tid & 31, c = 8 * c32, r0 = tid >> 5;
@@ -753,7 +783,7 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
   __syncthreads();
 
   // logits = u(key) A^ -> E
-  const int K16 = pad16(Dk) / 16, M16 = pad16(M) / 16, MT = pad32(M) / 32;
+  const int K16 = pad16(Dk) / 16, MT = pad32(M) / 32;
 #pragma unroll 1
   for (int mt = wave; mt < MT; mt += LW) {
     const int m = 32 * mt + li;
@@ -828,6 +858,7 @@ __global__ __launch_bounds__(LNT, 2) void level_fwd16(gpa_level_problem p) {
       }
       if (m < ldw) W[r * ldw + m] = (__bf16)w;
     }
+  }
   }
   __syncthreads();
 
@@ -961,10 +992,11 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
   const float eta0 = p.eta[2 * q.h], eta1 = p.eta[2 * q.h + 1];
   const bf16_t* key = reinterpret_cast<const bf16_t*>(p.key.ptr);
   const int MT = M / 32, KT = Dk / 32, VT = Dv / 32, K16 = Dk / 16, V16 = Dv / 16, M16 = M / 16;
+  const bool given = p.given_write != 0;  // the write is an input: its gradient ends at dw
 
   // ---- rows: norms of the keys (16 rows per pass, 32 lanes per row) and the
   // saved softmax statistics.
-  {
+  if (!given) {
     const int c = 8 * (tid & 31), r0 = tid >> 5;
     uint4 raw[LROWS / 16];
 #pragma unroll
@@ -1013,20 +1045,24 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
       put_t(WT, c, x);
     }
     for (int c = 8 * wave; c < Dk; c += 8 * BW) {  // drk^T, u^T, d eta0
-      const uint4 a = load8(g.dkey_out, c), b = saved8(p.rk, Dk, c), kk = load8(p.key, c);
-      float d[8], r[8], x[8];
+      const uint4 a = load8(g.dkey_out, c), b = saved8(p.rk, Dk, c);
+      float d[8], r[8];
       bf8_to_f32(a, d);
       bf8_to_f32(b, r);
-      bf8_to_f32(kk, x);
-      const float den = den_s[lane];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         d_eta0 -= d[e] * r[e];
         d[e] = round_as<bf16_t>(-eta0 * d[e]);
-        x[e] = x[e] / den;
       }
       put_t(DRKT, c, d);
-      put_t(UT, c, x);
+      if (!given) {
+        float x[8];
+        bf8_to_f32(load8(p.key, c), x);
+        const float den = den_s[lane];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = x[e] / den;
+        put_t(UT, c, x);
+      }
     }
     for (int c = 8 * wave; c < Dv; c += 8 * BW) {  // drv^T, d eta1
       const uint4 a = load8(g.dvalue_out, c), b = saved8(p.rv, Dv, c);
@@ -1073,7 +1109,9 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int tk = q.token(32 * rt + acc_row(r, hh));  // void rows: token 0, masked at use
-      dwr[r] = to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk >= 0 ? tk : 0) + m]);
+      dwr[r] = g.dwrite.ptr
+                   ? to_f32(reinterpret_cast<const bf16_t*>(g.dwrite.ptr)[q.at(g.dwrite, tk >= 0 ? tk : 0) + m])
+                   : 0.f;
     }
     // A fragments from global: drk and u (contraction k), drv (contraction v).
     const bf16_t* dkr = reinterpret_cast<const bf16_t*>(g.dkey_out.ptr) + (trow >= 0 ? q.at(g.dkey_out, trow) : 0);
@@ -1105,7 +1143,7 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
         raw8<true>(bv, s0 + jj < V16 ? c0 : 16 * (V16 - 1) + 8 * hh, vb[jj]);
         if (s0 + jj < K16) {
           rd[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dkr + c0) : make_uint4(0, 0, 0, 0);
-          rk[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
+          rk[jj] = trow >= 0 && !given ? *reinterpret_cast<const uint4*>(kr + c0) : make_uint4(0, 0, 0, 0);
         }
         if (s0 + jj < V16) {
           rv[jj] = trow >= 0 ? *reinterpret_cast<const uint4*>(dvr + c0) : make_uint4(0, 0, 0, 0);
@@ -1117,11 +1155,14 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
           mask8(ak, 16 * (s0 + jj) + 8 * hh, va[jj]);
           bf16x8 bh, bl;
           split8(va[jj], bh, bl);
-          const bf16x8 ad = a_frag(rd[jj], -eta0, false), au = a_frag(rk[jj], 1.f, true);
+          const bf16x8 ad = a_frag(rd[jj], -eta0, false);
           cw[0] = mfma16(ad, bh, cw[0]);
-          cl[0] = mfma16(au, bh, cl[0]);
           cw[1] = mfma16(ad, bl, cw[1]);
-          cl[1] = mfma16(au, bl, cl[1]);
+          if (!given) {
+            const bf16x8 au = a_frag(rk[jj], 1.f, true);
+            cl[0] = mfma16(au, bh, cl[0]);
+            cl[1] = mfma16(au, bl, cl[1]);
+          }
         }
         if (s0 + jj < V16) {
           mask8(bv, 16 * (s0 + jj) + 8 * hh, vb[jj]);
@@ -1138,7 +1179,7 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
     for (int r = 0; r < 16; ++r) {
       const int t = 32 * rt + acc_row(r, hh), tk = q.token(t);
       dk[r] = tk >= 0 ? round_as<bf16_t>(dwr[r] + round_as<bf16_t>(dwa[r])) : 0.f;
-      pk[r] = __expf(lga[r] - mx_s[t]) / sm_s[t];
+      pk[r] = given ? 0.f : __expf(lga[r] - mx_s[t]) / sm_s[t];
     }
   };
   auto add_dot = [&](int i, const float (&pk)[16], const float (&dk)[16]) {
@@ -1159,7 +1200,20 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
       DLL[m * TP + t] = (__bf16)(x - (float)hi);
     }
   };
-  if (TW == 1) {  // one tile per wave: p and dw stay in registers across the row-dot barrier
+  if (given) {  // dw is the given write's gradient
+#pragma unroll 1
+    for (int i = wave; i < 2 * MT; i += BW) {
+      float pk[16], dk[16];
+      dw_logits(i, pk, dk);
+      const int m = 32 * (i >> 1) + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tk = q.token(32 * (i & 1) + acc_row(r, hh));
+        if (tk >= 0)
+          reinterpret_cast<bf16_t*>(g.dwrite_given.ptr)[q.at(g.dwrite_given, tk) + m] = from_f32<bf16_t>(dk[r]);
+      }
+    }
+  } else if (TW == 1) {  // one tile per wave: p and dw stay in registers across the row-dot barrier
     const int i = wave;
     float pk[16], dk[16];
     const bool mine = (i >> 1) < MT;
@@ -1198,8 +1252,10 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
     for (int ts = 0; ts < LROWS / 16; ++ts) {
       const bf16x8 drk = frag_t(DRKT, 32 * kt + li, ts), u = frag_t(UT, 32 * kt + li, ts);
       a1 = mfma16(frag_t(WT, 32 * mt + li, ts), drk, a1);
-      a2 = mfma16(frag_t(DLH, 32 * mt + li, ts), u, a2);
-      a1 = mfma16(frag_t(DLL, 32 * mt + li, ts), u, a1);
+      if (!given) {
+        a2 = mfma16(frag_t(DLH, 32 * mt + li, ts), u, a2);
+        a1 = mfma16(frag_t(DLL, 32 * mt + li, ts), u, a1);
+      }
     }
     const int k = 32 * kt + li;
 #pragma unroll
@@ -1207,6 +1263,7 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
   }
   __syncthreads();  // w^T, drk^T and u^T are dead: du reuses their memory
 
+  if (!given) {
   // ---- du[t][k] = sum_m dl[t][m] A^[k][m], dl rows gathered from dl^T.
   for (int i = wave; i < 2 * KT; i += BW) {
     const int rt = i & 1, kt = i >> 1, k = 32 * kt + li;
@@ -1272,6 +1329,7 @@ __global__ __launch_bounds__(BNT, 1) void level_bwd16(gpa_level_problem p, gpa_l
       }
       *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(g.dkey.ptr) + q.at(g.dkey, t) + c) = f32_to_bf8(dko);
     }
+  }
   }
 
   {  // per-block sums of d eta
@@ -1380,7 +1438,7 @@ int launch_level_bwd(const gpa_level_problem& p, const gpa_level_grads& g, dim3 
 extern "C" int gpa_level_forward(const gpa_level_problem* problem, hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_level(problem)) return rc;
-  if (!problem->key_out.ptr || !problem->value_out.ptr || !problem->stats)
+  if (!problem->key_out.ptr || !problem->value_out.ptr || (!problem->given_write && !problem->stats))
     return fail(GPA_HIP_EINVAL, "level: null output");
   const int N = (problem->offset + problem->tokens + problem->chunk - 1) / problem->chunk;
   const dim3 grid(N, problem->batch * problem->heads);
@@ -1396,9 +1454,12 @@ extern "C" int gpa_level_backward(const gpa_level_problem* problem, const gpa_le
                                   hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_level(problem)) return rc;
-  if (!grads || !grads->dwrite.ptr || !grads->dkey_out.ptr || !grads->dvalue_out.ptr || !grads->dkey.ptr ||
-      !grads->da_states || !grads->db_states || !grads->deta || !problem->stats ||
-      (problem->a_first && !grads->da_first) || (problem->b_first && !grads->db_first))
+  const bool given = problem->given_write != 0;
+  if (!grads || !grads->dkey_out.ptr || !grads->dvalue_out.ptr ||
+      (given ? !grads->dwrite_given.ptr : (!grads->dwrite.ptr || !grads->dkey.ptr || !problem->stats)) ||
+      !grads->da_states ||
+      !grads->db_states || !grads->deta || (problem->a_first && !grads->da_first) ||
+      (problem->b_first && !grads->db_first))
     return fail(GPA_HIP_EINVAL, "level: null gradient buffer");
   const int N = (problem->offset + problem->tokens + problem->chunk - 1) / problem->chunk;
   const dim3 grid(N, problem->batch * problem->heads);

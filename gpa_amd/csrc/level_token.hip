@@ -317,6 +317,7 @@ int check_level_token(const gpa_level_problem* problem) {
     return fail(GPA_HIP_EINVAL, "level token: null pointer (the snapshots a_first and b_first are required)");
   if (!p.key_out.ptr != !p.value_out.ptr)
     return fail(GPA_HIP_EINVAL, "level token: key_out and value_out are both given or both null (write only)");
+  if (p.given_write) return fail(GPA_HIP_EUNSUPPORTED, "level token: the one-token kernels form their own write");
   return GPA_HIP_OK;
 }
 

@@ -10,7 +10,10 @@ The snapshots are the scans' chunk-start states, read in place (value-major,
 as `gdn_scan_hip` saves them), except block 0 when the call starts inside a
 block: then it is the cached snapshot.  `level_mix` is differentiable in the
 keys, values, both state tensors, the cached snapshots and eta; the state
-gradients come back in the states' own layout.
+gradients come back in the states' own layout.  `level_residual` is the same
+step for a write that is given (rsa_update's softmax(slot / .25) or softmax
+slot features, attention.py:186-188): only the reconstructions and the
+residual run on the kernels, and the write gets its gradient through them.
 """
 from __future__ import annotations
 
@@ -21,8 +24,9 @@ from . import _lib
 
 
 def supported(cfg, dtype: torch.dtype, key_dim: int, value_dim: int, slots: int) -> bool:
-    return (dtype in _lib.DTYPE_CODES and cfg.slot_feature == "linear" and not cfg.rsa_update
-            and max(key_dim, value_dim, slots) <= _lib.LEVEL_MAX_WIDTH and cfg.chunk_size <= 64)
+    """Whether the level kernels take these widths (either write mode)."""
+    return (dtype in _lib.DTYPE_CODES and max(key_dim, value_dim, slots) <= _lib.LEVEL_MAX_WIDTH
+            and cfg.chunk_size <= 64)
 
 
 def _snapshot(t: Tensor | None) -> tuple[Tensor | None, int]:
@@ -49,8 +53,31 @@ def _problem(key, value, a_vm, b_vm, a_first, b_first, eta, chunk, offset, outs,
     p.b_first, p.b_first_sb = (bf.data_ptr() if bf is not None else None), bsb
     p.eta = eta.data_ptr()
     p.write, p.key_out, p.value_out = (_lib.operand(t) for t in outs)
-    p.rk, p.rv, p.stats = (t.data_ptr() for t in saved)
+    p.rk, p.rv, p.stats = (t.data_ptr() if t is not None else None for t in saved)
     return p
+
+
+def _inputs(key, value, a_vm, b_vm, a_first, b_first, eta):
+    """The kernels' operand layouts: contiguous activations, float32
+    contiguous states, [B,H,R,C] snapshots (with their batch strides) and eta."""
+    key, value = key.contiguous(), value.contiguous()
+    a_vm, b_vm = a_vm.detach().float().contiguous(), b_vm.detach().float().contiguous()
+    return key, value, a_vm, b_vm, (_snapshot(a_first), _snapshot(b_first)), eta.detach().float().contiguous()
+
+
+def _state_grads(key, a_vm, b_vm, af, bf):
+    """Gradient buffers of the block states (block 0 zeroed where the cached
+    snapshots stand in for it) and of the cached snapshots."""
+    bsz, _, heads, dk = key.shape
+    da, db = torch.empty_like(a_vm), torch.empty_like(b_vm)
+    if af is not None:
+        da[:, :, 0].zero_()
+    if bf is not None:
+        db[:, :, 0].zero_()
+    da_first = torch.empty(bsz, heads, dk, a_vm.shape[-2], device=key.device) if af is not None else None
+    m, dv = b_vm.shape[-1], b_vm.shape[-2]  # b_vm is value-major [B,H,N,Dv,M]
+    db_first = torch.empty(bsz, heads, m, dv, device=key.device) if bf is not None else None
+    return da, db, da_first, db_first
 
 
 class _LevelMix(torch.autograd.Function):
@@ -62,10 +89,7 @@ class _LevelMix(torch.autograd.Function):
         dtype = key.dtype
         bsz, tokens, heads, dk = key.shape
         dv, m = value.shape[-1], a_vm.shape[-2]
-        key, value = key.contiguous(), value.contiguous()
-        a_vm, b_vm = a_vm.detach().float().contiguous(), b_vm.detach().float().contiguous()
-        firsts = (_snapshot(a_first), _snapshot(b_first))
-        eta = eta.detach().float().contiguous()
+        key, value, a_vm, b_vm, firsts, eta = _inputs(key, value, a_vm, b_vm, a_first, b_first, eta)
         write = torch.empty(bsz, tokens, heads, m, device=key.device, dtype=dtype)
         key_out, value_out = torch.empty_like(key), torch.empty_like(value)
         rk = torch.empty(bsz, tokens, heads, dk, device=key.device, dtype=dtype)
@@ -93,14 +117,7 @@ class _LevelMix(torch.autograd.Function):
         prob = _problem(key, value, a_vm, b_vm, (af, ctx.first_sb[0]), (bf, ctx.first_sb[1]), eta, ctx.chunk,
                         ctx.offset, (write, write, write), (rk, rv, stats))
         prob.key_out, prob.value_out = _lib.operand(key), _lib.operand(value)
-        da = torch.empty_like(a_vm)
-        db = torch.empty_like(b_vm)
-        if af is not None:
-            da[:, :, 0].zero_()
-        if bf is not None:
-            db[:, :, 0].zero_()
-        da_first = torch.empty(bsz, heads, dk, a_vm.shape[-2], device=key.device) if af is not None else None
-        db_first = torch.empty(bsz, heads, b_vm.shape[-1], dv, device=key.device) if bf is not None else None
+        da, db, da_first, db_first = _state_grads(key, a_vm, b_vm, af, bf)
         nblocks = a_vm.shape[2]
         deta = torch.empty(bsz * heads * nblocks, 2, device=key.device)
         dkey = torch.empty_like(key)
@@ -117,6 +134,59 @@ class _LevelMix(torch.autograd.Function):
             # the outer scan's state backward is not woken for nothing
             db, db_first, dvalue_out = None, None, None
         return dkey, dvalue_out, da, db, da_first, db_first, deta, None, None
+
+
+class _LevelResidual(torch.autograd.Function):
+    """(key', value') of one level whose write is an input: the kernels' given-
+    write mode.  The backward returns the write's gradient through A^ w and
+    w^T B^ (its other uses add theirs in autograd); key' depends on the key
+    only through the subtraction, so d key = d key'."""
+
+    @staticmethod
+    def forward(ctx, key, value, write, a_vm, b_vm, a_first, b_first, eta, chunk, offset):
+        _lib.require_device(key)
+        ctx.set_materialize_grads(False)
+        lib = _lib.load()
+        key, value, a_vm, b_vm, firsts, eta = _inputs(key, value, a_vm, b_vm, a_first, b_first, eta)
+        write = write.to(key.dtype).contiguous()
+        key_out, value_out = torch.empty_like(key), torch.empty_like(value)
+        rk, rv = torch.empty_like(key), torch.empty_like(value)
+        prob = _problem(key, value, a_vm, b_vm, *firsts, eta, chunk, offset, (write, key_out, value_out),
+                        (rk, rv, None))
+        prob.given_write = 1
+        _lib.check(lib.gpa_level_forward(prob, _lib.stream_handle(key.device)), "gpa_level_forward")
+        ctx.chunk, ctx.offset = chunk, offset
+        ctx.first_sb = (firsts[0][1], firsts[1][1])
+        ctx.save_for_backward(key, value, a_vm, b_vm, firsts[0][0], firsts[1][0], eta, write, rk, rv)
+        return key_out, value_out
+
+    @staticmethod
+    def backward(ctx, dkey_out, dvalue_out):
+        if dkey_out is None and dvalue_out is None:
+            return (None,) * 10
+        lib = _lib.load()
+        key, value, a_vm, b_vm, af, bf, eta, write, rk, rv = ctx.saved_tensors
+        bsz, _, heads, _ = key.shape
+        value_used = dvalue_out is not None
+        zeros = lambda t, like: torch.zeros_like(like) if t is None else t.to(key.dtype).contiguous()  # noqa: E731
+        dkey_out, dvalue_out = zeros(dkey_out, key), zeros(dvalue_out, value)
+        prob = _problem(key, value, a_vm, b_vm, (af, ctx.first_sb[0]), (bf, ctx.first_sb[1]), eta, ctx.chunk,
+                        ctx.offset, (write, key, value), (rk, rv, None))
+        prob.given_write = 1
+        da, db, da_first, db_first = _state_grads(key, a_vm, b_vm, af, bf)
+        nblocks = a_vm.shape[2]
+        deta = torch.empty(bsz * heads * nblocks, 2, device=key.device)
+        dwrite = torch.empty_like(write)
+        gr = _lib.LevelGrads()
+        gr.dkey_out, gr.dvalue_out, gr.dwrite_given = (_lib.operand(t) for t in (dkey_out, dvalue_out, dwrite))
+        gr.da_states, gr.db_states, gr.deta = da.data_ptr(), db.data_ptr(), deta.data_ptr()
+        gr.da_first = da_first.data_ptr() if da_first is not None else None
+        gr.db_first = db_first.data_ptr() if db_first is not None else None
+        _lib.check(lib.gpa_level_backward(prob, gr, _lib.stream_handle(key.device)), "gpa_level_backward")
+        deta = deta.view(bsz, heads, nblocks, 2).sum((0, 2))
+        if not value_used:
+            db, db_first, dvalue_out = None, None, None
+        return dkey_out, dvalue_out, dwrite, da, db, da_first, db_first, deta, None, None
 
 
 def _block_problem(key: Tensor, value: Tensor, a_first: Tensor, b_first: Tensor, eta: Tensor, chunk: int,
@@ -220,3 +290,11 @@ def level_mix(key: Tensor, value: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: T
     states; a_first [B,H,Dk,M] / b_first [B,H,M,Dv]: cached block-0 snapshots
     (None: block 0 is the scans' initial state); eta [H,2]."""
     return _LevelMix.apply(key, value, a_vm, b_vm, a_first, b_first, eta, chunk, offset)
+
+
+def level_residual(key: Tensor, value: Tensor, write: Tensor, a_vm: Tensor, b_vm: Tensor, a_first: Tensor | None,
+                   b_first: Tensor | None, eta: Tensor, chunk: int, offset: int):
+    """(key', value') of one level whose write [B,T,H,M] is given (arguments
+    otherwise as `level_mix`): key' = key - eta0 round(A^ w), value' = value -
+    eta1 round(w^T B^), differentiable in the write as in everything else."""
+    return _LevelResidual.apply(key, value, write, a_vm, b_vm, a_first, b_first, eta, chunk, offset)

@@ -37,7 +37,7 @@ from .counts import count_logits
 from .slots import slot_gates, slot_gates_act
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
-from .level import level_mix, level_mix_block, token_step_and_level, write_only_supported
+from .level import level_mix, level_mix_block, level_residual, token_step_and_level, write_only_supported
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
 from .route import product_read
@@ -222,8 +222,9 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             g_in, b_in, g_out, b_out = _gates(model, key, j, control)
         eta = _etas(model)[j]
         write = _assignment(cfg, slot)
-        fused_level = write is None and _FUSED_LEVEL[0] and fused_level_supported(
+        level_kernels = _FUSED_LEVEL[0] and fused_level_supported(
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
+        fused_level = write is None and level_kernels
         if token and fused_level and token_step_supported(key, slot) and token_step_supported(slot, value):
             step = (qr, key, slot, g_in, b_in, old.inner)
             # the last level's residual is never read (attention.py:327-329 after the
@@ -257,7 +258,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             # slot features): the A_j token step, then the residual from the cached block snapshots
             raw, a_final = gdn_token_hip(qr, key, slot, g_in, b_in, old.inner)
             write = write.to(dtype)
-            key_next, value_next = _token_residual(key, value, snap.inner, snap.outer, write, eta)
+            key_next, value_next = (_token_residual(key, value, snap.inner, snap.outer, write, eta)
+                                    if j + 1 < len(state.levels) else (None, None))  # the last is never read
             lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
             lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
             lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
@@ -294,6 +296,13 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         if fused_level:
             write, key_next, value_next = level_mix(key, value, a_starts.transpose(-1, -2),
                                                     b_starts.transpose(-1, -2), first_a, first_b, eta, chunk, offset)
+        elif write is not None and j + 1 == len(state.levels):
+            # a given write at the last level: its residual is never read
+            write, key_next, value_next = write.to(dtype), None, None
+        elif level_kernels:
+            write = write.to(dtype)
+            key_next, value_next = level_residual(key, value, write, a_starts.transpose(-1, -2),
+                                                  b_starts.transpose(-1, -2), first_a, first_b, eta, chunk, offset)
         else:
             write, key_next, value_next = _level_mix_torch(key, value, a_starts, b_starts, snap.inner, snap.outer,
                                                            eta, blocks, write)

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 23
+#define GPA_HIP_ABI_VERSION 24
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -425,19 +425,28 @@ typedef struct gpa_level_problem {
     gpa_operand write, key_out, value_out;   /* outputs */
     void *rk, *rv;                       /* saved rounded reconstructions, contiguous [B,T,H,Dk], [B,T,H,Dv] */
     float *stats;                        /* saved softmax row max and sum, contiguous [B,T,H,2] */
+    int32_t given_write;                 /* nonzero: `write` is an input (a write that does not read the
+                                            snapshots); stats are then neither written nor read */
 } gpa_level_problem;
 
 typedef struct gpa_level_grads {
-    gpa_operand dwrite, dkey_out, dvalue_out;  /* incoming; dwrite excludes the rk/rv paths */
+    gpa_operand dwrite, dkey_out, dvalue_out;  /* incoming; dwrite excludes the rk/rv paths (with
+                                                  given_write it may be null: zero) */
     gpa_operand dkey;                          /* out: the gradient of key through this step */
     float *da_states, *db_states;              /* out, layouts of a_states / b_states (block 0 included
                                                   unless a_first is given) */
     float *da_first, *db_first;                /* out when a_first / b_first are given: [B,H][Dk][M], [B,H][M][Dv] */
     float *deta;                               /* out [B*H*N][2]: per-block sums of d eta0, d eta1 */
+    gpa_operand dwrite_given;                  /* out when problem->given_write: the gradient of the
+                                                  given write, dwrite + (drk A^ + drv B^T) rounded;
+                                                  dkey is then not written (it equals dkey_out) */
 } gpa_level_grads;
 
 /* Forward / backward of the level write and residual (the reference's level
- * glue at attention.py:314-329, autograd through it for the backward). */
+ * glue at attention.py:314-329, autograd through it for the backward).  With
+ * given_write the write comes from the slot products (rsa_update's
+ * softmax(slot / .25), or softmax slot features: attention.py:186-188) and the
+ * kernels form only the reconstructions and the residual step. */
 int gpa_level_forward(const gpa_level_problem *problem, hipStream_t stream);
 int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *grads, hipStream_t stream);
 
@@ -448,7 +457,8 @@ int gpa_level_backward(const gpa_level_problem *problem, const gpa_level_grads *
  * key_out = key - eta0 round(A^ write), value_out = value - eta1 round(write^T B^).
  * With key_out and value_out both null the write alone is formed and B^ is
  * not read (the last level, whose residual nothing reads; shapes of the
- * register kernel only, e.g. Dk = 128 with M up to 256).
+ * register kernel only, e.g. Dk = 128 with M up to 256).  given_write is
+ * not taken (EUNSUPPORTED).
  * Replaces reference src/gpa/attention.py:314-329 and :190-194 at T = 1. */
 int gpa_level_token_forward(const gpa_level_problem *problem, hipStream_t stream);
 /* A level's inner one-token step and its one-token level write in one launch

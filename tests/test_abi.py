@@ -68,8 +68,8 @@ def test_ctypes_structs_match_c_layout():
     # 7 operands, 4 pointers
     assert ctypes.sizeof(_lib.RouteGrads) == 7 * 32 + 5 * 8 + 2 * 32 + 8
     # 9 int32 (+pad), 2 operands, 4 pointers, 2 int64, 1 pointer, 3 operands, 3 pointers
-    assert ctypes.sizeof(_lib.LevelProblem) == 40 + 2 * 32 + 4 * 8 + 2 * 8 + 8 + 3 * 32 + 3 * 8
-    assert ctypes.sizeof(_lib.LevelGrads) == 4 * 32 + 5 * 8
+    assert ctypes.sizeof(_lib.LevelProblem) == 40 + 2 * 32 + 4 * 8 + 2 * 8 + 8 + 3 * 32 + 3 * 8 + 8
+    assert ctypes.sizeof(_lib.LevelGrads) == 4 * 32 + 5 * 8 + 32
     # 5 int32 (+pad), 2 operands, count0 + its stride, 5 pointers
     assert ctypes.sizeof(_lib.CountProblem) == 24 + 2 * 32 + 2 * 8 + 5 * 8
     assert ctypes.sizeof(_lib.CountGrads) == 2 * 8 + 2 * 32 + 3 * 8

@@ -128,3 +128,66 @@ def test_host_built_level_mix_block_matches_level_mix(first, runner, tmp_path, m
         got = level.level_mix_block(key, value, fa, fb, eta, c, off)
     for a, r in zip(got, ref):
         assert torch.equal(a, r)
+
+
+def _run_given(spec, fused, key, value, a_vm, b_vm, fa, fb, raw, logits):
+    """The level step with a given write (rsa_update's softmax(slot / .25)):
+    torch forms the write from `logits`, the glue or the kernels' given-write
+    mode the residual; the write also enters the loss directly, as its other
+    uses (counts, relations) do."""
+    leaves = [x.clone().requires_grad_() for x in (key, value, a_vm, b_vm, raw, logits)]
+    firsts = [x.clone().requires_grad_() if x is not None else None for x in (fa, fb)]
+    key, value, a_vm, b_vm, raw, logits = leaves
+    fa, fb = firsts
+    if spec["first"] == "broadcast":
+        fa_in, fb_in = (x.unsqueeze(0).expand(spec["b"], *x.shape) for x in (fa, fb))
+    else:
+        fa_in, fb_in = fa, fb
+    eta = 1 + .25 * raw.tanh()
+    write = (logits / .25).softmax(-1).to(key.dtype)
+    a_starts, b_starts = a_vm.transpose(-1, -2), b_vm.transpose(-1, -2)
+    if fused:
+        outs = (write,) + level.level_residual(key, value, write, a_vm, b_vm, fa_in, fb_in, eta, spec["c"],
+                                               spec["offset"])
+    else:
+        blocks = schedule._Blocks(spec["t"], spec["offset"], spec["c"])
+        snap_a = fa_in if fa_in is not None else a_starts[:, :, 0]
+        snap_b = fb_in if fb_in is not None else b_starts[:, :, 0]
+        outs = schedule._level_mix_torch(key, value, a_starts, b_starts, snap_a, snap_b, eta, blocks, write)
+    gen = torch.Generator().manual_seed(23)
+    loss = sum((x.float() * torch.randn(x.shape, generator=gen)).sum() for x in outs)
+    loss.backward()
+    grads = {"key": key.grad, "value": value.grad, "a_states": a_vm.grad, "b_states": b_vm.grad,
+             "residual": raw.grad, "write_logits": logits.grad}
+    if fa is not None:
+        grads.update(a_first=fa.grad, b_first=fb.grad)
+    return outs, grads
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("name", list(CASES))
+def test_host_built_level_residual_with_a_given_write(name, dtype, runner, tmp_path, monkeypatch):
+    """The given-write mode (gpa_level_problem.given_write) against the glue
+    with the same write: key', value' and every gradient, the write's through
+    both reconstructions and its direct use."""
+    spec = CASES[name]
+    if name == "c3_widths" and dtype == torch.float32:
+        pytest.skip("C3 widths covered in bfloat16")
+    inputs = _inputs(spec, dtype)
+    g = torch.Generator().manual_seed(29)
+    logits = torch.randn(spec["b"], spec["t"], spec["h"], spec["m"], generator=g).to(dtype)
+    ref_out, ref_grads = _run_given(spec, False, *inputs, logits)
+    harness.use_host(monkeypatch, harness.HostLib(runner, str(tmp_path)))
+    got_out, got_grads = _run_given(spec, True, *inputs, logits)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    errors = {}
+    for label, a, b in zip(("write", "key'", "value'"), got_out, ref_out):
+        assert a.dtype == b.dtype == dtype and a.shape == b.shape, label
+        errors[label] = _rel(a, b)
+    for k in ref_grads:
+        assert got_grads[k] is not None and got_grads[k].shape == ref_grads[k].shape, k
+        errors["grad/" + k] = _rel(got_grads[k], ref_grads[k])
+    worst = max(errors.items(), key=lambda kv: kv[1])
+    print(name, dtype, "worst", worst)
+    bad = {k: v for k, v in errors.items() if v > tol}
+    assert not bad, bad
