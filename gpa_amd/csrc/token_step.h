@@ -1,4 +1,4 @@
-// The one-token GDN step of one 64-column block of one stream's state (the
+// The one-token GDN step of one column block of one stream's state (the
 // inference decode of the chunk model at T = 1): reference src/gpa/ops.py:29-42
 // (gdn_update) then :45-46 (memory_read).  Shared by the one-token step
 // kernels and the kernel that runs a level's inner step beside its one-token
@@ -10,22 +10,34 @@
 namespace gpa {
 namespace {
 
-constexpr int SNT = 256;   // threads per workgroup: 16 column quads x 16 row groups
-constexpr int SCOL = 64;   // state columns per workgroup
+constexpr int SNT = 256;   // threads per workgroup
 
-// Sum of the four row groups that share a wave's column quad (lanes c, c+16,
-// c+32, c+48), then of the four waves through LDS; every thread returns the
-// total of its quad.
-__device__ __forceinline__ float4 column_sums(float4 x, float4 (*part)[16], int wave, int rg, int c4) {
-  x.x += __shfl_xor(x.x, 16, 64);
-  x.y += __shfl_xor(x.y, 16, 64);
-  x.z += __shfl_xor(x.z, 16, 64);
-  x.w += __shfl_xor(x.w, 16, 64);
-  x.x += __shfl_xor(x.x, 32, 64);
-  x.y += __shfl_xor(x.y, 32, 64);
-  x.z += __shfl_xor(x.z, 32, 64);
-  x.w += __shfl_xor(x.w, 32, 64);
-  if ((rg & 3) == 0) part[wave][c4] = x;
+// The row classes (K <= 16 NI): a workgroup owns SC columns of one stream's
+// state, thread t columns 4 (t % CQ) .. +3 of rows t / CQ + RG i, i < NR.
+// K <= 128 takes 64-column blocks (16 column quads x 16 row groups); the
+// 256-row class takes 32-column blocks (8 x 32), so that a thread holds 8
+// rows as at K = 128, not 16: half the registers, twice the workgroups
+// resident per compute unit.
+template <int NI>
+struct TokenShape {
+  static constexpr int SC = NI == 16 ? 32 : 64;
+  static constexpr int CQ = SC / 4, RG = SNT / CQ, NR = 16 * NI / RG;
+};
+__host__ __device__ constexpr int token_cols(int ni) { return ni == 16 ? 32 : 64; }
+
+// Sum of the row groups that share a wave's column quad (lanes c, c + CQ,
+// ...), then of the four waves through LDS; every thread returns the total
+// of its quad.
+template <int CQ>
+__device__ __forceinline__ float4 column_sums(float4 x, float4 (*part)[CQ], int wave, int rg, int c4) {
+#pragma unroll
+  for (int m = CQ; m < 64; m *= 2) {
+    x.x += __shfl_xor(x.x, m, 64);
+    x.y += __shfl_xor(x.y, m, 64);
+    x.z += __shfl_xor(x.z, m, 64);
+    x.w += __shfl_xor(x.w, m, 64);
+  }
+  if ((rg & (64 / CQ - 1)) == 0) part[wave][c4] = x;
   lds_barrier();
   float4 s = part[0][c4];
 #pragma unroll
@@ -39,13 +51,12 @@ __device__ __forceinline__ float4 column_sums(float4 x, float4 (*part)[16], int 
   return s;
 }
 
-// Workgroup wg of one problem (one 64-column block of one stream); NI rows
-// per thread: K <= 16 NI.
+// Workgroup wg of one problem (one SC-column block of one stream).
 template <int NI>
 struct TokenLds {
   float kh[16 * NI], qh[16 * NI];
   float norms[2][4];
-  float4 part[2][4][16];
+  float4 part[2][4][TokenShape<NI>::CQ];
 };
 
 // t: the thread's index in its 256-thread unit; every thread of the
@@ -54,33 +65,35 @@ struct TokenLds {
 template <typename E, int NI>
 __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, const gpa_operand& out, int wg, int t,
                                           TokenLds<NI>& L) {
+  constexpr int SC = TokenShape<NI>::SC, CQ = TokenShape<NI>::CQ, RG = TokenShape<NI>::RG;
+  constexpr int NR = TokenShape<NI>::NR;
   float* const kh = L.kh;
   float* const qh = L.qh;
   float (*const norms)[4] = L.norms;
-  float4 (*const part)[4][16] = L.part;
-  const int ncb = (p.vdim + SCOL - 1) / SCOL;
+  float4 (*const part)[4][CQ] = L.part;
+  const int ncb = (p.vdim + SC - 1) / SC;
   const int s = wg / ncb, cb = wg - s * ncb;
   const int b = s / p.heads, h = s - b * p.heads;
   const int lane = t & 63, wave = t >> 6;
-  const int c4 = t & 15, rg = t >> 4;
+  const int c4 = t % CQ, rg = t / CQ;
   const int K = p.kdim, V = p.vdim;
-  const int col = SCOL * cb + 4 * c4;
+  const int col = SC * cb + 4 * c4;
   const bool cok = col < V;  // V % 4 == 0: a quad is all inside or all outside
   const int cc = cok ? col : 0;
   const bool update = p.k.ptr != nullptr, has_q = p.q.ptr != nullptr;
 
   // Every load first, at clamped addresses; masks afterwards.
   const float* s0 = p.s0 ? p.s0 + (int64_t)b * p.s0_sb + (int64_t)h * p.s0_sh : nullptr;
-  float4 st[NI];
+  float4 st[NR];
   if (s0) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = rg + 16 * i;
+    for (int i = 0; i < NR; ++i) {
+      const int row = rg + RG * i;
       st[i] = *reinterpret_cast<const float4*>(s0 + (int64_t)(row < K ? row : 0) * V + cc);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < NR; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const int tk = t < K ? t : 0;
   float xk = 0.f, xq = 0.f, vv[4] = {0.f, 0.f, 0.f, 0.f}, g = 0.f, beta = 0.f;
@@ -95,8 +108,8 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
   xk = t < K ? xk : 0.f;
   xq = t < K ? xq : 0.f;
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const bool ok = s0 && cok && rg + 16 * i < K;
+  for (int i = 0; i < NR; ++i) {
+    const bool ok = s0 && cok && rg + RG * i < K;
     st[i] = ok ? st[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
@@ -121,8 +134,8 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
     const float a = expf(g);
     float4 pk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float kr = kh[rg + 16 * i];
+    for (int i = 0; i < NR; ++i) {
+      const float kr = kh[rg + RG * i];
       st[i].x *= a;
       st[i].y *= a;
       st[i].z *= a;
@@ -132,12 +145,12 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
       pk.z += kr * st[i].z;
       pk.w += kr * st[i].w;
     }
-    const float4 pred = column_sums(pk, part[0], wave, rg, c4);
+    const float4 pred = column_sums<CQ>(pk, part[0], wave, rg, c4);
     const float r0 = vv[0] - pred.x, r1 = vv[1] - pred.y, r2 = vv[2] - pred.z, r3 = vv[3] - pred.w;
     float* dst = fin + (int64_t)s * K * V;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = rg + 16 * i;
+    for (int i = 0; i < NR; ++i) {
+      const int row = rg + RG * i;
       const float kr = kh[row];
       st[i].x += beta * (kr * r0);
       st[i].y += beta * (kr * r1);
@@ -150,15 +163,15 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
   if (has_q) {
     float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float qr = qh[rg + 16 * i];
+    for (int i = 0; i < NR; ++i) {
+      const float qr = qh[rg + RG * i];
       po.x += qr * st[i].x;
       po.y += qr * st[i].y;
       po.z += qr * st[i].z;
       po.w += qr * st[i].w;
     }
-    const float4 o = column_sums(po, part[1], wave, rg, c4);
-    if (t < 16 && cok) {
+    const float4 o = column_sums<CQ>(po, part[1], wave, rg, c4);
+    if (t < CQ && cok) {
       E* op = reinterpret_cast<E*>(out.ptr) + op_base(out, b, h) + col;
       op[0] = from_f32<E>(o.x);
       op[1] = from_f32<E>(o.y);
@@ -168,10 +181,11 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
   }
 }
 
-int64_t token_workgroups(const gpa_gdn_problem& p) {
-  return (int64_t)p.batch * p.heads * ((p.vdim + SCOL - 1) / SCOL);
-}
 int token_rows(const gpa_gdn_problem& p) { return p.kdim <= 64 ? 4 : (p.kdim <= 128 ? 8 : 16); }
+int64_t token_workgroups(const gpa_gdn_problem& p) {
+  const int sc = token_cols(token_rows(p));
+  return (int64_t)p.batch * p.heads * ((p.vdim + sc - 1) / sc);
+}
 
 bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
 

@@ -520,7 +520,7 @@ def _token_call(q, k, v, g, beta, s0):
 
 def gdn_token_many(calls) -> list[tuple[Tensor | None, Tensor]]:
     """`gdn_token_hip` of several independent groups, for inference: one
-    launch per element type and key-width class (`gpa_gdn_token_step_many`)
+    launch per element type, every key width in it (`gpa_gdn_token_step_many`),
     instead of one per group.  `calls` holds gdn_token_hip's argument tuples
     (q, k, v, g, beta, s0), at most `_lib.TOKEN_MAX_PACK` of them, on one
     device; returns [(out, final)] in the same order."""

@@ -223,7 +223,7 @@ int gpa_gdn_scan_noalloc(const gpa_gdn_problem *problem, gpa_operand out, float 
 int gpa_gdn_token_step(const gpa_gdn_problem *problem, float *final_state, gpa_operand out, hipStream_t stream);
 /* gpa_gdn_token_step of up to GPA_TOKEN_MAX_PACK independent problems
  * (final_states[i], outs[i] belong to problems[i]) in one launch per element
- * type and key-width class (K <= 64, <= 128, <= 256) present: the one-token
+ * type present, every key width (K <= 256) in the same launch: the one-token
  * steps of every relation edge (the _relations loop, attention.py:206-223)
  * or of every level's outer memory (attention.py:333-339) at once.  Results
  * are those of one gpa_gdn_token_step per problem; the problems must not

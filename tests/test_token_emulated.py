@@ -55,7 +55,8 @@ def _call(g, b, h, k, v, dtype, s0, query):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("b,h,k,v,s0,query", [(2, 1, 20, 12, None, True), (1, 2, 200, 4, "broadcast", True),
-                                              (2, 3, 64, 96, "full", False), (1, 1, 128, 128, "full", True)])
+                                              (2, 3, 64, 96, "full", False), (1, 1, 128, 128, "full", True),
+                                              (1, 2, 256, 128, "full", True), (2, 1, 160, 36, None, True)])
 def test_token_step_matches_oracle_step_and_read(host, b, h, k, v, s0, query, dtype):
     g = torch.Generator().manual_seed(b * 7 + k + v)
     q, key, val, lg, beta, state = _call(g, b, h, k, v, dtype, s0, query)
@@ -123,8 +124,9 @@ def test_level_token_kernel_matches_block_kernel(host, monkeypatch, b, h, dk, dv
                                             ((1, 2, 128, 256), (1, 2, 128, 256, 128)),
                                             ((3, 2, 128, 64), (2, 2, 128, 128, 128)),
                                             ((4, 2, 100, 128), (1, 2, 128, 128, 128)),
+                                            ((1, 2, 256, 128), (1, 2, 128, 128, 128)),
                                             ((2, 1, 20, 12), (2, 1, 20, 12, 8))],
-                         ids=["m128", "m256", "fewer_steps", "more_steps", "two_launches"])
+                         ids=["m128", "m256", "fewer_steps", "more_steps", "k256", "two_launches"])
 def test_token_level_matches_separate_calls(host, step_shape, lvl, dtype):
     g = torch.Generator().manual_seed(sum(step_shape) + sum(lvl))
     step = _call(g, *step_shape, dtype, "full", True)
