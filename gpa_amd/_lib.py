@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 24
+ABI_VERSION = 25
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -161,6 +161,10 @@ class GateProblem(ctypes.Structure):
                [(n, c_vp) for n in ("g_in", "b_in", "g_out", "b_out")]
 
 
+class TokenSlot(ctypes.Structure):
+    _fields_ = [("center", c_vp), ("gate_w", c_vp), ("gates", GateProblem), ("slot", Operand)]
+
+
 TOKEN_LOGITS_MAX_SLOTS = 256
 TOKEN_LOGITS_MAX_PACK = 8
 
@@ -192,6 +196,8 @@ EXPORTS = {
     "gpa_level_token_forward": ([ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
     "gpa_token_level_forward": ([ctypes.POINTER(Problem), c_vp, Operand, ctypes.POINTER(LevelProblem), c_vp],
                                 ctypes.c_int),
+    "gpa_token_slot_step": ([ctypes.POINTER(Problem), ctypes.POINTER(TokenSlot), c_vp, Operand,
+                             ctypes.POINTER(LevelProblem), c_vp], ctypes.c_int),
     "gpa_gdn_forward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Operand), c_i32,
                               ctypes.POINTER(Timing), c_vp], ctypes.c_int),
     "gpa_gdn_backward_many": ([ctypes.POINTER(Problem), ctypes.POINTER(Saved), ctypes.POINTER(Grads), c_i32,

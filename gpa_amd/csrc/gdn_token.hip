@@ -15,7 +15,7 @@ namespace {
 template <typename E, int NI>
 __global__ __launch_bounds__(SNT) void gdn_token_step(gpa_gdn_problem p, float* fin, gpa_operand out) {
   __shared__ TokenLds<NI> lds;
-  token_run<E, NI>(p, fin, out, blockIdx.x, threadIdx.x, lds);
+  token_run<E, NI>(p, fin, out, blockIdx.x, threadIdx.x, lds, gpa_token_slot{});
 }
 
 // Several problems with the same element type in one launch: workgroups
@@ -52,9 +52,10 @@ __global__ __launch_bounds__(SNT) void gdn_token_step_pack(TokenPack pk) {
     TokenLds<16> c16;
   } lds;
   const int wg = (int)blockIdx.x - kp->wg0[pi], ni = kp->ni[pi];
-  if (ni == 4) token_run<E, 4>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c4);
-  else if (ni == 8) token_run<E, 8>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c8);
-  else token_run<E, 16>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c16);
+  const gpa_token_slot none{};
+  if (ni == 4) token_run<E, 4>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c4, none);
+  else if (ni == 8) token_run<E, 8>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c8, none);
+  else token_run<E, 16>(p, kp->fin[pi], out, wg, threadIdx.x, lds.c16, none);
 }
 
 template <typename E>

@@ -21,14 +21,22 @@ __device__ __forceinline__ float sigmoid1(float x) { return 1.f / (1.f + expf(-x
 // 166-174): x = float(raw) + bias; decay -min(softplus(x), 10) * decay_scale,
 // strength beta_max sigmoid(x).  `raw` holds the four gate inputs as rounded
 // to the activation type; `i` indexes the [B,T,H] outputs.
-__device__ __forceinline__ void gate_row(const gpa_gate_problem& p, int h, int64_t i, const float raw[4]) {
+__device__ __forceinline__ void gate_values(const gpa_gate_problem& p, int h, const float raw[4], float v[4]) {
   float x[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) x[c] = raw[c] + p.bias[4 * h + c];
-  p.g_in[i] = __fmul_rn(-fminf(softplus20(x[0]), 10.f), p.decay_scale);
-  p.b_in[i] = __fmul_rn(p.beta_max, sigmoid1(x[1]));
-  p.g_out[i] = __fmul_rn(-fminf(softplus20(x[2]), 10.f), p.decay_scale);
-  p.b_out[i] = __fmul_rn(p.beta_max, sigmoid1(x[3]));
+  v[0] = __fmul_rn(-fminf(softplus20(x[0]), 10.f), p.decay_scale);
+  v[1] = __fmul_rn(p.beta_max, sigmoid1(x[1]));
+  v[2] = __fmul_rn(-fminf(softplus20(x[2]), 10.f), p.decay_scale);
+  v[3] = __fmul_rn(p.beta_max, sigmoid1(x[3]));
+}
+__device__ __forceinline__ void gate_row(const gpa_gate_problem& p, int h, int64_t i, const float raw[4]) {
+  float v[4];
+  gate_values(p, h, raw, v);
+  p.g_in[i] = v[0];
+  p.b_in[i] = v[1];
+  p.g_out[i] = v[2];
+  p.b_out[i] = v[3];
 }
 
 // One token of one level for the (b, h) row, by one 64-lane wave: n = count0

@@ -264,15 +264,23 @@ __global__ __launch_bounds__(NT) void level_token_reg(gpa_level_problem p) {
   level_token_reg_run<E, NT, RESID>(p, blockIdx.x);
 }
 
+// A one-token step whose value and gates are formed in it (gpa_token_slot_step).
+template <int NI>
+__global__ __launch_bounds__(SNT) void gdn_token_slot_step(gpa_gdn_problem p, gpa_token_slot ts, float* fin,
+                                                           gpa_operand out) {
+  __shared__ TokenLds<NI> lds;
+  token_run<bf16_t, NI, true>(p, fin, out, blockIdx.x, threadIdx.x, lds, ts);
+}
+
 // A level's inner one-token step (K <= 16 NI, every NT / 256 consecutive
 // step workgroups in one NT-thread workgroup) and its one-token level write
 // (one stream per workgroup) in one launch.  They share no buffers: the step
 // reads the running state and writes a new one, the level write reads the
 // block snapshots.  Step and level workgroups alternate while both last, so
 // that each compute unit streams both kinds of data at once.
-template <typename E, int NI, int NT, bool RESID = true>
+template <typename E, int NI, int NT, bool RESID = true, bool SLOT = false>
 __global__ __launch_bounds__(NT) void token_level(gpa_gdn_problem sp, float* fin, gpa_operand out,
-                                                  gpa_level_problem lp, int nstep) {
+                                                  gpa_level_problem lp, int nstep, gpa_token_slot ts) {
   __shared__ TokenLds<NI> tl[NT / SNT];
   const int nlev = lp.batch * lp.heads, blk = blockIdx.x, both = nstep < nlev ? nstep : nlev;
   bool step;
@@ -289,7 +297,7 @@ __global__ __launch_bounds__(NT) void token_level(gpa_gdn_problem sp, float* fin
     return;
   }
   const int u = threadIdx.x / SNT;
-  token_run<E, NI>(sp, fin, out, idx * (NT / SNT) + u, threadIdx.x % SNT, tl[u]);
+  token_run<E, NI, SLOT>(sp, fin, out, idx * (NT / SNT) + u, threadIdx.x % SNT, tl[u], ts);
 }
 
 // Threads for the register kernel (0: the shape is not covered).
@@ -348,37 +356,101 @@ extern "C" int gpa_level_token_forward(const gpa_level_problem* problem, hipStre
   return check_launch("gpa_level_token_forward");
 }
 
+namespace gpa {
+namespace {
+
+// The one-launch form of a step and its level write (token_level), or -1
+// where the shapes take two launches.  Only the 512-thread level kernel (M
+// <= 128 at Dk = Dv = 128).  At 1024 threads (M = 256) the one launch is
+// slower than the two: with the residual the step role's registers leave
+// room for one workgroup per compute unit, and the write-only form measured
+// 12-25 us slower too.
+int launch_token_level(const gpa_gdn_problem& step, float* final_state, gpa_operand out,
+                       const gpa_level_problem& level, const gpa_token_slot* ts, hipStream_t stream) {
+  const int nt = reg_threads(level), ni = token_rows(step);
+  const int64_t swg = token_workgroups(step), nlev = (int64_t)level.batch * level.heads;
+  const bool resid = level.key_out.ptr != nullptr;
+  const bool fused = step.dtype == level.dtype && nt == 512 && (ni == 8 || ni == 16) &&
+                     swg % (nt / SNT) == 0 && swg / (nt / SNT) + nlev <= INT32_MAX / 2;
+  if (!fused) return -1;
+  const int nstep = (int)(swg / (nt / SNT));
+  const dim3 grid((unsigned)(nstep + nlev));
+  const bool bf = step.dtype == GPA_DTYPE_BF16;
+  const gpa_token_slot none{};
+#define GPA_TOKEN_LEVEL(E, NI, R, S)                                                                      \
+  hipLaunchKernelGGL((token_level<E, NI, 512, R, S>), grid, dim3(512), 0, stream, step, final_state, out, \
+                     level, nstep, ts ? *ts : none)
+#define GPA_TOKEN_LEVEL_R(E, NI, S) \
+  do { if (resid) GPA_TOKEN_LEVEL(E, NI, true, S); else GPA_TOKEN_LEVEL(E, NI, false, S); } while (0)
+  if (ts) {  // bf16 only
+    if (ni == 8) GPA_TOKEN_LEVEL_R(bf16_t, 8, true); else GPA_TOKEN_LEVEL_R(bf16_t, 16, true);
+  } else if (bf) {
+    if (ni == 8) GPA_TOKEN_LEVEL_R(bf16_t, 8, false); else GPA_TOKEN_LEVEL_R(bf16_t, 16, false);
+  } else {
+    if (ni == 8) GPA_TOKEN_LEVEL_R(float, 8, false); else GPA_TOKEN_LEVEL_R(float, 16, false);
+  }
+#undef GPA_TOKEN_LEVEL_R
+#undef GPA_TOKEN_LEVEL
+  return 0;
+}
+
+// A slot-in-step call's checks; `sp` is the step problem with stand-ins for
+// v, g and beta (not read) so that check_token takes it.
+int check_token_slot(const gpa_gdn_problem* step, const gpa_token_slot* ts, gpa_gdn_problem& sp) {
+  if (!step || !ts) return fail(GPA_HIP_EINVAL, "slot step: null problem");
+  sp = *step;
+  if (sp.dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "slot step: bf16 activations only");
+  if (!sp.k.ptr) return fail(GPA_HIP_EINVAL, "slot step: needs a key (an update)");
+  if (sp.kdim < 1 || sp.kdim > 256 || sp.kdim % (sp.kdim > 128 ? 64 : 32))
+    return fail(GPA_HIP_EUNSUPPORTED, "slot step: K a multiple of 32 up to 128, or of 64 up to 256");
+  if (!ts->center || !ts->gate_w || !ts->slot.ptr || !ts->gates.bias || !ts->gates.g_in || !ts->gates.b_in ||
+      !ts->gates.g_out || !ts->gates.b_out)
+    return fail(GPA_HIP_EINVAL, "slot step: null center, gate weight, bias or output");
+  if (reinterpret_cast<uintptr_t>(ts->center) % 16)
+    return fail(GPA_HIP_EINVAL, "slot step: center must be 16-byte aligned");
+  sp.v = ts->slot;
+  sp.g.ptr = ts->gates.g_in;
+  sp.beta.ptr = ts->gates.b_in;
+  return GPA_HIP_OK;
+}
+
+void launch_slot_step(const gpa_gdn_problem& sp, const gpa_token_slot& ts, float* final_state, gpa_operand out,
+                      hipStream_t stream) {
+  const dim3 grid((unsigned)token_workgroups(sp));
+  switch (token_rows(sp)) {
+    case 4: hipLaunchKernelGGL((gdn_token_slot_step<4>), grid, dim3(SNT), 0, stream, sp, ts, final_state, out); break;
+    case 8: hipLaunchKernelGGL((gdn_token_slot_step<8>), grid, dim3(SNT), 0, stream, sp, ts, final_state, out); break;
+    default: hipLaunchKernelGGL((gdn_token_slot_step<16>), grid, dim3(SNT), 0, stream, sp, ts, final_state, out);
+  }
+}
+
+}  // namespace
+}  // namespace gpa
+
 extern "C" int gpa_token_level_forward(const gpa_gdn_problem* step, float* final_state, gpa_operand out,
                                        const gpa_level_problem* level, hipStream_t stream) {
   using namespace gpa;
   if (int rc = check_token(step, final_state, out)) return rc;
   if (int rc = check_level_token(level)) return rc;
-  const int nt = reg_threads(*level), ni = token_rows(*step);
-  const int64_t swg = token_workgroups(*step), nlev = (int64_t)level->batch * level->heads;
-  // Only the 512-thread level kernel (M <= 128 at Dk = Dv = 128).  At 1024
-  // threads (M = 256) the one launch is slower than the two: with the
-  // residual the step role's registers leave room for one workgroup per
-  // compute unit, and the write-only form measured 12-25 us slower too.
-  const bool resid = level->key_out.ptr != nullptr;
-  const bool fused = step->dtype == level->dtype && nt == 512 && (ni == 8 || ni == 16) &&
-                     swg % (nt / SNT) == 0 && swg / (nt / SNT) + nlev <= INT32_MAX / 2;
-  if (!fused) {
+  if (launch_token_level(*step, final_state, out, *level, nullptr, stream) < 0) {
     if (int rc = gpa_gdn_token_step(step, final_state, out, stream)) return rc;
     return gpa_level_token_forward(level, stream);
   }
-  const int nstep = (int)(swg / (nt / SNT));
-  const dim3 grid((unsigned)(nstep + nlev));
-  const bool bf = step->dtype == GPA_DTYPE_BF16;
-#define GPA_TOKEN_LEVEL(E, NI, NT, R) \
-  hipLaunchKernelGGL((token_level<E, NI, NT, R>), grid, dim3(NT), 0, stream, *step, final_state, out, *level, nstep)
-#define GPA_TOKEN_LEVEL_E(NI, NT, R) \
-  do { if (bf) GPA_TOKEN_LEVEL(bf16_t, NI, NT, R); else GPA_TOKEN_LEVEL(float, NI, NT, R); } while (0)
-  if (resid) {
-    if (ni == 8) GPA_TOKEN_LEVEL_E(8, 512, true); else GPA_TOKEN_LEVEL_E(16, 512, true);
-  } else {
-    if (ni == 8) GPA_TOKEN_LEVEL_E(8, 512, false); else GPA_TOKEN_LEVEL_E(16, 512, false);
-  }
-#undef GPA_TOKEN_LEVEL_E
-#undef GPA_TOKEN_LEVEL
   return check_launch("gpa_token_level_forward");
+}
+
+extern "C" int gpa_token_slot_step(const gpa_gdn_problem* step, const gpa_token_slot* slot, float* final_state,
+                                   gpa_operand out, const gpa_level_problem* level, hipStream_t stream) {
+  using namespace gpa;
+  gpa_gdn_problem sp;
+  if (int rc = check_token_slot(step, slot, sp)) return rc;
+  if (int rc = check_token(&sp, final_state, out)) return rc;
+  if (level) {
+    if (int rc = check_level_token(level)) return rc;
+    if (launch_token_level(sp, final_state, out, *level, slot, stream) == 0)
+      return check_launch("gpa_token_slot_step");
+  }
+  launch_slot_step(sp, *slot, final_state, out, stream);
+  if (int rc = check_launch("gpa_token_slot_step")) return rc;
+  return level ? gpa_level_token_forward(level, stream) : GPA_HIP_OK;
 }

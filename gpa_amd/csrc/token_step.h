@@ -5,7 +5,7 @@
 // level write.
 #pragma once
 
-#include "gdn_common.h"
+#include "glue_rows.h"
 
 namespace gpa {
 namespace {
@@ -57,14 +57,110 @@ struct TokenLds {
   float kh[16 * NI], qh[16 * NI];
   float norms[2][4];
   float4 part[2][4][TokenShape<NI>::CQ];
+  float kraw[16 * NI];             // the key as given (slot products in the step)
+  float vsl[TokenShape<NI>::SC];   // this block's slot values
+  float gates[2];                  // g_in, b_in
 };
+
+// The step's value and gates formed in the step (gpa_token_slot): slot
+// columns SC cb .. of stream (b, h), SNT / SC threads per column over 8-wide
+// key chunks of C's row (16-byte loads), summed by shuffles and rounded to
+// bf16; wave 0 forms the gate inputs round(unit(k) W_g) and their
+// nonlinearities (gate_values), written out by the stream's first block.
+// slot_loads issues the loads of C and W_g before the state's, so that the
+// products wait for them alone; slot_gates then runs once the rounded unit
+// key kh and the key kraw are in LDS.
+template <int NI>
+struct SlotRegs {
+  static constexpr int TPC = SNT / TokenShape<NI>::SC, CR = 16 * NI / (8 * TPC), GR = 16 * NI / 64;
+  uint4 c[CR];   // this thread's 8-wide chunks of its C row
+  uint2 w[GR];   // W_g rows d = lane + 64 i (wave 0)
+};
+
+template <int NI>
+__device__ __forceinline__ void slot_loads(const gpa_token_slot& ts, int h, int cb, int t, int K, int V,
+                                           SlotRegs<NI>& R) {
+  constexpr int SC = TokenShape<NI>::SC, TPC = SlotRegs<NI>::TPC;
+  const int c = t / TPC, part = t % TPC, m = SC * cb + c;
+  const bf16_t* cr = reinterpret_cast<const bf16_t*>(ts.center) + ((int64_t)h * V + (m < V ? m : V - 1)) * K;
+#pragma unroll
+  for (int i = 0; i < SlotRegs<NI>::CR; ++i) {
+    const int d0 = 8 * (part + TPC * i);
+    R.c[i] = *reinterpret_cast<const uint4*>(cr + (d0 < K ? d0 : 0));
+  }
+  if (t < 64) {
+    const bf16_t* gw = reinterpret_cast<const bf16_t*>(ts.gate_w) + (int64_t)h * K * 4;
+#pragma unroll
+    for (int i = 0; i < SlotRegs<NI>::GR; ++i) {
+      const int d = t + 64 * i;
+      R.w[i] = *reinterpret_cast<const uint2*>(gw + 4 * (d < K ? d : 0));
+    }
+  }
+}
+
+template <int NI>
+__device__ __forceinline__ void slot_gates(const gpa_token_slot& ts, const SlotRegs<NI>& R, int b, int h, int H,
+                                           int cb, int t, int K, int V, TokenLds<NI>& L) {
+  constexpr int SC = TokenShape<NI>::SC, TPC = SlotRegs<NI>::TPC;
+  const int c = t / TPC, part = t % TPC, m = SC * cb + c, lane = t & 63;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < SlotRegs<NI>::CR; ++i) {
+    const int d0 = 8 * (part + TPC * i);
+    if (d0 < K) {
+      const uint32_t ww[4] = {R.c[i].x, R.c[i].y, R.c[i].z, R.c[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc += L.kraw[d0 + 2 * e] * __uint_as_float(ww[e] << 16);
+        acc += L.kraw[d0 + 2 * e + 1] * __uint_as_float(ww[e] & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < TPC; o *= 2) acc += __shfl_xor(acc, o, 64);
+  if (part == 0 && m < V) {
+    const bf16_t sv = from_f32<bf16_t>(acc);
+    L.vsl[c] = to_f32(sv);
+    reinterpret_cast<bf16_t*>(ts.slot.ptr)[op_base(ts.slot, b, h) + m] = sv;
+  }
+  if (t < 64) {
+    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < SlotRegs<NI>::GR; ++i) {
+      const int d = lane + 64 * i;
+      if (d < K) {
+        const float u = L.kh[d];
+        g4[0] += u * __uint_as_float(R.w[i].x << 16);
+        g4[1] += u * __uint_as_float(R.w[i].x & 0xffff0000u);
+        g4[2] += u * __uint_as_float(R.w[i].y << 16);
+        g4[3] += u * __uint_as_float(R.w[i].y & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) g4[q] = round_as<bf16_t>(sum64(g4[q]));
+    if (lane == 0) {
+      float v[4];
+      gate_values(ts.gates, h, g4, v);
+      L.gates[0] = v[0];
+      L.gates[1] = v[1];
+      if (cb == 0) {
+        const int64_t i = (int64_t)b * H + h;
+        ts.gates.g_in[i] = v[0];
+        ts.gates.b_in[i] = v[1];
+        ts.gates.g_out[i] = v[2];
+        ts.gates.b_out[i] = v[3];
+      }
+    }
+  }
+}
 
 // t: the thread's index in its 256-thread unit; every thread of the
 // workgroup reaches the same barriers (the units of a workgroup run one
-// problem, so `update` and `has_q` agree).
-template <typename E, int NI>
+// problem, so `update` and `has_q` agree).  SLOT: the value, decay and
+// strength come from token_slot_gates (an update; bf16 activations).
+template <typename E, int NI, bool SLOT = false>
 __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, const gpa_operand& out, int wg, int t,
-                                          TokenLds<NI>& L) {
+                                          TokenLds<NI>& L, const gpa_token_slot& ts) {
   constexpr int SC = TokenShape<NI>::SC, CQ = TokenShape<NI>::CQ, RG = TokenShape<NI>::RG;
   constexpr int NR = TokenShape<NI>::NR;
   float* const kh = L.kh;
@@ -82,7 +178,22 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
   const int cc = cok ? col : 0;
   const bool update = p.k.ptr != nullptr, has_q = p.q.ptr != nullptr;
 
-  // Every load first, at clamped addresses; masks afterwards.
+  // Every load first, at clamped addresses, the small ones before the state
+  // (the norms and slot products wait for them alone); masks afterwards.
+  const int tk = t < K ? t : 0;
+  float xk = 0.f, xq = 0.f, vv[4] = {0.f, 0.f, 0.f, 0.f}, g = 0.f, beta = 0.f;
+  if (update) {
+    xk = op_load<E>(p.k, b, h, 0, tk);
+    if (!SLOT) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vv[j] = op_load<E>(p.v, b, h, 0, cc + j);
+      g = scalar_load(p.g, b, h, 0);
+      beta = scalar_load(p.beta, b, h, 0);
+    }
+  }
+  if (has_q) xq = op_load<E>(p.q, b, h, 0, tk);
+  SlotRegs<NI> sr;
+  if constexpr (SLOT) slot_loads<NI>(ts, h, cb, t, K, V, sr);
   const float* s0 = p.s0 ? p.s0 + (int64_t)b * p.s0_sb + (int64_t)h * p.s0_sh : nullptr;
   float4 st[NR];
   if (s0) {
@@ -95,16 +206,6 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
 #pragma unroll
     for (int i = 0; i < NR; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const int tk = t < K ? t : 0;
-  float xk = 0.f, xq = 0.f, vv[4] = {0.f, 0.f, 0.f, 0.f}, g = 0.f, beta = 0.f;
-  if (update) {
-    xk = op_load<E>(p.k, b, h, 0, tk);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = op_load<E>(p.v, b, h, 0, cc + j);
-    g = scalar_load(p.g, b, h, 0);
-    beta = scalar_load(p.beta, b, h, 0);
-  }
-  if (has_q) xq = op_load<E>(p.q, b, h, 0, tk);
   xk = t < K ? xk : 0.f;
   xq = t < K ? xq : 0.f;
 #pragma unroll
@@ -126,8 +227,17 @@ __device__ __forceinline__ void token_run(const gpa_gdn_problem& p, float* fin, 
   if (t < 16 * NI) {
     kh[t] = t < K ? round_as<E>(xk / nk) : 0.f;
     qh[t] = t < K ? round_as<E>(xq / nq) : 0.f;
+    if (SLOT) L.kraw[t] = xk;
   }
   lds_barrier();
+  if constexpr (SLOT) {
+    slot_gates<NI>(ts, sr, b, h, p.heads, cb, t, K, V, L);
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vv[j] = cok ? L.vsl[4 * c4 + j] : 0.f;
+    g = L.gates[0];
+    beta = L.gates[1];
+  }
 
   if (update) {
     // scaled = exp(g) S; predicted = u(k)^T scaled; S' = scaled + beta (u(k) (v - predicted)^T)

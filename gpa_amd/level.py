@@ -20,7 +20,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, params
 
 
 def supported(cfg, dtype: torch.dtype, key_dim: int, value_dim: int, slots: int) -> bool:
@@ -261,6 +261,52 @@ def token_step_and_level(step, key: Tensor, value: Tensor, a_first: Tensor, b_fi
     _lib.check(lib.gpa_token_level_forward(sp, final.data_ptr(), _lib.operand(out), lp,
                                            _lib.stream_handle(key.device)), "gpa_token_level_forward")
     return out, final, write, key_out, value_out
+
+
+def slot_step_supported(key: Tensor, slots: int) -> bool:
+    """Whether `token_slot_step` takes these widths: bf16 keys of one token,
+    K a multiple of 32 up to 128 (of 64 up to 256), slots a multiple of 4 up
+    to 256 (the slot products and gates themselves as `slots.supported`)."""
+    k = key.shape[-1]
+    return (key.dtype == torch.bfloat16 and key.ndim == 4 and key.shape[1] == 1 and k <= 256
+            and k % (64 if k > 128 else 32) == 0 and slots <= 256 and slots % 4 == 0)
+
+
+def token_slot_step(q: Tensor, key: Tensor, s0: Tensor, center: Tensor, gate_w: Tensor, bias: Tensor,
+                    beta_max: float, decay_scale: float, level=None):
+    """A level's one-token inner step `ops.gdn_token_hip(q, key, slot, g_in,
+    b_in, s0)` with its value slot = key C^T and its gates formed inside the
+    step (`gpa_token_slot_step`; the results of `slots.slot_gates_act`), and,
+    with `level` = (key, value, a_first, b_first, eta, chunk, offset,
+    residual), the level's one-token write in the same launch where the
+    library has it (as `token_step_and_level`).  Inference only.  Returns
+    (out, final, slot, g_in, b_in, g_out, b_out) + (write, key', value') with
+    a level."""
+    from .ops import _token_call
+    lib = _lib.load()
+    if torch.is_grad_enabled() and any(x.requires_grad for x in (q, key, center, gate_w, bias)):
+        raise RuntimeError("token_slot_step has no backward: call it under torch.no_grad() or inference_mode()")
+    b, _, h, _ = key.shape
+    cb = params.derived(("slot_center", id(center), key.dtype), (center,),
+                        lambda: center.detach().to(key.dtype).contiguous())
+    wg = params.derived(("slot_gate_w", id(gate_w), key.dtype), (gate_w,),
+                        lambda: gate_w.detach().to(key.dtype).contiguous())
+    slot = key.new_empty(b, 1, h, cb.shape[1])
+    gates = [torch.empty(b, 1, h, device=key.device, dtype=torch.float32) for _ in range(4)]
+    # the step's value and gates are the outputs: the kernel does not read them
+    sp, final, out, alive = _token_call(q, key, slot, gates[0], gates[1], s0)
+    bias = bias.detach().float().contiguous()
+    ts = _lib.TokenSlot()
+    ts.center, ts.gate_w, ts.slot = cb.data_ptr(), wg.data_ptr(), _lib.operand(slot)
+    ts.gates = _lib.GateProblem(b, 1, h, _lib.DTYPE_CODES[key.dtype], _lib.Operand(), bias.data_ptr(),
+                                float(beta_max), float(decay_scale), *(g.data_ptr() for g in gates))
+    lp, rest = None, ()
+    if level is not None:
+        lp, write, key_out, value_out, alive_l = _block_problem(*level)
+        rest = (write, key_out, value_out)
+    _lib.check(lib.gpa_token_slot_step(sp, ts, final.data_ptr(), _lib.operand(out), lp,
+                                       _lib.stream_handle(key.device)), "gpa_token_slot_step")
+    return (out, final, slot, *gates) + rest
 
 
 _TOKEN_KERNEL = [True]  # one-token calls of level_mix_block on gpa_level_token_forward

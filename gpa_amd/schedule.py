@@ -37,7 +37,8 @@ from .counts import count_logits
 from .slots import slot_gates, slot_gates_act
 from .slots import supported as slot_gates_supported
 from .counts import supported as fused_counts_supported
-from .level import level_mix, level_mix_block, level_residual, token_step_and_level, write_only_supported
+from .level import (level_mix, level_mix_block, level_residual, slot_step_supported, token_slot_step,
+                    token_step_and_level, write_only_supported)
 from .level import supported as fused_level_supported
 from .route import route_reader, route_reader_many
 from .route import product_read
@@ -208,8 +209,24 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     token_logits = []  # (level, j, inner read, old state) whose one-token logits come after the pass
     for j, (old, snap) in enumerate(zip(state.levels, frozen0)):
         lv = _Level()
-        if (_FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]) and _GLUE[0]
-                and not torch.is_grad_enabled() and cfg.slot_feature == "linear"):
+        act = (_FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]) and _GLUE[0]
+               and not torch.is_grad_enabled() and cfg.slot_feature == "linear")
+        if (token and act and _SLOT_STEP[0] and _TOKEN_LEVEL[0] and _FUSED_LEVEL[0]
+                and slot_step_supported(key, cfg.slots[j]) and value.shape[-1] % 4 == 0
+                and fused_level_supported(cfg, dtype, key.shape[-1], value.shape[-1], cfg.slots[j])):
+            # one token: the slot products and gates inside the A_j step, beside the
+            # level write (the last level's alone, as below)
+            eta = _etas(model)[j]
+            residual = j + 1 < len(state.levels) or not write_only_supported(
+                key.shape[-1], value.shape[-1], cfg.slots[j])
+            raw, a_final, slot, _, _, g_out, b_out, write, key_next, value_next = token_slot_step(
+                qr, key, old.inner, model.center[j], model.gate_weight[j], model.gate_bias[j], cfg.beta_max,
+                _decay_scale(model, j), (key, value, snap.inner, snap.outer, eta, chunk, offset, residual))
+            _token_level_done(model, lv, j, raw, a_final, slot, value, g_out, b_out, write, old, key, qr,
+                              position_ids, levels, token_logits)
+            key, value = key_next, value_next
+            continue
+        if act:
             # inference: slot products, gate inputs and gate nonlinearities in one launch
             slot, g_in, b_in, g_out, b_out = slot_gates_act(key, model.center[j], model.gate_weight[j],
                                                             model.gate_bias[j], cfg.beta_max, _decay_scale(model, j))
@@ -239,18 +256,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                 raw, a_final = gdn_token_hip(*step)
                 write, key_next, value_next = level_mix_block(key, value, snap.inner, snap.outer, eta, chunk, offset,
                                                               residual)
-            # The B_j step runs at its read, after the route reader (nothing
-            # before needs the new B_j): one pass over the state for both.
-            lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
-            lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
-            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
-            if old.position is None and _token_logits_supported(raw, write):
-                # nothing in the level pass reads the logits: every level's in one launch after it
-                token_logits.append((lv, j, raw, old))
-            else:
-                _moments(lv, key, qr, position_ids, old)
-                _level_logits(model, lv, j, raw, old)
-            levels.append(lv)
+            _token_level_done(model, lv, j, raw, a_final, slot, value, g_out, b_out, write, old, key, qr,
+                              position_ids, levels, token_logits)
             key, value = key_next, value_next
             continue
         if token and write is not None and token_step_supported(key, slot) and token_step_supported(slot, value):
@@ -260,15 +267,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             write = write.to(dtype)
             key_next, value_next = (_token_residual(key, value, snap.inner, snap.outer, write, eta)
                                     if j + 1 < len(state.levels) else (None, None))  # the last is never read
-            lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
-            lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
-            lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
-            if old.position is None and _token_logits_supported(raw, write):
-                token_logits.append((lv, j, raw, old))
-            else:
-                _moments(lv, key, qr, position_ids, old)
-                _level_logits(model, lv, j, raw, old)
-            levels.append(lv)
+            _token_level_done(model, lv, j, raw, a_final, slot, value, g_out, b_out, write, old, key, qr,
+                              position_ids, levels, token_logits)
             key, value = key_next, value_next
             continue
         # The outer read of this level (below) runs the B recurrence with the
@@ -571,6 +571,7 @@ def _count_scalars(model, j: int, like: Tensor):
 _FUSED_COUNTS = [True]  # counts and base logits in HIP (counts.py)
 _GLUE = [True]  # one-launch gate, one-token logits and output-mix kernels without autograd (glue.py)
 _FUSED_SLOTS = [True]  # slot products and gate inputs in HIP (slots.py)
+_SLOT_STEP = [True]  # one-token calls: slot products and gates inside the A_j step (level.token_slot_step)
 
 
 def _etas(model) -> Tensor:
@@ -605,6 +606,24 @@ def _token_residual(key, value, snap_inner, snap_outer, write, eta):
     rk = torch.matmul(snap_inner.float(), w.unsqueeze(-1))[..., 0]  # [B,H,Dk]
     rv = torch.matmul(w.unsqueeze(-2), snap_outer.float())[..., 0, :]  # [B,H,Dv]
     return _residual_eta(key, value, rk.unsqueeze(1), rv.unsqueeze(1), eta)
+
+
+def _token_level_done(model, lv, j, raw, a_final, slot, value, g_out, b_out, write, old, key, qr, position_ids,
+                      levels, token_logits):
+    """Bookkeeping of a level whose A_j step ran as one token step.  The B_j
+    step runs at its read, after the route reader (nothing before needs the
+    new B_j): one pass over the state for both.  Nothing in the level pass
+    reads the logits, so where the one-token logits kernel applies every
+    level's run in one launch after the pass."""
+    lv.b_read, lv.b_token = None, (slot, value, g_out, b_out, old.outer)
+    lv.slot, lv.value, lv.g_out, lv.b_out, lv.write = slot, value, g_out, b_out, write
+    lv.a_final, lv.b_final, lv.a_starts, lv.b_starts = a_final, None, None, None
+    if old.position is None and _token_logits_supported(raw, write):
+        token_logits.append((lv, j, raw, old))
+    else:
+        _moments(lv, key, qr, position_ids, old)
+        _level_logits(model, lv, j, raw, old)
+    levels.append(lv)
 
 
 def _level_mix_torch(key, value, a_starts, b_starts, snap_inner, snap_outer, eta, blocks, write=None):

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 24
+#define GPA_HIP_ABI_VERSION 25
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -561,6 +561,27 @@ int gpa_gate_act_forward(const gpa_gate_problem *problem, hipStream_t stream);
  * problem->raw, still written).  Results are those of the two calls. */
 int gpa_slot_gates_act_forward(const gpa_slot_problem *problem, const gpa_gate_problem *gates,
                                hipStream_t stream);
+
+/* A level's slot products and gates formed inside its one-token inner step
+ * (inference decode; bf16 activations, gates from unit(k): no control input,
+ * no rsa_update): the step's value is slot = round(k C^T) and its decay and
+ * strength are the gate nonlinearities of round(unit(k) W_g), the results of
+ * gpa_slot_gates_act_forward (attention.py:161-177), which are also written
+ * out (slot, and the four gates for the level's outer step).  The step
+ * problem's v, g and beta are not read.  K a multiple of 32 up to 128 (of 64
+ * up to 256), M = the step's V a multiple of 4 up to 256. */
+typedef struct gpa_token_slot {
+    const void *center;          /* [H][M][K] bf16, 16-byte aligned */
+    const void *gate_w;          /* [H][K][4] bf16 */
+    gpa_gate_problem gates;      /* bias, beta_max, decay_scale, the four [B,1,H] outputs (raw is not read) */
+    gpa_operand slot;            /* out [B,1,H,M] bf16 */
+} gpa_token_slot;
+/* gpa_gdn_token_step (level NULL) or gpa_token_level_forward with the step's
+ * value and gates formed in the step as above.  Replaces reference
+ * attention.py:309-311 (_slot, _gates) and ops.py:29-46 at T = 1 (with
+ * :314-329 when level is given). */
+int gpa_token_slot_step(const gpa_gdn_problem *step, const gpa_token_slot *slot, float *final_state,
+                        gpa_operand out, const gpa_level_problem *level, hipStream_t stream);
 
 /* One token (T = 1) of one level's slot counts, base logits and local read
  * distribution (attention.py:316-317, _base_logits :196-204, the softmax of

@@ -26,9 +26,10 @@ CLANG = "/opt/rocm/llvm/bin/clang++"
 ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2, "gpa_route_weight_grads": 3,
            "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6, "gpa_gdn_token_step": 7,
            "gpa_gdn_token_step_many": 8, "gpa_level_token_forward": 9,
-           "gpa_token_level_forward": 10, "gpa_product_read_forward": 11, "gpa_product_read_backward": 12}
+           "gpa_token_level_forward": 10, "gpa_product_read_forward": 11, "gpa_product_read_backward": 12,
+           "gpa_token_slot_step": 13, "gpa_slot_gates_act_forward": 14}
 SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip",
-           "product_read.hip"]
+           "product_read.hip", "slot_gates.hip"]
 
 
 def compiler() -> str | None:
@@ -161,6 +162,13 @@ class HostLib:
 
     def gpa_token_level_forward(self, step, final, out, level, stream):
         return self._call("gpa_token_level_forward", [step, out, level], [final])
+
+    def gpa_token_slot_step(self, step, slot, final, out, level, stream):
+        blobs = [step, slot, out] + ([level] if level is not None else [])
+        return self._call("gpa_token_slot_step", blobs, [final])
+
+    def gpa_slot_gates_act_forward(self, prob, gates, stream):
+        return self._call("gpa_slot_gates_act_forward", [prob, gates])
 
     def gpa_product_read_forward(self, prob, stream):
         return self._call("gpa_product_read_forward", [prob])

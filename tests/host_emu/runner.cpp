@@ -118,6 +118,17 @@ int main(int argc, char** argv) {
       rc = gpa_product_read_backward(reinterpret_cast<gpa_product_problem*>(blobs.at(0).data()),
                                      reinterpret_cast<gpa_product_grads*>(blobs.at(1).data()), nullptr);
       break;
+    case 13:
+      rc = gpa_token_slot_step(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                               reinterpret_cast<gpa_token_slot*>(blobs.at(1).data()), static_cast<float*>(raw.at(0)),
+                               *reinterpret_cast<gpa_operand*>(blobs.at(2).data()),
+                               blobs.size() > 3 ? reinterpret_cast<gpa_level_problem*>(blobs.at(3).data()) : nullptr,
+                               nullptr);
+      break;
+    case 14:
+      rc = gpa_slot_gates_act_forward(reinterpret_cast<gpa_slot_problem*>(blobs.at(0).data()),
+                                      reinterpret_cast<gpa_gate_problem*>(blobs.at(1).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

@@ -75,6 +75,7 @@ def test_ctypes_structs_match_c_layout():
     assert ctypes.sizeof(_lib.CountGrads) == 2 * 8 + 2 * 32 + 3 * 8
     # 6 int32, key operand, 3 pointers, 2 operands; 3 operands, 2 pointers
     assert ctypes.sizeof(_lib.SlotProblem) == 24 + 32 + 3 * 8 + 2 * 32
+    assert ctypes.sizeof(_lib.TokenSlot) == 2 * 8 + ctypes.sizeof(_lib.GateProblem) + 32
     assert ctypes.sizeof(_lib.SlotGrads) == 3 * 32 + 2 * 8
     # 7 int32 (+pad), base, 3 messages, 3 norms, counts, 3 pointers; pointer, 3 operands, 5 pointers
     assert ctypes.sizeof(_lib.ProductProblem) == 32 + 32 + 3 * 32 + 3 * 32 + 32 + 3 * 8

@@ -163,3 +163,46 @@ def test_write_only_level_token_gives_the_same_write(host, b, h, dk, dv, m, dtyp
     assert only[1] is None and only[2] is None and fused[3] is None and fused[4] is None
     assert torch.equal(only[0], full[0]) and torch.equal(fused[2], full[0])
     assert torch.equal(fused[0], apart[0]) and torch.equal(fused[1], apart[1])
+
+
+@pytest.mark.parametrize("b,h,k,m,dv,with_level", [(2, 2, 128, 128, 128, True), (3, 1, 64, 96, 32, True),
+                                                   (1, 2, 128, 256, 128, False), (2, 1, 32, 160, 12, True)],
+                         ids=["c3", "small", "m256_step_only", "narrow_keys"])
+def test_slot_in_step_matches_slot_gates_then_step(host, b, h, k, m, dv, with_level):
+    """gpa_token_slot_step (the slot products and gates inside the one-token
+    inner step, with the level write where given) against
+    gpa_slot_gates_act_forward followed by the step (and the level write):
+    the slot, gates, new state, read and level outputs.  The slot dot
+    products are summed in another order, so a slot may round to the
+    neighbouring bf16 value; everything downstream follows."""
+    from gpa_amd import slots
+    g = torch.Generator().manual_seed(b + k + m)
+    bf = torch.bfloat16
+    q = torch.randn(b, 1, h, k, generator=g).to(bf)
+    key = torch.randn(b, 1, h, k, generator=g).to(bf)
+    center = torch.randn(h, m, k, generator=g) / k ** .5
+    gate_w = torch.randn(h, k, 4, generator=g) * .3
+    bias = torch.randn(h, 4, generator=g)
+    s0 = torch.randn(b, h, k, m, generator=g) * .2
+    args = (center, gate_w, bias, .9, .5)
+    lvl = None
+    if with_level:
+        value = torch.randn(b, 1, h, dv, generator=g).to(bf)
+        fa, fb = torch.randn(b, h, k, m, generator=g) * .3, torch.randn(b, h, m, dv, generator=g) * .3
+        eta = 1 + .25 * torch.randn(h, 2, generator=g).tanh()
+        lvl = (key, value, fa, fb, eta, 4, 1, True)
+    with torch.no_grad():
+        got = level.token_slot_step(q, key, s0, *args, lvl)
+        slot, g_in, b_in, g_out, b_out = slots.slot_gates_act(key, *args)
+        out, final = ops.gdn_token_hip(q, key, slot, g_in, b_in, s0)
+        ref = (out, final, slot, g_in, b_in, g_out, b_out)
+        if with_level:
+            ref += level.level_mix_block(*lvl)
+    names = ("out", "final", "slot", "g_in", "b_in", "g_out", "b_out", "write", "key'", "value'")
+    assert len(got) == len(ref)
+    ulp = (got[2].float() - ref[2].float()).abs() / ref[2].float().abs().clamp_min(1e-30)
+    assert (ulp > 2 ** -8).sum() <= max(1, ref[2].numel() // 200), "slot: more than a rare 1-ulp difference"
+    for name, a, r in zip(names, got, ref):
+        assert a.dtype == r.dtype and a.shape == r.shape, name
+        tol = {"slot": 1e-2, "out": 2e-2, "final": 1e-2}.get(name, 1e-6)
+        assert _rel(a, r) <= tol, (name, _rel(a, r))
