@@ -34,10 +34,13 @@ namespace gpa {
 template <typename E, int KM>
 struct ChunkBwdLayout {
   static constexpr bool XR = KM > 128;
-  static constexpr int VS = 16;                   // value slice
-  // bf16 activations: the value slice runs as one 32x32x16 step (BFV), with
-  // dO rows read as 8-byte pairs (LDO a multiple of 4)
-  static constexpr bool BFV = std::is_same<E, bf16_t>::value && VS == 16;
+  // Value slice: 32 values for bf16 activations up to 128 keys (half the
+  // dependent load rounds of the value loop, twice the bytes in flight per
+  // round; the LDS still fits), else 16.
+  static constexpr int VS = std::is_same<E, bf16_t>::value && KM <= 128 ? 32 : 16;
+  // bf16 activations: each 16 values of a slice run as one 32x32x16 step
+  // (BFV), with dO rows read as 8-byte pairs (LDO a multiple of 4)
+  static constexpr bool BFV = std::is_same<E, bf16_t>::value;
   static constexpr int LDO = VS + 4, LT = R + 4, LS = KM + 4;
   static constexpr int LX = XR ? KM + 8 : KM + 4;  // row stride of x/|x| (bf16 elements when XR)
   static constexpr int XF = XR ? R * LX / 2 : R * LX;
@@ -337,8 +340,9 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
       }
       __syncthreads();
       if constexpr (BFV) {
-        // One 32x32x16 bf16 step per slice; fp32 operands split (mfma_tiles.h).
-        const int c0 = 8 * hh;
+        // One 32x32x16 bf16 step per 16 values of the slice; fp32 operands
+        // split (mfma_tiles.h).
+        auto vstep = [&](const int c0) {
         if (own) {
           const SplitBf8 bs = col_split_bf8(s_s, LS, 32 * kt + li, c0);
           const SplitBf8 bds = col_split_bf8(ds_s, LS, 32 * kt + li, c0);
@@ -355,6 +359,14 @@ __global__ __launch_bounds__(CB_NT, 1) void gdn_chunk_bwd_mfma(gpa_gdn_problem p
           if (has_q) mma_exact_split(dp, row_bf8(do_s, LDO, 32 * rr + li, c0), bu);
         } else {
           mma_split(dp, col_split_bf8(dd_s, LT, 32 * rr + li, c0), bu);
+        }
+        };
+        if constexpr (VS == 16) {
+          vstep(8 * hh);
+        } else {
+          // not unrolled: two steps' split operands live at once spill at 128 keys
+#pragma unroll 1
+          for (int ss = 0; ss < VS / 16; ++ss) vstep(16 * ss + 8 * hh);
         }
       } else {
 #pragma unroll
