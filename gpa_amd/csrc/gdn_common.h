@@ -151,6 +151,13 @@ int launch_prep_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, bool mf,
 // bf16-MFMA output read and its chunk-local gradient (gdn_out_mfma.hip); bf16,
 // kdim % 16 == 0 and vdim <= GPA_OUT_MFMA_MAX_V.
 constexpr int GPA_OUT_MFMA_MAX_V = 256;
+// The saved Qn and Kn rows hold bf16 (their values are exact in bf16: the
+// model rounds them to the activation type) where only the bf16 MFMA out and
+// dd0 kernels read them: bf16 problems with whole 16-wide key steps and V <=
+// GPA_OUT_MFMA_MAX_V.  Elsewhere (the FMA kernels) they hold float.
+__host__ __device__ inline bool qk_rows_bf16(const gpa_gdn_problem& p) {
+  return p.dtype == GPA_DTYPE_BF16 && p.kdim % 16 == 0 && p.vdim <= GPA_OUT_MFMA_MAX_V;
+}
 template <int KM>
 int launch_out_mfma(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, gpa_operand out, int nch, hipStream_t st);
 template <int KM>

@@ -4,12 +4,13 @@
 //   P   = causal e^{G_t-G_u} Qn Kn^T
 //   O   = diag(e^G) Qn S_n + P D                 (gdn_out_mfma)
 //   dd0 = P^T dO,   o = diag(e^G) dO             (gdn_dd0_mfma, value-major)
-// Qn and Kn are exact in bf16 (the model rounds them to the activation type);
-// the fp32 operands S_n, D and P are split into bf16 hi + lo and multiplied as
-// hi*hi + hi*lo + lo*hi, with fp32 accumulation.  Every global operand is read
-// as 32 contiguous bytes per lane straight into MFMA fragments: Qn and Kn rows
-// are position-major, and the chunk-start states and D are value-major, so a
-// lane's eight contraction indices of one value column are contiguous.
+// Qn and Kn are exact in bf16 (the model rounds them to the activation type)
+// and saved as bf16 rows (qk_rows_bf16); the fp32 operands S_n, D and P are
+// split into bf16 hi + lo and multiplied as hi*hi + hi*lo + lo*hi, with fp32
+// accumulation.  Every global operand is read as contiguous bytes per lane
+// straight into MFMA fragments (16 for a bf16 row, 32 for fp32): Qn and Kn
+// rows are position-major, and the chunk-start states and D are value-major,
+// so a lane's eight contraction indices of one value column are contiguous.
 // Reference: the output read of src/gpa/ops.py:29-46 in the chunked form.
 #include <hip/hip_runtime.h>
 
@@ -25,8 +26,6 @@ __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Eight contiguous floats that are exact in bf16, as a fragment.
-__device__ __forceinline__ bf16x8 frag_exact(const float* x) { return pack8(x); }
 
 // Eight contiguous floats split into bf16 hi and lo = bf16(x - hi).
 __device__ __forceinline__ void frag_split(const float* x, bf16x8& hi, bf16x8& lo) {
@@ -47,12 +46,6 @@ struct Raw8 {
 __device__ __forceinline__ Raw8 ld_raw8(const float* x) {
   return Raw8{*reinterpret_cast<const f32x4*>(x), *reinterpret_cast<const f32x4*>(x + 4)};
 }
-__device__ __forceinline__ bf16x8 exact_of(const Raw8& r) {
-  bf16x8 o;
-  o[0] = (__bf16)r.a.x; o[1] = (__bf16)r.a.y; o[2] = (__bf16)r.a.z; o[3] = (__bf16)r.a.w;
-  o[4] = (__bf16)r.b.x; o[5] = (__bf16)r.b.y; o[6] = (__bf16)r.b.z; o[7] = (__bf16)r.b.w;
-  return o;
-}
 __device__ __forceinline__ void split_of(const Raw8& r, bf16x8& hi, bf16x8& lo) {
   const float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
@@ -68,23 +61,31 @@ constexpr int lgroup() {
   return KM > 128 ? 4 : 8;
 }
 
+// Eight contiguous bf16 of a saved Qn / Kn row (bf16 rows: qk_rows_bf16).
+__device__ __forceinline__ bf16x8 ld_bf8(const bf16_t* x) {
+  const uint4 w = *reinterpret_cast<const uint4*>(x);
+  bf16x8 r;
+  __builtin_memcpy(&r, &w, 16);
+  return r;
+}
+
 // The (rt, ct) 32x32 tile of P = causal e^{G_t-G_u} Qn Kn^T, with qa the Qn
 // fragments of row tile rt (K16 k steps).  Lane l ends with column
 // u = 32 ct + l%32 and rows t = 32 rt + acc_row(r, l/32).
 template <int KM>
-__device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const float* kn, int K16, int K, int rt,
+__device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const bf16_t* kn, int K16, int K, int rt,
                                          int ct, int l, const float* gam_s) {
   const int li = l & 31, hh = l >> 5;
   f32x16 acc = {};
-  const float* krow = kn + (32 * ct + li) * K + 8 * hh;
+  const bf16_t* krow = kn + (32 * ct + li) * K + 8 * hh;
 #pragma unroll
   for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
-    Raw8 raw[lgroup<KM>()];
+    bf16x8 kb[lgroup<KM>()];
 #pragma unroll
-    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_raw8(krow + 16 * (k0 + j < K16 ? k0 + j : 0));
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) kb[j] = ld_bf8(krow + 16 * (k0 + j < K16 ? k0 + j : 0));
 #pragma unroll
     for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j)
-      if (k0 + j < K16) acc = mfma_bf16(qa[k0 + j], exact_of(raw[j]), acc);
+      if (k0 + j < K16) acc = mfma_bf16(qa[k0 + j], kb[j], acc);
   }
   const int u = 32 * ct + li;
 #pragma unroll
@@ -96,16 +97,20 @@ __device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const floa
 }
 
 template <int KM>
-__device__ __forceinline__ void load_q(bf16x8 (&qa)[KM / 16], const float* qn, int K16, int K, int rt, int l) {
-  const float* qrow = qn + (32 * rt + (l & 31)) * K + 8 * (l >> 5);
+__device__ __forceinline__ void load_q(bf16x8 (&qa)[KM / 16], const bf16_t* qn, int K16, int K, int rt, int l) {
+  const bf16_t* qrow = qn + (32 * rt + (l & 31)) * K + 8 * (l >> 5);
 #pragma unroll
   for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
-    Raw8 raw[lgroup<KM>()];
+    bf16x8 raw[lgroup<KM>()];
 #pragma unroll
-    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_raw8(qrow + 16 * (k0 + j < K16 ? k0 + j : 0));
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) raw[j] = ld_bf8(qrow + 16 * (k0 + j < K16 ? k0 + j : 0));
 #pragma unroll
-    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) qa[k0 + j] = k0 + j < K16 ? exact_of(raw[j]) : bf16x8{};
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) qa[k0 + j] = k0 + j < K16 ? raw[j] : bf16x8{};
   }
+}
+// The saved bf16 rows (qk_rows_bf16 holds wherever these kernels run).
+__device__ __forceinline__ const bf16_t* rows16(const float* base, int64_t off) {
+  return reinterpret_cast<const bf16_t*>(base) + off;
 }
 
 }  // namespace
@@ -120,10 +125,10 @@ __global__ __launch_bounds__(ONT, 2) void gdn_out_mfma(gpa_gdn_problem p, gpa_gd
   const int li = l & 31, hh = l >> 5, rt = w & 1;
   if (tid < R) gam_s[tid] = sv.gam[rows_off(s, n, nch, 0, 1) + tid];
   bf16x8 qa[KM / 16];
-  load_q<KM>(qa, sv.qn + rows_off(s, n, nch, 0, K), K16, K, rt, l);
+  load_q<KM>(qa, rows16(sv.qn, rows_off(s, n, nch, 0, K)), K16, K, rt, l);
   __syncthreads();
   {
-    const f32x16 pt = p_tile<KM>(qa, sv.kn + rows_off(s, n, nch, 0, K), K16, K, rt, w >> 1, l, gam_s);
+    const f32x16 pt = p_tile<KM>(qa, rows16(sv.kn, rows_off(s, n, nch, 0, K)), K16, K, rt, w >> 1, l, gam_s);
     const int u = 32 * (w >> 1) + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -213,10 +218,10 @@ __global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gd
     }
   }
   bf16x8 qa[KM / 16];
-  load_q<KM>(qa, sv.qn + rows_off(s, n, nch, 0, K), K16, K, rt, l);
+  load_q<KM>(qa, rows16(sv.qn, rows_off(s, n, nch, 0, K)), K16, K, rt, l);
   __syncthreads();
   {
-    const f32x16 pt = p_tile<KM>(qa, sv.kn + rows_off(s, n, nch, 0, K), K16, K, rt, w >> 1, l, gam_s);
+    const f32x16 pt = p_tile<KM>(qa, rows16(sv.kn, rows_off(s, n, nch, 0, K)), K16, K, rt, w >> 1, l, gam_s);
     const int u = 32 * (w >> 1) + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -335,7 +340,8 @@ __global__ __launch_bounds__(ONT) void gdn_prep_q(gpa_gdn_problem p, gpa_gdn_sav
       const int d = lane + 64 * i;
       if (d < K) {
         const float yq = round_as<E>(xq[j][i] / dq);
-        sv.qn[rows_off(s, n, nch, r, K) + d] = yq;
+        if (MF) reinterpret_cast<bf16_t*>(sv.qn)[rows_off(s, n, nch, r, K) + d] = from_f32<bf16_t>(yq);
+        else sv.qn[rows_off(s, n, nch, r, K) + d] = yq;
         if (MF) {  // Qn^T fragment (d/32, r/16), lane d%32 + 32 ((r/8) % 2), element r % 8
           const int rb = d >> 5, cs = r >> 4, ln = (d & 31) + 32 * ((r >> 3) & 1);
           qcol[((rb * 4 + cs) * 64 + ln) * 8 + (r & 7)] = (__bf16)yq;

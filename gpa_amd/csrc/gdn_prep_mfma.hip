@@ -56,7 +56,7 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
   const int li = lane & 31, hh = lane >> 5;
   const int K16 = K / 16;
   const int64_t chunk_id = (int64_t)s * nch + n;
-  const bool has_q = p.q.ptr != nullptr;
+  const bool has_q = p.q.ptr != nullptr, rows16 = MF && qk_rows_bf16(p);
 
   // ---- gates: G by a wave-wide inclusive scan (wave 0).
   if (wave == 0) {
@@ -114,10 +114,14 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
         const int d = lane + 64 * i;
         const float yk = round_as<E>(xk[j][i] / dk);
         kn_s[r * LK + d] = yk;
-        if (d < K) sv.kn[rows_off(s, n, nch, r, K) + d] = yk;
+        if (d < K) {
+          if (rows16) reinterpret_cast<bf16_t*>(sv.kn)[rows_off(s, n, nch, r, K) + d] = from_f32<bf16_t>(yk);
+          else sv.kn[rows_off(s, n, nch, r, K) + d] = yk;
+        }
         if (has_q && d < K) {
           const float yq = round_as<E>(xq[j][i] / dq);
-          sv.qn[rows_off(s, n, nch, r, K) + d] = yq;
+          if (rows16) reinterpret_cast<bf16_t*>(sv.qn)[rows_off(s, n, nch, r, K) + d] = from_f32<bf16_t>(yq);
+          else sv.qn[rows_off(s, n, nch, r, K) + d] = yq;
           if (MF) {  // Qn^T fragment (d/32, r/16), lane d%32 + 32 ((r/8) % 2), element r % 8
             const int rb = d >> 5, cs = r >> 4, ln = (d & 31) + 32 * ((r >> 3) & 1);
             qcol[((rb * 4 + cs) * 64 + ln) * 8 + (r & 7)] = (__bf16)yq;
