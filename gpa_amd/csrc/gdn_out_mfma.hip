@@ -70,19 +70,21 @@ __device__ __forceinline__ bf16x8 ld_bf8(const bf16_t* x) {
 }
 
 // The (rt, ct) 32x32 tile of P = causal e^{G_t-G_u} Qn Kn^T, with qa the Qn
-// fragments of row tile rt (K16 k steps).  Lane l ends with column
+// fragments of row tile rt (K16 k steps) and krow the chunk's Kn row
+// fragments (the state kernels' krow: fragment (ct, ks), lane l holds
+// Kn[32 ct + l%32][16 ks + 8 (l/32) + e]).  Lane l ends with column
 // u = 32 ct + l%32 and rows t = 32 rt + acc_row(r, l/32).
 template <int KM>
-__device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const bf16_t* kn, int K16, int K, int rt,
-                                         int ct, int l, const float* gam_s) {
+__device__ __forceinline__ f32x16 p_tile(const bf16x8 (&qa)[KM / 16], const bf16_t* krow, int K16, int rt, int ct,
+                                         int l, const float* gam_s) {
   const int li = l & 31, hh = l >> 5;
   f32x16 acc = {};
-  const bf16_t* krow = kn + (32 * ct + li) * K + 8 * hh;
+  const bf16_t* kf = krow + ((int64_t)ct * K16 * 64 + l) * 8;
 #pragma unroll
   for (int k0 = 0; k0 < KM / 16; k0 += lgroup<KM>()) {
     bf16x8 kb[lgroup<KM>()];
 #pragma unroll
-    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) kb[j] = ld_bf8(krow + 16 * (k0 + j < K16 ? k0 + j : 0));
+    for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j) kb[j] = ld_bf8(kf + 512 * (k0 + j < K16 ? k0 + j : 0));
 #pragma unroll
     for (int j = 0; j < lgroup<KM>() && k0 + j < KM / 16; ++j)
       if (k0 + j < K16) acc = mfma_bf16(qa[k0 + j], kb[j], acc);
@@ -112,6 +114,10 @@ __device__ __forceinline__ void load_q(bf16x8 (&qa)[KM / 16], const bf16_t* qn, 
 __device__ __forceinline__ const bf16_t* rows16(const float* base, int64_t off) {
   return reinterpret_cast<const bf16_t*>(base) + off;
 }
+// Chunk n of stream s in the Kn row fragments.
+__device__ __forceinline__ const bf16_t* krow_of(const gpa_gdn_saved& sv, int s, int n, int nch, int K) {
+  return reinterpret_cast<const bf16_t*>(sv.krow) + ((int64_t)s * nch + n) * frag_row_elems(K, 8);
+}
 
 }  // namespace
 
@@ -128,7 +134,7 @@ __global__ __launch_bounds__(ONT, 2) void gdn_out_mfma(gpa_gdn_problem p, gpa_gd
   load_q<KM>(qa, rows16(sv.qn, rows_off(s, n, nch, 0, K)), K16, K, rt, l);
   __syncthreads();
   {
-    const f32x16 pt = p_tile<KM>(qa, rows16(sv.kn, rows_off(s, n, nch, 0, K)), K16, K, rt, w >> 1, l, gam_s);
+    const f32x16 pt = p_tile<KM>(qa, krow_of(sv, s, n, nch, K), K16, rt, w >> 1, l, gam_s);
     const int u = 32 * (w >> 1) + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(ONT, 2) void gdn_dd0_mfma(gpa_gdn_problem p, gpa_gd
   load_q<KM>(qa, rows16(sv.qn, rows_off(s, n, nch, 0, K)), K16, K, rt, l);
   __syncthreads();
   {
-    const f32x16 pt = p_tile<KM>(qa, rows16(sv.kn, rows_off(s, n, nch, 0, K)), K16, K, rt, w >> 1, l, gam_s);
+    const f32x16 pt = p_tile<KM>(qa, krow_of(sv, s, n, nch, K), K16, rt, w >> 1, l, gam_s);
     const int u = 32 * (w >> 1) + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {

@@ -114,10 +114,9 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
         const int d = lane + 64 * i;
         const float yk = round_as<E>(xk[j][i] / dk);
         kn_s[r * LK + d] = yk;
-        if (d < K) {
-          if (rows16) reinterpret_cast<bf16_t*>(sv.kn)[rows_off(s, n, nch, r, K) + d] = from_f32<bf16_t>(yk);
-          else sv.kn[rows_off(s, n, nch, r, K) + d] = yk;
-        }
+        // (where the bf16 out and dd0 kernels read them, the Kn rows are the
+        // krow fragments written below)
+        if (d < K && !rows16) sv.kn[rows_off(s, n, nch, r, K) + d] = yk;
         if (has_q && d < K) {
           const float yq = round_as<E>(xq[j][i] / dq);
           if (rows16) reinterpret_cast<bf16_t*>(sv.qn)[rows_off(s, n, nch, r, K) + d] = from_f32<bf16_t>(yq);

@@ -82,9 +82,10 @@ typedef struct gpa_gdn_problem {
 /* Caller-owned intermediates, stream-major and contiguous (S = streams,
  * N = nchunks, per chunk):
  *   kn, qn         f32 [S,N,64,K]   normalised keys / queries (rows = positions); for bf16
- *                                   problems with K % 16 == 0 and V <= 256 they hold
- *                                   their exact bf16 values instead, bf16 [S,N,64,K] in
- *                                   the first half of the buffer
+ *                                   problems with K % 16 == 0 and V <= 256, qn holds its
+ *                                   exact bf16 values instead (bf16 [S,N,64,K] in the first
+ *                                   half of the buffer) and kn is not written (the krow
+ *                                   fragments below carry the same values)
  *   w              f32 [S,N,64,K]   W = T diag(b e^G) Kn  (FMA path only)
  *   u, delta       f32 [S,N,V,64]   U = T diag(b) V, D = U - W S_n  (value-major; on the
  *                                   MFMA path u is in fragment order instead, per chunk
