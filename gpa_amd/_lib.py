@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 25
+ABI_VERSION = 26
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -180,6 +180,17 @@ class MixProblem(ctypes.Structure):
                [("read", Operand * DECODE_MAX_LEVELS), ("weights", c_vp), ("out", Operand)]
 
 
+GATE_NONE, GATE_TOKEN, GATE_KEY, GATE_VALUE = 0, 1, 2, 3
+MOMENT_MAX_KDIM = 256
+MOMENT_MAX_PACK = 4
+
+
+class MomentProblem(ctypes.Structure):
+    _fields_ = [("batch", c_i32), ("heads", c_i32), ("tokens", c_i32), ("kdim", c_i32), ("vdim", c_i32),
+                ("dtype", c_i32), ("gate", c_i32), ("reverse", c_i32), ("y_f32", c_i32), ("pad_", c_i32),
+                ("q", Operand), ("k", Operand), ("v", Operand), ("g", Operand), ("y", Operand),
+                ("s0", c_vp), ("s0_sb", c_i64), ("s0_sh", c_i64), ("final", c_vp)]
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -227,6 +238,7 @@ EXPORTS = {
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
     "gpa_copy_many": ([ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(ctypes.c_int64), c_i32, c_vp],
                       ctypes.c_int),
+    "gpa_moment_scan_many": ([ctypes.POINTER(MomentProblem), c_i32, c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -3,20 +3,21 @@ embedding and the additive moment scan of the reference
 (src/gpa/ops.py:88-137), used by the block segment at attention.py:305,
 :318-323 and the token step at :265, :276-281.
 
-Both run as float32 (float64 for float64 inputs) device tensor operations on
-the inputs' device, with autograd.  The moment scan is the chunked form of the
-reference's per-token loop `S += k v^T; out = q^T S`: per 64-token chunk the
-state at the chunk start is the initial state plus the exclusive prefix sum of
-the earlier chunks' K^T V, and a token reads
-`q^T S_chunk_start + sum_{s <= t in the chunk} (q_t . k_s) v_s`.  The products
-are batched matmuls on contiguous float32 operands.
+The moment scan `S += k v^T; out = q^T S` runs in the gated moment-scan
+kernel (`gpa_amd.moment`, no decay) for key and value widths up to 256, with
+its three-scan backward.  Wider scans take the chunked form as device tensor
+operations: per 64-token chunk the state at the chunk start is the initial
+state plus the exclusive prefix sum of the earlier chunks' K^T V, and a token
+reads `q^T S_chunk_start + sum_{s <= t in the chunk} (q_t . k_s) v_s` (batched
+float32 matmuls).  The rotary embedding is a float32 (float64 for float64
+inputs) device tensor operation with autograd.
 """
 from __future__ import annotations
 
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, moment
 
 CHUNK = 64  # tokens per chunk of the moment scan
 
@@ -59,6 +60,8 @@ def additive_scan(q: Tensor, k: Tensor, v: Tensor, initial: Tensor) -> tuple[Ten
     vd = v.shape[-1]
     if tokens == 0:
         return v.new_empty(v.shape), initial
+    if q.dtype != torch.float64 and q.is_cuda and moment.supported(q, v):
+        return moment.moment_scan(q, k, v.to(q.dtype), None, initial)
     work = _work(q)
     n = -(-tokens // CHUNK)
     pad = n * CHUNK - tokens

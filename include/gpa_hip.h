@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 25
+#define GPA_HIP_ABI_VERSION 26
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -625,6 +625,50 @@ int gpa_output_mix_forward(const gpa_mix_problem *problem, hipStream_t stream);
  * token's q, k and v into the buffers a captured decode graph reads. */
 #define GPA_COPY_MAX 4
 int gpa_copy_many(void *const *dst, const void *const *src, const int64_t *bytes, int32_t n, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Gated moment scan: the per-token recurrence of the additive positional
+ * moments (reference src/gpa/ops.py:88-118, `linear_scan`: no gate) and of
+ * the counted core's moment and count scans (src/gpa/paper_dense.py:16-58,
+ * `moment_scan` and `decayed_counts`).  Per stream, tokens ascending:
+ *     S_t = a_t o S_{t-1} + k_t v_t^T,   y_t = S_t^T q_t,   a_t = exp(g_t)
+ * where the decay a_t is 1 (GPA_GATE_NONE), one value per token (g [B,T,H]),
+ * one per key row (g [B,T,H,K]: row k of S scaled by a_t[k]) or one per value
+ * column (g [B,T,H,V]).  No normalisation of q, k or v.  With reverse = 1 the
+ * tokens run descending and each step is S += k_t v_t^T; y_t = S^T q_t;
+ * S = a_t o S: the adjoint recursion D_t = a_{t+1} o D_{t+1} + q_t dy_t^T of
+ * the backward, whose three scans (dq forward on the transposed state, dv
+ * reverse, dk reverse on the transposed state) are each one problem.  The
+ * state is float32 in registers for the whole sequence, `final` receives it
+ * after the last step (for reverse, after the decay of token 0). */
+#define GPA_GATE_NONE 0
+#define GPA_GATE_TOKEN 1
+#define GPA_GATE_KEY 2
+#define GPA_GATE_VALUE 3
+#define GPA_MOMENT_MAX_KDIM 256
+#define GPA_MOMENT_MAX_PACK 4
+
+typedef struct gpa_moment_problem {
+    int32_t batch, heads;   /* streams = batch*heads */
+    int32_t tokens;         /* T >= 1 */
+    int32_t kdim, vdim;     /* 1..GPA_MOMENT_MAX_KDIM rows; vdim >= 1 columns */
+    int32_t dtype;          /* GPA_DTYPE_*: q, k, v (and y unless y_f32) */
+    int32_t gate;           /* GPA_GATE_* */
+    int32_t reverse;        /* 0 ascending, 1 descending (adjoint order) */
+    int32_t y_f32;          /* 1: y is float32 */
+    int32_t pad_;
+    gpa_operand q, k, v;    /* [B,T,H,K], [B,T,H,K], [B,T,H,V] */
+    gpa_operand g;          /* float32 log-decay: [B,T,H] (d = 0), [B,T,H,K] or [B,T,H,V]; unused for NONE */
+    gpa_operand y;          /* out [B,T,H,V] */
+    const float *s0;        /* [B,H,K,V] key-major at s0[b*s0_sb + h*s0_sh + k*V + v]; NULL = zeros */
+    int64_t s0_sb, s0_sh;
+    float *final;           /* out [B,H,K,V] contiguous float32; NULL = not written */
+} gpa_moment_problem;
+
+/* Up to GPA_MOMENT_MAX_PACK independent problems (any widths, gates and
+ * directions, one element type) in one launch; the forward is one problem,
+ * the backward three.  Results are those of one call per problem. */
+int gpa_moment_scan_many(const gpa_moment_problem *problems, int32_t n, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -22,8 +22,10 @@ DTYPES = {"float32": torch.float32, "float64": torch.float64, "bfloat16": torch.
 
 
 def names():
-    """The DenseGPA fixtures (operator fixtures start with "ops_", LM fixtures with "lm_")."""
-    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith(("ops_", "lm_")))
+    """The DenseGPA fixtures (operator fixtures start with "ops_" or "moment_", LM
+    fixtures with "lm_", counted-core fixtures with "paper_")."""
+    return sorted(f[:-4] for f in os.listdir(GOLDEN)
+                  if f.endswith(".npz") and not f.startswith(("ops_", "lm_", "paper_", "moment_")))
 
 
 def ops_names(prefix: str):
@@ -186,3 +188,92 @@ def compare_state(case: Case, prefix: str, state, rtol: float) -> list[str]:
         if msg:
             errors.append(msg)
     return errors
+
+
+class MomentCase:
+    """A moment-scan fixture (reference paper_dense.py:16-58, ops.py:88-118):
+    inputs, y, final state and counts, and the input gradients of
+    y.square().mean() + final.square().mean() + counts.square().mean()."""
+
+    ACT = ("q", "k", "v", "p")
+
+    def __init__(self, name: str):
+        self.name = name
+        with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+            self.z = {k: z[k] for k in z.files}
+        self.meta = json.loads(str(self.z["meta"]))
+        self.dtype = DTYPES[self.meta["dtype"]]
+        self.gate = self.meta["gate"]
+
+    def has(self, name: str) -> bool:
+        return ("full/" + name) in self.z or ("fp/" + name) in self.z
+
+    def inputs(self, dtype=None, device=None):
+        """The seeded inputs in the fixture script's draw order, activations in
+        `dtype` (default: the fixture's), the rest in its work type."""
+        dtype = dtype or self.dtype
+        work = torch.float64 if dtype == torch.float64 else torch.float32
+        m = self.meta
+        g = torch.Generator().manual_seed(m["seed"])
+        b, t, h, kd, vd = m["batch"], m["length"], m["heads"], m["kdim"], m["vdim"]
+        f64 = dict(generator=g, dtype=torch.float64)
+        x = {"q": torch.randn(b, t, h, kd, **f64), "k": torch.randn(b, t, h, kd, **f64),
+             "v": torch.randn(b, t, h, vd, **f64), "s0": torch.randn(b, h, kd, vd, **f64) * .1}
+        shape = {"token": (b, t, h), "key": (b, t, h, kd), "value": (b, t, h, vd)}.get(self.gate)
+        if shape:
+            x["g"] = -torch.rand(*shape, **f64) * .3
+        x["p"] = torch.rand(b, t, h, vd, **f64)
+        x["n0"] = torch.rand(b, h, vd, **f64)
+        x["cg"] = -torch.rand(*(shape if self.gate == "value" else (b, t, h)), **f64) * .3
+        return {n: v.to(device=device, dtype=dtype if n in self.ACT else work) for n, v in x.items()}
+
+
+class PaperCase:
+    """A counted-core fixture (reference paper_dense.py:87-278), seeded like
+    tests/golden/make_paper_golden.py."""
+
+    def __init__(self, name: str):
+        self.name = name
+        with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+            self.z = {k: z[k] for k in z.files}
+        self.cfg = json.loads(str(self.z["config"]))
+        self.cfg["slots"] = tuple(self.cfg["slots"])
+        if self.cfg.get("decay_tiers") is not None:
+            self.cfg["decay_tiers"] = tuple(self.cfg["decay_tiers"])
+        self.seed, self.batch, self.length, self.control_dim = (int(x) for x in self.z["meta"])
+        self.dtype = DTYPES[str(self.z["dtype"])]
+        self.perturb = float(self.z["perturb"])
+
+    def has(self, name: str) -> bool:
+        return ("full/" + name) in self.z or ("fp/" + name) in self.z
+
+    def build(self):
+        from gpa_amd.paper_dense import PaperConfig, PaperDenseGPA
+        torch.manual_seed(self.seed)
+        model = PaperDenseGPA(PaperConfig(**self.cfg))
+        if self.dtype == torch.float64:
+            model = model.double()
+        if self.perturb:
+            g = torch.Generator().manual_seed(self.seed + 100)
+            with torch.no_grad():
+                for pname in ("control_weight", "mlp_down", "relation_prefix", "residual_raw", "level_logits"):
+                    p = getattr(model, pname)
+                    p.add_(torch.randn(p.shape, generator=g, dtype=p.dtype) * self.perturb)
+        gen = torch.float64 if self.dtype == torch.float64 else torch.float32
+        h, dk, dv = self.cfg["heads"], self.cfg["key_dim"], self.cfg["value_dim"]
+        q = torch.randn(self.batch, self.length, h, dk, dtype=gen)
+        k = torch.randn_like(q)
+        v = torch.randn(self.batch, self.length, h, dv, dtype=gen)
+        ctrl = torch.randn(self.batch, self.length, self.control_dim, dtype=gen) if self.control_dim else None
+        q, k, v = (x.to(self.dtype) for x in (q, k, v))
+        if ctrl is not None:
+            ctrl = ctrl.to(self.dtype)
+        return model, q, k, v, ctrl
+
+
+def paper_names():
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and f.startswith("paper_"))
+
+
+def moment_names():
+    return sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and f.startswith("moment_"))

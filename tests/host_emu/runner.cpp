@@ -129,6 +129,10 @@ int main(int argc, char** argv) {
       rc = gpa_slot_gates_act_forward(reinterpret_cast<gpa_slot_problem*>(blobs.at(0).data()),
                                       reinterpret_cast<gpa_gate_problem*>(blobs.at(1).data()), nullptr);
       break;
+    case 15:
+      rc = gpa_moment_scan_many(reinterpret_cast<gpa_moment_problem*>(blobs.at(0).data()),
+                                (int32_t)(blobs.at(0).size() / sizeof(gpa_moment_problem)), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

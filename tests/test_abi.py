@@ -80,6 +80,8 @@ def test_ctypes_structs_match_c_layout():
     # 7 int32 (+pad), base, 3 messages, 3 norms, counts, 3 pointers; pointer, 3 operands, 5 pointers
     assert ctypes.sizeof(_lib.ProductProblem) == 32 + 32 + 3 * 32 + 3 * 32 + 32 + 3 * 8
     assert ctypes.sizeof(_lib.ProductGrads) == 8 + 3 * 32 + 3 * 8 + 2 * 8
+    # gpa_moment_problem: ten int32, five operands, s0 and its two strides, final
+    assert ctypes.sizeof(_lib.MomentProblem) == 40 + 5 * 32 + 3 * 8 + 8
 
 
 def test_backend_refuses_cpu_tensors():
