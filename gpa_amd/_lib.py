@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 26
+ABI_VERSION = 27
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -191,6 +191,17 @@ class MomentProblem(ctypes.Structure):
                 ("q", Operand), ("k", Operand), ("v", Operand), ("g", Operand), ("y", Operand),
                 ("s0", c_vp), ("s0_sb", c_i64), ("s0_sh", c_i64), ("final", c_vp)]
 
+QUAD_MAX_DIM = 256
+
+
+class QuadProblem(ctypes.Structure):
+    _fields_ = [("rows", c_i32), ("heads", c_i32), ("dim", c_i32), ("dtype", c_i32), ("x", c_vp),
+                ("row_stride", c_i64), ("wt", c_vp), ("w", c_vp), ("gain", c_vp), ("out", c_vp)]
+
+
+class QuadGrads(ctypes.Structure):
+    _fields_ = [("dout", c_vp), ("dx", c_vp), ("u", c_vp), ("dab", c_vp), ("dgain", c_vp)]
+
 EXPORTS = {
     "gpa_hip_abi_version": ([], ctypes.c_int),
     "gpa_hip_last_error": ([], ctypes.c_char_p),
@@ -239,6 +250,8 @@ EXPORTS = {
     "gpa_copy_many": ([ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(ctypes.c_int64), c_i32, c_vp],
                       ctypes.c_int),
     "gpa_moment_scan_many": ([ctypes.POINTER(MomentProblem), c_i32, c_vp], ctypes.c_int),
+    "gpa_quad_features_forward": ([ctypes.POINTER(QuadProblem), c_vp], ctypes.c_int),
+    "gpa_quad_features_backward": ([ctypes.POINTER(QuadProblem), ctypes.POINTER(QuadGrads), c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -13,11 +13,10 @@ from __future__ import annotations
 import math
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor, nn
 
 from .config import GPAConfig
-from .state import GPAState, LevelState, RelationState, state_dtype
+from .state import GPAState, LevelState, RelationState
 
 
 def _softplus_inverse(x: float) -> float:
@@ -28,6 +27,8 @@ class QuadraticFeatures(nn.Module):
     """Norm-preserving quadratic Q/K sketch (reference src/gpa/features.py:8-25).
 
     z = u(x) + 2*sigmoid(gain_raw)*sqrt(D)*(u(x)L)*(u(x)R);  out = u(z)*||x||.
+    Parameters and initialisation are the reference's; the map runs in the HIP
+    kernels of gpa_amd.features.
     """
 
     def __init__(self, heads: int, dim: int):
@@ -40,15 +41,10 @@ class QuadraticFeatures(nn.Module):
         self.dim = dim
 
     def forward(self, x: Tensor) -> Tensor:
-        work = state_dtype(x)
-        u = F.normalize(x.to(work), dim=-1, eps=1e-6).to(x.dtype)
-        left = torch.einsum("...hd,hdf->...hf", u, self.left.to(x.dtype)).to(work)
-        right = torch.einsum("...hd,hdf->...hf", u, self.right.to(x.dtype)).to(work)
-        gain = 2 * self.gain_raw.sigmoid()[..., None]
-        z = u.to(work) + gain * math.sqrt(self.dim) * left * right
-        norm = (x.to(work).square().sum(-1, keepdim=True) + 1e-12).sqrt()
-        z = F.normalize(z, dim=-1, eps=1e-6)
-        return (z * norm).to(x.dtype)
+        """x [..., H, D] on the GPU: one HIP launch forward, one backward (plus
+        the weight gradients' batched product), gpa_amd.features."""
+        from .features import quadratic_features
+        return quadratic_features(x, self.left, self.right, self.gain_raw)
 
 
 class DenseGPA(nn.Module):

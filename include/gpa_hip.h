@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 26
+#define GPA_HIP_ABI_VERSION 27
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -669,6 +669,41 @@ typedef struct gpa_moment_problem {
  * directions, one element type) in one launch; the forward is one problem,
  * the backward three.  Results are those of one call per problem. */
 int gpa_moment_scan_many(const gpa_moment_problem *problems, int32_t n, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Quadratic Q/K feature map (reference src/gpa/features.py:8-25, applied to q
+ * and k by DenseGPA.forward when quadratic_features is set):
+ *     u = unit(x) (rounded to dtype),  a = u L_h,  b = u R_h (dtype products),
+ *     z = u + gain[h] a b,  out = unit(z) sqrt(sum x^2 + 1e-12)
+ * with gain[h] = 2 sigmoid(gain_raw[h]) sqrt(dim) (float32).  x and out are
+ * [rows][heads][dim]: row r of head h at x[r*row_stride + h*dim] (out, dout
+ * and dx contiguous, row stride heads*dim).  The weights come in two
+ * caller-made copies in dtype, zero-padded to DP = ceil(dim/32)*32:
+ *     wt [heads][2][DP][DP]:  wt[h][p][n][k] = W_p[h][k][n]  (W_0 = L, W_1 = R)
+ *     w  [heads][DP][2*DP]:   w[h][k][p*DP + n] = W_p[h][k][n]
+ * The backward writes dx, u ([heads][rows][DP], zero past dim) and d(a)|d(b)
+ * ([heads][rows][2*DP]) for the weight gradients dW_p = u^T d(W_p u) (a plain
+ * batched product the caller runs), and dgain [ceil(rows/32)][heads]: partial
+ * sums of d(gain) per 32-row tile. */
+#define GPA_QUAD_MAX_DIM 256
+
+typedef struct gpa_quad_problem {
+    int32_t rows, heads, dim, dtype;
+    const void *x;
+    int64_t row_stride;
+    const void *wt, *w;
+    const float *gain;      /* [heads] */
+    void *out;              /* forward output; unused by the backward */
+} gpa_quad_problem;
+
+typedef struct gpa_quad_grads {
+    const void *dout;
+    void *dx, *u, *dab;
+    float *dgain;
+} gpa_quad_grads;
+
+int gpa_quad_features_forward(const gpa_quad_problem *problem, hipStream_t stream);
+int gpa_quad_features_backward(const gpa_quad_problem *problem, const gpa_quad_grads *grads, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -114,6 +114,28 @@ def two_stage(q, k, slots, v, gi, bi, go, bo, inner, outer, *, route_weight=None
     return out, a, b
 
 
+def quadratic_features(fm, x: Tensor) -> Tensor:
+    """The quadratic Q/K feature map (features.py:17-25) with the parameters of
+    `fm` (left, right [H,D,D], gain_raw [H]): u = unit(x); z = u +
+    2 sigmoid(gain_raw) sqrt(D) (u L)(u R); out = unit(z) sqrt(sum x^2 + 1e-12)."""
+    work = _work(x)
+    u = unit(x)
+    a = _typed_product("...hd,hdf->...hf", u, fm.left, x.dtype).to(work)
+    b = _typed_product("...hd,hdf->...hf", u, fm.right, x.dtype).to(work)
+    gain = 2 * fm.gain_raw.sigmoid()[..., None]
+    z = u.to(work) + gain * math.sqrt(x.shape[-1]) * a * b
+    norm = (x.to(work).square().sum(-1, keepdim=True) + 1e-12).sqrt()
+    return (F.normalize(z, p=2, dim=-1, eps=1e-6) * norm).to(x.dtype)
+
+
+def _typed_product(eq: str, x: Tensor, w: Tensor, dtype) -> Tensor:
+    """einsum of two `dtype` operands as the reference's typed einsum (bf16
+    operands multiplied in float32 and rounded once)."""
+    if dtype == torch.bfloat16:
+        return torch.einsum(eq, x.to(dtype).float(), w.to(dtype).float()).to(dtype)
+    return torch.einsum(eq, x.to(dtype), w.to(dtype))
+
+
 def _softplus_inverse(x: float) -> float:
     return math.log(math.expm1(x))
 
@@ -389,7 +411,7 @@ class OracleRun:
                                 or control_input.shape != q.shape[:2] + (cfg.control_dim,)):
             raise ValueError("full hidden controls [B,T,control_dim] required")
         if cfg.quadratic_features:
-            q, k = p.feature_map(torch.stack((q, k))).unbind(0)
+            q, k = quadratic_features(p.feature_map, torch.stack((q, k))).unbind(0)
         if state is None:
             state = initial_state(p, q.shape[0], device=q.device, dtype=q.dtype, chunk_size=cfg.chunk_size)
         if state.chunk_size != cfg.chunk_size:

@@ -27,9 +27,11 @@ ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2
            "gpa_level_forward": 4, "gpa_level_backward": 5, "gpa_route_forward_many": 6, "gpa_gdn_token_step": 7,
            "gpa_gdn_token_step_many": 8, "gpa_level_token_forward": 9,
            "gpa_token_level_forward": 10, "gpa_product_read_forward": 11, "gpa_product_read_backward": 12,
-           "gpa_token_slot_step": 13, "gpa_slot_gates_act_forward": 14, "gpa_moment_scan_many": 15}
+           "gpa_token_slot_step": 13, "gpa_slot_gates_act_forward": 14, "gpa_moment_scan_many": 15,
+           "gpa_quad_features_forward": 16, "gpa_quad_features_backward": 17}
 SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip",
-           "product_read.hip", "slot_gates.hip", "moment_scan.hip"]
+           "product_read.hip", "slot_gates.hip", "moment_scan.hip",
+           "quad_features.hip"]
 
 
 def compiler() -> str | None:
@@ -179,6 +181,12 @@ class HostLib:
     def gpa_moment_scan_many(self, probs, n, stream):
         assert n == len(probs)
         return self._call("gpa_moment_scan_many", [probs])
+
+    def gpa_quad_features_forward(self, prob, stream):
+        return self._call("gpa_quad_features_forward", [prob])
+
+    def gpa_quad_features_backward(self, prob, grads, stream):
+        return self._call("gpa_quad_features_backward", [prob, grads])
 
     def gpa_hip_last_error(self):
         return b""

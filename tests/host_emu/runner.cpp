@@ -133,6 +133,13 @@ int main(int argc, char** argv) {
       rc = gpa_moment_scan_many(reinterpret_cast<gpa_moment_problem*>(blobs.at(0).data()),
                                 (int32_t)(blobs.at(0).size() / sizeof(gpa_moment_problem)), nullptr);
       break;
+    case 16:
+      rc = gpa_quad_features_forward(reinterpret_cast<gpa_quad_problem*>(blobs.at(0).data()), nullptr);
+      break;
+    case 17:
+      rc = gpa_quad_features_backward(reinterpret_cast<gpa_quad_problem*>(blobs.at(0).data()),
+                                      reinterpret_cast<gpa_quad_grads*>(blobs.at(1).data()), nullptr);
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());

@@ -82,6 +82,8 @@ def test_ctypes_structs_match_c_layout():
     assert ctypes.sizeof(_lib.ProductGrads) == 8 + 3 * 32 + 3 * 8 + 2 * 8
     # gpa_moment_problem: ten int32, five operands, s0 and its two strides, final
     assert ctypes.sizeof(_lib.MomentProblem) == 40 + 5 * 32 + 3 * 8 + 8
+    assert ctypes.sizeof(_lib.QuadProblem) == 16 + 8 + 8 + 3 * 8 + 8
+    assert ctypes.sizeof(_lib.QuadGrads) == 5 * 8
 
 
 def test_backend_refuses_cpu_tensors():
