@@ -427,16 +427,22 @@ def _token(model, q, k, v, state: GPAState, control, position=None):
     dtype = q.dtype
     qr = rope(q, position) if cfg.positional_mode == "moments" else q
     step = dict(chunk=1, offset=0)
+    infer = _TOKEN_STEP[0] and not torch.is_grad_enabled()
     key, value = k, v
     new_levels, writes, logits = [], [], []
     for j, old in enumerate(state.levels):
         slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
         g_in, b_in, g_out, b_out = _gates(model, key, j, control)
-        (raw, _, a), (_, _, b) = _concurrent([
-            (lambda: gdn_scan_hip(qr, key, slot, g_in, b_in, old.inner, **step),
-             (qr, key, slot, g_in, b_in, old.inner)),
-            (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **step),
-             (slot, value, g_out, b_out, old.outer))])
+        if infer and token_step_supported(key, slot) and token_step_supported(slot, value):
+            # inference: both recurrences as one-token steps in one launch (no saved intermediates)
+            (raw, a), (_, b) = gdn_token_many([(qr, key, slot, g_in, b_in, old.inner),
+                                               (None, slot, value, g_out, b_out, old.outer)])
+        else:
+            (raw, _, a), (_, _, b) = _concurrent([
+                (lambda: gdn_scan_hip(qr, key, slot, g_in, b_in, old.inner, **step),
+                 (qr, key, slot, g_in, b_in, old.inner)),
+                (lambda: gdn_scan_hip(None, slot, value, g_out, b_out, old.outer, **step),
+                 (slot, value, g_out, b_out, old.outer))])
         write = _assignment(cfg, slot)
         if write is None:
             write = _read(key, a).softmax(-1)
@@ -454,7 +460,7 @@ def _token(model, q, k, v, state: GPAState, control, position=None):
         rv = torch.einsum("bthm,bhmv->bthv", write.float(), b)
         key, value = _residual(model, key, value, rk, rv, j)
     local = [lg.softmax(-1).to(dtype) for lg in logits]
-    incoming, relations = _relations(model, local, writes, state.relations, step)
+    incoming, relations = _relations(model, local, writes, state.relations, step, token=infer)
     routes, queries = _bridge(model, qr, logits, incoming, [lv.count[:, None] for lv in new_levels])
     weights = model.output_logits.softmax(0)
     out = 0

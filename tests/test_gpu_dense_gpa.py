@@ -123,6 +123,9 @@ CONFIGS = {
                                        paper_product_read=True, relation_marginal=True), b=2, t=5),
     # the tokenwise model (chunk_size 1)
     "tokenwise": dict(cfg=dict(heads=2, key_dim=16, value_dim=8, slots=(6, 4, 5), chunk_size=1), b=2, t=8),
+    # config 1's widths (the reference's CPU case): every recurrence takes the one-token kernels in inference
+    "tokenwise_c1": dict(cfg=dict(heads=4, key_dim=32, value_dim=48, slots=(64, 64, 64, 128), chunk_size=1),
+                         b=2, t=6),
     "tokenwise_lm": dict(cfg=dict(heads=2, key_dim=8, value_dim=6, slots=(8, 8), chunk_size=1, control_dim=5,
                                   rsa_update=True, paper_product_read=True, shared_query_center=True,
                                   balanced_bridge=True, relation_marginal=True, read_scale=8., beta_init=.6,
@@ -265,7 +268,7 @@ def test_dense_gpa_at_a_perturbed_parameter_point(name, dtype):
 
 
 @pytest.mark.parametrize("name", ["tiny_unequal_c3", "tiny_none_c4", "lm_flags", "c2_dims", "c3_dims",
-                                  "tokenwise", "moments", "tokenwise_moments", "product_marginal",
+                                  "tokenwise", "tokenwise_c1", "moments", "tokenwise_moments", "product_marginal",
                                   "product_center"])
 def test_cached_partitions_and_decode_match_oracle(name):
     """Cached calls cut at block-unaligned points, then three one-token decode
