@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 27
+ABI_VERSION = 28
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -192,6 +192,7 @@ class MomentProblem(ctypes.Structure):
                 ("s0", c_vp), ("s0_sb", c_i64), ("s0_sh", c_i64), ("final", c_vp)]
 
 QUAD_MAX_DIM = 256
+SUM_MAX = 8
 
 
 class QuadProblem(ctypes.Structure):
@@ -252,6 +253,7 @@ EXPORTS = {
     "gpa_moment_scan_many": ([ctypes.POINTER(MomentProblem), c_i32, c_vp], ctypes.c_int),
     "gpa_quad_features_forward": ([ctypes.POINTER(QuadProblem), c_vp], ctypes.c_int),
     "gpa_quad_features_backward": ([ctypes.POINTER(QuadProblem), ctypes.POINTER(QuadGrads), c_vp], ctypes.c_int),
+    "gpa_sum_many": ([c_vp, ctypes.POINTER(c_vp), c_i32, c_i64, c_i32, c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -220,6 +220,12 @@ class _GDNScanMany(torch.autograd.Function):
         ctx.geoms = [grp.geom for grp in groups]
         ctx.boxes = [box for _, _, box in spec]
         ctx.save_for_backward(*(t for grp in groups for t in grp.tensors))
+        # inputs that several groups read (a write is an edge's key and another's value)
+        seen: dict[int, list[int]] = {}
+        for pos, t in enumerate(flat):
+            if isinstance(t, torch.Tensor):
+                seen.setdefault(id(t), []).append(pos)
+        ctx.shared = [ps for ps in seen.values() if len(ps) > 1]
         return tuple(x for grp in groups for x in grp.outputs())
 
     @staticmethod
@@ -236,7 +242,43 @@ class _GDNScanMany(torch.autograd.Function):
         timing = profiling.backward_timing_many([gg.timing_args + (gg.inj,) for gg in groups])
         _lib.check(lib.gpa_gdn_backward_many(probs, saved, grads, n, timing,
                                              _lib.stream_handle(saved_t[1].device)), "gpa_gdn_backward_many")
-        return (None,) + tuple(x for gg in groups for x in gg.done())
+        flat = [x for gg in groups for x in gg.done()]
+        for ps in ctx.shared:  # one gradient per shared input, summed in one pass
+            live = [p for p in ps if flat[p] is not None]
+            if len(live) > 1:
+                flat[live[0]] = _sum_many([flat[p] for p in live])
+                for p in live[1:]:
+                    flat[p] = None
+        return (None,) + tuple(flat)
+
+
+def _sum_many(xs: list[Tensor]) -> Tensor:
+    """Elementwise sum of equally shaped tensors (gpa_sum_many: float32
+    accumulation, one rounding); pairwise device adds where the kernel's
+    alignment rules do not hold."""
+    x0 = xs[0]
+    per = 16 // x0.element_size()
+    ok = (x0.dtype in _lib.DTYPE_CODES and x0.numel() % per == 0
+          and all(x.shape == x0.shape and x.dtype == x0.dtype and x.is_contiguous() and x.data_ptr() % 16 == 0
+                  for x in xs))
+    if not ok:
+        out = xs[0]
+        for x in xs[1:]:
+            out = out + x
+        return out
+    lib = _lib.load()
+    out = torch.empty_like(x0)
+    rest = list(xs)
+    first = True
+    while rest:
+        take = rest[:_lib.SUM_MAX - (0 if first else 1)]
+        rest = rest[len(take):]
+        srcs = take if first else [out] + take
+        arr = (ctypes.c_void_p * len(srcs))(*(x.data_ptr() for x in srcs))
+        _lib.check(lib.gpa_sum_many(out.data_ptr(), arr, len(srcs), x0.numel(), _lib.DTYPE_CODES[x0.dtype],
+                                    _lib.stream_handle(x0.device)), "gpa_sum_many")
+        first = False
+    return out
 
 
 class _ReadBox:

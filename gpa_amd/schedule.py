@@ -207,6 +207,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
     key, value = k, v
     levels: list[_Level] = []
     token_logits = []  # (level, j, inner read, old state) whose one-token logits come after the pass
+    etas = _etas(model).unbind(0)  # one unbind: its backward stacks the levels' gradients once
     for j, (old, snap) in enumerate(zip(state.levels, frozen0)):
         lv = _Level()
         act = (_FUSED_SLOTS[0] and slot_gates_supported(cfg, key, cfg.slots[j]) and _GLUE[0]
@@ -216,7 +217,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                 and fused_level_supported(cfg, dtype, key.shape[-1], value.shape[-1], cfg.slots[j])):
             # one token: the slot products and gates inside the A_j step, beside the
             # level write (the last level's alone, as below)
-            eta = _etas(model)[j]
+            eta = etas[j]
             residual = j + 1 < len(state.levels) or not write_only_supported(
                 key.shape[-1], value.shape[-1], cfg.slots[j])
             raw, a_final, slot, _, _, g_out, b_out, write, key_next, value_next = token_slot_step(
@@ -237,7 +238,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         else:
             slot = _slot_feature(cfg, _mm(key, model.center[j], "bthd,hmd->bthm", key.dtype))
             g_in, b_in, g_out, b_out = _gates(model, key, j, control)
-        eta = _etas(model)[j]
+        eta = etas[j]
         write = _assignment(cfg, slot)
         level_kernels = _FUSED_LEVEL[0] and fused_level_supported(
             cfg, dtype, key.shape[-1], value.shape[-1], slot.shape[-1])
@@ -363,8 +364,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
                               and buf.dtype == reads[0].dtype else None)
     else:
         out = 0
-        for j, read in enumerate(reads):
-            out = out + weights[j][..., None] * read
+        for w_j, read in zip(weights.unbind(0), reads):
+            out = out + w_j[..., None] * read
         out = out.to(v.dtype)
 
     # ---- new cache, attention.py:342-344
@@ -684,12 +685,17 @@ def _relations(model, local, writes, rel_states, scan, token=False):
                            lambda: -F.softplus(rd) * (0. if cfg.positional_mode == "none" else 1.),
                            differentiable=True)
     strength = params.derived(("rel_beta", id(rb)), (rb,), lambda: rb.sigmoid(), differentiable=True)
+    # Per-edge [B,T,H] views of both, taken with one unbind: the backward then
+    # stacks the edges' gradients once and reduces them in one sum, instead of
+    # a reduction, a zero fill, a copy and an add per edge and tensor.
+    lead = writes[0].shape[:-1]
+    n_e = len(model.edges)
+    g_edge = decay[:, None, None, :].expand(n_e, *lead).unbind(0)
+    b_edge = strength[:, None, None, :].expand(n_e, *lead).unbind(0)
 
     def edge(e, i, j, old):
         def run():
-            lead = writes[i].shape[:-1]
-            g = decay[e].expand(lead)
-            beta = strength[e].expand(lead)
+            g, beta = g_edge[e], b_edge[e]
             target = writes[j]
             if cfg.rsa_update:
                 target, beta = _rsa_target(writes[i], target, beta)
@@ -701,10 +707,9 @@ def _relations(model, local, writes, rel_states, scan, token=False):
 
     if token and all(token_step_supported(writes[i], writes[j]) for i, j in model.edges):
         # every edge's one-token step, packed into as few launches as the library takes
-        lead = writes[0].shape[:-1]
         calls = []
         for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
-            g, beta, target = decay[e].expand(lead), strength[e].expand(lead), writes[j]
+            g, beta, target = g_edge[e], b_edge[e], writes[j]
             if cfg.rsa_update:
                 target, beta = _rsa_target(writes[i], target, beta)
             calls.append((local[i], writes[i], target, g, beta, old.memory))
@@ -712,10 +717,9 @@ def _relations(model, local, writes, rel_states, scan, token=False):
     elif _PACKED[0]:
         # every edge's scan in as few library calls as it takes: the state
         # recurrences of all edges advance together
-        lead = writes[0].shape[:-1]
         groups = []
         for e, ((i, j), old) in enumerate(zip(model.edges, rel_states)):
-            g, beta, target = decay[e].expand(lead), strength[e].expand(lead), writes[j]
+            g, beta, target = g_edge[e], b_edge[e], writes[j]
             if cfg.rsa_update:
                 target, beta = _rsa_target(writes[i], target, beta)
             groups.append(dict(q=local[i], k=writes[i], v=target, g=g, beta=beta, s0=old.memory, **scan))

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 27
+#define GPA_HIP_ABI_VERSION 28
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -704,6 +704,16 @@ typedef struct gpa_quad_grads {
 
 int gpa_quad_features_forward(const gpa_quad_problem *problem, hipStream_t stream);
 int gpa_quad_features_backward(const gpa_quad_problem *problem, const gpa_quad_grads *grads, hipStream_t stream);
+
+/* dst = src[0] + ... + src[n-1] elementwise over `count` elements of dtype,
+ * accumulated in float32 and rounded once; 1 <= n <= GPA_SUM_MAX, every
+ * pointer 16-byte aligned and count a whole number of 16-byte vectors (dst may
+ * be one of the sources).  No reference counterpart: autograd sums the
+ * gradients of an input that several groups of one packed scan call read
+ * (reference packed.py:121, a level's write feeds six relation edges) with
+ * pairwise adds; the packed call's backward forms that sum in one pass. */
+#define GPA_SUM_MAX 8
+int gpa_sum_many(void *dst, const void *const *src, int32_t n, int64_t count, int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -99,3 +99,26 @@ def test_two_stage_gdn_reproduces_reference_fixture(name):
     print(name, "worst", max(errors.items(), key=lambda kv: kv[1]))
     bad = {k: e for k, e in errors.items() if e > tol}
     assert not bad, bad
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("n", [1, 2, 6, 8, 11])
+def test_sum_many_matches_float32_sum(n, dtype):
+    """gpa_sum_many (the packed backward's gradient sum of a shared input):
+    float32 accumulation and one rounding, bit for bit against torch's float32
+    sum rounded once; more than 8 sources in several passes."""
+    from gpa_amd.ops import _sum_many
+    g = torch.Generator().manual_seed(n)
+    xs = [torch.randn(3, 40, 2, 16, generator=g).to(dtype).to("cuda") for _ in range(n)]
+    got = _sum_many(xs)
+    want = torch.stack([x.float() for x in xs]).sum(0)
+    assert got.shape == want.shape and got.dtype == dtype
+    err = (got.float() - want).abs()
+    if dtype == torch.float32:
+        assert (err <= 1e-6 * want.abs() + 1e-6).all()
+    else:  # one rounding per pass (8 sources, then the partial sum and the rest): half an ulp each
+        bound = 2 ** -8 * want.abs()
+        if n > 8:
+            bound = bound + 2 ** -8 * torch.stack([x.float() for x in xs[:8]]).sum(0).abs()
+        assert (err <= bound + 1e-6).all()
