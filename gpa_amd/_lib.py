@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 28
+ABI_VERSION = 29
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -180,6 +180,13 @@ class MixProblem(ctypes.Structure):
                [("read", Operand * DECODE_MAX_LEVELS), ("weights", c_vp), ("out", Operand)]
 
 
+MIX_MAX_HEADS = 256
+
+
+class MixGrads(ctypes.Structure):
+    _fields_ = [("dout", Operand), ("dread", Operand * DECODE_MAX_LEVELS), ("dweights", c_vp)]
+
+
 GATE_NONE, GATE_TOKEN, GATE_KEY, GATE_VALUE = 0, 1, 2, 3
 MOMENT_MAX_KDIM = 256
 MOMENT_MAX_PACK = 4
@@ -248,6 +255,7 @@ EXPORTS = {
     "gpa_product_read_backward": ([ctypes.POINTER(ProductProblem), ctypes.POINTER(ProductGrads), c_vp], ctypes.c_int),
     "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
+    "gpa_output_mix_backward": ([ctypes.POINTER(MixProblem), ctypes.POINTER(MixGrads), c_vp], ctypes.c_int),
     "gpa_copy_many": ([ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(ctypes.c_int64), c_i32, c_vp],
                       ctypes.c_int),
     "gpa_moment_scan_many": ([ctypes.POINTER(MomentProblem), c_i32, c_vp], ctypes.c_int),

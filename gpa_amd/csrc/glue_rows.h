@@ -25,10 +25,10 @@ __device__ __forceinline__ void gate_values(const gpa_gate_problem& p, int h, co
   float x[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) x[c] = raw[c] + p.bias[4 * h + c];
-  v[0] = __fmul_rn(-fminf(softplus20(x[0]), 10.f), p.decay_scale);
-  v[1] = __fmul_rn(p.beta_max, sigmoid1(x[1]));
-  v[2] = __fmul_rn(-fminf(softplus20(x[2]), 10.f), p.decay_scale);
-  v[3] = __fmul_rn(p.beta_max, sigmoid1(x[3]));
+  v[0] = mul_rn(-fminf(softplus20(x[0]), 10.f), p.decay_scale);
+  v[1] = mul_rn(p.beta_max, sigmoid1(x[1]));
+  v[2] = mul_rn(-fminf(softplus20(x[2]), 10.f), p.decay_scale);
+  v[3] = mul_rn(p.beta_max, sigmoid1(x[3]));
 }
 __device__ __forceinline__ void gate_row(const gpa_gate_problem& p, int h, int64_t i, const float raw[4]) {
   float v[4];
@@ -56,7 +56,7 @@ __device__ __forceinline__ void token_logits_row(const gpa_token_logits_problem&
       const float n = c0[m] + act_at<E>(p.write, b, 0, h, m);
       p.count[(int64_t)row * M + m] = n;
       // separate roundings, as the reference's tensor ops (no contraction)
-      lg[i] = __fadd_rn(__fmul_rn(scale, act_at<E>(p.raw, b, 0, h, m)), __fmul_rn(gain, log1pf(n)));
+      lg[i] = add_rn(mul_rn(scale, act_at<E>(p.raw, b, 0, h, m)), mul_rn(gain, log1pf(n)));
       p.logits[(int64_t)row * M + m] = lg[i];
       mx = fmaxf(mx, lg[i]);
     }

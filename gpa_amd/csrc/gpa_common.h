@@ -26,6 +26,26 @@ template <typename E> __device__ __forceinline__ E from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return f32_to_bf16(x); }
 
+// One IEEE operation, rounded on its own: the compiler may not fuse these into
+// an FMA (the pragma strips the contraction flag from the operation), which the
+// reference's separately rounded products and sums require.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
+
 // Value after a round trip through E: the reference rounds normalised keys and
 // queries to the activation dtype before the fp32 state arithmetic.
 template <typename E> __device__ __forceinline__ float round_as(float x) { return to_f32(from_f32<E>(x)); }

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(PNT) void product_fwd(gpa_product_problem p) {
   const int r = blockIdx.x * GPA_PRODUCT_ROWS + (threadIdx.x >> 6);
   if (r >= R) return;
   const int b = r / p.tokens, t = r - b * p.tokens;
-  const float gexp = p.gexp[h], mg = __fmul_rn((float)M, gexp);
+  const float gexp = p.gexp[h], mg = mul_rn((float)M, gexp);
   float wn[GPA_ROUTE_MAX_INCOMING], nr[GPA_ROUTE_MAX_INCOMING];
 #pragma unroll
   for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) {
@@ -56,9 +56,9 @@ __global__ __launch_bounds__(PNT) void product_fwd(gpa_product_problem p) {
     float inc = 0.f;
 #pragma unroll
     for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
-      if (e < p.incoming) inc = __fadd_rn(inc, __fmul_rn(__fmul_rn(wn[e], mv[e][i]), nr[e]));
-    float y = __fadd_rn(x[i], __fmul_rn(mg, inc));
-    if (p.marginal) y = __fsub_rn(y, __fmul_rn(gexp, log1pf(cv[i])));
+      if (e < p.incoming) inc = add_rn(inc, mul_rn(mul_rn(wn[e], mv[e][i]), nr[e]));
+    float y = add_rn(x[i], mul_rn(mg, inc));
+    if (p.marginal) y = sub_rn(y, mul_rn(gexp, log1pf(cv[i])));
     out[m] = y;
   }
 }
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(PNT) void product_bwd(gpa_product_problem p, gpa_pr
   float s_inc = 0.f, s_log = 0.f, s_w[GPA_ROUTE_MAX_INCOMING] = {};
   if (r < R) {
     const int b = r / p.tokens, t = r - b * p.tokens;
-    const float gexp = p.gexp[h], mg = __fmul_rn((float)M, gexp);
+    const float gexp = p.gexp[h], mg = mul_rn((float)M, gexp);
     float wn[GPA_ROUTE_MAX_INCOMING], nr[GPA_ROUTE_MAX_INCOMING];
 #pragma unroll
     for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e) {
@@ -95,26 +95,26 @@ __global__ __launch_bounds__(PNT) void product_bwd(gpa_product_problem p, gpa_pr
     for (int i = 0; i < PPER; ++i) {
       const int m = lane + 64 * i;
       if (m >= M) continue;
-      const float d = dv[i], dinc = __fmul_rn(d, mg);
+      const float d = dv[i], dinc = mul_rn(d, mg);
       float inc = 0.f;
 #pragma unroll
       for (int e = 0; e < GPA_ROUTE_MAX_INCOMING; ++e)
         if (e < NI) {
-          const float wm = __fmul_rn(wn[e], mv[e][i]);
-          inc = __fadd_rn(inc, __fmul_rn(wm, nr[e]));
-          const float gwm = __fmul_rn(dinc, nr[e]);  // gradient of w_e msg_e
+          const float wm = mul_rn(wn[e], mv[e][i]);
+          inc = add_rn(inc, mul_rn(wm, nr[e]));
+          const float gwm = mul_rn(dinc, nr[e]);  // gradient of w_e msg_e
           s_n[e] += dinc * wm;
           s_w[e] += gwm * mv[e][i];
           E* dm = reinterpret_cast<E*>(g.dmsg[e].ptr) + (int64_t)b * g.dmsg[e].sb + (int64_t)t * g.dmsg[e].st +
                   (int64_t)h * g.dmsg[e].sh;
-          dm[m] = from_f32<E>(__fmul_rn(gwm, wn[e]));
+          dm[m] = from_f32<E>(mul_rn(gwm, wn[e]));
         }
       s_inc += d * inc;
       if (p.marginal) {
         const float lg = log1pf(cv[i]);
         s_log += d * lg;
         // out -= gexp log1p(counts): d counts = (-dout gexp) / (1 + counts)
-        g.dcounts[row * M + m] = __fdiv_rn(-__fmul_rn(d, gexp), __fadd_rn(1.f, cv[i]));
+        g.dcounts[row * M + m] = div_rn(-mul_rn(d, gexp), add_rn(1.f, cv[i]));
       }
     }
 #pragma unroll

@@ -654,7 +654,8 @@ __global__ __launch_bounds__(64 * RPACK_W) void route_fwd_pack(RoutePack pk) {
 // The two reference flags that act on whole rows between the products (sums
 // over the M slots), as row kernels: 8 threads per row, the RR rows of one
 // head per workgroup (grid: row tiles x heads).  Products and sums whose
-// rounding the reference fixes are written with __fmul_rn / __fadd_rn.
+// rounding the reference fixes are written with mul_rn / add_rn (no FMA
+// contraction).
 
 struct RowCtx {
   int M, R, h, tile, row, part, r, rc;
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(RNT) void route_mix_fwd(gpa_route_problem p) {
       const int m = c.part + 8 * i;
       if (m < c.M) {
         const float ua = round_as<E>(a[i] / na), ub = round_as<E>(b[i] / nb);
-        qo[m] = from_f32<E>(round_as<E>(__fadd_rn(__fmul_rn(mix, ua), __fmul_rn(omix, ub))));
+        qo[m] = from_f32<E>(round_as<E>(add_rn(mul_rn(mix, ua), mul_rn(omix, ub))));
       }
     }
   }
@@ -772,8 +773,8 @@ __global__ __launch_bounds__(RNT) void route_mix_bwd(gpa_route_problem p, gpa_ro
     const bool on = c.part + 8 * i < c.M;
     const float ua = on ? round_as<E>(a[i] / ca) : 0.f, ub = on ? round_as<E>(b[i] / cb) : 0.f;
     part += d[i] * ua - d[i] * ub;
-    dua[i] = on ? round_as<E>(__fmul_rn(d[i], mix)) : 0.f;
-    dub[i] = on ? round_as<E>(__fmul_rn(d[i], omix)) : 0.f;
+    dua[i] = on ? round_as<E>(mul_rn(d[i], mix)) : 0.f;
+    dub[i] = on ? round_as<E>(mul_rn(d[i], omix)) : 0.f;
   }
   float dxa[RPER], dxb[RPER];
   unit_bwd(a, dua, na, dxa);

@@ -58,6 +58,7 @@ __global__ __launch_bounds__(256) void token_logits_pack(LogitsPack pk) {
 // out = round(sum_j w[j,h] read_j), summed in level order (attention.py:340-341).
 template <typename E>
 __global__ void output_mix(gpa_mix_problem p) {
+#pragma clang fp contract(off)
   const int64_t n = (int64_t)p.batch * p.tokens * p.heads * p.value_dim;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -67,10 +68,65 @@ __global__ void output_mix(gpa_mix_problem p) {
   r /= p.heads;
   const int t = (int)(r % p.tokens), b = (int)(r / p.tokens);
   float acc = 0.f;
-  for (int j = 0; j < p.levels; ++j)  // a product and a sum per level, rounded separately (no contraction)
-    acc = __fadd_rn(acc, __fmul_rn(p.weights[j * p.heads + h], act_at<E>(p.read[j], b, t, h, d)));
+  for (int j = 0; j < p.levels; ++j) {  // a product and a sum per level, rounded separately (no contraction)
+    const float prod = p.weights[j * p.heads + h] * act_at<E>(p.read[j], b, t, h, d);
+    acc = acc + prod;
+  }
   reinterpret_cast<E*>(p.out.ptr)[(int64_t)b * p.out.sb + (int64_t)t * p.out.st + (int64_t)h * p.out.sh + d] =
       from_f32<E>(acc);
+}
+
+// Backward of output_mix over tiles of MIX_ROWS tokens: dread_j = round(w[j,h]
+// dout) (the gradient of w x in float32, cast to the reads' type) and the
+// tile's partial sums of dw[j,h] = sum dout read_j.  Thread t owns the
+// columns t, t + 256, ... of a token's H*V values, so its column heads are
+// fixed and its partial sums stay in registers until one LDS reduction.
+constexpr int MIX_ROWS = 32, MIX_COLS = 16;
+
+template <typename E>
+__global__ __launch_bounds__(256) void output_mix_bwd(gpa_mix_problem p, gpa_mix_grads g) {
+  __shared__ float dw[GPA_DECODE_MAX_LEVELS * GPA_MIX_MAX_HEADS];
+  const int tid = threadIdx.x, H = p.heads, V = p.value_dim, HV = H * V, L = p.levels;
+  for (int i = tid; i < L * H; i += 256) dw[i] = 0.f;
+  __syncthreads();
+  float acc[GPA_DECODE_MAX_LEVELS][MIX_COLS];
+#pragma unroll
+  for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j)
+#pragma unroll
+    for (int ci = 0; ci < MIX_COLS; ++ci) acc[j][ci] = 0.f;
+  const int64_t rows = (int64_t)p.batch * p.tokens, r0 = (int64_t)blockIdx.x * MIX_ROWS;
+  const int64_t r1 = r0 + MIX_ROWS < rows ? r0 + MIX_ROWS : rows;
+  for (int64_t r = r0; r < r1; ++r) {
+    const int b = (int)(r / p.tokens), t = (int)(r % p.tokens);
+#pragma unroll
+    for (int ci = 0; ci < MIX_COLS; ++ci) {
+      const int c = tid + 256 * ci;
+      if (c < HV) {
+        const int h = c / V, d = c % V;
+        const float go = act_at<E>(g.dout, b, t, h, d);
+#pragma unroll
+        for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j) {
+          if (j >= L) break;
+          const float x = act_at<E>(p.read[j], b, t, h, d);
+          const gpa_operand& o = g.dread[j];
+          reinterpret_cast<E*>(o.ptr)[(int64_t)b * o.sb + (int64_t)t * o.st + (int64_t)h * o.sh + d] =
+              from_f32<E>(go * p.weights[j * H + h]);
+          acc[j][ci] += go * x;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int ci = 0; ci < MIX_COLS; ++ci) {
+    const int c = tid + 256 * ci;
+    if (c < HV) {
+#pragma unroll
+      for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j)
+        if (j < L) atomicAdd(&dw[j * H + c / V], acc[j][ci]);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < L * H; i += 256) g.dweights[(int64_t)blockIdx.x * L * H + i] = dw[i];
 }
 
 }  // namespace
@@ -206,4 +262,26 @@ extern "C" int gpa_copy_many(void* const* dst, const void* const* src, const int
   const int64_t blocks = (most + 255) / 256;
   hipLaunchKernelGGL(copy_many, dim3((unsigned)(blocks < 1024 ? blocks : 1024), (unsigned)n), dim3(256), 0, stream, pk);
   return check_launch("gpa_copy_many");
+}
+
+extern "C" int gpa_output_mix_backward(const gpa_mix_problem* p, const gpa_mix_grads* g, hipStream_t stream) {
+  using namespace gpa;
+  if (!p || !g || !p->weights || !g->dout.ptr || !g->dweights) return fail(GPA_HIP_EINVAL, "output mix backward: null pointer");
+  if (p->levels < 1 || p->levels > GPA_DECODE_MAX_LEVELS)
+    return fail(GPA_HIP_EINVAL, "output mix backward: 1 to 4 levels");
+  for (int j = 0; j < p->levels; ++j)
+    if (!p->read[j].ptr || !g->dread[j].ptr) return fail(GPA_HIP_EINVAL, "output mix backward: null read");
+  if (p->batch < 1 || p->tokens < 1 || p->heads < 1 || p->value_dim < 1)
+    return fail(GPA_HIP_EINVAL, "output mix backward: empty shape");
+  if (p->heads > GPA_MIX_MAX_HEADS || (int64_t)p->heads * p->value_dim > 256 * MIX_COLS)
+    return fail(GPA_HIP_EUNSUPPORTED, "output mix backward: heads <= GPA_MIX_MAX_HEADS, heads*value_dim <= 4096");
+  if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16)
+    return fail(GPA_HIP_EUNSUPPORTED, "output mix backward: dtype");
+  const int64_t tiles = ((int64_t)p->batch * p->tokens + MIX_ROWS - 1) / MIX_ROWS;
+  if (tiles > 0x7fffffff) return fail(GPA_HIP_EINVAL, "output mix backward: too many tokens");
+  if (p->dtype == GPA_DTYPE_BF16)
+    hipLaunchKernelGGL(output_mix_bwd<bf16_t>, dim3((unsigned)tiles), dim3(256), 0, stream, *p, *g);
+  else
+    hipLaunchKernelGGL(output_mix_bwd<float>, dim3((unsigned)tiles), dim3(256), 0, stream, *p, *g);
+  return check_launch("gpa_output_mix_backward");
 }

@@ -97,6 +97,64 @@ def output_mix(reads, weights: Tensor, out: Tensor | None = None) -> Tensor:
     return out
 
 
+def _mix_problem(reads, weights: Tensor, out: Tensor | None) -> _lib.MixProblem:
+    b, t, h, dv = reads[0].shape
+    p = _lib.MixProblem()
+    p.batch, p.tokens, p.heads, p.value_dim, p.levels = b, t, h, dv, len(reads)
+    p.dtype = _lib.DTYPE_CODES[reads[0].dtype]
+    for j, r in enumerate(reads):
+        p.read[j] = _lib.operand(r)
+    p.weights = weights.data_ptr()
+    p.out = _lib.operand(out)
+    return p
+
+
+class _OutputMix(torch.autograd.Function):
+    """The output mix with its gradient (attention.py:340-341):
+    gpa_output_mix_forward, then gpa_output_mix_backward (the reads' gradients
+    and per-tile partial sums of the weights' gradient)."""
+
+    @staticmethod
+    def forward(ctx, weights, *reads):
+        reads = [r if r.stride(-1) == 1 else r.contiguous() for r in reads]
+        w = weights.detach().float().contiguous()
+        out = output_mix(reads, w)
+        ctx.save_for_backward(w, *reads)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        w, *reads = ctx.saved_tensors
+        b, t, h, dv = reads[0].shape
+        dout = dout.to(reads[0].dtype)
+        dout = dout if dout.stride(-1) == 1 else dout.contiguous()
+        dreads = [torch.empty_like(r) for r in reads]
+        tiles = -(-(b * t) // 32)
+        part = torch.empty(tiles, len(reads), h, device=dout.device, dtype=torch.float32)
+        g = _lib.MixGrads()
+        g.dout = _lib.operand(dout)
+        for j, d in enumerate(dreads):
+            g.dread[j] = _lib.operand(d)
+        g.dweights = part.data_ptr()
+        _lib.check(lib.gpa_output_mix_backward(_mix_problem(reads, w, None), g, _lib.stream_handle(dout.device)),
+                   "gpa_output_mix_backward")
+        return (part.sum(0), *dreads)
+
+
+def output_mix_supported(reads) -> bool:
+    r0 = reads[0]
+    return (1 <= len(reads) <= _lib.DECODE_MAX_LEVELS and r0.dtype in _lib.DTYPE_CODES and r0.ndim == 4
+            and r0.shape[1] > 0 and r0.shape[2] <= _lib.MIX_MAX_HEADS and r0.shape[2] * r0.shape[3] <= 4096
+            and all(r.shape == r0.shape and r.dtype == r0.dtype for r in reads))
+
+
+def output_mix_train(reads, weights: Tensor) -> Tensor:
+    """sum_j weights[j][h] reads[j] rounded to the reads' dtype, differentiable
+    in the reads and the weights [L,H]."""
+    return _OutputMix.apply(weights, *reads)
+
+
 COPY_MAX = 4  # buffers per gpa_copy_many launch
 
 

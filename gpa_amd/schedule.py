@@ -362,6 +362,8 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
         buf = _OUT_BUFFER[0]
         out = glue.output_mix(reads, weights, buf if buf is not None and buf.shape == reads[0].shape
                               and buf.dtype == reads[0].dtype else None)
+    elif _GLUE[0] and all(r.dtype == v.dtype for r in reads) and glue.output_mix_supported(reads):
+        out = glue.output_mix_train(reads, weights)
     else:
         out = 0
         for w_j, read in zip(weights.unbind(0), reads):

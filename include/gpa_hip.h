@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 28
+#define GPA_HIP_ABI_VERSION 29
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -619,6 +619,18 @@ typedef struct gpa_mix_problem {
     gpa_operand out;                              /* [B,T,H,Dv] */
 } gpa_mix_problem;
 int gpa_output_mix_forward(const gpa_mix_problem *problem, hipStream_t stream);
+
+/* Backward of the output mix (its autograd, attention.py:340-341):
+ * dread_j = round(w[j][h] dout) and dweights [ceil(B*T/32)][levels][heads],
+ * per-32-token partial sums of sum dout read_j (the caller sums the tiles).
+ * heads <= GPA_MIX_MAX_HEADS, heads*value_dim <= 4096. */
+#define GPA_MIX_MAX_HEADS 256
+typedef struct gpa_mix_grads {
+    gpa_operand dout;                             /* [B,T,H,Dv] in dtype */
+    gpa_operand dread[GPA_DECODE_MAX_LEVELS];     /* out [B,T,H,Dv] in dtype */
+    float *dweights;                              /* out, see above */
+} gpa_mix_grads;
+int gpa_output_mix_backward(const gpa_mix_problem *problem, const gpa_mix_grads *grads, hipStream_t stream);
 /* Device-to-device copies of up to GPA_COPY_MAX buffers in one launch: dst[i]
  * <- src[i], bytes[i] each, every pointer and size a multiple of 16 bytes
  * (GPA_HIP_EINVAL otherwise).  No reference counterpart: it moves a decode

@@ -122,3 +122,35 @@ def test_sum_many_matches_float32_sum(n, dtype):
         if n > 8:
             bound = bound + 2 ** -8 * torch.stack([x.float() for x in xs[:8]]).sum(0).abs()
         assert (err <= bound + 1e-6).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("levels,b,t,h,dv", [(4, 1, 70, 2, 24), (3, 2, 33, 16, 128), (1, 1, 5, 3, 7)])
+def test_output_mix_train_matches_device_ops(levels, b, t, h, dv, dtype):
+    """The trainable output mix (attention.py:340-341) against the same sum as
+    device tensor operations: output bit for bit; the reads' gradients bit for
+    bit (each one product rounded once), the weights' gradient to float32
+    summation order."""
+    from gpa_amd import glue
+    g = torch.Generator().manual_seed(levels * 100 + t)
+    reads = [torch.randn(b, t, h, dv, generator=g).to(dtype).cuda().requires_grad_() for _ in range(levels)]
+    logits = torch.randn(levels, h, generator=g).cuda().requires_grad_()
+    dout = torch.randn(b, t, h, dv, generator=g).to(dtype).cuda()
+    out = glue.output_mix_train(reads, logits.softmax(0))
+    out.backward(dout)
+    got = [out.detach()] + [r.grad.clone() for r in reads] + [logits.grad.clone()]
+    for r in reads:
+        r.grad = None
+    logits.grad = None
+    w = logits.softmax(0)
+    ref = 0
+    for j, r in enumerate(reads):
+        ref = ref + w[j][..., None] * r
+    ref = ref.to(dtype)
+    ref.backward(dout)
+    want = [ref.detach()] + [r.grad for r in reads] + [logits.grad]
+    assert torch.equal(got[0], want[0])
+    for a, r in zip(got[1:-1], want[1:-1]):
+        assert torch.equal(a, r)
+    assert torch.allclose(got[-1], want[-1], rtol=1e-5, atol=1e-6)  # one level: the softmax's gradient is 0
