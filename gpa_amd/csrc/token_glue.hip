@@ -78,52 +78,119 @@ __global__ void output_mix(gpa_mix_problem p) {
 
 // Backward of output_mix over tiles of MIX_ROWS tokens: dread_j = round(w[j,h]
 // dout) (the gradient of w x in float32, cast to the reads' type) and the
-// tile's partial sums of dw[j,h] = sum dout read_j.  Thread t owns the
-// columns t, t + 256, ... of a token's H*V values, so its column heads are
-// fixed and its partial sums stay in registers until one LDS reduction.
-constexpr int MIX_ROWS = 32, MIX_COLS = 16;
+// tile's partial sums of dw[j,h] = sum dout read_j.  Thread t owns the 16-byte
+// column vectors t, t + 256 of a token's H*V values (one head each: V is a
+// whole number of vectors), so its partial sums stay in registers until one
+// LDS reduction; the loads of four rows are issued before their use.
+constexpr int MIX_ROWS = 32, MIX_VECS = 2, MIX_UNROLL = 4;
+
+template <typename E>
+struct MixVec {
+  static constexpr int N = 16 / sizeof(E);  // elements per 16-byte vector
+};
+
+template <typename E>
+__device__ __forceinline__ void unpack16(uint4 w, float (&x)[MixVec<E>::N]) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (sizeof(E) == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(u[i] << 16);
+      x[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(u[i]);
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ uint4 pack16(const float (&x)[MixVec<E>::N]) {
+  uint32_t u[4];
+  if constexpr (sizeof(E) == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      u[i] = (uint32_t)from_f32<bf16_t>(x[2 * i]).bits | ((uint32_t)from_f32<bf16_t>(x[2 * i + 1]).bits << 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = __float_as_uint(x[i]);
+  }
+  return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+__device__ __forceinline__ int64_t mix_at(const gpa_operand& o, int b, int t, int h, int d) {
+  return (int64_t)b * o.sb + (int64_t)t * o.st + (int64_t)h * o.sh + d;
+}
 
 template <typename E>
 __global__ __launch_bounds__(256) void output_mix_bwd(gpa_mix_problem p, gpa_mix_grads g) {
-  __shared__ float dw[GPA_DECODE_MAX_LEVELS * GPA_MIX_MAX_HEADS];
-  const int tid = threadIdx.x, H = p.heads, V = p.value_dim, HV = H * V, L = p.levels;
+  constexpr int N = MixVec<E>::N, LMAX = GPA_DECODE_MAX_LEVELS;
+  __shared__ float dw[LMAX * GPA_MIX_MAX_HEADS];
+  const int tid = threadIdx.x, H = p.heads, V = p.value_dim, NV = H * V / N, L = p.levels;
   for (int i = tid; i < L * H; i += 256) dw[i] = 0.f;
   __syncthreads();
-  float acc[GPA_DECODE_MAX_LEVELS][MIX_COLS];
+  float acc[MIX_VECS][LMAX];
+  float wv[MIX_VECS][LMAX];
+  int hv[MIX_VECS], dv[MIX_VECS];
 #pragma unroll
-  for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j)
+  for (int ci = 0; ci < MIX_VECS; ++ci) {
+    const int c = (tid + 256 * ci) * N, cc = c < H * V ? c : 0;
+    hv[ci] = cc / V;
+    dv[ci] = cc % V;
 #pragma unroll
-    for (int ci = 0; ci < MIX_COLS; ++ci) acc[j][ci] = 0.f;
+    for (int j = 0; j < LMAX; ++j) {
+      acc[ci][j] = 0.f;
+      wv[ci][j] = j < L ? p.weights[j * H + hv[ci]] : 0.f;
+    }
+  }
   const int64_t rows = (int64_t)p.batch * p.tokens, r0 = (int64_t)blockIdx.x * MIX_ROWS;
-  const int64_t r1 = r0 + MIX_ROWS < rows ? r0 + MIX_ROWS : rows;
-  for (int64_t r = r0; r < r1; ++r) {
-    const int b = (int)(r / p.tokens), t = (int)(r % p.tokens);
+  for (int64_t rb = r0; rb < r0 + MIX_ROWS; rb += MIX_UNROLL) {
 #pragma unroll
-    for (int ci = 0; ci < MIX_COLS; ++ci) {
-      const int c = tid + 256 * ci;
-      if (c < HV) {
-        const int h = c / V, d = c % V;
-        const float go = act_at<E>(g.dout, b, t, h, d);
+    for (int ci = 0; ci < MIX_VECS; ++ci) {
+      if (tid + 256 * ci >= NV) continue;
+      uint4 go[MIX_UNROLL], rd[MIX_UNROLL][LMAX];
+      // every load of the four rows first (clamped to a valid row), then the math
 #pragma unroll
-        for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j) {
+      for (int u = 0; u < MIX_UNROLL; ++u) {
+        const int64_t r = rb + u < rows ? rb + u : rows - 1;
+        const int b = (int)(r / p.tokens), t = (int)(r % p.tokens);
+        go[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const E*>(g.dout.ptr) +
+                                                mix_at(g.dout, b, t, hv[ci], dv[ci]));
+#pragma unroll
+        for (int j = 0; j < LMAX; ++j)
+          rd[u][j] = j < L ? *reinterpret_cast<const uint4*>(reinterpret_cast<const E*>(p.read[j].ptr) +
+                                                            mix_at(p.read[j], b, t, hv[ci], dv[ci]))
+                           : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < MIX_UNROLL; ++u) {
+        if (rb + u >= rows || rb + u >= r0 + MIX_ROWS) continue;
+        const int64_t r = rb + u;
+        const int b = (int)(r / p.tokens), t = (int)(r % p.tokens);
+        float gx[N];
+        unpack16<E>(go[u], gx);
+#pragma unroll
+        for (int j = 0; j < LMAX; ++j) {
           if (j >= L) break;
-          const float x = act_at<E>(p.read[j], b, t, h, d);
-          const gpa_operand& o = g.dread[j];
-          reinterpret_cast<E*>(o.ptr)[(int64_t)b * o.sb + (int64_t)t * o.st + (int64_t)h * o.sh + d] =
-              from_f32<E>(go * p.weights[j * H + h]);
-          acc[j][ci] += go * x;
+          float x[N], y[N];
+          unpack16<E>(rd[u][j], x);
+#pragma unroll
+          for (int e = 0; e < N; ++e) {
+            y[e] = gx[e] * wv[ci][j];
+            acc[ci][j] += gx[e] * x[e];
+          }
+          *reinterpret_cast<uint4*>(reinterpret_cast<E*>(g.dread[j].ptr) + mix_at(g.dread[j], b, t, hv[ci], dv[ci])) =
+              pack16<E>(y);
         }
       }
     }
   }
 #pragma unroll
-  for (int ci = 0; ci < MIX_COLS; ++ci) {
-    const int c = tid + 256 * ci;
-    if (c < HV) {
+  for (int ci = 0; ci < MIX_VECS; ++ci) {
+    if (tid + 256 * ci >= NV) continue;
 #pragma unroll
-      for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j)
-        if (j < L) atomicAdd(&dw[j * H + c / V], acc[j][ci]);
-    }
+    for (int j = 0; j < LMAX; ++j)
+      if (j < L) atomicAdd(&dw[j * H + hv[ci]], acc[ci][j]);
   }
   __syncthreads();
   for (int i = tid; i < L * H; i += 256) g.dweights[(int64_t)blockIdx.x * L * H + i] = dw[i];
@@ -273,8 +340,15 @@ extern "C" int gpa_output_mix_backward(const gpa_mix_problem* p, const gpa_mix_g
     if (!p->read[j].ptr || !g->dread[j].ptr) return fail(GPA_HIP_EINVAL, "output mix backward: null read");
   if (p->batch < 1 || p->tokens < 1 || p->heads < 1 || p->value_dim < 1)
     return fail(GPA_HIP_EINVAL, "output mix backward: empty shape");
-  if (p->heads > GPA_MIX_MAX_HEADS || (int64_t)p->heads * p->value_dim > 256 * MIX_COLS)
-    return fail(GPA_HIP_EUNSUPPORTED, "output mix backward: heads <= GPA_MIX_MAX_HEADS, heads*value_dim <= 4096");
+  const int vec = p->dtype == GPA_DTYPE_BF16 ? 8 : 4;  // elements per 16-byte vector
+  if (p->heads > GPA_MIX_MAX_HEADS || (int64_t)p->heads * p->value_dim > 256 * MIX_VECS * vec)
+    return fail(GPA_HIP_EUNSUPPORTED, "output mix backward: heads <= GPA_MIX_MAX_HEADS, heads*value_dim <= 512 vectors");
+  auto aligned = [&](const gpa_operand& o) {
+    return (uintptr_t)o.ptr % 16 == 0 && o.sb % vec == 0 && o.st % vec == 0 && o.sh % vec == 0;
+  };
+  bool ok = p->value_dim % vec == 0 && aligned(g->dout);
+  for (int j = 0; j < p->levels; ++j) ok = ok && aligned(p->read[j]) && aligned(g->dread[j]);
+  if (!ok) return fail(GPA_HIP_EINVAL, "output mix backward: 16-byte aligned rows, value_dim a whole number of vectors");
   if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16)
     return fail(GPA_HIP_EUNSUPPORTED, "output mix backward: dtype");
   const int64_t tiles = ((int64_t)p->batch * p->tokens + MIX_ROWS - 1) / MIX_ROWS;

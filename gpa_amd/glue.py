@@ -127,8 +127,7 @@ class _OutputMix(torch.autograd.Function):
         lib = _lib.load()
         w, *reads = ctx.saved_tensors
         b, t, h, dv = reads[0].shape
-        dout = dout.to(reads[0].dtype)
-        dout = dout if dout.stride(-1) == 1 else dout.contiguous()
+        dout = dout.to(reads[0].dtype).contiguous()
         dreads = [torch.empty_like(r) for r in reads]
         tiles = -(-(b * t) // 32)
         part = torch.empty(tiles, len(reads), h, device=dout.device, dtype=torch.float32)
@@ -143,10 +142,16 @@ class _OutputMix(torch.autograd.Function):
 
 
 def output_mix_supported(reads) -> bool:
+    """Shapes the backward kernel takes: 16-byte value vectors (V a multiple of
+    8 in bf16, 4 in float32), at most 512 of them per token, contiguous reads."""
     r0 = reads[0]
-    return (1 <= len(reads) <= _lib.DECODE_MAX_LEVELS and r0.dtype in _lib.DTYPE_CODES and r0.ndim == 4
-            and r0.shape[1] > 0 and r0.shape[2] <= _lib.MIX_MAX_HEADS and r0.shape[2] * r0.shape[3] <= 4096
-            and all(r.shape == r0.shape and r.dtype == r0.dtype for r in reads))
+    if not (1 <= len(reads) <= _lib.DECODE_MAX_LEVELS and r0.dtype in _lib.DTYPE_CODES and r0.ndim == 4):
+        return False
+    vec = 16 // r0.element_size()
+    return (r0.shape[1] > 0 and r0.shape[2] <= _lib.MIX_MAX_HEADS and r0.shape[3] % vec == 0
+            and r0.shape[2] * r0.shape[3] <= 512 * vec
+            and all(r.shape == r0.shape and r.dtype == r0.dtype and r.is_contiguous() and r.data_ptr() % 16 == 0
+                    for r in reads))
 
 
 def output_mix_train(reads, weights: Tensor) -> Tensor:

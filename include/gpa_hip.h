@@ -623,7 +623,8 @@ int gpa_output_mix_forward(const gpa_mix_problem *problem, hipStream_t stream);
 /* Backward of the output mix (its autograd, attention.py:340-341):
  * dread_j = round(w[j][h] dout) and dweights [ceil(B*T/32)][levels][heads],
  * per-32-token partial sums of sum dout read_j (the caller sums the tiles).
- * heads <= GPA_MIX_MAX_HEADS, heads*value_dim <= 4096. */
+ * heads <= GPA_MIX_MAX_HEADS; value_dim a multiple of 16 bytes, every row
+ * 16-byte aligned; heads*value_dim at most 512 such vectors. */
 #define GPA_MIX_MAX_HEADS 256
 typedef struct gpa_mix_grads {
     gpa_operand dout;                             /* [B,T,H,Dv] in dtype */

@@ -126,7 +126,7 @@ def test_sum_many_matches_float32_sum(n, dtype):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("levels,b,t,h,dv", [(4, 1, 70, 2, 24), (3, 2, 33, 16, 128), (1, 1, 5, 3, 7)])
+@pytest.mark.parametrize("levels,b,t,h,dv", [(4, 1, 70, 2, 24), (3, 2, 33, 16, 128), (1, 1, 5, 3, 8)])
 def test_output_mix_train_matches_device_ops(levels, b, t, h, dv, dtype):
     """The trainable output mix (attention.py:340-341) against the same sum as
     device tensor operations: output bit for bit; the reads' gradients bit for
@@ -135,6 +135,8 @@ def test_output_mix_train_matches_device_ops(levels, b, t, h, dv, dtype):
     from gpa_amd import glue
     g = torch.Generator().manual_seed(levels * 100 + t)
     reads = [torch.randn(b, t, h, dv, generator=g).to(dtype).cuda().requires_grad_() for _ in range(levels)]
+    assert glue.output_mix_supported(reads)
+    assert not glue.output_mix_supported([torch.zeros(b, t, h, 7, dtype=dtype, device="cuda")])
     logits = torch.randn(levels, h, generator=g).cuda().requires_grad_()
     dout = torch.randn(b, t, h, dv, generator=g).to(dtype).cuda()
     out = glue.output_mix_train(reads, logits.softmax(0))
