@@ -196,6 +196,43 @@ __global__ __launch_bounds__(256) void output_mix_bwd(gpa_mix_problem p, gpa_mix
   for (int i = tid; i < L * H; i += 256) g.dweights[(int64_t)blockIdx.x * L * H + i] = dw[i];
 }
 
+// output_mix over 16-byte vectors (V a whole number of vectors, aligned rows):
+// thread e handles vector e of the [B*T][H*V] output.
+template <typename E>
+__global__ __launch_bounds__(256) void output_mix_vec(gpa_mix_problem p) {
+#pragma clang fp contract(off)
+  constexpr int N = MixVec<E>::N;
+  const int H = p.heads, V = p.value_dim, NV = H * V / N;
+  const int64_t n = (int64_t)p.batch * p.tokens * NV;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t r = e / NV;
+  const int c = (int)(e % NV) * N, h = c / V, d = c % V;
+  const int b = (int)(r / p.tokens), t = (int)(r % p.tokens);
+  uint4 w[GPA_DECODE_MAX_LEVELS];
+#pragma unroll
+  for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j)
+    w[j] = j < p.levels ? *reinterpret_cast<const uint4*>(reinterpret_cast<const E*>(p.read[j].ptr) +
+                                                         mix_at(p.read[j], b, t, h, d))
+                        : make_uint4(0, 0, 0, 0);
+  float acc[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < GPA_DECODE_MAX_LEVELS; ++j) {
+    if (j >= p.levels) break;
+    float x[N];
+    unpack16<E>(w[j], x);
+    const float wj = p.weights[j * H + h];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {  // a product and a sum per level, rounded separately
+      const float prod = wj * x[i];
+      acc[i] = acc[i] + prod;
+    }
+  }
+  *reinterpret_cast<uint4*>(reinterpret_cast<E*>(p.out.ptr) + mix_at(p.out, b, t, h, d)) = pack16<E>(acc);
+}
+
 }  // namespace
 }  // namespace gpa
 
@@ -279,11 +316,26 @@ extern "C" int gpa_output_mix_forward(const gpa_mix_problem* p, hipStream_t stre
     return fail(GPA_HIP_EINVAL, "output mix: empty shape");
   if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "output mix: dtype");
   const int64_t n = (int64_t)p->batch * p->tokens * p->heads * p->value_dim;
-  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
-  if (p->dtype == GPA_DTYPE_BF16)
-    hipLaunchKernelGGL(output_mix<bf16_t>, grid, block, 0, stream, *p);
-  else
-    hipLaunchKernelGGL(output_mix<float>, grid, block, 0, stream, *p);
+  const int vec = p->dtype == GPA_DTYPE_BF16 ? 8 : 4;  // elements per 16-byte vector
+  auto aligned = [&](const gpa_operand& o) {
+    return (uintptr_t)o.ptr % 16 == 0 && o.sb % vec == 0 && o.st % vec == 0 && o.sh % vec == 0;
+  };
+  bool vectors = p->value_dim % vec == 0 && aligned(p->out);
+  for (int j = 0; j < p->levels; ++j) vectors = vectors && aligned(p->read[j]);
+  const dim3 block(256);
+  if (vectors) {
+    const dim3 grid((unsigned)((n / vec + 255) / 256));
+    if (p->dtype == GPA_DTYPE_BF16)
+      hipLaunchKernelGGL(output_mix_vec<bf16_t>, grid, block, 0, stream, *p);
+    else
+      hipLaunchKernelGGL(output_mix_vec<float>, grid, block, 0, stream, *p);
+  } else {
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (p->dtype == GPA_DTYPE_BF16)
+      hipLaunchKernelGGL(output_mix<bf16_t>, grid, block, 0, stream, *p);
+    else
+      hipLaunchKernelGGL(output_mix<float>, grid, block, 0, stream, *p);
+  }
   return check_launch("gpa_output_mix_forward");
 }
 
