@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 29
+ABI_VERSION = 30
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -256,6 +256,8 @@ EXPORTS = {
     "gpa_token_logits_forward": ([ctypes.POINTER(TokenLogitsProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_forward": ([ctypes.POINTER(MixProblem), c_vp], ctypes.c_int),
     "gpa_output_mix_backward": ([ctypes.POINTER(MixProblem), ctypes.POINTER(MixGrads), c_vp], ctypes.c_int),
+    "gpa_row_softmax_forward": ([c_vp, c_vp, c_i64, c_i32, c_i32, c_vp], ctypes.c_int),
+    "gpa_row_softmax_backward": ([c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp], ctypes.c_int),
     "gpa_copy_many": ([ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(ctypes.c_int64), c_i32, c_vp],
                       ctypes.c_int),
     "gpa_moment_scan_many": ([ctypes.POINTER(MomentProblem), c_i32, c_vp], ctypes.c_int),

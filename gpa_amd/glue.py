@@ -160,6 +160,43 @@ def output_mix_train(reads, weights: Tensor) -> Tensor:
     return _OutputMix.apply(weights, *reads)
 
 
+class _RowSoftmax(torch.autograd.Function):
+    """softmax(x, -1).to(dtype) of float32 logits with its gradient
+    (gpa_row_softmax_forward / _backward: the backward recomputes the float32
+    softmax from the logits)."""
+
+    @staticmethod
+    def forward(ctx, x, dtype):
+        lib = _lib.load()
+        x = x.contiguous()
+        y = torch.empty(x.shape, device=x.device, dtype=dtype)
+        _lib.check(lib.gpa_row_softmax_forward(x.data_ptr(), y.data_ptr(), x.numel() // x.shape[-1], x.shape[-1],
+                                               _lib.DTYPE_CODES[dtype], _lib.stream_handle(x.device)),
+                   "gpa_row_softmax_forward")
+        ctx.save_for_backward(x)
+        ctx.dtype = dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        lib = _lib.load()
+        (x,) = ctx.saved_tensors
+        dy = dy.to(ctx.dtype).contiguous()
+        dx = torch.empty_like(x)
+        _lib.check(lib.gpa_row_softmax_backward(x.data_ptr(), dy.data_ptr(), dx.data_ptr(), x.numel() // x.shape[-1],
+                                                x.shape[-1], _lib.DTYPE_CODES[ctx.dtype],
+                                                _lib.stream_handle(x.device)), "gpa_row_softmax_backward")
+        return dx, None
+
+
+def softmax_rows(x: Tensor, dtype: torch.dtype) -> Tensor:
+    """softmax(x, -1).to(dtype) for float32 logits on the device, rows of up to
+    1024 values; the device ops otherwise."""
+    if x.dtype != torch.float32 or dtype not in _lib.DTYPE_CODES or not 1 <= x.shape[-1] <= 1024 or not x.is_cuda:
+        return x.softmax(-1).to(dtype)
+    return _RowSoftmax.apply(x, dtype)
+
+
 COPY_MAX = 4  # buffers per gpa_copy_many launch
 
 

@@ -51,11 +51,16 @@ def _pack(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
 
 
 def _pack_now(w: Tensor, dtype: torch.dtype, transpose: bool) -> Tensor:
-    w = w.detach().to(dtype)
+    w = w.detach()
     if transpose:
         w = w.transpose(1, 2)
     h, n, k = w.shape
-    out = torch.zeros(h, _pad(n, 32), _pad(k, 16), device=w.device, dtype=dtype)
+    pn, pk = _pad(n, 32), _pad(k, 16)
+    if (pn, pk) == (n, k):  # no padding: the rounding and the transpose are one copy
+        out = torch.empty(h, n, k, device=w.device, dtype=dtype)
+        out.copy_(w)
+        return out
+    out = torch.zeros(h, pn, pk, device=w.device, dtype=dtype)
     out[:, :n, :k] = w
     return out
 

@@ -322,7 +322,7 @@ def run_segment(model, q: Tensor, k: Tensor, v: Tensor, state: GPAState, positio
             lv.counts = lv.final_count[:, None]
 
     # ---- relations, attention.py:206-223
-    local = [lv.local if lv.local is not None else lv.logits.softmax(-1).to(dtype) for lv in levels]
+    local = [lv.local if lv.local is not None else glue.softmax_rows(lv.logits, dtype) for lv in levels]
     incoming, relations = _relations(model, local, [lv.write for lv in levels], state.relations, scan, token)
 
     # ---- route reader, attention.py:225-262

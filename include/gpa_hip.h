@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 29
+#define GPA_HIP_ABI_VERSION 30
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -632,6 +632,14 @@ typedef struct gpa_mix_grads {
     float *dweights;                              /* out, see above */
 } gpa_mix_grads;
 int gpa_output_mix_backward(const gpa_mix_problem *problem, const gpa_mix_grads *grads, hipStream_t stream);
+
+/* Softmax over rows of float32 logits rounded to dtype, y = round(softmax(x))
+ * (the local read distribution softmax(logits).to(dtype), attention.py:330),
+ * x and y contiguous [rows][m], 1 <= m <= 1024; and its backward dx = s (dy -
+ * sum s dy) with s = softmax(x) recomputed in float32, dy in dtype. */
+int gpa_row_softmax_forward(const float *x, void *y, int64_t rows, int32_t m, int32_t dtype, hipStream_t stream);
+int gpa_row_softmax_backward(const float *x, const void *dy, float *dx, int64_t rows, int32_t m, int32_t dtype,
+                             hipStream_t stream);
 /* Device-to-device copies of up to GPA_COPY_MAX buffers in one launch: dst[i]
  * <- src[i], bytes[i] each, every pointer and size a multiple of 16 bytes
  * (GPA_HIP_EINVAL otherwise).  No reference counterpart: it moves a decode

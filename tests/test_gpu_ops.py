@@ -156,3 +156,28 @@ def test_output_mix_train_matches_device_ops(levels, b, t, h, dv, dtype):
     for a, r in zip(got[1:-1], want[1:-1]):
         assert torch.equal(a, r)
     assert torch.allclose(got[-1], want[-1], rtol=1e-5, atol=1e-6)  # one level: the softmax's gradient is 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 33, 3, 7), (1, 64, 16, 128), (1, 20, 2, 256), (3, 5, 1, 1000)])
+def test_row_softmax_matches_device_ops(shape, dtype):
+    """softmax(logits).to(dtype) of the local read distribution (attention.py:330)
+    and its gradient against the same device ops: float32 to 1e-6 (the exp and
+    the summation order), bf16 within one rounding."""
+    from gpa_amd import glue
+    g = torch.Generator().manual_seed(shape[-1])
+    x = (torch.randn(*shape, generator=g) * 3).cuda().requires_grad_()
+    dy = torch.randn(*shape, generator=g).to(dtype).cuda()
+    y = glue.softmax_rows(x, dtype)
+    y.backward(dy)
+    gx = x.grad.clone()
+    x.grad = None
+    ref = x.softmax(-1).to(dtype)
+    ref.backward(dy)
+    assert y.dtype == dtype and y.shape == ref.shape
+    if dtype == torch.float32:
+        assert torch.allclose(y, ref, rtol=1e-6, atol=1e-7)
+    else:
+        assert ((y.float() - ref.float()).abs() <= 2 ** -8 * ref.float().abs() + 1e-7).all()
+    assert ((gx - x.grad).norm() / x.grad.norm()).item() < 1e-5
