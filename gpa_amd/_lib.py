@@ -12,7 +12,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgpa_hip.so")
-ABI_VERSION = 30
+ABI_VERSION = 31
 DECODE_MAX_LEVELS = 4
 DECODE_MAX_EDGES = 12
 DECODE_MAX_WIDTH = 256
@@ -161,6 +161,14 @@ class GateProblem(ctypes.Structure):
                [(n, c_vp) for n in ("g_in", "b_in", "g_out", "b_out")]
 
 
+GATE_MAX_HEADS = 256
+
+
+class GateGrads(ctypes.Structure):
+    _fields_ = [("dg_in", c_vp), ("db_in", c_vp), ("dg_out", c_vp), ("db_out", c_vp), ("draw", Operand),
+                ("dbias", c_vp)]
+
+
 class TokenSlot(ctypes.Structure):
     _fields_ = [("center", c_vp), ("gate_w", c_vp), ("gates", GateProblem), ("slot", Operand)]
 
@@ -249,6 +257,7 @@ EXPORTS = {
     "gpa_slot_gates_forward": ([ctypes.POINTER(SlotProblem), c_vp], ctypes.c_int),
     "gpa_slot_gates_backward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(SlotGrads), c_vp], ctypes.c_int),
     "gpa_gate_act_forward": ([ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
+    "gpa_gate_act_backward": ([ctypes.POINTER(GateProblem), ctypes.POINTER(GateGrads), c_vp], ctypes.c_int),
     "gpa_slot_gates_act_forward": ([ctypes.POINTER(SlotProblem), ctypes.POINTER(GateProblem), c_vp], ctypes.c_int),
     "gpa_token_logits_many": ([ctypes.POINTER(TokenLogitsProblem), ctypes.c_int32, c_vp], ctypes.c_int),
     "gpa_product_read_forward": ([ctypes.POINTER(ProductProblem), c_vp], ctypes.c_int),

@@ -23,6 +23,55 @@ __global__ void gate_act(gpa_gate_problem p) {
   gate_row(p, h, i, raw);
 }
 
+// Backward of the gate nonlinearities (the autograd of attention.py:166-174):
+// x = float(raw) + bias; d decay / dx = -decay_scale softplus'(x) where
+// softplus(x) <= 10 (the clamp passes its bound), softplus' = z / (z + 1),
+// z = e^x (1 above the threshold 20); d strength / dx = beta_max s (1 - s).
+// draw is the float32 gradient rounded to the activation type (the cast's
+// backward); dbias gets per-workgroup partial sums over its rows (LDS atomics
+// by head).
+template <typename E>
+__global__ __launch_bounds__(256) void gate_act_bwd(gpa_gate_problem p, gpa_gate_grads g) {
+  __shared__ float db[GPA_GATE_MAX_HEADS * 4];
+  const int H = p.heads;
+  for (int i = threadIdx.x; i < 4 * H; i += 256) db[i] = 0.f;
+  __syncthreads();
+  const int64_t n = (int64_t)p.batch * p.tokens * H;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const int h = (int)(i % H);
+    const int64_t bt = i / H;
+    const int t = (int)(bt % p.tokens), b = (int)(bt / p.tokens);
+    float x[4], d[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = act_at<E>(p.raw, b, t, h, c) + p.bias[4 * h + c];
+    const float gi = g.dg_in ? g.dg_in[i] : 0.f, bi = g.db_in ? g.db_in[i] : 0.f;
+    const float go = g.dg_out ? g.dg_out[i] : 0.f, bo = g.db_out ? g.db_out[i] : 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c += 2) {  // decays: channels 0 and 2
+      const float dg = c == 0 ? gi : go;
+      const float sp = softplus20(x[c]);
+      const float z = expf(x[c]);
+      const float dsp = x[c] > 20.f ? 1.f : z / (z + 1.f);
+      d[c] = sp <= 10.f ? -(dg * p.decay_scale) * dsp : 0.f;
+    }
+#pragma unroll
+    for (int c = 1; c < 4; c += 2) {  // strengths: channels 1 and 3
+      const float dbv = (c == 1 ? bi : bo) * p.beta_max;
+      const float sg = sigmoid1(x[c]);
+      d[c] = dbv * (1.f - sg) * sg;
+    }
+    E* dr = reinterpret_cast<E*>(g.draw.ptr) + (int64_t)b * g.draw.sb + (int64_t)t * g.draw.st + (int64_t)h * g.draw.sh;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dr[c] = from_f32<E>(d[c]);
+      atomicAdd(&db[4 * h + c], d[c]);
+    }
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < 4 * H; k += 256) g.dbias[(int64_t)blockIdx.x * 4 * H + k] = db[k];
+}
+
 // One token of one level: n = count0 + write; logits = scale raw + gain
 // log1p(n); local = round(softmax(logits)).  One 64-lane wave per (b, h) row.
 template <typename E>
@@ -506,4 +555,20 @@ extern "C" int gpa_row_softmax_backward(const float* x, const void* dy, float* d
     hipLaunchKernelGGL(row_softmax_bwd<float>, grid, dim3(256), 0, stream, x, static_cast<const float*>(dy), dx,
                        rows, m);
   return check_launch("gpa_row_softmax_backward");
+}
+
+extern "C" int gpa_gate_act_backward(const gpa_gate_problem* p, const gpa_gate_grads* g, hipStream_t stream) {
+  using namespace gpa;
+  if (!p || !g || !p->raw.ptr || !p->bias || !g->draw.ptr || !g->dbias) return fail(GPA_HIP_EINVAL, "gates backward: null pointer");
+  if (p->batch < 1 || p->tokens < 1 || p->heads < 1) return fail(GPA_HIP_EINVAL, "gates backward: empty shape");
+  if (p->heads > GPA_GATE_MAX_HEADS) return fail(GPA_HIP_EUNSUPPORTED, "gates backward: heads <= GPA_GATE_MAX_HEADS");
+  if (p->dtype != GPA_DTYPE_F32 && p->dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "gates: dtype");
+  const int64_t n = (int64_t)p->batch * p->tokens * p->heads;
+  if ((n + 255) / 256 > 0x7fffffff) return fail(GPA_HIP_EUNSUPPORTED, "gates backward: too many rows");
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  if (p->dtype == GPA_DTYPE_BF16)
+    hipLaunchKernelGGL(gate_act_bwd<bf16_t>, grid, block, 0, stream, *p, *g);
+  else
+    hipLaunchKernelGGL(gate_act_bwd<float>, grid, block, 0, stream, *p, *g);
+  return check_launch("gpa_gate_act_backward");
 }

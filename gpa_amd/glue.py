@@ -27,6 +27,48 @@ def gate_act(raw: Tensor, bias: Tensor, beta_max: float, decay_scale: float):
     return tuple(outs)
 
 
+class _GateAct(torch.autograd.Function):
+    """The gate nonlinearities with their gradient (gpa_gate_act_forward /
+    gpa_gate_act_backward): the gate inputs' gradient in their dtype and the
+    bias gradient from per-workgroup partial sums."""
+
+    @staticmethod
+    def forward(ctx, raw, bias, beta_max, decay_scale):
+        ctx.set_materialize_grads(False)
+        raw = raw if raw.stride(-1) == 1 else raw.contiguous()
+        outs = gate_act(raw, bias, beta_max, decay_scale)
+        ctx.save_for_backward(raw, bias)
+        ctx.consts = (float(beta_max), float(decay_scale))
+        return outs
+
+    @staticmethod
+    def backward(ctx, dg_in, db_in, dg_out, db_out):
+        lib = _lib.load()
+        raw, bias = ctx.saved_tensors
+        b, t, h, _ = raw.shape
+        beta_max, decay_scale = ctx.consts
+        grads = [None if d is None else d.float().contiguous() for d in (dg_in, db_in, dg_out, db_out)]
+        draw = torch.empty_like(raw)
+        part = torch.empty(-(-(b * t * h) // 256), h, 4, device=raw.device, dtype=torch.float32)
+        bf = bias.detach().float().contiguous()
+        p = _lib.GateProblem(b, t, h, _lib.DTYPE_CODES[raw.dtype], _lib.operand(raw), bf.data_ptr(),
+                             beta_max, decay_scale, None, None, None, None)
+        gg = _lib.GateGrads(*(d.data_ptr() if d is not None else None for d in grads), _lib.operand(draw),
+                            part.data_ptr())
+        _lib.check(lib.gpa_gate_act_backward(p, gg, _lib.stream_handle(raw.device)), "gpa_gate_act_backward")
+        return draw, part.sum(0).to(bias.dtype), None, None
+
+
+def gate_act_supported(raw: Tensor) -> bool:
+    return raw.is_cuda and raw.dtype in _lib.DTYPE_CODES and raw.ndim == 4 and raw.shape[-1] == 4 \
+        and raw.shape[2] <= _lib.GATE_MAX_HEADS and raw.numel() > 0
+
+
+def gate_act_train(raw: Tensor, bias: Tensor, beta_max: float, decay_scale: float):
+    """gate_act with autograd through the gate inputs and the bias [H,4]."""
+    return _GateAct.apply(raw, bias, beta_max, decay_scale)
+
+
 def token_logits(raw: Tensor, write: Tensor, count0: Tensor, gain: Tensor, scale: Tensor):
     """(logits [B,1,H,M] float32, counts [B,H,M] float32, local [B,1,H,M] in
     raw's dtype) of one token of one level."""

@@ -528,6 +528,8 @@ def _gates(model, key: Tensor, j: int, control: Tensor | None, raw: Tensor | Non
     tier = _tier(cfg, j)
     if _GLUE[0] and not torch.is_grad_enabled() and raw.dtype in _lib.DTYPE_CODES:
         return glue.gate_act(raw, model.gate_bias[j], cfg.beta_max, _decay_scale(model, j))
+    if _GLUE[0] and glue.gate_act_supported(raw):
+        return glue.gate_act_train(raw, model.gate_bias[j], cfg.beta_max, _decay_scale(model, j))
     raw = raw.float() + model.gate_bias[j]
     g_in, b_in, g_out, b_out = raw.unbind(-1)
     g_in = -F.softplus(g_in).clamp(max=10.)

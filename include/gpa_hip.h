@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_HIP_ABI_VERSION 30
+#define GPA_HIP_ABI_VERSION 31
 #define GPA_CHUNK_ROWS 64   /* rows per stored chunk; chunk <= 64 */
 #define GPA_MAX_KDIM 256    /* key width of a scan (the reduced dimension) */
 #define GPA_MAX_VDIM 1024   /* value width of a scan */
@@ -556,6 +556,18 @@ typedef struct gpa_gate_problem {
     float *g_in, *b_in, *g_out, *b_out;           /* out [B,T,H] */
 } gpa_gate_problem;
 int gpa_gate_act_forward(const gpa_gate_problem *problem, hipStream_t stream);
+
+/* Backward of gpa_gate_act_forward (the autograd of the gate nonlinearities):
+ * the four output gradients (float32 [B,T,H], NULL = zero) give draw (the
+ * gate inputs' gradient, [B,T,H,4] in dtype) and dbias, partial sums
+ * [ceil(B*T*H/256)][H][4] (the caller sums the rows).  heads <= GPA_GATE_MAX_HEADS. */
+#define GPA_GATE_MAX_HEADS 256
+typedef struct gpa_gate_grads {
+    const float *dg_in, *db_in, *dg_out, *db_out;
+    gpa_operand draw;
+    float *dbias;
+} gpa_gate_grads;
+int gpa_gate_act_backward(const gpa_gate_problem *problem, const gpa_gate_grads *grads, hipStream_t stream);
 
 /* gpa_slot_gates_forward followed by gpa_gate_act_forward on its gate inputs,
  * in one launch (inference): the slot products and gate inputs of one level

@@ -181,3 +181,36 @@ def test_row_softmax_matches_device_ops(shape, dtype):
     else:
         assert ((y.float() - ref.float()).abs() <= 2 ** -8 * ref.float().abs() + 1e-7).all()
     assert ((gx - x.grad).norm() / x.grad.norm()).item() < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("decay_scale", [1.0, 0.01, 0.0])
+def test_gate_act_train_matches_device_ops(dtype, decay_scale):
+    """The gate nonlinearities with their gradient (attention.py:166-174)
+    against the reference's device ops: decays -min(softplus(x), 10) * scale
+    (inputs spanning the clamp and the softplus threshold), strengths
+    beta_max sigmoid(x); gradients of the gate inputs and of the bias."""
+    import torch.nn.functional as F
+    from gpa_amd import glue
+    g = torch.Generator().manual_seed(7)
+    b, t, h = 2, 300, 5
+    raw = (torch.randn(b, t, h, 4, generator=g) * 8).to(dtype).cuda().requires_grad_()
+    bias = torch.randn(h, 4, generator=g).cuda().requires_grad_()
+    ws = [torch.randn(b, t, h, generator=g).cuda() for _ in range(4)]
+    outs = glue.gate_act_train(raw, bias, .9, decay_scale)
+    sum((o * w).sum() for o, w in zip(outs, ws)).backward()
+    got = [o.detach() for o in outs] + [raw.grad.clone(), bias.grad.clone()]
+    raw.grad = bias.grad = None
+    x = raw.float() + bias
+    gi, bi, go, bo = x.unbind(-1)
+    ref = (-F.softplus(gi).clamp(max=10.) * decay_scale, .9 * bi.sigmoid(),
+           -F.softplus(go).clamp(max=10.) * decay_scale, .9 * bo.sigmoid())
+    sum((o * w).sum() for o, w in zip(ref, ws)).backward()
+    want = [o.detach() for o in ref] + [raw.grad, bias.grad]
+    for i, (a, r) in enumerate(zip(got, want)):
+        scale = r.abs().max().item()
+        if i == 4 and dtype == torch.bfloat16:  # one rounding of the input gradient
+            assert ((a.float() - r.float()).abs() <= 2 ** -8 * r.float().abs() + 1e-6 * max(scale, 1e-30)).all(), i
+        else:
+            assert (a.float() - r.float()).abs().max().item() <= 1e-5 * max(scale, 1e-30) + 1e-7, i
