@@ -286,64 +286,74 @@ __global__ __launch_bounds__(256) void output_mix_vec(gpa_mix_problem p) {
 // attention.py:330: softmax(logits).to(dtype)), one wave per row of m <= 1024
 // values (16 per lane), and its backward dx = s (dy - sum s dy) with s the
 // float32 softmax recomputed from the logits.
-constexpr int SMX_PER = 16;
-
-__device__ __forceinline__ void smx_row(const float* x, int m, int lane, float (&s)[SMX_PER]) {
-  float v[SMX_PER], mx = -INFINITY;
+template <int PER>
+__device__ __forceinline__ void smx_row(const float* x, int m, int lane, float (&s)[PER]) {
+  float v[PER], mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int c = lane + 64 * i;
     v[i] = x[c < m ? c : 0];
   }
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) {
+  for (int i = 0; i < PER; ++i) {
     if (lane + 64 * i >= m) v[i] = -INFINITY;
     mx = fmaxf(mx, v[i]);
   }
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) {
+  for (int i = 0; i < PER; ++i) {
     s[i] = lane + 64 * i < m ? expf(v[i] - mx) : 0.f;
     sum += s[i];
   }
   sum = sum64(sum);
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) s[i] = s[i] / sum;
+  for (int i = 0; i < PER; ++i) s[i] = s[i] / sum;
 }
 
-template <typename E>
+// PER values per lane: m <= 64 PER.
+template <typename E, int PER>
 __global__ __launch_bounds__(256) void row_softmax_fwd(const float* x, E* y, int64_t rows, int m) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
-  float s[SMX_PER];
-  smx_row(x + row * m, m, lane, s);
+  float s[PER];
+  smx_row<PER>(x + row * m, m, lane, s);
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i)
+  for (int i = 0; i < PER; ++i)
     if (lane + 64 * i < m) y[row * m + lane + 64 * i] = from_f32<E>(s[i]);
 }
 
-template <typename E>
+template <typename E, int PER>
 __global__ __launch_bounds__(256) void row_softmax_bwd(const float* x, const E* dy, float* dx, int64_t rows, int m) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
-  float g[SMX_PER], s[SMX_PER];
+  float g[PER], s[PER];
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int c = lane + 64 * i;
     g[i] = to_f32(dy[row * m + (c < m ? c : 0)]);
   }
-  smx_row(x + row * m, m, lane, s);
+  smx_row<PER>(x + row * m, m, lane, s);
   float dot = 0.f;
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i) dot += lane + 64 * i < m ? s[i] * g[i] : 0.f;
+  for (int i = 0; i < PER; ++i) dot += lane + 64 * i < m ? s[i] * g[i] : 0.f;
   dot = sum64(dot);
 #pragma unroll
-  for (int i = 0; i < SMX_PER; ++i)
+  for (int i = 0; i < PER; ++i)
     if (lane + 64 * i < m) dx[row * m + lane + 64 * i] = s[i] * (g[i] - dot);
 }
+
+// Launches KERNEL<E, PER> with the smallest PER in {1, 2, 4, 8, 16} that covers m.
+#define GPA_SMX_LAUNCH(KERNEL, E, m, grid, ...)                                                \
+  do {                                                                                        \
+    if ((m) <= 64) hipLaunchKernelGGL((KERNEL<E, 1>), grid, dim3(256), 0, __VA_ARGS__);       \
+    else if ((m) <= 128) hipLaunchKernelGGL((KERNEL<E, 2>), grid, dim3(256), 0, __VA_ARGS__); \
+    else if ((m) <= 256) hipLaunchKernelGGL((KERNEL<E, 4>), grid, dim3(256), 0, __VA_ARGS__); \
+    else if ((m) <= 512) hipLaunchKernelGGL((KERNEL<E, 8>), grid, dim3(256), 0, __VA_ARGS__); \
+    else hipLaunchKernelGGL((KERNEL<E, 16>), grid, dim3(256), 0, __VA_ARGS__);                \
+  } while (0)
 
 }  // namespace
 }  // namespace gpa
@@ -527,33 +537,31 @@ extern "C" int gpa_output_mix_backward(const gpa_mix_problem* p, const gpa_mix_g
 extern "C" int gpa_row_softmax_forward(const float* x, void* y, int64_t rows, int32_t m, int32_t dtype,
                                        hipStream_t stream) {
   using namespace gpa;
-  if (!x || !y || rows < 0 || m < 1 || m > 64 * SMX_PER) return fail(GPA_HIP_EINVAL, "row softmax: 1 <= m <= 1024");
+  if (!x || !y || rows < 0 || m < 1 || m > 1024) return fail(GPA_HIP_EINVAL, "row softmax: 1 <= m <= 1024");
   if (dtype != GPA_DTYPE_F32 && dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "row softmax: dtype");
   if (!rows) return GPA_HIP_OK;
   if ((rows + 3) / 4 > 0x7fffffff) return fail(GPA_HIP_EINVAL, "row softmax: too many rows");
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (dtype == GPA_DTYPE_BF16)
-    hipLaunchKernelGGL(row_softmax_fwd<bf16_t>, grid, dim3(256), 0, stream, x, static_cast<bf16_t*>(y), rows, m);
+    GPA_SMX_LAUNCH(row_softmax_fwd, bf16_t, m, grid, stream, x, static_cast<bf16_t*>(y), rows, m);
   else
-    hipLaunchKernelGGL(row_softmax_fwd<float>, grid, dim3(256), 0, stream, x, static_cast<float*>(y), rows, m);
+    GPA_SMX_LAUNCH(row_softmax_fwd, float, m, grid, stream, x, static_cast<float*>(y), rows, m);
   return check_launch("gpa_row_softmax_forward");
 }
 
 extern "C" int gpa_row_softmax_backward(const float* x, const void* dy, float* dx, int64_t rows, int32_t m,
                                         int32_t dtype, hipStream_t stream) {
   using namespace gpa;
-  if (!x || !dy || !dx || rows < 0 || m < 1 || m > 64 * SMX_PER)
+  if (!x || !dy || !dx || rows < 0 || m < 1 || m > 1024)
     return fail(GPA_HIP_EINVAL, "row softmax backward: 1 <= m <= 1024");
   if (dtype != GPA_DTYPE_F32 && dtype != GPA_DTYPE_BF16) return fail(GPA_HIP_EUNSUPPORTED, "row softmax: dtype");
   if (!rows) return GPA_HIP_OK;
   if ((rows + 3) / 4 > 0x7fffffff) return fail(GPA_HIP_EINVAL, "row softmax: too many rows");
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (dtype == GPA_DTYPE_BF16)
-    hipLaunchKernelGGL(row_softmax_bwd<bf16_t>, grid, dim3(256), 0, stream, x, static_cast<const bf16_t*>(dy), dx,
-                       rows, m);
+    GPA_SMX_LAUNCH(row_softmax_bwd, bf16_t, m, grid, stream, x, static_cast<const bf16_t*>(dy), dx, rows, m);
   else
-    hipLaunchKernelGGL(row_softmax_bwd<float>, grid, dim3(256), 0, stream, x, static_cast<const float*>(dy), dx,
-                       rows, m);
+    GPA_SMX_LAUNCH(row_softmax_bwd, float, m, grid, stream, x, static_cast<const float*>(dy), dx, rows, m);
   return check_launch("gpa_row_softmax_backward");
 }
 
