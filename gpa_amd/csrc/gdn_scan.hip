@@ -896,6 +896,27 @@ bool strip_path(const gpa_gdn_problem& p) {
   return use_mfma<E>(p) && p.kdim <= 128;
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The wide strip form when the split form would need more workgroups than the
+// device has CUs (each workgroup holds a CU for the whole chain), every group
+// can take it and the pack is `fast` with 128 keys.
+bool strip_go_wide(int km, bool fast, bool all_ok, int split_workgroups) {
+  const int cus = device_cus();
+  return km == 128 && fast && all_ok && cus > 0 && split_workgroups > cus;
+}
+
 // The state recurrence of one problem outside a pack.
 template <typename E, int KM>
 int fwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStream_t st) {
@@ -903,9 +924,10 @@ int fwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStr
   if (strip_path<E>(p)) {
     StripFwdPack pk{};
     pk.n = 1;
-    pk.p[0] = strip_fwd_one(p, sv, nch, 0);
     const bool fast = p.kdim == KM && p.vdim % 64 == 0;
-    return launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, st);
+    const bool wide = strip_go_wide(KM, fast, strip_wide_ok(p), strip_workgroups(p, false));
+    pk.p[0] = strip_fwd_one(p, sv, nch, 0, wide);
+    return launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, wide), fast, wide, st);
   }
   if (use_mfma<E>(p)) return launch_state_fwd_mfma<KM>(p, sv, nch, st);
   const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -951,9 +973,10 @@ int bwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_g
     const bool has_q = has_read(p, gr);
     StripBwdPack pk{};
     pk.n = 1;
-    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q);
-    const bool fast = p.kdim == KM && p.vdim % 64 == 0;
-    return launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p), fast, has_q, gr.dstates != nullptr,
+    const bool fast = p.kdim == KM && p.vdim % 64 == 0, has_inj = gr.dstates != nullptr;
+    const bool wide = strip_go_wide(KM, fast, strip_wide_ok(p) && !has_inj, strip_workgroups(p, false));
+    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q, wide);
+    return launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, wide), fast, has_q, has_inj, wide,
                                                         st);
   }
   if (use_mfma<E>(p)) return launch_state_bwd_mfma<KM>(p, sv, gr, nch, st);
@@ -1100,7 +1123,9 @@ struct SideScope {
 // Which groups of the call run on the side stream: the 256-key groups when
 // the call also has others; else, for a call of strip groups only (a level's
 // A/B pair), the second half of the groups, each half in its own strip pack,
-// so that one half's prep or out phase overlaps the other half's state chain.
+// so that one half's prep or out phase overlaps the other half's state chain
+// (only while all their strip workgroups fit on the device's CUs at once;
+// beyond that the groups stay in one pack, which takes the wide form).
 // Returns whether any group goes there (never for timed or captured calls).
 bool side_groups(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStream_t st, bool (&side)[GPA_GDN_MAX_PACK]) {
   bool mf = false, other = false, strips = true;
@@ -1115,6 +1140,10 @@ bool side_groups(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStre
     return true;
   }
   if (strips && n >= 2) {
+    int wg = 0;
+    for (int i = 0; i < n; ++i) wg += strip_workgroups(ps[i], false);
+    const int cus = device_cus();
+    if (cus <= 0 || wg > cus) return false;
     for (int i = n / 2; i < n; ++i) side[i] = true;
     return true;
   }
@@ -1160,19 +1189,27 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
-    StripFwdPack pk{};
-    int total = 0;
-    bool fast = true;
+    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0;
+    bool fast = true, all_ok = true;
     for (int j = i; j < n; ++j) {
       if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || on_side[j] != on_side[i]) continue;
-      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
-      pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total);
-      total += strip_workgroups(ps[j]);
+      members[nm++] = j;
+      split += strip_workgroups(ps[j], false);
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
+      all_ok = all_ok && strip_wide_ok(ps[j]);
       done[j] = true;
     }
-    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, stream_of(i))
-                            : launch_state_fwd_strip<128>(pk, total, fast, stream_of(i));
+    const bool wide = strip_go_wide(km, fast, all_ok, split);
+    StripFwdPack pk{};
+    int total = 0;
+    for (int m = 0; m < nm; ++m) {
+      const int j = members[m];
+      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+      pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total, wide);
+      total += strip_workgroups(ps[j], wide);
+    }
+    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, wide, stream_of(i))
+                            : launch_state_fwd_strip<128>(pk, total, fast, wide, stream_of(i));
     if (rc) return rc;
   }
   // the out phase of each group follows its state pack on the same stream
@@ -1234,21 +1271,29 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
-    StripBwdPack pk{};
-    int total = 0;
-    bool fast = true;
+    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0;
+    bool fast = true, all_ok = !hi;
     for (int j = i; j < n; ++j) {
       if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || has_read(ps[j], gr[j]) != hq ||
           (gr[j].dstates != nullptr) != hi || on_side[j] != on_side[i])
         continue;
-      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
-      pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq);
-      total += strip_workgroups(ps[j]);
+      members[nm++] = j;
+      split += strip_workgroups(ps[j], false);
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
+      all_ok = all_ok && strip_wide_ok(ps[j]);
       done[j] = true;
     }
-    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, stream_of(i))
-                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, stream_of(i));
+    const bool wide = strip_go_wide(km, fast, all_ok, split);
+    StripBwdPack pk{};
+    int total = 0;
+    for (int m = 0; m < nm; ++m) {
+      const int j = members[m];
+      const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
+      pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq, wide);
+      total += strip_workgroups(ps[j], wide);
+    }
+    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, wide, stream_of(i))
+                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, wide, stream_of(i));
     if (rc) return rc;
   }
   // the chunk phase of each group follows its state pack on the same stream

@@ -361,9 +361,11 @@ struct BwdLds {  // bytes
 };
 
 // ---------------------------------------------------------------------------------------- forward
-template <int KM, bool FAST>
+template <int KM, bool FAST, bool WIDE>
 __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
+  static_assert(!WIDE || (FAST && KM == 128), "the wide split is built for whole 128-key problems");
   constexpr int KT = KM / 32, K16M = KM / 16, NTW = KM / 64;
+  constexpr int OT = WIDE ? KT : NTW;  // row tiles of S a wave owns
   using L = FwdLds<KM>;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const StripFwdOne q = pack_entry<StripFwdPack, StripFwdOne>();
@@ -371,12 +373,14 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
   const int s = local / q.wg_per_stream, cb = local % q.wg_per_stream;
   const int b = s / q.heads, h = s % q.heads;
   // Wave-uniform values are scalar: branches on them are scalar.
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = w & 1;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = WIDE ? 0 : w & 1;
   const int K = FAST ? KM : q.K, V = q.V, nch = q.nch;
   const int K16 = K / 16, RB = (K + 31) / 32;
   const int wrow_n = 2 * K16 * 64 * 16, kcol_n = RB * 4 * 64 * 8;  // this problem's bf16 elements per chunk
-  const int col0 = 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
-  const bool active = FAST || col0 < V;  // FAST: V % 64 == 0
+  // Split: strip w/2 of the workgroup's 64 columns, key half w%2.  Wide: strip
+  // w of its 128 columns, every key row.
+  const int col0 = WIDE ? 128 * cb + 32 * w : 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
+  const bool active = FAST || col0 < V;  // FAST: V % 64 == 0 (wide: V % 128 == 0)
   const uint32_t lds0 = lds_offset(smem_raw);
   auto wbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + i * L::BUF); };
   auto kbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + i * L::BUF + L::WROW); };
@@ -392,11 +396,26 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
     dma_run(ksrc + (int64_t)n * (kcol_n / 8), lds0 + i * L::BUF + L::WROW, kcol_n / 8, w, l);
     return gate_load(gsrc + (int64_t)n * R, tid);
   };
-
-  f32x16 S[NTW];
+  // The wave's rows of a strip go to a value-major block NTW row tiles at a
+  // time (the capacity of its LDS slot).
+  auto store_own = [&](float* dst, const f32x16 (&x)[OT]) {
 #pragma unroll
-  for (int i = 0; i < NTW; ++i)
-    load_key_major(S[i], q.s0, (int64_t)b * q.s0_sb + (int64_t)h * q.s0_sh, v, V, K, 32 * (hk * NTW + i), l);
+    for (int h2 = 0; h2 < OT / NTW; ++h2) {
+      f32x16 part[NTW];
+#pragma unroll
+      for (int i = 0; i < NTW; ++i) part[i] = x[h2 * NTW + i];
+      store_cols<NTW, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * NTW), part, l);
+    }
+  };
+  constexpr int DT = WIDE ? 2 : 1;  // row tiles of D a wave saves
+  auto store_d = [&](float* dst, const f32x16 (&x)[DT]) {
+    store_cols<DT, !FAST>(slot, dst, R, R, V, col0, WIDE ? 0 : 32 * hk, x, l);
+  };
+
+  f32x16 S[OT];
+#pragma unroll
+  for (int i = 0; i < OT; ++i)
+    load_key_major(S[i], q.s0, (int64_t)b * q.s0_sb + (int64_t)h * q.s0_sh, v, V, K, 32 * (hk * OT + i), l);
   float g_next = fetch(0, 0);
   float ur[2][16], un[2][16];  // U of this chunk and of the next (fragment order, ufrag_idx)
   const int strip = col0 >> 5, nstrip = ufrag_v(V) >> 5;
@@ -404,7 +423,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
   load_ufrag<!FAST>(ur[1], q.u + ufrag_off(s, 0, nch, V), strip, nstrip, 1, l);
   dma_drain();  // every load of the preamble: the loop then starts with none pending
   gate_store(gl0, g_next, tid);
-  f32x16 dprev{};  // this wave's row tile of the previous chunk's D, stored one chunk late
+  f32x16 dprev[DT] = {};  // this wave's row tiles of the previous chunk's D, stored one chunk late
 
   for (int n = 0; n < nch; ++n) {
     const int cur = n & 1;
@@ -420,32 +439,29 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
     if (active) {
       load_ufrag<!FAST>(un[0], q.u + ufrag_off(s, nn, nch, V), strip, nstrip, 0, l);
       load_ufrag<!FAST>(un[1], q.u + ufrag_off(s, nn, nch, V), strip, nstrip, 1, l);
-      if (n > 0) {
-        const f32x16 dp[1] = {dprev};
-        store_cols<1, !FAST>(slot, q.delta + ((int64_t)s * nch + n - 1) * V * R, R, R, V, col0, 32 * hk, dp, l);
-      }
+      if (n > 0) store_d(q.delta + ((int64_t)s * nch + n - 1) * V * R, dprev);
       // (a) S_n -> the saved chunk-start states (own rows).
-      store_cols<NTW, !FAST>(slot, q.states + ((int64_t)s * nch + n) * K * V, K, K, V, col0, 32 * NTW * hk, S, l);
+      store_own(q.states + ((int64_t)s * nch + n) * K * V, S);
       // (b) W S over the own rows, for both row tiles of W; every W fragment is
       // read from LDS before the first product.
       const __bf16* wf = wbuf(cur);
-      bf16x8 wa[NTW][2][2][2];  // [own tile][hs][rt][hi, lo]
+      bf16x8 wa[OT][2][2][2];  // [own tile][hs][rt][hi, lo]
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
-            const int ks = 2 * (hk * NTW + i) + hs;
+            const int ks = 2 * (hk * OT + i) + hs;
             const __bf16* p = wf + (rt * K16 + (FAST || ks < K16 ? ks : 0)) * 1024 + l * 8;
             wa[i][hs][rt][0] = *reinterpret_cast<const bf16x8*>(p);
             wa[i][hs][rt][1] = *reinterpret_cast<const bf16x8*>(p + 512);
           }
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
-          const int ks = 2 * (hk * NTW + i) + hs;
+          const int ks = 2 * (hk * OT + i) + hs;
           if (FAST || ks < K16) {
             const BSplit sb = acc_b(S[i], hs);
 #pragma unroll
@@ -456,22 +472,28 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
             }
           }
         }
-      xch_put(slot, d, l);
+      if constexpr (!WIDE) xch_put(slot, d, l);
     }
-    lds_barrier();
+    // The split waves meet here to exchange their halves of W S; a wide wave
+    // holds the whole sum.
+    if constexpr (!WIDE) lds_barrier();
     if (active) {
-      // (c) D = U - (half 0 + half 1), summed in that order in both waves (half
-      // hk keeps row tile hk to save), then scaled by e^{G_C - G}.
+      // (c) D = U - W S (split: half 0 + half 1, summed in that order in both
+      // waves; half hk keeps row tile hk to save), then scaled by e^{G_C - G}.
       f32x16 pd[2];
-      xch_get(pd, pslot, l);
+      if constexpr (!WIDE) xch_get(pd, pslot, l);
       const float* gf = gl0 + cur * GATE_FLOATS;
       const float decay = gf[R];
       f32x16 D[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) D[rt][r] = ur[rt][r] - (hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r]);
-        if (rt == hk) dprev = D[rt];
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (WIDE) D[rt][r] = ur[rt][r] - d[rt][r];
+          else D[rt][r] = ur[rt][r] - (hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r]);
+        }
+        if constexpr (WIDE) dprev[rt] = D[rt];
+        else if (rt == hk) dprev[0] = D[rt];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const float4 f = *reinterpret_cast<const float4*>(gf + 32 * rt + 8 * g + 4 * (l >> 5));
@@ -484,22 +506,22 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
         for (int r = 0; r < 16; ++r) ur[rt][r] = un[rt][r];
       // (d) S = e^{G_C} S + Kn^T (e^{G_C-G} D) for the own rows.
       const __bf16* kf = kbuf(cur);
-      bf16x8 ka[NTW][4];
+      bf16x8 ka[OT][4];
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int ps = 0; ps < 4; ++ps) {
-          const int t = hk * NTW + i;
+          const int t = hk * OT + i;
           ka[i][ps] = *reinterpret_cast<const bf16x8*>(kf + (((FAST || t < RB ? t : 0) * 4 + ps) * 64 + l) * 8);
         }
 #pragma unroll
-      for (int i = 0; i < NTW; ++i) S[i] *= decay;
+      for (int i = 0; i < OT; ++i) S[i] *= decay;
 #pragma unroll
       for (int ps = 0; ps < 4; ++ps) {
         const BSplit db = acc_b(D[ps >> 1], ps & 1);
 #pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-          const int t = hk * NTW + i;
+        for (int i = 0; i < OT; ++i) {
+          const int t = hk * OT + i;
           if (FAST || t < RB) {
             S[i] = mfma(ka[i][ps], db.hi, S[i]);
             S[i] = mfma(ka[i][ps], db.lo, S[i]);
@@ -511,31 +533,34 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
     dma_drain();
   }
   if (active) {
-    const f32x16 dp[1] = {dprev};
-    store_cols<1, !FAST>(slot, q.delta + ((int64_t)s * nch + nch - 1) * V * R, R, R, V, col0, 32 * hk, dp, l);
+    store_d(q.delta + ((int64_t)s * nch + nch - 1) * V * R, dprev);
 #pragma unroll
-    for (int i = 0; i < NTW; ++i) {
-      const int t = hk * NTW + i;
+    for (int i = 0; i < OT; ++i) {
+      const int t = hk * OT + i;
       if (FAST || t < RB) store_key_major(q.final_state, (int64_t)s * K * V, v, V, K, 32 * t, S[i], l);
     }
   }
 }
 
 // --------------------------------------------------------------------------------------- backward
-template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, bool WIDE>
 __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
+  static_assert(!WIDE || (FAST && KM == 128 && !HAS_INJ), "the wide split is built for whole 128-key problems");
   constexpr int KT = KM / 32, K16M = KM / 16, NTW = KM / 64;
+  constexpr int OT = WIDE ? KT : NTW, DT = WIDE ? 2 : 1;  // row tiles of dS a wave owns, of dD it saves
   using L = BwdLds<KM, HAS_Q>;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const StripBwdOne q = pack_entry<StripBwdPack, StripBwdOne>();
   const int local = blockIdx.x - q.wg0;
   const int s = local / q.wg_per_stream, cb = local % q.wg_per_stream;
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = w & 1;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = WIDE ? 0 : w & 1;
   const int K = FAST ? KM : q.K, V = q.V, nch = q.nch;
   const int K16 = K / 16, RB = (K + 31) / 32;
   const int krow_n = 2 * K16 * 64 * 8, wcol_n = RB * 4 * 64 * 16, qcol_n = HAS_Q ? RB * 4 * 64 * 8 : 0;
-  const int col0 = 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
-  const bool active = FAST || col0 < V;  // FAST: V % 64 == 0
+  // Split: strip w/2 of the workgroup's 64 columns, key half w%2.  Wide: strip
+  // w of its 128 columns, every key row.
+  const int col0 = WIDE ? 128 * cb + 32 * w : 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
+  const bool active = FAST || col0 < V;  // FAST: V % 64 == 0 (wide: V % 128 == 0)
   const uint32_t lds0 = lds_offset(smem_raw);
   const __bf16* kf = reinterpret_cast<const __bf16*>(smem_raw);  // Kn rows (one buffer)
   auto lbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + L::LATE_OFF + i * L::LATE); };
@@ -555,10 +580,24 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
   };
   auto fetch_early = [&](int n) { dma_run(ksrc + (int64_t)n * (krow_n / 8), lds0, krow_n / 8, w, l); };
 
-  f32x16 dS[NTW];
+  // The wave's rows of a strip go to a value-major block NTW row tiles at a
+  // time (the capacity of its LDS slot).
+  auto store_own = [&](float* dst, const f32x16 (&x)[OT]) {
 #pragma unroll
-  for (int i = 0; i < NTW; ++i)
-    load_key_major(dS[i], q.dfinal, (int64_t)s * K * V, v, V, K, 32 * (hk * NTW + i), l);
+    for (int h2 = 0; h2 < OT / NTW; ++h2) {
+      f32x16 part[NTW];
+#pragma unroll
+      for (int i = 0; i < NTW; ++i) part[i] = x[h2 * NTW + i];
+      store_cols<NTW, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * NTW), part, l);
+    }
+  };
+  auto store_dd = [&](float* dst, const f32x16 (&x)[DT]) {
+    store_cols<DT, !FAST>(slot, dst, R, R, V, col0, WIDE ? 0 : 32 * hk, x, l);
+  };
+  f32x16 dS[OT];
+#pragma unroll
+  for (int i = 0; i < OT; ++i)
+    load_key_major(dS[i], q.dfinal, (int64_t)s * K * V, v, V, K, 32 * (hk * OT + i), l);
   float g_next = fetch_late(nch - 1, 0);
   fetch_early(nch - 1);
   // Per-column data of this chunk and of the next: dd0 and o (fragment order,
@@ -581,7 +620,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
   if (active) load_cols(nch - 1, d0r, orr, inj);
   dma_drain();  // every load of the preamble: the loop then starts with none pending
   gate_store(gl0, g_next, tid);
-  f32x16 ddprev{};  // this wave's row tile of the previous (later) chunk's dD, stored one chunk late
+  f32x16 ddprev[DT] = {};  // this wave's row tiles of the previous (later) chunk's dD, stored one chunk late
 
   for (int n = nch - 1, it = 0; n >= 0; --n, ++it) {
     const int cur = it & 1;
@@ -594,26 +633,23 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
     const __bf16* lf = lbuf(cur);
     if (active) {
       load_cols(nn, d0n, onx, injn);
-      if (n + 1 < nch) {
-        const f32x16 dp[1] = {ddprev};
-        store_cols<1, !FAST>(slot, q.ddelta + ((int64_t)s * nch + n + 1) * V * R, R, R, V, col0, 32 * hk, dp, l);
-      }
+      if (n + 1 < nch) store_dd(q.ddelta + ((int64_t)s * nch + n + 1) * V * R, ddprev);
       // (a) dS at the end of chunk n -> dhend (own rows).
-      store_cols<NTW, !FAST>(slot, q.dhend + ((int64_t)s * nch + n) * K * V, K, K, V, col0, 32 * NTW * hk, dS, l);
+      store_own(q.dhend + ((int64_t)s * nch + n) * K * V, dS);
       // (b) B operands of the own rows of dS; Kn fragments from LDS.
-      BSplit sb[NTW][2];
+      BSplit sb[OT][2];
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) sb[i][hs] = acc_b(dS[i], hs);
-      bf16x8 ka[NTW][2][2];  // [own tile][hs][rt]
+      bf16x8 ka[OT][2][2];  // [own tile][hs][rt]
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
-            const int ks = 2 * (hk * NTW + i) + hs;
+            const int ks = 2 * (hk * OT + i) + hs;
             ka[i][hs][rt] = *reinterpret_cast<const bf16x8*>(kf + ((rt * K16 + (FAST || ks < K16 ? ks : 0)) * 64 + l) * 8);
           }
       // (c) the update terms that do not need dD: e^{G_C} dS + dstates[n] + Qn^T o,
@@ -622,7 +658,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
       f32x16 ij[NTW];
       if constexpr (HAS_INJ) cols_to_acc(ij, inj, slot, l);
 #pragma unroll
-      for (int i = 0; i < NTW; ++i) {
+      for (int i = 0; i < OT; ++i) {
         dS[i] *= decay;
         if constexpr (HAS_INJ) dS[i] += ij[i];
       }
@@ -637,10 +673,10 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
-          const int ks = 2 * (hk * NTW + i) + hs;
+          const int ks = 2 * (hk * OT + i) + hs;
           if (FAST || ks < K16) {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
@@ -649,7 +685,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
             }
           }
           if constexpr (HAS_Q) {
-            const int t = hk * NTW + i;
+            const int t = hk * OT + i;
             if (FAST || t < RB) {
 #pragma unroll
               for (int pp = 0; pp < 2; ++pp) {
@@ -661,15 +697,17 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
             }
           }
         }
-      xch_put(slot, d, l);
+      if constexpr (!WIDE) xch_put(slot, d, l);
     }
+    // The split waves exchange their halves of Kn dS here; every wave has read
+    // this chunk's Kn rows before the copy of the next chunk's overwrites them.
     lds_barrier();
     fetch_early(nn);  // Kn rows are read only before the barrier above
     if (active) {
       // (d) dD = dd0 + e^{G_C-G} (half 0 + half 1) (saved: half hk stores row
       // tile hk), negated.
       f32x16 pd[2];
-      xch_get(pd, pslot, l);
+      if constexpr (!WIDE) xch_get(pd, pslot, l);
       f32x16 nd[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
@@ -681,11 +719,14 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * g + j;
-            const float sum = hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r];
+            float sum;
+            if constexpr (WIDE) sum = d[rt][r];
+            else sum = hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r];
             dd[r] = (HAS_Q ? d0r[rt][r] : 0.f) + fv[j] * sum;
           }
         }
-        if (rt == hk) ddprev = dd;
+        if constexpr (WIDE) ddprev[rt] = dd;
+        else if (rt == hk) ddprev[0] = dd;
         nd[rt] = -dd;
       }
       if constexpr (HAS_Q) {
@@ -699,12 +740,12 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
       }
       if constexpr (HAS_INJ) inj = injn;
       // (e) dS += W^T (-dD) for the own rows.
-      bf16x8 wa[NTW][4][2];  // [own tile][ps][hi, lo]
+      bf16x8 wa[OT][4][2];  // [own tile][ps][hi, lo]
 #pragma unroll
-      for (int i = 0; i < NTW; ++i)
+      for (int i = 0; i < OT; ++i)
 #pragma unroll
         for (int ps = 0; ps < 4; ++ps) {
-          const int t = hk * NTW + i;
+          const int t = hk * OT + i;
           const __bf16* p = lf + ((FAST || t < RB ? t : 0) * 4 + ps) * 1024 + l * 8;
           wa[i][ps][0] = *reinterpret_cast<const bf16x8*>(p);
           wa[i][ps][1] = *reinterpret_cast<const bf16x8*>(p + 512);
@@ -713,8 +754,8 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
       for (int ps = 0; ps < 4; ++ps) {
         const BSplit db = acc_b(nd[ps >> 1], ps & 1);
 #pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-          const int t = hk * NTW + i;
+        for (int i = 0; i < OT; ++i) {
+          const int t = hk * OT + i;
           if (FAST || t < RB) {
             dS[i] = mfma(wa[i][ps][0], db.hi, dS[i]);
             dS[i] = mfma(wa[i][ps][0], db.lo, dS[i]);
@@ -727,11 +768,10 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
     dma_drain();
   }
   if (active) {
-    const f32x16 dp[1] = {ddprev};
-    store_cols<1, !FAST>(slot, q.ddelta + (int64_t)s * nch * V * R, R, R, V, col0, 32 * hk, dp, l);
+    store_dd(q.ddelta + (int64_t)s * nch * V * R, ddprev);
 #pragma unroll
-    for (int i = 0; i < NTW; ++i) {
-      const int t = hk * NTW + i;
+    for (int i = 0; i < OT; ++i) {
+      const int t = hk * OT + i;
       if (FAST || t < RB) store_key_major(q.ds0, (int64_t)s * K * V, v, V, K, 32 * t, dS[i], l);
     }
   }
@@ -750,16 +790,16 @@ int allow_lds_strip(F kernel, size_t bytes) {
 
 }  // namespace
 
-int strip_wg_per_stream(int vdim) { return (vdim + 63) / 64; }
+int strip_wg_per_stream(int vdim, bool wide) { return wide ? (vdim + 127) / 128 : (vdim + 63) / 64; }
 
-StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0) {
+StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0, bool wide) {
   StripFwdOne o{};
   o.K = p.kdim;
   o.V = p.vdim;
   o.heads = p.heads;
   o.nch = nch;
   o.wg0 = wg0;
-  o.wg_per_stream = strip_wg_per_stream(p.vdim);
+  o.wg_per_stream = strip_wg_per_stream(p.vdim, wide);
   o.s0 = p.s0;
   o.s0_sb = p.s0_sb;
   o.s0_sh = p.s0_sh;
@@ -774,14 +814,14 @@ StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int
 }
 
 StripBwdOne strip_bwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
-                          int wg0, bool has_q) {
+                          int wg0, bool has_q, bool wide) {
   StripBwdOne o{};
   o.K = p.kdim;
   o.V = p.vdim;
   o.heads = p.heads;
   o.nch = nch;
   o.wg0 = wg0;
-  o.wg_per_stream = strip_wg_per_stream(p.vdim);
+  o.wg_per_stream = strip_wg_per_stream(p.vdim, wide);
   o.dfinal = gr.dfinal;
   o.dstates = gr.dstates;
   o.dd0 = has_q ? gr.dd0 : nullptr;
@@ -796,30 +836,38 @@ StripBwdOne strip_bwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
   return o;
 }
 
-template <int KM>
-int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, hipStream_t st) {
+template <int KM, bool FAST, bool WIDE>
+int launch_fwd_strip(const StripFwdPack& pk, int total_wg, hipStream_t st) {
   const size_t lds = FwdLds<KM>::BYTES;
-  if (fast) {
-    if (int rc = allow_lds_strip(gdn_state_fwd_strip<KM, true>, lds)) return rc;
-    hipLaunchKernelGGL((gdn_state_fwd_strip<KM, true>), dim3(total_wg), dim3(SNT), lds, st, pk);
-  } else {
-    if (int rc = allow_lds_strip(gdn_state_fwd_strip<KM, false>, lds)) return rc;
-    hipLaunchKernelGGL((gdn_state_fwd_strip<KM, false>), dim3(total_wg), dim3(SNT), lds, st, pk);
-  }
+  if (int rc = allow_lds_strip(gdn_state_fwd_strip<KM, FAST, WIDE>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_fwd_strip<KM, FAST, WIDE>), dim3(total_wg), dim3(SNT), lds, st, pk);
   return GPA_HIP_OK;
 }
 
-template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ>
+template <int KM>
+int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, bool wide, hipStream_t st) {
+  if constexpr (KM == 128)
+    if (wide) return launch_fwd_strip<KM, true, true>(pk, total_wg, st);
+  if (wide) return fail(GPA_HIP_EINVAL, "strip forward: the wide split is built for 128 keys only");
+  return fast ? launch_fwd_strip<KM, true, false>(pk, total_wg, st) : launch_fwd_strip<KM, false, false>(pk, total_wg, st);
+}
+
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, bool WIDE = false>
 int launch_bwd_strip(const StripBwdPack& pk, int total_wg, hipStream_t st) {
   const size_t lds = BwdLds<KM, HAS_Q>::BYTES;
-  if (int rc = allow_lds_strip(gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ>, lds)) return rc;
-  hipLaunchKernelGGL((gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ>), dim3(total_wg), dim3(SNT), lds, st, pk);
+  if (int rc = allow_lds_strip(gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, WIDE>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, WIDE>), dim3(total_wg), dim3(SNT), lds, st, pk);
   return GPA_HIP_OK;
 }
 
 template <int KM>
-int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj,
+int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj, bool wide,
                            hipStream_t st) {
+  if constexpr (KM == 128)
+    if (wide && !has_inj)
+      return has_q ? launch_bwd_strip<KM, true, true, false, true>(pk, total_wg, st)
+                   : launch_bwd_strip<KM, true, false, false, true>(pk, total_wg, st);
+  if (wide) return fail(GPA_HIP_EINVAL, "strip backward: the wide split is built for 128 keys without injections");
   if (fast) {
     if (has_q) return has_inj ? launch_bwd_strip<KM, true, true, true>(pk, total_wg, st)
                               : launch_bwd_strip<KM, true, true, false>(pk, total_wg, st);
@@ -832,9 +880,9 @@ int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool
                  : launch_bwd_strip<KM, false, false, false>(pk, total_wg, st);
 }
 
-template int launch_state_fwd_strip<64>(const StripFwdPack&, int, bool, hipStream_t);
-template int launch_state_fwd_strip<128>(const StripFwdPack&, int, bool, hipStream_t);
-template int launch_state_bwd_strip<64>(const StripBwdPack&, int, bool, bool, bool, hipStream_t);
-template int launch_state_bwd_strip<128>(const StripBwdPack&, int, bool, bool, bool, hipStream_t);
+template int launch_state_fwd_strip<64>(const StripFwdPack&, int, bool, bool, hipStream_t);
+template int launch_state_fwd_strip<128>(const StripFwdPack&, int, bool, bool, hipStream_t);
+template int launch_state_bwd_strip<64>(const StripBwdPack&, int, bool, bool, bool, bool, hipStream_t);
+template int launch_state_bwd_strip<128>(const StripBwdPack&, int, bool, bool, bool, bool, hipStream_t);
 
 }  // namespace gpa

@@ -169,8 +169,10 @@ int gpa_gdn_backward(const gpa_gdn_problem *problem, const gpa_gdn_saved *saved,
  * the sequential state recurrences of all groups on the bf16 strip kernels
  * (K <= 128) advance together in one launch per key-width class (and, in the
  * backward, per presence of a read gradient and of state injections).
- * Results are those of one gpa_gdn_forward / gpa_gdn_backward per group; the
- * groups must not write a buffer another one reads.  timing (may be NULL)
+ * Results are those of one gpa_gdn_forward / gpa_gdn_backward per group, up
+ * to the order of the sums over the key rows when a strip launch exceeds the
+ * device's compute units and runs in its wide form (one workgroup per 128
+ * value columns); the groups must not write a buffer another one reads.  timing (may be NULL)
  * marks every launch in order: the preps, the state launches, the reads
  * (forward); the dd0 kernels, the state launches, the chunk kernels
  * (backward). */

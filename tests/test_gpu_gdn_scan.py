@@ -160,6 +160,121 @@ def _oracle_segments_autograd(leaves, g, beta, s0, chunk, offset):
     return torch.cat(outs, 1), torch.stack(starts, 2), state
 
 
+# The wide strip form: a state launch whose split form would need more
+# workgroups than the device has CUs (two 64-column workgroups per 128-key
+# stream) runs one 128-column workgroup per stream, each wave with every key
+# row of its strip.  These shapes put 288 and 576 split workgroups in one launch.
+WIDE_FWD = [(9, 130, 16, 128, 128, 64, 0, torch.bfloat16), (3, 70, 48, 128, 256, 64, 17, torch.bfloat16)]
+WIDE_BWD = [(9, 40, 16, 128, 128, 16, 5, torch.bfloat16), (1, 40, 72, 128, 256, 32, 0, torch.bfloat16)]
+
+
+def _kernel_names(fn):
+    """Names of the device kernels `fn` launches (torch profiler)."""
+    from torch.profiler import ProfilerActivity, profile
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return {e.name for e in prof.events()}
+
+
+def _wide_ran(names, kind):
+    want = {"fwd": "gdn_state_fwd_strip<128, true, true>", "bwd_q": "gdn_state_bwd_strip<128, true, true, false, true>",
+            "bwd": "gdn_state_bwd_strip<128, true, false, false, true>"}[kind]
+    return any(want in n for n in names)
+
+
+@pytest.mark.parametrize("case", WIDE_FWD, ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}V{c[4]}")
+def test_wide_strip_forward_matches_recurrence(case):
+    from gpa_amd.ops import gdn_scan_hip
+    b, t, h, kd, vd, chunk, offset, dtype = case
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=11)
+    res = {}
+
+    def run():
+        res["r"] = gdn_scan_hip(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), s0.to(DEV), chunk=chunk,
+                                offset=offset)
+    names = _kernel_names(run)
+    assert _wide_ran(names, "fwd"), sorted(n for n in names if "state" in n)
+    out, states, final = res["r"]
+    ref_out, ref_states, ref_final = _oracle_segments(q, k, v, g, beta, s0, chunk, offset)
+    errs = [_rel(out, ref_out), _rel(states, ref_states), _rel(final, ref_final)]
+    print(case, errs)
+    assert max(errs) < 2e-2, errs
+
+
+@pytest.mark.parametrize("with_q", [True, False])
+@pytest.mark.parametrize("case", WIDE_BWD, ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}V{c[4]}")
+def test_wide_strip_backward_matches_autograd_of_recurrence(case, with_q):
+    from gpa_amd.ops import gdn_scan_hip
+    b, t, h, kd, vd, chunk, offset, dtype = case
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=13, q=with_q)
+    gen = torch.Generator().manual_seed(5)
+    w_out = torch.randn(b, t, h, vd, generator=gen, dtype=torch.float64)
+    w_final = torch.randn(b, h, kd, vd, generator=gen, dtype=torch.float64)
+
+    def loss(out, final):  # no state injections: the wide backward is built without them
+        total = (final.double() * w_final.to(final.device)).sum()
+        return total + (out.double() * w_out.to(out.device)).sum() if out is not None else total
+
+    leaves = [x.to(DEV).requires_grad_() if x is not None else None for x in (q, k, v)]
+    g_d, b_d, s_d = (x.to(DEV).requires_grad_() for x in (g, beta, s0))
+    out, states, final = gdn_scan_hip(leaves[0], leaves[1], leaves[2], g_d, b_d, s_d, chunk=chunk, offset=offset)
+    names = _kernel_names(lambda: loss(out, final).backward())
+    assert _wide_ran(names, "bwd_q" if with_q else "bwd"), sorted(n for n in names if "state" in n)
+    ref_leaves = [x.detach().double().requires_grad_() if x is not None else None for x in (q, k, v)]
+    g_r, b_r, s_r = (x.double().requires_grad_() for x in (g, beta, s0))
+    ro, _, rf = _oracle_segments_autograd(ref_leaves, g_r, b_r, s_r, chunk, offset)
+    loss(ro if with_q else None, rf).backward()
+    pairs = [("dk", leaves[1].grad, ref_leaves[1].grad), ("dv", leaves[2].grad, ref_leaves[2].grad),
+             ("dg", g_d.grad, g_r.grad), ("dbeta", b_d.grad, b_r.grad), ("ds0", s_d.grad, s_r.grad)]
+    if with_q:
+        pairs.append(("dq", leaves[0].grad, ref_leaves[0].grad))
+    errs = {name: _rel(a, r) for name, a, r in pairs}
+    print(case, with_q, errs)
+    assert all(e < 2e-2 for e in errs.values()), errs
+
+
+def test_wide_pack_matches_split_single_calls():
+    """Nine 128-key groups in one packed call (the relation edges' shape at
+    B=1, H=16: 288 split workgroups) take the wide form; one call per group
+    takes the split form.  The two differ only in the order of the sums over
+    the key rows."""
+    from gpa_amd.ops import gdn_scan_hip, gdn_scan_many
+    results = {}
+    for packed in (True, False):
+        groups = []
+        for i in range(9):
+            xs = _inputs(1, 130, 16, 128, 128, torch.bfloat16, 40 + i)
+            groups.append([x.to(DEV).requires_grad_() if x is not None else None for x in xs])
+
+        def fwd():
+            if packed:
+                return gdn_scan_many([dict(q=lv[0], k=lv[1], v=lv[2], g=lv[3], beta=lv[4], s0=lv[5], chunk=64,
+                                           offset=0, deferred=False) for lv in groups])
+            return [gdn_scan_hip(*lv, chunk=64, offset=0) for lv in groups]
+        res = {}
+        names = _kernel_names(lambda: res.setdefault("r", fwd()))
+        assert _wide_ran(names, "fwd") == packed
+        gen = torch.Generator().manual_seed(9)
+        loss = 0.
+        for out, states, final in res["r"]:
+            for x in (out, final):
+                if x is not None:
+                    loss = loss + (x.float() * torch.randn(x.shape, generator=gen).to(DEV)).sum()
+        names = _kernel_names(loss.backward)
+        assert _wide_ran(names, "bwd_q") == packed
+        fwd_t = [x.detach() for r in res["r"] for x in r if x is not None]
+        grads = [x.grad for lv in groups for x in lv if x is not None]
+        results[packed] = (fwd_t, grads)
+    (fa, ga), (fb, gb) = results[True], results[False]
+    for i, (a, b) in enumerate(zip(fa, fb)):
+        tol = 1e-5 if a.dtype == torch.float32 else 2e-3
+        assert _rel(a, b) < tol, ("forward", i, _rel(a, b))
+    for i, (a, b) in enumerate(zip(ga, gb)):
+        assert _rel(a, b) < 2e-3, ("grad", i, _rel(a, b))
+
+
 def test_gdn_rejects_bad_geometry_before_launch():
     from gpa_amd.ops import gdn_scan_hip
     q, k, v, g, beta, s0 = _inputs(1, 4, 1, 8, 8, torch.float32, seed=1)
