@@ -8,6 +8,28 @@
 
 namespace gpa {
 
+// bf16 pairs for the split (hi + lo) MFMA operands.  bf2_pack rounds two
+// floats to bf16 (round to nearest even, one v_cvt_pk_bf16_f32), x0 in the
+// low half; bf2_low / bf2_high widen a half back to float (exact).
+// bf2_split gives hi = bf16(x) and lo = bf16(x - hi) of a pair, forming
+// x - hi from the packed hi word: one shift or mask per value, where
+// converting each hi element back costs a second rounding and a shift.
+typedef __bf16 bf16pair_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf2_pack(float x0, float x1) {
+  const bf16pair_t h = {(__bf16)x0, (__bf16)x1};
+  uint32_t w;
+  __builtin_memcpy(&w, &h, 4);
+  return w;
+}
+// (The low half moves up through v_perm_b32, bytes 1:0 -> 3:2 over zeros, so
+// that the compiler does not turn the shift back into a second rounding.)
+__device__ __forceinline__ float bf2_low(uint32_t w) { return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu)); }
+__device__ __forceinline__ float bf2_high(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ void bf2_split(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = bf2_pack(x0, x1);
+  lo = bf2_pack(x0 - bf2_low(hi), x1 - bf2_high(hi));
+}
+
 constexpr int R = GPA_CHUNK_ROWS;  // rows per chunk tile
 constexpr int NT = 256;            // threads per block
 constexpr int VT = 32;             // state columns per sequential block

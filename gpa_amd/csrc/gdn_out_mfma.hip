@@ -31,11 +31,7 @@ __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
 __device__ __forceinline__ void frag_split(const float* x, bf16x8& hi, bf16x8& lo) {
   const f32x4 a = *reinterpret_cast<const f32x4*>(x), c = *reinterpret_cast<const f32x4*>(x + 4);
   const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    hi[e] = (__bf16)v[e];
-    lo[e] = (__bf16)(v[e] - (float)hi[e]);
-  }
+  split8(v, hi, lo);
 }
 
 // Eight contiguous floats kept raw: a group's loads are all issued before the
@@ -48,11 +44,7 @@ __device__ __forceinline__ Raw8 ld_raw8(const float* x) {
 }
 __device__ __forceinline__ void split_of(const Raw8& r, bf16x8& hi, bf16x8& lo) {
   const float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    hi[e] = (__bf16)v[e];
-    lo[e] = (__bf16)(v[e] - (float)hi[e]);
-  }
+  split8(v, hi, lo);
 }
 // Fragments loaded per group (fewer with 256 keys, whose Qn fragments
 // already hold 64 registers).

@@ -262,10 +262,9 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
       const int ln = piece & 63, ks = (piece >> 6) % K16, rt = (piece >> 6) / K16;
       const float* src = w_s + (32 * rt + (ln & 31)) * LK + 16 * ks + 8 * (ln >> 5);
       bf16x8v hi, lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        hi[e] = (__bf16)src[e];
-        lo[e] = (__bf16)(src[e] - (float)hi[e]);
+      {
+        const float v[8] = {src[0], src[1], src[2], src[3], src[4], src[5], src[6], src[7]};
+        split8(v, hi, lo);
       }
       __bf16* dst = wrow + (int64_t)(piece >> 6) * 1024 + ln * 8;
       *reinterpret_cast<bf16x8v*>(dst) = hi;
@@ -278,11 +277,11 @@ __global__ __launch_bounds__(PREP_NT, 1) void gdn_prep_mfma(gpa_gdn_problem p, g
       const int ln = piece & 63, cs = (piece >> 6) & 3, rb = piece >> 8;
       const int k = 32 * rb + (ln & 31), c0 = 16 * cs + 8 * (ln >> 5);
       bf16x8v hi, lo;
+      {
+        float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = k < K ? w_s[(c0 + e) * LK + k] : 0.f;
-        hi[e] = (__bf16)x;
-        lo[e] = (__bf16)(x - (float)hi[e]);
+        for (int e = 0; e < 8; ++e) v[e] = k < K ? w_s[(c0 + e) * LK + k] : 0.f;
+        split8(v, hi, lo);
       }
       __bf16* dst = wcol + (int64_t)(piece >> 6) * 1024 + ln * 8;
       *reinterpret_cast<bf16x8v*>(dst) = hi;

@@ -67,16 +67,12 @@ __device__ __forceinline__ void put_split_t(__bf16* hi, __bf16* lo, int ld, int 
                                             int l) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    bf16x4 xh, xl;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = acc[4 * g + e];
-      xh[e] = (__bf16)v;
-      xl[e] = (__bf16)(v - (float)xh[e]);
-    }
+    uint2 xh, xl;
+    bf2_split(acc[4 * g], acc[4 * g + 1], xh.x, xl.x);
+    bf2_split(acc[4 * g + 2], acc[4 * g + 3], xh.y, xl.y);
     const int off = (col0 + (l & 31)) * ld + row0 + 8 * g + 4 * (l >> 5);
-    *reinterpret_cast<bf16x4*>(&hi[off]) = xh;
-    *reinterpret_cast<bf16x4*>(&lo[off]) = xl;
+    *reinterpret_cast<uint2*>(&hi[off]) = xh;
+    *reinterpret_cast<uint2*>(&lo[off]) = xl;
   }
 }
 

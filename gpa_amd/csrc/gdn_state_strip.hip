@@ -48,7 +48,6 @@ namespace {
 
 constexpr int SW = 4;            // waves per workgroup
 constexpr int SNT = 64 * SW;     // threads per workgroup
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // one 16-byte piece
 
 struct BSplit {
@@ -62,11 +61,6 @@ __device__ __forceinline__ void swap_halves(uint32_t& x, uint32_t& y) {
   y = r[1];
 }
 
-__device__ __forceinline__ uint2 as_u2(bf16x4 x) {
-  uint2 u;
-  __builtin_memcpy(&u, &x, 8);
-  return u;
-}
 __device__ __forceinline__ bf16x8 as_b8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   const uint4 u = make_uint4(a, b, c, d);
   bf16x8 r;
@@ -77,16 +71,11 @@ __device__ __forceinline__ bf16x8 as_b8(uint32_t a, uint32_t b, uint32_t c, uint
 // Rows 16 hs .. 16 hs + 15 of a 32-row accumulator tile as the split B operand
 // of one 16-deep MFMA step.
 __device__ __forceinline__ BSplit acc_b(const f32x16& a, int hs) {
-  bf16x4 xh, xl, yh, yl;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float x = a[8 * hs + e], y = a[8 * hs + 4 + e];
-    xh[e] = (__bf16)x;
-    xl[e] = (__bf16)(x - (float)xh[e]);
-    yh[e] = (__bf16)y;
-    yl[e] = (__bf16)(y - (float)yh[e]);
-  }
-  uint2 XH = as_u2(xh), XL = as_u2(xl), YH = as_u2(yh), YL = as_u2(yl);
+  uint2 XH, XL, YH, YL;
+  bf2_split(a[8 * hs], a[8 * hs + 1], XH.x, XL.x);
+  bf2_split(a[8 * hs + 2], a[8 * hs + 3], XH.y, XL.y);
+  bf2_split(a[8 * hs + 4], a[8 * hs + 5], YH.x, YL.x);
+  bf2_split(a[8 * hs + 6], a[8 * hs + 7], YH.y, YL.y);
   swap_halves(XH.x, YH.x);
   swap_halves(XH.y, YH.y);
   swap_halves(XL.x, YL.x);
@@ -105,11 +94,8 @@ __device__ __forceinline__ BSplit vc_b(const float* m, int v, int V, int ps, int
   x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
   BSplit r;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float y = ok ? x[e] : 0.f;
-    r.hi[e] = (__bf16)y;
-    r.lo[e] = (__bf16)(y - (float)r.hi[e]);
-  }
+  for (int e = 0; e < 8; ++e) x[e] = ok ? x[e] : 0.f;
+  split8(x, r.hi, r.lo);
   return r;
 }
 

@@ -608,13 +608,6 @@ __device__ __forceinline__ void mask8(const Col& c, int first, float (&v)[8]) {
   for (int e = 0; e < 8; ++e) v[e] = (c.ok && first + e < c.count) ? v[e] : 0.f;
 }
 
-__device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    hi[e] = (__bf16)v[e];
-    lo[e] = (__bf16)(v[e] - (float)hi[e]);
-  }
-}
 
 __device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);

@@ -111,13 +111,17 @@ __device__ __forceinline__ bf16x8 pack8(const float* x) {
 struct SplitBf8 {
   bf16x8 hi, lo;
 };
+// Eight floats as bf16 hi and lo vectors (element e of x is element e of each).
+__device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  uint32_t h[4], o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bf2_split(x[2 * i], x[2 * i + 1], h[i], o[i]);
+  __builtin_memcpy(&hi, h, 16);
+  __builtin_memcpy(&lo, o, 16);
+}
 __device__ __forceinline__ SplitBf8 split_bf8(const float (&x)[8]) {
   SplitBf8 s;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s.hi[e] = (__bf16)x[e];
-    s.lo[e] = (__bf16)(x[e] - (float)s.hi[e]);
-  }
+  split8(x, s.hi, s.lo);
   return s;
 }
 // Elements (c0 + e, x), e = 0..7, of an fp32 matrix stored with x contiguous.

@@ -121,6 +121,20 @@ inline emu_f32x4 emu_mfma_16x16x4_f32(float a, float b, emu_f32x4 c) {
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, x, y, z) emu_mfma_32x32x16_bf16(a, b, c)
 // Only used on values that are uniform over the wave, where it is the identity.
 #define __builtin_amdgcn_readfirstlane(x) (x)
+// v_perm_b32: byte i of the result is byte sel.byte[i] of {a (bytes 4-7), b
+// (bytes 0-3)}, or 0x00 for selector 0x0c (the only other selector used).
+inline uint32_t emu_perm(uint32_t a, uint32_t b, uint32_t sel) {
+  const uint64_t c = ((uint64_t)a << 32) | b;
+  uint32_t d = 0;
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t s = (sel >> (8 * i)) & 0xff;
+    if (s != 0x0c && s > 7) abort();
+    const uint32_t byte = s == 0x0c ? 0u : (uint32_t)((c >> (8 * s)) & 0xff);
+    d |= byte << (8 * i);
+  }
+  return d;
+}
+#define __builtin_amdgcn_perm(a, b, s) emu_perm((uint32_t)(a), (uint32_t)(b), (uint32_t)(s))
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu_mfma_32x32x2_f32(a, b, c)
 #define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) emu_mfma_16x16x4_f32(a, b, c)
 
