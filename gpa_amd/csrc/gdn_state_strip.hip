@@ -464,8 +464,9 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
     // holds the whole sum.
     if constexpr (!WIDE) lds_barrier();
     if (active) {
-      // (c) D = U - W S (split: half 0 + half 1, summed in that order in both
-      // waves; half hk keeps row tile hk to save), then scaled by e^{G_C - G}.
+      // (c) D = U - W S (split: own half + partner half, the same bits in both
+      // waves since + commutes; half hk keeps row tile hk to save), then
+      // scaled by e^{G_C - G}.
       f32x16 pd[2];
       if constexpr (!WIDE) xch_get(pd, pslot, l);
       const float* gf = gl0 + cur * GATE_FLOATS;
@@ -476,7 +477,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           if constexpr (WIDE) D[rt][r] = ur[rt][r] - d[rt][r];
-          else D[rt][r] = ur[rt][r] - (hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r]);
+          else D[rt][r] = ur[rt][r] - (d[rt][r] + pd[rt][r]);
         }
         if constexpr (WIDE) dprev[rt] = D[rt];
         else if (rt == hk) dprev[0] = D[rt];
@@ -707,7 +708,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
             const int r = 4 * g + j;
             float sum;
             if constexpr (WIDE) sum = d[rt][r];
-            else sum = hk == 0 ? d[rt][r] + pd[rt][r] : pd[rt][r] + d[rt][r];
+            else sum = d[rt][r] + pd[rt][r];  // the same bits in both waves (+ commutes)
             dd[r] = (HAS_Q ? d0r[rt][r] : 0.f) + fv[j] * sum;
           }
         }
