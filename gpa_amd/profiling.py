@@ -382,6 +382,38 @@ def summarize_mfma(path: str, clock_mhz: float = 2400.0, xcds: int = 8, simds: i
     return "\n".join(lines) + "\n"
 
 
+STALL_PASSES = (
+    ("SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY",
+     "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_SCA"),
+    ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAVES"),
+)
+
+
+def summarize_stalls(first: str, second: str, top: int = 24) -> str:
+    """Where the waves of each kernel spend their cycles, from the two `--pmc`
+    passes of STALL_PASSES: the share of wave cycles waiting at an s_waitcnt
+    or barrier (WAIT_ANY), waiting for an instruction's dependency to issue
+    (WAIT_INST_ANY, of which LDS: WAIT_INST_LDS), and issuing any, VALU (MFMA
+    included), LDS and scalar instructions; and the share of LDS-active
+    cycles lost to bank conflicts.  Kernels in order of total wave cycles."""
+    a, b = _read_counters(first), _read_counters(second)
+    kernels = {k for k, c in a if c == "SQ_WAVE_CYCLES"}
+
+    def tot(stats, k, ctr):
+        return stats.get((k, ctr), (0, 0.0))[1]
+
+    order = sorted(kernels, key=lambda k: -tot(a, k, "SQ_WAVE_CYCLES"))[:top]
+    cols = STALL_PASSES[0][1:]
+    lines = ["| kernel | dispatches | " + " | ".join(c[3:].lower() for c in cols) + " | LDS bank conflict |",
+             "|---|---:|" + "---:|" * (len(cols) + 1)]
+    for k in order:
+        w = tot(a, k, "SQ_WAVE_CYCLES") or 1.0
+        conflict = tot(b, k, "SQ_LDS_BANK_CONFLICT") / (tot(b, k, "SQ_LDS_IDX_ACTIVE") or 1.0)
+        lines.append(f"| `{timer_name(k)}` | {a[(k, 'SQ_WAVE_CYCLES')][0]} | "
+                     + " | ".join(f"{100 * tot(a, k, c) / w:.0f} %" for c in cols) + f" | {100 * conflict:.0f} % |")
+    return "\n".join(lines) + "\n"
+
+
 def copy_kernel(nbytes: int, reps: int = 3) -> None:
     """A plain device copy of `nbytes` (reads and writes that many bytes per
     launch): the calibration kernel for FETCH_SIZE / WRITE_SIZE."""
@@ -407,8 +439,10 @@ if __name__ == "__main__":
         print(summarize_traffic(*args[:4], int(args[4])))
     elif cmd == "mfma":
         print(summarize_mfma(args[0]))
+    elif cmd == "stalls":
+        print(summarize_stalls(args[0], args[1]))
     elif cmd == "copy":
         copy_kernel(int(args[0]))
     else:
-        raise SystemExit("usage: python -m gpa_amd.profiling trace|counters|mfma <csv> | "
+        raise SystemExit("usage: python -m gpa_amd.profiling trace|counters|mfma <csv> | stalls <csv> <csv> | "
                          "traffic <fetch csv> <write csv> <copy fetch csv> <copy write csv> <copy bytes> | copy <bytes>")
