@@ -909,12 +909,15 @@ int device_cus() {
   return cus[dev];
 }
 
-// The wide strip form when the split form would need more workgroups than the
-// device has CUs (each workgroup holds a CU for the whole chain), every group
-// can take it and the pack is `fast` with 128 keys.
-bool strip_go_wide(int km, bool fast, bool all_ok, int split_workgroups) {
+// The strip form of a pack (waves per strip, gdn_strip.h): quarter when its
+// workgroups fit on the device's CUs, else split when those fit, else wide;
+// each only where every group can take it.
+int strip_form(int km, bool fast, bool wide_ok, bool quarter_ok, int quarter_workgroups, int split_workgroups) {
   const int cus = device_cus();
-  return km == 128 && fast && all_ok && cus > 0 && split_workgroups > cus;
+  if (km != 128 || !fast || cus <= 0) return 2;
+  if (quarter_ok && quarter_workgroups <= cus) return 4;
+  if (wide_ok && split_workgroups > cus) return 1;
+  return 2;
 }
 
 // The state recurrence of one problem outside a pack.
@@ -925,9 +928,10 @@ int fwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, hipStr
     StripFwdPack pk{};
     pk.n = 1;
     const bool fast = p.kdim == KM && p.vdim % 64 == 0;
-    const bool wide = strip_go_wide(KM, fast, strip_wide_ok(p), strip_workgroups(p, false));
-    pk.p[0] = strip_fwd_one(p, sv, nch, 0, wide);
-    return launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, wide), fast, wide, st);
+    const int nq = strip_form(KM, fast, strip_wide_ok(p), strip_quarter_ok(p), strip_workgroups(p, 4),
+                              strip_workgroups(p, 2));
+    pk.p[0] = strip_fwd_one(p, sv, nch, 0, nq);
+    return launch_state_fwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, nq), fast, nq, st);
   }
   if (use_mfma<E>(p)) return launch_state_fwd_mfma<KM>(p, sv, nch, st);
   const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -974,10 +978,10 @@ int bwd_state(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_g
     StripBwdPack pk{};
     pk.n = 1;
     const bool fast = p.kdim == KM && p.vdim % 64 == 0, has_inj = gr.dstates != nullptr;
-    const bool wide = strip_go_wide(KM, fast, strip_wide_ok(p) && !has_inj, strip_workgroups(p, false));
-    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q, wide);
-    return launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, wide), fast, has_q, has_inj, wide,
-                                                        st);
+    const int nq = strip_form(KM, fast, strip_wide_ok(p) && !has_inj, strip_quarter_ok(p), strip_workgroups(p, 4),
+                              strip_workgroups(p, 2));
+    pk.p[0] = strip_bwd_one(p, sv, gr, nch, 0, has_q, nq);
+    return launch_state_bwd_strip<KM <= 64 ? 64 : 128>(pk, strip_workgroups(p, nq), fast, has_q, has_inj, nq, st);
   }
   if (use_mfma<E>(p)) return launch_state_bwd_mfma<KM>(p, sv, gr, nch, st);
   const dim3 grid_s((p.vdim + VT - 1) / VT, p.batch * p.heads);
@@ -1141,7 +1145,7 @@ bool side_groups(const gpa_gdn_problem* ps, int n, const gpa_timing* tm, hipStre
   }
   if (strips && n >= 2) {
     int wg = 0;
-    for (int i = 0; i < n; ++i) wg += strip_workgroups(ps[i], false);
+    for (int i = 0; i < n; ++i) wg += strip_workgroups(ps[i], 2);
     const int cus = device_cus();
     if (cus <= 0 || wg > cus) return false;
     for (int i = n / 2; i < n; ++i) side[i] = true;
@@ -1189,27 +1193,29 @@ int launch_forward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, con
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
-    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0;
-    bool fast = true, all_ok = true;
+    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0, quarter = 0;
+    bool fast = true, wide_ok = true, quarter_ok = true;
     for (int j = i; j < n; ++j) {
       if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || on_side[j] != on_side[i]) continue;
       members[nm++] = j;
-      split += strip_workgroups(ps[j], false);
+      split += strip_workgroups(ps[j], 2);
+      quarter += strip_workgroups(ps[j], 4);
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
-      all_ok = all_ok && strip_wide_ok(ps[j]);
+      wide_ok = wide_ok && strip_wide_ok(ps[j]);
+      quarter_ok = quarter_ok && strip_quarter_ok(ps[j]);
       done[j] = true;
     }
-    const bool wide = strip_go_wide(km, fast, all_ok, split);
+    const int nq = strip_form(km, fast, wide_ok, quarter_ok, quarter, split);
     StripFwdPack pk{};
     int total = 0;
     for (int m = 0; m < nm; ++m) {
       const int j = members[m];
       const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
-      pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total, wide);
-      total += strip_workgroups(ps[j], wide);
+      pk.p[pk.n++] = strip_fwd_one(ps[j], svs[j], nch, total, nq);
+      total += strip_workgroups(ps[j], nq);
     }
-    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, wide, stream_of(i))
-                            : launch_state_fwd_strip<128>(pk, total, fast, wide, stream_of(i));
+    const int rc = km <= 64 ? launch_state_fwd_strip<64>(pk, total, fast, nq, stream_of(i))
+                            : launch_state_fwd_strip<128>(pk, total, fast, nq, stream_of(i));
     if (rc) return rc;
   }
   // the out phase of each group follows its state pack on the same stream
@@ -1271,29 +1277,31 @@ int launch_backward_many(const gpa_gdn_problem* ps, const gpa_gdn_saved* svs, co
       continue;
     }
     const int km = kmax_for(ps[i].kdim);
-    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0;
-    bool fast = true, all_ok = !hi;
+    int members[GPA_GDN_MAX_PACK], nm = 0, split = 0, quarter = 0;
+    bool fast = true, wide_ok = !hi, quarter_ok = true;
     for (int j = i; j < n; ++j) {
       if (done[j] || !on_strips(ps[j]) || kmax_for(ps[j].kdim) != km || has_read(ps[j], gr[j]) != hq ||
           (gr[j].dstates != nullptr) != hi || on_side[j] != on_side[i])
         continue;
       members[nm++] = j;
-      split += strip_workgroups(ps[j], false);
+      split += strip_workgroups(ps[j], 2);
+      quarter += strip_workgroups(ps[j], 4);
       fast = fast && ps[j].kdim == km && ps[j].vdim % 64 == 0;
-      all_ok = all_ok && strip_wide_ok(ps[j]);
+      wide_ok = wide_ok && strip_wide_ok(ps[j]);
+      quarter_ok = quarter_ok && strip_quarter_ok(ps[j]);
       done[j] = true;
     }
-    const bool wide = strip_go_wide(km, fast, all_ok, split);
+    const int nq = strip_form(km, fast, wide_ok, quarter_ok, quarter, split);
     StripBwdPack pk{};
     int total = 0;
     for (int m = 0; m < nm; ++m) {
       const int j = members[m];
       const int nch = gpa_gdn_nchunks(ps[j].tokens, ps[j].offset, ps[j].chunk);
-      pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq, wide);
-      total += strip_workgroups(ps[j], wide);
+      pk.p[pk.n++] = strip_bwd_one(ps[j], svs[j], gr[j], nch, total, hq, nq);
+      total += strip_workgroups(ps[j], nq);
     }
-    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, wide, stream_of(i))
-                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, wide, stream_of(i));
+    const int rc = km <= 64 ? launch_state_bwd_strip<64>(pk, total, fast, hq, hi, nq, stream_of(i))
+                            : launch_state_bwd_strip<128>(pk, total, fast, hq, hi, nq, stream_of(i));
     if (rc) return rc;
   }
   // the chunk phase of each group follows its state pack on the same stream

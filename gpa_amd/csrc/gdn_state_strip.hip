@@ -330,6 +330,37 @@ __device__ __forceinline__ void xch_get(f32x16 (&d)[2], const float* x, int l) {
     }
 }
 
+// The full product of a strip from the NQ waves' parts: wave hk holds its own
+// part in d, the others' parts are in their exchange slots (strip_slots +
+// q slot_floats).  Summed in the order of the parts, ((p0 + p1) + p2) + p3, in
+// every wave, so that every wave of a strip holds the same bits.
+template <int NQ>
+__device__ __forceinline__ void strip_sum(f32x16 (&sum)[2], const f32x16 (&d)[2], const float* strip_slots,
+                                          int slot_floats, int hk, int l) {
+  if constexpr (NQ == 1) {
+    sum[0] = d[0];
+    sum[1] = d[1];
+  } else {
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      f32x16 part[2];
+      if (qi == hk) {
+        part[0] = d[0];
+        part[1] = d[1];
+      } else {
+        xch_get(part, strip_slots + qi * slot_floats, l);
+      }
+      if (qi == 0) {
+        sum[0] = part[0];
+        sum[1] = part[1];
+      } else {
+        sum[0] += part[0];
+        sum[1] += part[1];
+      }
+    }
+  }
+}
+
 template <int KM>
 struct FwdLds {  // bytes
   static constexpr int WROW = 2 * (KM / 16) * 64 * 16 * 2, KCOL = (KM / 32) * 4 * 64 * 8 * 2;
@@ -347,11 +378,12 @@ struct BwdLds {  // bytes
 };
 
 // ---------------------------------------------------------------------------------------- forward
-template <int KM, bool FAST, bool WIDE>
+template <int KM, bool FAST, int NQ>
 __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
-  static_assert(!WIDE || (FAST && KM == 128), "the wide split is built for whole 128-key problems");
+  static_assert(NQ == 2 || (FAST && KM == 128), "the wide and quarter forms are built for whole 128-key problems");
   constexpr int KT = KM / 32, K16M = KM / 16, NTW = KM / 64;
-  constexpr int OT = WIDE ? KT : NTW;  // row tiles of S a wave owns
+  constexpr int OT = KT / NQ;  // row tiles of S a wave owns
+  constexpr int CPW = 32 * (SW / NQ);  // value columns per workgroup
   using L = FwdLds<KM>;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const StripFwdOne q = pack_entry<StripFwdPack, StripFwdOne>();
@@ -359,20 +391,20 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
   const int s = local / q.wg_per_stream, cb = local % q.wg_per_stream;
   const int b = s / q.heads, h = s % q.heads;
   // Wave-uniform values are scalar: branches on them are scalar.
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = WIDE ? 0 : w & 1;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = w % NQ;
   const int K = FAST ? KM : q.K, V = q.V, nch = q.nch;
   const int K16 = K / 16, RB = (K + 31) / 32;
   const int wrow_n = 2 * K16 * 64 * 16, kcol_n = RB * 4 * 64 * 8;  // this problem's bf16 elements per chunk
-  // Split: strip w/2 of the workgroup's 64 columns, key half w%2.  Wide: strip
-  // w of its 128 columns, every key row.
-  const int col0 = WIDE ? 128 * cb + 32 * w : 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
+  // Strip w/NQ of the workgroup's CPW columns, key part w%NQ (split: halves,
+  // wide: all rows, quarter: quarters).
+  const int col0 = CPW * cb + 32 * (w / NQ), v = col0 + (l & 31);
   const bool active = FAST || col0 < V;  // FAST: V % 64 == 0 (wide: V % 128 == 0)
   const uint32_t lds0 = lds_offset(smem_raw);
   auto wbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + i * L::BUF); };
   auto kbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + i * L::BUF + L::WROW); };
   float* gl0 = reinterpret_cast<float*>(smem_raw + L::GATE_OFF);
   float* slot = reinterpret_cast<float*>(smem_raw + L::XCH_OFF) + w * Slot<NTW>::FLOATS;
-  const float* pslot = reinterpret_cast<const float*>(smem_raw + L::XCH_OFF) + (w ^ 1) * Slot<NTW>::FLOATS;
+  const float* strip_slots = reinterpret_cast<const float*>(smem_raw + L::XCH_OFF) + (w - hk) * Slot<NTW>::FLOATS;
 
   const u32x4* wsrc = reinterpret_cast<const u32x4*>(q.wrow + (int64_t)s * nch * wrow_n);
   const u32x4* ksrc = reinterpret_cast<const u32x4*>(q.kcol + (int64_t)s * nch * kcol_n);
@@ -385,17 +417,21 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
   // The wave's rows of a strip go to a value-major block NTW row tiles at a
   // time (the capacity of its LDS slot).
   auto store_own = [&](float* dst, const f32x16 (&x)[OT]) {
+    constexpr int SCH = OT < NTW ? OT : NTW;
 #pragma unroll
-    for (int h2 = 0; h2 < OT / NTW; ++h2) {
-      f32x16 part[NTW];
+    for (int h2 = 0; h2 < OT / SCH; ++h2) {
+      f32x16 part[SCH];
 #pragma unroll
-      for (int i = 0; i < NTW; ++i) part[i] = x[h2 * NTW + i];
-      store_cols<NTW, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * NTW), part, l);
+      for (int i = 0; i < SCH; ++i) part[i] = x[h2 * SCH + i];
+      store_cols<SCH, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * SCH), part, l);
     }
   };
-  constexpr int DT = WIDE ? 2 : 1;  // row tiles of D a wave saves
+  // Row tiles of D a wave saves: wide both, split and quarter the tile of its
+  // index hk (quarter: waves 0 and 1 of a strip; saves_d).
+  constexpr int DT = NQ == 1 ? 2 : 1;
+  const bool saves_d = NQ != 4 || hk < 2;
   auto store_d = [&](float* dst, const f32x16 (&x)[DT]) {
-    store_cols<DT, !FAST>(slot, dst, R, R, V, col0, WIDE ? 0 : 32 * hk, x, l);
+    if (saves_d) store_cols<DT, !FAST>(slot, dst, R, R, V, col0, NQ == 1 ? 0 : 32 * hk, x, l);
   };
 
   f32x16 S[OT];
@@ -458,28 +494,25 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
             }
           }
         }
-      if constexpr (!WIDE) xch_put(slot, d, l);
+      if constexpr (NQ > 1) xch_put(slot, d, l);
     }
-    // The split waves meet here to exchange their halves of W S; a wide wave
-    // holds the whole sum.
-    if constexpr (!WIDE) lds_barrier();
+    // The waves of a strip meet here to exchange their parts of W S; a wide
+    // wave holds the whole sum.
+    if constexpr (NQ > 1) lds_barrier();
     if (active) {
       // (c) D = U - W S (split: own half + partner half, the same bits in both
       // waves since + commutes; half hk keeps row tile hk to save), then
       // scaled by e^{G_C - G}.
-      f32x16 pd[2];
-      if constexpr (!WIDE) xch_get(pd, pslot, l);
+      f32x16 sum[2];
+      strip_sum<NQ>(sum, d, strip_slots, Slot<NTW>::FLOATS, hk, l);
       const float* gf = gl0 + cur * GATE_FLOATS;
       const float decay = gf[R];
       f32x16 D[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if constexpr (WIDE) D[rt][r] = ur[rt][r] - d[rt][r];
-          else D[rt][r] = ur[rt][r] - (d[rt][r] + pd[rt][r]);
-        }
-        if constexpr (WIDE) dprev[rt] = D[rt];
+        for (int r = 0; r < 16; ++r) D[rt][r] = ur[rt][r] - sum[rt][r];
+        if constexpr (NQ == 1) dprev[rt] = D[rt];
         else if (rt == hk) dprev[0] = D[rt];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -530,30 +563,31 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_fwd_strip(StripFwdPack pk) {
 }
 
 // --------------------------------------------------------------------------------------- backward
-template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, bool WIDE>
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, int NQ>
 __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
-  static_assert(!WIDE || (FAST && KM == 128 && !HAS_INJ), "the wide split is built for whole 128-key problems");
+  static_assert(NQ == 2 || (FAST && KM == 128), "the wide and quarter forms are built for whole 128-key problems");
+  static_assert(NQ != 1 || !HAS_INJ, "the wide form is built without state injections");
   constexpr int KT = KM / 32, K16M = KM / 16, NTW = KM / 64;
-  constexpr int OT = WIDE ? KT : NTW, DT = WIDE ? 2 : 1;  // row tiles of dS a wave owns, of dD it saves
+  constexpr int OT = KT / NQ, DT = NQ == 1 ? 2 : 1;  // row tiles of dS a wave owns, of dD it saves
+  constexpr int CPW = 32 * (SW / NQ);  // value columns per workgroup
   using L = BwdLds<KM, HAS_Q>;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const StripBwdOne q = pack_entry<StripBwdPack, StripBwdOne>();
   const int local = blockIdx.x - q.wg0;
   const int s = local / q.wg_per_stream, cb = local % q.wg_per_stream;
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = WIDE ? 0 : w & 1;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hk = w % NQ;
   const int K = FAST ? KM : q.K, V = q.V, nch = q.nch;
   const int K16 = K / 16, RB = (K + 31) / 32;
   const int krow_n = 2 * K16 * 64 * 8, wcol_n = RB * 4 * 64 * 16, qcol_n = HAS_Q ? RB * 4 * 64 * 8 : 0;
-  // Split: strip w/2 of the workgroup's 64 columns, key half w%2.  Wide: strip
-  // w of its 128 columns, every key row.
-  const int col0 = WIDE ? 128 * cb + 32 * w : 64 * cb + 32 * (w >> 1), v = col0 + (l & 31);
+  // Strip w/NQ of the workgroup's CPW columns, key part w%NQ.
+  const int col0 = CPW * cb + 32 * (w / NQ), v = col0 + (l & 31);
   const bool active = FAST || col0 < V;  // FAST: V % 64 == 0 (wide: V % 128 == 0)
   const uint32_t lds0 = lds_offset(smem_raw);
   const __bf16* kf = reinterpret_cast<const __bf16*>(smem_raw);  // Kn rows (one buffer)
   auto lbuf = [&](int i) { return reinterpret_cast<const __bf16*>(smem_raw + L::LATE_OFF + i * L::LATE); };
   float* gl0 = reinterpret_cast<float*>(smem_raw + L::GATE_OFF);
   float* slot = reinterpret_cast<float*>(smem_raw + L::XCH_OFF) + w * Slot<NTW>::FLOATS;
-  const float* pslot = reinterpret_cast<const float*>(smem_raw + L::XCH_OFF) + (w ^ 1) * Slot<NTW>::FLOATS;
+  const float* strip_slots = reinterpret_cast<const float*>(smem_raw + L::XCH_OFF) + (w - hk) * Slot<NTW>::FLOATS;
 
   const u32x4* ksrc = reinterpret_cast<const u32x4*>(q.krow + (int64_t)s * nch * krow_n);
   const u32x4* wsrc = reinterpret_cast<const u32x4*>(q.wcol + (int64_t)s * nch * wcol_n);
@@ -570,16 +604,18 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
   // The wave's rows of a strip go to a value-major block NTW row tiles at a
   // time (the capacity of its LDS slot).
   auto store_own = [&](float* dst, const f32x16 (&x)[OT]) {
+    constexpr int SCH = OT < NTW ? OT : NTW;
 #pragma unroll
-    for (int h2 = 0; h2 < OT / NTW; ++h2) {
-      f32x16 part[NTW];
+    for (int h2 = 0; h2 < OT / SCH; ++h2) {
+      f32x16 part[SCH];
 #pragma unroll
-      for (int i = 0; i < NTW; ++i) part[i] = x[h2 * NTW + i];
-      store_cols<NTW, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * NTW), part, l);
+      for (int i = 0; i < SCH; ++i) part[i] = x[h2 * SCH + i];
+      store_cols<SCH, !FAST>(slot, dst, K, K, V, col0, 32 * (hk * OT + h2 * SCH), part, l);
     }
   };
+  const bool saves_d = NQ != 4 || hk < 2;  // quarter: waves 0 and 1 of a strip save dD
   auto store_dd = [&](float* dst, const f32x16 (&x)[DT]) {
-    store_cols<DT, !FAST>(slot, dst, R, R, V, col0, WIDE ? 0 : 32 * hk, x, l);
+    if (saves_d) store_cols<DT, !FAST>(slot, dst, R, R, V, col0, NQ == 1 ? 0 : 32 * hk, x, l);
   };
   f32x16 dS[OT];
 #pragma unroll
@@ -593,8 +629,8 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
   const int strip = col0 >> 5, nstrip = ufrag_v(V) >> 5;
   float d0r[HAS_Q ? 2 : 1][16], d0n[HAS_Q ? 2 : 1][16];
   float orr[HAS_Q ? 2 : 1][16], onx[HAS_Q ? 2 : 1][16];
-  ColsRaw<NTW> inj, injn;
-  auto load_cols = [&](int n, float (&d0)[HAS_Q ? 2 : 1][16], float (&ov)[HAS_Q ? 2 : 1][16], ColsRaw<NTW>& ij) {
+  ColsRaw<OT> inj, injn;
+  auto load_cols = [&](int n, float (&d0)[HAS_Q ? 2 : 1][16], float (&ov)[HAS_Q ? 2 : 1][16], ColsRaw<OT>& ij) {
     if constexpr (HAS_Q) {
       load_ufrag<!FAST>(d0[0], q.dd0 + ufrag_off(s, n, nch, V), strip, nstrip, 0, l);
       load_ufrag<!FAST>(d0[1], q.dd0 + ufrag_off(s, n, nch, V), strip, nstrip, 1, l);
@@ -602,7 +638,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
       load_ufrag<!FAST>(ov[1], q.o + ufrag_off(s, n, nch, V), strip, nstrip, 1, l);
     }
     if constexpr (HAS_INJ)
-      cols_load<NTW, !FAST>(ij, q.dstates + ((int64_t)s * nch + n) * K * V, K, K, V, col0, 32 * NTW * hk, l);
+      cols_load<OT, !FAST>(ij, q.dstates + ((int64_t)s * nch + n) * K * V, K, K, V, col0, 32 * OT * hk, l);
   };
   if (active) load_cols(nch - 1, d0r, orr, inj);
   dma_drain();  // every load of the preamble: the loop then starts with none pending
@@ -642,7 +678,7 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
       // (c) the update terms that do not need dD: e^{G_C} dS + dstates[n] + Qn^T o,
       // interleaved with Kn dS over the own rows.
       const float decay = gf[R];
-      f32x16 ij[NTW];
+      f32x16 ij[OT];
       if constexpr (HAS_INJ) cols_to_acc(ij, inj, slot, l);
 #pragma unroll
       for (int i = 0; i < OT; ++i) {
@@ -684,17 +720,17 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
             }
           }
         }
-      if constexpr (!WIDE) xch_put(slot, d, l);
+      if constexpr (NQ > 1) xch_put(slot, d, l);
     }
-    // The split waves exchange their halves of Kn dS here; every wave has read
+    // The waves of a strip exchange their parts of Kn dS here; every wave has read
     // this chunk's Kn rows before the copy of the next chunk's overwrites them.
     lds_barrier();
     fetch_early(nn);  // Kn rows are read only before the barrier above
     if (active) {
       // (d) dD = dd0 + e^{G_C-G} (half 0 + half 1) (saved: half hk stores row
       // tile hk), negated.
-      f32x16 pd[2];
-      if constexpr (!WIDE) xch_get(pd, pslot, l);
+      f32x16 sum[2];
+      strip_sum<NQ>(sum, d, strip_slots, Slot<NTW>::FLOATS, hk, l);
       f32x16 nd[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
@@ -706,13 +742,10 @@ __global__ __launch_bounds__(SNT, 1) void gdn_state_bwd_strip(StripBwdPack pk) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * g + j;
-            float sum;
-            if constexpr (WIDE) sum = d[rt][r];
-            else sum = d[rt][r] + pd[rt][r];  // the same bits in both waves (+ commutes)
-            dd[r] = (HAS_Q ? d0r[rt][r] : 0.f) + fv[j] * sum;
+            dd[r] = (HAS_Q ? d0r[rt][r] : 0.f) + fv[j] * sum[rt][r];
           }
         }
-        if constexpr (WIDE) ddprev[rt] = dd;
+        if constexpr (NQ == 1) ddprev[rt] = dd;
         else if (rt == hk) ddprev[0] = dd;
         nd[rt] = -dd;
       }
@@ -777,16 +810,19 @@ int allow_lds_strip(F kernel, size_t bytes) {
 
 }  // namespace
 
-int strip_wg_per_stream(int vdim, bool wide) { return wide ? (vdim + 127) / 128 : (vdim + 63) / 64; }
+int strip_wg_per_stream(int vdim, int nq) {
+  const int cols = 32 * (SW / nq);
+  return (vdim + cols - 1) / cols;
+}
 
-StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0, bool wide) {
+StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0, int nq) {
   StripFwdOne o{};
   o.K = p.kdim;
   o.V = p.vdim;
   o.heads = p.heads;
   o.nch = nch;
   o.wg0 = wg0;
-  o.wg_per_stream = strip_wg_per_stream(p.vdim, wide);
+  o.wg_per_stream = strip_wg_per_stream(p.vdim, nq);
   o.s0 = p.s0;
   o.s0_sb = p.s0_sb;
   o.s0_sh = p.s0_sh;
@@ -801,14 +837,14 @@ StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int
 }
 
 StripBwdOne strip_bwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
-                          int wg0, bool has_q, bool wide) {
+                          int wg0, bool has_q, int nq) {
   StripBwdOne o{};
   o.K = p.kdim;
   o.V = p.vdim;
   o.heads = p.heads;
   o.nch = nch;
   o.wg0 = wg0;
-  o.wg_per_stream = strip_wg_per_stream(p.vdim, wide);
+  o.wg_per_stream = strip_wg_per_stream(p.vdim, nq);
   o.dfinal = gr.dfinal;
   o.dstates = gr.dstates;
   o.dd0 = has_q ? gr.dd0 : nullptr;
@@ -823,38 +859,49 @@ StripBwdOne strip_bwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, con
   return o;
 }
 
-template <int KM, bool FAST, bool WIDE>
+template <int KM, bool FAST, int NQ>
 int launch_fwd_strip(const StripFwdPack& pk, int total_wg, hipStream_t st) {
   const size_t lds = FwdLds<KM>::BYTES;
-  if (int rc = allow_lds_strip(gdn_state_fwd_strip<KM, FAST, WIDE>, lds)) return rc;
-  hipLaunchKernelGGL((gdn_state_fwd_strip<KM, FAST, WIDE>), dim3(total_wg), dim3(SNT), lds, st, pk);
+  if (int rc = allow_lds_strip(gdn_state_fwd_strip<KM, FAST, NQ>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_fwd_strip<KM, FAST, NQ>), dim3(total_wg), dim3(SNT), lds, st, pk);
   return GPA_HIP_OK;
 }
 
 template <int KM>
-int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, bool wide, hipStream_t st) {
-  if constexpr (KM == 128)
-    if (wide) return launch_fwd_strip<KM, true, true>(pk, total_wg, st);
-  if (wide) return fail(GPA_HIP_EINVAL, "strip forward: the wide split is built for 128 keys only");
-  return fast ? launch_fwd_strip<KM, true, false>(pk, total_wg, st) : launch_fwd_strip<KM, false, false>(pk, total_wg, st);
+int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, int nq, hipStream_t st) {
+  if constexpr (KM == 128) {
+    if (nq == 1 && fast) return launch_fwd_strip<KM, true, 1>(pk, total_wg, st);
+    if (nq == 4 && fast) return launch_fwd_strip<KM, true, 4>(pk, total_wg, st);
+  }
+  if (nq != 2) return fail(GPA_HIP_EINVAL, "strip forward: the wide and quarter forms are built for whole 128-key groups");
+  return fast ? launch_fwd_strip<KM, true, 2>(pk, total_wg, st) : launch_fwd_strip<KM, false, 2>(pk, total_wg, st);
 }
 
-template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, bool WIDE = false>
+template <int KM, bool FAST, bool HAS_Q, bool HAS_INJ, int NQ = 2>
 int launch_bwd_strip(const StripBwdPack& pk, int total_wg, hipStream_t st) {
   const size_t lds = BwdLds<KM, HAS_Q>::BYTES;
-  if (int rc = allow_lds_strip(gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, WIDE>, lds)) return rc;
-  hipLaunchKernelGGL((gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, WIDE>), dim3(total_wg), dim3(SNT), lds, st, pk);
+  if (int rc = allow_lds_strip(gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, NQ>, lds)) return rc;
+  hipLaunchKernelGGL((gdn_state_bwd_strip<KM, FAST, HAS_Q, HAS_INJ, NQ>), dim3(total_wg), dim3(SNT), lds, st, pk);
   return GPA_HIP_OK;
 }
 
 template <int KM>
-int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj, bool wide,
+int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj, int nq,
                            hipStream_t st) {
-  if constexpr (KM == 128)
-    if (wide && !has_inj)
-      return has_q ? launch_bwd_strip<KM, true, true, false, true>(pk, total_wg, st)
-                   : launch_bwd_strip<KM, true, false, false, true>(pk, total_wg, st);
-  if (wide) return fail(GPA_HIP_EINVAL, "strip backward: the wide split is built for 128 keys without injections");
+  if constexpr (KM == 128) {
+    if (nq == 1 && fast && !has_inj)
+      return has_q ? launch_bwd_strip<KM, true, true, false, 1>(pk, total_wg, st)
+                   : launch_bwd_strip<KM, true, false, false, 1>(pk, total_wg, st);
+    if (nq == 4 && fast) {
+      if (has_q) return has_inj ? launch_bwd_strip<KM, true, true, true, 4>(pk, total_wg, st)
+                                : launch_bwd_strip<KM, true, true, false, 4>(pk, total_wg, st);
+      return has_inj ? launch_bwd_strip<KM, true, false, true, 4>(pk, total_wg, st)
+                     : launch_bwd_strip<KM, true, false, false, 4>(pk, total_wg, st);
+    }
+  }
+  if (nq != 2)
+    return fail(GPA_HIP_EINVAL, "strip backward: the wide form (no injections) and the quarter form are built for "
+                                "whole 128-key groups");
   if (fast) {
     if (has_q) return has_inj ? launch_bwd_strip<KM, true, true, true>(pk, total_wg, st)
                               : launch_bwd_strip<KM, true, true, false>(pk, total_wg, st);
@@ -867,9 +914,9 @@ int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool
                  : launch_bwd_strip<KM, false, false, false>(pk, total_wg, st);
 }
 
-template int launch_state_fwd_strip<64>(const StripFwdPack&, int, bool, bool, hipStream_t);
-template int launch_state_fwd_strip<128>(const StripFwdPack&, int, bool, bool, hipStream_t);
-template int launch_state_bwd_strip<64>(const StripBwdPack&, int, bool, bool, bool, bool, hipStream_t);
-template int launch_state_bwd_strip<128>(const StripBwdPack&, int, bool, bool, bool, bool, hipStream_t);
+template int launch_state_fwd_strip<64>(const StripFwdPack&, int, bool, int, hipStream_t);
+template int launch_state_fwd_strip<128>(const StripFwdPack&, int, bool, int, hipStream_t);
+template int launch_state_bwd_strip<64>(const StripBwdPack&, int, bool, bool, bool, int, hipStream_t);
+template int launch_state_bwd_strip<128>(const StripBwdPack&, int, bool, bool, bool, int, hipStream_t);
 
 }  // namespace gpa

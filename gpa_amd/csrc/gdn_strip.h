@@ -13,7 +13,7 @@ constexpr int GPA_STRIP_MAXP = 12;  // scan groups per launch
 // (key-major, may be null) and the buffers of include/gpa_hip.h's
 // gpa_gdn_saved that the recurrence reads (wrow, kcol, u, gam) and writes
 // (delta, states, final).  Workgroups wg0 .. wg0 + streams * wg_per_stream - 1
-// run it, wg_per_stream = strip_wg_per_stream(V, wide) per stream.
+// run it, wg_per_stream = strip_wg_per_stream(V, nq) per stream.
 struct StripFwdOne {
   int K, V, heads, nch, wg0, wg_per_stream;
   const float* s0;
@@ -52,31 +52,34 @@ struct StripBwdPack {
   StripBwdOne p[GPA_STRIP_MAXP];
 };
 
-// Workgroups per stream: the split form covers 64 value columns per workgroup
-// (two waves per 32-column strip, each with half of the key rows), the wide
-// form 128 (one wave per strip with every key row).  A workgroup holds a
-// whole CU (its LDS), so a launch of more workgroups than the device has CUs
-// runs its chains in two rounds; the wide form halves the workgroups for
-// such launches at the cost of a longer chunk step per wave.
-int strip_wg_per_stream(int vdim, bool wide);
+// The forms of the strip kernels, by the waves that share a 32-column strip
+// (nq): split (2, each with half of the key rows; 64 value columns per
+// workgroup), wide (1, every key row; 128 columns) and quarter (4, a quarter of
+// the rows each; 32 columns).  A workgroup holds a whole CU (its LDS) and the
+// chunk step is bound by each wave's own instruction stream, so fewer rows per
+// wave shorten the step while the workgroups fit on the CUs (quarter), and a
+// launch that would exceed them runs in the wide form rather than two rounds.
+int strip_wg_per_stream(int vdim, int nq);
 // Pack entries for one scan group (the buffers of gpa_gdn_saved / gpa_gdn_grads),
 // its workgroups starting at wg0.  has_q: the backward has a read gradient.
-StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0, bool wide);
+StripFwdOne strip_fwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, int nch, int wg0, int nq);
 StripBwdOne strip_bwd_one(const gpa_gdn_problem& p, const gpa_gdn_saved& sv, const gpa_gdn_grads& gr, int nch,
-                          int wg0, bool has_q, bool wide);
-inline int strip_workgroups(const gpa_gdn_problem& p, bool wide) {
-  return p.batch * p.heads * strip_wg_per_stream(p.vdim, wide);
+                          int wg0, bool has_q, int nq);
+inline int strip_workgroups(const gpa_gdn_problem& p, int nq) {
+  return p.batch * p.heads * strip_wg_per_stream(p.vdim, nq);
 }
-// Whether a group can run in the wide form: 128 keys, V a multiple of 128.
+// Whether a group can run in the wide form (128 keys, V a multiple of 128) or
+// the quarter form (128 keys, V a multiple of 64).
 inline bool strip_wide_ok(const gpa_gdn_problem& p) { return p.kdim == 128 && p.vdim % 128 == 0; }
+inline bool strip_quarter_ok(const gpa_gdn_problem& p) { return p.kdim == 128 && p.vdim % 64 == 0; }
 // All groups of a pack share the key-width class KM (K <= KM, K % 16 == 0);
-// `fast` when every group has K == KM and V % 64 == 0; `wide` (KM = 128, every
-// group strip_wide_ok, the backward without state injections) selects the
-// wide form.
+// `fast` when every group has K == KM and V % 64 == 0; nq selects the form
+// (1 and 4: KM = 128 and fast; 1: every group strip_wide_ok and, backward,
+// no state injections).
 template <int KM>
-int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, bool wide, hipStream_t st);
+int launch_state_fwd_strip(const StripFwdPack& pk, int total_wg, bool fast, int nq, hipStream_t st);
 template <int KM>
-int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj, bool wide,
+int launch_state_bwd_strip(const StripBwdPack& pk, int total_wg, bool fast, bool has_q, bool has_inj, int nq,
                            hipStream_t st);
 
 }  // namespace gpa

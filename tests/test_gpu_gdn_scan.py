@@ -160,12 +160,17 @@ def _oracle_segments_autograd(leaves, g, beta, s0, chunk, offset):
     return torch.cat(outs, 1), torch.stack(starts, 2), state
 
 
-# The wide strip form: a state launch whose split form would need more
-# workgroups than the device has CUs (two 64-column workgroups per 128-key
-# stream) runs one 128-column workgroup per stream, each wave with every key
-# row of its strip.  These shapes put 288 and 576 split workgroups in one launch.
+# The forms of the 128-key strip state kernels, by the waves that share a
+# 32-column strip: quarter (4 waves, 32-column workgroups) while its
+# workgroups fit on the device's 256 CUs, split (2 waves, 64 columns) while
+# those fit, else wide (1 wave, 128 columns).  The wide shapes put 288 and 576
+# split workgroups in one launch; the split shapes 320 quarter and 160 split
+# workgroups; the quarter shapes 128.
 WIDE_FWD = [(9, 130, 16, 128, 128, 64, 0, torch.bfloat16), (3, 70, 48, 128, 256, 64, 17, torch.bfloat16)]
 WIDE_BWD = [(9, 40, 16, 128, 128, 16, 5, torch.bfloat16), (1, 40, 72, 128, 256, 32, 0, torch.bfloat16)]
+FORM_CASES = [("quarter", (1, 130, 32, 128, 128, 64, 0, torch.bfloat16)),
+              ("quarter", (2, 40, 8, 128, 256, 16, 5, torch.bfloat16)),
+              ("split", (5, 70, 16, 128, 128, 64, 17, torch.bfloat16))]
 
 
 def _kernel_names(fn):
@@ -178,10 +183,16 @@ def _kernel_names(fn):
     return {e.name for e in prof.events()}
 
 
-def _wide_ran(names, kind):
-    want = {"fwd": "gdn_state_fwd_strip<128, true, true>", "bwd_q": "gdn_state_bwd_strip<128, true, true, false, true>",
-            "bwd": "gdn_state_bwd_strip<128, true, false, false, true>"}[kind]
+def _form_ran(names, kind, nq):
+    want = {"fwd": f"gdn_state_fwd_strip<128, true, {nq}>",
+            "bwd_q": f"gdn_state_bwd_strip<128, true, true, false, {nq}>",
+            "bwd_q_inj": f"gdn_state_bwd_strip<128, true, true, true, {nq}>",
+            "bwd": f"gdn_state_bwd_strip<128, true, false, false, {nq}>"}[kind]
     return any(want in n for n in names)
+
+
+def _wide_ran(names, kind):
+    return _form_ran(names, kind, 1)
 
 
 @pytest.mark.parametrize("case", WIDE_FWD, ids=lambda c: f"B{c[0]}T{c[1]}H{c[2]}V{c[4]}")
@@ -238,7 +249,7 @@ def test_wide_strip_backward_matches_autograd_of_recurrence(case, with_q):
 def test_wide_pack_matches_split_single_calls():
     """Nine 128-key groups in one packed call (the relation edges' shape at
     B=1, H=16: 288 split workgroups) take the wide form; one call per group
-    takes the split form.  The two differ only in the order of the sums over
+    takes the quarter form.  The two differ only in the order of the sums over
     the key rows."""
     from gpa_amd.ops import gdn_scan_hip, gdn_scan_many
     results = {}
@@ -273,6 +284,47 @@ def test_wide_pack_matches_split_single_calls():
         assert _rel(a, b) < tol, ("forward", i, _rel(a, b))
     for i, (a, b) in enumerate(zip(ga, gb)):
         assert _rel(a, b) < 2e-3, ("grad", i, _rel(a, b))
+
+
+@pytest.mark.parametrize("form,case", FORM_CASES, ids=lambda c: c if isinstance(c, str) else f"B{c[0]}H{c[2]}V{c[4]}")
+def test_strip_forms_match_autograd_of_recurrence(form, case):
+    """Forward and backward (read gradient and chunk-start state injections,
+    as the level scans have) in the quarter and split forms, checked through
+    the profiler for the form that ran."""
+    from gpa_amd.ops import gdn_scan_hip
+    nq = {"quarter": 4, "split": 2}[form]
+    b, t, h, kd, vd, chunk, offset, dtype = case
+    q, k, v, g, beta, s0 = _inputs(b, t, h, kd, vd, dtype, seed=17)
+    gen = torch.Generator().manual_seed(6)
+    nch = (offset + t + chunk - 1) // chunk
+    w_out = torch.randn(b, t, h, vd, generator=gen, dtype=torch.float64)
+    w_states = torch.randn(b, h, nch, kd, vd, generator=gen, dtype=torch.float64) * .1
+    w_final = torch.randn(b, h, kd, vd, generator=gen, dtype=torch.float64)
+
+    def loss(out, states, final):
+        return ((final.double() * w_final.to(final.device)).sum() + (states.double() * w_states.to(states.device)).sum()
+                + (out.double() * w_out.to(out.device)).sum())
+
+    leaves = [x.to(DEV).requires_grad_() for x in (q, k, v)]
+    g_d, b_d, s_d = (x.to(DEV).requires_grad_() for x in (g, beta, s0))
+    res = {}
+    names = _kernel_names(lambda: res.setdefault("r", gdn_scan_hip(*leaves, g_d, b_d, s_d, chunk=chunk,
+                                                                    offset=offset)))
+    assert _form_ran(names, "fwd", nq), sorted(n for n in names if "state" in n)
+    out, states, final = res["r"]
+    names = _kernel_names(lambda: loss(out, states, final).backward())
+    assert _form_ran(names, "bwd_q_inj", nq), sorted(n for n in names if "state" in n)
+    ref_leaves = [x.detach().double().requires_grad_() for x in (q, k, v)]
+    g_r, b_r, s_r = (x.double().requires_grad_() for x in (g, beta, s0))
+    ro, rs, rf = _oracle_segments_autograd(ref_leaves, g_r, b_r, s_r, chunk, offset)
+    errs = {"out": _rel(out, ro), "states": _rel(states, rs), "final": _rel(final, rf)}
+    loss(ro, rs, rf).backward()
+    pairs = [("dq", leaves[0].grad, ref_leaves[0].grad), ("dk", leaves[1].grad, ref_leaves[1].grad),
+             ("dv", leaves[2].grad, ref_leaves[2].grad), ("dg", g_d.grad, g_r.grad), ("dbeta", b_d.grad, b_r.grad),
+             ("ds0", s_d.grad, s_r.grad)]
+    errs.update({name: _rel(a, r) for name, a, r in pairs})
+    print(form, case, errs)
+    assert all(e < 2e-2 for e in errs.values()), errs
 
 
 def test_gdn_rejects_bad_geometry_before_launch():
