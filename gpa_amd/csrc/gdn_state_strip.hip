@@ -16,11 +16,15 @@
 // per pair of registers exchanges them (swap_halves).  So the recurrence has
 // no LDS round trip and no barrier between its two products.
 //
-// Work split.  Two waves share a 32-column strip, each holding half of its K
+// Work split.  NQ waves share a 32-column strip, each holding K/NQ of its K
 // rows; the first product of a chunk is a sum over K, so each wave computes it
-// over its own rows and the two partial sums meet through LDS (one exchange
-// and one barrier per chunk); the second product updates each wave's own rows.
-// A workgroup of four waves covers 64 columns of one stream.
+// over its own rows and the partial sums meet through LDS (one exchange and
+// one barrier per chunk); the second product updates each wave's own rows.
+// A workgroup of four waves covers 32 (4 / NQ) columns of one stream.  The
+// forms: split (NQ = 2, 64 columns), quarter (NQ = 4, 32 columns; fewer rows
+// per wave shorten the chunk step, which each wave's instruction stream
+// bounds) and wide (NQ = 1, 128 columns, no exchange; for launches that would
+// otherwise need more workgroups than the device has CUs).
 //
 // Operands.  The chunk's matrix fragments (W rows and Kn^T rows forward; Kn
 // rows, W^T rows and Qn^T rows backward; the layouts of include/gpa_hip.h,
@@ -237,11 +241,11 @@ constexpr int GATE_FLOATS = R + 4;
 
 }  // namespace
 
-// Both kernels.  Four waves: strip c = w / 2 of the workgroup's 64 columns,
-// half hk = w % 2 of the key rows (tiles hk NTW .. hk NTW + NTW - 1 of 32 rows,
-// NTW = KM / 64).  LDS holds the chunk operands (double-buffered, except the
-// backward's Kn rows), the gate factors (double-buffered) and one 64 x 32 fp32
-// partial product per wave for the exchange.
+// Both kernels.  Four waves: strip w / NQ of the workgroup's columns, part
+// hk = w % NQ of the key rows (row tiles hk OT .. hk OT + OT - 1 of 32 rows,
+// OT = KM / (32 NQ)).  LDS holds the chunk operands (double-buffered, except
+// the backward's Kn rows), the gate factors (double-buffered) and one 64 x 32
+// fp32 partial product per wave for the exchange.
 // Per-wave slot of the exchange area (floats): a 64 x 32 fp32 partial product,
 // or a wave's rows of its strip transposed for a store (RW rows + 4 of padding
 // per column).
