@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import gc
 import os
+import re
 import shutil
 import struct
 import subprocess
@@ -28,24 +29,66 @@ ENTRIES = {"gpa_decode_step": 0, "gpa_route_forward": 1, "gpa_route_backward": 2
            "gpa_gdn_token_step_many": 8, "gpa_level_token_forward": 9,
            "gpa_token_level_forward": 10, "gpa_product_read_forward": 11, "gpa_product_read_backward": 12,
            "gpa_token_slot_step": 13, "gpa_slot_gates_act_forward": 14, "gpa_moment_scan_many": 15,
-           "gpa_quad_features_forward": 16, "gpa_quad_features_backward": 17}
+           "gpa_quad_features_forward": 16, "gpa_quad_features_backward": 17, "gpa_gdn_forward": 18,
+           "gpa_gdn_backward": 19, "gpa_gdn_forward_many": 20, "gpa_gdn_backward_many": 21,
+           "gpa_gdn_nchunks": 22, "gpa_gdn_path": 23}
 SOURCES = ["gpa_decode.hip", "route_reader.hip", "level_mix.hip", "gdn_token.hip", "level_token.hip",
            "product_read.hip", "slot_gates.hip", "moment_scan.hip",
-           "quad_features.hip"]
+           "quad_features.hip", "gdn_scan.hip", "gdn_prep_mfma.hip", "gdn_state_mfma.hip", "gdn_out_mfma.hip",
+           "gdn_chunk_bwd_mfma.hip"]
+# Test-side sources of the host build: stand-ins for kernels it does not emulate.
+HOST_SOURCES = ["strip_absent.cpp"]
 
 
 def compiler() -> str | None:
     return CLANG if os.path.exists(CLANG) else shutil.which("clang++")
 
 
-def build(out_dir: str, sources=None) -> str:
+_EXTERN_SHARED = re.compile(r"extern\s+__shared__\s+(?:__align__\(\d+\)\s+)?(\w+(?:\s+\w+)*?)\s+(\w+)\[\];")
+
+
+def _host_source(out_dir: str, name: str) -> str:
+    """The kernel source as the host build compiles it.  `__shared__` is a
+    static object here, so `extern __shared__ T x[];` (the launch's dynamic
+    LDS) is spelled `HIP_DYNAMIC_SHARED(T, x)`, which points x at the
+    launch's allocation; a #line directive keeps diagnostics and
+    AddressSanitizer reports on the original file and lines."""
+    path = os.path.join(ROOT, "gpa_amd", "csrc", name)
+    text = open(path).read()
+    if not _EXTERN_SHARED.search(text):
+        return path
+    copy = os.path.join(out_dir, name)
+    with open(copy, "w") as f:
+        f.write(f'#line 1 "{path}"\n' + _EXTERN_SHARED.sub(r"HIP_DYNAMIC_SHARED(\1, \2)", text))
+    return copy
+
+
+def build(out_dir: str, sources=None, jobs: int = 8) -> str:
+    """Compile every source to an object (up to `jobs` compilers at once),
+    then link the runner."""
     exe = os.path.join(out_dir, "host_runner")
-    cmd = [compiler(), "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
-           "-Wno-unused-command-line-argument", "-I", HERE, "-I", os.path.join(ROOT, "include"),
-           "-I", os.path.join(ROOT, "gpa_amd", "csrc"), "-x", "c++"]
-    cmd += [os.path.join(ROOT, "gpa_amd", "csrc", s) for s in (sources or SOURCES)]
-    cmd += ["-x", "none", os.path.join(HERE, "runner.cpp"), "-o", exe, "-lpthread"]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    flags = [compiler(), "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
+             "-Wno-unused-command-line-argument", "-Wno-psabi", "-I", HERE, "-I", os.path.join(ROOT, "include"),
+             "-I", os.path.join(ROOT, "gpa_amd", "csrc")]
+    units = [_host_source(out_dir, s) for s in (sources or SOURCES)]
+    units += [os.path.join(HERE, s) for s in HOST_SOURCES + ["runner.cpp"]]
+    objs, running = [], []
+
+    def finish(proc):
+        out, err = proc.communicate()
+        if proc.returncode:
+            raise RuntimeError(err[-4000:])
+
+    for i, src in enumerate(units):
+        obj = os.path.join(out_dir, f"{i:02d}_{os.path.basename(src)}.o")
+        objs.append(obj)
+        running.append(subprocess.Popen(flags + ["-x", "c++", "-c", src, "-o", obj], stdout=subprocess.PIPE,
+                                        stderr=subprocess.PIPE, text=True))
+        if len(running) >= jobs:
+            finish(running.pop(0))
+    for proc in running:
+        finish(proc)
+    res = subprocess.run(flags + objs + ["-o", exe, "-lpthread"], capture_output=True, text=True)
     if res.returncode:
         raise RuntimeError(res.stderr[-4000:])
     return exe
@@ -53,10 +96,13 @@ def build(out_dir: str, sources=None) -> str:
 
 def _pointer_fields(ctype, base=0):
     out = []
-    if issubclass(ctype, ctypes.Array):  # an array of structs or pointers passed as one blob
+    if issubclass(ctype, ctypes.Array):  # an array of structs, pointers or scalars passed as one blob
         for i in range(ctype._length_):
             off = base + i * ctypes.sizeof(ctype._type_)
-            out += [off] if ctype._type_ is ctypes.c_void_p else _pointer_fields(ctype._type_, off)
+            if ctype._type_ is ctypes.c_void_p:
+                out.append(off)
+            elif issubclass(ctype._type_, (ctypes.Structure, ctypes.Array)):
+                out += _pointer_fields(ctype._type_, off)
         return out
     for name, t in ctype._fields_:
         off = base + getattr(ctype, name).offset
@@ -128,7 +174,7 @@ class HostLib:
         for b, n in spans:
             ctypes.memmove(b, data[pos:pos + n], n)
             pos += n
-        return 0
+        return int(res.stdout.split()[-1])
 
     def gpa_decode_step(self, prob, stream):
         return self._call("gpa_decode_step", [prob])
@@ -187,6 +233,28 @@ class HostLib:
 
     def gpa_quad_features_backward(self, prob, grads, stream):
         return self._call("gpa_quad_features_backward", [prob, grads])
+
+    def gpa_gdn_forward(self, prob, saved, out, timing, stream):
+        assert not timing
+        return self._call("gpa_gdn_forward", [prob, saved, out])
+
+    def gpa_gdn_backward(self, prob, saved, grads, timing, stream):
+        assert not timing
+        return self._call("gpa_gdn_backward", [prob, saved, grads])
+
+    def gpa_gdn_forward_many(self, probs, saved, outs, n, timing, stream):
+        assert not timing and n == len(probs) == len(saved) == len(outs)
+        return self._call("gpa_gdn_forward_many", [probs, saved, outs])
+
+    def gpa_gdn_backward_many(self, probs, saved, grads, n, timing, stream):
+        assert not timing and n == len(probs) == len(saved) == len(grads)
+        return self._call("gpa_gdn_backward_many", [probs, saved, grads])
+
+    def gpa_gdn_nchunks(self, tokens, offset, chunk):
+        return self._call("gpa_gdn_nchunks", [(ctypes.c_int32 * 3)(tokens, offset, chunk)])
+
+    def gpa_gdn_path(self, prob):
+        return self._call("gpa_gdn_path", [prob])
 
     def gpa_hip_last_error(self):
         return b""

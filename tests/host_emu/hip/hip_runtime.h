@@ -60,6 +60,29 @@ inline float __shfl_xor(float v, int m, int width = 64) {
   emu_wave_barrier[w]->arrive_and_wait();
   return r;
 }
+// __shfl_up / __shfl_down / __shfl: lanes whose source falls outside their
+// width-lane segment keep their own value (up, down); __shfl reads lane
+// `src` of the segment.
+inline float emu_shfl_from(float v, int src) {
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  emu_xchg[w][l] = v;
+  emu_wave_barrier[w]->arrive_and_wait();
+  const float r = emu_xchg[w][src];
+  emu_wave_barrier[w]->arrive_and_wait();
+  return r;
+}
+inline float __shfl_up(float v, unsigned d, int width = 64) {
+  const int l = threadIdx.x % 64;
+  return emu_shfl_from(v, (l % width) >= (int)d ? l - (int)d : l);
+}
+inline float __shfl_down(float v, unsigned d, int width = 64) {
+  const int l = threadIdx.x % 64;
+  return emu_shfl_from(v, (l % width) + (int)d < width ? l + (int)d : l);
+}
+inline float __shfl(float v, int src, int width = 64) {
+  const int l = threadIdx.x % 64;
+  return emu_shfl_from(v, l - l % width + src % width);
+}
 inline float atomicAdd(float* p, float v) { return std::atomic_ref<float>(*p).fetch_add(v); }
 
 // MFMA: every lane posts its operands, then computes its own accumulator
@@ -144,6 +167,49 @@ extern char* emu_dynamic_lds;
 #define hipSuccess 0
 #define hipFuncAttributeMaxDynamicSharedMemorySize 8
 inline int hipFuncSetAttribute(const void*, int, int) { return 0; }
+
+// The runtime calls of the scan library's host code.  Launches run to
+// completion here, one after another, so streams and events order nothing:
+// they are opaque non-null handles.  The device is one MI355X (256 CUs).
+typedef int hipDevice_t;
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+#define hipStreamNonBlocking 1u
+#define hipEventDisableTiming 2u
+#define hipDeviceAttributeMultiprocessorCount 63
+inline hipError_t hipGetDevice(int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+inline hipError_t hipSetDevice(int) { return hipSuccess; }
+inline hipError_t hipDeviceGetAttribute(int* v, int, int) {
+  *v = 256;
+  return hipSuccess;
+}
+inline hipError_t hipStreamGetDevice(hipStream_t, hipDevice_t* d) {
+  *d = 0;
+  return hipSuccess;
+}
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* s) {
+  *s = hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+inline char emu_handles[2];
+inline hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) {
+  *s = reinterpret_cast<hipStream_t>(&emu_handles[0]);
+  return hipSuccess;
+}
+inline hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) {
+  *e = reinterpret_cast<hipEvent_t>(&emu_handles[1]);
+  return hipSuccess;
+}
+inline hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
+inline hipError_t hipStreamWaitEvent(hipStream_t, hipEvent_t, unsigned) { return hipSuccess; }
+inline const char* hipGetErrorString(hipError_t) { return "host build"; }
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void** p, const void* symbol) {
+  *p = const_cast<void*>(symbol);
+  return hipSuccess;
+}
 inline float __expf(float x) { return expf(x); }
 // correctly rounded single operations (the host build is compiled without FMA contraction)
 inline float __fadd_rn(float a, float b) { return a + b; }

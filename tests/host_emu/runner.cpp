@@ -25,6 +25,7 @@ int fail(int code, const char* message) {
   return code;
 }
 int check_launch(const char*) { return 0; }
+void mark(gpa_timing*, hipStream_t) {}  // the host tests pass no timing record
 
 static int64_t get(FILE* f) {
   int64_t x = 0;
@@ -65,6 +66,7 @@ int main(int argc, char** argv) {
   }
   fclose(f);
   int rc = -1;
+  int64_t value = 0;  // the result of an entry point that returns a value
   switch (entry) {
     case 0:
       rc = gpa_decode_step(reinterpret_cast<gpa_decode_problem*>(blobs.at(0).data()), nullptr);
@@ -140,6 +142,38 @@ int main(int argc, char** argv) {
       rc = gpa_quad_features_backward(reinterpret_cast<gpa_quad_problem*>(blobs.at(0).data()),
                                       reinterpret_cast<gpa_quad_grads*>(blobs.at(1).data()), nullptr);
       break;
+    case 18:
+      rc = gpa_gdn_forward(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                           reinterpret_cast<gpa_gdn_saved*>(blobs.at(1).data()),
+                           *reinterpret_cast<gpa_operand*>(blobs.at(2).data()), nullptr, nullptr);
+      break;
+    case 19:
+      rc = gpa_gdn_backward(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                            reinterpret_cast<gpa_gdn_saved*>(blobs.at(1).data()),
+                            reinterpret_cast<gpa_gdn_grads*>(blobs.at(2).data()), nullptr, nullptr);
+      break;
+    case 20:
+      rc = gpa_gdn_forward_many(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                                reinterpret_cast<gpa_gdn_saved*>(blobs.at(1).data()),
+                                reinterpret_cast<gpa_operand*>(blobs.at(2).data()),
+                                (int32_t)(blobs.at(0).size() / sizeof(gpa_gdn_problem)), nullptr, nullptr);
+      break;
+    case 21:
+      rc = gpa_gdn_backward_many(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()),
+                                 reinterpret_cast<gpa_gdn_saved*>(blobs.at(1).data()),
+                                 reinterpret_cast<gpa_gdn_grads*>(blobs.at(2).data()),
+                                 (int32_t)(blobs.at(0).size() / sizeof(gpa_gdn_problem)), nullptr, nullptr);
+      break;
+    case 22: {
+      const int32_t* a = reinterpret_cast<const int32_t*>(blobs.at(0).data());
+      value = gpa_gdn_nchunks(a[0], a[1], a[2]);
+      rc = 0;
+      break;
+    }
+    case 23:
+      value = gpa_gdn_path(reinterpret_cast<gpa_gdn_problem*>(blobs.at(0).data()));
+      rc = 0;
+      break;
   }
   if (rc) {
     fprintf(stderr, "entry %ld rc=%d: %s\n", (long)entry, rc, last_error.c_str());
@@ -149,5 +183,6 @@ int main(int argc, char** argv) {
   for (int64_t i = 0; i < nbuf; ++i) fwrite(buf[i], 1, bytes[i], f);
   fclose(f);
   for (char* b : buf) free(b);
+  printf("%lld\n", (long long)value);
   return 0;
 }
