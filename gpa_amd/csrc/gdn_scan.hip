@@ -671,6 +671,7 @@ __global__ __launch_bounds__(NT) void gdn_chunk_bwd(gpa_gdn_problem p, gpa_gdn_s
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * c2[j];
     }
+    __syncthreads();  // every row of xm is read above before dKK overwrites it below
     // dA_ts (s<t) = -acc; A_ts = b_t E_ts KK_ts.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
