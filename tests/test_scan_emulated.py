@@ -4,8 +4,9 @@ AddressSanitizer (tests/host_emu/), against the oracle's per-token
 recurrence in float64 (reference ops.py:29-85), on the CPU.
 
 The cases reach the float32 FMA path (state, out and dd0 kernels of
-gdn_scan.hip, the chunk backward on fp32 MFMA) and the bfloat16 MFMA path
-above 128 keys (gdn_state_fwd_mfma / gdn_state_bwd_mfma at 256 keys, with K
+gdn_scan.hip, the chunk backward on fp32 MFMA, or the FMA chunk backward
+when K is not a multiple of 4), the bfloat16 FMA path (K not a multiple of
+16) and the bfloat16 MFMA path above 128 keys (gdn_state_fwd_mfma / gdn_state_bwd_mfma at 256 keys, with K
 below and at the tile), with chunk offsets, ragged last chunks and tiny
 shapes.  Every global access of those kernels is checked against the exact
 extent of the buffer it addresses; the results are held to the GPU tests'
@@ -23,6 +24,8 @@ from tests.test_gpu_gdn_scan import _inputs, _oracle_segments, _oracle_segments_
 CASES = [
     # (B, T, H, K, V, chunk, offset, dtype)
     (2, 9, 2, 4, 3, 4, 2, torch.float32),
+    (2, 11, 1, 6, 5, 4, 1, torch.float32),  # K % 4 != 0: the FMA chunk backward at 64 keys
+    (1, 40, 2, 40, 24, 16, 5, torch.bfloat16),  # K % 16 != 0: the bfloat16 FMA state path
     (1, 70, 2, 32, 48, 64, 17, torch.float32),
     (1, 40, 1, 256, 64, 16, 3, torch.float32),
     (1, 40, 1, 256, 64, 64, 3, torch.float32),
